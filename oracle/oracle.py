@@ -1,0 +1,306 @@
+"""ctypes bindings for the CPU oracle (TEST INFRASTRUCTURE ONLY).
+
+Loads ``oracle/librefcpu.so`` (this repository's C++ restatement of the
+reference attention composite) and, where it was built, ``oracle/_ref/
+libmftref.so`` (the reference's own operators compiled from its sources).
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline
+leg import this module; the product path never does.
+
+Each wrapper names the reference function it restates; the C files carry the
+file:line citations.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "librefcpu.so")
+REF_PATH = os.path.join(HERE, "_ref", "libmftref.so")
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+_i64 = C.c_int64
+
+_lib = None
+_ref = None
+
+
+def build() -> None:
+    """Compile the oracle (and the reference CPU path where its sources exist)."""
+    subprocess.run(["make", "-s", "-C", HERE, "-j8"], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"oracle library missing: {LIB_PATH} (run make -C oracle)")
+        L = C.CDLL(LIB_PATH)
+        L.orc_uniform.restype = C.c_double
+        L.orc_uniform.argtypes = [C.c_uint64, C.c_uint32, C.c_uint64]
+        L.orc_fill_normal.argtypes = [_f32p, _i64, C.c_uint64, C.c_uint32, C.c_float]
+        L.orc_fill_mod.argtypes = [_f32p, _i64, C.c_float, C.c_int, C.c_int]
+        L.orc_stress_rows.argtypes = [_f32p, _i64, _i64, _i64, _i64, _i64, C.c_float, C.c_uint64]
+        L.orc_f32_to_bf16_bits.restype = C.c_uint16
+        L.orc_f32_to_bf16_bits.argtypes = [C.c_float]
+        L.orc_round_bf16.argtypes = [_f32p, _i64]
+        L.orc_to_bf16_bits.argtypes = [_f32p, _u16p, _i64]
+        L.orc_from_bf16_bits.argtypes = [_u16p, _f32p, _i64]
+        opt_f32 = C.c_void_p
+        L.orc_attn_composite.restype = C.c_int
+        L.orc_attn_composite.argtypes = [_f32p, _f32p, _f32p, opt_f32,
+                                         _i64, _i64, _i64, _i64, _i64, C.c_float, C.c_int,
+                                         opt_f32, opt_f32, opt_f32, opt_f32, opt_f32]
+        L.orc_attn_streaming.restype = C.c_int
+        L.orc_attn_streaming.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64,
+                                         C.c_float, C.c_int, _f32p]
+        L.orc_attn_f64.restype = C.c_int
+        L.orc_attn_f64.argtypes = [_f32p, _f32p, _f32p, opt_f32,
+                                   _i64, _i64, _i64, _i64, _i64, C.c_double, C.c_int,
+                                   opt_f32, opt_f32, opt_f32, opt_f32, opt_f32]
+        L.orc_repeat_kv.argtypes = [_f32p, _f32p, _i64, _i64, _i64, _i64, _i64]
+        L.orc_repeat_kv_backward.argtypes = [_f32p, _f32p, _i64, _i64, _i64, _i64, _i64]
+        _lib = L
+    return _lib
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_PATH)
+
+
+def ref():
+    global _ref
+    if _ref is None:
+        if not ref_available():
+            raise RuntimeError(f"reference CPU library missing: {REF_PATH}")
+        R = C.CDLL(REF_PATH)
+        opt = C.c_void_p
+        R.mftref_composite.restype = C.c_int
+        R.mftref_composite.argtypes = [_f32p, _f32p, _f32p, opt, _i64, _i64, _i64, _i64, _i64,
+                                       C.c_float, C.c_int, opt, opt, opt, opt,
+                                       C.POINTER(C.c_double), C.POINTER(C.c_double),
+                                       C.POINTER(C.c_int64)]
+        R.mftref_memeff_nograd.restype = C.c_int
+        R.mftref_memeff_nograd.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64,
+                                           C.c_float, C.c_int, _f32p]
+        R.mftref_memeff_grad.restype = C.c_int
+        R.mftref_memeff_grad.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i64,
+                                         C.c_float, C.c_int, _f32p, _f32p, _f32p, _f32p]
+        R.mftref_repeat_kv.restype = C.c_int
+        R.mftref_repeat_kv.argtypes = [_f32p, opt, _i64, _i64, _i64, _i64, _i64, _f32p, opt]
+        R.mftref_f32_to_bf16_bits.restype = C.c_uint16
+        R.mftref_f32_to_bf16_bits.argtypes = [C.c_float]
+        _ref = R
+    return _ref
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+# ---------------------------------------------------------------- generator
+def normal(n: int, seed: int, stream: int, sigma: float = 1.0) -> np.ndarray:
+    x = np.empty(n, dtype=np.float32)
+    lib().orc_fill_normal(x, n, seed, stream, sigma)
+    return x
+
+
+def fill_mod(n: int, a: float, m: int, o: int) -> np.ndarray:
+    x = np.empty(n, dtype=np.float32)
+    lib().orc_fill_mod(x, n, a, m, o)
+    return x
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    y = np.ascontiguousarray(x, dtype=np.float32).copy()
+    lib().orc_round_bf16(y.reshape(-1), y.size)
+    return y
+
+
+def to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().orc_to_bf16_bits(x.reshape(-1), out.reshape(-1), x.size)
+    return out
+
+
+# ------------------------------------------------------------------ configs
+# BASELINE.json configs; seed = 1000 + config number, streams Q=0 K=1 V=2 dO=3.
+CONFIGS = {
+    "c1": dict(B=4, Hq=12, Hkv=12, D=64, S=128, dtype="f32", scale=1 / 8, do_sigma=1.0, stress=False,
+               name="GPT-2-small MHA fp32"),
+    "c2": dict(B=4, Hq=16, Hkv=16, D=64, S=512, dtype="f32", scale=1 / 8, do_sigma=0.1, stress=False,
+               name="GPT-2-medium MHA fp32"),
+    "c3": dict(B=2, Hq=14, Hkv=2, D=64, S=2048, dtype="bf16", scale=1 / 8, do_sigma=0.1, stress=False,
+               name="Qwen2.5-0.5B GQA bf16"),
+    "c4": dict(B=4, Hq=4, Hkv=1, D=256, S=1024, dtype="bf16", scale=1 / 16, do_sigma=0.1, stress=True,
+               name="Gemma-3-270M GQA bf16 (K-row stress)"),
+    "c5": dict(B=1, Hq=4, Hkv=1, D=256, S=4096, dtype="bf16", scale=1 / 16, do_sigma=0.1, stress=False,
+               name="Gemma-3-1B GQA bf16"),
+    "c5f32": dict(B=1, Hq=4, Hkv=1, D=256, S=4096, dtype="f32", scale=1 / 16, do_sigma=0.1, stress=False,
+                  name="Gemma-3-1B GQA fp32 exactness variant"),
+}
+SEEDS = {"c1": 1001, "c2": 1002, "c3": 1003, "c4": 1004, "c5": 1005, "c5f32": 1005}
+
+
+def make_inputs(B, Hq, Hkv, S, D, seed, dtype="f32", do_sigma=1.0, stress=False):
+    """Seeded Q, K, V, dO as float32 arrays ([B,H,S,D]).  For bf16 the values
+    are rounded to bf16 (RNE), so the fp32 oracle sees exactly the kernel input."""
+    q = normal(B * Hq * S * D, seed, 0).reshape(B, Hq, S, D)
+    k = normal(B * Hkv * S * D, seed, 1).reshape(B, Hkv, S, D)
+    v = normal(B * Hkv * S * D, seed, 2).reshape(B, Hkv, S, D)
+    do = normal(B * Hq * S * D, seed, 3, do_sigma).reshape(B, Hq, S, D)
+    if stress:
+        cnt = int(round(0.01 * S))
+        lib().orc_stress_rows(k.reshape(-1), B, Hkv, S, D, cnt, 8.0, seed)
+    if dtype == "bf16":
+        q, k, v, do = (round_bf16(t) for t in (q, k, v, do))
+    return q, k, v, do
+
+
+def config_inputs(cfg_id):
+    c = CONFIGS[cfg_id]
+    return make_inputs(c["B"], c["Hq"], c["Hkv"], c["S"], c["D"], SEEDS[cfg_id], c["dtype"],
+                       c["do_sigma"], c["stress"])
+
+
+# ---------------------------------------------------------------- composite
+def composite(q, k, v, dO=None, scale=None, causal=True, want_lse=False):
+    """Reference composite forward (+ Engine backward if dO is given)."""
+    B, Hq, S, D = q.shape
+    Hkv = k.shape[1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    q, k, v = (np.ascontiguousarray(t, dtype=np.float32) for t in (q, k, v))
+    o = np.empty_like(q)
+    lse = np.empty((B, Hq, S), dtype=np.float32) if want_lse else None
+    dq = dk = dv = None
+    if dO is not None:
+        dO = np.ascontiguousarray(dO, dtype=np.float32)
+        dq = np.empty_like(q)
+        dk = np.empty_like(k)
+        dv = np.empty_like(v)
+    rc = lib().orc_attn_composite(q, k, v, _ptr(dO), B, Hq, Hkv, S, D, float(scale), int(causal),
+                                  _ptr(o), _ptr(lse), _ptr(dq), _ptr(dk), _ptr(dv))
+    if rc != 0:
+        raise ValueError("orc_attn_composite rejected its arguments")
+    return dict(o=o, lse=lse, dq=dq, dk=dk, dv=dv)
+
+
+def streaming(q, k, v, scale=None, causal=True):
+    B, H, S, D = q.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    o = np.empty_like(q)
+    rc = lib().orc_attn_streaming(np.ascontiguousarray(q), np.ascontiguousarray(k),
+                                  np.ascontiguousarray(v), B, H, S, D, float(scale), int(causal), o)
+    if rc != 0:
+        raise ValueError("orc_attn_streaming rejected its arguments")
+    return o
+
+
+def brute_f64(q, k, v, dO=None, scale=None, causal=True):
+    B, Hq, S, D = q.shape
+    Hkv = k.shape[1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    o = np.empty(q.shape, np.float64)
+    lse = np.empty((B, Hq, S), np.float64)
+    dq = dk = dv = None
+    if dO is not None:
+        dO = np.ascontiguousarray(dO, dtype=np.float32)
+        dq = np.empty(q.shape, np.float64)
+        dk = np.empty(k.shape, np.float64)
+        dv = np.empty(v.shape, np.float64)
+    rc = lib().orc_attn_f64(np.ascontiguousarray(q), np.ascontiguousarray(k), np.ascontiguousarray(v),
+                            _ptr(dO), B, Hq, Hkv, S, D, float(scale), int(causal),
+                            _ptr(o), _ptr(lse), _ptr(dq), _ptr(dk), _ptr(dv))
+    if rc != 0:
+        raise ValueError("orc_attn_f64 rejected its arguments")
+    return dict(o=o, lse=lse, dq=dq, dk=dk, dv=dv)
+
+
+def repeat_kv(kv, r):
+    B, H, S, D = kv.shape
+    out = np.empty((B, H * r, S, D), np.float32)
+    lib().orc_repeat_kv(np.ascontiguousarray(kv), out, B, H, S, D, r)
+    return out
+
+
+def repeat_kv_backward(g, r):
+    B, Hr, S, D = g.shape
+    out = np.empty((B, Hr // r, S, D), np.float32)
+    lib().orc_repeat_kv_backward(np.ascontiguousarray(g), out, B, Hr // r, S, D, r)
+    return out
+
+
+# ------------------------------------------------- reference (oracle/_ref)
+def ref_composite(q, k, v, dO=None, scale=None, causal=True):
+    """The reference's own operators (compiled from its sources)."""
+    B, Hq, S, D = q.shape
+    Hkv = k.shape[1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    q, k, v = (np.ascontiguousarray(t, dtype=np.float32) for t in (q, k, v))
+    o = np.empty_like(q)
+    dq = dk = dv = None
+    if dO is not None:
+        dO = np.ascontiguousarray(dO, dtype=np.float32)
+        dq, dk, dv = np.empty_like(q), np.empty_like(k), np.empty_like(v)
+    tf, tb, held = C.c_double(), C.c_double(), C.c_int64()
+    rc = ref().mftref_composite(q, k, v, _ptr(dO), B, Hq, Hkv, S, D, float(scale), int(causal),
+                                _ptr(o), _ptr(dq), _ptr(dk), _ptr(dv),
+                                C.byref(tf), C.byref(tb), C.byref(held))
+    if rc != 0:
+        raise RuntimeError("reference composite raised")
+    return dict(o=o, dq=dq, dk=dk, dv=dv, t_fwd=tf.value, t_bwd=tb.value, held_bytes=held.value)
+
+
+def ref_memeff_nograd(q, k, v, scale=None, causal=True):
+    B, H, S, D = q.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    o = np.empty_like(q)
+    rc = ref().mftref_memeff_nograd(np.ascontiguousarray(q), np.ascontiguousarray(k),
+                                    np.ascontiguousarray(v), B, H, S, D, float(scale), int(causal), o)
+    if rc != 0:
+        raise RuntimeError("reference memory_efficient_attention raised")
+    return o
+
+
+def ref_repeat_kv(kv, r, g=None):
+    B, H, S, D = kv.shape
+    out = np.empty((B, H * r, S, D), np.float32)
+    dkv = np.empty_like(kv) if g is not None else None
+    rc = ref().mftref_repeat_kv(np.ascontiguousarray(kv),
+                                _ptr(None if g is None else np.ascontiguousarray(g)),
+                                B, H, S, D, r, out, _ptr(dkv))
+    if rc != 0:
+        raise RuntimeError("reference repeat_kv_heads raised")
+    return out, dkv
+
+
+# ------------------------------------------------------------------ metrics
+def max_rel(x, ref) -> float:
+    """max_i |x_i - ref_i| / max_i |ref_i| (the tolerance measure of the build)."""
+    x = np.asarray(x, np.float64)
+    ref = np.asarray(ref, np.float64)
+    den = np.max(np.abs(ref))
+    num = np.max(np.abs(x - ref))
+    return float(num / den) if den > 0 else float(num)
+
+
+def rel_l2(x, ref) -> float:
+    """||x - ref||_2 / ||ref||_2, the reference tests' rel_diff
+    (optim/test_qkt_softmax_grad.cpp:11-24)."""
+    x = np.asarray(x, np.float64)
+    ref = np.asarray(ref, np.float64)
+    nb = np.sum(ref * ref)
+    nd = np.sum((x - ref) ** 2)
+    return float(math.sqrt(nd / nb)) if nb > 0 else float(math.sqrt(nd))

@@ -1,0 +1,180 @@
+// ref_harness — C entry points over the REAL reference operators.
+//
+// TEST INFRASTRUCTURE ONLY.  oracle/Makefile compiles this file together with
+// the reference's own sources (read in place under /root/reference, never
+// copied) into oracle/_ref/libmftref.so.  It is used to
+//   * pin the restatement in refcpu.cpp bit for bit (tests/test_oracle.py),
+//   * write the golden fixtures (tests/golden/make_golden.py), and
+//   * time the reference CPU path beside the GPU (bench.py cpu_baseline).
+//
+// The graph built here is the one the reference's model code builds for
+// attention (graph/gemma_model.cpp:481-505, graph/qwen_model.cpp:302-318,
+// core/memory_efficient_attention.cpp:23-43):
+//   repeat_kv_heads -> transpose -> matmul -> mul(scale) -> add(causal mask)
+//   -> softmax -> matmul, then autograd::Engine::run_backward({out}, {dO}).
+#include "core/autograd_engine.h"
+#include "core/memory_efficient_attention.h"
+#include "core/memory_manager.h"
+#include "core/ops.h"
+
+#include <chrono>
+#include <cstring>
+#include <exception>
+#include <iostream>
+
+using namespace ops;
+
+namespace {
+
+TensorPtr from_host(const float* src, const std::vector<int64_t>& shape, bool requires_grad) {
+    auto t = zeros(shape, kFloat32, kCPU);
+    std::memcpy(t->data<float>(), src, sizeof(float) * static_cast<size_t>(t->numel()));
+    t->set_requires_grad(requires_grad);
+    return t;
+}
+
+void to_host(const TensorPtr& t, float* dst) {
+    if (!dst) return;
+    if (!t) return;
+    std::memcpy(dst, t->data<float>(), sizeof(float) * static_cast<size_t>(t->numel()));
+}
+
+double now_s() {
+    return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+}  // namespace
+
+extern "C" {
+
+// Returns 0 on success.  Timings in seconds; held_bytes = MemoryManager bytes
+// in use after the forward minus before it (what the autograd graph keeps
+// alive until backward), the reference's saved-activation measure.
+int mftref_composite(const float* q, const float* k, const float* v, const float* dO,
+                     int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
+                     float scale, int causal,
+                     float* o, float* dq, float* dk, float* dv,
+                     double* t_fwd, double* t_bwd, int64_t* held_bytes) {
+    try {
+        const bool grad = dO != nullptr;
+        auto qt = from_host(q, {B, Hq, S, D}, grad);
+        auto kt = from_host(k, {B, Hkv, S, D}, grad);
+        auto vt = from_host(v, {B, Hkv, S, D}, grad);
+        TensorPtr gt;
+        if (grad) gt = from_host(dO, {B, Hq, S, D}, false);
+        const size_t before = MemoryManager::instance().get_memory_usage();
+
+        const double t0 = now_s();
+        TensorPtr k_use = kt, v_use = vt;
+        if (Hq != Hkv) {
+            const int rep = static_cast<int>(Hq / Hkv);
+            k_use = repeat_kv_heads(kt, rep);
+            v_use = repeat_kv_heads(vt, rep);
+        }
+        auto k_t = transpose(k_use, 2, 3);
+        auto scores = mul(matmul(qt, k_t), scale);
+        if (causal) scores = add(scores, create_causal_mask(static_cast<int>(S), kFloat32, kCPU));
+        auto probs = softmax(scores, -1);
+        auto out = matmul(probs, v_use);
+        const double t1 = now_s();
+        const size_t after = MemoryManager::instance().get_memory_usage();
+        // Drop the local handles that are not graph-held so that the count
+        // below reflects what the graph itself keeps.
+        k_t.reset(); scores.reset(); probs.reset(); k_use.reset(); v_use.reset();
+        to_host(out, o);
+        if (t_fwd) *t_fwd = t1 - t0;
+        if (held_bytes) *held_bytes = static_cast<int64_t>(after) - static_cast<int64_t>(before);
+
+        if (grad) {
+            const double t2 = now_s();
+            autograd::Engine::instance().run_backward({out}, {gt});
+            const double t3 = now_s();
+            if (t_bwd) *t_bwd = t3 - t2;
+            to_host(qt->grad(), dq);
+            to_host(kt->grad(), dk);
+            to_host(vt->grad(), dv);
+        } else if (t_bwd) {
+            *t_bwd = 0.0;
+        }
+        autograd::Engine::instance().clear_graph();
+        return 0;
+    } catch (const std::exception& e) {
+        std::cerr << "[mftref_composite] " << e.what() << std::endl;
+        return -1;
+    }
+}
+
+// ops::memory_efficient_attention with no input requiring grad: the
+// reference's streaming path (core/memory_efficient_attention.cpp:110-200).
+int mftref_memeff_nograd(const float* q, const float* k, const float* v,
+                         int64_t B, int64_t H, int64_t S, int64_t D,
+                         float scale, int causal, float* o) {
+    try {
+        auto qt = from_host(q, {B, H, S, D}, false);
+        auto kt = from_host(k, {B, H, S, D}, false);
+        auto vt = from_host(v, {B, H, S, D}, false);
+        MemoryEfficientAttentionConfig cfg;
+        cfg.use_causal_mask = causal != 0;
+        cfg.scale = scale;
+        auto out = memory_efficient_attention(qt, kt, vt, nullptr, cfg);
+        to_host(out, o);
+        return 0;
+    } catch (const std::exception& e) {
+        std::cerr << "[mftref_memeff_nograd] " << e.what() << std::endl;
+        return -1;
+    }
+}
+
+// ops::memory_efficient_attention with inputs requiring grad: the reference
+// falls back to the composite (core/memory_efficient_attention.cpp:106-108);
+// gradients come from Engine::run_backward.
+int mftref_memeff_grad(const float* q, const float* k, const float* v, const float* dO,
+                       int64_t B, int64_t H, int64_t S, int64_t D,
+                       float scale, int causal,
+                       float* o, float* dq, float* dk, float* dv) {
+    try {
+        auto qt = from_host(q, {B, H, S, D}, true);
+        auto kt = from_host(k, {B, H, S, D}, true);
+        auto vt = from_host(v, {B, H, S, D}, true);
+        auto gt = from_host(dO, {B, H, S, D}, false);
+        MemoryEfficientAttentionConfig cfg;
+        cfg.use_causal_mask = causal != 0;
+        cfg.scale = scale;
+        auto out = memory_efficient_attention(qt, kt, vt, nullptr, cfg);
+        to_host(out, o);
+        autograd::Engine::instance().run_backward({out}, {gt});
+        to_host(qt->grad(), dq);
+        to_host(kt->grad(), dk);
+        to_host(vt->grad(), dv);
+        autograd::Engine::instance().clear_graph();
+        return 0;
+    } catch (const std::exception& e) {
+        std::cerr << "[mftref_memeff_grad] " << e.what() << std::endl;
+        return -1;
+    }
+}
+
+// repeat_kv_heads forward and its Engine backward (RepeatKVHeadsBackward).
+int mftref_repeat_kv(const float* kv, const float* g, int64_t B, int64_t Hkv, int64_t S,
+                     int64_t D, int64_t r, float* out, float* dkv) {
+    try {
+        auto kt = from_host(kv, {B, Hkv, S, D}, g != nullptr);
+        auto rep = repeat_kv_heads(kt, static_cast<int>(r));
+        to_host(rep, out);
+        if (g) {
+            auto gt = from_host(g, {B, Hkv * r, S, D}, false);
+            autograd::Engine::instance().run_backward({rep}, {gt});
+            to_host(kt->grad(), dkv);
+        }
+        autograd::Engine::instance().clear_graph();
+        return 0;
+    } catch (const std::exception& e) {
+        std::cerr << "[mftref_repeat_kv] " << e.what() << std::endl;
+        return -1;
+    }
+}
+
+// The reference's bf16 rounding (core/dtype.h:114-121), for pinning refcpu's.
+uint16_t mftref_f32_to_bf16_bits(float x) { return float32_to_bf16_bits(x); }
+
+}  // extern "C"

@@ -1,0 +1,371 @@
+// refcpu — CPU restatement of MobileFineTuner's attention composite.
+//
+// TEST INFRASTRUCTURE ONLY: the parity oracle and the CPU baseline.  Nothing
+// in the product (libmft_attn.so, the finetune_ops adapter) links this file.
+//
+// Build: oracle/Makefile (g++ -O2 -std=c++17 -ffp-contract=off, no -march),
+// the same flags the reference build uses, so that each float operation below
+// rounds exactly as the reference's does.
+//
+// Pinning (what checks this file): tests/test_oracle.py compares it bit for
+// bit with the reference compiled from its own sources (oracle/_ref) and with
+// the golden fixtures in tests/golden/, and against the fp64 brute force and
+// closed-form invariants (softmax rows sum to 1, O_0 = V_0 under the causal
+// mask, sum_keys dV = sum_queries dO, GQA group sums).
+#include "refcpu.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+namespace {
+
+uint64_t splitmix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    uint64_t z = x;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// C[M,N] = A[M,K] * B[K,N], all row-major.  Every C[i][j] starts at 0.0f and
+// accumulates a[i][k]*b[k][j] for k = 0..K-1 in increasing order, one rounding
+// for the product and one for the add: the arithmetic of the reference's
+// matmul_fallback_nn (core/ops.cpp:61-84).  The k-blocking only changes the
+// memory traversal, never the order of additions into one C element.
+void mm_nn(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K) {
+    std::fill(C, C + M * N, 0.0f);
+    constexpr int64_t KB = 32;
+    for (int64_t k0 = 0; k0 < K; k0 += KB) {
+        const int64_t k1 = std::min(K, k0 + KB);
+        for (int64_t i = 0; i < M; ++i) {
+            float* c = C + i * N;
+            const float* a = A + i * K;
+            for (int64_t kk = k0; kk < k1; ++kk) {
+                const float av = a[kk];
+                const float* b = B + kk * N;
+                for (int64_t j = 0; j < N; ++j) c[j] += av * b[j];
+            }
+        }
+    }
+}
+
+// Materialised 2-D transpose, as ops::transpose does for the last two dims
+// (core/ops.cpp:990-1072).  Pure data movement.
+void transpose2d(const float* src, float* dst, int64_t R, int64_t C) {
+    for (int64_t r = 0; r < R; ++r)
+        for (int64_t c = 0; c < C; ++c) dst[c * R + r] = src[r * C + c];
+}
+
+}  // namespace
+
+extern "C" {
+
+double orc_uniform(uint64_t seed, uint32_t stream, uint64_t counter) {
+    const uint64_t z = splitmix64(seed ^ (static_cast<uint64_t>(stream) << 32) ^ counter);
+    return (static_cast<double>(z >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+}
+
+void orc_fill_normal(float* x, int64_t n, uint64_t seed, uint32_t stream, float sigma) {
+    const double two_pi = 6.283185307179586476925286766559;
+    for (int64_t i = 0; i < n; i += 2) {
+        const double u1 = orc_uniform(seed, stream, static_cast<uint64_t>(i));
+        const double u2 = orc_uniform(seed, stream, static_cast<uint64_t>(i + 1));
+        const double rad = std::sqrt(-2.0 * std::log(u1));
+        x[i] = static_cast<float>(sigma * (rad * std::cos(two_pi * u2)));
+        if (i + 1 < n) x[i + 1] = static_cast<float>(sigma * (rad * std::sin(two_pi * u2)));
+    }
+}
+
+void orc_fill_mod(float* x, int64_t n, float a, int m, int o) {
+    // Same expression as the reference tests: a * ((i % m) - o), the integer
+    // part computed first and converted once.
+    for (int64_t i = 0; i < n; ++i) x[i] = a * static_cast<float>((i % m) - o);
+}
+
+void orc_stress_rows(float* k, int64_t B, int64_t Hkv, int64_t S, int64_t D,
+                     int64_t count, float factor, uint64_t seed) {
+    std::vector<int64_t> perm(static_cast<size_t>(S));
+    for (int64_t b = 0; b < B; ++b) {
+        for (int64_t h = 0; h < Hkv; ++h) {
+            for (int64_t s = 0; s < S; ++s) perm[s] = s;
+            const uint64_t base = static_cast<uint64_t>((b * Hkv + h) * S);
+            for (int64_t i = 0; i < count && i < S; ++i) {
+                const double u = orc_uniform(seed, 4u, base + static_cast<uint64_t>(i));
+                int64_t j = i + static_cast<int64_t>(u * static_cast<double>(S - i));
+                if (j >= S) j = S - 1;
+                std::swap(perm[i], perm[j]);
+                float* row = k + ((b * Hkv + h) * S + perm[i]) * D;
+                for (int64_t d = 0; d < D; ++d) row[d] *= factor;
+            }
+        }
+    }
+}
+
+uint16_t orc_f32_to_bf16_bits(float x) {
+    // Round-to-nearest-even by adding 0x7FFF + lsb, then truncating
+    // (core/dtype.h:114-121).
+    uint32_t bits;
+    std::memcpy(&bits, &x, sizeof(bits));
+    const uint32_t lsb = (bits >> 16) & 1u;
+    bits += 0x7FFFu + lsb;
+    return static_cast<uint16_t>(bits >> 16);
+}
+
+float orc_bf16_bits_to_f32(uint16_t b) {
+    const uint32_t bits = static_cast<uint32_t>(b) << 16;
+    float f;
+    std::memcpy(&f, &bits, sizeof(f));
+    return f;
+}
+
+void orc_round_bf16(float* x, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) x[i] = orc_bf16_bits_to_f32(orc_f32_to_bf16_bits(x[i]));
+}
+
+void orc_to_bf16_bits(const float* x, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_f32_to_bf16_bits(x[i]);
+}
+
+void orc_from_bf16_bits(const uint16_t* b, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_bf16_bits_to_f32(b[i]);
+}
+
+int orc_attn_composite(const float* q, const float* k, const float* v, const float* dO,
+                       int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
+                       float scale, int causal,
+                       float* o, float* lse, float* dq, float* dk, float* dv) {
+    if (!q || !k || !v || B <= 0 || Hq <= 0 || Hkv <= 0 || S <= 0 || D <= 0) return -1;
+    if (Hq % Hkv != 0) return -1;
+    const int64_t r = Hq / Hkv;
+    const int64_t SS = S * S, SD = S * D;
+    const bool want_bwd = dO != nullptr && (dq || dk || dv);
+
+    std::vector<float> kt(SD), sc(SS), p(SS), out(SD);
+    std::vector<float> vt, dp, pt, dmm, qt, dvr, dkt;
+    if (want_bwd) {
+        vt.resize(SD); dp.resize(SS); pt.resize(SS); dmm.resize(SS);
+        qt.resize(SD); dvr.resize(SD); dkt.resize(SD);
+    }
+    if (dk) std::fill(dk, dk + B * Hkv * SD, 0.0f);
+    if (dv) std::fill(dv, dv + B * Hkv * SD, 0.0f);
+
+    for (int64_t b = 0; b < B; ++b) {
+        for (int64_t h = 0; h < Hq; ++h) {
+            const int64_t hk = h / r;  // repeat_kv_heads: out_head = kv_h * r + rep
+            const float* Q = q + (b * Hq + h) * SD;
+            const float* K = k + (b * Hkv + hk) * SD;
+            const float* V = v + (b * Hkv + hk) * SD;
+
+            // scores = mul(matmul(q, transpose(k, 2, 3)), scale) [+ causal mask]
+            transpose2d(K, kt.data(), S, D);
+            mm_nn(Q, kt.data(), sc.data(), S, S, D);
+            for (int64_t i = 0; i < S; ++i) {
+                for (int64_t j = 0; j < S; ++j) {
+                    float x = sc[i * S + j] * scale;
+                    if (causal) x = x + (j > i ? -1e10f : 0.0f);
+                    sc[i * S + j] = x;
+                }
+            }
+            // softmax over the last dim: float max, exp, sequential float sum, divide.
+            for (int64_t i = 0; i < S; ++i) {
+                const float* row = sc.data() + i * S;
+                float* pr = p.data() + i * S;
+                const float mx = *std::max_element(row, row + S);
+                float sum = 0.0f;
+                for (int64_t j = 0; j < S; ++j) {
+                    pr[j] = std::exp(row[j] - mx);
+                    sum += pr[j];
+                }
+                for (int64_t j = 0; j < S; ++j) pr[j] /= sum;
+                if (lse) {
+                    // Not a reference output: the per-row log-sum-exp implied by
+                    // the same max and sum, for checking the kernel's saved LSE.
+                    lse[(b * Hq + h) * S + i] =
+                        static_cast<float>(static_cast<double>(mx) + std::log(static_cast<double>(sum)));
+                }
+            }
+            // context = matmul(probs, v)
+            mm_nn(p.data(), V, out.data(), S, D, S);
+            if (o) std::memcpy(o + (b * Hq + h) * SD, out.data(), sizeof(float) * SD);
+
+            if (!want_bwd) continue;
+            const float* G = dO + (b * Hq + h) * SD;
+            // MatmulBackward(probs, v): dP = G v^T, dV = P^T G.
+            transpose2d(V, vt.data(), S, D);
+            mm_nn(G, vt.data(), dp.data(), S, S, D);
+            transpose2d(p.data(), pt.data(), S, S);
+            mm_nn(pt.data(), G, dvr.data(), S, D, S);
+            // SoftmaxBackward: s = sum_j go*y in double, gx = y * (go - (float)s).
+            // AddBackward passes the gradient through; ScaleBackward multiplies.
+            for (int64_t i = 0; i < S; ++i) {
+                const float* y = p.data() + i * S;
+                const float* go = dp.data() + i * S;
+                double s = 0.0;
+                for (int64_t j = 0; j < S; ++j)
+                    s += static_cast<double>(go[j]) * static_cast<double>(y[j]);
+                const float sf = static_cast<float>(s);
+                for (int64_t j = 0; j < S; ++j) {
+                    const float gx = y[j] * (go[j] - sf);
+                    dmm[i * S + j] = gx * scale;
+                }
+            }
+            // MatmulBackward(q, k^T): dq = dMM (k^T)^T = dMM k, dk^T = q^T dMM.
+            if (dq) mm_nn(dmm.data(), K, dq + (b * Hq + h) * SD, S, D, S);
+            if (dk) {
+                transpose2d(Q, qt.data(), S, D);
+                mm_nn(qt.data(), dmm.data(), dkt.data(), D, S, S);
+                float* dst = dk + (b * Hkv + hk) * SD;
+                // TransposeBackward, then RepeatKVHeadsBackward's float += in rep order.
+                for (int64_t j = 0; j < S; ++j)
+                    for (int64_t d = 0; d < D; ++d) dst[j * D + d] += dkt[d * S + j];
+            }
+            if (dv) {
+                float* dst = dv + (b * Hkv + hk) * SD;
+                for (int64_t i = 0; i < SD; ++i) dst[i] += dvr[i];
+            }
+        }
+    }
+    return 0;
+}
+
+int orc_attn_streaming(const float* q, const float* k, const float* v,
+                       int64_t B, int64_t H, int64_t S, int64_t D,
+                       float scale, int causal, float* o) {
+    if (!q || !k || !v || !o || B <= 0 || H <= 0 || S <= 0 || D <= 0) return -1;
+    std::vector<float> scores(static_cast<size_t>(S));
+    for (int64_t bh = 0; bh < B * H; ++bh) {
+        const float* Q = q + bh * S * D;
+        const float* K = k + bh * S * D;
+        const float* V = v + bh * S * D;
+        float* O = o + bh * S * D;
+        for (int64_t i = 0; i < S; ++i) {
+            const float* qr = Q + i * D;
+            float mx = -INFINITY;
+            for (int64_t j = 0; j < S; ++j) {
+                const float* kr = K + j * D;
+                float dot = 0.0f;
+                for (int64_t d = 0; d < D; ++d) dot += qr[d] * kr[d];
+                float s = dot * scale;
+                if (causal && j > i) s = -1e10f;
+                scores[j] = s;
+                mx = std::max(mx, s);
+            }
+            float* orow = O + i * D;
+            std::fill(orow, orow + D, 0.0f);
+            double sum_exp = 0.0;
+            for (int64_t j = 0; j < S; ++j) sum_exp += std::exp(scores[j] - mx);
+            const float inv = 1.0f / static_cast<float>(sum_exp);
+            for (int64_t j = 0; j < S; ++j) {
+                const float w = std::exp(scores[j] - mx) * inv;
+                const float* vr = V + j * D;
+                for (int64_t d = 0; d < D; ++d) orow[d] += w * vr[d];
+            }
+        }
+    }
+    return 0;
+}
+
+int orc_attn_f64(const float* q, const float* k, const float* v, const float* dO,
+                 int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
+                 double scale, int causal,
+                 double* o, double* lse, double* dq, double* dk, double* dv) {
+    if (!q || !k || !v || B <= 0 || Hq <= 0 || Hkv <= 0 || S <= 0 || D <= 0) return -1;
+    if (Hq % Hkv != 0) return -1;
+    const int64_t r = Hq / Hkv, SD = S * D;
+    std::vector<double> P(S * S), dP(S * S);
+    if (dk) std::fill(dk, dk + B * Hkv * SD, 0.0);
+    if (dv) std::fill(dv, dv + B * Hkv * SD, 0.0);
+    for (int64_t b = 0; b < B; ++b) {
+        for (int64_t h = 0; h < Hq; ++h) {
+            const int64_t hk = h / r;
+            const float* Q = q + (b * Hq + h) * SD;
+            const float* K = k + (b * Hkv + hk) * SD;
+            const float* V = v + (b * Hkv + hk) * SD;
+            for (int64_t i = 0; i < S; ++i) {
+                const int64_t jn = causal ? i + 1 : S;
+                double mx = -INFINITY;
+                for (int64_t j = 0; j < jn; ++j) {
+                    double s = 0.0;
+                    for (int64_t d = 0; d < D; ++d) s += double(Q[i * D + d]) * double(K[j * D + d]);
+                    P[i * S + j] = s * scale;
+                    mx = std::max(mx, P[i * S + j]);
+                }
+                double sum = 0.0;
+                for (int64_t j = 0; j < jn; ++j) {
+                    P[i * S + j] = std::exp(P[i * S + j] - mx);
+                    sum += P[i * S + j];
+                }
+                for (int64_t j = 0; j < jn; ++j) P[i * S + j] /= sum;
+                for (int64_t j = jn; j < S; ++j) P[i * S + j] = 0.0;
+                if (lse) lse[(b * Hq + h) * S + i] = mx + std::log(sum);
+                if (o) {
+                    for (int64_t d = 0; d < D; ++d) {
+                        double acc = 0.0;
+                        for (int64_t j = 0; j < jn; ++j) acc += P[i * S + j] * double(V[j * D + d]);
+                        o[(b * Hq + h) * SD + i * D + d] = acc;
+                    }
+                }
+            }
+            if (!dO) continue;
+            const float* G = dO + (b * Hq + h) * SD;
+            for (int64_t i = 0; i < S; ++i) {
+                double delta = 0.0;
+                for (int64_t j = 0; j < S; ++j) {
+                    double s = 0.0;
+                    for (int64_t d = 0; d < D; ++d) s += double(G[i * D + d]) * double(V[j * D + d]);
+                    dP[i * S + j] = s;
+                    delta += s * P[i * S + j];
+                }
+                for (int64_t j = 0; j < S; ++j) dP[i * S + j] = P[i * S + j] * (dP[i * S + j] - delta);
+            }
+            for (int64_t i = 0; i < S; ++i) {
+                for (int64_t d = 0; d < D; ++d) {
+                    if (dq) {
+                        double acc = 0.0;
+                        for (int64_t j = 0; j < S; ++j) acc += dP[i * S + j] * double(K[j * D + d]);
+                        dq[(b * Hq + h) * SD + i * D + d] = acc * scale;
+                    }
+                }
+            }
+            for (int64_t j = 0; j < S; ++j) {
+                for (int64_t d = 0; d < D; ++d) {
+                    double ak = 0.0, av = 0.0;
+                    for (int64_t i = 0; i < S; ++i) {
+                        ak += dP[i * S + j] * double(Q[i * D + d]);
+                        av += P[i * S + j] * double(G[i * D + d]);
+                    }
+                    if (dk) dk[(b * Hkv + hk) * SD + j * D + d] += ak * scale;
+                    if (dv) dv[(b * Hkv + hk) * SD + j * D + d] += av;
+                }
+            }
+        }
+    }
+    return 0;
+}
+
+void orc_repeat_kv(const float* kv, float* out, int64_t B, int64_t Hkv, int64_t S,
+                   int64_t D, int64_t r) {
+    const int64_t SD = S * D;
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t h = 0; h < Hkv; ++h)
+            for (int64_t rep = 0; rep < r; ++rep)
+                std::memcpy(out + (b * Hkv * r + h * r + rep) * SD, kv + (b * Hkv + h) * SD,
+                            sizeof(float) * SD);
+}
+
+void orc_repeat_kv_backward(const float* g, float* dkv, int64_t B, int64_t Hkv,
+                            int64_t S, int64_t D, int64_t r) {
+    const int64_t SD = S * D;
+    std::fill(dkv, dkv + B * Hkv * SD, 0.0f);
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t h = 0; h < Hkv; ++h)
+            for (int64_t rep = 0; rep < r; ++rep) {
+                const float* src = g + (b * Hkv * r + h * r + rep) * SD;
+                float* dst = dkv + (b * Hkv + h) * SD;
+                for (int64_t i = 0; i < SD; ++i) dst[i] += src[i];
+            }
+}
+
+}  // extern "C"

@@ -1,0 +1,90 @@
+/*
+ * refcpu — CPU restatement of MobileFineTuner's causal attention composite.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity oracle for the HIP
+ * kernels and the CPU baseline timed by bench.py.  Only tests/, the smoke()
+ * entry and bench.py's cpu_baseline leg may load it; the product library
+ * (libmft_attn.so) never links or calls it.
+ *
+ * Every function restates a reference operator on plain float arrays, with
+ * the same floating-point operation order, so that on the same compiler the
+ * results are bit-identical to the reference build (checked against
+ * oracle/_ref and the golden fixtures under tests/golden/).
+ *
+ * Layout of every tensor: contiguous row-major [B, H, S, D] (fp32).
+ */
+#ifndef MFT_ORACLE_REFCPU_H
+#define MFT_ORACLE_REFCPU_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- deterministic input generator (the reference randn is unseeded) ---- */
+/* splitmix64(seed ^ (stream << 32) ^ counter) -> 53-bit uniform in (0,1). */
+double orc_uniform(uint64_t seed, uint32_t stream, uint64_t counter);
+/* x[i] = sigma * N(0,1) by Box-Muller over consecutive uniform pairs. */
+void orc_fill_normal(float* x, int64_t n, uint64_t seed, uint32_t stream, float sigma);
+/* Deterministic closed-form fill used by the reference unit tests:
+ * x[i] = a * ((i % m) - o)   (e.g. optim/test_qkt_softmax_grad.cpp:41-42). */
+void orc_fill_mod(float* x, int64_t n, float a, int m, int o);
+/* K-row stress of config C4: per (b, kv) pick `count` distinct rows by a
+ * partial Fisher-Yates shuffle on stream 4 and multiply them by `factor`. */
+void orc_stress_rows(float* k, int64_t B, int64_t Hkv, int64_t S, int64_t D,
+                     int64_t count, float factor, uint64_t seed);
+
+/* ---- bf16 (core/dtype.h:114-128) ---- */
+uint16_t orc_f32_to_bf16_bits(float x);
+float orc_bf16_bits_to_f32(uint16_t b);
+/* Round every value to the nearest bf16 (RNE), keeping it as float. */
+void orc_round_bf16(float* x, int64_t n);
+void orc_to_bf16_bits(const float* x, uint16_t* out, int64_t n);
+void orc_from_bf16_bits(const uint16_t* b, float* out, int64_t n);
+
+/* ---- the reference composite, forward + backward ----
+ * Restates, per (b, h):
+ *   repeat_kv_heads  (core/ops.cpp:2260-2335)       q-head h uses kv head h / (Hq/Hkv)
+ *   transpose+matmul (core/ops.cpp:61-84, 619-822)  S = Q K^T, float, sequential over d
+ *   mul(scale)       (core/ops.cpp:550-560)
+ *   add(causal mask) (core/ops.cpp:415-442, 2167-2180)  -1e10 above the diagonal
+ *   softmax(-1)      (core/ops.cpp:1307-1363)       float max / exp / sum / divide
+ *   matmul(P, V)     (core/ops.cpp:61-84)
+ * and the Engine backward of that graph (core/autograd_engine.cpp:144-273):
+ *   MatmulBackward   (core/backward_functions.cpp:94-147)
+ *   SoftmaxBackward  (core/backward_functions.cpp:306-349) double row dot
+ *   AddBackward/ScaleBackward (core/backward_functions.cpp:36-72, 981-985)
+ *   TransposeBackward, RepeatKVHeadsBackward (core/backward_functions.cpp:422-426, 693-726)
+ * Any of o, dO/dq/dk/dv may be NULL to skip that part (dO NULL skips the
+ * backward).  dk, dv are [B, Hkv, S, D] (summed over the repeated heads).
+ * Returns 0 on success, -1 on bad arguments. */
+int orc_attn_composite(const float* q, const float* k, const float* v, const float* dO,
+                       int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
+                       float scale, int causal,
+                       float* o, float* lse, float* dq, float* dk, float* dv);
+
+/* The no-grad streaming path of ops::memory_efficient_attention
+ * (core/memory_efficient_attention.cpp:110-200): double sum_exp, float
+ * inv_sum, float context accumulation.  MHA only (Hq == Hkv), as there. */
+int orc_attn_streaming(const float* q, const float* k, const float* v,
+                       int64_t B, int64_t H, int64_t S, int64_t D,
+                       float scale, int causal, float* o);
+
+/* Independent fp64 brute-force attention (textbook formula, no reference
+ * op order) used as a third check.  Outputs are double. */
+int orc_attn_f64(const float* q, const float* k, const float* v, const float* dO,
+                 int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
+                 double scale, int causal,
+                 double* o, double* lse, double* dq, double* dk, double* dv);
+
+/* repeat_kv_heads forward / RepeatKVHeadsBackward on float arrays. */
+void orc_repeat_kv(const float* kv, float* out, int64_t B, int64_t Hkv, int64_t S,
+                   int64_t D, int64_t r);
+void orc_repeat_kv_backward(const float* g, float* dkv, int64_t B, int64_t Hkv,
+                            int64_t S, int64_t D, int64_t r);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
