@@ -1,0 +1,116 @@
+/*
+ * mft/attention.h — C ABI of the MI355X (gfx950) fused causal GQA attention.
+ *
+ * This is the drop-in boundary for MobileFineTuner's attention hot path.  It
+ * replaces, for tensors resident on the GPU:
+ *
+ *   ops::memory_efficient_attention(q, k, v, mask, cfg)
+ *       operator/finetune_ops/core/memory_efficient_attention.h:49-55
+ *       (its grad path is the composite of core/memory_efficient_attention.cpp:23-43)
+ *   the composite the model graphs call directly,
+ *       repeat_kv_heads -> transpose -> matmul -> mul(scale) -> add(mask)
+ *       -> softmax -> matmul
+ *       graph/gemma_model.cpp:481-505, graph/qwen_model.cpp:302-318
+ *   and its Engine backward (MatmulBackward, SoftmaxBackward, ScaleBackward,
+ *   AddBackward, TransposeBackward, RepeatKVHeadsBackward;
+ *       core/backward_functions.cpp:36-147, 306-349, 422-426, 693-726, 981-985)
+ *   ops::repeat_kv_heads / RepeatKVHeadsBackward
+ *       core/ops.h:177, core/ops.cpp:2260-2335, core/backward_functions.cpp:693-726
+ *
+ * Conventions
+ *   - Tensors are contiguous row-major [B, H, S, D] in device memory (the
+ *     reference Tensor is contiguous row-major, core/tensor.h:78-237).
+ *   - q, o, dO have Hq heads; k, v, dk, dv have Hkv heads; Hq % Hkv == 0 and
+ *     q-head h reads kv head h / (Hq / Hkv) (core/ops.cpp:2283-2284).
+ *   - Element type of q, k, v, o, dO: MFT_F32 or MFT_BF16.  lse, dq, dk, dv
+ *     are always fp32: the reference Engine accumulates gradients as float
+ *     only (core/autograd_engine.cpp:135-140).
+ *   - lse[b, h, i] = log(sum_j exp(scale * q_i . k_j)) over the visible keys
+ *     (natural log, fp32, [B, Hq, S]).  The backward recomputes the softmax
+ *     from it; no S x S tensor is ever stored.
+ *   - All pointers are caller-owned device memory; the library allocates
+ *     nothing.  Work is enqueued on `stream` (NULL = the null stream) and is
+ *     ordered there; the calls return before the GPU finishes.
+ *   - Errors: a non-zero mft_status, and mft_last_error() returns a
+ *     thread-local message.  The C++ adapter rethrows it as the reference's
+ *     TensorError / std::runtime_error (core/memory_efficient_attention.cpp:86-99).
+ *   - Thread safety: stateless; calls on different streams may overlap.
+ */
+#ifndef MFT_ATTENTION_H
+#define MFT_ATTENTION_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    MFT_OK = 0,
+    MFT_ERR_INVALID_ARG = 1, /* null pointer, bad shape, Hq % Hkv != 0 ...          */
+    MFT_ERR_UNSUPPORTED = 2, /* valid request the kernels do not cover (D > 256)     */
+    MFT_ERR_HIP = 3          /* a HIP runtime call failed (launch error, ...)         */
+} mft_status;
+
+/* Values match ops::DType (core/dtype.h:9-18): kFloat32 = 0, kBFloat16 = 2. */
+typedef enum { MFT_F32 = 0, MFT_BF16 = 2 } mft_dtype;
+
+typedef struct {
+    int64_t B, Hq, Hkv, S, D; /* batch, query heads, kv heads, sequence, head dim     */
+    float scale;              /* > 0: softmax scale; <= 0: 1/sqrt(D), as
+                                 MemoryEfficientAttentionConfig::scale
+                                 (core/memory_efficient_attention.h:26-31, .cpp:103) */
+    int32_t causal;           /* 1: key j visible to query i iff j <= i (the -1e10
+                                 mask of core/ops.cpp:2167-2180); 0: all visible      */
+    mft_dtype dtype;          /* element type of q, k, v, o, dO                        */
+} mft_attn_desc;
+
+/* Workspace bytes the calls need (fwd: 0; bwd: per-row softmax terms and,
+ * when dK/dV are split across head groups, their fp32 partials).
+ * Replaces: nothing (the reference allocates from its pool implicitly). */
+mft_status mft_attn_workspace_size(const mft_attn_desc* desc, size_t* fwd_bytes,
+                                   size_t* bwd_bytes);
+
+/* Forward: o = softmax(scale * q k^T [causal]) v, and lse.
+ * Replaces the composite forward / memory_efficient_attention
+ * (core/memory_efficient_attention.cpp:73-203 and :23-43).
+ * lse may be NULL when no backward will follow (no-grad path). */
+mft_status mft_attn_fwd(const mft_attn_desc* desc, const void* q, const void* k,
+                        const void* v, void* o, float* lse, void* workspace,
+                        hipStream_t stream);
+
+/* Backward: dq, dk, dv of sum(o * dO), recomputing P from lse.
+ * dk, dv are [B, Hkv, S, D]: already summed over the Hq/Hkv query heads that
+ * share each kv head (RepeatKVHeadsBackward folded in).
+ * Replaces Engine::run_backward over the composite's nodes
+ * (core/autograd_engine.cpp:144-273 with the backward functions cited above). */
+mft_status mft_attn_bwd(const mft_attn_desc* desc, const void* q, const void* k,
+                        const void* v, const void* o, const void* dO, const float* lse,
+                        float* dq, float* dk, float* dv, void* workspace,
+                        hipStream_t stream);
+
+/* repeat_kv_heads forward: out[b, h*r + i] = kv[b, h] for i < r
+ * ([B,Hkv,S,D] -> [B,Hkv*r,S,D], element type `dtype`).
+ * Replaces ops::repeat_kv_heads (core/ops.cpp:2260-2335). */
+mft_status mft_repeat_kv_fwd(const void* kv, void* out, int64_t B, int64_t Hkv, int64_t S,
+                             int64_t D, int64_t r, mft_dtype dtype, hipStream_t stream);
+
+/* repeat_kv_heads backward: dkv[b, h] = sum_{i<r} g[b, h*r + i] (fp32,
+ * float accumulation in i order).
+ * Replaces RepeatKVHeadsBackward::apply (core/backward_functions.cpp:693-726). */
+mft_status mft_repeat_kv_bwd(const float* g, float* dkv, int64_t B, int64_t Hkv, int64_t S,
+                             int64_t D, int64_t r, hipStream_t stream);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* mft_last_error(void);
+
+/* Library version, for the bindings' sanity check. */
+int mft_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MFT_ATTENTION_H */

@@ -1,0 +1,112 @@
+"""torch-tensor plumbing over the C ABI (device memory and streams only).
+
+The arithmetic is entirely in libmft_attn.so.  These helpers allocate the
+outputs and the workspace as torch tensors on the current device and enqueue
+the C-ABI calls on torch's current stream, so tests and the benchmark can drive
+the kernels without writing HIP host code.  There is no fallback: a missing
+library or a non-GPU tensor raises.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import capi
+
+_DT = {torch.float32: capi.MFT_F32, torch.bfloat16: capi.MFT_BF16}
+
+
+def _check(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor (the fused attention has no CPU path)")
+    if t.dim() != 4:
+        raise ValueError(f"{name} must be 4D [B,H,S,D]")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _desc(q, k, scale, causal):
+    if q.dtype not in _DT:
+        raise ValueError(f"unsupported dtype {q.dtype}")
+    B, Hq, S, D = q.shape
+    return capi.desc(B, Hq, k.shape[1], S, D, scale, causal, _DT[q.dtype])
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def workspace_bytes(q, k, scale=-1.0, causal=True):
+    return capi.workspace_size(_desc(q, k, scale, causal))[1]
+
+
+def attention_forward(q, k, v, scale: float = -1.0, causal: bool = True, want_lse: bool = True):
+    """o, lse = fused attention forward (lse None when want_lse is False)."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _check(t, n)
+    if k.dtype != q.dtype or v.dtype != q.dtype or k.shape != v.shape:
+        raise ValueError("q, k, v must share dtype and k, v must have equal shapes")
+    if k.shape[0] != q.shape[0] or k.shape[2:] != q.shape[2:]:
+        raise ValueError("k/v must be [B, Hkv, S, D] with q's B, S, D")
+    d = _desc(q, k, scale, causal)
+    o = torch.empty_like(q)
+    lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device) if want_lse else None
+    capi.attn_fwd(d, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                  lse.data_ptr() if lse is not None else None, None, _stream())
+    return o, lse
+
+
+def attention_backward(q, k, v, o, dO, lse, scale: float = -1.0, causal: bool = True, workspace=None):
+    """dq, dk, dv (fp32; dk, dv already summed over the GQA group)."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (o, "o"), (dO, "dO"), (lse, "lse")):
+        if not t.is_cuda or not t.is_contiguous():
+            raise ValueError(f"{n} must be a contiguous GPU tensor")
+    if dO.dtype != q.dtype or o.dtype != q.dtype or lse.dtype != torch.float32:
+        raise ValueError("o and dO must have q's dtype; lse must be float32")
+    d = _desc(q, k, scale, causal)
+    nbytes = capi.workspace_size(d)[1]
+    if workspace is None or workspace.numel() < nbytes:
+        workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    dq = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    dk = torch.empty(k.shape, dtype=torch.float32, device=q.device)
+    dv = torch.empty(v.shape, dtype=torch.float32, device=q.device)
+    capi.attn_bwd(d, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dO.data_ptr(),
+                  lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                  workspace.data_ptr(), _stream())
+    return dq, dk, dv
+
+
+def repeat_kv(kv: torch.Tensor, r: int) -> torch.Tensor:
+    _check(kv, "kv")
+    B, H, S, D = kv.shape
+    out = torch.empty((B, H * r, S, D), dtype=kv.dtype, device=kv.device)
+    capi.repeat_kv_fwd(kv.data_ptr(), out.data_ptr(), B, H, S, D, r, _DT[kv.dtype], _stream())
+    return out
+
+
+def repeat_kv_backward(g: torch.Tensor, r: int) -> torch.Tensor:
+    _check(g, "g")
+    if g.dtype != torch.float32:
+        raise ValueError("repeat_kv backward takes fp32 gradients")
+    B, Hr, S, D = g.shape
+    if Hr % r:
+        raise ValueError("repeat_factor does not divide head dimension")
+    out = torch.empty((B, Hr // r, S, D), dtype=torch.float32, device=g.device)
+    capi.repeat_kv_bwd(g.data_ptr(), out.data_ptr(), B, Hr // r, S, D, r, _stream())
+    return out
+
+
+class FusedAttention(torch.autograd.Function):
+    """Autograd node that saves only q, k, v, o and the row log-sum-exp."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, scale=-1.0, causal=True):
+        o, lse = attention_forward(q, k, v, scale, causal)
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.scale, ctx.causal = scale, causal
+        return o
+
+    @staticmethod
+    def backward(ctx, dO):
+        q, k, v, o, lse = ctx.saved_tensors
+        dq, dk, dv = attention_backward(q, k, v, o, dO.contiguous().to(q.dtype), lse, ctx.scale, ctx.causal)
+        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None

@@ -1,0 +1,96 @@
+"""ctypes binding of the C ABI in ``include/mft/attention.h``.
+
+This is the binding a Python caller would use (the C++ finetune_ops adapter
+links the same library directly).  It raises when the library is missing: the
+HIP path is the only implementation, there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "lib", "libmft_attn.so")
+
+MFT_OK, MFT_ERR_INVALID_ARG, MFT_ERR_UNSUPPORTED, MFT_ERR_HIP = 0, 1, 2, 3
+MFT_F32, MFT_BF16 = 0, 2
+
+# Every symbol the header declares (checked by tests/test_capi.py).
+EXPORTS = (
+    "mft_attn_workspace_size", "mft_attn_fwd", "mft_attn_bwd",
+    "mft_repeat_kv_fwd", "mft_repeat_kv_bwd", "mft_last_error", "mft_version",
+)
+
+
+class AttnDesc(C.Structure):
+    _fields_ = [
+        ("B", C.c_int64), ("Hq", C.c_int64), ("Hkv", C.c_int64), ("S", C.c_int64), ("D", C.c_int64),
+        ("scale", C.c_float), ("causal", C.c_int32), ("dtype", C.c_int32),
+    ]
+
+
+class MftError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"[mft status {status}] {msg}")
+        self.status = status
+
+
+_lib = None
+
+
+def lib():
+    """Load libmft_attn.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m mobilefinetuner_amd.build`")
+    L = C.CDLL(LIB_PATH)
+    vp, i64 = C.c_void_p, C.c_int64
+    L.mft_version.restype = C.c_int
+    L.mft_last_error.restype = C.c_char_p
+    L.mft_attn_workspace_size.restype = C.c_int
+    L.mft_attn_workspace_size.argtypes = [C.POINTER(AttnDesc), C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+    L.mft_attn_fwd.restype = C.c_int
+    L.mft_attn_fwd.argtypes = [C.POINTER(AttnDesc), vp, vp, vp, vp, vp, vp, vp]
+    L.mft_attn_bwd.restype = C.c_int
+    L.mft_attn_bwd.argtypes = [C.POINTER(AttnDesc), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    L.mft_repeat_kv_fwd.restype = C.c_int
+    L.mft_repeat_kv_fwd.argtypes = [vp, vp, i64, i64, i64, i64, i64, C.c_int32, vp]
+    L.mft_repeat_kv_bwd.restype = C.c_int
+    L.mft_repeat_kv_bwd.argtypes = [vp, vp, i64, i64, i64, i64, i64, vp]
+    if L.mft_version() != 1:
+        raise RuntimeError("libmft_attn.so version mismatch")
+    _lib = L
+    return L
+
+
+def check(status: int) -> None:
+    if status != MFT_OK:
+        raise MftError(status, lib().mft_last_error().decode())
+
+
+def desc(B, Hq, Hkv, S, D, scale=-1.0, causal=True, dtype=MFT_BF16) -> AttnDesc:
+    return AttnDesc(int(B), int(Hq), int(Hkv), int(S), int(D), float(scale), int(bool(causal)), int(dtype))
+
+
+def workspace_size(d: AttnDesc):
+    f, b = C.c_size_t(), C.c_size_t()
+    check(lib().mft_attn_workspace_size(C.byref(d), C.byref(f), C.byref(b)))
+    return f.value, b.value
+
+
+def attn_fwd(d: AttnDesc, q, k, v, o, lse, workspace, stream) -> None:
+    check(lib().mft_attn_fwd(C.byref(d), q, k, v, o, lse, workspace, stream))
+
+
+def attn_bwd(d: AttnDesc, q, k, v, o, dO, lse, dq, dk, dv, workspace, stream) -> None:
+    check(lib().mft_attn_bwd(C.byref(d), q, k, v, o, dO, lse, dq, dk, dv, workspace, stream))
+
+
+def repeat_kv_fwd(kv, out, B, Hkv, S, D, r, dtype, stream) -> None:
+    check(lib().mft_repeat_kv_fwd(kv, out, B, Hkv, S, D, r, dtype, stream))
+
+
+def repeat_kv_bwd(g, dkv, B, Hkv, S, D, r, stream) -> None:
+    check(lib().mft_repeat_kv_bwd(g, dkv, B, Hkv, S, D, r, stream))

@@ -1,0 +1,620 @@
+// Fused causal GQA attention backward for gfx950.
+//
+// Replaces Engine::run_backward over the composite's nodes
+// (core/autograd_engine.cpp:144-273): MatmulBackward for P.V and Q.K^T
+// (core/backward_functions.cpp:94-147), SoftmaxBackward (:306-349),
+// ScaleBackward (:981-985), AddBackward (:36-72), TransposeBackward
+// (:422-426) and RepeatKVHeadsBackward (:693-726).  Nothing of size S x S is
+// read: P is recomputed from the saved row log-sum-exp, and the softmax row
+// term sum_j dP_ij P_ij is computed as delta_i = dO_i . O_i (equal in exact
+// arithmetic; the reference forms it in double from dP and P).
+//
+// Three kernels:
+//   prep  : delta[b,h,i] = sum_d dO[i,d] * O[i,d]                (HBM bound)
+//   dkdv  : one workgroup per (32*NW keys, kv head, head-group split); wave w
+//           owns 32 keys, one key per lane column.  It loops over the query
+//           heads of its group and over 32-row query blocks (causal: from its
+//           first key on), recomputing S = Q K^T and dP = dO V^T with keys
+//           along the accumulator columns, and accumulates
+//             dV^T += dO^T P,   dK^T += Q^T dS
+//           in registers.  GQA: the group's heads sum in registers, so dK/dV
+//           come out already reduced over repeat_kv (no atomics).  When the
+//           group is split across workgroups for parallelism, each split
+//           writes fp32 partials and `reduce` sums them in split order.
+//   dq    : one workgroup per (32*NW query rows, query head): recomputes S^T
+//           and dP^T with one query row per lane (like the forward) and
+//           accumulates dQ^T += K^T dS^T.  No atomics; deterministic.
+// bf16 inputs use v_mfma_f32_32x32x16_bf16 with fp32 accumulation; operands
+// that must be read along the reduction dimension are staged transposed in
+// LDS.  fp32 inputs use v_mfma_f32_32x32x2_f32 and need no transposes.
+#include "attn_common.h"
+#include "attn_kernels.h"
+
+namespace mft {
+namespace {
+
+struct BwdArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    const void* o;
+    const void* dO;
+    const float* lse;
+    float* dq;
+    float* dk;
+    float* dv;
+    float* delta;
+    float* part;
+    int64_t part_stride;  // B*Hkv*S*D
+    int64_t total_rows;   // B*Hq*S
+    int S, D, Hq, Hkv, group, splits, heads_per_split, n_tiles;
+    float scale, scale_log2;
+    int vec_ok, vec4_ok;
+};
+
+// ------------------------------------------------------------------ prep
+template <typename T, int DP>
+__global__ __launch_bounds__(256) void attn_bwd_prep_kernel(BwdArgs a) {
+    typedef typename Elt<T>::vec V;
+    constexpr int VEC = Elt<T>::VEC;
+    constexpr int TPR = DP / VEC;  // threads per row, a power of two <= 64
+    constexpr int RPB = 256 / TPR;
+    const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
+    const int c = threadIdx.x % TPR;
+    float acc = 0.f;
+    if (row < a.total_rows) {
+        const T* o = (const T*)a.o + row * a.D;
+        const T* g = (const T*)a.dO + row * a.D;
+        const V x = load_chunk<T>(o, c * VEC, a.D, true, a.vec_ok != 0);
+        const V y = load_chunk<T>(g, c * VEC, a.D, true, a.vec_ok != 0);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) acc += (float)x[i] * (float)y[i];
+    }
+#pragma unroll
+    for (int off = TPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+    if (row < a.total_rows && c == 0) a.delta[row] = acc;
+}
+
+// Output rows of dK / dV for this workgroup's split.
+__device__ __forceinline__ void dkdv_out_rows(const BwdArgs& a, int b, int hk, int split, int key,
+                                              float** dkp, float** dvp) {
+    const int64_t off = ((int64_t)(b * a.Hkv + hk) * a.S + key) * a.D;
+    if (a.splits == 1) {
+        *dkp = a.dk + off;
+        *dvp = a.dv + off;
+    } else {
+        *dkp = a.part + (int64_t)split * a.part_stride + off;
+        *dvp = a.part + (int64_t)(a.splits + split) * a.part_stride + off;
+    }
+}
+
+// ----------------------------------------------------------- dkdv (bf16)
+template <int DP, int NW, bool CAUSAL>
+__global__ __launch_bounds__(NW * 64) void attn_bwd_dkdv_bf16(BwdArgs a) {
+    constexpr int NC = DP / 16, NDT = DP / 32, NT = NW * 64, BNK = 32 * NW;
+    constexpr int QSTR = DP + 8;  // row-major 32-row tiles of Q and dO
+    constexpr int TSTR = 32 + 4;  // transposed tiles Q^T, dO^T: [DP][32 + 4]
+    __shared__ __attribute__((aligned(16))) bf16 Qs[32 * QSTR];
+    __shared__ __attribute__((aligned(16))) bf16 Gs[32 * QSTR];
+    __shared__ __attribute__((aligned(16))) bf16 Qt[DP * TSTR];
+    __shared__ __attribute__((aligned(16))) bf16 Gt[DP * TSTR];
+    __shared__ __attribute__((aligned(16))) float Ls[32];
+    __shared__ __attribute__((aligned(16))) float Dl[32];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
+    const int S = a.S, D = a.D;
+    const bool vec_ok = a.vec_ok != 0;
+    const int j0 = (int)blockIdx.x * BNK;
+    const int hk = (int)blockIdx.y / a.splits, split = (int)blockIdx.y % a.splits, b = blockIdx.z;
+    const int h_begin = hk * a.group + split * a.heads_per_split;
+    const int h_end = min(h_begin + a.heads_per_split, (hk + 1) * a.group);
+    const int wkey0 = j0 + 32 * w;
+    const int key = wkey0 + n;
+    const int keyc = key < S ? key : S - 1;
+
+    const bf16* K = (const bf16*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
+    const bf16* Vg = (const bf16*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
+    bf16x8 kf[NC], vf[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        kf[c] = load_chunk<bf16>(K + (int64_t)keyc * D, 16 * c + 8 * hh, D, key < S, vec_ok);
+        vf[c] = load_chunk<bf16>(Vg + (int64_t)keyc * D, 16 * c + 8 * hh, D, key < S, vec_ok);
+    }
+    f32x16 dk[NDT], dv[NDT];
+#pragma unroll
+    for (int i = 0; i < NDT; ++i) {
+        dk[i] = zero16();
+        dv[i] = zero16();
+    }
+
+    const int qstart = CAUSAL ? j0 : 0;
+    for (int h = h_begin; h < h_end; ++h) {
+        const bf16* Q = (const bf16*)a.q + (int64_t)(b * a.Hq + h) * S * D;
+        const bf16* G = (const bf16*)a.dO + (int64_t)(b * a.Hq + h) * S * D;
+        const float* lse = a.lse + (int64_t)(b * a.Hq + h) * S;
+        const float* dl = a.delta + (int64_t)(b * a.Hq + h) * S;
+        for (int qb = qstart; qb < S; qb += 32) {
+            __syncthreads();
+            {   // stage 32 query rows: row-major and transposed (4 rows x 8 columns per item)
+                constexpr int DG = DP / 8;
+                for (int idx = tid; idx < 8 * DG; idx += NT) {
+                    const int rg = idx / DG, c = idx - rg * DG;
+                    bf16x8 xq[4], xg[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int r = qb + 4 * rg + i;
+                        const int rc = r < S ? r : S - 1;
+                        xq[i] = load_chunk<bf16>(Q + (int64_t)rc * D, 8 * c, D, r < S, vec_ok);
+                        xg[i] = load_chunk<bf16>(G + (int64_t)rc * D, 8 * c, D, r < S, vec_ok);
+                        *reinterpret_cast<bf16x8*>(Qs + (4 * rg + i) * QSTR + 8 * c) = xq[i];
+                        *reinterpret_cast<bf16x8*>(Gs + (4 * rg + i) * QSTR + 8 * c) = xg[i];
+                    }
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const bf16x4 tq = {xq[0][j], xq[1][j], xq[2][j], xq[3][j]};
+                        const bf16x4 tg = {xg[0][j], xg[1][j], xg[2][j], xg[3][j]};
+                        *reinterpret_cast<bf16x4*>(Qt + (8 * c + j) * TSTR + 4 * rg) = tq;
+                        *reinterpret_cast<bf16x4*>(Gt + (8 * c + j) * TSTR + 4 * rg) = tg;
+                    }
+                }
+                if (tid < 32) {
+                    const int r = qb + tid;
+                    Ls[tid] = r < S ? lse[r] * kLog2e : INFINITY;
+                    Dl[tid] = r < S ? dl[r] : 0.f;
+                }
+            }
+            __syncthreads();
+            if (wkey0 >= S) continue;                  // no valid keys in this wave
+            if (CAUSAL && qb + 31 < wkey0) continue;   // every query precedes every key
+
+            f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const bf16x8 qa = *reinterpret_cast<const bf16x8*>(Qs + n * QSTR + 16 * c + 8 * hh);
+                s = mfma_bf16(qa, kf[c], s);
+                const bf16x8 ga = *reinterpret_cast<const bf16x8*>(Gs + n * QSTR + 16 * c + 8 * hh);
+                dp = mfma_bf16(ga, vf[c], dp);
+            }
+            // lane column n = key; register r = query qb + row_of_reg(r, hh)
+            const bool need_mask = CAUSAL && qb < wkey0 + 31;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 l4 = *reinterpret_cast<const f32x4*>(Ls + 8 * g + 4 * hh);
+                const f32x4 d4 = *reinterpret_cast<const f32x4*>(Dl + 8 * g + 4 * hh);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 4 * g + i;
+                    float p = fast_exp2(s[r] * a.scale_log2 - l4[i]);
+                    if (need_mask && qb + 8 * g + 4 * hh + i < key) p = 0.f;
+                    dp[r] = p * (dp[r] - d4[i]);
+                    s[r] = p;
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                bf16x8 pb, db;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    pb[j] = (bf16)s[8 * e + j];
+                    db[j] = (bf16)dp[8 * e + j];
+                }
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) {
+                    const bf16* gp = Gt + (32 * dt + n) * TSTR + 16 * e + 4 * hh;
+                    const bf16x4 glo = *reinterpret_cast<const bf16x4*>(gp);
+                    const bf16x4 ghi = *reinterpret_cast<const bf16x4*>(gp + 8);
+                    const bf16x8 ga = {glo[0], glo[1], glo[2], glo[3], ghi[0], ghi[1], ghi[2], ghi[3]};
+                    dv[dt] = mfma_bf16(ga, pb, dv[dt]);
+                    const bf16* qp = Qt + (32 * dt + n) * TSTR + 16 * e + 4 * hh;
+                    const bf16x4 qlo = *reinterpret_cast<const bf16x4*>(qp);
+                    const bf16x4 qhi = *reinterpret_cast<const bf16x4*>(qp + 8);
+                    const bf16x8 qa = {qlo[0], qlo[1], qlo[2], qlo[3], qhi[0], qhi[1], qhi[2], qhi[3]};
+                    dk[dt] = mfma_bf16(qa, db, dk[dt]);
+                }
+            }
+        }
+    }
+    if (key >= S) return;
+    float *dkp, *dvp;
+    dkdv_out_rows(a, b, hk, split, key, &dkp, &dvp);
+    const bool v4 = a.vec4_ok != 0;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d0 = 32 * dt + 8 * g + 4 * hh;
+            store4<float>(dkp, d0, D, dk[dt][4 * g] * a.scale, dk[dt][4 * g + 1] * a.scale,
+                          dk[dt][4 * g + 2] * a.scale, dk[dt][4 * g + 3] * a.scale, v4);
+            store4<float>(dvp, d0, D, dv[dt][4 * g], dv[dt][4 * g + 1], dv[dt][4 * g + 2],
+                          dv[dt][4 * g + 3], v4);
+        }
+}
+
+// ----------------------------------------------------------- dkdv (fp32)
+template <int DP, int NW, bool CAUSAL>
+__global__ __launch_bounds__(NW * 64) void attn_bwd_dkdv_f32(BwdArgs a) {
+    constexpr int NC = DP / 8, NDT = DP / 32, NT = NW * 64, BNK = 32 * NW;
+    constexpr int STR = DP + 4;
+    __shared__ __attribute__((aligned(16))) float Ks[BNK * STR];
+    __shared__ __attribute__((aligned(16))) float Vs[BNK * STR];
+    __shared__ __attribute__((aligned(16))) float Qs[32 * STR];
+    __shared__ __attribute__((aligned(16))) float Gs[32 * STR];
+    __shared__ __attribute__((aligned(16))) float Ls[32];
+    __shared__ __attribute__((aligned(16))) float Dl[32];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
+    const int S = a.S, D = a.D;
+    const bool vec_ok = a.vec_ok != 0;
+    const int j0 = (int)blockIdx.x * BNK;
+    const int hk = (int)blockIdx.y / a.splits, split = (int)blockIdx.y % a.splits, b = blockIdx.z;
+    const int h_begin = hk * a.group + split * a.heads_per_split;
+    const int h_end = min(h_begin + a.heads_per_split, (hk + 1) * a.group);
+    const int wkey0 = j0 + 32 * w;
+    const int key = wkey0 + n;
+
+    const float* K = (const float*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
+    const float* Vg = (const float*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
+    {
+        constexpr int CPR = DP / 4;
+        for (int idx = tid; idx < BNK * CPR; idx += NT) {
+            const int rr = idx / CPR, c = idx - rr * CPR;
+            const int kr = j0 + rr, krc = kr < S ? kr : S - 1;
+            *reinterpret_cast<f32x4*>(Ks + rr * STR + 4 * c) =
+                load_chunk<float>(K + (int64_t)krc * D, 4 * c, D, kr < S, vec_ok);
+            *reinterpret_cast<f32x4*>(Vs + rr * STR + 4 * c) =
+                load_chunk<float>(Vg + (int64_t)krc * D, 4 * c, D, kr < S, vec_ok);
+        }
+    }
+    f32x16 dk[NDT], dv[NDT];
+#pragma unroll
+    for (int i = 0; i < NDT; ++i) {
+        dk[i] = zero16();
+        dv[i] = zero16();
+    }
+    const float* Kw = Ks + (32 * w + n) * STR;
+    const float* Vw = Vs + (32 * w + n) * STR;
+
+    const int qstart = CAUSAL ? j0 : 0;
+    for (int h = h_begin; h < h_end; ++h) {
+        const float* Q = (const float*)a.q + (int64_t)(b * a.Hq + h) * S * D;
+        const float* G = (const float*)a.dO + (int64_t)(b * a.Hq + h) * S * D;
+        const float* lse = a.lse + (int64_t)(b * a.Hq + h) * S;
+        const float* dl = a.delta + (int64_t)(b * a.Hq + h) * S;
+        for (int qb = qstart; qb < S; qb += 32) {
+            __syncthreads();
+            {
+                constexpr int CPR = DP / 4;
+                for (int idx = tid; idx < 32 * CPR; idx += NT) {
+                    const int rr = idx / CPR, c = idx - rr * CPR;
+                    const int r = qb + rr, rc = r < S ? r : S - 1;
+                    *reinterpret_cast<f32x4*>(Qs + rr * STR + 4 * c) =
+                        load_chunk<float>(Q + (int64_t)rc * D, 4 * c, D, r < S, vec_ok);
+                    *reinterpret_cast<f32x4*>(Gs + rr * STR + 4 * c) =
+                        load_chunk<float>(G + (int64_t)rc * D, 4 * c, D, r < S, vec_ok);
+                }
+                if (tid < 32) {
+                    const int r = qb + tid;
+                    Ls[tid] = r < S ? lse[r] * kLog2e : INFINITY;
+                    Dl[tid] = r < S ? dl[r] : 0.f;
+                }
+            }
+            __syncthreads();
+            if (wkey0 >= S) continue;
+            if (CAUSAL && qb + 31 < wkey0) continue;
+
+            f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const f32x4 qa = *reinterpret_cast<const f32x4*>(Qs + n * STR + 8 * c + 4 * hh);
+                const f32x4 kb = *reinterpret_cast<const f32x4*>(Kw + 8 * c + 4 * hh);
+                s = mfma_chunk(qa, kb, s);
+                const f32x4 ga = *reinterpret_cast<const f32x4*>(Gs + n * STR + 8 * c + 4 * hh);
+                const f32x4 vb = *reinterpret_cast<const f32x4*>(Vw + 8 * c + 4 * hh);
+                dp = mfma_chunk(ga, vb, dp);
+            }
+            const bool need_mask = CAUSAL && qb < wkey0 + 31;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 l4 = *reinterpret_cast<const f32x4*>(Ls + 8 * g + 4 * hh);
+                const f32x4 d4 = *reinterpret_cast<const f32x4*>(Dl + 8 * g + 4 * hh);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 4 * g + i;
+                    float p = fast_exp2(s[r] * a.scale_log2 - l4[i]);
+                    if (need_mask && qb + 8 * g + 4 * hh + i < key) p = 0.f;
+                    dp[r] = p * (dp[r] - d4[i]);
+                    s[r] = p;
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int ql = row_of_reg(r, hh);
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) {
+                    dv[dt] = mfma_f32(Gs[ql * STR + 32 * dt + n], s[r], dv[dt]);
+                    dk[dt] = mfma_f32(Qs[ql * STR + 32 * dt + n], dp[r], dk[dt]);
+                }
+            }
+        }
+    }
+    if (key >= S) return;
+    float *dkp, *dvp;
+    dkdv_out_rows(a, b, hk, split, key, &dkp, &dvp);
+    const bool v4 = a.vec4_ok != 0;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d0 = 32 * dt + 8 * g + 4 * hh;
+            store4<float>(dkp, d0, D, dk[dt][4 * g] * a.scale, dk[dt][4 * g + 1] * a.scale,
+                          dk[dt][4 * g + 2] * a.scale, dk[dt][4 * g + 3] * a.scale, v4);
+            store4<float>(dvp, d0, D, dv[dt][4 * g], dv[dt][4 * g + 1], dv[dt][4 * g + 2],
+                          dv[dt][4 * g + 3], v4);
+        }
+}
+
+// -------------------------------------------------------------------- dq
+template <typename T, int DP, int BN> struct DqLds {
+    static constexpr bool KT = sizeof(T) == 2;  // K^T staged (bf16)
+    static constexpr int STR = DP + Elt<T>::VEC;
+    static constexpr int TSTR = BN + 4;
+    static constexpr int KV_ELEMS = BN * STR;
+    static constexpr int KT_ELEMS = KT ? DP * TSTR : 1;
+};
+
+template <typename T, int DP, int NW, int BN, bool CAUSAL>
+__global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(BwdArgs a) {
+    typedef typename Elt<T>::vec V;
+    typedef DqLds<T, DP, BN> L;
+    constexpr int VEC = Elt<T>::VEC;
+    constexpr int NC = DP / (2 * VEC);
+    constexpr int NDT = DP / 32, NKK = BN / 32, BM = 32 * NW, NT = NW * 64;
+    __shared__ __attribute__((aligned(16))) T Ks[L::KV_ELEMS];
+    __shared__ __attribute__((aligned(16))) T Vs[L::KV_ELEMS];
+    __shared__ __attribute__((aligned(16))) T Kt[L::KT_ELEMS];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
+    const int S = a.S, D = a.D;
+    const bool vec_ok = a.vec_ok != 0;
+    const int qt = a.n_tiles - 1 - (int)blockIdx.x;
+    const int h = blockIdx.y, b = blockIdx.z, hk = h / a.group;
+    const int m0 = qt * BM, wrow0 = m0 + 32 * w, row = wrow0 + n;
+    const int rowc = row < S ? row : S - 1;
+
+    const T* Q = (const T*)a.q + (int64_t)(b * a.Hq + h) * S * D;
+    const T* G = (const T*)a.dO + (int64_t)(b * a.Hq + h) * S * D;
+    const T* K = (const T*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
+    const T* Vg = (const T*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
+    V qf[NC], gf[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        qf[c] = load_chunk<T>(Q + (int64_t)rowc * D, 2 * VEC * c + VEC * hh, D, row < S, vec_ok);
+        gf[c] = load_chunk<T>(G + (int64_t)rowc * D, 2 * VEC * c + VEC * hh, D, row < S, vec_ok);
+    }
+    const int64_t rbase = (int64_t)(b * a.Hq + h) * S;
+    const float lse2 = row < S ? a.lse[rbase + row] * kLog2e : INFINITY;
+    const float dlt = row < S ? a.delta[rbase + row] : 0.f;
+
+    f32x16 dq[NDT];
+#pragma unroll
+    for (int i = 0; i < NDT; ++i) dq[i] = zero16();
+
+    const int kend = CAUSAL ? min(S, m0 + BM) : S;
+    const int ntiles = (kend + BN - 1) / BN;
+    for (int t = 0; t < ntiles; ++t) {
+        const int kbase = t * BN;
+        __syncthreads();
+        {
+            constexpr int CPR = DP / VEC;
+            for (int idx = tid; idx < BN * CPR; idx += NT) {
+                const int rr = idx / CPR, c = idx - rr * CPR;
+                const int kr = kbase + rr, krc = kr < S ? kr : S - 1;
+                *reinterpret_cast<V*>(Ks + rr * L::STR + c * VEC) =
+                    load_chunk<T>(K + (int64_t)krc * D, c * VEC, D, kr < S, vec_ok);
+                *reinterpret_cast<V*>(Vs + rr * L::STR + c * VEC) =
+                    load_chunk<T>(Vg + (int64_t)krc * D, c * VEC, D, kr < S, vec_ok);
+            }
+        }
+        if constexpr (L::KT) {
+            constexpr int DG = DP / 8;
+            for (int idx = tid; idx < (BN / 4) * DG; idx += NT) {
+                const int kg = idx / DG, c = idx - kg * DG;
+                bf16x8 x[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int kr = kbase + 4 * kg + i, krc = kr < S ? kr : S - 1;
+                    x[i] = load_chunk<bf16>((const bf16*)K + (int64_t)krc * D, 8 * c, D, kr < S, vec_ok);
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const bf16x4 tv = {x[0][j], x[1][j], x[2][j], x[3][j]};
+                    *reinterpret_cast<bf16x4*>((bf16*)Kt + (8 * c + j) * L::TSTR + 4 * kg) = tv;
+                }
+            }
+        }
+        __syncthreads();
+        if (wrow0 >= S || (CAUSAL && kbase > wrow0 + 31)) continue;
+
+        const bool need_mask = (CAUSAL && kbase + BN - 1 > wrow0) || (kbase + BN > S);
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) {
+            f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const V ka = *reinterpret_cast<const V*>(Ks + (32 * kk + n) * L::STR + 2 * VEC * c + VEC * hh);
+                s = mfma_chunk(ka, qf[c], s);
+                const V va = *reinterpret_cast<const V*>(Vs + (32 * kk + n) * L::STR + 2 * VEC * c + VEC * hh);
+                dp = mfma_chunk(va, gf[c], dp);
+            }
+            // lane column n = query row; register r = key kbase + 32kk + row_of_reg(r, hh)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float p = fast_exp2(s[r] * a.scale_log2 - lse2);
+                if (need_mask) {
+                    const int kr = kbase + 32 * kk + row_of_reg(r, hh);
+                    if (kr >= S || (CAUSAL && kr > row)) p = 0.f;
+                }
+                s[r] = p * (dp[r] - dlt);
+            }
+            if constexpr (L::KT) {
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    bf16x8 db;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) db[j] = (bf16)s[8 * e + j];
+#pragma unroll
+                    for (int dt = 0; dt < NDT; ++dt) {
+                        const bf16* kp = (const bf16*)Kt + (32 * dt + n) * L::TSTR + 32 * kk + 16 * e + 4 * hh;
+                        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(kp);
+                        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(kp + 8);
+                        const bf16x8 ka = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                        dq[dt] = mfma_bf16(ka, db, dq[dt]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int kl = 32 * kk + row_of_reg(r, hh);
+#pragma unroll
+                    for (int dt = 0; dt < NDT; ++dt)
+                        dq[dt] = mfma_f32((float)Ks[kl * L::STR + 32 * dt + n], s[r], dq[dt]);
+                }
+            }
+        }
+    }
+    if (row >= S) return;
+    float* dqp = a.dq + (rbase + row) * D;
+    const bool v4 = a.vec4_ok != 0;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            store4<float>(dqp, 32 * dt + 8 * g + 4 * hh, D, dq[dt][4 * g] * a.scale,
+                          dq[dt][4 * g + 1] * a.scale, dq[dt][4 * g + 2] * a.scale,
+                          dq[dt][4 * g + 3] * a.scale, v4);
+}
+
+// ---------------------------------------------------------------- reduce
+// dk = sum over splits of the dK partials (split order), same for dv.
+__global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(BwdArgs a) {
+    const int64_t n = a.part_stride;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        float sk = 0.f, sv = 0.f;
+        for (int s = 0; s < a.splits; ++s) {
+            sk += a.part[(int64_t)s * n + i];
+            sv += a.part[(int64_t)(a.splits + s) * n + i];
+        }
+        a.dk[i] = sk;
+        a.dv[i] = sv;
+    }
+}
+
+template <typename T, int DP>
+hipError_t launch_bwd_t(const AttnShape& s, BwdArgs a, hipStream_t st) {
+    constexpr bool BF = sizeof(T) == 2;
+    // prep
+    {
+        constexpr int TPR = DP / Elt<T>::VEC;
+        constexpr int RPB = 256 / TPR;
+        const int64_t blocks = (a.total_rows + RPB - 1) / RPB;
+        hipLaunchKernelGGL((attn_bwd_prep_kernel<T, DP>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+    }
+    // dK / dV
+    {
+        constexpr int NW = BF ? 4 : (DP >= 256 ? 1 : DP >= 128 ? 2 : 4);
+        constexpr int BNK = 32 * NW;
+        dim3 grid((unsigned)((s.S + BNK - 1) / BNK), (unsigned)(s.Hkv * a.splits), (unsigned)s.B);
+        if constexpr (BF) {
+            if (s.causal)
+                hipLaunchKernelGGL((attn_bwd_dkdv_bf16<DP, NW, true>), grid, dim3(NW * 64), 0, st, a);
+            else
+                hipLaunchKernelGGL((attn_bwd_dkdv_bf16<DP, NW, false>), grid, dim3(NW * 64), 0, st, a);
+        } else {
+            if (s.causal)
+                hipLaunchKernelGGL((attn_bwd_dkdv_f32<DP, NW, true>), grid, dim3(NW * 64), 0, st, a);
+            else
+                hipLaunchKernelGGL((attn_bwd_dkdv_f32<DP, NW, false>), grid, dim3(NW * 64), 0, st, a);
+        }
+    }
+    // dQ
+    {
+        constexpr int NW = 4, BN = (!BF && DP >= 256) ? 32 : 64, BM = 32 * NW;
+        a.n_tiles = (int)((s.S + BM - 1) / BM);
+        dim3 grid((unsigned)a.n_tiles, (unsigned)s.Hq, (unsigned)s.B);
+        if (s.causal)
+            hipLaunchKernelGGL((attn_bwd_dq_kernel<T, DP, NW, BN, true>), grid, dim3(NW * 64), 0, st, a);
+        else
+            hipLaunchKernelGGL((attn_bwd_dq_kernel<T, DP, NW, BN, false>), grid, dim3(NW * 64), 0, st, a);
+    }
+    if (a.splits > 1) {
+        int64_t blocks = (a.part_stride + 255) / 256;
+        if (blocks > 4096) blocks = 4096;
+        hipLaunchKernelGGL(attn_bwd_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
+    }
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_bwd_dispatch(const AttnShape& s, const BwdArgs& a, hipStream_t st) {
+    if (s.D <= 32) return launch_bwd_t<T, 32>(s, a, st);
+    if (s.D <= 64) return launch_bwd_t<T, 64>(s, a, st);
+    if (s.D <= 128) return launch_bwd_t<T, 128>(s, a, st);
+    return launch_bwd_t<T, 256>(s, a, st);
+}
+
+}  // namespace
+
+int dkdv_keys_per_block(const AttnShape& s) {
+    if (s.bf16) return 128;
+    return s.D > 128 ? 32 : s.D > 64 ? 64 : 128;
+}
+
+int dkdv_splits(const AttnShape& s) {
+    // Split the query heads of a group across workgroups until the grid has
+    // about one workgroup per CU; splits must divide the group size.
+    const int64_t group = s.Hq / s.Hkv;
+    const int64_t kb = dkdv_keys_per_block(s);
+    const int64_t base = ((s.S + kb - 1) / kb) * s.Hkv * s.B;
+    int64_t best = 1;
+    for (int64_t d = 1; d <= group; ++d) {
+        if (group % d) continue;
+        best = d;
+        if (base * d >= 256) break;
+    }
+    return (int)best;
+}
+
+hipError_t launch_attn_bwd(const AttnShape& s, const void* q, const void* k, const void* v,
+                           const void* o, const void* dO, const float* lse, float* dq, float* dk,
+                           float* dv, float* delta, float* part, hipStream_t st) {
+    BwdArgs a;
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.o = o;
+    a.dO = dO;
+    a.lse = lse;
+    a.dq = dq;
+    a.dk = dk;
+    a.dv = dv;
+    a.delta = delta;
+    a.part = part;
+    a.part_stride = s.B * s.Hkv * s.S * s.D;
+    a.total_rows = s.B * s.Hq * s.S;
+    a.S = (int)s.S;
+    a.D = (int)s.D;
+    a.Hq = (int)s.Hq;
+    a.Hkv = (int)s.Hkv;
+    a.group = (int)(s.Hq / s.Hkv);
+    a.splits = dkdv_splits(s);
+    a.heads_per_split = a.group / a.splits;
+    a.n_tiles = 0;
+    a.scale = s.scale;
+    a.scale_log2 = s.scale * kLog2e;
+    a.vec_ok = (s.D % (s.bf16 ? 8 : 4)) == 0;
+    a.vec4_ok = (s.D % 4) == 0;
+    return s.bf16 ? launch_bwd_dispatch<bf16>(s, a, st) : launch_bwd_dispatch<float>(s, a, st);
+}
+
+}  // namespace mft

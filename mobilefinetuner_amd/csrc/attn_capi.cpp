@@ -1,0 +1,137 @@
+// C ABI of the fused attention (declared in include/mft/attention.h).
+//
+// Validates the request the way the reference validates its operator inputs
+// (core/memory_efficient_attention.cpp:85-103: 4-D shapes, matching sizes,
+// scale <= 0 meaning 1/sqrt(D)), resolves the workspace layout, and enqueues
+// the kernels.  Errors are reported as a status plus a thread-local message;
+// nothing is allocated here.
+#include "mft/attention.h"
+
+#include <cmath>
+#include <cstdio>
+#include <string>
+
+#include "attn_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+mft_status fail(mft_status st, const std::string& msg) {
+    g_last_error = msg;
+    return st;
+}
+
+size_t round_up(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+mft_status check_desc(const mft_attn_desc* d, mft::AttnShape* s) {
+    if (!d) return fail(MFT_ERR_INVALID_ARG, "mft_attn: desc is NULL");
+    if (d->B <= 0 || d->Hq <= 0 || d->Hkv <= 0 || d->S <= 0 || d->D <= 0)
+        return fail(MFT_ERR_INVALID_ARG, "mft_attn: B, Hq, Hkv, S, D must be positive (inputs must be 4D [B,H,S,D])");
+    if (d->Hq % d->Hkv != 0)
+        return fail(MFT_ERR_INVALID_ARG, "mft_attn: query heads (" + std::to_string(d->Hq) +
+                                             ") must be a multiple of kv heads (" + std::to_string(d->Hkv) + ")");
+    if (d->dtype != MFT_F32 && d->dtype != MFT_BF16)
+        return fail(MFT_ERR_INVALID_ARG, "mft_attn: dtype must be MFT_F32 or MFT_BF16");
+    if (d->D > 256) return fail(MFT_ERR_UNSUPPORTED, "mft_attn: head_dim > 256 is not supported");
+    if (d->S > (int64_t(1) << 24)) return fail(MFT_ERR_UNSUPPORTED, "mft_attn: sequence length > 2^24");
+    if (d->S * d->D > (int64_t(1) << 31) - 1)
+        return fail(MFT_ERR_UNSUPPORTED, "mft_attn: one head block exceeds 2^31 elements");
+    if (d->B * d->Hq > 65535 || d->B > 65535 || d->Hq > 65535)
+        return fail(MFT_ERR_UNSUPPORTED, "mft_attn: batch/head grid dimensions too large");
+    if (!(std::isfinite(d->scale)))
+        return fail(MFT_ERR_INVALID_ARG, "mft_attn: scale must be finite");
+    s->B = d->B;
+    s->Hq = d->Hq;
+    s->Hkv = d->Hkv;
+    s->S = d->S;
+    s->D = d->D;
+    s->scale = d->scale > 0.f ? d->scale : 1.0f / std::sqrt(static_cast<float>(d->D));
+    s->causal = d->causal != 0;
+    s->bf16 = d->dtype == MFT_BF16;
+    return MFT_OK;
+}
+
+// Backward workspace: delta [B*Hq*S] fp32, then (splits > 1) dK and dV
+// partials [2 * splits * B*Hkv*S*D] fp32.
+void bwd_layout(const mft::AttnShape& s, size_t* delta_bytes, size_t* part_bytes) {
+    *delta_bytes = round_up(sizeof(float) * static_cast<size_t>(s.B * s.Hq * s.S));
+    const int splits = mft::dkdv_splits(s);
+    *part_bytes = splits > 1 ? round_up(sizeof(float) * 2 * static_cast<size_t>(splits) *
+                                        static_cast<size_t>(s.B * s.Hkv * s.S * s.D))
+                             : 0;
+}
+
+mft_status hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return MFT_OK;
+    return fail(MFT_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+}  // namespace
+
+extern "C" {
+
+int mft_version(void) { return 1; }
+
+const char* mft_last_error(void) { return g_last_error.c_str(); }
+
+mft_status mft_attn_workspace_size(const mft_attn_desc* desc, size_t* fwd_bytes, size_t* bwd_bytes) {
+    mft::AttnShape s;
+    const mft_status st = check_desc(desc, &s);
+    if (st != MFT_OK) return st;
+    if (fwd_bytes) *fwd_bytes = 0;
+    if (bwd_bytes) {
+        size_t a, b;
+        bwd_layout(s, &a, &b);
+        *bwd_bytes = a + b;
+    }
+    return MFT_OK;
+}
+
+mft_status mft_attn_fwd(const mft_attn_desc* desc, const void* q, const void* k, const void* v, void* o,
+                        float* lse, void* workspace, hipStream_t stream) {
+    (void)workspace;
+    mft::AttnShape s;
+    const mft_status st = check_desc(desc, &s);
+    if (st != MFT_OK) return st;
+    if (!q || !k || !v || !o) return fail(MFT_ERR_INVALID_ARG, "mft_attn_fwd: q, k, v, o must be non-NULL");
+    return hip_status(mft::launch_attn_fwd(s, q, k, v, o, lse, stream), "mft_attn_fwd launch");
+}
+
+mft_status mft_attn_bwd(const mft_attn_desc* desc, const void* q, const void* k, const void* v, const void* o,
+                        const void* dO, const float* lse, float* dq, float* dk, float* dv, void* workspace,
+                        hipStream_t stream) {
+    mft::AttnShape s;
+    const mft_status st = check_desc(desc, &s);
+    if (st != MFT_OK) return st;
+    if (!q || !k || !v || !o || !dO || !lse || !dq || !dk || !dv)
+        return fail(MFT_ERR_INVALID_ARG, "mft_attn_bwd: q, k, v, o, dO, lse, dq, dk, dv must be non-NULL");
+    if (!workspace) return fail(MFT_ERR_INVALID_ARG, "mft_attn_bwd: workspace is NULL (see mft_attn_workspace_size)");
+    size_t delta_bytes, part_bytes;
+    bwd_layout(s, &delta_bytes, &part_bytes);
+    float* delta = static_cast<float*>(workspace);
+    float* part = part_bytes ? reinterpret_cast<float*>(static_cast<char*>(workspace) + delta_bytes) : nullptr;
+    return hip_status(mft::launch_attn_bwd(s, q, k, v, o, dO, lse, dq, dk, dv, delta, part, stream),
+                      "mft_attn_bwd launch");
+}
+
+mft_status mft_repeat_kv_fwd(const void* kv, void* out, int64_t B, int64_t Hkv, int64_t S, int64_t D, int64_t r,
+                             mft_dtype dtype, hipStream_t stream) {
+    if (!kv || !out) return fail(MFT_ERR_INVALID_ARG, "mft_repeat_kv_fwd: kv and out must be non-NULL");
+    if (B <= 0 || Hkv <= 0 || S <= 0 || D <= 0 || r <= 0)
+        return fail(MFT_ERR_INVALID_ARG, "repeat_kv_heads expects 4D tensor with positive sizes and repeat factor");
+    if (dtype != MFT_F32 && dtype != MFT_BF16)
+        return fail(MFT_ERR_INVALID_ARG, "mft_repeat_kv_fwd: dtype must be MFT_F32 or MFT_BF16");
+    const int esize = dtype == MFT_F32 ? 4 : 2;
+    return hip_status(mft::launch_repeat_kv_fwd(kv, out, B, Hkv, S, D, r, esize, stream), "mft_repeat_kv_fwd launch");
+}
+
+mft_status mft_repeat_kv_bwd(const float* g, float* dkv, int64_t B, int64_t Hkv, int64_t S, int64_t D, int64_t r,
+                             hipStream_t stream) {
+    if (!g || !dkv) return fail(MFT_ERR_INVALID_ARG, "mft_repeat_kv_bwd: g and dkv must be non-NULL");
+    if (B <= 0 || Hkv <= 0 || S <= 0 || D <= 0 || r <= 0)
+        return fail(MFT_ERR_INVALID_ARG, "RepeatKVHeadsBackward expects 4D gradient with positive sizes");
+    return hip_status(mft::launch_repeat_kv_bwd(g, dkv, B, Hkv, S, D, r, stream), "mft_repeat_kv_bwd launch");
+}
+
+}  // extern "C"
