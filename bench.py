@@ -1,0 +1,223 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused causal GQA attention fwd+bwd on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c5] [--all-configs]
+                    [--no-cpu-baseline]
+
+A step is one forward plus one backward of the attention over the config's
+synthetic batch (inputs resident in HBM).  Prints ONE JSON line.  `value` is
+the algorithmic causal throughput  7*B*H*D*S*(S+1) / step time  in TFLOP/s
+The roofline object covers the dominant kernel,
+timed live with HIP events on the stream the kernels run on.  The
+cpu_baseline object times the reference CPU operators (oracle/_ref, compiled
+from the reference sources) on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+METRIC = "causal GQA attn fwd+bwd TFLOP/s & % MFMA peak (1 GPU); saved-act bytes"
+PEAK_TFLOPS = {"bf16": 2500.0, "f32": 157.3}  # MI355X dense MFMA (published)
+HBM_GBS = 8000.0
+
+# BASELINE.json configs (shapes, dtype, scale, dO sigma); all causal.
+CONFIGS = {
+    "c1": dict(B=4, Hq=12, Hkv=12, D=64, S=128, dtype="f32", scale=1 / 8, do_sigma=1.0,
+               name="GPT-2-small attention fwd+bwd, fp32, causal MHA"),
+    "c2": dict(B=4, Hq=16, Hkv=16, D=64, S=512, dtype="f32", scale=1 / 8, do_sigma=0.1,
+               name="GPT-2-medium attention fwd+bwd, fp32, causal MHA"),
+    "c3": dict(B=2, Hq=14, Hkv=2, D=64, S=2048, dtype="bf16", scale=1 / 8, do_sigma=0.1,
+               name="Qwen2.5-0.5B-shaped GQA attention fwd+bwd, bf16 in / fp32 accumulate"),
+    "c4": dict(B=4, Hq=4, Hkv=1, D=256, S=1024, dtype="bf16", scale=1 / 16, do_sigma=0.1,
+               name="Gemma-3-270M-shaped GQA attention fwd+bwd, bf16"),
+    "c5": dict(B=1, Hq=4, Hkv=1, D=256, S=4096, dtype="bf16", scale=1 / 16, do_sigma=0.1,
+               name="Gemma-3-1B-shaped GQA attention fwd+bwd, bf16"),
+    "c5f32": dict(B=1, Hq=4, Hkv=1, D=256, S=4096, dtype="f32", scale=1 / 16, do_sigma=0.1,
+                  name="Gemma-3-1B-shaped GQA attention fwd+bwd, fp32 exactness variant"),
+}
+
+
+def flop_units(c):
+    """One causal S x S x D contraction per query head: D*S*(S+1) flops."""
+    return c["B"] * c["Hq"] * c["D"] * c["S"] * (c["S"] + 1)
+
+
+def saved_bytes(c):
+    esz = 2 if c["dtype"] == "bf16" else 4
+    B, Hq, Hkv, S, D = c["B"], c["Hq"], c["Hkv"], c["S"], c["D"]
+    new = esz * (2 * B * Hq * S * D + 2 * B * Hkv * S * D) + 4 * B * Hq * S
+    # Reference: four S x S fp32 tensors per query head stay alive until
+    # backward, plus the transposed and (GQA) repeated K/V copies
+    # (measured formula).
+    ref = 4 * B * Hq * S * S * 4 + 2 * B * Hq * S * D * 4 + (2 * B * Hq * S * D * 4 if Hq != Hkv else 0)
+    return new, ref
+
+
+def gpu_leg(cfg_id, steps, warmup):
+    import torch
+    from mobilefinetuner_amd import attention as A
+    from mobilefinetuner_amd import capi
+
+    c = CONFIGS[cfg_id]
+    dev = torch.device("cuda:0")
+    dt = torch.bfloat16 if c["dtype"] == "bf16" else torch.float32
+    g = torch.Generator(device=dev)
+    g.manual_seed(1000 + int(cfg_id[1]))
+    B, Hq, Hkv, S, D = c["B"], c["Hq"], c["Hkv"], c["S"], c["D"]
+    q = torch.randn(B, Hq, S, D, device=dev, generator=g).to(dt)
+    k = torch.randn(B, Hkv, S, D, device=dev, generator=g).to(dt)
+    v = torch.randn(B, Hkv, S, D, device=dev, generator=g).to(dt)
+    dO = (torch.randn(B, Hq, S, D, device=dev, generator=g) * c["do_sigma"]).to(dt)
+    scale = c["scale"]
+    ws = torch.empty(max(A.workspace_bytes(q, k, scale, True), 1), dtype=torch.uint8, device=dev)
+    o = torch.empty_like(q)
+    lse = torch.empty(B, Hq, S, dtype=torch.float32, device=dev)
+    dq = torch.empty(q.shape, dtype=torch.float32, device=dev)
+    dk = torch.empty(k.shape, dtype=torch.float32, device=dev)
+    dv = torch.empty(v.shape, dtype=torch.float32, device=dev)
+    d = A._desc(q, k, scale, True)
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    P = [t.data_ptr() for t in (q, k, v, o, dO, lse, dq, dk, dv, ws)]
+
+    def fwd():
+        capi.attn_fwd(d, P[0], P[1], P[2], P[3], P[5], None, sp)
+
+    def bwd():
+        capi.attn_bwd(d, P[0], P[1], P[2], P[3], P[4], P[5], P[6], P[7], P[8], P[9], sp)
+
+    def bwd_main():
+        capi.attn_bwd_stage(d, capi.MFT_BWD_MAIN, P[0], P[1], P[2], P[3], P[4], P[5], P[6], P[7], P[8],
+                            P[9], sp)
+
+    def timed(fn, n):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n  # ms
+
+    for _ in range(warmup):
+        fwd()
+        bwd()
+    torch.cuda.synchronize()
+    step_ms = timed(lambda: (fwd(), bwd()), steps)
+    n_phase = max(steps, 10)
+    fwd_ms = timed(fwd, n_phase)
+    bwd_ms = timed(bwd, n_phase)
+    capi.attn_bwd_stage(d, capi.MFT_BWD_DELTA, *P[:9], P[9], sp)  # delta for the main stage
+    main_ms = timed(bwd_main, n_phase)
+    units = flop_units(c)
+    return dict(step_ms=step_ms, fwd_ms=fwd_ms, bwd_ms=bwd_ms, bwd_main_ms=main_ms, units=units)
+
+
+def cpu_leg(cfg_id):
+    """Reference CPU operators on a bounded sample: one query head of the
+    workload (same S, D), fwd+bwd, single-threaded as the reference is."""
+    from oracle import oracle as O
+    c = CONFIGS[cfg_id]
+    S, D = c["S"], c["D"]
+    # Keep the sample to roughly 10-30 s of CPU work: one head, and a shorter
+    # sequence when one head of the full length would be too long.
+    Ss = S
+    while 7 * D * Ss * (Ss + 1) > 1.2e11:
+        Ss //= 2
+    q, k, v, dO = O.make_inputs(1, 1, 1, Ss, D, 4242, c["dtype"], c["do_sigma"])
+    kind = "reference" if O.ref_available() else "port"
+    t0 = time.time()
+    if kind == "reference":
+        r = O.ref_composite(q, k, v, dO, scale=c["scale"], causal=True)
+        secs = r["t_fwd"] + r["t_bwd"]
+    else:
+        O.composite(q, k, v, dO, scale=c["scale"], causal=True)
+        secs = time.time() - t0
+    units = D * Ss * (Ss + 1)
+    return dict(value=round(7 * units / secs / 1e12, 6), unit="TFLOP/s", cores=1, kind=kind,
+                seconds=round(secs, 3),
+                sample=f"1 query head of {cfg_id} (B=1,H=1,S={Ss},D={D}), fp32 composite fwd+bwd "
+                       f"(repeat/transpose/matmul/mul/add-mask/softmax/matmul + Engine backward), "
+                       f"pure C++ build, 1 thread")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c5", choices=sorted(CONFIGS))
+    ap.add_argument("--all-configs", action="store_true", help="also report every config (extra key)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: the attention path is built and measured on a single "
+              "MI355X (multi-GPU sharding is design-only); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    c = CONFIGS[args.config]
+    r = gpu_leg(args.config, args.steps, args.warmup)
+    units = r["units"]
+    peak = PEAK_TFLOPS[c["dtype"]]
+    tflops = 7 * units / (r["step_ms"] * 1e-3) / 1e12
+    fwd_tf = 2 * units / (r["fwd_ms"] * 1e-3) / 1e12
+    main_tf = 5 * units / (r["bwd_main_ms"] * 1e-3) / 1e12
+    # Dominant kernel: the longer of the forward kernel and the backward main
+    # kernel; achieved = its algorithmic flops / its measured launch time.
+    if r["bwd_main_ms"] >= r["fwd_ms"]:
+        dom, ach = "attn_bwd_main (dK/dV + dQ)", main_tf
+    else:
+        dom, ach = "attn_fwd", fwd_tf
+    new_b, ref_b = saved_bytes(c)
+    out = {
+        "metric": METRIC,
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["step_ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": c["dtype"],
+        "data": "synthetic: seeded Q,K,V ~ N(0,1), dO ~ N(0,0.1) (sigma), resident in HBM",
+        "config": {"workload": f"{args.config}: {c['name']}", "B": c["B"], "Hq": c["Hq"], "Hkv": c["Hkv"],
+                   "S": c["S"], "D": c["D"], "causal": True, "scale": c["scale"]},
+        "pct_mfma_peak": round(100 * tflops / peak, 2),
+        "tokens_per_s": round(c["B"] * c["S"] / (r["step_ms"] * 1e-3), 1),
+        "fwd_ms": round(r["fwd_ms"], 5),
+        "bwd_ms": round(r["bwd_ms"], 5),
+        "fwd_tflops": round(fwd_tf, 2),
+        "bwd_tflops": round(5 * units / (r["bwd_ms"] * 1e-3) / 1e12, 2),
+        "saved_bytes": {"new": new_b, "reference": ref_b, "ratio": round(ref_b / new_b, 1)},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(ach, 2), "peak": peak,
+                     "unit": "TFLOP/s", "frac": round(ach / peak, 4), "traffic": None},
+    }
+    if args.all_configs:
+        per = {}
+        for cid in ("c1", "c2", "c3", "c4", "c5", "c5f32"):
+            cc = CONFIGS[cid]
+            rr = gpu_leg(cid, max(10, args.steps // 2), 5)
+            u = rr["units"]
+            tf = 7 * u / (rr["step_ms"] * 1e-3) / 1e12
+            nb, rb = saved_bytes(cc)
+            per[cid] = {"ms_per_step": round(rr["step_ms"], 5), "fwd_ms": round(rr["fwd_ms"], 5),
+                        "bwd_ms": round(rr["bwd_ms"], 5), "tflops": round(tf, 2),
+                        "pct_peak": round(100 * tf / PEAK_TFLOPS[cc["dtype"]], 2),
+                        "tokens_per_s": round(cc["B"] * cc["S"] / (rr["step_ms"] * 1e-3), 1),
+                        "saved_bytes_new": nb, "saved_bytes_ref": rb}
+        out["per_config"] = per
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_leg(args.config)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -92,6 +92,22 @@ mft_status mft_attn_bwd(const mft_attn_desc* desc, const void* q, const void* k,
                         float* dq, float* dk, float* dv, void* workspace,
                         hipStream_t stream);
 
+/* The backward's stages, as a bit mask for mft_attn_bwd_stage.
+ *   DELTA : delta_i = dO_i . O_i into the workspace           (one launch)
+ *   MAIN  : dK/dV and dQ; bf16 runs both in one launch        (fp32: two)
+ *   REDUCE: sums the dK/dV partials of split head groups      (0 or 1 launch)
+ * mft_attn_bwd == mft_attn_bwd_stage(MFT_BWD_ALL).  Callers may run the
+ * stages separately, in this order, on one stream (e.g. to time them or to
+ * start DELTA early); MAIN reads what DELTA wrote into the same workspace. */
+enum { MFT_BWD_DELTA = 1, MFT_BWD_MAIN = 2, MFT_BWD_REDUCE = 4, MFT_BWD_ALL = 7 };
+
+/* Backward, selected stages only (same arguments as mft_attn_bwd).
+ * Replaces: the same Engine backward as mft_attn_bwd, split into launches. */
+mft_status mft_attn_bwd_stage(const mft_attn_desc* desc, int stages, const void* q,
+                              const void* k, const void* v, const void* o, const void* dO,
+                              const float* lse, float* dq, float* dk, float* dv,
+                              void* workspace, hipStream_t stream);
+
 /* repeat_kv_heads forward: out[b, h*r + i] = kv[b, h] for i < r
  * ([B,Hkv,S,D] -> [B,Hkv*r,S,D], element type `dtype`).
  * Replaces ops::repeat_kv_heads (core/ops.cpp:2260-2335). */

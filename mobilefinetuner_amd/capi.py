@@ -14,10 +14,11 @@ LIB_PATH = os.path.join(_PKG, "lib", "libmft_attn.so")
 
 MFT_OK, MFT_ERR_INVALID_ARG, MFT_ERR_UNSUPPORTED, MFT_ERR_HIP = 0, 1, 2, 3
 MFT_F32, MFT_BF16 = 0, 2
+MFT_BWD_DELTA, MFT_BWD_MAIN, MFT_BWD_REDUCE, MFT_BWD_ALL = 1, 2, 4, 7
 
 # Every symbol the header declares (checked by tests/test_capi.py).
 EXPORTS = (
-    "mft_attn_workspace_size", "mft_attn_fwd", "mft_attn_bwd",
+    "mft_attn_workspace_size", "mft_attn_fwd", "mft_attn_bwd", "mft_attn_bwd_stage",
     "mft_repeat_kv_fwd", "mft_repeat_kv_bwd", "mft_last_error", "mft_version",
 )
 
@@ -55,6 +56,8 @@ def lib():
     L.mft_attn_fwd.argtypes = [C.POINTER(AttnDesc), vp, vp, vp, vp, vp, vp, vp]
     L.mft_attn_bwd.restype = C.c_int
     L.mft_attn_bwd.argtypes = [C.POINTER(AttnDesc), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    L.mft_attn_bwd_stage.restype = C.c_int
+    L.mft_attn_bwd_stage.argtypes = [C.POINTER(AttnDesc), C.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
     L.mft_repeat_kv_fwd.restype = C.c_int
     L.mft_repeat_kv_fwd.argtypes = [vp, vp, i64, i64, i64, i64, i64, C.c_int32, vp]
     L.mft_repeat_kv_bwd.restype = C.c_int
@@ -86,6 +89,10 @@ def attn_fwd(d: AttnDesc, q, k, v, o, lse, workspace, stream) -> None:
 
 def attn_bwd(d: AttnDesc, q, k, v, o, dO, lse, dq, dk, dv, workspace, stream) -> None:
     check(lib().mft_attn_bwd(C.byref(d), q, k, v, o, dO, lse, dq, dk, dv, workspace, stream))
+
+
+def attn_bwd_stage(d: AttnDesc, stages: int, q, k, v, o, dO, lse, dq, dk, dv, workspace, stream) -> None:
+    check(lib().mft_attn_bwd_stage(C.byref(d), int(stages), q, k, v, o, dO, lse, dq, dk, dv, workspace, stream))
 
 
 def repeat_kv_fwd(kv, out, B, Hkv, S, D, r, dtype, stream) -> None:

@@ -9,21 +9,26 @@
 // term sum_j dP_ij P_ij is computed as delta_i = dO_i . O_i (equal in exact
 // arithmetic; the reference forms it in double from dP and P).
 //
-// Three kernels:
-//   prep  : delta[b,h,i] = sum_d dO[i,d] * O[i,d]                (HBM bound)
-//   dkdv  : one workgroup per (32*NW keys, kv head, head-group split); wave w
-//           owns 32 keys, one key per lane column.  It loops over the query
-//           heads of its group and over 32-row query blocks (causal: from its
-//           first key on), recomputing S = Q K^T and dP = dO V^T with keys
-//           along the accumulator columns, and accumulates
-//             dV^T += dO^T P,   dK^T += Q^T dS
-//           in registers.  GQA: the group's heads sum in registers, so dK/dV
-//           come out already reduced over repeat_kv (no atomics).  When the
-//           group is split across workgroups for parallelism, each split
-//           writes fp32 partials and `reduce` sums them in split order.
-//   dq    : one workgroup per (32*NW query rows, query head): recomputes S^T
-//           and dP^T with one query row per lane (like the forward) and
-//           accumulates dQ^T += K^T dS^T.  No atomics; deterministic.
+// Stages (each a launch; mft_attn_bwd runs all three in order):
+//   DELTA  : delta[b,h,i] = sum_d dO[i,d] * O[i,d]                  (HBM bound)
+//   MAIN   : one launch holding two kinds of workgroup (bf16; fp32 uses two
+//            launches of the same bodies):
+//     dK/dV role — one workgroup per (32*NW keys, kv head, head-group split);
+//       wave w owns 32 keys, one key per lane column.  It loops over the
+//       query heads of its group and over 32-row query blocks (causal: from
+//       its first key on), recomputing S = Q K^T and dP = dO V^T with keys
+//       along the accumulator columns, and accumulates
+//         dV^T += dO^T P,   dK^T += Q^T dS
+//       in registers.  GQA: the group's heads sum in registers, so dK/dV come
+//       out already reduced over repeat_kv (no atomics).
+//     dQ role — one workgroup per (32*NW query rows, query head): recomputes
+//       S^T and dP^T with one query row per lane (like the forward) and
+//       accumulates dQ^T += K^T dS^T.  No atomics; deterministic.
+//     The two roles are independent (both only need delta), so running them
+//     in one grid fills the 256 CUs even when B*Hkv is 1.  Blocks alternate
+//     between roles, heaviest causal tiles first.
+//   REDUCE : when a group is split across workgroups for parallelism, each
+//            split wrote fp32 dK/dV partials; sum them in split order.
 // bf16 inputs use v_mfma_f32_32x32x16_bf16 with fp32 accumulation; operands
 // that must be read along the reduction dimension are staged transposed in
 // LDS.  fp32 inputs use v_mfma_f32_32x32x2_f32 and need no transposes.
@@ -45,16 +50,20 @@ struct BwdArgs {
     float* dv;
     float* delta;
     float* part;
+    float* stats;         // fast path: per 32-row block [32 x lse*log2e][32 x delta]
+    int nqb_total;        // 32-row blocks per head (ceil(S / 32))
     int64_t part_stride;  // B*Hkv*S*D
     int64_t total_rows;   // B*Hq*S
-    int S, D, Hq, Hkv, group, splits, heads_per_split, n_tiles;
+    int S, D, Hq, Hkv, B, group, splits, heads_per_split;
+    int n_ktiles, n_qtiles;   // key tiles of the dK/dV role, query tiles of the dQ role
+    int n_kv_blocks, n_q_blocks;
     float scale, scale_log2;
     int vec_ok, vec4_ok;
 };
 
-// ------------------------------------------------------------------ prep
+// ------------------------------------------------------------------ DELTA
 template <typename T, int DP>
-__global__ __launch_bounds__(256) void attn_bwd_prep_kernel(BwdArgs a) {
+__global__ __launch_bounds__(256) void attn_bwd_delta_kernel(BwdArgs a) {
     typedef typename Elt<T>::vec V;
     constexpr int VEC = Elt<T>::VEC;
     constexpr int TPR = DP / VEC;  // threads per row, a power of two <= 64
@@ -75,7 +84,7 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_kernel(BwdArgs a) {
     if (row < a.total_rows && c == 0) a.delta[row] = acc;
 }
 
-// Output rows of dK / dV for this workgroup's split.
+// Output rows of dK / dV for a split.
 __device__ __forceinline__ void dkdv_out_rows(const BwdArgs& a, int b, int hk, int split, int key,
                                               float** dkp, float** dvp) {
     const int64_t off = ((int64_t)(b * a.Hkv + hk) * a.S + key) * a.D;
@@ -88,24 +97,45 @@ __device__ __forceinline__ void dkdv_out_rows(const BwdArgs& a, int b, int hk, i
     }
 }
 
-// ----------------------------------------------------------- dkdv (bf16)
+template <int NDT>
+__device__ __forceinline__ void store_dkdv(const BwdArgs& a, float* dkp, float* dvp, int hh, const f32x16 (&dk)[NDT],
+                                           const f32x16 (&dv)[NDT]) {
+    const bool v4 = a.vec4_ok != 0;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d0 = 32 * dt + 8 * g + 4 * hh;
+            store4<float>(dkp, d0, a.D, dk[dt][4 * g] * a.scale, dk[dt][4 * g + 1] * a.scale,
+                          dk[dt][4 * g + 2] * a.scale, dk[dt][4 * g + 3] * a.scale, v4);
+            store4<float>(dvp, d0, a.D, dv[dt][4 * g], dv[dt][4 * g + 1], dv[dt][4 * g + 2], dv[dt][4 * g + 3], v4);
+        }
+}
+
+// ------------------------------------------------------- dK/dV role (bf16)
+template <int DP> struct DkdvBf16Lds {
+    static constexpr int QSTR = DP + 8;  // row-major 32-row tiles of Q and dO
+    static constexpr int TSTR = 32 + 4;  // transposed tiles Q^T, dO^T: [DP][32 + 4]
+    static constexpr int BYTES = 2 * (2 * 32 * QSTR + 2 * DP * TSTR) + 2 * 32 * 4;
+};
+
 template <int DP, int NW, bool CAUSAL>
-__global__ __launch_bounds__(NW * 64) void attn_bwd_dkdv_bf16(BwdArgs a) {
+__device__ __forceinline__ void dkdv_bf16_body(const BwdArgs& a, char* smem, int kt, int ysplit, int b) {
+    typedef DkdvBf16Lds<DP> L;
     constexpr int NC = DP / 16, NDT = DP / 32, NT = NW * 64, BNK = 32 * NW;
-    constexpr int QSTR = DP + 8;  // row-major 32-row tiles of Q and dO
-    constexpr int TSTR = 32 + 4;  // transposed tiles Q^T, dO^T: [DP][32 + 4]
-    __shared__ __attribute__((aligned(16))) bf16 Qs[32 * QSTR];
-    __shared__ __attribute__((aligned(16))) bf16 Gs[32 * QSTR];
-    __shared__ __attribute__((aligned(16))) bf16 Qt[DP * TSTR];
-    __shared__ __attribute__((aligned(16))) bf16 Gt[DP * TSTR];
-    __shared__ __attribute__((aligned(16))) float Ls[32];
-    __shared__ __attribute__((aligned(16))) float Dl[32];
+    constexpr int QSTR = L::QSTR, TSTR = L::TSTR;
+    bf16* Qs = reinterpret_cast<bf16*>(smem);
+    bf16* Gs = Qs + 32 * QSTR;
+    bf16* Qt = Gs + 32 * QSTR;
+    bf16* Gt = Qt + DP * TSTR;
+    float* Ls = reinterpret_cast<float*>(Gt + DP * TSTR);
+    float* Dl = Ls + 32;
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
     const int S = a.S, D = a.D;
     const bool vec_ok = a.vec_ok != 0;
-    const int j0 = (int)blockIdx.x * BNK;
-    const int hk = (int)blockIdx.y / a.splits, split = (int)blockIdx.y % a.splits, b = blockIdx.z;
+    const int j0 = kt * BNK;
+    const int hk = ysplit / a.splits, split = ysplit % a.splits;
     const int h_begin = hk * a.group + split * a.heads_per_split;
     const int h_end = min(h_begin + a.heads_per_split, (hk + 1) * a.group);
     const int wkey0 = j0 + 32 * w;
@@ -217,36 +247,31 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkdv_bf16(BwdArgs a) {
     if (key >= S) return;
     float *dkp, *dvp;
     dkdv_out_rows(a, b, hk, split, key, &dkp, &dvp);
-    const bool v4 = a.vec4_ok != 0;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int d0 = 32 * dt + 8 * g + 4 * hh;
-            store4<float>(dkp, d0, D, dk[dt][4 * g] * a.scale, dk[dt][4 * g + 1] * a.scale,
-                          dk[dt][4 * g + 2] * a.scale, dk[dt][4 * g + 3] * a.scale, v4);
-            store4<float>(dvp, d0, D, dv[dt][4 * g], dv[dt][4 * g + 1], dv[dt][4 * g + 2],
-                          dv[dt][4 * g + 3], v4);
-        }
+    store_dkdv<NDT>(a, dkp, dvp, hh, dk, dv);
 }
 
-// ----------------------------------------------------------- dkdv (fp32)
+// ------------------------------------------------------- dK/dV role (fp32)
+template <int DP, int NW> struct DkdvF32Lds {
+    static constexpr int STR = DP + 4;
+    static constexpr int BYTES = 4 * (2 * 32 * NW * STR + 2 * 32 * STR + 64);
+};
+
 template <int DP, int NW, bool CAUSAL>
-__global__ __launch_bounds__(NW * 64) void attn_bwd_dkdv_f32(BwdArgs a) {
+__device__ __forceinline__ void dkdv_f32_body(const BwdArgs& a, char* smem, int kt, int ysplit, int b) {
     constexpr int NC = DP / 8, NDT = DP / 32, NT = NW * 64, BNK = 32 * NW;
-    constexpr int STR = DP + 4;
-    __shared__ __attribute__((aligned(16))) float Ks[BNK * STR];
-    __shared__ __attribute__((aligned(16))) float Vs[BNK * STR];
-    __shared__ __attribute__((aligned(16))) float Qs[32 * STR];
-    __shared__ __attribute__((aligned(16))) float Gs[32 * STR];
-    __shared__ __attribute__((aligned(16))) float Ls[32];
-    __shared__ __attribute__((aligned(16))) float Dl[32];
+    constexpr int STR = DkdvF32Lds<DP, NW>::STR;
+    float* Ks = reinterpret_cast<float*>(smem);
+    float* Vs = Ks + BNK * STR;
+    float* Qs = Vs + BNK * STR;
+    float* Gs = Qs + 32 * STR;
+    float* Ls = Gs + 32 * STR;
+    float* Dl = Ls + 32;
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
     const int S = a.S, D = a.D;
     const bool vec_ok = a.vec_ok != 0;
-    const int j0 = (int)blockIdx.x * BNK;
-    const int hk = (int)blockIdx.y / a.splits, split = (int)blockIdx.y % a.splits, b = blockIdx.z;
+    const int j0 = kt * BNK;
+    const int hk = ysplit / a.splits, split = ysplit % a.splits;
     const int h_begin = hk * a.group + split * a.heads_per_split;
     const int h_end = min(h_begin + a.heads_per_split, (hk + 1) * a.group);
     const int wkey0 = j0 + 32 * w;
@@ -340,44 +365,34 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkdv_f32(BwdArgs a) {
     if (key >= S) return;
     float *dkp, *dvp;
     dkdv_out_rows(a, b, hk, split, key, &dkp, &dvp);
-    const bool v4 = a.vec4_ok != 0;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int d0 = 32 * dt + 8 * g + 4 * hh;
-            store4<float>(dkp, d0, D, dk[dt][4 * g] * a.scale, dk[dt][4 * g + 1] * a.scale,
-                          dk[dt][4 * g + 2] * a.scale, dk[dt][4 * g + 3] * a.scale, v4);
-            store4<float>(dvp, d0, D, dv[dt][4 * g], dv[dt][4 * g + 1], dv[dt][4 * g + 2],
-                          dv[dt][4 * g + 3], v4);
-        }
+    store_dkdv<NDT>(a, dkp, dvp, hh, dk, dv);
 }
 
-// -------------------------------------------------------------------- dq
+// ------------------------------------------------------------- dQ role
 template <typename T, int DP, int BN> struct DqLds {
     static constexpr bool KT = sizeof(T) == 2;  // K^T staged (bf16)
     static constexpr int STR = DP + Elt<T>::VEC;
     static constexpr int TSTR = BN + 4;
     static constexpr int KV_ELEMS = BN * STR;
-    static constexpr int KT_ELEMS = KT ? DP * TSTR : 1;
+    static constexpr int KT_ELEMS = KT ? DP * TSTR : 0;
+    static constexpr int BYTES = (int)sizeof(T) * (2 * KV_ELEMS + KT_ELEMS);
 };
 
 template <typename T, int DP, int NW, int BN, bool CAUSAL>
-__global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(BwdArgs a) {
+__device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int qt, int h, int b) {
     typedef typename Elt<T>::vec V;
     typedef DqLds<T, DP, BN> L;
     constexpr int VEC = Elt<T>::VEC;
     constexpr int NC = DP / (2 * VEC);
     constexpr int NDT = DP / 32, NKK = BN / 32, BM = 32 * NW, NT = NW * 64;
-    __shared__ __attribute__((aligned(16))) T Ks[L::KV_ELEMS];
-    __shared__ __attribute__((aligned(16))) T Vs[L::KV_ELEMS];
-    __shared__ __attribute__((aligned(16))) T Kt[L::KT_ELEMS];
+    T* Ks = reinterpret_cast<T*>(smem);
+    T* Vs = Ks + L::KV_ELEMS;
+    T* Kt = Vs + L::KV_ELEMS;
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
     const int S = a.S, D = a.D;
     const bool vec_ok = a.vec_ok != 0;
-    const int qt = a.n_tiles - 1 - (int)blockIdx.x;
-    const int h = blockIdx.y, b = blockIdx.z, hk = h / a.group;
+    const int hk = h / a.group;
     const int m0 = qt * BM, wrow0 = m0 + 32 * w, row = wrow0 + n;
     const int rowc = row < S ? row : S - 1;
 
@@ -494,7 +509,359 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(BwdArgs a) {
                           dq[dt][4 * g + 3] * a.scale, v4);
 }
 
-// ---------------------------------------------------------------- reduce
+// Block -> role.  Roles alternate while both have blocks left; within a role
+// the heaviest causal tiles come first (small key tiles for dK/dV, large
+// query tiles for dQ).
+__device__ __forceinline__ bool decode_block(const BwdArgs& a, int bid, int* t, int* y, int* b) {
+    const int m = min(a.n_kv_blocks, a.n_q_blocks);
+    bool kv;
+    int i;
+    if (bid < 2 * m) {
+        kv = (bid & 1) == 0;
+        i = bid >> 1;
+    } else {
+        kv = a.n_kv_blocks > a.n_q_blocks;
+        i = bid - m;
+    }
+    if (kv) {
+        const int yb = a.Hkv * a.splits * a.B;
+        *t = i / yb;
+        const int rest = i - *t * yb;
+        *y = rest % (a.Hkv * a.splits);
+        *b = rest / (a.Hkv * a.splits);
+    } else {
+        const int yb = a.Hq * a.B;
+        const int ti = i / yb;
+        const int rest = i - ti * yb;
+        *t = a.n_qtiles - 1 - ti;
+        *y = rest % a.Hq;
+        *b = rest / a.Hq;
+    }
+    return kv;
+}
+
+template <int A, int B> struct Max { static constexpr int value = A > B ? A : B; };
+
+// bf16: both roles in one launch (4 waves each).
+template <int DP, bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_bwd_main_bf16(BwdArgs a) {
+    constexpr int BYTES = Max<DkdvBf16Lds<DP>::BYTES, DqLds<bf16, DP, 64>::BYTES>::value;
+    __shared__ __attribute__((aligned(16))) char smem[BYTES];
+    int t, y, b;
+    if (decode_block(a, (int)blockIdx.x, &t, &y, &b))
+        dkdv_bf16_body<DP, 4, CAUSAL>(a, smem, t, y, b);
+    else
+        dq_body<bf16, DP, 4, 64, CAUSAL>(a, smem, t, y, b);
+}
+
+// fp32: the roles use different block sizes, so they are two launches.
+template <int DP, int NW, bool CAUSAL>
+__global__ __launch_bounds__(NW * 64) void attn_bwd_dkdv_f32(BwdArgs a) {
+    __shared__ __attribute__((aligned(16))) char smem[DkdvF32Lds<DP, NW>::BYTES];
+    const int i = blockIdx.x;
+    const int yb = a.Hkv * a.splits * a.B;
+    const int t = i / yb, rest = i - t * yb;
+    dkdv_f32_body<DP, NW, CAUSAL>(a, smem, t, rest % (a.Hkv * a.splits), rest / (a.Hkv * a.splits));
+}
+
+template <int DP, int BN, bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_bwd_dq_f32(BwdArgs a) {
+    __shared__ __attribute__((aligned(16))) char smem[DqLds<float, DP, BN>::BYTES];
+    const int i = blockIdx.x;
+    const int yb = a.Hq * a.B;
+    const int ti = i / yb, rest = i - ti * yb;
+    dq_body<float, DP, 4, BN, CAUSAL>(a, smem, a.n_qtiles - 1 - ti, rest % a.Hq, rest / a.Hq);
+}
+
+
+// ===========================================================================
+// bf16 fast path (D % 8 == 0, 32 < D <= 256)
+//
+// The same two roles, with all tile traffic moved HBM -> LDS by
+// global_load_lds_dwordx4 into double buffers (the next block streams in
+// while the current one is multiplied), unpadded XOR-swizzled LDS tiles, and
+// every transposed operand (dO^T, Q^T for dV/dK, K^T for dQ) read with
+// ds_read_b64_tr_b16 from the row-major tile instead of being stored twice.
+//
+// STATS stage: stats[(b*Hq + h) * nqb + blk][0..31] = lse * log2(e) of rows
+// 32*blk + 0..31 (+inf past S), [32..63] = delta (0 past S).  256-byte blocks
+// let the dK/dV role fetch a query block's row terms with one direct load.
+template <typename T, int DP>
+__global__ __launch_bounds__(256) void attn_bwd_stats_kernel(BwdArgs a) {
+    typedef typename Elt<T>::vec V;
+    constexpr int VEC = Elt<T>::VEC;
+    constexpr int TPR = DP / VEC;
+    constexpr int RPB = 256 / TPR;
+    const int64_t spad = (int64_t)a.nqb_total * 32;
+    const int64_t total = (int64_t)a.B * a.Hq * spad;
+    const int64_t prow = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;  // padded row index
+    const int c = threadIdx.x % TPR;
+    const int64_t bh = prow / spad;
+    const int i = (int)(prow - bh * spad);
+    const bool valid = prow < total && i < a.S;
+    float acc = 0.f;
+    if (valid) {
+        const int64_t row = bh * a.S + i;
+        const V x = load_chunk<T>((const T*)a.o + row * a.D, c * VEC, a.D, true, a.vec_ok != 0);
+        const V y = load_chunk<T>((const T*)a.dO + row * a.D, c * VEC, a.D, true, a.vec_ok != 0);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) acc += (float)x[k] * (float)y[k];
+    }
+#pragma unroll
+    for (int off = TPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+    if (prow < total && c == 0) {
+        float* blk = a.stats + (bh * a.nqb_total + i / 32) * 64;
+        blk[i % 32] = valid ? a.lse[bh * a.S + i] * kLog2e : INFINITY;
+        blk[32 + i % 32] = valid ? acc : 0.f;
+    }
+}
+
+template <int DP> struct BwdFastLds {
+    // V_LDS: the dK/dV role reads V of its 128 keys from LDS (B operand of
+    // dP) instead of keeping it in registers; a register-pressure fallback,
+    // off while K, V, dK and dV fit in the 512 VGPRs of a wave.
+    static constexpr bool V_LDS = false;
+    static constexpr int KV_BUF = 2 * 32 * DP + 4 * 512;  // Q, dO tiles + 4 waves x 1 KiB stats (elements)
+    static constexpr int KV_ELEMS = 2 * KV_BUF + (V_LDS ? 128 * DP : 0);
+    static constexpr int Q_BUF = 2 * 64 * DP;             // K, V tiles
+    static constexpr int Q_ELEMS = 2 * Q_BUF;
+    static constexpr int ELEMS = KV_ELEMS > Q_ELEMS ? KV_ELEMS : Q_ELEMS;
+};
+
+template <int DP, bool CAUSAL>
+__device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int kt, int ysplit, int b) {
+    constexpr int NT = 256, BNK = 128, CPR = DP / 8, NC = DP / 16, NDT = DP / 32;
+    constexpr int QT = 32 * DP;
+    constexpr int BUF = BwdFastLds<DP>::KV_BUF;
+    constexpr int LOADS = 2 * (32 * CPR / NT) + 1;
+    constexpr bool V_LDS = BwdFastLds<DP>::V_LDS;
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
+    const int i16 = lane & 15, nh = (lane >> 4) & 1;
+    const int S = a.S, D = a.D;
+    const int j0 = kt * BNK;
+    const int hk = ysplit / a.splits, split = ysplit % a.splits;
+    const int h_begin = hk * a.group + split * a.heads_per_split;
+    const int h_end = min(h_begin + a.heads_per_split, (hk + 1) * a.group);
+    const int wkey0 = j0 + 32 * w;
+    const int key = wkey0 + n;
+    const int keyc = key < S ? key : S - 1;
+
+    const bf16* K = (const bf16*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
+    const bf16* Vg = (const bf16*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
+    const int qstart = CAUSAL ? j0 : 0;
+    const int nqb = (S - qstart + 31) / 32;
+    const int niter = (h_end - h_begin) * nqb;
+
+    auto issue = [&](int it, bf16* buf) {
+        const int h = h_begin + it / nqb, qb = qstart + (it % nqb) * 32;
+        const int64_t hoff = (int64_t)(b * a.Hq + h) * S * D;
+        issue_tile<DP, 32, NT, SWZ_DUAL>((const bf16*)a.q + hoff, qb, S, D, buf);
+        issue_tile<DP, 32, NT, SWZ_DUAL>((const bf16*)a.dO + hoff, qb, S, D, buf + QT);
+        const float* st = a.stats + ((int64_t)(b * a.Hq + h) * a.nqb_total + qb / 32) * 64;
+        load_lds_16(st + 4 * i16, buf + 2 * QT + w * 512);
+    };
+    bf16* Vl = smem + 2 * BUF;  // V rows of this workgroup's keys (V_LDS only)
+    if constexpr (V_LDS) issue_tile<DP, BNK, NT, SWZ_ROW>(Vg, j0, S, D, Vl);
+    if (niter > 0) issue(0, smem);
+
+    bf16x8 kf[NC], vf[V_LDS ? 1 : NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        kf[c] = load_chunk<bf16>(K + (int64_t)keyc * D, 16 * c + 8 * hh, D, key < S, true);
+        if constexpr (!V_LDS) vf[c] = load_chunk<bf16>(Vg + (int64_t)keyc * D, 16 * c + 8 * hh, D, key < S, true);
+    }
+    f32x16 dk[NDT], dv[NDT];
+#pragma unroll
+    for (int i = 0; i < NDT; ++i) {
+        dk[i] = zero16();
+        dv[i] = zero16();
+    }
+
+    for (int it = 0; it < niter; ++it) {
+        const bf16* Qb = smem + (it & 1) * BUF;
+        const bf16* Gb = Qb + QT;
+        const float* stt = reinterpret_cast<const float*>(Qb + 2 * QT + w * 512);
+        if (it + 1 < niter) {
+            __syncthreads();
+            issue(it + 1, smem + ((it + 1) & 1) * BUF);
+            wait_vmcnt<LOADS>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        __syncthreads();
+        const int qb = qstart + (it % nqb) * 32;
+        if (wkey0 >= S) continue;
+        if (CAUSAL && qb + 31 < wkey0) continue;
+
+        f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int col = 16 * c + 8 * hh;
+            s = mfma_bf16(*reinterpret_cast<const bf16x8*>(Qb + tile_off<CPR, SWZ_DUAL>(n, col)), kf[c], s);
+            bf16x8 vb;
+            if constexpr (V_LDS)
+                vb = *reinterpret_cast<const bf16x8*>(Vl + tile_off<CPR, SWZ_ROW>(32 * w + n, col));
+            else
+                vb = vf[c];
+            dp = mfma_bf16(*reinterpret_cast<const bf16x8*>(Gb + tile_off<CPR, SWZ_DUAL>(n, col)), vb, dp);
+        }
+        // lane column n = key; register r = query qb + row_of_reg(r, hh)
+        const bool need_mask = CAUSAL && qb < wkey0 + 31;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const f32x4 l4 = *reinterpret_cast<const f32x4*>(stt + 8 * g + 4 * hh);
+            const f32x4 d4 = *reinterpret_cast<const f32x4*>(stt + 32 + 8 * g + 4 * hh);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 4 * g + i;
+                float p = fast_exp2(s[r] * a.scale_log2 - l4[i]);
+                if (need_mask && qb + 8 * g + 4 * hh + i < key) p = 0.f;
+                dp[r] = p * (dp[r] - d4[i]);
+                s[r] = p;
+            }
+        }
+#pragma unroll 1
+        for (int e = 0; e < 2; ++e) {
+            bf16x8 pb, db;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                pb[j] = (bf16)s[8 * e + j];
+                db[j] = (bf16)dp[8 * e + j];
+            }
+            const int r0 = 16 * e + 4 * hh + (i16 >> 2), r1 = r0 + 8;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                const int col = 32 * dt + 16 * nh + 4 * (i16 & 3);
+                const bf16x4 glo = ds_read_tr4(Gb + tile_off<CPR, SWZ_DUAL>(r0, col));
+                const bf16x4 ghi = ds_read_tr4(Gb + tile_off<CPR, SWZ_DUAL>(r1, col));
+                const bf16x8 ga = {glo[0], glo[1], glo[2], glo[3], ghi[0], ghi[1], ghi[2], ghi[3]};
+                dv[dt] = mfma_bf16(ga, pb, dv[dt]);
+                const bf16x4 qlo = ds_read_tr4(Qb + tile_off<CPR, SWZ_DUAL>(r0, col));
+                const bf16x4 qhi = ds_read_tr4(Qb + tile_off<CPR, SWZ_DUAL>(r1, col));
+                const bf16x8 qa = {qlo[0], qlo[1], qlo[2], qlo[3], qhi[0], qhi[1], qhi[2], qhi[3]};
+                dk[dt] = mfma_bf16(qa, db, dk[dt]);
+            }
+        }
+    }
+    if (key >= S) return;
+    float *dkp, *dvp;
+    dkdv_out_rows(a, b, hk, split, key, &dkp, &dvp);
+    store_dkdv<NDT>(a, dkp, dvp, hh, dk, dv);
+}
+
+template <int DP, bool CAUSAL>
+__device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int qt, int h, int b) {
+    constexpr int NT = 256, BN = 64, BM = 128, CPR = DP / 8, NC = DP / 16, NDT = DP / 32, NKK = BN / 32;
+    constexpr int TILE = BN * DP;
+    constexpr int BUF = BwdFastLds<DP>::Q_BUF;
+    constexpr int LOADS = 2 * (BN * CPR / NT);
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
+    const int i16 = lane & 15, nh = (lane >> 4) & 1;
+    const int S = a.S, D = a.D;
+    const int hk = h / a.group;
+    const int m0 = qt * BM, wrow0 = m0 + 32 * w, row = wrow0 + n;
+    const int rowc = row < S ? row : S - 1;
+
+    const bf16* K = (const bf16*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
+    const bf16* Vg = (const bf16*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
+    const int kend = CAUSAL ? min(S, m0 + BM) : S;
+    const int ntiles = (kend + BN - 1) / BN;
+    issue_tile<DP, BN, NT, SWZ_DUAL>(K, 0, S, D, smem);
+    issue_tile<DP, BN, NT, SWZ_ROW>(Vg, 0, S, D, smem + TILE);
+
+    const bf16* Q = (const bf16*)a.q + (int64_t)(b * a.Hq + h) * S * D;
+    const bf16* G = (const bf16*)a.dO + (int64_t)(b * a.Hq + h) * S * D;
+    bf16x8 qf[NC], gf[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        qf[c] = load_chunk<bf16>(Q + (int64_t)rowc * D, 16 * c + 8 * hh, D, row < S, true);
+        gf[c] = load_chunk<bf16>(G + (int64_t)rowc * D, 16 * c + 8 * hh, D, row < S, true);
+    }
+    const float* blk = a.stats + ((int64_t)(b * a.Hq + h) * a.nqb_total + rowc / 32) * 64;
+    const float lse2 = row < S ? blk[rowc % 32] : INFINITY;
+    const float dlt = row < S ? blk[32 + rowc % 32] : 0.f;
+
+    f32x16 dq[NDT];
+#pragma unroll
+    for (int i = 0; i < NDT; ++i) dq[i] = zero16();
+
+    for (int t = 0; t < ntiles; ++t) {
+        const bf16* Kb = smem + (t & 1) * BUF;
+        const bf16* Vb = Kb + TILE;
+        if (t + 1 < ntiles) {
+            __syncthreads();
+            bf16* nb = smem + ((t + 1) & 1) * BUF;
+            issue_tile<DP, BN, NT, SWZ_DUAL>(K, (t + 1) * BN, S, D, nb);
+            issue_tile<DP, BN, NT, SWZ_ROW>(Vg, (t + 1) * BN, S, D, nb + TILE);
+            wait_vmcnt<LOADS>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        __syncthreads();
+        const int kbase = t * BN;
+        if (wrow0 >= S || (CAUSAL && kbase > wrow0 + 31)) continue;
+
+        const bool need_mask = (CAUSAL && kbase + BN - 1 > wrow0) || (kbase + BN > S);
+#pragma unroll 1
+        for (int kk = 0; kk < NKK; ++kk) {
+            f32x16 s = zero16(), dp = zero16();
+            const int r = 32 * kk + n;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const int col = 16 * c + 8 * hh;
+                s = mfma_bf16(*reinterpret_cast<const bf16x8*>(Kb + tile_off<CPR, SWZ_DUAL>(r, col)), qf[c], s);
+                dp = mfma_bf16(*reinterpret_cast<const bf16x8*>(Vb + tile_off<CPR, SWZ_ROW>(r, col)), gf[c], dp);
+            }
+            // lane column n = query row; register r = key kbase + 32kk + row_of_reg(r, hh)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                float p = fast_exp2(s[q] * a.scale_log2 - lse2);
+                if (need_mask) {
+                    const int kr = kbase + 32 * kk + row_of_reg(q, hh);
+                    if (kr >= S || (CAUSAL && kr > row)) p = 0.f;
+                }
+                s[q] = p * (dp[q] - dlt);
+            }
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                bf16x8 db;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) db[j] = (bf16)s[8 * e + j];
+                const int r0 = 32 * kk + 16 * e + 4 * hh + (i16 >> 2), r1 = r0 + 8;
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) {
+                    const int col = 32 * dt + 16 * nh + 4 * (i16 & 3);
+                    const bf16x4 lo = ds_read_tr4(Kb + tile_off<CPR, SWZ_DUAL>(r0, col));
+                    const bf16x4 hi = ds_read_tr4(Kb + tile_off<CPR, SWZ_DUAL>(r1, col));
+                    const bf16x8 ka = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    dq[dt] = mfma_bf16(ka, db, dq[dt]);
+                }
+            }
+        }
+    }
+    if (row >= S) return;
+    float* dqp = a.dq + ((int64_t)(b * a.Hq + h) * S + row) * D;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            store4<float>(dqp, 32 * dt + 8 * g + 4 * hh, D, dq[dt][4 * g] * a.scale, dq[dt][4 * g + 1] * a.scale,
+                          dq[dt][4 * g + 2] * a.scale, dq[dt][4 * g + 3] * a.scale, true);
+}
+
+template <int DP, bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_bwd_main_bf16_fast(BwdArgs a) {
+    __shared__ __attribute__((aligned(1024))) bf16 smem[BwdFastLds<DP>::ELEMS];
+    int t, y, b;
+    if (decode_block(a, (int)blockIdx.x, &t, &y, &b))
+        dkdv_fast_body<DP, CAUSAL>(a, smem, t, y, b);
+    else
+        dq_fast_body<DP, CAUSAL>(a, smem, t, y, b);
+}
+
+// ----------------------------------------------------------------- REDUCE
 // dk = sum over splits of the dK partials (split order), same for dv.
 __global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(BwdArgs a) {
     const int64_t n = a.part_stride;
@@ -510,44 +877,60 @@ __global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(BwdArgs a) {
     }
 }
 
+constexpr int f32_dkdv_warps(int DP) { return DP >= 256 ? 1 : DP >= 128 ? 2 : 4; }
+constexpr int f32_dq_bn(int DP) { return DP >= 256 ? 32 : 64; }
+
+template <int DP>
+hipError_t launch_bwd_fast(const AttnShape& s, BwdArgs a, int stages, hipStream_t st) {
+    if (stages & BWD_STAGE_DELTA) {
+        constexpr int RPB = 256 / (DP / 8);
+        const int64_t rows = s.B * s.Hq * (int64_t)a.nqb_total * 32;
+        hipLaunchKernelGGL((attn_bwd_stats_kernel<bf16, DP>), dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256), 0,
+                           st, a);
+    }
+    if (stages & BWD_STAGE_MAIN) {
+        const unsigned blocks = (unsigned)(a.n_kv_blocks + a.n_q_blocks);
+        if (s.causal)
+            hipLaunchKernelGGL((attn_bwd_main_bf16_fast<DP, true>), dim3(blocks), dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL((attn_bwd_main_bf16_fast<DP, false>), dim3(blocks), dim3(256), 0, st, a);
+    }
+    if ((stages & BWD_STAGE_REDUCE) && a.splits > 1) {
+        int64_t blocks = (a.part_stride + 255) / 256;
+        if (blocks > 4096) blocks = 4096;
+        hipLaunchKernelGGL(attn_bwd_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
+    }
+    return hipGetLastError();
+}
+
 template <typename T, int DP>
-hipError_t launch_bwd_t(const AttnShape& s, BwdArgs a, hipStream_t st) {
+hipError_t launch_bwd_t(const AttnShape& s, BwdArgs a, int stages, hipStream_t st) {
     constexpr bool BF = sizeof(T) == 2;
-    // prep
-    {
+    if (stages & BWD_STAGE_DELTA) {
         constexpr int TPR = DP / Elt<T>::VEC;
         constexpr int RPB = 256 / TPR;
         const int64_t blocks = (a.total_rows + RPB - 1) / RPB;
-        hipLaunchKernelGGL((attn_bwd_prep_kernel<T, DP>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((attn_bwd_delta_kernel<T, DP>), dim3((unsigned)blocks), dim3(256), 0, st, a);
     }
-    // dK / dV
-    {
-        constexpr int NW = BF ? 4 : (DP >= 256 ? 1 : DP >= 128 ? 2 : 4);
-        constexpr int BNK = 32 * NW;
-        dim3 grid((unsigned)((s.S + BNK - 1) / BNK), (unsigned)(s.Hkv * a.splits), (unsigned)s.B);
+    if (stages & BWD_STAGE_MAIN) {
         if constexpr (BF) {
+            const unsigned blocks = (unsigned)(a.n_kv_blocks + a.n_q_blocks);
             if (s.causal)
-                hipLaunchKernelGGL((attn_bwd_dkdv_bf16<DP, NW, true>), grid, dim3(NW * 64), 0, st, a);
+                hipLaunchKernelGGL((attn_bwd_main_bf16<DP, true>), dim3(blocks), dim3(256), 0, st, a);
             else
-                hipLaunchKernelGGL((attn_bwd_dkdv_bf16<DP, NW, false>), grid, dim3(NW * 64), 0, st, a);
+                hipLaunchKernelGGL((attn_bwd_main_bf16<DP, false>), dim3(blocks), dim3(256), 0, st, a);
         } else {
-            if (s.causal)
-                hipLaunchKernelGGL((attn_bwd_dkdv_f32<DP, NW, true>), grid, dim3(NW * 64), 0, st, a);
-            else
-                hipLaunchKernelGGL((attn_bwd_dkdv_f32<DP, NW, false>), grid, dim3(NW * 64), 0, st, a);
+            constexpr int NW = f32_dkdv_warps(DP), BN = f32_dq_bn(DP);
+            if (s.causal) {
+                hipLaunchKernelGGL((attn_bwd_dkdv_f32<DP, NW, true>), dim3(a.n_kv_blocks), dim3(NW * 64), 0, st, a);
+                hipLaunchKernelGGL((attn_bwd_dq_f32<DP, BN, true>), dim3(a.n_q_blocks), dim3(256), 0, st, a);
+            } else {
+                hipLaunchKernelGGL((attn_bwd_dkdv_f32<DP, NW, false>), dim3(a.n_kv_blocks), dim3(NW * 64), 0, st, a);
+                hipLaunchKernelGGL((attn_bwd_dq_f32<DP, BN, false>), dim3(a.n_q_blocks), dim3(256), 0, st, a);
+            }
         }
     }
-    // dQ
-    {
-        constexpr int NW = 4, BN = (!BF && DP >= 256) ? 32 : 64, BM = 32 * NW;
-        a.n_tiles = (int)((s.S + BM - 1) / BM);
-        dim3 grid((unsigned)a.n_tiles, (unsigned)s.Hq, (unsigned)s.B);
-        if (s.causal)
-            hipLaunchKernelGGL((attn_bwd_dq_kernel<T, DP, NW, BN, true>), grid, dim3(NW * 64), 0, st, a);
-        else
-            hipLaunchKernelGGL((attn_bwd_dq_kernel<T, DP, NW, BN, false>), grid, dim3(NW * 64), 0, st, a);
-    }
-    if (a.splits > 1) {
+    if ((stages & BWD_STAGE_REDUCE) && a.splits > 1) {
         int64_t blocks = (a.part_stride + 255) / 256;
         if (blocks > 4096) blocks = 4096;
         hipLaunchKernelGGL(attn_bwd_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
@@ -556,38 +939,49 @@ hipError_t launch_bwd_t(const AttnShape& s, BwdArgs a, hipStream_t st) {
 }
 
 template <typename T>
-hipError_t launch_bwd_dispatch(const AttnShape& s, const BwdArgs& a, hipStream_t st) {
-    if (s.D <= 32) return launch_bwd_t<T, 32>(s, a, st);
-    if (s.D <= 64) return launch_bwd_t<T, 64>(s, a, st);
-    if (s.D <= 128) return launch_bwd_t<T, 128>(s, a, st);
-    return launch_bwd_t<T, 256>(s, a, st);
+hipError_t launch_bwd_dispatch(const AttnShape& s, const BwdArgs& a, int stages, hipStream_t st) {
+    if (bwd_fast_path(s)) {
+        if (s.D <= 64) return launch_bwd_fast<64>(s, a, stages, st);
+        if (s.D <= 128) return launch_bwd_fast<128>(s, a, stages, st);
+        return launch_bwd_fast<256>(s, a, stages, st);
+    }
+    if (s.D <= 32) return launch_bwd_t<T, 32>(s, a, stages, st);
+    if (s.D <= 64) return launch_bwd_t<T, 64>(s, a, stages, st);
+    if (s.D <= 128) return launch_bwd_t<T, 128>(s, a, stages, st);
+    return launch_bwd_t<T, 256>(s, a, stages, st);
 }
+
+int padded_d(int64_t D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256; }
 
 }  // namespace
 
+bool bwd_fast_path(const AttnShape& s) { return s.bf16 && s.D % 8 == 0 && s.D > 32; }
+
 int dkdv_keys_per_block(const AttnShape& s) {
     if (s.bf16) return 128;
-    return s.D > 128 ? 32 : s.D > 64 ? 64 : 128;
+    return 32 * (padded_d(s.D) >= 256 ? 1 : padded_d(s.D) >= 128 ? 2 : 4);
 }
 
 int dkdv_splits(const AttnShape& s) {
-    // Split the query heads of a group across workgroups until the grid has
-    // about one workgroup per CU; splits must divide the group size.
+    // Split the query heads of a group across workgroups until the whole
+    // MAIN grid (dK/dV blocks + dQ blocks) has about one workgroup per CU;
+    // splits must divide the group size.
     const int64_t group = s.Hq / s.Hkv;
     const int64_t kb = dkdv_keys_per_block(s);
-    const int64_t base = ((s.S + kb - 1) / kb) * s.Hkv * s.B;
+    const int64_t kv_base = ((s.S + kb - 1) / kb) * s.Hkv * s.B;
+    const int64_t q_blocks = s.bf16 ? ((s.S + 127) / 128) * s.Hq * s.B : 0;
     int64_t best = 1;
     for (int64_t d = 1; d <= group; ++d) {
         if (group % d) continue;
         best = d;
-        if (base * d >= 256) break;
+        if (kv_base * d + q_blocks >= 256) break;
     }
     return (int)best;
 }
 
 hipError_t launch_attn_bwd(const AttnShape& s, const void* q, const void* k, const void* v,
                            const void* o, const void* dO, const float* lse, float* dq, float* dk,
-                           float* dv, float* delta, float* part, hipStream_t st) {
+                           float* dv, float* delta, float* part, int stages, hipStream_t st) {
     BwdArgs a;
     a.q = q;
     a.k = k;
@@ -599,6 +993,8 @@ hipError_t launch_attn_bwd(const AttnShape& s, const void* q, const void* k, con
     a.dk = dk;
     a.dv = dv;
     a.delta = delta;
+    a.stats = delta;  // the fast path lays the same workspace out as row-stat blocks
+    a.nqb_total = (int)((s.S + 31) / 32);
     a.part = part;
     a.part_stride = s.B * s.Hkv * s.S * s.D;
     a.total_rows = s.B * s.Hq * s.S;
@@ -606,15 +1002,20 @@ hipError_t launch_attn_bwd(const AttnShape& s, const void* q, const void* k, con
     a.D = (int)s.D;
     a.Hq = (int)s.Hq;
     a.Hkv = (int)s.Hkv;
+    a.B = (int)s.B;
     a.group = (int)(s.Hq / s.Hkv);
     a.splits = dkdv_splits(s);
     a.heads_per_split = a.group / a.splits;
-    a.n_tiles = 0;
+    const int kb = dkdv_keys_per_block(s);
+    a.n_ktiles = (int)((s.S + kb - 1) / kb);
+    a.n_qtiles = (int)((s.S + 127) / 128);
+    a.n_kv_blocks = a.n_ktiles * a.Hkv * a.splits * a.B;
+    a.n_q_blocks = a.n_qtiles * a.Hq * a.B;
     a.scale = s.scale;
     a.scale_log2 = s.scale * kLog2e;
     a.vec_ok = (s.D % (s.bf16 ? 8 : 4)) == 0;
     a.vec4_ok = (s.D % 4) == 0;
-    return s.bf16 ? launch_bwd_dispatch<bf16>(s, a, st) : launch_bwd_dispatch<float>(s, a, st);
+    return s.bf16 ? launch_bwd_dispatch<bf16>(s, a, stages, st) : launch_bwd_dispatch<float>(s, a, stages, st);
 }
 
 }  // namespace mft

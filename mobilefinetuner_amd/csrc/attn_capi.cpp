@@ -52,10 +52,14 @@ mft_status check_desc(const mft_attn_desc* d, mft::AttnShape* s) {
     return MFT_OK;
 }
 
-// Backward workspace: delta [B*Hq*S] fp32, then (splits > 1) dK and dV
-// partials [2 * splits * B*Hkv*S*D] fp32.
+// Backward workspace: per-row softmax terms (fp32), then (splits > 1) dK and
+// dV partials [2 * splits * B*Hkv*S*D] fp32.
 void bwd_layout(const mft::AttnShape& s, size_t* delta_bytes, size_t* part_bytes) {
-    *delta_bytes = round_up(sizeof(float) * static_cast<size_t>(s.B * s.Hq * s.S));
+    // delta [B*Hq*S] (general path) or row-stat blocks [B*Hq*ceil(S/32)*64] (bf16 fast path)
+    const size_t rows = static_cast<size_t>(s.B * s.Hq);
+    const size_t stat_floats = rows * static_cast<size_t>((s.S + 31) / 32) * 64;
+    const size_t delta_floats = rows * static_cast<size_t>(s.S);
+    *delta_bytes = round_up(sizeof(float) * (stat_floats > delta_floats ? stat_floats : delta_floats));
     const int splits = mft::dkdv_splits(s);
     *part_bytes = splits > 1 ? round_up(sizeof(float) * 2 * static_cast<size_t>(splits) *
                                         static_cast<size_t>(s.B * s.Hkv * s.S * s.D))
@@ -98,12 +102,14 @@ mft_status mft_attn_fwd(const mft_attn_desc* desc, const void* q, const void* k,
     return hip_status(mft::launch_attn_fwd(s, q, k, v, o, lse, stream), "mft_attn_fwd launch");
 }
 
-mft_status mft_attn_bwd(const mft_attn_desc* desc, const void* q, const void* k, const void* v, const void* o,
-                        const void* dO, const float* lse, float* dq, float* dk, float* dv, void* workspace,
-                        hipStream_t stream) {
+mft_status mft_attn_bwd_stage(const mft_attn_desc* desc, int stages, const void* q, const void* k,
+                              const void* v, const void* o, const void* dO, const float* lse, float* dq,
+                              float* dk, float* dv, void* workspace, hipStream_t stream) {
     mft::AttnShape s;
     const mft_status st = check_desc(desc, &s);
     if (st != MFT_OK) return st;
+    if (stages <= 0 || (stages & ~MFT_BWD_ALL) != 0)
+        return fail(MFT_ERR_INVALID_ARG, "mft_attn_bwd_stage: stages must be a non-empty mask of MFT_BWD_*");
     if (!q || !k || !v || !o || !dO || !lse || !dq || !dk || !dv)
         return fail(MFT_ERR_INVALID_ARG, "mft_attn_bwd: q, k, v, o, dO, lse, dq, dk, dv must be non-NULL");
     if (!workspace) return fail(MFT_ERR_INVALID_ARG, "mft_attn_bwd: workspace is NULL (see mft_attn_workspace_size)");
@@ -111,8 +117,14 @@ mft_status mft_attn_bwd(const mft_attn_desc* desc, const void* q, const void* k,
     bwd_layout(s, &delta_bytes, &part_bytes);
     float* delta = static_cast<float*>(workspace);
     float* part = part_bytes ? reinterpret_cast<float*>(static_cast<char*>(workspace) + delta_bytes) : nullptr;
-    return hip_status(mft::launch_attn_bwd(s, q, k, v, o, dO, lse, dq, dk, dv, delta, part, stream),
+    return hip_status(mft::launch_attn_bwd(s, q, k, v, o, dO, lse, dq, dk, dv, delta, part, stages, stream),
                       "mft_attn_bwd launch");
+}
+
+mft_status mft_attn_bwd(const mft_attn_desc* desc, const void* q, const void* k, const void* v, const void* o,
+                        const void* dO, const float* lse, float* dq, float* dk, float* dv, void* workspace,
+                        hipStream_t stream) {
+    return mft_attn_bwd_stage(desc, MFT_BWD_ALL, q, k, v, o, dO, lse, dq, dk, dv, workspace, stream);
 }
 
 mft_status mft_repeat_kv_fwd(const void* kv, void* out, int64_t B, int64_t Hkv, int64_t S, int64_t D, int64_t r,

@@ -124,4 +124,92 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 __device__ __forceinline__ float other_half(float x) { return __shfl_xor(x, 32); }
 
+// ---------------------------------------------------------------------------
+// LDS staging primitives of the bf16 fast path (gfx950).
+//
+// global_load_lds_dwordx4: every lane fetches 16 bytes from its own global
+// address and the wave writes them to LDS at base + 16 * lane (measured on
+// gfx950), without passing through VGPRs.  `base` must be wave-uniform.
+// The load counts against vmcnt like an ordinary global load.
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
+
+__device__ __forceinline__ void load_lds_16(const void* gptr, void* lds_base) {
+    __builtin_amdgcn_global_load_lds(gptr, (lds_void_t*)lds_base, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(n) with the other counters left unconstrained (gfx9
+// encoding: vmcnt low bits [3:0], high bits [15:14], expcnt [6:4], lgkmcnt [11:8]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// ds_read_b64_tr_b16 (measured on gfx950): within each aligned group of 16
+// lanes, reader lane j supplies an 8-byte row M[j][0..3]; output lane i gets
+// { M[i/4][i%4], M[4+i/4][i%4], M[8+i/4][i%4], M[12+i/4][i%4] }.  So if lane j
+// reads X[r0 + j/4][c0 + 4*(j%4) .. +3] of a row-major b16 matrix, lane i
+// receives X[r0 + 0..3][c0 + i]: four consecutive rows of one column.
+__device__ __forceinline__ bf16x4 ds_read_tr4(const bf16* lds_elem_ptr) {
+    const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(lds_elem_ptr));
+    return __builtin_bit_cast(bf16x4, r);
+}
+
+// XOR swizzles of 16-byte chunks inside an unpadded LDS tile row of CPR
+// chunks (CPR = row bytes / 16; 8, 16 or 32).  A tile element (r, col) lives
+// at r * ROW + ((col / 8) ^ swz(r)) * 8 + col % 8 (bf16 elements).
+// LDS has 64 four-byte banks (256 bytes per cycle).
+//  swz_row : for row reads, where 16 lanes read one chunk column of 16
+//            consecutive rows (ds_read_b128) -> 16 distinct bank groups.
+//  swz_tr  : for transposing reads, where a wave reads 8 consecutive rows x
+//            64 bytes (ds_read_b64_tr_b16) -> 2 cycles, the minimum.
+//  swz_dual: both patterns at their minimum (tiles read both ways).
+template <int CPR> __device__ __forceinline__ int swz_row(int r) {
+    return CPR >= 16 ? (r & 15) : ((r >> 1) & 7);
+}
+template <int CPR> __device__ __forceinline__ int swz_tr(int r) {
+    return (CPR >= 16 ? (r & 3) : ((r >> 1) & 1)) << 2;
+}
+template <int CPR> __device__ __forceinline__ int swz_dual(int r) {
+    return CPR >= 16 ? (4 * (r & 3) + ((r >> 2) & 3)) : (4 * ((r >> 1) & 1) + ((r >> 2) & 3));
+}
+
+enum { SWZ_ROW = 0, SWZ_TR = 1, SWZ_DUAL = 2 };
+
+template <int CPR, int SWZ> __device__ __forceinline__ int swz(int r) {
+    return SWZ == SWZ_ROW ? swz_row<CPR>(r) : SWZ == SWZ_TR ? swz_tr<CPR>(r) : swz_dual<CPR>(r);
+}
+
+// Element offset of (row r, column col) in a swizzled bf16 tile.
+template <int CPR, int SWZ>
+__device__ __forceinline__ int tile_off(int r, int col) {
+    return r * (CPR * 8) + (((col >> 3) ^ swz<CPR, SWZ>(r)) << 3) + (col & 7);
+}
+
+// Issue the direct loads of a [ROWS x DP] bf16 tile whose first global row is
+// row0 (row stride D elements) into a swizzled LDS tile.  NT threads share
+// the work; every thread issues ROWS*DP/8/NT loads (wave-uniform count).
+// Rows >= S read row S-1 and chunks >= D read chunk 0, so every address is
+// in bounds; callers mask such rows and never use such columns.
+template <int DP, int ROWS, int NT, int SWZ>
+__device__ __forceinline__ void issue_tile(const bf16* __restrict__ src, int row0, int S, int D,
+                                           bf16* lds_tile) {
+    constexpr int CPR = DP / 8;
+    constexpr int PER_WAVE = ROWS * CPR / NT;
+    static_assert(PER_WAVE * NT == ROWS * CPR, "tile must split evenly over the threads");
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int j = 0; j < PER_WAVE; ++j) {
+        const int m = w * PER_WAVE + j;
+        const int P = m * 64 + lane;
+        const int r = P / CPR, p = P % CPR;
+        const int c = p ^ swz<CPR, SWZ>(r);
+        const int gr = min(row0 + r, S - 1);
+        const int col = 8 * c < D ? 8 * c : 0;
+        load_lds_16(src + (int64_t)gr * D + col, lds_tile + m * 512);
+    }
+}
+
 }  // namespace mft

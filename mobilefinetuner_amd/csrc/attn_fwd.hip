@@ -226,6 +226,166 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
     if (a.lse && hh == 0) a.lse[(int64_t)(b * a.Hq + h) * S + row] = (m_run + log2f(l_tot)) * kLn2;
 }
 
+// ---------------------------------------------------------------------------
+// bf16 fast path (D % 8 == 0, 32 < D <= 256).
+//
+// Same decomposition and math as attn_fwd_kernel, but K/V tiles move
+// HBM -> LDS with global_load_lds_dwordx4 (no VGPR round trip), double
+// buffered so the next tile streams in while the current one is computed.
+// LDS rows are unpadded and XOR-swizzled in 16-byte chunks:
+//   K: swz_row (row reads of the S^T A operand), V: swz_tr (transposing
+//      reads of the O^T A operand); see attn_common.h.
+// V stays row-major; the transposing LDS read delivers V^T to the MFMA A
+// operand directly (see ds_read_tr4).
+
+template <int DP, bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_fwd_bf16_fast(FwdArgs a) {
+    constexpr int NW = 4, BN = 64, BM = 32 * NW, NT = 256;
+    constexpr int CPR = DP / 8, NC = DP / 16, NDT = DP / 32, NKK = BN / 32;
+    constexpr int TILE = BN * DP;                       // elements of one K or V tile
+    constexpr int LOADS = 2 * BN * CPR / NT;            // direct loads per thread per tile
+    __shared__ __attribute__((aligned(1024))) bf16 smem[2 * 2 * TILE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
+    const int S = a.S, D = a.D;
+    const int qt = a.n_qtiles - 1 - (int)blockIdx.x;
+    const int h = blockIdx.y, b = blockIdx.z, hk = h / a.group;
+    const int m0 = qt * BM;
+    const int wrow0 = m0 + 32 * w;
+    const int row = wrow0 + n;
+    const int rowc = row < S ? row : S - 1;
+
+    const bf16* __restrict__ Q = (const bf16*)a.q + (int64_t)(b * a.Hq + h) * S * D;
+    const bf16* __restrict__ K = (const bf16*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
+    const bf16* __restrict__ Vg = (const bf16*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
+
+    const int kend = CAUSAL ? min(S, m0 + BM) : S;
+    const int ntiles = (kend + BN - 1) / BN;
+    issue_tile<DP, BN, NT, SWZ_ROW>(K, 0, S, D, smem);
+    issue_tile<DP, BN, NT, SWZ_TR>(Vg, 0, S, D, smem + TILE);
+
+    bf16x8 qf[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+        qf[c] = load_chunk<bf16>(Q + (int64_t)rowc * D, 16 * c + 8 * hh, D, row < S, true);
+
+    f32x16 oacc[NDT];
+#pragma unroll
+    for (int i = 0; i < NDT; ++i) oacc[i] = zero16();
+    float m_run = -INFINITY, l_run = 0.f;
+
+    const int g16 = lane >> 4, i16 = lane & 15, nh = g16 & 1;
+    for (int t = 0; t < ntiles; ++t) {
+        const bf16* Kb = smem + (t & 1) * 2 * TILE;
+        const bf16* Vb = Kb + TILE;
+        if (t + 1 < ntiles) {
+            __syncthreads();  // every wave is done with the buffer tile t+1 reuses
+            bf16* nb = smem + ((t + 1) & 1) * 2 * TILE;
+            issue_tile<DP, BN, NT, SWZ_ROW>(K, (t + 1) * BN, S, D, nb);
+            issue_tile<DP, BN, NT, SWZ_TR>(Vg, (t + 1) * BN, S, D, nb + TILE);
+            wait_vmcnt<LOADS>();  // this thread's loads of tile t have landed
+        } else {
+            wait_vmcnt<0>();
+        }
+        __syncthreads();  // ... and everyone else's
+        const int kbase = t * BN;
+        if (wrow0 >= S || (CAUSAL && kbase > wrow0 + 31)) continue;
+
+        f32x16 s[NKK];
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) {
+            s[kk] = zero16();
+            const int r = 32 * kk + n;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const bf16x8 ka = *reinterpret_cast<const bf16x8*>(Kb + tile_off<CPR, SWZ_ROW>(r, 16 * c + 8 * hh));
+                s[kk] = mfma_bf16(ka, qf[c], s[kk]);
+            }
+        }
+
+        const bool need_mask = (CAUSAL && kbase + BN - 1 > wrow0) || (kbase + BN > S);
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float x = s[kk][r];
+                if (need_mask) {
+                    const int key = kbase + 32 * kk + row_of_reg(r, hh);
+                    if (key >= S || (CAUSAL && key > row)) x = -INFINITY;
+                }
+                s[kk][r] = x;
+                mx = fmaxf(mx, x);
+            }
+        }
+        mx = fmaxf(mx, other_half(mx));
+        const float m_new = fmaxf(m_run, mx * a.scale_log2);
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        const float alpha = fast_exp2(m_run - m_use);
+        float psum = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = fast_exp2(s[kk][r] * a.scale_log2 - m_use);
+                s[kk][r] = p;
+                psum += p;
+            }
+        }
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                bf16x8 pb;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) pb[j] = (bf16)s[kk][8 * e + j];
+                const int r0 = 32 * kk + 16 * e + 4 * hh + (i16 >> 2);
+                const int r1 = r0 + 8;
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) {
+                    const int col = 32 * dt + 16 * nh + 4 * (i16 & 3);
+                    const bf16x4 lo = ds_read_tr4(Vb + tile_off<CPR, SWZ_TR>(r0, col));
+                    const bf16x4 hi = ds_read_tr4(Vb + tile_off<CPR, SWZ_TR>(r1, col));
+                    const bf16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    oacc[dt] = mfma_bf16(va, pb, oacc[dt]);
+                }
+            }
+        }
+    }
+
+    if (wrow0 >= S) return;
+    const float l_tot = l_run + other_half(l_run);
+    if (row >= S) return;
+    const float inv = 1.f / l_tot;
+    bf16* O = (bf16*)a.o + (int64_t)(b * a.Hq + h) * S * D + (int64_t)row * D;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            store4<bf16>(O, 32 * dt + 8 * g + 4 * hh, D, oacc[dt][4 * g] * inv, oacc[dt][4 * g + 1] * inv,
+                         oacc[dt][4 * g + 2] * inv, oacc[dt][4 * g + 3] * inv, true);
+    if (a.lse && hh == 0) a.lse[(int64_t)(b * a.Hq + h) * S + row] = (m_run + log2f(l_tot)) * kLn2;
+}
+
+template <int DP>
+hipError_t launch_fwd_fast(const AttnShape& s, FwdArgs a, hipStream_t st) {
+    a.n_qtiles = (int)((s.S + 127) / 128);
+    dim3 grid(a.n_qtiles, (unsigned)s.Hq, (unsigned)s.B);
+    if (s.causal)
+        hipLaunchKernelGGL((attn_fwd_bf16_fast<DP, true>), grid, dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((attn_fwd_bf16_fast<DP, false>), grid, dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
 template <typename T, int DP, int NW, int BN>
 hipError_t launch_fwd_t(const AttnShape& s, FwdArgs a, hipStream_t st) {
     constexpr int BM = 32 * NW;
@@ -241,6 +401,13 @@ hipError_t launch_fwd_t(const AttnShape& s, FwdArgs a, hipStream_t st) {
 template <typename T>
 hipError_t launch_fwd_dispatch(const AttnShape& s, FwdArgs a, hipStream_t st) {
     constexpr bool F32 = sizeof(T) == 4;
+    if constexpr (!F32) {
+        if (s.D % 8 == 0 && s.D > 32) {
+            if (s.D <= 64) return launch_fwd_fast<64>(s, a, st);
+            if (s.D <= 128) return launch_fwd_fast<128>(s, a, st);
+            return launch_fwd_fast<256>(s, a, st);
+        }
+    }
     if (s.D <= 32) return launch_fwd_t<T, 32, 4, 64>(s, a, st);
     if (s.D <= 64) return launch_fwd_t<T, 64, 4, 64>(s, a, st);
     if (s.D <= 128) return launch_fwd_t<T, 128, 4, 64>(s, a, st);

@@ -1,0 +1,141 @@
+"""Write the golden fixtures of the attention path from the REAL reference.
+
+Runs in the build container only (it needs oracle/_ref/libmftref.so, which is
+compiled from /root/reference by oracle/Makefile).  Outputs, all data:
+
+  tests/golden/tiny.npz      full tensors of small cases: the deterministic
+                             fills and shapes of the reference's four hot-path
+                             unit tests plus seeded GQA cases
+  tests/golden/<cfg>.npz     for each BASELINE.json config: the first values
+                             of every input stream, input checksums, and for
+                             O, dQ, dK, dV the L2 norm, max |x| and 2048
+                             sampled (flat index, value) pairs
+
+While generating, the restatement (oracle/refcpu.cpp) is run on the same
+inputs and must be bit-identical to the reference; the outcome is stored as
+`refcpu_bitwise` in each fixture.
+
+    python tests/golden/make_golden.py [cfg ...]
+"""
+from __future__ import annotations
+
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+from oracle import oracle as O  # noqa: E402
+
+NSAMPLE = 2048
+
+
+def fill(shape, a, m, o):
+    return O.fill_mod(int(np.prod(shape)), a, m, o).reshape(shape)
+
+
+def tiny_cases():
+    """(name, q, k, v, dO, scale, causal).  Fills cite the reference tests."""
+    cases = []
+    # optim/test_qkt_softmax_grad.cpp:28-59 (q, k fills; scale 256^-0.5; no mask).
+    # That test has no V; v takes the fill of test_repeat_kv_softmax_grad.cpp:52.
+    s = (1, 1, 3, 4)
+    cases.append(("qkt_softmax_grad", fill(s, 0.1, 7, 3), fill(s, 0.07, 5, 2), fill(s, 0.03, 5, 2),
+                  fill(s, 0.03, 11, 5), 256.0 ** -0.5, False))
+    # optim/test_repeat_kv_softmax_grad.cpp:26-79: kvH=1 -> H=4, S=3, D=4, mask off.
+    qs, ks = (1, 4, 3, 4), (1, 1, 3, 4)
+    cases.append(("repeat_kv_softmax_grad", fill(qs, 0.05, 9, 4), fill(ks, 0.04, 7, 3),
+                  fill(ks, 0.03, 5, 2), fill(qs, 0.02, 11, 5), 0.5, False))
+    # optim/test_attention_single_layer_backward.cpp:50-108: B=1,H=4,S=8,D=8, kvH=1, causal.
+    qs, ks = (1, 4, 8, 8), (1, 1, 8, 8)
+    cases.append(("attention_single_layer_backward", fill(qs, 0.013, 17, 8), fill(ks, 0.011, 13, 6),
+                  fill(ks, 0.015, 19, 9), fill(qs, 0.02, 11, 5), 256.0 ** -0.5, True))
+    # core/test_memory_efficient_attention_grad.cpp:61-87: B=1,H=2,S=4,D=3, causal.
+    s = (1, 2, 4, 3)
+    cases.append(("memory_efficient_attention_grad", fill(s, 0.07, 11, 5), fill(s, 0.05, 9, 4),
+                  fill(s, 0.03, 7, 3), fill(s, 0.02, 13, 6), 1.0 / math.sqrt(3.0), True))
+    # Seeded GQA cases (groups of 4 and 7, D 64 and 256, causal on and off).
+    for i, (B, Hq, Hkv, S, D, causal) in enumerate([(1, 4, 1, 64, 64, True), (1, 7, 1, 48, 64, False),
+                                                    (2, 8, 2, 40, 256, True), (1, 14, 2, 33, 64, True)]):
+        q, k, v, dO = O.make_inputs(B, Hq, Hkv, S, D, 500 + i, "f32", 0.5)
+        cases.append((f"gqa_{B}x{Hq}x{Hkv}x{S}x{D}_{'causal' if causal else 'full'}", q, k, v, dO,
+                      1.0 / math.sqrt(D), causal))
+    return cases
+
+
+def bitwise(a, b):
+    return bool(np.array_equal(np.asarray(a, np.float32).view(np.uint32),
+                               np.asarray(b, np.float32).view(np.uint32)))
+
+
+def make_tiny():
+    out = {}
+    names = []
+    for name, q, k, v, dO, scale, causal in tiny_cases():
+        r = O.ref_composite(q, k, v, dO, scale=scale, causal=causal)
+        m = O.composite(q, k, v, dO, scale=scale, causal=causal)
+        ok = all(bitwise(m[n], r[n]) for n in ("o", "dq", "dk", "dv"))
+        print(f"[tiny] {name}: refcpu bitwise={ok}")
+        names.append(name)
+        for key, arr in (("q", q), ("k", k), ("v", v), ("dO", dO), ("o", r["o"]), ("dq", r["dq"]),
+                         ("dk", r["dk"]), ("dv", r["dv"])):
+            out[f"{name}/{key}"] = np.asarray(arr, np.float32)
+        out[f"{name}/scale"] = np.float32(scale)
+        out[f"{name}/causal"] = np.int32(causal)
+        out[f"{name}/refcpu_bitwise"] = np.int32(ok)
+    out["names"] = np.array(names)
+    np.savez_compressed(os.path.join(HERE, "tiny.npz"), **out)
+
+
+def make_config(cfg):
+    c = O.CONFIGS[cfg]
+    seed = O.SEEDS[cfg]
+    q, k, v, dO = O.config_inputs(cfg)
+    rng = np.random.default_rng(seed)
+    t0 = time.time()
+    r = O.ref_composite(q, k, v, dO, scale=c["scale"], causal=True)
+    t_ref = time.time() - t0
+    t0 = time.time()
+    m = O.composite(q, k, v, dO, scale=c["scale"], causal=True)
+    t_orc = time.time() - t0
+    ok = all(bitwise(m[n], r[n]) for n in ("o", "dq", "dk", "dv"))
+    print(f"[{cfg}] ref {t_ref:.1f}s (fwd {r['t_fwd']:.2f} bwd {r['t_bwd']:.2f}) refcpu {t_orc:.1f}s "
+          f"bitwise={ok} held={r['held_bytes'] / 2**20:.1f} MiB")
+    out = dict(cfg=cfg, seed=np.int64(seed), scale=np.float32(c["scale"]),
+               refcpu_bitwise=np.int32(ok), held_bytes=np.int64(r["held_bytes"]),
+               ref_t_fwd=np.float64(r["t_fwd"]), ref_t_bwd=np.float64(r["t_bwd"]))
+    for name, arr in (("q", q), ("k", k), ("v", v), ("dO", dO)):
+        flat = arr.reshape(-1)
+        out[f"in_{name}_head"] = flat[:8].copy()
+        out[f"in_{name}_sum"] = np.float64(np.sum(flat, dtype=np.float64))
+        out[f"in_{name}_abssum"] = np.float64(np.sum(np.abs(flat), dtype=np.float64))
+    for name in ("o", "dq", "dk", "dv"):
+        flat = r[name].reshape(-1)
+        idx = np.sort(rng.choice(flat.size, size=min(NSAMPLE, flat.size), replace=False)).astype(np.int64)
+        out[f"{name}_idx"] = idx
+        out[f"{name}_val"] = flat[idx].copy()
+        out[f"{name}_l2"] = np.float64(np.sqrt(np.sum(flat.astype(np.float64) ** 2)))
+        out[f"{name}_maxabs"] = np.float64(np.max(np.abs(flat)))
+        out[f"{name}_sum"] = np.float64(np.sum(flat, dtype=np.float64))
+    np.savez_compressed(os.path.join(HERE, f"{cfg}.npz"), **out)
+
+
+def main(argv):
+    if not O.ref_available():
+        O.build()
+    if not O.ref_available():
+        raise SystemExit("oracle/_ref/libmftref.so could not be built (needs /root/reference)")
+    todo = argv or ["tiny", "c1", "c2", "c4", "c5", "c5f32", "c3"]
+    for t in todo:
+        if t == "tiny":
+            make_tiny()
+        else:
+            make_config(t)
+
+
+if __name__ == "__main__":
+    main(sys.argv[1:])
