@@ -39,6 +39,12 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm toolchain required to build libmft_attn.so)")
 
 
+# Files whose MFMA accumulators should be allocated in VGPRs: their kernels
+# keep all live state within 256 VGPRs, and the VGPR form avoids copying the
+# loop-carried accumulators between AGPRs and VGPRs on every iteration.
+VGPR_FORM = {"attn_fwd.hip", "attn_bwd_fast64.hip"}
+
+
 def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC)
                   if f.endswith((".hip", ".cpp")))
@@ -47,6 +53,8 @@ def sources():
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
     cmd = [hipcc(), *HIP_FLAGS, "-I", os.path.join(ROOT, "include"), "-I", CSRC, "-c", src, "-o", obj]
+    if os.path.basename(src) in VGPR_FORM:
+        cmd[1:1] = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
     if src.endswith(".cpp"):
         cmd[1:1] = ["-x", "hip"]
     res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)

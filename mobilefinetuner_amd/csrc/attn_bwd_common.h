@@ -1,0 +1,116 @@
+// Backward definitions shared by the general (attn_bwd.hip) and bf16 fast
+// path (attn_bwd_fast.h) translation units.
+#pragma once
+
+#include "attn_common.h"
+#include "attn_kernels.h"
+
+namespace mft {
+namespace bwd {
+
+struct BwdArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    const void* o;
+    const void* dO;
+    const float* lse;
+    float* dq;
+    float* dk;
+    float* dv;
+    float* delta;
+    float* part;
+    float* stats;         // fast path: per 32-row block [32 x lse*log2e][32 x delta]
+    int nqb_total;        // 32-row blocks per head (ceil(S / 32))
+    int64_t part_stride;  // B*Hkv*S*D
+    int64_t total_rows;   // B*Hq*S
+    int S, D, Hq, Hkv, B, group, splits, heads_per_split;
+    int n_ktiles, n_qtiles;   // key tiles of the dK/dV role, query tiles of the dQ role
+    int n_kv_blocks, n_q_blocks;
+    float scale, scale_log2;
+    int vec_ok, vec4_ok;
+};
+
+// Output rows of dK / dV for a split.
+__device__ __forceinline__ void dkdv_out_rows(const BwdArgs& a, int b, int hk, int split, int key,
+                                              float** dkp, float** dvp) {
+    const int64_t off = ((int64_t)(b * a.Hkv + hk) * a.S + key) * a.D;
+    if (a.splits == 1) {
+        *dkp = a.dk + off;
+        *dvp = a.dv + off;
+    } else {
+        *dkp = a.part + (int64_t)split * a.part_stride + off;
+        *dvp = a.part + (int64_t)(a.splits + split) * a.part_stride + off;
+    }
+}
+
+template <int NDT>
+__device__ __forceinline__ void store_dkdv(const BwdArgs& a, float* dkp, float* dvp, int hh, const f32x16 (&dk)[NDT],
+                                           const f32x16 (&dv)[NDT]) {
+    const bool v4 = a.vec4_ok != 0;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d0 = 32 * dt + 8 * g + 4 * hh;
+            store4<float>(dkp, d0, a.D, dk[dt][4 * g] * a.scale, dk[dt][4 * g + 1] * a.scale,
+                          dk[dt][4 * g + 2] * a.scale, dk[dt][4 * g + 3] * a.scale, v4);
+            store4<float>(dvp, d0, a.D, dv[dt][4 * g], dv[dt][4 * g + 1], dv[dt][4 * g + 2], dv[dt][4 * g + 3], v4);
+        }
+}
+
+// Block -> role.  Roles alternate while both have blocks left; within a role
+// the heaviest causal tiles come first (small key tiles for dK/dV, large
+// query tiles for dQ).
+__device__ __forceinline__ bool decode_block(const BwdArgs& a, int bid, int* t, int* y, int* b) {
+    const int m = min(a.n_kv_blocks, a.n_q_blocks);
+    bool kv;
+    int i;
+    if (bid < 2 * m) {
+        kv = (bid & 1) == 0;
+        i = bid >> 1;
+    } else {
+        kv = a.n_kv_blocks > a.n_q_blocks;
+        i = bid - m;
+    }
+    if (kv) {
+        const int yb = a.Hkv * a.splits * a.B;
+        *t = i / yb;
+        const int rest = i - *t * yb;
+        *y = rest % (a.Hkv * a.splits);
+        *b = rest / (a.Hkv * a.splits);
+    } else {
+        const int yb = a.Hq * a.B;
+        const int ti = i / yb;
+        const int rest = i - ti * yb;
+        *t = a.n_qtiles - 1 - ti;
+        *y = rest % a.Hq;
+        *b = rest / a.Hq;
+    }
+    return kv;
+}
+
+// ----------------------------------------------------------------- REDUCE
+// dk = sum over splits of the dK partials (split order), same for dv.
+static __global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(BwdArgs a) {
+    const int64_t n = a.part_stride;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        float sk = 0.f, sv = 0.f;
+        for (int s = 0; s < a.splits; ++s) {
+            sk += a.part[(int64_t)s * n + i];
+            sv += a.part[(int64_t)(a.splits + s) * n + i];
+        }
+        a.dk[i] = sk;
+        a.dv[i] = sv;
+    }
+}
+
+
+// Launchers of the bf16 fast path (attn_bwd_fast.h), one per padded head dim.
+hipError_t launch_bwd_fast_64(const AttnShape& s, const BwdArgs& a, int stages, hipStream_t st);
+hipError_t launch_bwd_fast_128(const AttnShape& s, const BwdArgs& a, int stages, hipStream_t st);
+hipError_t launch_bwd_fast_256(const AttnShape& s, const BwdArgs& a, int stages, hipStream_t st);
+
+}  // namespace bwd
+}  // namespace mft

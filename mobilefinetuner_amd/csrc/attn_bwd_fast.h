@@ -1,0 +1,325 @@
+// bf16 fast path of the attention backward (D % 8 == 0, 32 < D <= 256).
+// Included by attn_bwd_fast64.hip (D <= 128 instantiations) and
+// attn_bwd_fast256.hip, which are compiled with different MFMA register
+// forms (see mobilefinetuner_amd/build.py).
+#pragma once
+
+#include "attn_bwd_common.h"
+
+namespace mft {
+namespace bwd {
+namespace {
+
+// ===========================================================================
+// bf16 fast path (D % 8 == 0, 32 < D <= 256)
+//
+// The same two roles, with all tile traffic moved HBM -> LDS by
+// global_load_lds_dwordx4 into double buffers (the next block streams in
+// while the current one is multiplied), unpadded XOR-swizzled LDS tiles, and
+// every transposed operand (dO^T, Q^T for dV/dK, K^T for dQ) read with
+// ds_read_b64_tr_b16 from the row-major tile instead of being stored twice.
+//
+// STATS stage: stats[(b*Hq + h) * nqb + blk][0..31] = lse * log2(e) of rows
+// 32*blk + 0..31 (+inf past S), [32..63] = delta (0 past S).  256-byte blocks
+// let the dK/dV role fetch a query block's row terms with one direct load.
+template <typename T, int DP>
+__global__ __launch_bounds__(256) void attn_bwd_stats_kernel(BwdArgs a) {
+    typedef typename Elt<T>::vec V;
+    constexpr int VEC = Elt<T>::VEC;
+    constexpr int TPR = DP / VEC;
+    constexpr int RPB = 256 / TPR;
+    const int64_t spad = (int64_t)a.nqb_total * 32;
+    const int64_t total = (int64_t)a.B * a.Hq * spad;
+    const int64_t prow = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;  // padded row index
+    const int c = threadIdx.x % TPR;
+    const int64_t bh = prow / spad;
+    const int i = (int)(prow - bh * spad);
+    const bool valid = prow < total && i < a.S;
+    float acc = 0.f;
+    if (valid) {
+        const int64_t row = bh * a.S + i;
+        const V x = load_chunk<T>((const T*)a.o + row * a.D, c * VEC, a.D, true, a.vec_ok != 0);
+        const V y = load_chunk<T>((const T*)a.dO + row * a.D, c * VEC, a.D, true, a.vec_ok != 0);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) acc += (float)x[k] * (float)y[k];
+    }
+#pragma unroll
+    for (int off = TPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+    if (prow < total && c == 0) {
+        float* blk = a.stats + (bh * a.nqb_total + i / 32) * 64;
+        blk[i % 32] = valid ? a.lse[bh * a.S + i] * kLog2e : INFINITY;
+        blk[32 + i % 32] = valid ? acc : 0.f;
+    }
+}
+
+template <int DP> struct BwdFastLds {
+    // V_LDS: the dK/dV role reads V of its 128 keys from LDS (B operand of
+    // dP) instead of keeping it in registers; a register-pressure fallback,
+    // off while K, V, dK and dV fit in the 512 VGPRs of a wave.
+    static constexpr bool V_LDS = false;
+    static constexpr int KV_BUF = 2 * 32 * DP + 4 * 512;  // Q, dO tiles + 4 waves x 1 KiB stats (elements)
+    static constexpr int KV_ELEMS = 2 * KV_BUF + (V_LDS ? 128 * DP : 0);
+    static constexpr int Q_BUF = 2 * 64 * DP;             // K, V tiles
+    static constexpr int Q_ELEMS = 2 * Q_BUF;
+    static constexpr int ELEMS = KV_ELEMS > Q_ELEMS ? KV_ELEMS : Q_ELEMS;
+};
+
+template <int DP, bool CAUSAL>
+__device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int kt, int ysplit, int b) {
+    constexpr int NT = 256, BNK = 128, CPR = DP / 8, NC = DP / 16, NDT = DP / 32;
+    constexpr int QT = 32 * DP;
+    constexpr int BUF = BwdFastLds<DP>::KV_BUF;
+    constexpr int LOADS = 2 * (32 * CPR / NT) + 1;
+    constexpr bool V_LDS = BwdFastLds<DP>::V_LDS;
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
+    const int i16 = lane & 15, nh = (lane >> 4) & 1;
+    const int S = a.S, D = a.D;
+    const int j0 = kt * BNK;
+    const int hk = ysplit / a.splits, split = ysplit % a.splits;
+    const int h_begin = hk * a.group + split * a.heads_per_split;
+    const int h_end = min(h_begin + a.heads_per_split, (hk + 1) * a.group);
+    const int wkey0 = j0 + 32 * w;
+    const int key = wkey0 + n;
+    const int keyc = key < S ? key : S - 1;
+
+    const bf16* K = (const bf16*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
+    const bf16* Vg = (const bf16*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
+    const int qstart = CAUSAL ? j0 : 0;
+    const int nqb = (S - qstart + 31) / 32;
+    const int niter = (h_end - h_begin) * nqb;
+
+    auto issue = [&](int it, bf16* buf) {
+        const int h = h_begin + it / nqb, qb = qstart + (it % nqb) * 32;
+        const int64_t hoff = (int64_t)(b * a.Hq + h) * S * D;
+        issue_tile<DP, 32, NT, SWZ_DUAL>((const bf16*)a.q + hoff, qb, S, D, buf);
+        issue_tile<DP, 32, NT, SWZ_DUAL>((const bf16*)a.dO + hoff, qb, S, D, buf + QT);
+        const float* st = a.stats + ((int64_t)(b * a.Hq + h) * a.nqb_total + qb / 32) * 64;
+        load_lds_16(st + 4 * i16, buf + 2 * QT + w * 512);
+    };
+    bf16* Vl = smem + 2 * BUF;  // V rows of this workgroup's keys (V_LDS only)
+    if constexpr (V_LDS) issue_tile<DP, BNK, NT, SWZ_ROW>(Vg, j0, S, D, Vl);
+    if (niter > 0) issue(0, smem);
+
+    bf16x8 kf[NC], vf[V_LDS ? 1 : NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        kf[c] = load_chunk<bf16>(K + (int64_t)keyc * D, 16 * c + 8 * hh, D, key < S, true);
+        if constexpr (!V_LDS) vf[c] = load_chunk<bf16>(Vg + (int64_t)keyc * D, 16 * c + 8 * hh, D, key < S, true);
+    }
+    f32x16 dk[NDT], dv[NDT];
+#pragma unroll
+    for (int i = 0; i < NDT; ++i) {
+        dk[i] = zero16();
+        dv[i] = zero16();
+    }
+
+    for (int it = 0; it < niter; ++it) {
+        const bf16* Qb = smem + (it & 1) * BUF;
+        const bf16* Gb = Qb + QT;
+        const float* stt = reinterpret_cast<const float*>(Qb + 2 * QT + w * 512);
+        if (it + 1 < niter) {
+            __syncthreads();
+            issue(it + 1, smem + ((it + 1) & 1) * BUF);
+            wait_vmcnt<LOADS>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        __syncthreads();
+        const int qb = qstart + (it % nqb) * 32;
+        if (wkey0 >= S) continue;
+        if (CAUSAL && qb + 31 < wkey0) continue;
+
+        f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int col = 16 * c + 8 * hh;
+            s = mfma_bf16(*reinterpret_cast<const bf16x8*>(Qb + tile_off<CPR, SWZ_DUAL>(n, col)), kf[c], s);
+            bf16x8 vb;
+            if constexpr (V_LDS)
+                vb = *reinterpret_cast<const bf16x8*>(Vl + tile_off<CPR, SWZ_ROW>(32 * w + n, col));
+            else
+                vb = vf[c];
+            dp = mfma_bf16(*reinterpret_cast<const bf16x8*>(Gb + tile_off<CPR, SWZ_DUAL>(n, col)), vb, dp);
+        }
+        // lane column n = key; register r = query qb + row_of_reg(r, hh)
+        const bool need_mask = CAUSAL && qb < wkey0 + 31;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const f32x4 l4 = *reinterpret_cast<const f32x4*>(stt + 8 * g + 4 * hh);
+            const f32x4 d4 = *reinterpret_cast<const f32x4*>(stt + 32 + 8 * g + 4 * hh);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 4 * g + i;
+                float p = fast_exp2(s[r] * a.scale_log2 - l4[i]);
+                p = (need_mask && qb + 8 * g + 4 * hh + i < key) ? 0.f : p;
+                dp[r] = p * (dp[r] - d4[i]);
+                s[r] = p;
+            }
+        }
+#pragma unroll 1
+        for (int e = 0; e < 2; ++e) {
+            bf16x8 pb, db;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                pb[j] = (bf16)s[8 * e + j];
+                db[j] = (bf16)dp[8 * e + j];
+            }
+            const int r0 = 16 * e + 4 * hh + (i16 >> 2), r1 = r0 + 8;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                const int col = 32 * dt + 16 * nh + 4 * (i16 & 3);
+                const bf16x4 glo = ds_read_tr4(Gb + tile_off<CPR, SWZ_DUAL>(r0, col));
+                const bf16x4 ghi = ds_read_tr4(Gb + tile_off<CPR, SWZ_DUAL>(r1, col));
+                const bf16x8 ga = {glo[0], glo[1], glo[2], glo[3], ghi[0], ghi[1], ghi[2], ghi[3]};
+                dv[dt] = mfma_bf16(ga, pb, dv[dt]);
+                const bf16x4 qlo = ds_read_tr4(Qb + tile_off<CPR, SWZ_DUAL>(r0, col));
+                const bf16x4 qhi = ds_read_tr4(Qb + tile_off<CPR, SWZ_DUAL>(r1, col));
+                const bf16x8 qa = {qlo[0], qlo[1], qlo[2], qlo[3], qhi[0], qhi[1], qhi[2], qhi[3]};
+                dk[dt] = mfma_bf16(qa, db, dk[dt]);
+            }
+        }
+    }
+    if (key >= S) return;
+    float *dkp, *dvp;
+    dkdv_out_rows(a, b, hk, split, key, &dkp, &dvp);
+    store_dkdv<NDT>(a, dkp, dvp, hh, dk, dv);
+}
+
+template <int DP, bool CAUSAL>
+__device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int qt, int h, int b) {
+    constexpr int NT = 256, BN = 64, BM = 128, CPR = DP / 8, NC = DP / 16, NDT = DP / 32, NKK = BN / 32;
+    constexpr int TILE = BN * DP;
+    constexpr int BUF = BwdFastLds<DP>::Q_BUF;
+    constexpr int LOADS = 2 * (BN * CPR / NT);
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
+    const int i16 = lane & 15, nh = (lane >> 4) & 1;
+    const int S = a.S, D = a.D;
+    const int hk = h / a.group;
+    const int m0 = qt * BM, wrow0 = m0 + 32 * w, row = wrow0 + n;
+    const int rowc = row < S ? row : S - 1;
+
+    const bf16* K = (const bf16*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
+    const bf16* Vg = (const bf16*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
+    const int kend = CAUSAL ? min(S, m0 + BM) : S;
+    const int ntiles = (kend + BN - 1) / BN;
+    issue_tile<DP, BN, NT, SWZ_DUAL>(K, 0, S, D, smem);
+    issue_tile<DP, BN, NT, SWZ_ROW>(Vg, 0, S, D, smem + TILE);
+
+    const bf16* Q = (const bf16*)a.q + (int64_t)(b * a.Hq + h) * S * D;
+    const bf16* G = (const bf16*)a.dO + (int64_t)(b * a.Hq + h) * S * D;
+    bf16x8 qf[NC], gf[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        qf[c] = load_chunk<bf16>(Q + (int64_t)rowc * D, 16 * c + 8 * hh, D, row < S, true);
+        gf[c] = load_chunk<bf16>(G + (int64_t)rowc * D, 16 * c + 8 * hh, D, row < S, true);
+    }
+    const float* blk = a.stats + ((int64_t)(b * a.Hq + h) * a.nqb_total + rowc / 32) * 64;
+    const float lse2 = row < S ? blk[rowc % 32] : INFINITY;
+    const float dlt = row < S ? blk[32 + rowc % 32] : 0.f;
+
+    f32x16 dq[NDT];
+#pragma unroll
+    for (int i = 0; i < NDT; ++i) dq[i] = zero16();
+
+    for (int t = 0; t < ntiles; ++t) {
+        const bf16* Kb = smem + (t & 1) * BUF;
+        const bf16* Vb = Kb + TILE;
+        if (t + 1 < ntiles) {
+            __syncthreads();
+            bf16* nb = smem + ((t + 1) & 1) * BUF;
+            issue_tile<DP, BN, NT, SWZ_DUAL>(K, (t + 1) * BN, S, D, nb);
+            issue_tile<DP, BN, NT, SWZ_ROW>(Vg, (t + 1) * BN, S, D, nb + TILE);
+            wait_vmcnt<LOADS>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        __syncthreads();
+        const int kbase = t * BN;
+        if (wrow0 >= S || (CAUSAL && kbase > wrow0 + 31)) continue;
+
+        const bool need_mask = (CAUSAL && kbase + BN - 1 > wrow0) || (kbase + BN > S);
+#pragma unroll 1
+        for (int kk = 0; kk < NKK; ++kk) {
+            f32x16 s = zero16(), dp = zero16();
+            const int r = 32 * kk + n;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const int col = 16 * c + 8 * hh;
+                s = mfma_bf16(*reinterpret_cast<const bf16x8*>(Kb + tile_off<CPR, SWZ_DUAL>(r, col)), qf[c], s);
+                dp = mfma_bf16(*reinterpret_cast<const bf16x8*>(Vb + tile_off<CPR, SWZ_ROW>(r, col)), gf[c], dp);
+            }
+            // lane column n = query row; register r = key kbase + 32kk + row_of_reg(r, hh)
+            const int lim = need_mask ? (CAUSAL ? min(row, S - 1) : S - 1) - kbase - 32 * kk : 64;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                float p = fast_exp2(s[q] * a.scale_log2 - lse2);
+                p = row_of_reg(q, hh) > lim ? 0.f : p;
+                s[q] = p * (dp[q] - dlt);
+            }
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                bf16x8 db;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) db[j] = (bf16)s[8 * e + j];
+                const int r0 = 32 * kk + 16 * e + 4 * hh + (i16 >> 2), r1 = r0 + 8;
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) {
+                    const int col = 32 * dt + 16 * nh + 4 * (i16 & 3);
+                    const bf16x4 lo = ds_read_tr4(Kb + tile_off<CPR, SWZ_DUAL>(r0, col));
+                    const bf16x4 hi = ds_read_tr4(Kb + tile_off<CPR, SWZ_DUAL>(r1, col));
+                    const bf16x8 ka = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    dq[dt] = mfma_bf16(ka, db, dq[dt]);
+                }
+            }
+        }
+    }
+    if (row >= S) return;
+    float* dqp = a.dq + ((int64_t)(b * a.Hq + h) * S + row) * D;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            store4<float>(dqp, 32 * dt + 8 * g + 4 * hh, D, dq[dt][4 * g] * a.scale, dq[dt][4 * g + 1] * a.scale,
+                          dq[dt][4 * g + 2] * a.scale, dq[dt][4 * g + 3] * a.scale, true);
+}
+
+template <int DP, bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_bwd_main_bf16_fast(BwdArgs a) {
+    __shared__ __attribute__((aligned(1024))) bf16 smem[BwdFastLds<DP>::ELEMS];
+    int t, y, b;
+    if (decode_block(a, (int)blockIdx.x, &t, &y, &b))
+        dkdv_fast_body<DP, CAUSAL>(a, smem, t, y, b);
+    else
+        dq_fast_body<DP, CAUSAL>(a, smem, t, y, b);
+}
+
+
+template <int DP>
+hipError_t launch_bwd_fast(const AttnShape& s, BwdArgs a, int stages, hipStream_t st) {
+    if (stages & BWD_STAGE_DELTA) {
+        constexpr int RPB = 256 / (DP / 8);
+        const int64_t rows = s.B * s.Hq * (int64_t)a.nqb_total * 32;
+        hipLaunchKernelGGL((attn_bwd_stats_kernel<bf16, DP>), dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256), 0,
+                           st, a);
+    }
+    if (stages & BWD_STAGE_MAIN) {
+        const unsigned blocks = (unsigned)(a.n_kv_blocks + a.n_q_blocks);
+        if (s.causal)
+            hipLaunchKernelGGL((attn_bwd_main_bf16_fast<DP, true>), dim3(blocks), dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL((attn_bwd_main_bf16_fast<DP, false>), dim3(blocks), dim3(256), 0, st, a);
+    }
+    if ((stages & BWD_STAGE_REDUCE) && a.splits > 1) {
+        int64_t blocks = (a.part_stride + 255) / 256;
+        if (blocks > 4096) blocks = 4096;
+        hipLaunchKernelGGL(attn_bwd_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
+    }
+    return hipGetLastError();
+}
+
+
+}  // namespace
+}  // namespace bwd
+}  // namespace mft

@@ -25,6 +25,8 @@ typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+// Online softmax: headroom (log2 units) before the running max is moved.
+constexpr float kLazyRescale = 8.0f;
 
 // Element traits: a "vec" is one 16-byte chunk of a row.
 template <typename T> struct Elt;
@@ -177,6 +179,24 @@ template <int CPR> __device__ __forceinline__ int swz_dual(int r) {
 }
 
 enum { SWZ_ROW = 0, SWZ_TR = 1, SWZ_DUAL = 2 };
+
+// Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
+enum { SG_MFMA = 0x008, SG_DS_READ = 0x100 };
+
+// Pin the order of an unrolled "PF operand reads ahead" loop in the current
+// scheduling region: PF LDS reads, then (1 MFMA, R LDS reads) NI-PF times,
+// then the last PF MFMAs.  Without it the machine scheduler moves every
+// read next to its MFMA and the LDS latency is exposed once per MFMA.
+template <int NI, int PF, int R>
+__device__ __forceinline__ void pin_read_ahead() {
+    __builtin_amdgcn_sched_group_barrier(SG_DS_READ, PF * R, 0);
+#pragma unroll
+    for (int i = 0; i < NI - PF; ++i) {
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_DS_READ, R, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(SG_MFMA, PF, 0);
+}
 
 template <int CPR, int SWZ> __device__ __forceinline__ int swz(int r) {
     return SWZ == SWZ_ROW ? swz_row<CPR>(r) : SWZ == SWZ_TR ? swz_tr<CPR>(r) : swz_dual<CPR>(r);

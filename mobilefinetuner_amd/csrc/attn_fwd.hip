@@ -244,6 +244,7 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_fast(FwdArgs a) {
     constexpr int CPR = DP / 8, NC = DP / 16, NDT = DP / 32, NKK = BN / 32;
     constexpr int TILE = BN * DP;                       // elements of one K or V tile
     constexpr int LOADS = 2 * BN * CPR / NT;            // direct loads per thread per tile
+    constexpr int PF = 4;                               // LDS operand prefetch depth
     __shared__ __attribute__((aligned(1024))) bf16 smem[2 * 2 * TILE];
 
     const int tid = threadIdx.x;
@@ -292,37 +293,62 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_fast(FwdArgs a) {
         const int kbase = t * BN;
         if (wrow0 >= S || (CAUSAL && kbase > wrow0 + 31)) continue;
 
+        // S^T = K Q^T: the NKK independent accumulator chains are interleaved
+        // and the K operands stream through a PF-deep register ring, so LDS
+        // latency overlaps the MFMAs instead of stalling each one.
         f32x16 s[NKK];
 #pragma unroll
-        for (int kk = 0; kk < NKK; ++kk) {
-            s[kk] = zero16();
-            const int r = 32 * kk + n;
+        for (int kk = 0; kk < NKK; ++kk) s[kk] = zero16();
+        {
+            constexpr int NI = NKK * NC;
+            auto kread = [&](int it) {
+                return *reinterpret_cast<const bf16x8*>(
+                    Kb + tile_off<CPR, SWZ_ROW>(32 * (it % NKK) + n, 16 * (it / NKK) + 8 * hh));
+            };
+            bf16x8 ring[PF];
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                const bf16x8 ka = *reinterpret_cast<const bf16x8*>(Kb + tile_off<CPR, SWZ_ROW>(r, 16 * c + 8 * hh));
-                s[kk] = mfma_bf16(ka, qf[c], s[kk]);
+            for (int it = 0; it < PF; ++it) ring[it] = kread(it);
+#pragma unroll
+            for (int it = 0; it < NI; ++it) {
+                const bf16x8 ka = ring[it % PF];
+                if (it + PF < NI) ring[it % PF] = kread(it + PF);
+                s[it % NKK] = mfma_bf16(ka, qf[it / NKK], s[it % NKK]);
             }
+            pin_read_ahead<NI, PF, 1>();
         }
 
-        const bool need_mask = (CAUSAL && kbase + BN - 1 > wrow0) || (kbase + BN > S);
+        // Keys past `lim` (causal: this lane's row; always: S-1) are masked,
+        // as selects so the hot loop stays branch-free.
+        if ((CAUSAL && kbase + BN - 1 > wrow0) || (kbase + BN > S)) {
+            const int lim = (CAUSAL ? min(row, S - 1) : S - 1) - kbase;
+#pragma unroll
+            for (int kk = 0; kk < NKK; ++kk)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    s[kk][r] = 32 * kk + row_of_reg(r, hh) > lim ? -INFINITY : s[kk][r];
+        }
         float mx = -INFINITY;
 #pragma unroll
-        for (int kk = 0; kk < NKK; ++kk) {
+        for (int kk = 0; kk < NKK; ++kk)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float x = s[kk][r];
-                if (need_mask) {
-                    const int key = kbase + 32 * kk + row_of_reg(r, hh);
-                    if (key >= S || (CAUSAL && key > row)) x = -INFINITY;
-                }
-                s[kk][r] = x;
-                mx = fmaxf(mx, x);
-            }
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kk][r]);
+        mx = fmaxf(mx, other_half(mx)) * a.scale_log2;
+        // Lazy rescaling: the reference point m_run only moves (and O, l are
+        // rescaled) when some row of the wave sees a max above m_run + 8, so
+        // exp2 arguments stay <= 8 and P <= 256.  Any reference point gives
+        // the same O = acc / l and LSE = m_run + log2(l); this one skips the
+        // per-tile O multiply, which lives in accumulation registers.
+        if (__any(mx > m_run + kLazyRescale)) {
+            const float m_new = fmaxf(m_run, mx);
+            const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.f : m_new));
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+            m_run = m_new;
         }
-        mx = fmaxf(mx, other_half(mx));
-        const float m_new = fmaxf(m_run, mx * a.scale_log2);
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = fast_exp2(m_run - m_use);
+        const float m_use = m_run == -INFINITY ? 0.f : m_run;
         float psum = 0.f;
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk) {
@@ -333,31 +359,36 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_fast(FwdArgs a) {
                 psum += p;
             }
         }
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+        l_run += psum;
 
+        // O^T += V^T P^T, V^T operands through the same kind of register ring.
+        {
+            bf16x8 pb[2 * NKK];
 #pragma unroll
-        for (int kk = 0; kk < NKK; ++kk) {
+            for (int kk = 0; kk < NKK; ++kk)
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                bf16x8 pb;
+                for (int e = 0; e < 2; ++e)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) pb[j] = (bf16)s[kk][8 * e + j];
-                const int r0 = 32 * kk + 16 * e + 4 * hh + (i16 >> 2);
-                const int r1 = r0 + 8;
+                    for (int j = 0; j < 8; ++j) pb[2 * kk + e][j] = (bf16)s[kk][8 * e + j];
+            constexpr int NI = 2 * NKK * NDT;  // iteration = (kk, e) block x dt
+            auto vread = [&](int it) {
+                const int ke = it / NDT, dt = it % NDT;
+                const int r0 = 16 * ke + 4 * hh + (i16 >> 2);
+                const int col = 32 * dt + 16 * nh + 4 * (i16 & 3);
+                const bf16x4 lo = ds_read_tr4(Vb + tile_off<CPR, SWZ_TR>(r0, col));
+                const bf16x4 hi = ds_read_tr4(Vb + tile_off<CPR, SWZ_TR>(r0 + 8, col));
+                return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            };
+            bf16x8 ring[PF];
 #pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) {
-                    const int col = 32 * dt + 16 * nh + 4 * (i16 & 3);
-                    const bf16x4 lo = ds_read_tr4(Vb + tile_off<CPR, SWZ_TR>(r0, col));
-                    const bf16x4 hi = ds_read_tr4(Vb + tile_off<CPR, SWZ_TR>(r1, col));
-                    const bf16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    oacc[dt] = mfma_bf16(va, pb, oacc[dt]);
-                }
+            for (int it = 0; it < PF; ++it) ring[it] = vread(it);
+#pragma unroll
+            for (int it = 0; it < NI; ++it) {
+                const bf16x8 va = ring[it % PF];
+                if (it + PF < NI) ring[it % PF] = vread(it + PF);
+                oacc[it % NDT] = mfma_bf16(va, pb[it / NDT], oacc[it % NDT]);
             }
+            pin_read_ahead<NI, PF, 2>();
         }
     }
 
