@@ -53,10 +53,10 @@ __global__ __launch_bounds__(256) void attn_bwd_stats_kernel(BwdArgs a) {
 }
 
 template <int DP> struct BwdFastLds {
-    // V_LDS: the dK/dV role reads V of its 128 keys from LDS (B operand of
-    // dP) instead of keeping it in registers; a register-pressure fallback,
-    // off while K, V, dK and dV fit in the 512 VGPRs of a wave.
-    static constexpr bool V_LDS = false;
+    // V_LDS: at D = 256 the dK/dV role reads V of its 128 keys from LDS (B
+    // operand of dP) instead of registers: K, dK and dV already take 320 of
+    // a wave's 512 registers and the LDS operand pipeline needs the rest.
+    static constexpr bool V_LDS = DP >= 256;
     static constexpr int KV_BUF = 2 * 32 * DP + 4 * 512;  // Q, dO tiles + 4 waves x 1 KiB stats (elements)
     static constexpr int KV_ELEMS = 2 * KV_BUF + (V_LDS ? 128 * DP : 0);
     static constexpr int Q_BUF = 2 * 64 * DP;             // K, V tiles
@@ -71,6 +71,7 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
     constexpr int BUF = BwdFastLds<DP>::KV_BUF;
     constexpr int LOADS = 2 * (32 * CPR / NT) + 1;
     constexpr bool V_LDS = BwdFastLds<DP>::V_LDS;
+    constexpr int PF = 4;  // LDS operand prefetch depth
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
     const int i16 = lane & 15, nh = (lane >> 4) & 1;
@@ -98,7 +99,22 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
         load_lds_16(st + 4 * i16, buf + 2 * QT + w * 512);
     };
     bf16* Vl = smem + 2 * BUF;  // V rows of this workgroup's keys (V_LDS only)
-    if constexpr (V_LDS) issue_tile<DP, BNK, NT, SWZ_ROW>(Vg, j0, S, D, Vl);
+    if constexpr (V_LDS) {
+        issue_tile<DP, BNK, NT, SWZ_ROW>(Vg, j0, S, D, Vl);
+        if (D < DP) {
+            // Staged columns >= D hold copies of column chunk 0, and so do
+            // those of the dO tiles: zero them here so that dP = dO V^T sums
+            // only the D real columns.
+            wait_vmcnt<0>();
+            __syncthreads();
+            const bf16x8 z = zero_vec<bf16x8>();
+            for (int idx = tid; idx < BNK * CPR; idx += NT) {
+                const int r = idx / CPR, c = idx % CPR;
+                if (8 * c >= D) *reinterpret_cast<bf16x8*>(Vl + r * DP + ((c ^ swz_row<CPR>(r)) << 3)) = z;
+            }
+            __syncthreads();
+        }
+    }
     if (niter > 0) issue(0, smem);
 
     bf16x8 kf[NC], vf[V_LDS ? 1 : NC];
@@ -130,17 +146,35 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
         if (wkey0 >= S) continue;
         if (CAUSAL && qb + 31 < wkey0) continue;
 
+        // S = Q K^T and dP = dO V^T, one chunk of both per step; the steps'
+        // LDS operands (Q, dO and, with V_LDS, V) are read PF steps ahead.
         f32x16 s = zero16(), dp = zero16();
+        {
+            constexpr int R = V_LDS ? 3 : 2;
+            struct Ops { bf16x8 q, g, v; };
+            auto sread = [&](int c) {
+                const int col = 16 * c + 8 * hh;
+                Ops o;
+                o.q = *reinterpret_cast<const bf16x8*>(Qb + tile_off<CPR, SWZ_DUAL>(n, col));
+                o.g = *reinterpret_cast<const bf16x8*>(Gb + tile_off<CPR, SWZ_DUAL>(n, col));
+                if constexpr (V_LDS)
+                    o.v = *reinterpret_cast<const bf16x8*>(Vl + tile_off<CPR, SWZ_ROW>(32 * w + n, col));
+                return o;
+            };
+            Ops ring[PF];
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const int col = 16 * c + 8 * hh;
-            s = mfma_bf16(*reinterpret_cast<const bf16x8*>(Qb + tile_off<CPR, SWZ_DUAL>(n, col)), kf[c], s);
-            bf16x8 vb;
-            if constexpr (V_LDS)
-                vb = *reinterpret_cast<const bf16x8*>(Vl + tile_off<CPR, SWZ_ROW>(32 * w + n, col));
-            else
-                vb = vf[c];
-            dp = mfma_bf16(*reinterpret_cast<const bf16x8*>(Gb + tile_off<CPR, SWZ_DUAL>(n, col)), vb, dp);
+            for (int c = 0; c < PF; ++c) ring[c] = sread(c);
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const Ops o = ring[c % PF];
+                if (c + PF < NC) ring[c % PF] = sread(c + PF);
+                s = mfma_bf16(o.q, kf[c], s);
+                if constexpr (V_LDS)
+                    dp = mfma_bf16(o.g, o.v, dp);
+                else
+                    dp = mfma_bf16(o.g, vf[c], dp);
+            }
+            pin_read_ahead<NC, PF, R, 2>();
         }
         // lane column n = key; register r = query qb + row_of_reg(r, hh)
         const bool need_mask = CAUSAL && qb < wkey0 + 31;
@@ -165,19 +199,30 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
                 pb[j] = (bf16)s[8 * e + j];
                 db[j] = (bf16)dp[8 * e + j];
             }
-            const int r0 = 16 * e + 4 * hh + (i16 >> 2), r1 = r0 + 8;
+            // dV^T += dO^T P (even steps) and dK^T += Q^T dS (odd steps); the
+            // transposed A operands come two ds_read_b64_tr_b16 per step.
+            const int r0 = 16 * e + 4 * hh + (i16 >> 2);
+            constexpr int NI = 2 * NDT;
+            auto tread = [&](int it) {
+                const bf16* t = (it & 1) ? Qb : Gb;
+                const int col = 32 * (it >> 1) + 16 * nh + 4 * (i16 & 3);
+                const bf16x4 lo = ds_read_tr4(t + tile_off<CPR, SWZ_DUAL>(r0, col));
+                const bf16x4 hi = ds_read_tr4(t + tile_off<CPR, SWZ_DUAL>(r0 + 8, col));
+                return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            };
+            bf16x8 ring[PF];
 #pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) {
-                const int col = 32 * dt + 16 * nh + 4 * (i16 & 3);
-                const bf16x4 glo = ds_read_tr4(Gb + tile_off<CPR, SWZ_DUAL>(r0, col));
-                const bf16x4 ghi = ds_read_tr4(Gb + tile_off<CPR, SWZ_DUAL>(r1, col));
-                const bf16x8 ga = {glo[0], glo[1], glo[2], glo[3], ghi[0], ghi[1], ghi[2], ghi[3]};
-                dv[dt] = mfma_bf16(ga, pb, dv[dt]);
-                const bf16x4 qlo = ds_read_tr4(Qb + tile_off<CPR, SWZ_DUAL>(r0, col));
-                const bf16x4 qhi = ds_read_tr4(Qb + tile_off<CPR, SWZ_DUAL>(r1, col));
-                const bf16x8 qa = {qlo[0], qlo[1], qlo[2], qlo[3], qhi[0], qhi[1], qhi[2], qhi[3]};
-                dk[dt] = mfma_bf16(qa, db, dk[dt]);
+            for (int it = 0; it < PF; ++it) ring[it] = tread(it);
+#pragma unroll
+            for (int it = 0; it < NI; ++it) {
+                const bf16x8 av = ring[it % PF];
+                if (it + PF < NI) ring[it % PF] = tread(it + PF);
+                if (it & 1)
+                    dk[it >> 1] = mfma_bf16(av, db, dk[it >> 1]);
+                else
+                    dv[it >> 1] = mfma_bf16(av, pb, dv[it >> 1]);
             }
+            pin_read_ahead<NI, PF, 2>();
         }
     }
     if (key >= S) return;
@@ -192,6 +237,7 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int q
     constexpr int TILE = BN * DP;
     constexpr int BUF = BwdFastLds<DP>::Q_BUF;
     constexpr int LOADS = 2 * (BN * CPR / NT);
+    constexpr int PF = 4;  // LDS operand prefetch depth
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
     const int i16 = lane & 15, nh = (lane >> 4) & 1;
@@ -244,11 +290,27 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int q
         for (int kk = 0; kk < NKK; ++kk) {
             f32x16 s = zero16(), dp = zero16();
             const int r = 32 * kk + n;
+            {
+                // S^T = K Q^T (even steps), dP^T = V dO^T (odd steps)
+                constexpr int NI = 2 * NC;
+                auto aread = [&](int it) {
+                    const int col = 16 * (it >> 1) + 8 * hh;
+                    return (it & 1) ? *reinterpret_cast<const bf16x8*>(Vb + tile_off<CPR, SWZ_ROW>(r, col))
+                                    : *reinterpret_cast<const bf16x8*>(Kb + tile_off<CPR, SWZ_DUAL>(r, col));
+                };
+                bf16x8 ring[PF];
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                const int col = 16 * c + 8 * hh;
-                s = mfma_bf16(*reinterpret_cast<const bf16x8*>(Kb + tile_off<CPR, SWZ_DUAL>(r, col)), qf[c], s);
-                dp = mfma_bf16(*reinterpret_cast<const bf16x8*>(Vb + tile_off<CPR, SWZ_ROW>(r, col)), gf[c], dp);
+                for (int it = 0; it < PF; ++it) ring[it] = aread(it);
+#pragma unroll
+                for (int it = 0; it < NI; ++it) {
+                    const bf16x8 av = ring[it % PF];
+                    if (it + PF < NI) ring[it % PF] = aread(it + PF);
+                    if (it & 1)
+                        dp = mfma_bf16(av, gf[it >> 1], dp);
+                    else
+                        s = mfma_bf16(av, qf[it >> 1], s);
+                }
+                pin_read_ahead<NI, PF, 1>();
             }
             // lane column n = query row; register r = key kbase + 32kk + row_of_reg(r, hh)
             const int lim = need_mask ? (CAUSAL ? min(row, S - 1) : S - 1) - kbase - 32 * kk : 64;
@@ -258,20 +320,31 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int q
                 p = row_of_reg(q, hh) > lim ? 0.f : p;
                 s[q] = p * (dp[q] - dlt);
             }
+            {
+                // dQ^T += K^T dS^T over the two 16-key halves (e) of this block
+                bf16x8 db[2];
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                bf16x8 db;
+                for (int e = 0; e < 2; ++e)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) db[j] = (bf16)s[8 * e + j];
-                const int r0 = 32 * kk + 16 * e + 4 * hh + (i16 >> 2), r1 = r0 + 8;
-#pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) {
-                    const int col = 32 * dt + 16 * nh + 4 * (i16 & 3);
+                    for (int j = 0; j < 8; ++j) db[e][j] = (bf16)s[8 * e + j];
+                constexpr int NI = 2 * NDT;
+                auto tread = [&](int it) {
+                    const int r0 = 32 * kk + 16 * (it / NDT) + 4 * hh + (i16 >> 2);
+                    const int col = 32 * (it % NDT) + 16 * nh + 4 * (i16 & 3);
                     const bf16x4 lo = ds_read_tr4(Kb + tile_off<CPR, SWZ_DUAL>(r0, col));
-                    const bf16x4 hi = ds_read_tr4(Kb + tile_off<CPR, SWZ_DUAL>(r1, col));
-                    const bf16x8 ka = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    dq[dt] = mfma_bf16(ka, db, dq[dt]);
+                    const bf16x4 hi = ds_read_tr4(Kb + tile_off<CPR, SWZ_DUAL>(r0 + 8, col));
+                    return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                };
+                bf16x8 ring[PF];
+#pragma unroll
+                for (int it = 0; it < PF; ++it) ring[it] = tread(it);
+#pragma unroll
+                for (int it = 0; it < NI; ++it) {
+                    const bf16x8 av = ring[it % PF];
+                    if (it + PF < NI) ring[it % PF] = tread(it + PF);
+                    dq[it % NDT] = mfma_bf16(av, db[it / NDT], dq[it % NDT]);
                 }
+                pin_read_ahead<NI, PF, 2>();
             }
         }
     }

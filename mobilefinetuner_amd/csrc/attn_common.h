@@ -183,19 +183,20 @@ enum { SWZ_ROW = 0, SWZ_TR = 1, SWZ_DUAL = 2 };
 // Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
 enum { SG_MFMA = 0x008, SG_DS_READ = 0x100 };
 
-// Pin the order of an unrolled "PF operand reads ahead" loop in the current
-// scheduling region: PF LDS reads, then (1 MFMA, R LDS reads) NI-PF times,
-// then the last PF MFMAs.  Without it the machine scheduler moves every
-// read next to its MFMA and the LDS latency is exposed once per MFMA.
-template <int NI, int PF, int R>
+// Pin the order of an unrolled "operands read PF steps ahead" loop in the
+// current scheduling region.  A step reads R LDS operands and issues M
+// MFMAs: PF steps of reads, then (M MFMAs, R reads) NI-PF times, then the
+// last PF steps of MFMAs.  Without it the machine scheduler moves every read
+// next to its MFMA and the LDS latency is exposed once per MFMA.
+template <int NI, int PF, int R, int M = 1>
 __device__ __forceinline__ void pin_read_ahead() {
     __builtin_amdgcn_sched_group_barrier(SG_DS_READ, PF * R, 0);
 #pragma unroll
     for (int i = 0; i < NI - PF; ++i) {
-        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, M, 0);
         __builtin_amdgcn_sched_group_barrier(SG_DS_READ, R, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(SG_MFMA, PF, 0);
+    __builtin_amdgcn_sched_group_barrier(SG_MFMA, PF * M, 0);
 }
 
 template <int CPR, int SWZ> __device__ __forceinline__ int swz(int r) {
