@@ -135,13 +135,12 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
         const bf16* Gb = Qb + QT;
         const float* stt = reinterpret_cast<const float*>(Qb + 2 * QT + w * 512);
         if (it + 1 < niter) {
-            __syncthreads();
+            lds_barrier();
             issue(it + 1, smem + ((it + 1) & 1) * BUF);
-            wait_vmcnt<LOADS>();
+            lds_barrier_vm<LOADS>();
         } else {
-            wait_vmcnt<0>();
+            lds_barrier_vm<0>();
         }
-        __syncthreads();
         const int qb = qstart + (it % nqb) * 32;
         if (wkey0 >= S) continue;
         if (CAUSAL && qb + 31 < wkey0) continue;
@@ -273,15 +272,14 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int q
         const bf16* Kb = smem + (t & 1) * BUF;
         const bf16* Vb = Kb + TILE;
         if (t + 1 < ntiles) {
-            __syncthreads();
+            lds_barrier();
             bf16* nb = smem + ((t + 1) & 1) * BUF;
             issue_tile<DP, BN, NT, SWZ_DUAL>(K, (t + 1) * BN, S, D, nb);
             issue_tile<DP, BN, NT, SWZ_ROW>(Vg, (t + 1) * BN, S, D, nb + TILE);
-            wait_vmcnt<LOADS>();
+            lds_barrier_vm<LOADS>();
         } else {
-            wait_vmcnt<0>();
+            lds_barrier_vm<0>();
         }
-        __syncthreads();
         const int kbase = t * BN;
         if (wrow0 >= S || (CAUSAL && kbase > wrow0 + 31)) continue;
 

@@ -149,6 +149,22 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// Workgroup barriers for the direct-to-LDS pipelines.  __syncthreads()
+// carries a release fence, which makes every wave wait for ALL its
+// outstanding loads (vmcnt(0)) - including the prefetch of the next tile -
+// before the barrier, serialising the double buffer.  These barriers wait
+// only for this wave's LDS operations and, with VM = N, for all but its N
+// most recent global loads (loads return in order), then s_barrier.  The
+// "memory" clobber keeps the compiler from moving memory operations across.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+template <int VM>
+__device__ __forceinline__ void lds_barrier_vm() {
+    static_assert(VM >= 0 && VM < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(VM) : "memory");
+}
+
 // ds_read_b64_tr_b16 (measured on gfx950): within each aligned group of 16
 // lanes, reader lane j supplies an 8-byte row M[j][0..3]; output lane i gets
 // { M[i/4][i%4], M[4+i/4][i%4], M[8+i/4][i%4], M[12+i/4][i%4] }.  So if lane j

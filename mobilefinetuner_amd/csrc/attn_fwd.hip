@@ -281,15 +281,14 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_fast(FwdArgs a) {
         const bf16* Kb = smem + (t & 1) * 2 * TILE;
         const bf16* Vb = Kb + TILE;
         if (t + 1 < ntiles) {
-            __syncthreads();  // every wave is done with the buffer tile t+1 reuses
+            lds_barrier();  // every wave is done with the buffer tile t+1 reuses
             bf16* nb = smem + ((t + 1) & 1) * 2 * TILE;
             issue_tile<DP, BN, NT, SWZ_ROW>(K, (t + 1) * BN, S, D, nb);
             issue_tile<DP, BN, NT, SWZ_TR>(Vg, (t + 1) * BN, S, D, nb + TILE);
-            wait_vmcnt<LOADS>();  // this thread's loads of tile t have landed
+            lds_barrier_vm<LOADS>();  // tile t has landed (all waves), tile t+1 in flight
         } else {
-            wait_vmcnt<0>();
+            lds_barrier_vm<0>();
         }
-        __syncthreads();  // ... and everyone else's
         const int kbase = t * BN;
         if (wrow0 >= S || (CAUSAL && kbase > wrow0 + 31)) continue;
 
