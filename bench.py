@@ -91,9 +91,9 @@ def gpu_leg(cfg_id, steps, warmup):
     def bwd():
         capi.attn_bwd(d, P[0], P[1], P[2], P[3], P[4], P[5], P[6], P[7], P[8], P[9], sp)
 
-    def bwd_main():
-        capi.attn_bwd_stage(d, capi.MFT_BWD_MAIN, P[0], P[1], P[2], P[3], P[4], P[5], P[6], P[7], P[8],
-                            P[9], sp)
+    def stage(mask):
+        return lambda: capi.attn_bwd_stage(d, mask, P[0], P[1], P[2], P[3], P[4], P[5], P[6], P[7], P[8],
+                                           P[9], sp)
 
     def timed(fn, n):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -113,10 +113,11 @@ def gpu_leg(cfg_id, steps, warmup):
     n_phase = max(steps, 10)
     fwd_ms = timed(fwd, n_phase)
     bwd_ms = timed(bwd, n_phase)
-    capi.attn_bwd_stage(d, capi.MFT_BWD_DELTA, *P[:9], P[9], sp)  # delta for the main stage
-    main_ms = timed(bwd_main, n_phase)
+    stage(capi.MFT_BWD_DELTA)()  # row terms for the gradient stages
+    dkdv_ms = timed(stage(capi.MFT_BWD_DKDV), n_phase)
+    dq_ms = timed(stage(capi.MFT_BWD_DQ), n_phase)
     units = flop_units(c)
-    return dict(step_ms=step_ms, fwd_ms=fwd_ms, bwd_ms=bwd_ms, bwd_main_ms=main_ms, units=units)
+    return dict(step_ms=step_ms, fwd_ms=fwd_ms, bwd_ms=bwd_ms, dkdv_ms=dkdv_ms, dq_ms=dq_ms, units=units)
 
 
 def cpu_leg(cfg_id):
@@ -166,14 +167,15 @@ def main():
     units = r["units"]
     peak = PEAK_TFLOPS[c["dtype"]]
     tflops = 7 * units / (r["step_ms"] * 1e-3) / 1e12
+    # Dominant kernel: the longest of the forward, dK/dV and dQ launches;
+    # achieved = its algorithmic flops / its measured launch time.  Algorithmic
+    # work per launch in causal contraction units (D*S*(S+1) per query head):
+    # forward 2 (QK^T, PV); dK/dV 4 (QK^T recompute, dO V^T, P^T dO, dS^T Q);
+    # dQ 1 (dS K) - its QK^T and dO V^T recomputes are not counted.
+    kern = {"attn_fwd": (r["fwd_ms"], 2), "attn_bwd_dkdv": (r["dkdv_ms"], 4), "attn_bwd_dq": (r["dq_ms"], 1)}
+    dom = max(kern, key=lambda k: kern[k][0])
+    ach = kern[dom][1] * units / (kern[dom][0] * 1e-3) / 1e12
     fwd_tf = 2 * units / (r["fwd_ms"] * 1e-3) / 1e12
-    main_tf = 5 * units / (r["bwd_main_ms"] * 1e-3) / 1e12
-    # Dominant kernel: the longer of the forward kernel and the backward main
-    # kernel; achieved = its algorithmic flops / its measured launch time.
-    if r["bwd_main_ms"] >= r["fwd_ms"]:
-        dom, ach = "attn_bwd_main (dK/dV + dQ)", main_tf
-    else:
-        dom, ach = "attn_fwd", fwd_tf
     new_b, ref_b = saved_bytes(c)
     out = {
         "metric": METRIC,
@@ -194,6 +196,8 @@ def main():
         "tokens_per_s": round(c["B"] * c["S"] / (r["step_ms"] * 1e-3), 1),
         "fwd_ms": round(r["fwd_ms"], 5),
         "bwd_ms": round(r["bwd_ms"], 5),
+        "dkdv_ms": round(r["dkdv_ms"], 5),
+        "dq_ms": round(r["dq_ms"], 5),
         "fwd_tflops": round(fwd_tf, 2),
         "bwd_tflops": round(5 * units / (r["bwd_ms"] * 1e-3) / 1e12, 2),
         "saved_bytes": {"new": new_b, "reference": ref_b, "ratio": round(ref_b / new_b, 1)},

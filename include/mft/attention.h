@@ -93,13 +93,22 @@ mft_status mft_attn_bwd(const mft_attn_desc* desc, const void* q, const void* k,
                         hipStream_t stream);
 
 /* The backward's stages, as a bit mask for mft_attn_bwd_stage.
- *   DELTA : delta_i = dO_i . O_i into the workspace           (one launch)
- *   MAIN  : dK/dV and dQ; bf16 runs both in one launch        (fp32: two)
- *   REDUCE: sums the dK/dV partials of split head groups      (0 or 1 launch)
- * mft_attn_bwd == mft_attn_bwd_stage(MFT_BWD_ALL).  Callers may run the
- * stages separately, in this order, on one stream (e.g. to time them or to
- * start DELTA early); MAIN reads what DELTA wrote into the same workspace. */
-enum { MFT_BWD_DELTA = 1, MFT_BWD_MAIN = 2, MFT_BWD_REDUCE = 4, MFT_BWD_ALL = 7 };
+ *   DELTA : per-row softmax terms (delta_i = dO_i . O_i) into the workspace
+ *   DKDV  : dK and dV (one launch)
+ *   DQ    : dQ (one launch)
+ *   REDUCE: sums the fp32 partials of tiles split across work units
+ * MAIN = DKDV | DQ.  mft_attn_bwd == mft_attn_bwd_stage(MFT_BWD_ALL).
+ * Callers may run the stages separately on one stream, DELTA first and REDUCE
+ * last (e.g. to time them, or to start DELTA early); later stages read what
+ * earlier ones wrote into the same workspace. */
+enum {
+    MFT_BWD_DELTA = 1,
+    MFT_BWD_DKDV = 2,
+    MFT_BWD_REDUCE = 4,
+    MFT_BWD_DQ = 8,
+    MFT_BWD_MAIN = 10,
+    MFT_BWD_ALL = 15
+};
 
 /* Backward, selected stages only (same arguments as mft_attn_bwd).
  * Replaces: the same Engine backward as mft_attn_bwd, split into launches. */

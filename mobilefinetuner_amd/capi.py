@@ -14,7 +14,8 @@ LIB_PATH = os.path.join(_PKG, "lib", "libmft_attn.so")
 
 MFT_OK, MFT_ERR_INVALID_ARG, MFT_ERR_UNSUPPORTED, MFT_ERR_HIP = 0, 1, 2, 3
 MFT_F32, MFT_BF16 = 0, 2
-MFT_BWD_DELTA, MFT_BWD_MAIN, MFT_BWD_REDUCE, MFT_BWD_ALL = 1, 2, 4, 7
+MFT_BWD_DELTA, MFT_BWD_DKDV, MFT_BWD_REDUCE, MFT_BWD_DQ = 1, 2, 4, 8
+MFT_BWD_MAIN, MFT_BWD_ALL = 10, 15
 
 # Every symbol the header declares (checked by tests/test_capi.py).
 EXPORTS = (

@@ -34,6 +34,9 @@
 // LDS.  fp32 inputs use v_mfma_f32_32x32x2_f32 and need no transposes.
 #include "attn_bwd_common.h"
 
+#include <algorithm>
+#include <atomic>
+
 namespace mft {
 namespace {
 using namespace bwd;
@@ -458,18 +461,23 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int qt, in
                           dq[dt][4 * g + 3] * a.scale, v4);
 }
 
-template <int A, int B> struct Max { static constexpr int value = A > B ? A : B; };
-
-// bf16: both roles in one launch (4 waves each).
+// bf16 (head dims the fast path does not take): one launch per role.
 template <int DP, bool CAUSAL>
-__global__ __launch_bounds__(256) void attn_bwd_main_bf16(BwdArgs a) {
-    constexpr int BYTES = Max<DkdvBf16Lds<DP>::BYTES, DqLds<bf16, DP, 64>::BYTES>::value;
-    __shared__ __attribute__((aligned(16))) char smem[BYTES];
-    int t, y, b;
-    if (decode_block(a, (int)blockIdx.x, &t, &y, &b))
-        dkdv_bf16_body<DP, 4, CAUSAL>(a, smem, t, y, b);
-    else
-        dq_body<bf16, DP, 4, 64, CAUSAL>(a, smem, t, y, b);
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_bf16(BwdArgs a) {
+    __shared__ __attribute__((aligned(16))) char smem[DkdvBf16Lds<DP>::BYTES];
+    const int i = blockIdx.x;
+    const int yb = a.Hkv * a.splits * a.B;
+    const int t = i / yb, rest = i - t * yb;
+    dkdv_bf16_body<DP, 4, CAUSAL>(a, smem, t, rest % (a.Hkv * a.splits), rest / (a.Hkv * a.splits));
+}
+
+template <int DP, bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_bwd_dq_bf16(BwdArgs a) {
+    __shared__ __attribute__((aligned(16))) char smem[DqLds<bf16, DP, 64>::BYTES];
+    const int i = blockIdx.x;
+    const int yb = a.Hq * a.B;
+    const int ti = i / yb, rest = i - ti * yb;
+    dq_body<bf16, DP, 4, 64, CAUSAL>(a, smem, a.n_qtiles - 1 - ti, rest % a.Hq, rest / a.Hq);
 }
 
 // fp32: the roles use different block sizes, so they are two launches.
@@ -504,21 +512,24 @@ hipError_t launch_bwd_t(const AttnShape& s, BwdArgs a, int stages, hipStream_t s
         const int64_t blocks = (a.total_rows + RPB - 1) / RPB;
         hipLaunchKernelGGL((attn_bwd_delta_kernel<T, DP>), dim3((unsigned)blocks), dim3(256), 0, st, a);
     }
-    if (stages & BWD_STAGE_MAIN) {
+    if (stages & (BWD_STAGE_DKDV | BWD_STAGE_DQ)) {
+        constexpr int NW = BF ? 4 : f32_dkdv_warps(DP), BN = BF ? 64 : f32_dq_bn(DP);
+        const bool kv = stages & BWD_STAGE_DKDV, q = stages & BWD_STAGE_DQ;
         if constexpr (BF) {
-            const unsigned blocks = (unsigned)(a.n_kv_blocks + a.n_q_blocks);
-            if (s.causal)
-                hipLaunchKernelGGL((attn_bwd_main_bf16<DP, true>), dim3(blocks), dim3(256), 0, st, a);
-            else
-                hipLaunchKernelGGL((attn_bwd_main_bf16<DP, false>), dim3(blocks), dim3(256), 0, st, a);
-        } else {
-            constexpr int NW = f32_dkdv_warps(DP), BN = f32_dq_bn(DP);
             if (s.causal) {
-                hipLaunchKernelGGL((attn_bwd_dkdv_f32<DP, NW, true>), dim3(a.n_kv_blocks), dim3(NW * 64), 0, st, a);
-                hipLaunchKernelGGL((attn_bwd_dq_f32<DP, BN, true>), dim3(a.n_q_blocks), dim3(256), 0, st, a);
+                if (kv) hipLaunchKernelGGL((attn_bwd_dkdv_bf16<DP, true>), dim3(a.n_kv_blocks), dim3(256), 0, st, a);
+                if (q) hipLaunchKernelGGL((attn_bwd_dq_bf16<DP, true>), dim3(a.n_q_blocks), dim3(256), 0, st, a);
             } else {
-                hipLaunchKernelGGL((attn_bwd_dkdv_f32<DP, NW, false>), dim3(a.n_kv_blocks), dim3(NW * 64), 0, st, a);
-                hipLaunchKernelGGL((attn_bwd_dq_f32<DP, BN, false>), dim3(a.n_q_blocks), dim3(256), 0, st, a);
+                if (kv) hipLaunchKernelGGL((attn_bwd_dkdv_bf16<DP, false>), dim3(a.n_kv_blocks), dim3(256), 0, st, a);
+                if (q) hipLaunchKernelGGL((attn_bwd_dq_bf16<DP, false>), dim3(a.n_q_blocks), dim3(256), 0, st, a);
+            }
+        } else {
+            if (s.causal) {
+                if (kv) hipLaunchKernelGGL((attn_bwd_dkdv_f32<DP, NW, true>), dim3(a.n_kv_blocks), dim3(NW * 64), 0, st, a);
+                if (q) hipLaunchKernelGGL((attn_bwd_dq_f32<DP, BN, true>), dim3(a.n_q_blocks), dim3(256), 0, st, a);
+            } else {
+                if (kv) hipLaunchKernelGGL((attn_bwd_dkdv_f32<DP, NW, false>), dim3(a.n_kv_blocks), dim3(NW * 64), 0, st, a);
+                if (q) hipLaunchKernelGGL((attn_bwd_dq_f32<DP, BN, false>), dim3(a.n_q_blocks), dim3(256), 0, st, a);
             }
         }
     }
@@ -549,6 +560,69 @@ int padded_d(int64_t D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 
 
 bool bwd_fast_path(const AttnShape& s) { return s.bf16 && s.D % 8 == 0 && s.D > 32; }
 
+namespace {
+// Compute units of the current device (256 on MI355X), cached per device.
+int device_cus() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
+}  // namespace
+
+BwdPlan plan_bwd_fast(const AttnShape& s) {
+    const int S = (int)s.S, causal = s.causal ? 1 : 0, group = (int)(s.Hq / s.Hkv);
+    const int nt = (S + 127) / 128;
+    const int64_t n_kv = bwd::fast_kv_start(S, causal, group, nt);  // iterations per (batch, kv head)
+    const int64_t n_q = bwd::fast_q_start(S, causal, nt);           // iterations per (batch, query head)
+    const int64_t pairs_kv = s.B * s.Hkv, pairs_q = s.B * s.Hq;
+    // The two roles run as separate launches: each is cut into about one
+    // unit per CU (units no shorter than 8 iterations).
+    const int cus = device_cus();
+    const int64_t u_kv = std::max<int64_t>(1, (cus + pairs_kv - 1) / pairs_kv);
+    const int64_t u_q = std::max<int64_t>(1, (cus + pairs_q - 1) / pairs_q);
+    BwdPlan p;
+    p.kv_chunk = (int)std::min<int64_t>(n_kv, std::max<int64_t>(8, (n_kv + u_kv - 1) / u_kv));
+    p.q_chunk = (int)std::min<int64_t>(n_q, std::max<int64_t>(8, (n_q + u_q - 1) / u_q));
+    p.kv_units = (int)((n_kv + p.kv_chunk - 1) / p.kv_chunk);
+    p.q_units = (int)((n_q + p.q_chunk - 1) / p.q_chunk);
+    p.kv_parts_max = p.q_parts_max = 1;
+    for (int t = 0; t < nt; ++t) {
+        p.kv_parts_max = std::max(p.kv_parts_max,
+                                  bwd::fast_slots(bwd::fast_kv_start(S, causal, group, t),
+                                                  bwd::fast_kv_n(S, causal, group, t), p.kv_chunk));
+        p.q_parts_max = std::max(p.q_parts_max, bwd::fast_slots(bwd::fast_q_start(S, causal, t),
+                                                                bwd::fast_q_n(S, causal, t), p.q_chunk));
+    }
+    return p;
+}
+
+BwdLayout bwd_layout(const AttnShape& s) {
+    auto up = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
+    const size_t rows = static_cast<size_t>(s.B * s.Hq);
+    const size_t stat_floats = rows * static_cast<size_t>((s.S + 31) / 32) * 64;
+    const size_t delta_floats = rows * static_cast<size_t>(s.S);
+    const size_t kv_elems = static_cast<size_t>(s.B * s.Hkv * s.S * s.D);
+    const size_t q_elems = static_cast<size_t>(s.B * s.Hq * s.S * s.D);
+    BwdLayout l;
+    l.stats = up(sizeof(float) * std::max(stat_floats, delta_floats));
+    if (bwd_fast_path(s)) {
+        const BwdPlan p = plan_bwd_fast(s);
+        l.kv_part = p.kv_parts_max > 1 ? up(sizeof(float) * 2 * p.kv_parts_max * kv_elems) : 0;
+        l.q_part = p.q_parts_max > 1 ? up(sizeof(float) * p.q_parts_max * q_elems) : 0;
+    } else {
+        const int splits = dkdv_splits(s);
+        l.kv_part = splits > 1 ? up(sizeof(float) * 2 * splits * kv_elems) : 0;
+        l.q_part = 0;
+    }
+    l.total = l.stats + l.kv_part + l.q_part;
+    return l;
+}
+
 int dkdv_keys_per_block(const AttnShape& s) {
     if (s.bf16) return 128;
     return 32 * (padded_d(s.D) >= 256 ? 1 : padded_d(s.D) >= 128 ? 2 : 4);
@@ -573,7 +647,11 @@ int dkdv_splits(const AttnShape& s) {
 
 hipError_t launch_attn_bwd(const AttnShape& s, const void* q, const void* k, const void* v,
                            const void* o, const void* dO, const float* lse, float* dq, float* dk,
-                           float* dv, float* delta, float* part, int stages, hipStream_t st) {
+                           float* dv, void* workspace, int stages, hipStream_t st) {
+    const BwdLayout lay = bwd_layout(s);
+    char* ws = static_cast<char*>(workspace);
+    float* delta = reinterpret_cast<float*>(ws);
+    float* part = lay.kv_part ? reinterpret_cast<float*>(ws + lay.stats) : nullptr;
     BwdArgs a;
     a.q = q;
     a.k = k;
@@ -607,6 +685,19 @@ hipError_t launch_attn_bwd(const AttnShape& s, const void* q, const void* k, con
     a.scale_log2 = s.scale * kLog2e;
     a.vec_ok = (s.D % (s.bf16 ? 8 : 4)) == 0;
     a.vec4_ok = (s.D % 4) == 0;
+    a.causal = s.causal ? 1 : 0;
+    a.kv_part = part;
+    a.q_part = lay.q_part ? reinterpret_cast<float*>(ws + lay.stats + lay.kv_part) : nullptr;
+    a.q_part_stride = s.B * s.Hq * s.S * s.D;
+    if (bwd_fast_path(s)) {
+        const BwdPlan p = plan_bwd_fast(s);
+        a.kv_chunk = p.kv_chunk;
+        a.q_chunk = p.q_chunk;
+        a.kv_units = p.kv_units;
+        a.q_units = p.q_units;
+    } else {
+        a.kv_chunk = a.q_chunk = a.kv_units = a.q_units = 0;
+    }
     return s.bf16 ? launch_bwd_dispatch<bf16>(s, a, stages, st) : launch_bwd_dispatch<float>(s, a, stages, st);
 }
 

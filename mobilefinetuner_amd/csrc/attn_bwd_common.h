@@ -29,7 +29,39 @@ struct BwdArgs {
     int n_kv_blocks, n_q_blocks;
     float scale, scale_log2;
     int vec_ok, vec4_ok;
+    // fast path work units (see BwdPlan)
+    int causal;
+    int kv_chunk, q_chunk, kv_units, q_units;  // iterations per unit, units per (batch, head)
+    float* kv_part;   // [kv_parts_max][2][B*Hkv*S*D]: dK then dV partials
+    float* q_part;    // [q_parts_max][B*Hq*S*D]
+    int64_t q_part_stride;  // B*Hq*S*D
 };
+
+// Fast-path work geometry (host and device use the same formulas).
+// dK/dV: per (batch, kv head) the iterations (128-key tile kt, query head of
+// the group, 32-row query block) are flattened kt-major; tile kt holds
+// fast_kv_n(kt) of them starting at fast_kv_start(kt).  dQ: per (batch, query
+// head) the iterations (128-row query tile qt, 64-key tile) are flattened
+// qt-major.  Work units are equal chunks of these ranges.
+__host__ __device__ inline int fast_nb(int S) { return (S + 31) / 32; }
+__host__ __device__ inline int fast_kv_n(int S, int causal, int group, int kt) {
+    return group * (causal ? fast_nb(S) - 4 * kt : fast_nb(S));
+}
+__host__ __device__ inline int64_t fast_kv_start(int S, int causal, int group, int kt) {
+    const int64_t nb = fast_nb(S);
+    return causal ? group * (kt * nb - 2 * (int64_t)kt * (kt - 1)) : (int64_t)group * nb * kt;
+}
+__host__ __device__ inline int fast_q_n(int S, int causal, int qt) {
+    const int kend = causal ? min(S, 128 * (qt + 1)) : S;
+    return (kend + 63) / 64;
+}
+__host__ __device__ inline int64_t fast_q_start(int S, int causal, int qt) {
+    return causal ? (int64_t)qt * (qt + 1) : (int64_t)qt * ((S + 63) / 64);
+}
+// Units [first, last] of chunk size `chunk` that touch the range [start, start + n).
+__host__ __device__ inline int fast_slots(int64_t start, int n, int64_t chunk) {
+    return (int)((start + n - 1) / chunk - start / chunk + 1);
+}
 
 // Output rows of dK / dV for a split.
 __device__ __forceinline__ void dkdv_out_rows(const BwdArgs& a, int b, int hk, int split, int key,
@@ -57,37 +89,6 @@ __device__ __forceinline__ void store_dkdv(const BwdArgs& a, float* dkp, float* 
                           dk[dt][4 * g + 2] * a.scale, dk[dt][4 * g + 3] * a.scale, v4);
             store4<float>(dvp, d0, a.D, dv[dt][4 * g], dv[dt][4 * g + 1], dv[dt][4 * g + 2], dv[dt][4 * g + 3], v4);
         }
-}
-
-// Block -> role.  Roles alternate while both have blocks left; within a role
-// the heaviest causal tiles come first (small key tiles for dK/dV, large
-// query tiles for dQ).
-__device__ __forceinline__ bool decode_block(const BwdArgs& a, int bid, int* t, int* y, int* b) {
-    const int m = min(a.n_kv_blocks, a.n_q_blocks);
-    bool kv;
-    int i;
-    if (bid < 2 * m) {
-        kv = (bid & 1) == 0;
-        i = bid >> 1;
-    } else {
-        kv = a.n_kv_blocks > a.n_q_blocks;
-        i = bid - m;
-    }
-    if (kv) {
-        const int yb = a.Hkv * a.splits * a.B;
-        *t = i / yb;
-        const int rest = i - *t * yb;
-        *y = rest % (a.Hkv * a.splits);
-        *b = rest / (a.Hkv * a.splits);
-    } else {
-        const int yb = a.Hq * a.B;
-        const int ti = i / yb;
-        const int rest = i - ti * yb;
-        *t = a.n_qtiles - 1 - ti;
-        *y = rest % a.Hq;
-        *b = rest / a.Hq;
-    }
-    return kv;
 }
 
 // ----------------------------------------------------------------- REDUCE

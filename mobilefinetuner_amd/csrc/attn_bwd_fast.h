@@ -65,7 +65,7 @@ template <int DP> struct BwdFastLds {
 };
 
 template <int DP, bool CAUSAL>
-__device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int kt, int ysplit, int b) {
+__device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int unit, int b, int hk) {
     constexpr int NT = 256, BNK = 128, CPR = DP / 8, NC = DP / 16, NDT = DP / 32;
     constexpr int QT = 32 * DP;
     constexpr int BUF = BwdFastLds<DP>::KV_BUF;
@@ -75,76 +75,93 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
     const int i16 = lane & 15, nh = (lane >> 4) & 1;
-    const int S = a.S, D = a.D;
-    const int j0 = kt * BNK;
-    const int hk = ysplit / a.splits, split = ysplit % a.splits;
-    const int h_begin = hk * a.group + split * a.heads_per_split;
-    const int h_end = min(h_begin + a.heads_per_split, (hk + 1) * a.group);
-    const int wkey0 = j0 + 32 * w;
-    const int key = wkey0 + n;
-    const int keyc = key < S ? key : S - 1;
-
+    const int S = a.S, D = a.D, G = a.group;
     const bf16* K = (const bf16*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
     const bf16* Vg = (const bf16*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
-    const int qstart = CAUSAL ? j0 : 0;
-    const int nqb = (S - qstart + 31) / 32;
-    const int niter = (h_end - h_begin) * nqb;
 
-    auto issue = [&](int it, bf16* buf) {
-        const int h = h_begin + it / nqb, qb = qstart + (it % nqb) * 32;
+    // This unit's chunk of the flattened (key tile, query head, query block)
+    // iterations; it may start inside one key tile and end inside a later one.
+    const int nkt = (S + BNK - 1) / BNK;
+    const int64_t g0 = (int64_t)unit * a.kv_chunk;
+    const int niter = (int)min((int64_t)a.kv_chunk, fast_kv_start(S, CAUSAL, G, nkt) - g0);
+    int kt = 0;
+    while (fast_kv_start(S, CAUSAL, G, kt + 1) <= g0) ++kt;
+
+    // Prefetch cursor: key tile and index in it of the next iteration to load.
+    int pf_kt = kt, pf_it = (int)(g0 - fast_kv_start(S, CAUSAL, G, kt));
+    int pf_n = fast_kv_n(S, CAUSAL, G, kt);
+    auto issue = [&](bf16* buf) {
+        const int nqb = pf_n / G;
+        const int h = hk * G + pf_it / nqb, qb = (CAUSAL ? pf_kt * BNK : 0) + (pf_it % nqb) * 32;
+        if (++pf_it == pf_n) {
+            ++pf_kt;
+            pf_it = 0;
+            pf_n = fast_kv_n(S, CAUSAL, G, pf_kt);
+        }
         const int64_t hoff = (int64_t)(b * a.Hq + h) * S * D;
         issue_tile<DP, 32, NT, SWZ_DUAL>((const bf16*)a.q + hoff, qb, S, D, buf);
         issue_tile<DP, 32, NT, SWZ_DUAL>((const bf16*)a.dO + hoff, qb, S, D, buf + QT);
         const float* st = a.stats + ((int64_t)(b * a.Hq + h) * a.nqb_total + qb / 32) * 64;
         load_lds_16(st + 4 * i16, buf + 2 * QT + w * 512);
     };
-    bf16* Vl = smem + 2 * BUF;  // V rows of this workgroup's keys (V_LDS only)
-    if constexpr (V_LDS) {
-        issue_tile<DP, BNK, NT, SWZ_ROW>(Vg, j0, S, D, Vl);
-        if (D < DP) {
-            // Staged columns >= D hold copies of column chunk 0, and so do
-            // those of the dO tiles: zero them here so that dP = dO V^T sums
-            // only the D real columns.
-            wait_vmcnt<0>();
-            __syncthreads();
-            const bf16x8 z = zero_vec<bf16x8>();
-            for (int idx = tid; idx < BNK * CPR; idx += NT) {
-                const int r = idx / CPR, c = idx % CPR;
-                if (8 * c >= D) *reinterpret_cast<bf16x8*>(Vl + r * DP + ((c ^ swz_row<CPR>(r)) << 3)) = z;
-            }
-            __syncthreads();
-        }
-    }
-    if (niter > 0) issue(0, smem);
 
+    bf16* Vl = smem + 2 * BUF;  // V rows of the current key tile (V_LDS only)
     bf16x8 kf[NC], vf[V_LDS ? 1 : NC];
+    // Per key tile: this lane's K (and V) fragments, and with V_LDS the V tile.
+    auto load_keys = [&](int t) {
+        const int key = t * BNK + 32 * w + n, keyc = key < S ? key : S - 1;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        kf[c] = load_chunk<bf16>(K + (int64_t)keyc * D, 16 * c + 8 * hh, D, key < S, true);
-        if constexpr (!V_LDS) vf[c] = load_chunk<bf16>(Vg + (int64_t)keyc * D, 16 * c + 8 * hh, D, key < S, true);
-    }
+        for (int c = 0; c < NC; ++c) {
+            kf[c] = load_chunk<bf16>(K + (int64_t)keyc * D, 16 * c + 8 * hh, D, key < S, true);
+            if constexpr (!V_LDS) vf[c] = load_chunk<bf16>(Vg + (int64_t)keyc * D, 16 * c + 8 * hh, D, key < S, true);
+        }
+        if constexpr (V_LDS) {
+            issue_tile<DP, BNK, NT, SWZ_ROW>(Vg, t * BNK, S, D, Vl);
+            if (D < DP) {
+                // Staged columns >= D hold copies of column chunk 0, and so do
+                // those of the dO tiles: zero them so that dP = dO V^T sums
+                // only the D real columns.
+                lds_barrier_vm<0>();
+                const bf16x8 z = zero_vec<bf16x8>();
+                for (int idx = tid; idx < BNK * CPR; idx += NT) {
+                    const int r = idx / CPR, c = idx % CPR;
+                    if (8 * c >= D) *reinterpret_cast<bf16x8*>(Vl + r * DP + ((c ^ swz_row<CPR>(r)) << 3)) = z;
+                }
+            }
+        }
+    };
+    load_keys(kt);
+    issue(smem);
+
     f32x16 dk[NDT], dv[NDT];
 #pragma unroll
     for (int i = 0; i < NDT; ++i) {
         dk[i] = zero16();
         dv[i] = zero16();
     }
+    int64_t kstart = fast_kv_start(S, CAUSAL, G, kt);
+    int kn = fast_kv_n(S, CAUSAL, G, kt);
 
-    for (int it = 0; it < niter; ++it) {
-        const bf16* Qb = smem + (it & 1) * BUF;
+    for (int i = 0;;) {
+      // Iterations of key tile kt inside this unit, then its dK/dV store.
+      const int seg_end = (int)min((int64_t)niter, kstart + kn - g0);
+      for (; i < seg_end; ++i) {
+        const bf16* Qb = smem + (i & 1) * BUF;
         const bf16* Gb = Qb + QT;
         const float* stt = reinterpret_cast<const float*>(Qb + 2 * QT + w * 512);
-        if (it + 1 < niter) {
+        if (i + 1 < niter) {
             lds_barrier();
-            issue(it + 1, smem + ((it + 1) & 1) * BUF);
+            issue(smem + ((i + 1) & 1) * BUF);
             lds_barrier_vm<LOADS>();
         } else {
             lds_barrier_vm<0>();
         }
-        const int qb = qstart + (it % nqb) * 32;
-        if (wkey0 >= S) continue;
-        if (CAUSAL && qb + 31 < wkey0) continue;
-
+        const int it = (int)(g0 + i - kstart);
+        const int qb = (CAUSAL ? kt * BNK : 0) + (it % (kn / G)) * 32;
+        const int wkey0 = kt * BNK + 32 * w;
+        const int key = wkey0 + n;
+        // Waves whose keys are past S or all after this query block skip it.
+        if (wkey0 < S && !(CAUSAL && qb + 31 < wkey0)) {
         // S = Q K^T and dP = dO V^T, one chunk of both per step; the steps'
         // LDS operands (Q, dO and, with V_LDS, V) are read PF steps ahead.
         f32x16 s = zero16(), dp = zero16();
@@ -223,15 +240,38 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
             }
             pin_read_ahead<NI, PF, 2>();
         }
+        }  // active wave
+      }
+      // End of this unit's part of key tile kt: a tile covered by one unit
+      // writes dK/dV, otherwise slot (unit - first unit of kt).
+      const int key = kt * BNK + 32 * w + n;
+      if (key < S) {
+          const int64_t off = ((int64_t)(b * a.Hkv + hk) * S + key) * D;
+          float *dkp = a.dk + off, *dvp = a.dv + off;
+          if (fast_slots(kstart, kn, a.kv_chunk) > 1) {
+              const int slot = unit - (int)(kstart / a.kv_chunk);
+              dkp = a.kv_part + (int64_t)(2 * slot) * a.part_stride + off;
+              dvp = dkp + a.part_stride;
+          }
+          store_dkdv<NDT>(a, dkp, dvp, hh, dk, dv);
+      }
+      if (i >= niter) break;
+      ++kt;
+      kstart = fast_kv_start(S, CAUSAL, G, kt);
+      kn = fast_kv_n(S, CAUSAL, G, kt);
+#pragma unroll
+      for (int d = 0; d < NDT; ++d) {
+          dk[d] = zero16();
+          dv[d] = zero16();
+      }
+      if constexpr (V_LDS) lds_barrier_vm<0>();  // all waves done with the old V tile
+      load_keys(kt);
+      if constexpr (V_LDS) lds_barrier_vm<0>();
     }
-    if (key >= S) return;
-    float *dkp, *dvp;
-    dkdv_out_rows(a, b, hk, split, key, &dkp, &dvp);
-    store_dkdv<NDT>(a, dkp, dvp, hh, dk, dv);
 }
 
 template <int DP, bool CAUSAL>
-__device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int qt, int h, int b) {
+__device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int unit, int b, int h) {
     constexpr int NT = 256, BN = 64, BM = 128, CPR = DP / 8, NC = DP / 16, NDT = DP / 32, NKK = BN / 32;
     constexpr int TILE = BN * DP;
     constexpr int BUF = BwdFastLds<DP>::Q_BUF;
@@ -242,47 +282,75 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int q
     const int i16 = lane & 15, nh = (lane >> 4) & 1;
     const int S = a.S, D = a.D;
     const int hk = h / a.group;
-    const int m0 = qt * BM, wrow0 = m0 + 32 * w, row = wrow0 + n;
-    const int rowc = row < S ? row : S - 1;
-
     const bf16* K = (const bf16*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
     const bf16* Vg = (const bf16*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
-    const int kend = CAUSAL ? min(S, m0 + BM) : S;
-    const int ntiles = (kend + BN - 1) / BN;
-    issue_tile<DP, BN, NT, SWZ_DUAL>(K, 0, S, D, smem);
-    issue_tile<DP, BN, NT, SWZ_ROW>(Vg, 0, S, D, smem + TILE);
-
     const bf16* Q = (const bf16*)a.q + (int64_t)(b * a.Hq + h) * S * D;
     const bf16* G = (const bf16*)a.dO + (int64_t)(b * a.Hq + h) * S * D;
-    bf16x8 qf[NC], gf[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        qf[c] = load_chunk<bf16>(Q + (int64_t)rowc * D, 16 * c + 8 * hh, D, row < S, true);
-        gf[c] = load_chunk<bf16>(G + (int64_t)rowc * D, 16 * c + 8 * hh, D, row < S, true);
+
+    // This unit's chunk of the flattened (query tile, key tile) iterations.
+    const int nqt = (S + BM - 1) / BM;
+    const int64_t g0 = (int64_t)unit * a.q_chunk;
+    const int niter = (int)min((int64_t)a.q_chunk, fast_q_start(S, CAUSAL, nqt) - g0);
+    int qt = 0;
+    while (fast_q_start(S, CAUSAL, qt + 1) <= g0) ++qt;
+    // Prefetch cursor: query tile and key tile of the next iteration to load.
+    int pf_qt = qt, pf_t = (int)(g0 - fast_q_start(S, CAUSAL, qt)), pf_n = fast_q_n(S, CAUSAL, qt);
+    auto next_key_tile = [&]() {
+        const int t = pf_t;
+        if (++pf_t == pf_n) {
+            ++pf_qt;
+            pf_t = 0;
+            pf_n = fast_q_n(S, CAUSAL, pf_qt);
+        }
+        return t;
+    };
+    {
+        const int kt0 = next_key_tile();
+        issue_tile<DP, BN, NT, SWZ_DUAL>(K, kt0 * BN, S, D, smem);
+        issue_tile<DP, BN, NT, SWZ_ROW>(Vg, kt0 * BN, S, D, smem + TILE);
     }
-    const float* blk = a.stats + ((int64_t)(b * a.Hq + h) * a.nqb_total + rowc / 32) * 64;
-    const float lse2 = row < S ? blk[rowc % 32] : INFINITY;
-    const float dlt = row < S ? blk[32 + rowc % 32] : 0.f;
+
+    bf16x8 qf[NC], gf[NC];
+    float lse2, dlt;
+    auto load_rows = [&](int t) {  // this lane's query row of tile t: Q, dO fragments and row terms
+        const int row = t * BM + 32 * w + n, rowc = row < S ? row : S - 1;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            qf[c] = load_chunk<bf16>(Q + (int64_t)rowc * D, 16 * c + 8 * hh, D, row < S, true);
+            gf[c] = load_chunk<bf16>(G + (int64_t)rowc * D, 16 * c + 8 * hh, D, row < S, true);
+        }
+        const float* blk = a.stats + ((int64_t)(b * a.Hq + h) * a.nqb_total + rowc / 32) * 64;
+        lse2 = row < S ? blk[rowc % 32] : INFINITY;
+        dlt = row < S ? blk[32 + rowc % 32] : 0.f;
+    };
+    load_rows(qt);
+    int64_t qstart = fast_q_start(S, CAUSAL, qt);
+    int qn = fast_q_n(S, CAUSAL, qt);
 
     f32x16 dq[NDT];
 #pragma unroll
     for (int i = 0; i < NDT; ++i) dq[i] = zero16();
 
-    for (int t = 0; t < ntiles; ++t) {
-        const bf16* Kb = smem + (t & 1) * BUF;
+    for (int i = 0;;) {
+      // Iterations of query tile qt inside this unit, then its dQ store.
+      const int seg_end = (int)min((int64_t)niter, qstart + qn - g0);
+      for (; i < seg_end; ++i) {
+        const bf16* Kb = smem + (i & 1) * BUF;
         const bf16* Vb = Kb + TILE;
-        if (t + 1 < ntiles) {
+        if (i + 1 < niter) {
             lds_barrier();
-            bf16* nb = smem + ((t + 1) & 1) * BUF;
-            issue_tile<DP, BN, NT, SWZ_DUAL>(K, (t + 1) * BN, S, D, nb);
-            issue_tile<DP, BN, NT, SWZ_ROW>(Vg, (t + 1) * BN, S, D, nb + TILE);
+            bf16* nb = smem + ((i + 1) & 1) * BUF;
+            const int ktn = next_key_tile();
+            issue_tile<DP, BN, NT, SWZ_DUAL>(K, ktn * BN, S, D, nb);
+            issue_tile<DP, BN, NT, SWZ_ROW>(Vg, ktn * BN, S, D, nb + TILE);
             lds_barrier_vm<LOADS>();
         } else {
             lds_barrier_vm<0>();
         }
+        const int t = (int)(g0 + i - qstart);
         const int kbase = t * BN;
-        if (wrow0 >= S || (CAUSAL && kbase > wrow0 + 31)) continue;
-
+        const int wrow0 = qt * BM + 32 * w, row = wrow0 + n;
+        if (!(wrow0 >= S || (CAUSAL && kbase > wrow0 + 31))) {
         const bool need_mask = (CAUSAL && kbase + BN - 1 > wrow0) || (kbase + BN > S);
 #pragma unroll 1
         for (int kk = 0; kk < NKK; ++kk) {
@@ -345,25 +413,77 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int q
                 pin_read_ahead<NI, PF, 2>();
             }
         }
+        }  // active wave
+      }
+      // End of this unit's part of query tile qt: a tile covered by one unit
+      // writes dQ, otherwise slot (unit - first unit of qt).
+      const int row = qt * BM + 32 * w + n;
+      if (row < S) {
+          const int64_t off = ((int64_t)(b * a.Hq + h) * S + row) * D;
+          float* dqp = a.dq + off;
+          if (fast_slots(qstart, qn, a.q_chunk) > 1)
+              dqp = a.q_part + (int64_t)(unit - (int)(qstart / a.q_chunk)) * a.q_part_stride + off;
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+              for (int g = 0; g < 4; ++g)
+                  store4<float>(dqp, 32 * dt + 8 * g + 4 * hh, D, dq[dt][4 * g] * a.scale,
+                                dq[dt][4 * g + 1] * a.scale, dq[dt][4 * g + 2] * a.scale,
+                                dq[dt][4 * g + 3] * a.scale, true);
+      }
+      if (i >= niter) break;
+      ++qt;
+      qstart = fast_q_start(S, CAUSAL, qt);
+      qn = fast_q_n(S, CAUSAL, qt);
+#pragma unroll
+      for (int d = 0; d < NDT; ++d) dq[d] = zero16();
+      load_rows(qt);
     }
-    if (row >= S) return;
-    float* dqp = a.dq + ((int64_t)(b * a.Hq + h) * S + row) * D;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-            store4<float>(dqp, 32 * dt + 8 * g + 4 * hh, D, dq[dt][4 * g] * a.scale, dq[dt][4 * g + 1] * a.scale,
-                          dq[dt][4 * g + 2] * a.scale, dq[dt][4 * g + 3] * a.scale, true);
+}
+
+// One workgroup per unit; unit u of every (batch, head) precedes unit u+1.
+template <int DP, bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_bf16_fast(BwdArgs a) {
+    __shared__ __attribute__((aligned(1024))) bf16 smem[BwdFastLds<DP>::KV_ELEMS];
+    const int bh = a.B * a.Hkv, i = (int)blockIdx.x;
+    dkdv_fast_body<DP, CAUSAL>(a, smem, i / bh, (i % bh) / a.Hkv, (i % bh) % a.Hkv);
 }
 
 template <int DP, bool CAUSAL>
-__global__ __launch_bounds__(256) void attn_bwd_main_bf16_fast(BwdArgs a) {
-    __shared__ __attribute__((aligned(1024))) bf16 smem[BwdFastLds<DP>::ELEMS];
-    int t, y, b;
-    if (decode_block(a, (int)blockIdx.x, &t, &y, &b))
-        dkdv_fast_body<DP, CAUSAL>(a, smem, t, y, b);
-    else
-        dq_fast_body<DP, CAUSAL>(a, smem, t, y, b);
+__global__ __launch_bounds__(256) void attn_bwd_dq_bf16_fast(BwdArgs a) {
+    __shared__ __attribute__((aligned(1024))) bf16 smem[BwdFastLds<DP>::Q_ELEMS];
+    const int bh = a.B * a.Hq, i = (int)blockIdx.x;
+    dq_fast_body<DP, CAUSAL>(a, smem, i / bh, (i % bh) / a.Hq, (i % bh) % a.Hq);
+}
+
+// REDUCE: sum the partial slots of every tile that was split, in slot order.
+template <bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_bwd_fast_reduce(BwdArgs a) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t nkv = a.part_stride, nq = a.q_part_stride;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < nkv + nq; e += stride) {
+        if (e < nkv) {
+            const int kt = (int)((e / a.D) % a.S) / 128;
+            const int np = fast_slots(fast_kv_start(a.S, CAUSAL, a.group, kt), fast_kv_n(a.S, CAUSAL, a.group, kt),
+                                      a.kv_chunk);
+            if (np <= 1) continue;
+            float sk = 0.f, sv = 0.f;
+            for (int p = 0; p < np; ++p) {
+                sk += a.kv_part[(int64_t)(2 * p) * nkv + e];
+                sv += a.kv_part[(int64_t)(2 * p + 1) * nkv + e];
+            }
+            a.dk[e] = sk;
+            a.dv[e] = sv;
+        } else {
+            const int64_t f = e - nkv;
+            const int qt = (int)((f / a.D) % a.S) / 128;
+            const int np = fast_slots(fast_q_start(a.S, CAUSAL, qt), fast_q_n(a.S, CAUSAL, qt), a.q_chunk);
+            if (np <= 1) continue;
+            float sq = 0.f;
+            for (int p = 0; p < np; ++p) sq += a.q_part[(int64_t)p * nq + f];
+            a.dq[f] = sq;
+        }
+    }
 }
 
 
@@ -375,17 +495,28 @@ hipError_t launch_bwd_fast(const AttnShape& s, BwdArgs a, int stages, hipStream_
         hipLaunchKernelGGL((attn_bwd_stats_kernel<bf16, DP>), dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256), 0,
                            st, a);
     }
-    if (stages & BWD_STAGE_MAIN) {
-        const unsigned blocks = (unsigned)(a.n_kv_blocks + a.n_q_blocks);
+    const BwdPlan pl = plan_bwd_fast(s);
+    if (stages & BWD_STAGE_DKDV) {
+        const dim3 grid((unsigned)(pl.kv_units * s.B * s.Hkv));
         if (s.causal)
-            hipLaunchKernelGGL((attn_bwd_main_bf16_fast<DP, true>), dim3(blocks), dim3(256), 0, st, a);
+            hipLaunchKernelGGL((attn_bwd_dkdv_bf16_fast<DP, true>), grid, dim3(256), 0, st, a);
         else
-            hipLaunchKernelGGL((attn_bwd_main_bf16_fast<DP, false>), dim3(blocks), dim3(256), 0, st, a);
+            hipLaunchKernelGGL((attn_bwd_dkdv_bf16_fast<DP, false>), grid, dim3(256), 0, st, a);
     }
-    if ((stages & BWD_STAGE_REDUCE) && a.splits > 1) {
-        int64_t blocks = (a.part_stride + 255) / 256;
-        if (blocks > 4096) blocks = 4096;
-        hipLaunchKernelGGL(attn_bwd_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
+    if (stages & BWD_STAGE_DQ) {
+        const dim3 grid((unsigned)(pl.q_units * s.B * s.Hq));
+        if (s.causal)
+            hipLaunchKernelGGL((attn_bwd_dq_bf16_fast<DP, true>), grid, dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL((attn_bwd_dq_bf16_fast<DP, false>), grid, dim3(256), 0, st, a);
+    }
+    if ((stages & BWD_STAGE_REDUCE) && (pl.kv_parts_max > 1 || pl.q_parts_max > 1)) {
+        int64_t blocks = (a.part_stride + a.q_part_stride + 255) / 256;
+        if (blocks > 8192) blocks = 8192;
+        if (s.causal)
+            hipLaunchKernelGGL(attn_bwd_fast_reduce<true>, dim3((unsigned)blocks), dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL(attn_bwd_fast_reduce<false>, dim3((unsigned)blocks), dim3(256), 0, st, a);
     }
     return hipGetLastError();
 }

@@ -22,8 +22,6 @@ mft_status fail(mft_status st, const std::string& msg) {
     return st;
 }
 
-size_t round_up(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
-
 mft_status check_desc(const mft_attn_desc* d, mft::AttnShape* s) {
     if (!d) return fail(MFT_ERR_INVALID_ARG, "mft_attn: desc is NULL");
     if (d->B <= 0 || d->Hq <= 0 || d->Hkv <= 0 || d->S <= 0 || d->D <= 0)
@@ -52,20 +50,6 @@ mft_status check_desc(const mft_attn_desc* d, mft::AttnShape* s) {
     return MFT_OK;
 }
 
-// Backward workspace: per-row softmax terms (fp32), then (splits > 1) dK and
-// dV partials [2 * splits * B*Hkv*S*D] fp32.
-void bwd_layout(const mft::AttnShape& s, size_t* delta_bytes, size_t* part_bytes) {
-    // delta [B*Hq*S] (general path) or row-stat blocks [B*Hq*ceil(S/32)*64] (bf16 fast path)
-    const size_t rows = static_cast<size_t>(s.B * s.Hq);
-    const size_t stat_floats = rows * static_cast<size_t>((s.S + 31) / 32) * 64;
-    const size_t delta_floats = rows * static_cast<size_t>(s.S);
-    *delta_bytes = round_up(sizeof(float) * (stat_floats > delta_floats ? stat_floats : delta_floats));
-    const int splits = mft::dkdv_splits(s);
-    *part_bytes = splits > 1 ? round_up(sizeof(float) * 2 * static_cast<size_t>(splits) *
-                                        static_cast<size_t>(s.B * s.Hkv * s.S * s.D))
-                             : 0;
-}
-
 mft_status hip_status(hipError_t e, const char* what) {
     if (e == hipSuccess) return MFT_OK;
     return fail(MFT_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
@@ -84,11 +68,7 @@ mft_status mft_attn_workspace_size(const mft_attn_desc* desc, size_t* fwd_bytes,
     const mft_status st = check_desc(desc, &s);
     if (st != MFT_OK) return st;
     if (fwd_bytes) *fwd_bytes = 0;
-    if (bwd_bytes) {
-        size_t a, b;
-        bwd_layout(s, &a, &b);
-        *bwd_bytes = a + b;
-    }
+    if (bwd_bytes) *bwd_bytes = mft::bwd_layout(s).total;
     return MFT_OK;
 }
 
@@ -113,11 +93,7 @@ mft_status mft_attn_bwd_stage(const mft_attn_desc* desc, int stages, const void*
     if (!q || !k || !v || !o || !dO || !lse || !dq || !dk || !dv)
         return fail(MFT_ERR_INVALID_ARG, "mft_attn_bwd: q, k, v, o, dO, lse, dq, dk, dv must be non-NULL");
     if (!workspace) return fail(MFT_ERR_INVALID_ARG, "mft_attn_bwd: workspace is NULL (see mft_attn_workspace_size)");
-    size_t delta_bytes, part_bytes;
-    bwd_layout(s, &delta_bytes, &part_bytes);
-    float* delta = static_cast<float*>(workspace);
-    float* part = part_bytes ? reinterpret_cast<float*>(static_cast<char*>(workspace) + delta_bytes) : nullptr;
-    return hip_status(mft::launch_attn_bwd(s, q, k, v, o, dO, lse, dq, dk, dv, delta, part, stages, stream),
+    return hip_status(mft::launch_attn_bwd(s, q, k, v, o, dO, lse, dq, dk, dv, workspace, stages, stream),
                       "mft_attn_bwd launch");
 }
 

@@ -23,19 +23,39 @@ int dkdv_splits(const AttnShape& s);
 // bf16 with D % 8 == 0 and 32 < D <= 256 takes the direct-to-LDS kernels.
 bool bwd_fast_path(const AttnShape& s);
 
+// Work decomposition of the bf16 fast backward.  Per (batch, kv head) the
+// dK/dV iterations (128-key tile, query head, 32-row query block) and per
+// (batch, query head) the dQ iterations (128-row query tile, 64-key tile) are
+// cut into equal chunks (kv_chunk / q_chunk iterations), about one unit per
+// CU in total, so the causal triangle no longer sets the critical path.  A
+// tile touched by several units gets fp32 partials (at most kv_parts_max /
+// q_parts_max slots) that REDUCE sums in slot order.
+struct BwdPlan {
+    int kv_chunk, q_chunk;
+    int kv_parts_max, q_parts_max;
+    int kv_units, q_units;  // units per (batch, kv head) and per (batch, query head)
+};
+BwdPlan plan_bwd_fast(const AttnShape& s);
+
+// Backward workspace layout in bytes: [delta or row-stat blocks][dK/dV
+// partials][dQ partials]; each region 256-byte aligned.
+struct BwdLayout {
+    size_t stats, kv_part, q_part, total;
+};
+BwdLayout bwd_layout(const AttnShape& s);
+
 hipError_t launch_attn_fwd(const AttnShape& s, const void* q, const void* k, const void* v,
                            void* o, float* lse, hipStream_t st);
 
-// Backward stages (bit mask): DELTA writes delta; MAIN runs the dK/dV and dQ
-// work (writing dK/dV partials when dkdv_splits(s) > 1); REDUCE sums them.
-enum { BWD_STAGE_DELTA = 1, BWD_STAGE_MAIN = 2, BWD_STAGE_REDUCE = 4, BWD_STAGE_ALL = 7 };
+// Backward stages (bit mask, values of MFT_BWD_*): DELTA writes the per-row
+// terms; DKDV and DQ compute the gradients (writing fp32 partials for split
+// tiles); REDUCE sums the partials.
+enum { BWD_STAGE_DELTA = 1, BWD_STAGE_DKDV = 2, BWD_STAGE_REDUCE = 4, BWD_STAGE_DQ = 8, BWD_STAGE_ALL = 15 };
 
-// delta: [B, Hq, S] fp32 scratch.  part: 2 * splits * B*Hkv*S*D fp32 scratch
-// (only used when dkdv_splits(s) > 1).
+// workspace: bwd_layout(s).total bytes.
 hipError_t launch_attn_bwd(const AttnShape& s, const void* q, const void* k, const void* v,
                            const void* o, const void* dO, const float* lse, float* dq,
-                           float* dk, float* dv, float* delta, float* part, int stages,
-                           hipStream_t st);
+                           float* dk, float* dv, void* workspace, int stages, hipStream_t st);
 
 hipError_t launch_repeat_kv_fwd(const void* kv, void* out, int64_t B, int64_t Hkv, int64_t S,
                                 int64_t D, int64_t r, int esize, hipStream_t st);

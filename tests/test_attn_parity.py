@@ -29,6 +29,7 @@ SHAPES = [
     (1, 4, 1, 160, 256),
     (1, 8, 2, 257, 256),
     (2, 4, 1, 64, 200),
+    (1, 2, 1, 640, 64),   # long enough that the bf16 backward splits query tiles over units
 ]
 
 
