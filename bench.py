@@ -120,6 +120,32 @@ def gpu_leg(cfg_id, steps, warmup):
     return dict(step_ms=step_ms, fwd_ms=fwd_ms, bwd_ms=bwd_ms, dkdv_ms=dkdv_ms, dq_ms=dq_ms, units=units)
 
 
+COPY_BYTES = 1 << 30
+
+
+def copy_calibration():
+    """A plain elementwise copy (reads COPY_BYTES, writes COPY_BYTES): the
+    known-size kernel that rocprofv3's FETCH_SIZE / WRITE_SIZE are scaled by."""
+    import torch
+    x = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda:0")
+    y = torch.empty_like(x)
+    for _ in range(3):
+        torch.mul(x, 1.0, out=y)
+    torch.cuda.synchronize()
+
+
+def hbm_traffic(cfg_id, kernel):
+    """HBM bytes per launch of `kernel` from the committed pmc summary
+    (profiles/hbm_traffic_<config>.json, written by
+    `python -m mobilefinetuner_amd.profiling traffic`), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"hbm_traffic_{cfg_id}.json")
+    try:
+        with open(path) as fh:
+            return json.load(fh)["kernels"][kernel]["hbm_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_leg(cfg_id):
     """Reference CPU operators on a bounded sample: one query head of the
     workload (same S, D), fwd+bwd, single-threaded as the reference is."""
@@ -156,6 +182,8 @@ def main():
     ap.add_argument("--config", default="c5", choices=sorted(CONFIGS))
     ap.add_argument("--all-configs", action="store_true", help="also report every config (extra key)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain copy of COPY_BYTES (for scaling rocprofv3 FETCH/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the attention path is built and measured on a single "
@@ -177,6 +205,7 @@ def main():
     ach = kern[dom][1] * units / (kern[dom][0] * 1e-3) / 1e12
     fwd_tf = 2 * units / (r["fwd_ms"] * 1e-3) / 1e12
     new_b, ref_b = saved_bytes(c)
+    traffic = hbm_traffic(args.config, dom)
     out = {
         "metric": METRIC,
         "value": round(tflops, 3),
@@ -202,7 +231,7 @@ def main():
         "bwd_tflops": round(5 * units / (r["bwd_ms"] * 1e-3) / 1e12, 2),
         "saved_bytes": {"new": new_b, "reference": ref_b, "ratio": round(ref_b / new_b, 1)},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(ach, 2), "peak": peak,
-                     "unit": "TFLOP/s", "frac": round(ach / peak, 4), "traffic": None},
+                     "unit": "TFLOP/s", "frac": round(ach / peak, 4), "traffic": traffic},
     }
     if args.all_configs:
         per = {}
@@ -218,6 +247,8 @@ def main():
                         "tokens_per_s": round(cc["B"] * cc["S"] / (rr["step_ms"] * 1e-3), 1),
                         "saved_bytes_new": nb, "saved_bytes_ref": rb}
         out["per_config"] = per
+    if args.copy_calibration:
+        copy_calibration()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_leg(args.config)
     print(json.dumps(out), flush=True)

@@ -1,0 +1,122 @@
+"""The C-ABI library without a GPU: it loads, exports every entry point that
+include/mft/attention.h declares, and rejects bad requests the way the
+reference rejects bad operator inputs (core/memory_efficient_attention.cpp:85-103)
+before any device work is enqueued."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mft", "attention.h")
+
+
+@pytest.fixture(scope="module")
+def capi():
+    from mobilefinetuner_amd import capi as M
+    if not os.path.exists(M.LIB_PATH):
+        from mobilefinetuner_amd import build
+        build.build(verbose=False)
+    M.lib()
+    return M
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return sorted(set(re.findall(r"\b(mft_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    fns = header_functions()
+    for f in ("mft_attn_workspace_size", "mft_attn_fwd", "mft_attn_bwd", "mft_repeat_kv_fwd",
+              "mft_repeat_kv_bwd", "mft_last_error"):
+        assert f in fns
+
+
+def test_every_header_symbol_is_exported(capi):
+    fns = header_functions()
+    assert sorted(capi.EXPORTS) == fns
+    out = subprocess.run(["nm", "-D", "--defined-only", capi.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    missing = [f for f in fns if f not in exported]
+    assert not missing, missing
+    L = capi.lib()
+    for f in fns:
+        assert hasattr(L, f)
+
+
+def test_header_compiles_as_c(tmp_path):
+    """The header is plain C (extern "C", C99 types, no torch types)."""
+    src = tmp_path / "t.c"
+    src.write_text('#include "mft/attention.h"\nint main(void){return mft_version()==1?0:1;}\n')
+    res = subprocess.run(["gcc", "-std=c99", "-fsyntax-only", "-D__HIP_PLATFORM_AMD__",
+                          "-I", os.path.join(ROOT, "include"), "-I", "/opt/rocm/include", str(src)],
+                         capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr
+
+
+def test_version(capi):
+    assert capi.lib().mft_version() == 1
+
+
+def _err(capi, fn):
+    with pytest.raises(capi.MftError) as e:
+        fn()
+    return e.value
+
+
+@pytest.mark.parametrize("kw,status,needle", [
+    (dict(B=0), 1, "positive"),
+    (dict(Hq=6, Hkv=4), 1, "multiple of kv heads"),
+    (dict(D=320), 2, "head_dim > 256"),
+    (dict(dtype=1), 1, "dtype"),
+    (dict(scale=float("nan")), 1, "scale"),
+])
+def test_desc_validation(capi, kw, status, needle):
+    args = dict(B=1, Hq=4, Hkv=1, S=64, D=64, scale=-1.0, causal=True, dtype=capi.MFT_BF16)
+    args.update(kw)
+    e = _err(capi, lambda: capi.workspace_size(capi.desc(**args)))
+    assert e.status == status and needle in str(e)
+
+
+def test_null_pointers_rejected_before_launch(capi):
+    d = capi.desc(1, 4, 1, 64, 64)
+    e = _err(capi, lambda: capi.attn_fwd(d, None, None, None, None, None, None, None))
+    assert e.status == capi.MFT_ERR_INVALID_ARG
+    e = _err(capi, lambda: capi.attn_bwd(d, 1, 1, 1, 1, 1, 1, 1, 1, 1, None, None))
+    assert e.status == capi.MFT_ERR_INVALID_ARG and "workspace" in str(e)
+    e = _err(capi, lambda: capi.attn_bwd_stage(d, 16, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, None))
+    assert "stages" in str(e)
+    e = _err(capi, lambda: capi.repeat_kv_fwd(None, None, 1, 1, 1, 1, 1, capi.MFT_F32, None))
+    assert e.status == capi.MFT_ERR_INVALID_ARG
+    e = _err(capi, lambda: capi.repeat_kv_bwd(1, 1, 1, 1, 1, 1, 0, None))
+    assert e.status == capi.MFT_ERR_INVALID_ARG
+
+
+def test_last_error_is_thread_local(capi):
+    import threading
+    _err(capi, lambda: capi.workspace_size(capi.desc(1, 3, 2, 8, 8)))
+    seen = []
+    t = threading.Thread(target=lambda: seen.append(capi.lib().mft_last_error()))
+    t.start()
+    t.join()
+    assert seen == [b""]
+    assert b"multiple" in capi.lib().mft_last_error()
+
+
+def test_workspace_is_aligned_and_subquadratic(capi):
+    """The backward workspace holds per-row statistics (O(S)) and fp32
+    partial tiles of split work units (bounded by the unit count): it never
+    grows like the S x S score matrices the reference keeps."""
+    sizes = []
+    for S in (1024, 4096, 16384):
+        f, b = capi.workspace_size(capi.desc(1, 4, 1, S, 256, 1 / 16, True, capi.MFT_BF16))
+        assert b % 256 == 0 and b > 0
+        sizes.append(b)
+        assert b < 4 * 4 * S * S * 4 or S <= 1024  # reference holds four S x S fp32 tensors per head
+    assert sizes[2] < 16 * sizes[1]  # 4x longer sequence, far less than 16x the bytes
