@@ -75,6 +75,8 @@ def gpu_leg(cfg_id, steps, warmup):
     dO = (torch.randn(B, Hq, S, D, device=dev, generator=g) * c["do_sigma"]).to(dt)
     scale = c["scale"]
     ws = torch.empty(max(A.workspace_bytes(q, k, scale, True), 1), dtype=torch.uint8, device=dev)
+    fws_n = A.fwd_workspace_bytes(q, k, scale, True)
+    fws = torch.empty(max(fws_n, 1), dtype=torch.uint8, device=dev)
     o = torch.empty_like(q)
     lse = torch.empty(B, Hq, S, dtype=torch.float32, device=dev)
     dq = torch.empty(q.shape, dtype=torch.float32, device=dev)
@@ -85,8 +87,10 @@ def gpu_leg(cfg_id, steps, warmup):
     sp = stream.cuda_stream
     P = [t.data_ptr() for t in (q, k, v, o, dO, lse, dq, dk, dv, ws)]
 
+    fws_ptr = fws.data_ptr() if fws_n else None
+
     def fwd():
-        capi.attn_fwd(d, P[0], P[1], P[2], P[3], P[5], None, sp)
+        capi.attn_fwd(d, P[0], P[1], P[2], P[3], P[5], fws_ptr, sp)
 
     def bwd():
         capi.attn_bwd(d, P[0], P[1], P[2], P[3], P[4], P[5], P[6], P[7], P[8], P[9], sp)

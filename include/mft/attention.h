@@ -28,8 +28,8 @@
  *   - lse[b, h, i] = log(sum_j exp(scale * q_i . k_j)) over the visible keys
  *     (natural log, fp32, [B, Hq, S]).  The backward recomputes the softmax
  *     from it; no S x S tensor is ever stored.
- *   - All pointers are caller-owned device memory; the library allocates
- *     nothing.  Work is enqueued on `stream` (NULL = the null stream) and is
+ *   - All pointers are caller-owned device memory, 16-byte aligned; the
+ *     library allocates nothing.  Work is enqueued on `stream` (NULL = the null stream) and is
  *     ordered there; the calls return before the GPU finishes.
  *   - Errors: a non-zero mft_status, and mft_last_error() returns a
  *     thread-local message.  The C++ adapter rethrows it as the reference's
@@ -68,8 +68,12 @@ typedef struct {
     mft_dtype dtype;          /* element type of q, k, v, o, dO                        */
 } mft_attn_desc;
 
-/* Workspace bytes the calls need (fwd: 0; bwd: per-row softmax terms and,
- * when dK/dV are split across head groups, their fp32 partials).
+/* Workspace bytes of the calls.
+ *   fwd: fp32 partial output tiles of query tiles whose key range is split
+ *        across work units (bf16 fast path; 0 for the other paths).  The
+ *        forward also accepts workspace = NULL and then runs one workgroup per
+ *        query tile (same results, no cross-unit load balancing).
+ *   bwd: per-row softmax terms and the fp32 partials of split tiles.
  * Replaces: nothing (the reference allocates from its pool implicitly). */
 mft_status mft_attn_workspace_size(const mft_attn_desc* desc, size_t* fwd_bytes,
                                    size_t* bwd_bytes);
@@ -77,7 +81,8 @@ mft_status mft_attn_workspace_size(const mft_attn_desc* desc, size_t* fwd_bytes,
 /* Forward: o = softmax(scale * q k^T [causal]) v, and lse.
  * Replaces the composite forward / memory_efficient_attention
  * (core/memory_efficient_attention.cpp:73-203 and :23-43).
- * lse may be NULL when no backward will follow (no-grad path). */
+ * lse may be NULL when no backward will follow (no-grad path).
+ * workspace: fwd_bytes from mft_attn_workspace_size, or NULL (see there). */
 mft_status mft_attn_fwd(const mft_attn_desc* desc, const void* q, const void* k,
                         const void* v, void* o, float* lse, void* workspace,
                         hipStream_t stream);

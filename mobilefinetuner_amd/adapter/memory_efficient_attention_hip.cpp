@@ -267,8 +267,11 @@ TensorPtr memory_efficient_attention(const TensorPtr& q, const TensorPtr& k, con
     saved->v = upload(v);
     saved->o = std::make_unique<DeviceBuffer>(static_cast<size_t>(q->numel()) * elt_size(dt));
     if (needs_grad) saved->lse = std::make_unique<DeviceBuffer>(static_cast<size_t>(B * Hq * S) * 4);
+    size_t fwd_ws = 0, bwd_ws = 0;
+    mft_check(mft_attn_workspace_size(&d, &fwd_ws, &bwd_ws));
+    DeviceBuffer ws(fwd_ws);
     mft_check(mft_attn_fwd(&d, saved->q->get(), saved->k->get(), saved->v->get(), saved->o->get(),
-                           needs_grad ? static_cast<float*>(saved->lse->get()) : nullptr, nullptr,
+                           needs_grad ? static_cast<float*>(saved->lse->get()) : nullptr, ws.get(),
                            adapter_stream()));
     auto out = download_as_f32(*saved->o, qs, dt);
 

@@ -36,11 +36,22 @@ def _stream():
 
 
 def workspace_bytes(q, k, scale=-1.0, causal=True):
+    """Backward workspace bytes."""
     return capi.workspace_size(_desc(q, k, scale, causal))[1]
 
 
-def attention_forward(q, k, v, scale: float = -1.0, causal: bool = True, want_lse: bool = True):
-    """o, lse = fused attention forward (lse None when want_lse is False)."""
+def fwd_workspace_bytes(q, k, scale=-1.0, causal=True):
+    """Forward workspace bytes (0 when the forward needs none)."""
+    return capi.workspace_size(_desc(q, k, scale, causal))[0]
+
+
+def attention_forward(q, k, v, scale: float = -1.0, causal: bool = True, want_lse: bool = True,
+                      workspace=None, balanced: bool = True):
+    """o, lse = fused attention forward (lse None when want_lse is False).
+
+    balanced=True passes the forward workspace (allocated here unless given),
+    which selects the launch that splits long query tiles across work units;
+    balanced=False passes none (one workgroup per query tile)."""
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
         _check(t, n)
     if k.dtype != q.dtype or v.dtype != q.dtype or k.shape != v.shape:
@@ -50,8 +61,15 @@ def attention_forward(q, k, v, scale: float = -1.0, causal: bool = True, want_ls
     d = _desc(q, k, scale, causal)
     o = torch.empty_like(q)
     lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device) if want_lse else None
+    ws_ptr = None
+    if balanced:
+        nbytes = capi.workspace_size(d)[0]
+        if nbytes:
+            if workspace is None or workspace.numel() < nbytes:
+                workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+            ws_ptr = workspace.data_ptr()
     capi.attn_fwd(d, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                  lse.data_ptr() if lse is not None else None, None, _stream())
+                  lse.data_ptr() if lse is not None else None, ws_ptr, _stream())
     return o, lse
 
 

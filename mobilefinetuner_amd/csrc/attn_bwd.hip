@@ -560,7 +560,6 @@ int padded_d(int64_t D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 
 
 bool bwd_fast_path(const AttnShape& s) { return s.bf16 && s.D % 8 == 0 && s.D > 32; }
 
-namespace {
 // Compute units of the current device (256 on MI355X), cached per device.
 int device_cus() {
     static std::atomic<int> cache[64];
@@ -572,7 +571,6 @@ int device_cus() {
     cache[dev].store(n, std::memory_order_relaxed);
     return n;
 }
-}  // namespace
 
 BwdPlan plan_bwd_fast(const AttnShape& s) {
     const int S = (int)s.S, causal = s.causal ? 1 : 0, group = (int)(s.Hq / s.Hkv);
@@ -586,8 +584,12 @@ BwdPlan plan_bwd_fast(const AttnShape& s) {
     const int64_t u_kv = std::max<int64_t>(1, (cus + pairs_kv - 1) / pairs_kv);
     const int64_t u_q = std::max<int64_t>(1, (cus + pairs_q - 1) / pairs_q);
     BwdPlan p;
-    p.kv_chunk = (int)std::min<int64_t>(n_kv, std::max<int64_t>(8, (n_kv + u_kv - 1) / u_kv));
-    p.q_chunk = (int)std::min<int64_t>(n_q, std::max<int64_t>(8, (n_q + u_q - 1) / u_q));
+    // Units no shorter than 8 iterations, and long enough that no tile spans
+    // more than 63 units (REDUCE keeps a tile's slot list in LDS, 64 entries).
+    const int64_t kv_min = std::max<int64_t>(8, (bwd::fast_kv_n(S, causal, group, 0) + 60) / 61);
+    const int64_t q_min = std::max<int64_t>(8, (bwd::fast_q_n(S, causal, nt - 1) + 60) / 61);
+    p.kv_chunk = (int)std::min<int64_t>(n_kv, std::max<int64_t>(kv_min, (n_kv + u_kv - 1) / u_kv));
+    p.q_chunk = (int)std::min<int64_t>(n_q, std::max<int64_t>(q_min, (n_q + u_q - 1) / u_q));
     p.kv_units = (int)((n_kv + p.kv_chunk - 1) / p.kv_chunk);
     p.q_units = (int)((n_q + p.q_chunk - 1) / p.q_chunk);
     p.kv_parts_max = p.q_parts_max = 1;
@@ -612,8 +614,11 @@ BwdLayout bwd_layout(const AttnShape& s) {
     l.stats = up(sizeof(float) * std::max(stat_floats, delta_floats));
     if (bwd_fast_path(s)) {
         const BwdPlan p = plan_bwd_fast(s);
-        l.kv_part = p.kv_parts_max > 1 ? up(sizeof(float) * 2 * p.kv_parts_max * kv_elems) : 0;
-        l.q_part = p.q_parts_max > 1 ? up(sizeof(float) * p.q_parts_max * q_elems) : 0;
+        // two slots per unit (split_slot), each one 128-row tile: dK and dV
+        // tiles for the dK/dV role, a dQ tile for the dQ role
+        const size_t tile = static_cast<size_t>(128 * s.D);
+        l.kv_part = p.kv_parts_max > 1 ? up(sizeof(float) * 2 * tile * 2 * p.kv_units * s.B * s.Hkv) : 0;
+        l.q_part = p.q_parts_max > 1 ? up(sizeof(float) * tile * 2 * p.q_units * s.B * s.Hq) : 0;
     } else {
         const int splits = dkdv_splits(s);
         l.kv_part = splits > 1 ? up(sizeof(float) * 2 * splits * kv_elems) : 0;

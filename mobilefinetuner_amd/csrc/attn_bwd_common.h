@@ -3,6 +3,7 @@
 #pragma once
 
 #include "attn_common.h"
+#include "attn_geometry.h"
 #include "attn_kernels.h"
 
 namespace mft {
@@ -32,36 +33,19 @@ struct BwdArgs {
     // fast path work units (see BwdPlan)
     int causal;
     int kv_chunk, q_chunk, kv_units, q_units;  // iterations per unit, units per (batch, head)
-    float* kv_part;   // [kv_parts_max][2][B*Hkv*S*D]: dK then dV partials
-    float* q_part;    // [q_parts_max][B*Hq*S*D]
+    float* kv_part;   // [B*Hkv][2*kv_units][dK, dV][128][D] partial tiles (split_slot)
+    float* q_part;    // [B*Hq][2*q_units][128][D] partial dQ tiles (split_slot)
     int64_t q_part_stride;  // B*Hq*S*D
 };
 
-// Fast-path work geometry (host and device use the same formulas).
-// dK/dV: per (batch, kv head) the iterations (128-key tile kt, query head of
-// the group, 32-row query block) are flattened kt-major; tile kt holds
-// fast_kv_n(kt) of them starting at fast_kv_start(kt).  dQ: per (batch, query
-// head) the iterations (128-row query tile qt, 64-key tile) are flattened
-// qt-major.  Work units are equal chunks of these ranges.
-__host__ __device__ inline int fast_nb(int S) { return (S + 31) / 32; }
-__host__ __device__ inline int fast_kv_n(int S, int causal, int group, int kt) {
-    return group * (causal ? fast_nb(S) - 4 * kt : fast_nb(S));
-}
-__host__ __device__ inline int64_t fast_kv_start(int S, int causal, int group, int kt) {
-    const int64_t nb = fast_nb(S);
-    return causal ? group * (kt * nb - 2 * (int64_t)kt * (kt - 1)) : (int64_t)group * nb * kt;
-}
-__host__ __device__ inline int fast_q_n(int S, int causal, int qt) {
-    const int kend = causal ? min(S, 128 * (qt + 1)) : S;
-    return (kend + 63) / 64;
-}
-__host__ __device__ inline int64_t fast_q_start(int S, int causal, int qt) {
-    return causal ? (int64_t)qt * (qt + 1) : (int64_t)qt * ((S + 63) / 64);
-}
-// Units [first, last] of chunk size `chunk` that touch the range [start, start + n).
-__host__ __device__ inline int fast_slots(int64_t start, int n, int64_t chunk) {
-    return (int)((start + n - 1) / chunk - start / chunk + 1);
-}
+// Work geometry of the fast path (attn_geometry.h), shared with the forward.
+using ::mft::fast_kv_n;
+using ::mft::fast_kv_start;
+using ::mft::fast_nb;
+using ::mft::fast_q_n;
+using ::mft::fast_q_start;
+using ::mft::fast_slots;
+using ::mft::split_slot;
 
 // Output rows of dK / dV for a split.
 __device__ __forceinline__ void dkdv_out_rows(const BwdArgs& a, int b, int hk, int split, int key,

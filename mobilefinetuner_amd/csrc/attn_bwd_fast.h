@@ -142,7 +142,7 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
     int64_t kstart = fast_kv_start(S, CAUSAL, G, kt);
     int kn = fast_kv_n(S, CAUSAL, G, kt);
 
-    for (int i = 0;;) {
+    for (int i = 0, first = 1;; first = 0) {
       // Iterations of key tile kt inside this unit, then its dK/dV store.
       const int seg_end = (int)min((int64_t)niter, kstart + kn - g0);
       for (; i < seg_end; ++i) {
@@ -243,15 +243,16 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
         }  // active wave
       }
       // End of this unit's part of key tile kt: a tile covered by one unit
-      // writes dK/dV, otherwise slot (unit - first unit of kt).
+      // writes dK/dV, otherwise this unit's slot (split_slot): [dK | dV]
+      // tiles of 128 key rows.
       const int key = kt * BNK + 32 * w + n;
       if (key < S) {
           const int64_t off = ((int64_t)(b * a.Hkv + hk) * S + key) * D;
           float *dkp = a.dk + off, *dvp = a.dv + off;
           if (fast_slots(kstart, kn, a.kv_chunk) > 1) {
-              const int slot = unit - (int)(kstart / a.kv_chunk);
-              dkp = a.kv_part + (int64_t)(2 * slot) * a.part_stride + off;
-              dvp = dkp + a.part_stride;
+              const int64_t slot = (int64_t)(b * a.Hkv + hk) * 2 * a.kv_units + 2 * unit + (first ? 0 : 1);
+              dkp = a.kv_part + (slot * 2 * BNK + (32 * w + n)) * D;
+              dvp = dkp + BNK * D;
           }
           store_dkdv<NDT>(a, dkp, dvp, hh, dk, dv);
       }
@@ -331,7 +332,7 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
 #pragma unroll
     for (int i = 0; i < NDT; ++i) dq[i] = zero16();
 
-    for (int i = 0;;) {
+    for (int i = 0, first = 1;; first = 0) {
       // Iterations of query tile qt inside this unit, then its dQ store.
       const int seg_end = (int)min((int64_t)niter, qstart + qn - g0);
       for (; i < seg_end; ++i) {
@@ -421,8 +422,10 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
       if (row < S) {
           const int64_t off = ((int64_t)(b * a.Hq + h) * S + row) * D;
           float* dqp = a.dq + off;
-          if (fast_slots(qstart, qn, a.q_chunk) > 1)
-              dqp = a.q_part + (int64_t)(unit - (int)(qstart / a.q_chunk)) * a.q_part_stride + off;
+          if (fast_slots(qstart, qn, a.q_chunk) > 1) {
+              const int64_t slot = (int64_t)(b * a.Hq + h) * 2 * a.q_units + 2 * unit + (first ? 0 : 1);
+              dqp = a.q_part + (slot * BM + 32 * w + n) * D;
+          }
 #pragma unroll
           for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -456,36 +459,69 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_bf16_fast(BwdArgs a) {
     dq_fast_body<DP, CAUSAL>(a, smem, i / bh, (i % bh) / a.Hq, (i % bh) % a.Hq);
 }
 
-// REDUCE: sum the partial slots of every tile that was split, in slot order.
-template <bool CAUSAL>
-__global__ __launch_bounds__(256) void attn_bwd_fast_reduce(BwdArgs a) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    const int64_t nkv = a.part_stride, nq = a.q_part_stride;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < nkv + nq; e += stride) {
-        if (e < nkv) {
-            const int kt = (int)((e / a.D) % a.S) / 128;
-            const int np = fast_slots(fast_kv_start(a.S, CAUSAL, a.group, kt), fast_kv_n(a.S, CAUSAL, a.group, kt),
-                                      a.kv_chunk);
-            if (np <= 1) continue;
-            float sk = 0.f, sv = 0.f;
-            for (int p = 0; p < np; ++p) {
-                sk += a.kv_part[(int64_t)(2 * p) * nkv + e];
-                sv += a.kv_part[(int64_t)(2 * p + 1) * nkv + e];
-            }
-            a.dk[e] = sk;
-            a.dv[e] = sv;
-        } else {
-            const int64_t f = e - nkv;
-            const int qt = (int)((f / a.D) % a.S) / 128;
-            const int np = fast_slots(fast_q_start(a.S, CAUSAL, qt), fast_q_n(a.S, CAUSAL, qt), a.q_chunk);
-            if (np <= 1) continue;
-            float sq = 0.f;
-            for (int p = 0; p < np; ++p) sq += a.q_part[(int64_t)p * nq + f];
-            a.dq[f] = sq;
+// REDUCE: sum the partial slots of every split tile in unit order.  One
+// workgroup per (batch, head, 128-row tile, 16-row group) of the dK/dV role
+// (rows = keys; dK and dV) and then of the dQ role (rows = queries);
+// workgroups of unsplit tiles return at once.
+constexpr int kRedRows = 16, kRedMaxSlots = 64;
+
+__device__ __forceinline__ void reduce_rows(const float* part, const int64_t* slot_of, int nsl, int64_t tile_elems,
+                                            int64_t row_in_tile, int D, float* dst) {
+    // thread -> 16-byte column chunks (tid % 16) + 16 j of row tid / 16
+    const int cl = threadIdx.x % 16, cg = D / 4;
+    constexpr int MAXJ = 256 / 4 / 16;
+    f32x4 acc[MAXJ];
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int p = 0; p < nsl; ++p) {
+        const float* src = part + slot_of[p] * tile_elems + row_in_tile * D;
+        f32x4 x[MAXJ];
+#pragma unroll
+        for (int j = 0; j < MAXJ; ++j) {
+            const int c = cl + 16 * j;
+            x[j] = c < cg ? *reinterpret_cast<const f32x4*>(src + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
         }
+#pragma unroll
+        for (int j = 0; j < MAXJ; ++j) acc[j] += x[j];
+    }
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j) {
+        const int c = cl + 16 * j;
+        if (c < cg) *reinterpret_cast<f32x4*>(dst + 4 * c) = acc[j];
     }
 }
 
+template <bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_bwd_fast_reduce(BwdArgs a) {
+    constexpr int RG = 128 / kRedRows;
+    __shared__ int64_t slot_of[kRedMaxSlots];
+    const int S = a.S, D = a.D, nt = (S + 127) / 128;
+    const int64_t kv_blocks = (int64_t)a.B * a.Hkv * nt * RG;
+    int64_t blk = blockIdx.x;
+    const bool kv = blk < kv_blocks;
+    if (!kv) blk -= kv_blocks;
+    const int rg = (int)(blk % RG), t = (int)((blk / RG) % nt), bh = (int)(blk / (RG * nt));
+    const int64_t start = kv ? fast_kv_start(S, CAUSAL, a.group, t) : fast_q_start(S, CAUSAL, t);
+    const int n = kv ? fast_kv_n(S, CAUSAL, a.group, t) : fast_q_n(S, CAUSAL, t);
+    const int64_t chunk = kv ? a.kv_chunk : a.q_chunk;
+    const int nsl = fast_slots(start, n, chunk);
+    const int r0 = t * 128 + rg * kRedRows;
+    if (nsl <= 1 || r0 >= S) return;
+    const int64_t u0 = start / chunk, head_slots = (int64_t)bh * 2 * (kv ? a.kv_units : a.q_units);
+    if ((int)threadIdx.x < nsl) slot_of[threadIdx.x] = head_slots + split_slot(start, chunk, u0 + threadIdx.x, u0);
+    __syncthreads();
+    const int r = threadIdx.x / 16;
+    if (r0 + r >= S) return;
+    const int64_t row = (int64_t)bh * S + r0 + r;
+    const int64_t rit = rg * kRedRows + r;  // row inside the tile
+    if (kv) {
+        // slot layout [dK rows 0..127][dV rows 0..127]
+        reduce_rows(a.kv_part, slot_of, nsl, 2 * 128 * (int64_t)D, rit, D, a.dk + row * D);
+        reduce_rows(a.kv_part, slot_of, nsl, 2 * 128 * (int64_t)D, 128 + rit, D, a.dv + row * D);
+    } else {
+        reduce_rows(a.q_part, slot_of, nsl, 128 * (int64_t)D, rit, D, a.dq + row * D);
+    }
+}
 
 template <int DP>
 hipError_t launch_bwd_fast(const AttnShape& s, BwdArgs a, int stages, hipStream_t st) {
@@ -511,8 +547,8 @@ hipError_t launch_bwd_fast(const AttnShape& s, BwdArgs a, int stages, hipStream_
             hipLaunchKernelGGL((attn_bwd_dq_bf16_fast<DP, false>), grid, dim3(256), 0, st, a);
     }
     if ((stages & BWD_STAGE_REDUCE) && (pl.kv_parts_max > 1 || pl.q_parts_max > 1)) {
-        int64_t blocks = (a.part_stride + a.q_part_stride + 255) / 256;
-        if (blocks > 8192) blocks = 8192;
+        const int64_t nt = (s.S + 127) / 128;
+        const int64_t blocks = (s.B * s.Hkv + s.B * s.Hq) * nt * (128 / kRedRows);
         if (s.causal)
             hipLaunchKernelGGL(attn_bwd_fast_reduce<true>, dim3((unsigned)blocks), dim3(256), 0, st, a);
         else

@@ -8,6 +8,7 @@
 #include "mft/attention.h"
 
 #include <cmath>
+#include <cstdint>
 #include <cstdio>
 #include <string>
 
@@ -50,6 +51,9 @@ mft_status check_desc(const mft_attn_desc* d, mft::AttnShape* s) {
     return MFT_OK;
 }
 
+// Tensors are read and written in 16-byte vectors.
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 mft_status hip_status(hipError_t e, const char* what) {
     if (e == hipSuccess) return MFT_OK;
     return fail(MFT_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
@@ -67,19 +71,20 @@ mft_status mft_attn_workspace_size(const mft_attn_desc* desc, size_t* fwd_bytes,
     mft::AttnShape s;
     const mft_status st = check_desc(desc, &s);
     if (st != MFT_OK) return st;
-    if (fwd_bytes) *fwd_bytes = 0;
+    if (fwd_bytes) *fwd_bytes = mft::fwd_workspace_bytes(s);
     if (bwd_bytes) *bwd_bytes = mft::bwd_layout(s).total;
     return MFT_OK;
 }
 
 mft_status mft_attn_fwd(const mft_attn_desc* desc, const void* q, const void* k, const void* v, void* o,
                         float* lse, void* workspace, hipStream_t stream) {
-    (void)workspace;
     mft::AttnShape s;
     const mft_status st = check_desc(desc, &s);
     if (st != MFT_OK) return st;
     if (!q || !k || !v || !o) return fail(MFT_ERR_INVALID_ARG, "mft_attn_fwd: q, k, v, o must be non-NULL");
-    return hip_status(mft::launch_attn_fwd(s, q, k, v, o, lse, stream), "mft_attn_fwd launch");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(lse) || !aligned16(workspace))
+        return fail(MFT_ERR_INVALID_ARG, "mft_attn_fwd: buffers must be 16-byte aligned");
+    return hip_status(mft::launch_attn_fwd(s, q, k, v, o, lse, workspace, stream), "mft_attn_fwd launch");
 }
 
 mft_status mft_attn_bwd_stage(const mft_attn_desc* desc, int stages, const void* q, const void* k,
@@ -93,6 +98,9 @@ mft_status mft_attn_bwd_stage(const mft_attn_desc* desc, int stages, const void*
     if (!q || !k || !v || !o || !dO || !lse || !dq || !dk || !dv)
         return fail(MFT_ERR_INVALID_ARG, "mft_attn_bwd: q, k, v, o, dO, lse, dq, dk, dv must be non-NULL");
     if (!workspace) return fail(MFT_ERR_INVALID_ARG, "mft_attn_bwd: workspace is NULL (see mft_attn_workspace_size)");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(dO) || !aligned16(lse) ||
+        !aligned16(dq) || !aligned16(dk) || !aligned16(dv) || !aligned16(workspace))
+        return fail(MFT_ERR_INVALID_ARG, "mft_attn_bwd: buffers must be 16-byte aligned");
     return hip_status(mft::launch_attn_bwd(s, q, k, v, o, dO, lse, dq, dk, dv, workspace, stages, stream),
                       "mft_attn_bwd launch");
 }

@@ -21,7 +21,10 @@
 // key order inside a 32-key block is permuted identically in V^T).
 // Causal: key tiles beyond the workgroup's last row are never visited and
 // query tiles run longest-first.
+#include <algorithm>
+
 #include "attn_common.h"
+#include "attn_geometry.h"
 #include "attn_kernels.h"
 
 namespace mft {
@@ -33,10 +36,15 @@ struct FwdArgs {
     const void* v;
     void* o;
     float* lse;
-    int S, D, Hq, Hkv, group, n_qtiles;
+    int B, S, D, Hq, Hkv, group, n_qtiles;
     float scale_log2;  // softmax scale * log2(e)
     int vec_ok;        // D % (16 bytes / element size) == 0
     int vec4_ok;       // D % 4 == 0
+    // balanced launch (bf16 fast path with a workspace; see FwdPlan)
+    int chunk;               // iterations per unit
+    int units;               // units per (batch, head)
+    float* part_o;           // [B*Hq][2*units][128][D] unnormalised O (split_slot)
+    float* part_ml;          // [B*Hq][2*units][128][2] running max (log2 units), sum
 };
 
 template <typename T, int DP, int BN> struct FwdLds {
@@ -237,25 +245,168 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
 //      reads of the O^T A operand); see attn_common.h.
 // V stays row-major; the transposing LDS read delivers V^T to the MFMA A
 // operand directly (see ds_read_tr4).
+//
+// Two launch shapes share the per-tile step:
+//   attn_fwd_bf16_fast  one workgroup per 128-row query tile (longest first);
+//   attn_fwd_bf16_split the (query tile, 64-key tile) iterations of each
+//                       (batch, head) flattened and cut into equal units, about
+//                       one per CU; a query tile spread over several units
+//                       leaves unnormalised fp32 partials (O, running max, sum)
+//                       that attn_fwd_combine merges by log-sum-exp in slot order.
+
+constexpr int kFwdBM = 128, kFwdBN = 64;
+
+// One 64-key tile for this wave's 32 rows: S^T = K Q^T, online softmax with
+// lazy rescale, O^T += V^T P^T.  Kb/Vb: the tile in LDS.
+template <int DP, bool CAUSAL>
+__device__ __forceinline__ void fwd_fast_tile(const FwdArgs& a, const bf16* Kb, const bf16* Vb, int kbase,
+                                              int wrow0, int row, const bf16x8 (&qf)[DP / 16],
+                                              f32x16 (&oacc)[DP / 32], float& m_run, float& l_run) {
+    constexpr int BN = kFwdBN, CPR = DP / 8, NC = DP / 16, NDT = DP / 32, NKK = BN / 32;
+    constexpr int PF = 4;  // LDS operand prefetch depth
+    const int lane = threadIdx.x & 63, n = lane & 31, hh = lane >> 5;
+    const int i16 = lane & 15, nh = (lane >> 4) & 1;
+    const int S = a.S;
+
+    // S^T = K Q^T: the NKK independent accumulator chains are interleaved
+    // and the K operands stream through a PF-deep register ring, so LDS
+    // latency overlaps the MFMAs instead of stalling each one.
+    f32x16 s[NKK];
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) s[kk] = zero16();
+    {
+        constexpr int NI = NKK * NC;
+        auto kread = [&](int it) {
+            return *reinterpret_cast<const bf16x8*>(
+                Kb + tile_off<CPR, SWZ_ROW>(32 * (it % NKK) + n, 16 * (it / NKK) + 8 * hh));
+        };
+        bf16x8 ring[PF];
+#pragma unroll
+        for (int it = 0; it < PF; ++it) ring[it] = kread(it);
+#pragma unroll
+        for (int it = 0; it < NI; ++it) {
+            const bf16x8 ka = ring[it % PF];
+            if (it + PF < NI) ring[it % PF] = kread(it + PF);
+            s[it % NKK] = mfma_bf16(ka, qf[it / NKK], s[it % NKK]);
+        }
+        pin_read_ahead<NI, PF, 1>();
+    }
+
+    // Keys past `lim` (causal: this lane's row; always: S-1) are masked,
+    // as selects so the hot loop stays branch-free.
+    if ((CAUSAL && kbase + BN - 1 > wrow0) || (kbase + BN > S)) {
+        const int lim = (CAUSAL ? min(row, S - 1) : S - 1) - kbase;
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[kk][r] = 32 * kk + row_of_reg(r, hh) > lim ? -INFINITY : s[kk][r];
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kk][r]);
+    mx = fmaxf(mx, other_half(mx)) * a.scale_log2;
+    // Lazy rescaling: the reference point m_run only moves (and O, l are
+    // rescaled) when some row of the wave sees a max above m_run + 8, so
+    // exp2 arguments stay <= 8 and P <= 256.  Any reference point gives
+    // the same O = acc / l and LSE = m_run + log2(l); this one skips the
+    // per-tile O multiply, which lives in accumulation registers.
+    if (__any(mx > m_run + kLazyRescale)) {
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.f : m_new));
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+        m_run = m_new;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    float psum = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float p = fast_exp2(s[kk][r] * a.scale_log2 - m_use);
+            s[kk][r] = p;
+            psum += p;
+        }
+    }
+    l_run += psum;
+
+    // O^T += V^T P^T, V^T operands through the same kind of register ring.
+    {
+        bf16x8 pb[2 * NKK];
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk)
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) pb[2 * kk + e][j] = (bf16)s[kk][8 * e + j];
+        constexpr int NI = 2 * NKK * NDT;  // iteration = (kk, e) block x dt
+        auto vread = [&](int it) {
+            const int ke = it / NDT, dt = it % NDT;
+            const int r0 = 16 * ke + 4 * hh + (i16 >> 2);
+            const int col = 32 * dt + 16 * nh + 4 * (i16 & 3);
+            const bf16x4 lo = ds_read_tr4(Vb + tile_off<CPR, SWZ_TR>(r0, col));
+            const bf16x4 hi = ds_read_tr4(Vb + tile_off<CPR, SWZ_TR>(r0 + 8, col));
+            return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        };
+        bf16x8 ring[PF];
+#pragma unroll
+        for (int it = 0; it < PF; ++it) ring[it] = vread(it);
+#pragma unroll
+        for (int it = 0; it < NI; ++it) {
+            const bf16x8 va = ring[it % PF];
+            if (it + PF < NI) ring[it % PF] = vread(it + PF);
+            oacc[it % NDT] = mfma_bf16(va, pb[it / NDT], oacc[it % NDT]);
+        }
+        pin_read_ahead<NI, PF, 2>();
+    }
+}
+
+// This lane's query row: Q fragments (B operand of S^T).
+template <int DP>
+__device__ __forceinline__ void fwd_load_q(const bf16* Q, int row, int S, int D, bf16x8 (&qf)[DP / 16]) {
+    const int hh = (threadIdx.x & 63) >> 5;
+    const int rowc = row < S ? row : S - 1;
+#pragma unroll
+    for (int c = 0; c < DP / 16; ++c) qf[c] = load_chunk<bf16>(Q + (int64_t)rowc * D, 16 * c + 8 * hh, D, row < S, true);
+}
+
+// Normalised O row and its LSE (rows < S; call with the wave's l_tot).
+template <int DP>
+__device__ __forceinline__ void fwd_store_row(const FwdArgs& a, int b, int h, int row, const f32x16 (&oacc)[DP / 32],
+                                              float m_run, float l_tot) {
+    const int hh = (threadIdx.x & 63) >> 5;
+    const float inv = 1.f / l_tot;
+    bf16* O = (bf16*)a.o + (int64_t)(b * a.Hq + h) * a.S * a.D + (int64_t)row * a.D;
+#pragma unroll
+    for (int dt = 0; dt < DP / 32; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            store4<bf16>(O, 32 * dt + 8 * g + 4 * hh, a.D, oacc[dt][4 * g] * inv, oacc[dt][4 * g + 1] * inv,
+                         oacc[dt][4 * g + 2] * inv, oacc[dt][4 * g + 3] * inv, true);
+    if (a.lse && hh == 0) a.lse[(int64_t)(b * a.Hq + h) * a.S + row] = (m_run + log2f(l_tot)) * kLn2;
+}
 
 template <int DP, bool CAUSAL>
 __global__ __launch_bounds__(256) void attn_fwd_bf16_fast(FwdArgs a) {
-    constexpr int NW = 4, BN = 64, BM = 32 * NW, NT = 256;
-    constexpr int CPR = DP / 8, NC = DP / 16, NDT = DP / 32, NKK = BN / 32;
-    constexpr int TILE = BN * DP;                       // elements of one K or V tile
-    constexpr int LOADS = 2 * BN * CPR / NT;            // direct loads per thread per tile
-    constexpr int PF = 4;                               // LDS operand prefetch depth
+    constexpr int BN = kFwdBN, BM = kFwdBM, NT = 256;
+    constexpr int CPR = DP / 8, NC = DP / 16, NDT = DP / 32;
+    constexpr int TILE = BN * DP;             // elements of one K or V tile
+    constexpr int LOADS = 2 * BN * CPR / NT;  // direct loads per thread per tile
     __shared__ __attribute__((aligned(1024))) bf16 smem[2 * 2 * TILE];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
+    const int lane = tid & 63, w = tid >> 6, n = lane & 31;
     const int S = a.S, D = a.D;
     const int qt = a.n_qtiles - 1 - (int)blockIdx.x;
     const int h = blockIdx.y, b = blockIdx.z, hk = h / a.group;
     const int m0 = qt * BM;
     const int wrow0 = m0 + 32 * w;
     const int row = wrow0 + n;
-    const int rowc = row < S ? row : S - 1;
 
     const bf16* __restrict__ Q = (const bf16*)a.q + (int64_t)(b * a.Hq + h) * S * D;
     const bf16* __restrict__ K = (const bf16*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
@@ -267,16 +418,12 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_fast(FwdArgs a) {
     issue_tile<DP, BN, NT, SWZ_TR>(Vg, 0, S, D, smem + TILE);
 
     bf16x8 qf[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-        qf[c] = load_chunk<bf16>(Q + (int64_t)rowc * D, 16 * c + 8 * hh, D, row < S, true);
-
+    fwd_load_q<DP>(Q, row, S, D, qf);
     f32x16 oacc[NDT];
 #pragma unroll
     for (int i = 0; i < NDT; ++i) oacc[i] = zero16();
     float m_run = -INFINITY, l_run = 0.f;
 
-    const int g16 = lane >> 4, i16 = lane & 15, nh = g16 & 1;
     for (int t = 0; t < ntiles; ++t) {
         const bf16* Kb = smem + (t & 1) * 2 * TILE;
         const bf16* Vb = Kb + TILE;
@@ -291,123 +438,218 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_fast(FwdArgs a) {
         }
         const int kbase = t * BN;
         if (wrow0 >= S || (CAUSAL && kbase > wrow0 + 31)) continue;
-
-        // S^T = K Q^T: the NKK independent accumulator chains are interleaved
-        // and the K operands stream through a PF-deep register ring, so LDS
-        // latency overlaps the MFMAs instead of stalling each one.
-        f32x16 s[NKK];
-#pragma unroll
-        for (int kk = 0; kk < NKK; ++kk) s[kk] = zero16();
-        {
-            constexpr int NI = NKK * NC;
-            auto kread = [&](int it) {
-                return *reinterpret_cast<const bf16x8*>(
-                    Kb + tile_off<CPR, SWZ_ROW>(32 * (it % NKK) + n, 16 * (it / NKK) + 8 * hh));
-            };
-            bf16x8 ring[PF];
-#pragma unroll
-            for (int it = 0; it < PF; ++it) ring[it] = kread(it);
-#pragma unroll
-            for (int it = 0; it < NI; ++it) {
-                const bf16x8 ka = ring[it % PF];
-                if (it + PF < NI) ring[it % PF] = kread(it + PF);
-                s[it % NKK] = mfma_bf16(ka, qf[it / NKK], s[it % NKK]);
-            }
-            pin_read_ahead<NI, PF, 1>();
-        }
-
-        // Keys past `lim` (causal: this lane's row; always: S-1) are masked,
-        // as selects so the hot loop stays branch-free.
-        if ((CAUSAL && kbase + BN - 1 > wrow0) || (kbase + BN > S)) {
-            const int lim = (CAUSAL ? min(row, S - 1) : S - 1) - kbase;
-#pragma unroll
-            for (int kk = 0; kk < NKK; ++kk)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    s[kk][r] = 32 * kk + row_of_reg(r, hh) > lim ? -INFINITY : s[kk][r];
-        }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int kk = 0; kk < NKK; ++kk)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kk][r]);
-        mx = fmaxf(mx, other_half(mx)) * a.scale_log2;
-        // Lazy rescaling: the reference point m_run only moves (and O, l are
-        // rescaled) when some row of the wave sees a max above m_run + 8, so
-        // exp2 arguments stay <= 8 and P <= 256.  Any reference point gives
-        // the same O = acc / l and LSE = m_run + log2(l); this one skips the
-        // per-tile O multiply, which lives in accumulation registers.
-        if (__any(mx > m_run + kLazyRescale)) {
-            const float m_new = fmaxf(m_run, mx);
-            const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.f : m_new));
-            l_run *= alpha;
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
-            m_run = m_new;
-        }
-        const float m_use = m_run == -INFINITY ? 0.f : m_run;
-        float psum = 0.f;
-#pragma unroll
-        for (int kk = 0; kk < NKK; ++kk) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float p = fast_exp2(s[kk][r] * a.scale_log2 - m_use);
-                s[kk][r] = p;
-                psum += p;
-            }
-        }
-        l_run += psum;
-
-        // O^T += V^T P^T, V^T operands through the same kind of register ring.
-        {
-            bf16x8 pb[2 * NKK];
-#pragma unroll
-            for (int kk = 0; kk < NKK; ++kk)
-#pragma unroll
-                for (int e = 0; e < 2; ++e)
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) pb[2 * kk + e][j] = (bf16)s[kk][8 * e + j];
-            constexpr int NI = 2 * NKK * NDT;  // iteration = (kk, e) block x dt
-            auto vread = [&](int it) {
-                const int ke = it / NDT, dt = it % NDT;
-                const int r0 = 16 * ke + 4 * hh + (i16 >> 2);
-                const int col = 32 * dt + 16 * nh + 4 * (i16 & 3);
-                const bf16x4 lo = ds_read_tr4(Vb + tile_off<CPR, SWZ_TR>(r0, col));
-                const bf16x4 hi = ds_read_tr4(Vb + tile_off<CPR, SWZ_TR>(r0 + 8, col));
-                return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            };
-            bf16x8 ring[PF];
-#pragma unroll
-            for (int it = 0; it < PF; ++it) ring[it] = vread(it);
-#pragma unroll
-            for (int it = 0; it < NI; ++it) {
-                const bf16x8 va = ring[it % PF];
-                if (it + PF < NI) ring[it % PF] = vread(it + PF);
-                oacc[it % NDT] = mfma_bf16(va, pb[it / NDT], oacc[it % NDT]);
-            }
-            pin_read_ahead<NI, PF, 2>();
-        }
+        fwd_fast_tile<DP, CAUSAL>(a, Kb, Vb, kbase, wrow0, row, qf, oacc, m_run, l_run);
     }
 
     if (wrow0 >= S) return;
     const float l_tot = l_run + other_half(l_run);
     if (row >= S) return;
-    const float inv = 1.f / l_tot;
-    bf16* O = (bf16*)a.o + (int64_t)(b * a.Hq + h) * S * D + (int64_t)row * D;
+    fwd_store_row<DP>(a, b, h, row, oacc, m_run, l_tot);
+}
+
+// Balanced launch: workgroup i = unit i / (B*Hq) of (batch, head) i % (B*Hq).
+template <int DP, bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
+    constexpr int BN = kFwdBN, BM = kFwdBM, NT = 256;
+    constexpr int CPR = DP / 8, NC = DP / 16, NDT = DP / 32;
+    constexpr int TILE = BN * DP;
+    constexpr int LOADS = 2 * BN * CPR / NT;
+    __shared__ __attribute__((aligned(1024))) bf16 smem[2 * 2 * TILE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
+    const int S = a.S, D = a.D;
+    const int bh = a.B * a.Hq, blk = (int)blockIdx.x;
+    const int unit = blk / bh, b = (blk % bh) / a.Hq, h = (blk % bh) % a.Hq, hk = h / a.group;
+
+    const bf16* __restrict__ Q = (const bf16*)a.q + (int64_t)(b * a.Hq + h) * S * D;
+    const bf16* __restrict__ K = (const bf16*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
+    const bf16* __restrict__ Vg = (const bf16*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
+
+    // This unit's chunk of the flattened (query tile, key tile) iterations.
+    const int nqt = (S + BM - 1) / BM;
+    const int64_t g0 = (int64_t)unit * a.chunk;
+    const int niter = (int)min((int64_t)a.chunk, fast_q_start(S, CAUSAL, nqt) - g0);
+    int qt = 0;
+    while (fast_q_start(S, CAUSAL, qt + 1) <= g0) ++qt;
+    // Prefetch cursor: query tile and key tile of the next iteration to load.
+    int pf_qt = qt, pf_t = (int)(g0 - fast_q_start(S, CAUSAL, qt)), pf_n = fast_q_n(S, CAUSAL, qt);
+    auto next_key_tile = [&]() {
+        const int t = pf_t;
+        if (++pf_t == pf_n) {
+            ++pf_qt;
+            pf_t = 0;
+            pf_n = fast_q_n(S, CAUSAL, pf_qt);
+        }
+        return t;
+    };
+    {
+        const int t0 = next_key_tile();
+        issue_tile<DP, BN, NT, SWZ_ROW>(K, t0 * BN, S, D, smem);
+        issue_tile<DP, BN, NT, SWZ_TR>(Vg, t0 * BN, S, D, smem + TILE);
+    }
+
+    bf16x8 qf[NC];
+    f32x16 oacc[NDT];
+    float m_run, l_run;
+    int64_t qstart = fast_q_start(S, CAUSAL, qt);
+    int qn = fast_q_n(S, CAUSAL, qt);
+    fwd_load_q<DP>(Q, qt * BM + 32 * w + n, S, D, qf);
+
+    for (int i = 0, first = 1;; first = 0) {
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+        for (int d = 0; d < NDT; ++d) oacc[d] = zero16();
+        m_run = -INFINITY;
+        l_run = 0.f;
+        const int wrow0 = qt * BM + 32 * w, row = wrow0 + n;
+        // Iterations of query tile qt inside this unit, then its output.
+        const int seg_end = (int)min((int64_t)niter, qstart + qn - g0);
+        for (; i < seg_end; ++i) {
+            const bf16* Kb = smem + (i & 1) * 2 * TILE;
+            const bf16* Vb = Kb + TILE;
+            if (i + 1 < niter) {
+                lds_barrier();
+                bf16* nb = smem + ((i + 1) & 1) * 2 * TILE;
+                const int tn = next_key_tile();
+                issue_tile<DP, BN, NT, SWZ_ROW>(K, tn * BN, S, D, nb);
+                issue_tile<DP, BN, NT, SWZ_TR>(Vg, tn * BN, S, D, nb + TILE);
+                lds_barrier_vm<LOADS>();
+            } else {
+                lds_barrier_vm<0>();
+            }
+            const int kbase = (int)(g0 + i - qstart) * BN;
+            if (!(wrow0 >= S || (CAUSAL && kbase > wrow0 + 31)))
+                fwd_fast_tile<DP, CAUSAL>(a, Kb, Vb, kbase, wrow0, row, qf, oacc, m_run, l_run);
+        }
+        // End of this unit's part of query tile qt: a tile inside one unit is
+        // written normalised; otherwise this unit's slot gets the unnormalised
+        // partial (O, running max, sum) for attn_fwd_combine.
+        if (wrow0 < S) {
+            const float l_tot = l_run + other_half(l_run);
+            const int nsl = fast_slots(qstart, qn, a.chunk);
+            if (nsl <= 1) {
+                if (row < S) fwd_store_row<DP>(a, b, h, row, oacc, m_run, l_tot);
+            } else if (row < S) {
+                const int64_t slot = (int64_t)(b * a.Hq + h) * 2 * a.units + 2 * unit + (first ? 0 : 1);
+                float* po = a.part_o + (slot * BM + 32 * w + n) * D;
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-            store4<bf16>(O, 32 * dt + 8 * g + 4 * hh, D, oacc[dt][4 * g] * inv, oacc[dt][4 * g + 1] * inv,
-                         oacc[dt][4 * g + 2] * inv, oacc[dt][4 * g + 3] * inv, true);
-    if (a.lse && hh == 0) a.lse[(int64_t)(b * a.Hq + h) * S + row] = (m_run + log2f(l_tot)) * kLn2;
+                for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g)
+                        store4<float>(po, 32 * dt + 8 * g + 4 * hh, D, oacc[dt][4 * g], oacc[dt][4 * g + 1],
+                                      oacc[dt][4 * g + 2], oacc[dt][4 * g + 3], true);
+                if (hh == 0) {
+                    float* pml = a.part_ml + (slot * BM + 32 * w + n) * 2;
+                    pml[0] = m_run;
+                    pml[1] = l_tot;
+                }
+            }
+        }
+        if (i >= niter) break;
+        ++qt;
+        qstart = fast_q_start(S, CAUSAL, qt);
+        qn = fast_q_n(S, CAUSAL, qt);
+        fwd_load_q<DP>(Q, qt * BM + 32 * w + n, S, D, qf);
+    }
+}
+
+// Merge the partial slots of every split query tile, in slot order:
+// m = max_i m_i, l = sum_i l_i 2^(m_i - m), O = sum_i O_i 2^(m_i - m) / l,
+// LSE = (m + log2 l) ln 2.  One workgroup per (batch, head, query tile,
+// 16-row group); workgroups of tiles that were not split return at once.
+// The per-(slot, row) weights go through LDS, then each thread sums 16-byte
+// column chunks over the slots.
+constexpr int kCombRows = 16, kCombMaxSlots = 64;
+
+template <bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_fwd_combine(FwdArgs a) {
+    constexpr int BM = kFwdBM, RG = BM / kCombRows;
+    __shared__ float wgt[kCombMaxSlots][kCombRows];
+    __shared__ float2 ml[kCombMaxSlots][kCombRows];
+    __shared__ float inv_l[kCombRows];
+    const int S = a.S, D = a.D;
+    const int nqt = (S + BM - 1) / BM;
+    const int rg = (int)blockIdx.x % RG, qt = ((int)blockIdx.x / RG) % nqt, bh = (int)blockIdx.x / (RG * nqt);
+    const int64_t qstart = fast_q_start(S, CAUSAL, qt);
+    const int nsl = fast_slots(qstart, fast_q_n(S, CAUSAL, qt), a.chunk);
+    const int r0 = qt * BM + rg * kCombRows;
+    if (nsl <= 1 || r0 >= S) return;
+    const int64_t u0 = qstart / a.chunk, head_slots = (int64_t)bh * 2 * a.units;
+    __shared__ int64_t slot_of[kCombMaxSlots];
+    const int rows = min(kCombRows, S - r0);
+    const int tid = threadIdx.x;
+    if (tid < nsl) slot_of[tid] = head_slots + split_slot(qstart, a.chunk, u0 + tid, u0);
+    __syncthreads();
+    // (running max, sum) of every (slot, row), loaded in parallel.
+    for (int i = tid; i < nsl * kCombRows; i += 256) {
+        const int p = i / kCombRows, r = i % kCombRows;
+        ml[p][r] = *reinterpret_cast<const float2*>(a.part_ml + (slot_of[p] * BM + rg * kCombRows + r) * 2);
+    }
+    __syncthreads();
+    if (tid < rows) {
+        float m = -INFINITY;
+        for (int p = 0; p < nsl; ++p) m = fmaxf(m, ml[p][tid].x);
+        float l = 0.f;
+        for (int p = 0; p < nsl; ++p) {
+            const float wp = ml[p][tid].x == -INFINITY ? 0.f : fast_exp2(ml[p][tid].x - m);
+            l += ml[p][tid].y * wp;
+            wgt[p][tid] = wp;
+        }
+        inv_l[tid] = 1.f / l;
+        if (a.lse) a.lse[(int64_t)bh * S + r0 + tid] = (m + log2f(l)) * kLn2;
+    }
+    __syncthreads();
+    // Thread -> row tid / 16, 16-byte column chunks (tid % 16) + 16 j: the
+    // chunks' loads of one slot are independent and issued together.
+    const int r = tid / 16, cl = tid % 16, cg = D / 4;  // fast path: D % 8 == 0
+    if (r >= rows) return;
+    constexpr int MAXJ = 256 / 4 / 16;
+    const int64_t rr = rg * kCombRows + r;
+    f32x4 acc[MAXJ];
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int p = 0; p < nsl; ++p) {
+        const float* src = a.part_o + (slot_of[p] * BM + rr) * D;
+        const float wp = wgt[p][r];
+        f32x4 x[MAXJ];
+#pragma unroll
+        for (int j = 0; j < MAXJ; ++j) {
+            const int c = cl + 16 * j;
+            x[j] = c < cg ? *reinterpret_cast<const f32x4*>(src + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int j = 0; j < MAXJ; ++j) acc[j] += x[j] * wp;
+    }
+    const float il = inv_l[r];
+    bf16* O = (bf16*)a.o + (int64_t)bh * S * D + (int64_t)(r0 + r) * D;
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j) {
+        const int c = cl + 16 * j;
+        if (c < cg) store4<bf16>(O, 4 * c, D, acc[j][0] * il, acc[j][1] * il, acc[j][2] * il, acc[j][3] * il, true);
+    }
 }
 
 template <int DP>
 hipError_t launch_fwd_fast(const AttnShape& s, FwdArgs a, hipStream_t st) {
-    a.n_qtiles = (int)((s.S + 127) / 128);
+    a.n_qtiles = (int)((s.S + kFwdBM - 1) / kFwdBM);
+    if (a.part_o) {
+        const FwdPlan p = plan_fwd_split(s);
+        a.chunk = p.chunk;
+        a.units = p.units;
+        const dim3 grid((unsigned)(p.units * s.B * s.Hq));
+        if (s.causal)
+            hipLaunchKernelGGL((attn_fwd_bf16_split<DP, true>), grid, dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL((attn_fwd_bf16_split<DP, false>), grid, dim3(256), 0, st, a);
+        if (p.any_split) {
+            const dim3 cgrid((unsigned)(s.B * s.Hq * a.n_qtiles * (kFwdBM / kCombRows)));
+            if (s.causal)
+                hipLaunchKernelGGL(attn_fwd_combine<true>, cgrid, dim3(256), 0, st, a);
+            else
+                hipLaunchKernelGGL(attn_fwd_combine<false>, cgrid, dim3(256), 0, st, a);
+        }
+        return hipGetLastError();
+    }
     dim3 grid(a.n_qtiles, (unsigned)s.Hq, (unsigned)s.B);
     if (s.causal)
         hipLaunchKernelGGL((attn_fwd_bf16_fast<DP, true>), grid, dim3(256), 0, st, a);
@@ -448,14 +690,44 @@ hipError_t launch_fwd_dispatch(const AttnShape& s, FwdArgs a, hipStream_t st) {
 
 int fwd_rows_per_block(const AttnShape&) { return 128; }
 
+FwdPlan plan_fwd_split(const AttnShape& s) {
+    const int S = (int)s.S, causal = s.causal ? 1 : 0;
+    const int nqt = (S + kFwdBM - 1) / kFwdBM;
+    const int64_t n = fast_q_start(S, causal, nqt);  // iterations per (batch, head)
+    const int64_t pairs = s.B * s.Hq;
+    const int64_t u = std::max<int64_t>(1, (device_cus() + pairs - 1) / pairs);
+    FwdPlan p;
+    // Units no shorter than 4 key tiles: a split costs one fp32 partial tile.
+    // A query tile has at most 2*S/64 key tiles; keep its slots <= kCombMaxSlots.
+    const int64_t max_tile = fast_q_n(S, causal, nqt - 1);
+    const int64_t min_chunk = std::max<int64_t>(4, (max_tile + kCombMaxSlots - 3) / (kCombMaxSlots - 2));
+    p.chunk = (int)std::min<int64_t>(n, std::max<int64_t>(min_chunk, (n + u - 1) / u));
+    p.units = (int)((n + p.chunk - 1) / p.chunk);
+    p.any_split = false;
+    for (int t = 0; t < nqt && !p.any_split; ++t)
+        p.any_split = fast_slots(fast_q_start(S, causal, t), fast_q_n(S, causal, t), p.chunk) > 1;
+    return p;
+}
+
+size_t fwd_workspace_bytes(const AttnShape& s) {
+    if (!(s.bf16 && s.D % 8 == 0 && s.D > 32)) return 0;
+    const FwdPlan p = plan_fwd_split(s);
+    const size_t rows = p.any_split ? static_cast<size_t>(s.B * s.Hq) * 2 * p.units * kFwdBM : 0;
+    auto up = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
+    // Always non-zero for this path, so that a caller that passes the queried
+    // workspace gets the balanced launch.
+    return up(rows * static_cast<size_t>(s.D) * 4) + up(rows * 2 * 4) + 256;
+}
+
 hipError_t launch_attn_fwd(const AttnShape& s, const void* q, const void* k, const void* v, void* o,
-                           float* lse, hipStream_t st) {
+                           float* lse, void* workspace, hipStream_t st) {
     FwdArgs a;
     a.q = q;
     a.k = k;
     a.v = v;
     a.o = o;
     a.lse = lse;
+    a.B = (int)s.B;
     a.S = (int)s.S;
     a.D = (int)s.D;
     a.Hq = (int)s.Hq;
@@ -465,6 +737,17 @@ hipError_t launch_attn_fwd(const AttnShape& s, const void* q, const void* k, con
     a.scale_log2 = s.scale * kLog2e;
     a.vec_ok = (s.D % (s.bf16 ? 8 : 4)) == 0;
     a.vec4_ok = (s.D % 4) == 0;
+    a.chunk = 0;
+    a.units = 0;
+    a.part_o = nullptr;
+    a.part_ml = nullptr;
+    if (workspace && fwd_workspace_bytes(s) > 0) {
+        const FwdPlan p = plan_fwd_split(s);
+        const size_t rows = p.any_split ? static_cast<size_t>(s.B * s.Hq) * 2 * p.units * kFwdBM : 0;
+        const size_t ob = (rows * static_cast<size_t>(s.D) * 4 + 255) & ~static_cast<size_t>(255);
+        a.part_o = static_cast<float*>(workspace);
+        a.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + ob);
+    }
     return s.bf16 ? launch_fwd_dispatch<bf16>(s, a, st) : launch_fwd_dispatch<float>(s, a, st);
 }
 

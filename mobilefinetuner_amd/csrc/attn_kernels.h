@@ -44,8 +44,25 @@ struct BwdLayout {
 };
 BwdLayout bwd_layout(const AttnShape& s);
 
+// Compute units of the current device (cached; 256 when the query fails).
+int device_cus();
+
+// Balanced forward (bf16 fast path): per (batch, head) the iterations
+// (128-row query tile, 64-key tile) are cut into `units` chunks of `chunk`
+// iterations; a query tile split across units leaves fp32 partials in the
+// units' slots (split_slot, attn_geometry.h).
+struct FwdPlan {
+    int chunk, units;
+    bool any_split;
+};
+FwdPlan plan_fwd_split(const AttnShape& s);
+// Forward workspace bytes (0 where the forward takes no workspace).  With a
+// workspace of this size the forward uses the balanced launch; without one
+// (NULL) it runs one workgroup per query tile.
+size_t fwd_workspace_bytes(const AttnShape& s);
+
 hipError_t launch_attn_fwd(const AttnShape& s, const void* q, const void* k, const void* v,
-                           void* o, float* lse, hipStream_t st);
+                           void* o, float* lse, void* workspace, hipStream_t st);
 
 // Backward stages (bit mask, values of MFT_BWD_*): DELTA writes the per-row
 // terms; DKDV and DQ compute the gradients (writing fp32 partials for split

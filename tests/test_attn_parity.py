@@ -30,6 +30,7 @@ SHAPES = [
     (1, 8, 2, 257, 256),
     (2, 4, 1, 64, 200),
     (1, 2, 1, 640, 64),   # long enough that the bf16 backward splits query tiles over units
+    (1, 4, 1, 1000, 256),  # Gemma-shaped, ragged: forward and backward split tiles over units
 ]
 
 
@@ -88,3 +89,23 @@ def test_default_scale_is_inv_sqrt_d(orc, dev):
     b = run_hip(q, k, v, dO, "f32", 1.0 / math.sqrt(48), True, dev)
     for n in ("o", "dq", "dk", "dv"):
         assert np.array_equal(a[n], b[n]), n
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_forward_launch_shapes_agree(orc, dev, causal):
+    """The balanced forward (workspace given: query tiles split across units,
+    partials merged by log-sum-exp) and the one-workgroup-per-tile forward
+    (workspace NULL) both meet the bar against the oracle."""
+    import torch
+    from gpu_util import TOL, to_dev
+    from mobilefinetuner_amd import attention as A
+    B, Hq, Hkv, S, D = 1, 4, 1, 1536, 256
+    q, k, v, _ = orc.make_inputs(B, Hq, Hkv, S, D, 61, "bf16")
+    ref = orc.composite(q, k, v, scale=1 / 16, causal=causal, want_lse=True)
+    tq, tk, tv = (to_dev(x, "bf16", dev) for x in (q, k, v))
+    assert A.fwd_workspace_bytes(tq, tk, 1 / 16, causal) > 0
+    for balanced in (True, False):
+        o, lse = A.attention_forward(tq, tk, tv, 1 / 16, causal, balanced=balanced)
+        torch.cuda.synchronize()
+        assert orc.max_rel(o.float().cpu().numpy(), ref["o"]) <= TOL["bf16"], balanced
+        assert np.max(np.abs(lse.cpu().numpy() - ref["lse"])) <= 1e-3, balanced

@@ -92,6 +92,10 @@ def test_null_pointers_rejected_before_launch(capi):
     assert e.status == capi.MFT_ERR_INVALID_ARG and "workspace" in str(e)
     e = _err(capi, lambda: capi.attn_bwd_stage(d, 16, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, None))
     assert "stages" in str(e)
+    e = _err(capi, lambda: capi.attn_fwd(d, 16, 32, 48, 8, None, None, None))
+    assert e.status == capi.MFT_ERR_INVALID_ARG and "aligned" in str(e)
+    e = _err(capi, lambda: capi.attn_bwd(d, 16, 16, 16, 16, 16, 16, 16, 16, 20, 16, None))
+    assert "aligned" in str(e)
     e = _err(capi, lambda: capi.repeat_kv_fwd(None, None, 1, 1, 1, 1, 1, capi.MFT_F32, None))
     assert e.status == capi.MFT_ERR_INVALID_ARG
     e = _err(capi, lambda: capi.repeat_kv_bwd(1, 1, 1, 1, 1, 1, 0, None))
