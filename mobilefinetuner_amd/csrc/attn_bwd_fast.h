@@ -69,7 +69,6 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
     constexpr int NT = 256, BNK = 128, CPR = DP / 8, NC = DP / 16, NDT = DP / 32;
     constexpr int QT = 32 * DP;
     constexpr int BUF = BwdFastLds<DP>::KV_BUF;
-    constexpr int LOADS = 2 * (32 * CPR / NT) + 1;
     constexpr bool V_LDS = BwdFastLds<DP>::V_LDS;
     constexpr int PF = 4;  // LDS operand prefetch depth
 
@@ -87,22 +86,55 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
     int kt = 0;
     while (fast_kv_start(S, CAUSAL, G, kt + 1) <= g0) ++kt;
 
-    // Prefetch cursor: key tile and index in it of the next iteration to load.
-    int pf_kt = kt, pf_it = (int)(g0 - fast_kv_start(S, CAUSAL, G, kt));
-    int pf_n = fast_kv_n(S, CAUSAL, G, kt);
-    auto issue = [&](bf16* buf) {
-        const int nqb = pf_n / G;
-        const int h = hk * G + pf_it / nqb, qb = (CAUSAL ? pf_kt * BNK : 0) + (pf_it % nqb) * 32;
-        if (++pf_it == pf_n) {
-            ++pf_kt;
-            pf_it = 0;
-            pf_n = fast_kv_n(S, CAUSAL, G, pf_kt);
+    // Prefetch cursor of the next iteration to load: key tile, query head of
+    // the group, query block (iterations of a key tile run head-major over
+    // its nqb = fast_kv_n / G query blocks); advanced without divisions.
+    const int nb = fast_nb(S);
+    int pf_kt = kt, pf_nqb = CAUSAL ? nb - 4 * kt : nb;
+    int pf_h, pf_qi;
+    {
+        const int it0 = (int)(g0 - fast_kv_start(S, CAUSAL, G, kt));
+        pf_h = it0 / pf_nqb;
+        pf_qi = it0 - pf_h * pf_nqb;
+    }
+    // The next block's loads: issue_begin resolves its sources (and advances
+    // the cursor), issue_part(j) issues load j of NPARTS, so that the loads
+    // can be spread between the MFMAs of the current block.
+    constexpr int PER = 32 * CPR / NT, NPARTS = 2 * PER + 1;
+    struct Pending {
+        const bf16* q;
+        const bf16* g;
+        const float* st;
+        bf16* buf;
+        int qb;
+    };
+    auto issue_begin = [&](bf16* buf) {
+        const int h = hk * G + pf_h, qb = (CAUSAL ? pf_kt * BNK : 0) + pf_qi * 32;
+        if (++pf_qi == pf_nqb) {
+            pf_qi = 0;
+            if (++pf_h == G) {
+                pf_h = 0;
+                ++pf_kt;
+                pf_nqb = CAUSAL ? nb - 4 * pf_kt : nb;
+            }
         }
         const int64_t hoff = (int64_t)(b * a.Hq + h) * S * D;
-        issue_tile<DP, 32, NT, SWZ_DUAL>((const bf16*)a.q + hoff, qb, S, D, buf);
-        issue_tile<DP, 32, NT, SWZ_DUAL>((const bf16*)a.dO + hoff, qb, S, D, buf + QT);
-        const float* st = a.stats + ((int64_t)(b * a.Hq + h) * a.nqb_total + qb / 32) * 64;
-        load_lds_16(st + 4 * i16, buf + 2 * QT + w * 512);
+        return Pending{(const bf16*)a.q + hoff, (const bf16*)a.dO + hoff,
+                       a.stats + ((int64_t)(b * a.Hq + h) * a.nqb_total + qb / 32) * 64, buf, qb};
+    };
+    auto issue_part = [&](const Pending& p, int j) {
+        if (j < PER)
+            issue_tile_part<DP, 32, NT, SWZ_DUAL>(p.q, p.qb, S, D, p.buf, j);
+        else if (j < 2 * PER)
+            issue_tile_part<DP, 32, NT, SWZ_DUAL>(p.g, p.qb, S, D, p.buf + QT, j - PER);
+        else
+            load_lds_16(p.st + 4 * i16, p.buf + 2 * QT + w * 512);
+    };
+    auto issue = [&](bf16* buf) {
+        const Pending p = issue_begin(buf);
+#pragma unroll
+        for (int j = 0; j < NPARTS; ++j) issue_part(p, j);
+        return p.qb;
     };
 
     bf16* Vl = smem + 2 * BUF;  // V rows of the current key tile (V_LDS only)
@@ -131,7 +163,10 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
         }
     };
     load_keys(kt);
-    issue(smem);
+    int cur_qb = issue(smem);  // query block of the block in the current buffer
+    // The key fragments are complete before the loop (the compiler then sees
+    // nothing pending inside it; the direct loads are untracked, see load_lds_16).
+    wait_vmcnt<0>();
 
     f32x16 dk[NDT], dv[NDT];
 #pragma unroll
@@ -149,19 +184,23 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
         const bf16* Qb = smem + (i & 1) * BUF;
         const bf16* Gb = Qb + QT;
         const float* stt = reinterpret_cast<const float*>(Qb + 2 * QT + w * 512);
-        if (i + 1 < niter) {
-            lds_barrier();
-            issue(smem + ((i + 1) & 1) * BUF);
-            lds_barrier_vm<LOADS>();
-        } else {
-            lds_barrier_vm<0>();
-        }
-        const int it = (int)(g0 + i - kstart);
-        const int qb = (CAUSAL ? kt * BNK : 0) + (it % (kn / G)) * 32;
+        // This wave's loads of buffer i&1 (issued one iteration ago) have
+        // landed; after the barrier every wave's have, and every wave is done
+        // with buffer (i+1)&1, which the next block then streams into.
+        wait_vmcnt<0>();
+        lds_barrier();
+        // The last block prefetches a harmless copy of itself into the idle
+        // buffer, so that the load schedule below needs no branch (the unit
+        // waits for it before it ends).
+        const Pending pend = i + 1 < niter ? issue_begin(smem + ((i + 1) & 1) * BUF)
+                                           : Pending{(const bf16*)a.q, (const bf16*)a.dO, a.stats,
+                                                     smem + ((i + 1) & 1) * BUF, 0};
+        const int qb = cur_qb;
+        cur_qb = pend.qb;
         const int wkey0 = kt * BNK + 32 * w;
         const int key = wkey0 + n;
         // Waves whose keys are past S or all after this query block skip it.
-        if (wkey0 < S && !(CAUSAL && qb + 31 < wkey0)) {
+        if (wave_uniform(wkey0 < S && !(CAUSAL && qb + 31 < wkey0))) {
         // S = Q K^T and dP = dO V^T, one chunk of both per step; the steps'
         // LDS operands (Q, dO and, with V_LDS, V) are read PF steps ahead.
         f32x16 s = zero16(), dp = zero16();
@@ -189,8 +228,11 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
                     dp = mfma_bf16(o.g, o.v, dp);
                 else
                     dp = mfma_bf16(o.g, vf[c], dp);
+                // next block's loads, one per step, behind this step's MFMAs
+                if (c < NPARTS) issue_part(pend, c);
             }
-            pin_read_ahead<NC, PF, R, 2>();
+#pragma unroll
+            for (int j = NC; j < NPARTS; ++j) issue_part(pend, j);
         }
         // lane column n = key; register r = query qb + row_of_reg(r, hh)
         const bool need_mask = CAUSAL && qb < wkey0 + 31;
@@ -240,6 +282,9 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
             }
             pin_read_ahead<NI, PF, 2>();
         }
+        } else {
+#pragma unroll
+            for (int j = 0; j < NPARTS; ++j) issue_part(pend, j);
         }  // active wave
       }
       // End of this unit's part of key tile kt: a tile covered by one unit
@@ -256,7 +301,10 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
           }
           store_dkdv<NDT>(a, dkp, dvp, hh, dk, dv);
       }
-      if (i >= niter) break;
+      if (i >= niter) {
+          wait_vmcnt<0>();  // the last block's self-copy has landed before the unit ends
+          break;
+      }
       ++kt;
       kstart = fast_kv_start(S, CAUSAL, G, kt);
       kn = fast_kv_n(S, CAUSAL, G, kt);
@@ -268,6 +316,7 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
       if constexpr (V_LDS) lds_barrier_vm<0>();  // all waves done with the old V tile
       load_keys(kt);
       if constexpr (V_LDS) lds_barrier_vm<0>();
+      wait_vmcnt<0>();
     }
 }
 
@@ -275,12 +324,15 @@ template <int DP, bool CAUSAL>
 __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int unit, int b, int h) {
     constexpr int NT = 256, BN = 64, BM = 128, CPR = DP / 8, NC = DP / 16, NDT = DP / 32, NKK = BN / 32;
     constexpr int TILE = BN * DP;
+    constexpr int PER = BN * CPR / NT;  // loads per thread of a K (V) tile: the K tile's are spread
+                                        // over the S/dP steps of kk = 0, the V tile's over kk = 1
+    static_assert(NKK == 2, "one tile's loads per 32-key block");
     constexpr int BUF = BwdFastLds<DP>::Q_BUF;
-    constexpr int LOADS = 2 * (BN * CPR / NT);
     constexpr int PF = 4;  // LDS operand prefetch depth
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
     const int i16 = lane & 15, nh = (lane >> 4) & 1;
+    const int wu = wave_id();
     const int S = a.S, D = a.D;
     const int hk = h / a.group;
     const bf16* K = (const bf16*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
@@ -325,6 +377,7 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
         dlt = row < S ? blk[32 + rowc % 32] : 0.f;
     };
     load_rows(qt);
+    wait_vmcnt<0>();
     int64_t qstart = fast_q_start(S, CAUSAL, qt);
     int qn = fast_q_n(S, CAUSAL, qt);
 
@@ -338,20 +391,28 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
       for (; i < seg_end; ++i) {
         const bf16* Kb = smem + (i & 1) * BUF;
         const bf16* Vb = Kb + TILE;
-        if (i + 1 < niter) {
-            lds_barrier();
-            bf16* nb = smem + ((i + 1) & 1) * BUF;
-            const int ktn = next_key_tile();
-            issue_tile<DP, BN, NT, SWZ_DUAL>(K, ktn * BN, S, D, nb);
-            issue_tile<DP, BN, NT, SWZ_ROW>(Vg, ktn * BN, S, D, nb + TILE);
-            lds_barrier_vm<LOADS>();
-        } else {
-            lds_barrier_vm<0>();
-        }
+        wait_vmcnt<0>();  // see dkdv_fast_body
+        lds_barrier();
+        // Next key tile's loads (K then V, NPARTS per thread), spread over the
+        // S/dP steps below; the last block re-loads key tile 0 into the idle
+        // buffer so that the schedule has no branch (waited for at the end).
+        bf16* const nbuf = smem + ((i + 1) & 1) * BUF;
+        const int ktn = i + 1 < niter ? next_key_tile() : 0;
+        // Load j of the K tile (v = 0) or of the V tile (v = 1; v may be a
+        // runtime value: the two tiles differ only in source, destination
+        // and swizzle, which are selected without a branch).
+        auto issue_part = [&](int v, int j) {
+            const int m = wu * PER + j, P = m * 64 + lane;
+            const int r = P / CPR, p = P % CPR;
+            const int c = p ^ (v ? swz<CPR, SWZ_ROW>(r) : swz<CPR, SWZ_DUAL>(r));
+            const int gr = min(ktn * BN + r, S - 1);
+            const int col = 8 * c < D ? 8 * c : 0;
+            load_lds_16((v ? Vg : K) + (int64_t)gr * D + col, (v ? nbuf + TILE : nbuf) + m * 512);
+        };
         const int t = (int)(g0 + i - qstart);
         const int kbase = t * BN;
         const int wrow0 = qt * BM + 32 * w, row = wrow0 + n;
-        if (!(wrow0 >= S || (CAUSAL && kbase > wrow0 + 31))) {
+        if (wave_uniform(!(wrow0 >= S || (CAUSAL && kbase > wrow0 + 31)))) {
         const bool need_mask = (CAUSAL && kbase + BN - 1 > wrow0) || (kbase + BN > S);
 #pragma unroll 1
         for (int kk = 0; kk < NKK; ++kk) {
@@ -376,8 +437,10 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
                         dp = mfma_bf16(av, gf[it >> 1], dp);
                     else
                         s = mfma_bf16(av, qf[it >> 1], s);
+                    if ((it & 1) && (it >> 1) < PER) issue_part(kk, it >> 1);
                 }
-                pin_read_ahead<NI, PF, 1>();
+#pragma unroll
+                for (int j = NI / 2; j < PER; ++j) issue_part(kk, j);
             }
             // lane column n = query row; register r = key kbase + 32kk + row_of_reg(r, hh)
             const int lim = need_mask ? (CAUSAL ? min(row, S - 1) : S - 1) - kbase - 32 * kk : 64;
@@ -414,6 +477,12 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
                 pin_read_ahead<NI, PF, 2>();
             }
         }
+        } else {
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                issue_part(0, j);
+                issue_part(1, j);
+            }
         }  // active wave
       }
       // End of this unit's part of query tile qt: a tile covered by one unit
@@ -434,13 +503,17 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
                                 dq[dt][4 * g + 1] * a.scale, dq[dt][4 * g + 2] * a.scale,
                                 dq[dt][4 * g + 3] * a.scale, true);
       }
-      if (i >= niter) break;
+      if (i >= niter) {
+          wait_vmcnt<0>();  // the last block's re-load has landed before the unit ends
+          break;
+      }
       ++qt;
       qstart = fast_q_start(S, CAUSAL, qt);
       qn = fast_q_n(S, CAUSAL, qt);
 #pragma unroll
       for (int d = 0; d < NDT; ++d) dq[d] = zero16();
       load_rows(qt);
+      wait_vmcnt<0>();
     }
 }
 

@@ -137,8 +137,27 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
 
+// global_load_lds_dwordx4: lane l copies 16 bytes from gptr (its own address)
+// to LDS byte address M0 + 16 l, without a VGPR round trip.  Issued as inline
+// asm so that the compiler does not track it as an LDS write: it would
+// otherwise wait for every outstanding direct load (vmcnt(0)) before LDS
+// reads it cannot prove disjoint, including reads of the OTHER buffer while
+// the next tile streams in.  The kernels order these loads themselves with
+// lds_barrier_vm (explicit vmcnt) and workgroup barriers.  Loads complete in
+// order, so the compiler's own vmcnt waits stay correct (they only become
+// more conservative).
+// Wave index in the workgroup as a wave-uniform (scalar) value, for LDS
+// addresses of the direct loads.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// A condition that is the same in every lane of the wave, as a scalar: an
+// if/else on it is a scalar branch, so a wave that skips a block does not
+// step through it with an empty exec mask (and vice versa).
+__device__ __forceinline__ bool wave_uniform(bool c) { return __builtin_amdgcn_readfirstlane((int)c) != 0; }
+
 __device__ __forceinline__ void load_lds_16(const void* gptr, void* lds_base) {
-    __builtin_amdgcn_global_load_lds(gptr, (lds_void_t*)lds_base, 16, 0, 0);
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds_base);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(m0) : "memory", "m0");
 }
 
 // s_waitcnt vmcnt(n) with the other counters left unconstrained (gfx9
@@ -230,23 +249,31 @@ __device__ __forceinline__ int tile_off(int r, int col) {
 // the work; every thread issues ROWS*DP/8/NT loads (wave-uniform count).
 // Rows >= S read row S-1 and chunks >= D read chunk 0, so every address is
 // in bounds; callers mask such rows and never use such columns.
+// Load j (0 <= j < ROWS*DP/8/NT) of this thread's share of such a tile, so
+// that a tile's loads can be spread between other instructions.
 template <int DP, int ROWS, int NT, int SWZ>
-__device__ __forceinline__ void issue_tile(const bf16* __restrict__ src, int row0, int S, int D,
-                                           bf16* lds_tile) {
+__device__ __forceinline__ void issue_tile_part(const bf16* __restrict__ src, int row0, int S, int D,
+                                                bf16* lds_tile, int j) {
     constexpr int CPR = DP / 8;
     constexpr int PER_WAVE = ROWS * CPR / NT;
     static_assert(PER_WAVE * NT == ROWS * CPR, "tile must split evenly over the threads");
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int w = wave_id();
+    const int m = w * PER_WAVE + j;
+    const int P = m * 64 + lane;
+    const int r = P / CPR, p = P % CPR;
+    const int c = p ^ swz<CPR, SWZ>(r);
+    const int gr = min(row0 + r, S - 1);
+    const int col = 8 * c < D ? 8 * c : 0;
+    load_lds_16(src + (int64_t)gr * D + col, lds_tile + m * 512);
+}
+
+template <int DP, int ROWS, int NT, int SWZ>
+__device__ __forceinline__ void issue_tile(const bf16* __restrict__ src, int row0, int S, int D,
+                                           bf16* lds_tile) {
+    constexpr int PER_WAVE = ROWS * (DP / 8) / NT;
 #pragma unroll
-    for (int j = 0; j < PER_WAVE; ++j) {
-        const int m = w * PER_WAVE + j;
-        const int P = m * 64 + lane;
-        const int r = P / CPR, p = P % CPR;
-        const int c = p ^ swz<CPR, SWZ>(r);
-        const int gr = min(row0 + r, S - 1);
-        const int col = 8 * c < D ? 8 * c : 0;
-        load_lds_16(src + (int64_t)gr * D + col, lds_tile + m * 512);
-    }
+    for (int j = 0; j < PER_WAVE; ++j) issue_tile_part<DP, ROWS, NT, SWZ>(src, row0, S, D, lds_tile, j);
 }
 
 }  // namespace mft

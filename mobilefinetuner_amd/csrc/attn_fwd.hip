@@ -256,12 +256,21 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
 
 constexpr int kFwdBM = 128, kFwdBN = 64;
 
+// Direct loads per thread of one K (or V) tile, and of both.
+template <int DP> struct FwdLoads {
+    static constexpr int PER = kFwdBN * (DP / 8) / 256, NPARTS = 2 * PER;
+};
+
 // One 64-key tile for this wave's 32 rows: S^T = K Q^T, online softmax with
-// lazy rescale, O^T += V^T P^T.  Kb/Vb: the tile in LDS.
-template <int DP, bool CAUSAL>
+// lazy rescale, O^T += V^T P^T.  Kb/Vb: the tile in LDS.  issue_part(j),
+// j < FwdLoads<DP>::NPARTS, issues the next tile's loads; they are spread
+// over the S^T steps.
+template <int DP, bool CAUSAL, class IssuePart>
 __device__ __forceinline__ void fwd_fast_tile(const FwdArgs& a, const bf16* Kb, const bf16* Vb, int kbase,
                                               int wrow0, int row, const bf16x8 (&qf)[DP / 16],
-                                              f32x16 (&oacc)[DP / 32], float& m_run, float& l_run) {
+                                              f32x16 (&oacc)[DP / 32], float& m_run, float& l_run,
+                                              const IssuePart& issue_part) {
+    constexpr int NPARTS = FwdLoads<DP>::NPARTS;
     constexpr int BN = kFwdBN, CPR = DP / 8, NC = DP / 16, NDT = DP / 32, NKK = BN / 32;
     constexpr int PF = 4;  // LDS operand prefetch depth
     const int lane = threadIdx.x & 63, n = lane & 31, hh = lane >> 5;
@@ -288,8 +297,10 @@ __device__ __forceinline__ void fwd_fast_tile(const FwdArgs& a, const bf16* Kb, 
             const bf16x8 ka = ring[it % PF];
             if (it + PF < NI) ring[it % PF] = kread(it + PF);
             s[it % NKK] = mfma_bf16(ka, qf[it / NKK], s[it % NKK]);
+            if ((it & 1) && (it >> 1) < NPARTS) issue_part(it >> 1);
         }
-        pin_read_ahead<NI, PF, 1>();
+#pragma unroll
+        for (int j = NI / 2; j < NPARTS; ++j) issue_part(j);
     }
 
     // Keys past `lim` (causal: this lane's row; always: S-1) are masked,
@@ -396,7 +407,6 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_fast(FwdArgs a) {
     constexpr int BN = kFwdBN, BM = kFwdBM, NT = 256;
     constexpr int CPR = DP / 8, NC = DP / 16, NDT = DP / 32;
     constexpr int TILE = BN * DP;             // elements of one K or V tile
-    constexpr int LOADS = 2 * BN * CPR / NT;  // direct loads per thread per tile
     __shared__ __attribute__((aligned(1024))) bf16 smem[2 * 2 * TILE];
 
     const int tid = threadIdx.x;
@@ -419,6 +429,7 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_fast(FwdArgs a) {
 
     bf16x8 qf[NC];
     fwd_load_q<DP>(Q, row, S, D, qf);
+    wait_vmcnt<0>();  // Q complete before the loop (direct loads are untracked)
     f32x16 oacc[NDT];
 #pragma unroll
     for (int i = 0; i < NDT; ++i) oacc[i] = zero16();
@@ -427,19 +438,31 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_fast(FwdArgs a) {
     for (int t = 0; t < ntiles; ++t) {
         const bf16* Kb = smem + (t & 1) * 2 * TILE;
         const bf16* Vb = Kb + TILE;
-        if (t + 1 < ntiles) {
-            lds_barrier();  // every wave is done with the buffer tile t+1 reuses
-            bf16* nb = smem + ((t + 1) & 1) * 2 * TILE;
-            issue_tile<DP, BN, NT, SWZ_ROW>(K, (t + 1) * BN, S, D, nb);
-            issue_tile<DP, BN, NT, SWZ_TR>(Vg, (t + 1) * BN, S, D, nb + TILE);
-            lds_barrier_vm<LOADS>();  // tile t has landed (all waves), tile t+1 in flight
-        } else {
-            lds_barrier_vm<0>();
-        }
+        // This wave's loads of tile t (issued one tile ago) have landed; after
+        // the barrier every wave's have, and every wave is done with the
+        // buffer tile t+1 streams into.
+        wait_vmcnt<0>();
+        lds_barrier();
+        // Next tile's loads, spread over this tile's S^T steps; the last
+        // tile re-loads tile 0 into the idle buffer (no branch in the
+        // schedule; waited for before the end).
+        bf16* const nb = smem + ((t + 1) & 1) * 2 * TILE;
+        const int nrow = t + 1 < ntiles ? (t + 1) * BN : 0;
+        auto issue_part = [&](int j) {
+            if (j < FwdLoads<DP>::PER)
+                issue_tile_part<DP, BN, NT, SWZ_ROW>(K, nrow, S, D, nb, j);
+            else
+                issue_tile_part<DP, BN, NT, SWZ_TR>(Vg, nrow, S, D, nb + TILE, j - FwdLoads<DP>::PER);
+        };
         const int kbase = t * BN;
-        if (wrow0 >= S || (CAUSAL && kbase > wrow0 + 31)) continue;
-        fwd_fast_tile<DP, CAUSAL>(a, Kb, Vb, kbase, wrow0, row, qf, oacc, m_run, l_run);
+        if (wave_uniform(!(wrow0 >= S || (CAUSAL && kbase > wrow0 + 31)))) {
+            fwd_fast_tile<DP, CAUSAL>(a, Kb, Vb, kbase, wrow0, row, qf, oacc, m_run, l_run, issue_part);
+        } else {
+#pragma unroll
+            for (int j = 0; j < FwdLoads<DP>::NPARTS; ++j) issue_part(j);
+        }
     }
+    wait_vmcnt<0>();
 
     if (wrow0 >= S) return;
     const float l_tot = l_run + other_half(l_run);
@@ -453,7 +476,6 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
     constexpr int BN = kFwdBN, BM = kFwdBM, NT = 256;
     constexpr int CPR = DP / 8, NC = DP / 16, NDT = DP / 32;
     constexpr int TILE = BN * DP;
-    constexpr int LOADS = 2 * BN * CPR / NT;
     __shared__ __attribute__((aligned(1024))) bf16 smem[2 * 2 * TILE];
 
     const int tid = threadIdx.x;
@@ -495,6 +517,7 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
     int64_t qstart = fast_q_start(S, CAUSAL, qt);
     int qn = fast_q_n(S, CAUSAL, qt);
     fwd_load_q<DP>(Q, qt * BM + 32 * w + n, S, D, qf);
+    wait_vmcnt<0>();  // Q complete before the loop (direct loads are untracked)
 
     for (int i = 0, first = 1;; first = 0) {
 #pragma unroll
@@ -507,19 +530,23 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
         for (; i < seg_end; ++i) {
             const bf16* Kb = smem + (i & 1) * 2 * TILE;
             const bf16* Vb = Kb + TILE;
-            if (i + 1 < niter) {
-                lds_barrier();
-                bf16* nb = smem + ((i + 1) & 1) * 2 * TILE;
-                const int tn = next_key_tile();
-                issue_tile<DP, BN, NT, SWZ_ROW>(K, tn * BN, S, D, nb);
-                issue_tile<DP, BN, NT, SWZ_TR>(Vg, tn * BN, S, D, nb + TILE);
-                lds_barrier_vm<LOADS>();
-            } else {
-                lds_barrier_vm<0>();
-            }
+            wait_vmcnt<0>();  // as in attn_fwd_bf16_fast
+            lds_barrier();
+            bf16* const nb = smem + ((i + 1) & 1) * 2 * TILE;
+            const int nrow = i + 1 < niter ? next_key_tile() * BN : 0;
+            auto issue_part = [&](int j) {
+                if (j < FwdLoads<DP>::PER)
+                    issue_tile_part<DP, BN, NT, SWZ_ROW>(K, nrow, S, D, nb, j);
+                else
+                    issue_tile_part<DP, BN, NT, SWZ_TR>(Vg, nrow, S, D, nb + TILE, j - FwdLoads<DP>::PER);
+            };
             const int kbase = (int)(g0 + i - qstart) * BN;
-            if (!(wrow0 >= S || (CAUSAL && kbase > wrow0 + 31)))
-                fwd_fast_tile<DP, CAUSAL>(a, Kb, Vb, kbase, wrow0, row, qf, oacc, m_run, l_run);
+            if (wave_uniform(!(wrow0 >= S || (CAUSAL && kbase > wrow0 + 31)))) {
+                fwd_fast_tile<DP, CAUSAL>(a, Kb, Vb, kbase, wrow0, row, qf, oacc, m_run, l_run, issue_part);
+            } else {
+#pragma unroll
+                for (int j = 0; j < FwdLoads<DP>::NPARTS; ++j) issue_part(j);
+            }
         }
         // End of this unit's part of query tile qt: a tile inside one unit is
         // written normalised; otherwise this unit's slot gets the unnormalised
@@ -545,11 +572,15 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
                 }
             }
         }
-        if (i >= niter) break;
+        if (i >= niter) {
+            wait_vmcnt<0>();  // the last tile's re-load has landed before the unit ends
+            break;
+        }
         ++qt;
         qstart = fast_q_start(S, CAUSAL, qt);
         qn = fast_q_n(S, CAUSAL, qt);
         fwd_load_q<DP>(Q, qt * BM + 32 * w + n, S, D, qf);
+        wait_vmcnt<0>();
     }
 }
 
