@@ -576,13 +576,13 @@ BwdPlan plan_bwd_fast(const AttnShape& s) {
     const int S = (int)s.S, causal = s.causal ? 1 : 0, group = (int)(s.Hq / s.Hkv);
     const int nt = (S + 127) / 128;
     const int64_t n_kv = bwd::fast_kv_start(S, causal, group, nt);  // iterations per (batch, kv head)
-    const int64_t n_q = bwd::fast_q_start(S, causal, nt);           // iterations per (batch, query head)
+    const int64_t n_q = fast_q_total(S, causal);           // iterations per (batch, query head)
     const int64_t pairs_kv = s.B * s.Hkv, pairs_q = s.B * s.Hq;
     // The two roles run as separate launches: each is cut into about one
     // unit per CU (units no shorter than 8 iterations).
     const int cus = device_cus();
-    const int64_t u_kv = std::max<int64_t>(1, (cus + pairs_kv - 1) / pairs_kv);
-    const int64_t u_q = std::max<int64_t>(1, (cus + pairs_q - 1) / pairs_q);
+    const int64_t u_kv = balanced_units(pairs_kv, cus);
+    const int64_t u_q = balanced_units(pairs_q, cus);
     BwdPlan p;
     // Units no shorter than 8 iterations, and long enough that no tile spans
     // more than 63 units (REDUCE keeps a tile's slot list in LDS, 64 entries).

@@ -343,7 +343,7 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
     // This unit's chunk of the flattened (query tile, key tile) iterations.
     const int nqt = (S + BM - 1) / BM;
     const int64_t g0 = (int64_t)unit * a.q_chunk;
-    const int niter = (int)min((int64_t)a.q_chunk, fast_q_start(S, CAUSAL, nqt) - g0);
+    const int niter = (int)min((int64_t)a.q_chunk, fast_q_total(S, CAUSAL) - g0);
     int qt = 0;
     while (fast_q_start(S, CAUSAL, qt + 1) <= g0) ++qt;
     // Prefetch cursor: query tile and key tile of the next iteration to load.

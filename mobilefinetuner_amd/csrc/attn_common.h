@@ -145,7 +145,15 @@ typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
 // the next tile streams in.  The kernels order these loads themselves with
 // lds_barrier_vm (explicit vmcnt) and workgroup barriers.  Loads complete in
 // order, so the compiler's own vmcnt waits stay correct (they only become
-// more conservative).
+// more conservative).  An LDS DMA that reads M0 right after an SALU write of
+// M0 needs one wait state (the s_nop), which the compiler's hazard pass
+// cannot insert inside an asm block.
+__device__ __forceinline__ void load_lds_16(const void* gptr, void* lds_base) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds_base);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(m0)
+                 : "memory", "m0");
+}
+
 // Wave index in the workgroup as a wave-uniform (scalar) value, for LDS
 // addresses of the direct loads.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
@@ -154,11 +162,6 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 // if/else on it is a scalar branch, so a wave that skips a block does not
 // step through it with an empty exec mask (and vice versa).
 __device__ __forceinline__ bool wave_uniform(bool c) { return __builtin_amdgcn_readfirstlane((int)c) != 0; }
-
-__device__ __forceinline__ void load_lds_16(const void* gptr, void* lds_base) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds_base);
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(m0) : "memory", "m0");
-}
 
 // s_waitcnt vmcnt(n) with the other counters left unconstrained (gfx9
 // encoding: vmcnt low bits [3:0], high bits [15:14], expcnt [6:4], lgkmcnt [11:8]).

@@ -491,7 +491,7 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
     // This unit's chunk of the flattened (query tile, key tile) iterations.
     const int nqt = (S + BM - 1) / BM;
     const int64_t g0 = (int64_t)unit * a.chunk;
-    const int niter = (int)min((int64_t)a.chunk, fast_q_start(S, CAUSAL, nqt) - g0);
+    const int niter = (int)min((int64_t)a.chunk, fast_q_total(S, CAUSAL) - g0);
     int qt = 0;
     while (fast_q_start(S, CAUSAL, qt + 1) <= g0) ++qt;
     // Prefetch cursor: query tile and key tile of the next iteration to load.
@@ -724,9 +724,9 @@ int fwd_rows_per_block(const AttnShape&) { return 128; }
 FwdPlan plan_fwd_split(const AttnShape& s) {
     const int S = (int)s.S, causal = s.causal ? 1 : 0;
     const int nqt = (S + kFwdBM - 1) / kFwdBM;
-    const int64_t n = fast_q_start(S, causal, nqt);  // iterations per (batch, head)
+    const int64_t n = fast_q_total(S, causal);  // iterations per (batch, head)
     const int64_t pairs = s.B * s.Hq;
-    const int64_t u = std::max<int64_t>(1, (device_cus() + pairs - 1) / pairs);
+    const int64_t u = balanced_units(pairs, device_cus());
     FwdPlan p;
     // Units no shorter than 4 key tiles: a split costs one fp32 partial tile.
     // A query tile has at most 2*S/64 key tiles; keep its slots <= kCombMaxSlots.

@@ -31,6 +31,8 @@ SHAPES = [
     (2, 4, 1, 64, 200),
     (1, 2, 1, 640, 64),   # long enough that the bf16 backward splits query tiles over units
     (1, 4, 1, 1000, 256),  # Gemma-shaped, ragged: forward and backward split tiles over units
+    (1, 7, 1, 300, 128),   # partial last query tile (work totals must not count it as full)
+    (3, 5, 5, 129, 64),
 ]
 
 
