@@ -57,6 +57,11 @@ def lib():
         L.orc_attn_composite.argtypes = [_f32p, _f32p, _f32p, opt_f32,
                                          _i64, _i64, _i64, _i64, _i64, C.c_float, C.c_int,
                                          opt_f32, opt_f32, opt_f32, opt_f32, opt_f32]
+        L.orc_attn_composite_masked.restype = C.c_int
+        L.orc_attn_composite_masked.argtypes = [_f32p, _f32p, _f32p, opt_f32,
+                                                _i64, _i64, _i64, _i64, _i64, C.c_float, C.c_int,
+                                                opt_f32, opt_f32,
+                                                opt_f32, opt_f32, opt_f32, opt_f32, opt_f32]
         L.orc_attn_streaming.restype = C.c_int
         L.orc_attn_streaming.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64,
                                          C.c_float, C.c_int, _f32p]
@@ -193,6 +198,64 @@ def composite(q, k, v, dO=None, scale=None, causal=True, want_lse=False):
     return dict(o=o, lse=lse, dq=dq, dk=dk, dv=dv)
 
 
+# ------------------------------------------------------------------ masks
+MASK_VALUE = np.float32(-1e10)  # kMaskValue, graph/gemma_model.cpp:175
+
+
+def causal_mask(S):
+    """create_causal_mask (core/ops.cpp:2167-2180): -1e10 above the diagonal."""
+    m = np.zeros((S, S), np.float32)
+    m[np.triu_indices(S, 1)] = MASK_VALUE
+    return m
+
+
+def sliding_mask(S, window):
+    """GemmaModel::build_sliding_mask (graph/gemma_model.cpp:272-285): key j is
+    allowed for query i iff j <= i and i - j < window."""
+    i = np.arange(S)[:, None]
+    j = np.arange(S)[None, :]
+    allow = (j <= i) & (i - j < window)
+    return np.where(allow, np.float32(0), MASK_VALUE).astype(np.float32)
+
+
+def padding_mask(attention_mask):
+    """GemmaModel::build_padding_mask (graph/gemma_model.cpp:287-321) from a
+    [B,S] attention mask (float: <= 0.5 is padding; int32: 0 is padding);
+    returns the [B,S] additive mask (the [B,1,1,S] tensor without its unit dims)."""
+    am = np.asarray(attention_mask)
+    pad = am <= 0.5 if am.dtype.kind == "f" else am == 0
+    return np.where(pad, MASK_VALUE, np.float32(0)).astype(np.float32)
+
+
+def lengths_attention_mask(lengths, S):
+    """[B,S] int32 attention mask with the first lengths[b] tokens real."""
+    return (np.arange(S)[None, :] < np.asarray(lengths)[:, None]).astype(np.int32)
+
+
+def composite_masked(q, k, v, dO=None, scale=None, base_mask=None, pad_mask=None, causal=True,
+                     want_lse=False):
+    """Reference composite with additive masks: base_mask [S,S] (None: the
+    causal mask when causal) then pad_mask [B,S]."""
+    B, Hq, S, D = q.shape
+    Hkv = k.shape[1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    q, k, v = (np.ascontiguousarray(t, dtype=np.float32) for t in (q, k, v))
+    bm = None if base_mask is None else np.ascontiguousarray(base_mask, np.float32)
+    pm = None if pad_mask is None else np.ascontiguousarray(pad_mask, np.float32)
+    o = np.empty_like(q)
+    lse = np.empty((B, Hq, S), dtype=np.float32) if want_lse else None
+    dq = dk = dv = None
+    if dO is not None:
+        dO = np.ascontiguousarray(dO, dtype=np.float32)
+        dq, dk, dv = np.empty_like(q), np.empty_like(k), np.empty_like(v)
+    rc = lib().orc_attn_composite_masked(q, k, v, _ptr(dO), B, Hq, Hkv, S, D, float(scale), int(causal),
+                                         _ptr(bm), _ptr(pm), _ptr(o), _ptr(lse), _ptr(dq), _ptr(dk), _ptr(dv))
+    if rc != 0:
+        raise ValueError("orc_attn_composite_masked rejected its arguments")
+    return dict(o=o, lse=lse, dq=dq, dk=dk, dv=dv)
+
+
 def streaming(q, k, v, scale=None, causal=True):
     B, H, S, D = q.shape
     if scale is None:
@@ -260,6 +323,32 @@ def ref_composite(q, k, v, dO=None, scale=None, causal=True):
     if rc != 0:
         raise RuntimeError("reference composite raised")
     return dict(o=o, dq=dq, dk=dk, dv=dv, t_fwd=tf.value, t_bwd=tb.value, held_bytes=held.value)
+
+
+def ref_composite_masked(q, k, v, dO=None, scale=None, base_mask=None, pad_mask=None):
+    """The reference's composite with additive masks (ref_harness.cpp)."""
+    B, Hq, S, D = q.shape
+    Hkv = k.shape[1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    q, k, v = (np.ascontiguousarray(t, dtype=np.float32) for t in (q, k, v))
+    bm = None if base_mask is None else np.ascontiguousarray(base_mask, np.float32)
+    pm = None if pad_mask is None else np.ascontiguousarray(pad_mask, np.float32)
+    o = np.empty_like(q)
+    dq = dk = dv = None
+    if dO is not None:
+        dO = np.ascontiguousarray(dO, dtype=np.float32)
+        dq, dk, dv = np.empty_like(q), np.empty_like(k), np.empty_like(v)
+    R = ref()
+    R.mftref_composite_masked.restype = C.c_int
+    R.mftref_composite_masked.argtypes = [_f32p, _f32p, _f32p, C.c_void_p, _i64, _i64, _i64, _i64, _i64,
+                                          C.c_float, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                          C.c_void_p, C.c_void_p]
+    rc = R.mftref_composite_masked(q, k, v, _ptr(dO), B, Hq, Hkv, S, D, float(scale), _ptr(bm), _ptr(pm),
+                                   _ptr(o), _ptr(dq), _ptr(dk), _ptr(dv))
+    if rc != 0:
+        raise RuntimeError("reference composite (masked) raised")
+    return dict(o=o, dq=dq, dk=dk, dv=dv)
 
 
 def ref_memeff_nograd(q, k, v, scale=None, causal=True):

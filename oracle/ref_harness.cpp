@@ -104,6 +104,45 @@ int mftref_composite(const float* q, const float* k, const float* v, const float
     }
 }
 
+// The composite with explicit additive masks, as graph/gemma_model.cpp:481-505
+// applies them: scores = add(scores, base_mask [S,S]) (causal or sliding
+// window), then add(scores, pad_mask [B,1,1,S]).  Either mask may be NULL.
+int mftref_composite_masked(const float* q, const float* k, const float* v, const float* dO,
+                            int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
+                            float scale, const float* base_mask, const float* pad_mask,
+                            float* o, float* dq, float* dk, float* dv) {
+    try {
+        const bool grad = dO != nullptr;
+        auto qt = from_host(q, {B, Hq, S, D}, grad);
+        auto kt = from_host(k, {B, Hkv, S, D}, grad);
+        auto vt = from_host(v, {B, Hkv, S, D}, grad);
+        TensorPtr gt;
+        if (grad) gt = from_host(dO, {B, Hq, S, D}, false);
+        TensorPtr k_use = kt, v_use = vt;
+        if (Hq != Hkv) {
+            const int rep = static_cast<int>(Hq / Hkv);
+            k_use = repeat_kv_heads(kt, rep);
+            v_use = repeat_kv_heads(vt, rep);
+        }
+        auto scores = mul(matmul(qt, transpose(k_use, 2, 3)), scale);
+        if (base_mask) scores = add(scores, from_host(base_mask, {S, S}, false));
+        if (pad_mask) scores = add(scores, from_host(pad_mask, {B, 1, 1, S}, false));
+        auto out = matmul(softmax(scores, -1), v_use);
+        to_host(out, o);
+        if (grad) {
+            autograd::Engine::instance().run_backward({out}, {gt});
+            to_host(qt->grad(), dq);
+            to_host(kt->grad(), dk);
+            to_host(vt->grad(), dv);
+        }
+        autograd::Engine::instance().clear_graph();
+        return 0;
+    } catch (const std::exception& e) {
+        std::cerr << "[mftref_composite_masked] " << e.what() << std::endl;
+        return -1;
+    }
+}
+
 // ops::memory_efficient_attention with no input requiring grad: the
 // reference's streaming path (core/memory_efficient_attention.cpp:110-200).
 int mftref_memeff_nograd(const float* q, const float* k, const float* v,

@@ -136,6 +136,14 @@ int orc_attn_composite(const float* q, const float* k, const float* v, const flo
                        int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
                        float scale, int causal,
                        float* o, float* lse, float* dq, float* dk, float* dv) {
+    return orc_attn_composite_masked(q, k, v, dO, B, Hq, Hkv, S, D, scale, causal, nullptr, nullptr, o, lse, dq,
+                                     dk, dv);
+}
+
+int orc_attn_composite_masked(const float* q, const float* k, const float* v, const float* dO,
+                              int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
+                              float scale, int causal, const float* base_mask, const float* pad_mask,
+                              float* o, float* lse, float* dq, float* dk, float* dv) {
     if (!q || !k || !v || B <= 0 || Hq <= 0 || Hkv <= 0 || S <= 0 || D <= 0) return -1;
     if (Hq % Hkv != 0) return -1;
     const int64_t r = Hq / Hkv;
@@ -161,10 +169,20 @@ int orc_attn_composite(const float* q, const float* k, const float* v, const flo
             // scores = mul(matmul(q, transpose(k, 2, 3)), scale) [+ causal mask]
             transpose2d(K, kt.data(), S, D);
             mm_nn(Q, kt.data(), sc.data(), S, S, D);
+            // Additive masks, one float add each as the reference graphs apply
+            // them (graph/gemma_model.cpp:494-499): the [S,S] base mask
+            // (causal: create_causal_mask, core/ops.cpp:2167-2180; or any
+            // given one, e.g. build_sliding_mask, graph/gemma_model.cpp:272-285),
+            // then the [B,1,1,S] padding mask (build_padding_mask, :287-321).
+            const float* pm = pad_mask ? pad_mask + b * S : nullptr;
             for (int64_t i = 0; i < S; ++i) {
                 for (int64_t j = 0; j < S; ++j) {
                     float x = sc[i * S + j] * scale;
-                    if (causal) x = x + (j > i ? -1e10f : 0.0f);
+                    if (base_mask)
+                        x = x + base_mask[i * S + j];
+                    else if (causal)
+                        x = x + (j > i ? -1e10f : 0.0f);
+                    if (pm) x = x + pm[j];
                     sc[i * S + j] = x;
                 }
             }

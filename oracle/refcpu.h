@@ -64,6 +64,14 @@ int orc_attn_composite(const float* q, const float* k, const float* v, const flo
                        float scale, int causal,
                        float* o, float* lse, float* dq, float* dk, float* dv);
 
+// The same with explicit additive masks (either may be NULL): base_mask
+// [S,S] replaces the causal mask, pad_mask [B,S] is added after it
+// (graph/gemma_model.cpp:494-499).
+int orc_attn_composite_masked(const float* q, const float* k, const float* v, const float* dO,
+                              int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
+                              float scale, int causal, const float* base_mask, const float* pad_mask,
+                              float* o, float* lse, float* dq, float* dk, float* dv);
+
 /* The no-grad streaming path of ops::memory_efficient_attention
  * (core/memory_efficient_attention.cpp:110-200): double sum_exp, float
  * inv_sum, float context accumulation.  MHA only (Hq == Hkv), as there. */

@@ -227,3 +227,45 @@ def test_lse_is_log_normaliser(orc):
     assert np.allclose(r["lse"][0, 0], lse, atol=1e-5)
     p = np.exp(s - lse[:, None])
     assert np.allclose(p @ v[0, 0], r["o"][0, 0], atol=1e-5)
+
+
+# ------------------------------------------------- masks (widened path)
+@pytest.mark.parametrize("window,lengths", [(5, None), (None, [40, 23]), (16, [40, 40]), (1, None), (64, None)])
+def test_masked_composite_equals_live_reference(orc, window, lengths):
+    """Sliding-window (build_sliding_mask) and padding (build_padding_mask)
+    masks added as the Gemma graph adds them (graph/gemma_model.cpp:494-499)."""
+    _need_ref(orc)
+    B, Hq, Hkv, S, D = 2, 4, 2, 40, 16
+    q, k, v, dO = orc.make_inputs(B, Hq, Hkv, S, D, 71, "f32", 0.5)
+    base = orc.sliding_mask(S, window) if window else orc.causal_mask(S)
+    pad = orc.padding_mask(orc.lengths_attention_mask(lengths, S)) if lengths else None
+    a = orc.composite_masked(q, k, v, dO, scale=0.25, base_mask=base, pad_mask=pad)
+    b = orc.ref_composite_masked(q, k, v, dO, scale=0.25, base_mask=base, pad_mask=pad)
+    for t in ("o", "dq", "dk", "dv"):
+        assert np.array_equal(_bits(a[t]), _bits(b[t])), t
+
+
+def test_mask_builders_and_invariants(orc):
+    S = 12
+    # the causal mask is the sliding mask with a window of S or more
+    assert np.array_equal(orc.sliding_mask(S, S), orc.causal_mask(S))
+    assert np.array_equal(orc.sliding_mask(S, 1000), orc.causal_mask(S))
+    # float and int32 attention masks give the same padding mask
+    am = orc.lengths_attention_mask([5, 12], S)
+    assert np.array_equal(orc.padding_mask(am), orc.padding_mask(am.astype(np.float32)))
+    assert orc.padding_mask(am)[0, 4] == 0 and orc.padding_mask(am)[0, 5] == orc.MASK_VALUE
+    q, k, v, dO = orc.make_inputs(1, 2, 2, S, 8, 3, "f32", 0.5)
+    # window 1: each query sees only itself, O_i = V_i
+    r = orc.composite_masked(q, k, v, dO, scale=0.3, base_mask=orc.sliding_mask(S, 1))
+    assert np.array_equal(r["o"], v)
+    # the causal path through the masked entry point is the plain composite
+    a = orc.composite_masked(q, k, v, dO, scale=0.3, base_mask=orc.causal_mask(S))
+    b = orc.composite(q, k, v, dO, scale=0.3, causal=True)
+    for t in ("o", "dq", "dk", "dv"):
+        assert np.array_equal(a[t], b[t]), t
+    # padded keys get no gradient and no weight when every row sees a real key
+    pad = orc.padding_mask(orc.lengths_attention_mask([7], S))
+    r = orc.composite_masked(q, k, v, dO, scale=0.3, pad_mask=pad)
+    assert np.all(r["dk"][0, :, 7:] == 0) and np.all(r["dv"][0, :, 7:] == 0)
+    ref7 = orc.composite(q[:, :, :7], k[:, :, :7], v[:, :, :7], dO[:, :, :7], scale=0.3, causal=True)
+    assert np.allclose(r["o"][:, :, :7], ref7["o"], atol=1e-6)
