@@ -66,7 +66,25 @@ typedef struct {
     int32_t causal;           /* 1: key j visible to query i iff j <= i (the -1e10
                                  mask of core/ops.cpp:2167-2180); 0: all visible      */
     mft_dtype dtype;          /* element type of q, k, v, o, dO                        */
+    int32_t window;           /* > 0 (needs causal = 1): also i - j < window, the
+                                 Gemma sliding mask (graph/gemma_model.cpp:272-285,
+                                 config sliding_window); 0: no window.  A window
+                                 >= S is the plain causal mask.                       */
+    const int32_t* kv_len;    /* NULL, or device int32 [B]: keys j >= kv_len[b] are
+                                 hidden in batch b, the padding mask of an
+                                 attention_mask that is 1 on the first kv_len[b]
+                                 positions (graph/gemma_model.cpp:287-320,
+                                 graph/qwen_model.cpp:338-353; the datasets pad on
+                                 the right, data/wikitext2_dataset.cpp:461-500).
+                                 Values are clamped to [0, S].                        */
 } mft_attn_desc;
+
+/* Rows with no visible key.  With kv_len a query row can see no key (every
+ * row when kv_len[b] = 0; with a window, rows i >= kv_len[b] + window - 1).
+ * The reference's -1e10 masks then leave a uniform softmax over the keys
+ * hidden by exactly one of its two masks; o, and the gradients, follow that
+ * (see mobilefinetuner_amd/csrc/attn_masked_rows.hip), and lse is +inf for
+ * such rows. */
 
 /* Workspace bytes of the calls.
  *   fwd: fp32 partial output tiles of query tiles whose key range is split
@@ -78,7 +96,7 @@ typedef struct {
 mft_status mft_attn_workspace_size(const mft_attn_desc* desc, size_t* fwd_bytes,
                                    size_t* bwd_bytes);
 
-/* Forward: o = softmax(scale * q k^T [causal]) v, and lse.
+/* Forward: o = softmax(scale * q k^T [masks]) v, and lse.
  * Replaces the composite forward / memory_efficient_attention
  * (core/memory_efficient_attention.cpp:73-203 and :23-43).
  * lse may be NULL when no backward will follow (no-grad path).
@@ -101,7 +119,8 @@ mft_status mft_attn_bwd(const mft_attn_desc* desc, const void* q, const void* k,
  *   DELTA : per-row softmax terms (delta_i = dO_i . O_i) into the workspace
  *   DKDV  : dK and dV (one launch)
  *   DQ    : dQ (one launch)
- *   REDUCE: sums the fp32 partials of tiles split across work units
+ *   REDUCE: sums the fp32 partials of tiles split across work units, and
+ *           with kv_len writes the terms of rows with no visible key
  * MAIN = DKDV | DQ.  mft_attn_bwd == mft_attn_bwd_stage(MFT_BWD_ALL).
  * Callers may run the stages separately on one stream, DELTA first and REDUCE
  * last (e.g. to time them, or to start DELTA early); later stages read what

@@ -24,41 +24,49 @@ def _check(t: torch.Tensor, name: str) -> None:
         raise ValueError(f"{name} must be contiguous")
 
 
-def _desc(q, k, scale, causal):
+def _desc(q, k, scale, causal, window=0, kv_len=None):
+    """kv_len: None or an int32 [B] GPU tensor of valid keys per batch (key padding)."""
     if q.dtype not in _DT:
         raise ValueError(f"unsupported dtype {q.dtype}")
     B, Hq, S, D = q.shape
-    return capi.desc(B, Hq, k.shape[1], S, D, scale, causal, _DT[q.dtype])
+    lp = None
+    if kv_len is not None:
+        if not kv_len.is_cuda or kv_len.dtype != torch.int32 or kv_len.shape != (B,) or not kv_len.is_contiguous():
+            raise ValueError("kv_len must be a contiguous int32 GPU tensor of shape [B]")
+        lp = kv_len.data_ptr()
+    return capi.desc(B, Hq, k.shape[1], S, D, scale, causal, _DT[q.dtype], window, lp)
 
 
 def _stream():
     return torch.cuda.current_stream().cuda_stream
 
 
-def workspace_bytes(q, k, scale=-1.0, causal=True):
+def workspace_bytes(q, k, scale=-1.0, causal=True, window=0, kv_len=None):
     """Backward workspace bytes."""
-    return capi.workspace_size(_desc(q, k, scale, causal))[1]
+    return capi.workspace_size(_desc(q, k, scale, causal, window, kv_len))[1]
 
 
-def fwd_workspace_bytes(q, k, scale=-1.0, causal=True):
+def fwd_workspace_bytes(q, k, scale=-1.0, causal=True, window=0, kv_len=None):
     """Forward workspace bytes (0 when the forward needs none)."""
-    return capi.workspace_size(_desc(q, k, scale, causal))[0]
+    return capi.workspace_size(_desc(q, k, scale, causal, window, kv_len))[0]
 
 
 def attention_forward(q, k, v, scale: float = -1.0, causal: bool = True, want_lse: bool = True,
-                      workspace=None, balanced: bool = True):
+                      workspace=None, balanced: bool = True, window: int = 0, kv_len=None):
     """o, lse = fused attention forward (lse None when want_lse is False).
 
     balanced=True passes the forward workspace (allocated here unless given),
     which selects the launch that splits long query tiles across work units;
-    balanced=False passes none (one workgroup per query tile)."""
+    balanced=False passes none (one workgroup per query tile).  window > 0:
+    causal sliding window of that many keys; kv_len: int32 [B] GPU tensor of
+    valid (unpadded) keys per batch."""
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
         _check(t, n)
     if k.dtype != q.dtype or v.dtype != q.dtype or k.shape != v.shape:
         raise ValueError("q, k, v must share dtype and k, v must have equal shapes")
     if k.shape[0] != q.shape[0] or k.shape[2:] != q.shape[2:]:
         raise ValueError("k/v must be [B, Hkv, S, D] with q's B, S, D")
-    d = _desc(q, k, scale, causal)
+    d = _desc(q, k, scale, causal, window, kv_len)
     o = torch.empty_like(q)
     lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device) if want_lse else None
     ws_ptr = None
@@ -73,14 +81,15 @@ def attention_forward(q, k, v, scale: float = -1.0, causal: bool = True, want_ls
     return o, lse
 
 
-def attention_backward(q, k, v, o, dO, lse, scale: float = -1.0, causal: bool = True, workspace=None):
+def attention_backward(q, k, v, o, dO, lse, scale: float = -1.0, causal: bool = True, workspace=None,
+                       window: int = 0, kv_len=None):
     """dq, dk, dv (fp32; dk, dv already summed over the GQA group)."""
     for t, n in ((q, "q"), (k, "k"), (v, "v"), (o, "o"), (dO, "dO"), (lse, "lse")):
         if not t.is_cuda or not t.is_contiguous():
             raise ValueError(f"{n} must be a contiguous GPU tensor")
     if dO.dtype != q.dtype or o.dtype != q.dtype or lse.dtype != torch.float32:
         raise ValueError("o and dO must have q's dtype; lse must be float32")
-    d = _desc(q, k, scale, causal)
+    d = _desc(q, k, scale, causal, window, kv_len)
     nbytes = capi.workspace_size(d)[1]
     if workspace is None or workspace.numel() < nbytes:
         workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
@@ -117,14 +126,15 @@ class FusedAttention(torch.autograd.Function):
     """Autograd node that saves only q, k, v, o and the row log-sum-exp."""
 
     @staticmethod
-    def forward(ctx, q, k, v, scale=-1.0, causal=True):
-        o, lse = attention_forward(q, k, v, scale, causal)
+    def forward(ctx, q, k, v, scale=-1.0, causal=True, window=0, kv_len=None):
+        o, lse = attention_forward(q, k, v, scale, causal, window=window, kv_len=kv_len)
         ctx.save_for_backward(q, k, v, o, lse)
-        ctx.scale, ctx.causal = scale, causal
+        ctx.scale, ctx.causal, ctx.window, ctx.kv_len = scale, causal, window, kv_len
         return o
 
     @staticmethod
     def backward(ctx, dO):
         q, k, v, o, lse = ctx.saved_tensors
-        dq, dk, dv = attention_backward(q, k, v, o, dO.contiguous().to(q.dtype), lse, ctx.scale, ctx.causal)
-        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None
+        dq, dk, dv = attention_backward(q, k, v, o, dO.contiguous().to(q.dtype), lse, ctx.scale, ctx.causal,
+                                        window=ctx.window, kv_len=ctx.kv_len)
+        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None

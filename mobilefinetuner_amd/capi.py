@@ -28,6 +28,7 @@ class AttnDesc(C.Structure):
     _fields_ = [
         ("B", C.c_int64), ("Hq", C.c_int64), ("Hkv", C.c_int64), ("S", C.c_int64), ("D", C.c_int64),
         ("scale", C.c_float), ("causal", C.c_int32), ("dtype", C.c_int32),
+        ("window", C.c_int32), ("kv_len", C.c_void_p),
     ]
 
 
@@ -63,7 +64,7 @@ def lib():
     L.mft_repeat_kv_fwd.argtypes = [vp, vp, i64, i64, i64, i64, i64, C.c_int32, vp]
     L.mft_repeat_kv_bwd.restype = C.c_int
     L.mft_repeat_kv_bwd.argtypes = [vp, vp, i64, i64, i64, i64, i64, vp]
-    if L.mft_version() != 1:
+    if L.mft_version() != 2:
         raise RuntimeError("libmft_attn.so version mismatch")
     _lib = L
     return L
@@ -74,8 +75,10 @@ def check(status: int) -> None:
         raise MftError(status, lib().mft_last_error().decode())
 
 
-def desc(B, Hq, Hkv, S, D, scale=-1.0, causal=True, dtype=MFT_BF16) -> AttnDesc:
-    return AttnDesc(int(B), int(Hq), int(Hkv), int(S), int(D), float(scale), int(bool(causal)), int(dtype))
+def desc(B, Hq, Hkv, S, D, scale=-1.0, causal=True, dtype=MFT_BF16, window=0, kv_len=None) -> AttnDesc:
+    """kv_len: device address of an int32 [B] array of valid keys per batch, or None."""
+    return AttnDesc(int(B), int(Hq), int(Hkv), int(S), int(D), float(scale), int(bool(causal)), int(dtype),
+                    int(window), kv_len)
 
 
 def workspace_size(d: AttnDesc):

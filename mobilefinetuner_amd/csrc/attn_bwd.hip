@@ -109,13 +109,16 @@ __device__ __forceinline__ void dkdv_bf16_body(const BwdArgs& a, char* smem, int
         dv[i] = zero16();
     }
 
+    const KeyVis vis = key_vis(a, b, CAUSAL);
+    // Causal: rows from the first key on; window: up to the last key + W - 1.
     const int qstart = CAUSAL ? j0 : 0;
+    const int qend = (CAUSAL && a.window > 0) ? min(S, j0 + BNK - 1 + a.window) : S;
     for (int h = h_begin; h < h_end; ++h) {
         const bf16* Q = (const bf16*)a.q + (int64_t)(b * a.Hq + h) * S * D;
         const bf16* G = (const bf16*)a.dO + (int64_t)(b * a.Hq + h) * S * D;
         const float* lse = a.lse + (int64_t)(b * a.Hq + h) * S;
         const float* dl = a.delta + (int64_t)(b * a.Hq + h) * S;
-        for (int qb = qstart; qb < S; qb += 32) {
+        for (int qb = qstart; qb < qend; qb += 32) {
             __syncthreads();
             {   // stage 32 query rows: row-major and transposed (4 rows x 8 columns per item)
                 constexpr int DG = DP / 8;
@@ -146,8 +149,9 @@ __device__ __forceinline__ void dkdv_bf16_body(const BwdArgs& a, char* smem, int
                 }
             }
             __syncthreads();
-            if (wkey0 >= S) continue;                  // no valid keys in this wave
-            if (CAUSAL && qb + 31 < wkey0) continue;   // every query precedes every key
+            if (wkey0 >= S) continue;  // no valid keys in this wave
+            // no row of the block sees a key of this wave
+            if (!vis.any(qb, min(qb + 31, S - 1), wkey0, min(wkey0 + 31, S - 1))) continue;
 
             f32x16 s = zero16(), dp = zero16();
 #pragma unroll
@@ -158,7 +162,7 @@ __device__ __forceinline__ void dkdv_bf16_body(const BwdArgs& a, char* smem, int
                 dp = mfma_bf16(ga, vf[c], dp);
             }
             // lane column n = key; register r = query qb + row_of_reg(r, hh)
-            const bool need_mask = CAUSAL && qb < wkey0 + 31;
+            const bool need_mask = !vis.all(qb, qb + 31, wkey0, wkey0 + 31);
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const f32x4 l4 = *reinterpret_cast<const f32x4*>(Ls + 8 * g + 4 * hh);
@@ -167,7 +171,7 @@ __device__ __forceinline__ void dkdv_bf16_body(const BwdArgs& a, char* smem, int
                 for (int i = 0; i < 4; ++i) {
                     const int r = 4 * g + i;
                     float p = fast_exp2(s[r] * a.scale_log2 - l4[i]);
-                    if (need_mask && qb + 8 * g + 4 * hh + i < key) p = 0.f;
+                    if (need_mask && !vis.visible(qb + 8 * g + 4 * hh + i, key)) p = 0.f;
                     dp[r] = p * (dp[r] - d4[i]);
                     s[r] = p;
                 }
@@ -251,13 +255,15 @@ __device__ __forceinline__ void dkdv_f32_body(const BwdArgs& a, char* smem, int 
     const float* Kw = Ks + (32 * w + n) * STR;
     const float* Vw = Vs + (32 * w + n) * STR;
 
+    const KeyVis vis = key_vis(a, b, CAUSAL);
     const int qstart = CAUSAL ? j0 : 0;
+    const int qend = (CAUSAL && a.window > 0) ? min(S, j0 + BNK - 1 + a.window) : S;
     for (int h = h_begin; h < h_end; ++h) {
         const float* Q = (const float*)a.q + (int64_t)(b * a.Hq + h) * S * D;
         const float* G = (const float*)a.dO + (int64_t)(b * a.Hq + h) * S * D;
         const float* lse = a.lse + (int64_t)(b * a.Hq + h) * S;
         const float* dl = a.delta + (int64_t)(b * a.Hq + h) * S;
-        for (int qb = qstart; qb < S; qb += 32) {
+        for (int qb = qstart; qb < qend; qb += 32) {
             __syncthreads();
             {
                 constexpr int CPR = DP / 4;
@@ -277,7 +283,7 @@ __device__ __forceinline__ void dkdv_f32_body(const BwdArgs& a, char* smem, int 
             }
             __syncthreads();
             if (wkey0 >= S) continue;
-            if (CAUSAL && qb + 31 < wkey0) continue;
+            if (!vis.any(qb, min(qb + 31, S - 1), wkey0, min(wkey0 + 31, S - 1))) continue;
 
             f32x16 s = zero16(), dp = zero16();
 #pragma unroll
@@ -289,7 +295,7 @@ __device__ __forceinline__ void dkdv_f32_body(const BwdArgs& a, char* smem, int 
                 const f32x4 vb = *reinterpret_cast<const f32x4*>(Vw + 8 * c + 4 * hh);
                 dp = mfma_chunk(ga, vb, dp);
             }
-            const bool need_mask = CAUSAL && qb < wkey0 + 31;
+            const bool need_mask = !vis.all(qb, qb + 31, wkey0, wkey0 + 31);
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const f32x4 l4 = *reinterpret_cast<const f32x4*>(Ls + 8 * g + 4 * hh);
@@ -298,7 +304,7 @@ __device__ __forceinline__ void dkdv_f32_body(const BwdArgs& a, char* smem, int 
                 for (int i = 0; i < 4; ++i) {
                     const int r = 4 * g + i;
                     float p = fast_exp2(s[r] * a.scale_log2 - l4[i]);
-                    if (need_mask && qb + 8 * g + 4 * hh + i < key) p = 0.f;
+                    if (need_mask && !vis.visible(qb + 8 * g + 4 * hh + i, key)) p = 0.f;
                     dp[r] = p * (dp[r] - d4[i]);
                     s[r] = p;
                 }
@@ -366,9 +372,11 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int qt, in
 #pragma unroll
     for (int i = 0; i < NDT; ++i) dq[i] = zero16();
 
+    const KeyVis vis = key_vis(a, b, CAUSAL);
     const int kend = CAUSAL ? min(S, m0 + BM) : S;
     const int ntiles = (kend + BN - 1) / BN;
-    for (int t = 0; t < ntiles; ++t) {
+    const int t0 = (CAUSAL && a.window > 0) ? max(0, m0 - a.window + 1) / BN : 0;
+    for (int t = t0; t < ntiles; ++t) {
         const int kbase = t * BN;
         __syncthreads();
         {
@@ -400,9 +408,9 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int qt, in
             }
         }
         __syncthreads();
-        if (wrow0 >= S || (CAUSAL && kbase > wrow0 + 31)) continue;
+        if (wrow0 >= S || !vis.any(wrow0, min(wrow0 + 31, S - 1), kbase, kbase + BN - 1)) continue;
 
-        const bool need_mask = (CAUSAL && kbase + BN - 1 > wrow0) || (kbase + BN > S);
+        const bool need_mask = !vis.all(wrow0, wrow0 + 31, kbase, kbase + BN - 1);
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk) {
             f32x16 s = zero16(), dp = zero16();
@@ -417,10 +425,7 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int qt, in
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 float p = fast_exp2(s[r] * a.scale_log2 - lse2);
-                if (need_mask) {
-                    const int kr = kbase + 32 * kk + row_of_reg(r, hh);
-                    if (kr >= S || (CAUSAL && kr > row)) p = 0.f;
-                }
+                if (need_mask && !vis.visible(row, kbase + 32 * kk + row_of_reg(r, hh))) p = 0.f;
                 s[r] = p * (dp[r] - dlt);
             }
             if constexpr (L::KT) {
@@ -573,10 +578,10 @@ int device_cus() {
 }
 
 BwdPlan plan_bwd_fast(const AttnShape& s) {
-    const int S = (int)s.S, causal = s.causal ? 1 : 0, group = (int)(s.Hq / s.Hkv);
+    const int S = (int)s.S, causal = s.causal ? 1 : 0, group = (int)(s.Hq / s.Hkv), W = s.window;
     const int nt = (S + 127) / 128;
-    const int64_t n_kv = bwd::fast_kv_start(S, causal, group, nt);  // iterations per (batch, kv head)
-    const int64_t n_q = fast_q_total(S, causal);           // iterations per (batch, query head)
+    const int64_t n_kv = bwd::fast_kv_start(S, causal, W, group, nt);  // iterations per (batch, kv head)
+    const int64_t n_q = fast_q_total(S, causal, W);                    // iterations per (batch, query head)
     const int64_t pairs_kv = s.B * s.Hkv, pairs_q = s.B * s.Hq;
     // The two roles run as separate launches: each is cut into about one
     // unit per CU (units no shorter than 8 iterations).
@@ -586,8 +591,13 @@ BwdPlan plan_bwd_fast(const AttnShape& s) {
     BwdPlan p;
     // Units no shorter than 8 iterations, and long enough that no tile spans
     // more than 63 units (REDUCE keeps a tile's slot list in LDS, 64 entries).
-    const int64_t kv_min = std::max<int64_t>(8, (bwd::fast_kv_n(S, causal, group, 0) + 60) / 61);
-    const int64_t q_min = std::max<int64_t>(8, (bwd::fast_q_n(S, causal, nt - 1) + 60) / 61);
+    int64_t kv_tile_max = 0, q_tile_max = 0;
+    for (int t = 0; t < nt; ++t) {
+        kv_tile_max = std::max<int64_t>(kv_tile_max, bwd::fast_kv_n(S, causal, W, group, t));
+        q_tile_max = std::max<int64_t>(q_tile_max, bwd::fast_q_n(S, causal, W, t));
+    }
+    const int64_t kv_min = std::max<int64_t>(8, (kv_tile_max + 60) / 61);
+    const int64_t q_min = std::max<int64_t>(8, (q_tile_max + 60) / 61);
     p.kv_chunk = (int)std::min<int64_t>(n_kv, std::max<int64_t>(kv_min, (n_kv + u_kv - 1) / u_kv));
     p.q_chunk = (int)std::min<int64_t>(n_q, std::max<int64_t>(q_min, (n_q + u_q - 1) / u_q));
     p.kv_units = (int)((n_kv + p.kv_chunk - 1) / p.kv_chunk);
@@ -595,10 +605,10 @@ BwdPlan plan_bwd_fast(const AttnShape& s) {
     p.kv_parts_max = p.q_parts_max = 1;
     for (int t = 0; t < nt; ++t) {
         p.kv_parts_max = std::max(p.kv_parts_max,
-                                  bwd::fast_slots(bwd::fast_kv_start(S, causal, group, t),
-                                                  bwd::fast_kv_n(S, causal, group, t), p.kv_chunk));
-        p.q_parts_max = std::max(p.q_parts_max, bwd::fast_slots(bwd::fast_q_start(S, causal, t),
-                                                                bwd::fast_q_n(S, causal, t), p.q_chunk));
+                                  bwd::fast_slots(bwd::fast_kv_start(S, causal, W, group, t),
+                                                  bwd::fast_kv_n(S, causal, W, group, t), p.kv_chunk));
+        p.q_parts_max = std::max(p.q_parts_max, bwd::fast_slots(bwd::fast_q_start(S, causal, W, t),
+                                                                bwd::fast_q_n(S, causal, W, t), p.q_chunk));
     }
     return p;
 }
@@ -624,7 +634,8 @@ BwdLayout bwd_layout(const AttnShape& s) {
         l.kv_part = splits > 1 ? up(sizeof(float) * 2 * splits * kv_elems) : 0;
         l.q_part = 0;
     }
-    l.total = l.stats + l.kv_part + l.q_part;
+    l.masked = masked_rows_workspace_bytes(s);
+    l.total = l.stats + l.kv_part + l.q_part + l.masked;
     return l;
 }
 
@@ -691,6 +702,8 @@ hipError_t launch_attn_bwd(const AttnShape& s, const void* q, const void* k, con
     a.vec_ok = (s.D % (s.bf16 ? 8 : 4)) == 0;
     a.vec4_ok = (s.D % 4) == 0;
     a.causal = s.causal ? 1 : 0;
+    a.window = s.window;
+    a.kv_len = s.kv_len;
     a.kv_part = part;
     a.q_part = lay.q_part ? reinterpret_cast<float*>(ws + lay.stats + lay.kv_part) : nullptr;
     a.q_part_stride = s.B * s.Hq * s.S * s.D;
@@ -703,7 +716,10 @@ hipError_t launch_attn_bwd(const AttnShape& s, const void* q, const void* k, con
     } else {
         a.kv_chunk = a.q_chunk = a.kv_units = a.q_units = 0;
     }
-    return s.bf16 ? launch_bwd_dispatch<bf16>(s, a, stages, st) : launch_bwd_dispatch<float>(s, a, stages, st);
+    const hipError_t e =
+        s.bf16 ? launch_bwd_dispatch<bf16>(s, a, stages, st) : launch_bwd_dispatch<float>(s, a, stages, st);
+    if (e != hipSuccess || !(stages & BWD_STAGE_REDUCE)) return e;
+    return launch_bwd_masked_rows(s, q, k, v, o, dO, dq, dk, dv, ws + lay.stats + lay.kv_part + lay.q_part, st);
 }
 
 }  // namespace mft

@@ -30,6 +30,8 @@ struct BwdArgs {
     int n_kv_blocks, n_q_blocks;
     float scale, scale_log2;
     int vec_ok, vec4_ok;
+    int window;         // causal sliding window, 0 = none
+    const int* kv_len;  // [B] valid keys per batch, or null
     // fast path work units (see BwdPlan)
     int causal;
     int kv_chunk, q_chunk, kv_units, q_units;  // iterations per unit, units per (batch, head)
@@ -40,12 +42,20 @@ struct BwdArgs {
 
 // Work geometry of the fast path (attn_geometry.h), shared with the forward.
 using ::mft::fast_kv_n;
+using ::mft::fast_kv_nqb;
 using ::mft::fast_kv_start;
 using ::mft::fast_nb;
+using ::mft::fast_q_lo;
 using ::mft::fast_q_n;
 using ::mft::fast_q_start;
+using ::mft::fast_q_total;
 using ::mft::fast_slots;
 using ::mft::split_slot;
+
+// Key visibility of batch b (see KeyVis).
+__device__ __forceinline__ KeyVis key_vis(const BwdArgs& a, int b, bool causal) {
+    return KeyVis{a.S, a.window, a.kv_len ? min(max(a.kv_len[b], 0), a.S) : a.S, causal};
+}
 
 // Output rows of dK / dV for a split.
 __device__ __forceinline__ void dkdv_out_rows(const BwdArgs& a, int b, int hk, int split, int key,

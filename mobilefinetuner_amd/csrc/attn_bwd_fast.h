@@ -74,7 +74,8 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
     const int i16 = lane & 15, nh = (lane >> 4) & 1;
-    const int S = a.S, D = a.D, G = a.group;
+    const int S = a.S, D = a.D, G = a.group, W = a.window;
+    const KeyVis vis = key_vis(a, b, CAUSAL);
     const bf16* K = (const bf16*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
     const bf16* Vg = (const bf16*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
 
@@ -82,18 +83,17 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
     // iterations; it may start inside one key tile and end inside a later one.
     const int nkt = (S + BNK - 1) / BNK;
     const int64_t g0 = (int64_t)unit * a.kv_chunk;
-    const int niter = (int)min((int64_t)a.kv_chunk, fast_kv_start(S, CAUSAL, G, nkt) - g0);
+    const int niter = (int)min((int64_t)a.kv_chunk, fast_kv_start(S, CAUSAL, W, G, nkt) - g0);
     int kt = 0;
-    while (fast_kv_start(S, CAUSAL, G, kt + 1) <= g0) ++kt;
+    while (fast_kv_start(S, CAUSAL, W, G, kt + 1) <= g0) ++kt;
 
     // Prefetch cursor of the next iteration to load: key tile, query head of
     // the group, query block (iterations of a key tile run head-major over
     // its nqb = fast_kv_n / G query blocks); advanced without divisions.
-    const int nb = fast_nb(S);
-    int pf_kt = kt, pf_nqb = CAUSAL ? nb - 4 * kt : nb;
+    int pf_kt = kt, pf_nqb = fast_kv_nqb(S, CAUSAL, W, kt);
     int pf_h, pf_qi;
     {
-        const int it0 = (int)(g0 - fast_kv_start(S, CAUSAL, G, kt));
+        const int it0 = (int)(g0 - fast_kv_start(S, CAUSAL, W, G, kt));
         pf_h = it0 / pf_nqb;
         pf_qi = it0 - pf_h * pf_nqb;
     }
@@ -115,7 +115,7 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
             if (++pf_h == G) {
                 pf_h = 0;
                 ++pf_kt;
-                pf_nqb = CAUSAL ? nb - 4 * pf_kt : nb;
+                pf_nqb = fast_kv_nqb(S, CAUSAL, W, pf_kt);
             }
         }
         const int64_t hoff = (int64_t)(b * a.Hq + h) * S * D;
@@ -174,8 +174,8 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
         dk[i] = zero16();
         dv[i] = zero16();
     }
-    int64_t kstart = fast_kv_start(S, CAUSAL, G, kt);
-    int kn = fast_kv_n(S, CAUSAL, G, kt);
+    int64_t kstart = fast_kv_start(S, CAUSAL, W, G, kt);
+    int kn = fast_kv_n(S, CAUSAL, W, G, kt);
 
     for (int i = 0, first = 1;; first = 0) {
       // Iterations of key tile kt inside this unit, then its dK/dV store.
@@ -199,8 +199,9 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
         cur_qb = pend.qb;
         const int wkey0 = kt * BNK + 32 * w;
         const int key = wkey0 + n;
-        // Waves whose keys are past S or all after this query block skip it.
-        if (wave_uniform(wkey0 < S && !(CAUSAL && qb + 31 < wkey0))) {
+        // Waves whose keys are past S, or none of which a row of this query
+        // block sees, skip it.
+        if (wave_uniform(wkey0 < S && vis.any(qb, min(qb + 31, S - 1), wkey0, min(wkey0 + 31, S - 1)))) {
         // S = Q K^T and dP = dO V^T, one chunk of both per step; the steps'
         // LDS operands (Q, dO and, with V_LDS, V) are read PF steps ahead.
         f32x16 s = zero16(), dp = zero16();
@@ -235,7 +236,9 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
             for (int j = NC; j < NPARTS; ++j) issue_part(pend, j);
         }
         // lane column n = key; register r = query qb + row_of_reg(r, hh)
-        const bool need_mask = CAUSAL && qb < wkey0 + 31;
+        const bool need_mask = wave_uniform(!vis.all(qb, qb + 31, wkey0, wkey0 + 31));
+        // this lane's key is seen by rows qb + [r_lo, r_hi)
+        const int r_lo = need_mask ? vis.rlo(key) - qb : -64, r_hi = need_mask ? vis.rhi(key) - qb : 64;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const f32x4 l4 = *reinterpret_cast<const f32x4*>(stt + 8 * g + 4 * hh);
@@ -244,7 +247,8 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
             for (int i = 0; i < 4; ++i) {
                 const int r = 4 * g + i;
                 float p = fast_exp2(s[r] * a.scale_log2 - l4[i]);
-                p = (need_mask && qb + 8 * g + 4 * hh + i < key) ? 0.f : p;
+                const int rr = 8 * g + 4 * hh + i;
+                p = (rr < r_lo || rr >= r_hi) ? 0.f : p;
                 dp[r] = p * (dp[r] - d4[i]);
                 s[r] = p;
             }
@@ -306,8 +310,8 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
           break;
       }
       ++kt;
-      kstart = fast_kv_start(S, CAUSAL, G, kt);
-      kn = fast_kv_n(S, CAUSAL, G, kt);
+      kstart = fast_kv_start(S, CAUSAL, W, G, kt);
+      kn = fast_kv_n(S, CAUSAL, W, G, kt);
 #pragma unroll
       for (int d = 0; d < NDT; ++d) {
           dk[d] = zero16();
@@ -333,7 +337,8 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
     const int i16 = lane & 15, nh = (lane >> 4) & 1;
     const int wu = wave_id();
-    const int S = a.S, D = a.D;
+    const int S = a.S, D = a.D, W = a.window;
+    const KeyVis vis = key_vis(a, b, CAUSAL);
     const int hk = h / a.group;
     const bf16* K = (const bf16*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
     const bf16* Vg = (const bf16*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
@@ -341,19 +346,21 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
     const bf16* G = (const bf16*)a.dO + (int64_t)(b * a.Hq + h) * S * D;
 
     // This unit's chunk of the flattened (query tile, key tile) iterations.
-    const int nqt = (S + BM - 1) / BM;
     const int64_t g0 = (int64_t)unit * a.q_chunk;
-    const int niter = (int)min((int64_t)a.q_chunk, fast_q_total(S, CAUSAL) - g0);
+    const int niter = (int)min((int64_t)a.q_chunk, fast_q_total(S, CAUSAL, W) - g0);
     int qt = 0;
-    while (fast_q_start(S, CAUSAL, qt + 1) <= g0) ++qt;
-    // Prefetch cursor: query tile and key tile of the next iteration to load.
-    int pf_qt = qt, pf_t = (int)(g0 - fast_q_start(S, CAUSAL, qt)), pf_n = fast_q_n(S, CAUSAL, qt);
+    while (fast_q_start(S, CAUSAL, W, qt + 1) <= g0) ++qt;
+    // Prefetch cursor: query tile and key tile of the next iteration to load
+    // (pf_t counts from the tile's first key tile pf_lo).
+    int pf_qt = qt, pf_t = (int)(g0 - fast_q_start(S, CAUSAL, W, qt)), pf_n = fast_q_n(S, CAUSAL, W, qt);
+    int pf_lo = fast_q_lo(CAUSAL, W, qt);
     auto next_key_tile = [&]() {
-        const int t = pf_t;
+        const int t = pf_lo + pf_t;
         if (++pf_t == pf_n) {
             ++pf_qt;
             pf_t = 0;
-            pf_n = fast_q_n(S, CAUSAL, pf_qt);
+            pf_n = fast_q_n(S, CAUSAL, W, pf_qt);
+            pf_lo = fast_q_lo(CAUSAL, W, pf_qt);
         }
         return t;
     };
@@ -378,8 +385,9 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
     };
     load_rows(qt);
     wait_vmcnt<0>();
-    int64_t qstart = fast_q_start(S, CAUSAL, qt);
-    int qn = fast_q_n(S, CAUSAL, qt);
+    int64_t qstart = fast_q_start(S, CAUSAL, W, qt);
+    int qn = fast_q_n(S, CAUSAL, W, qt);
+    int qlo = fast_q_lo(CAUSAL, W, qt);
 
     f32x16 dq[NDT];
 #pragma unroll
@@ -409,11 +417,10 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
             const int col = 8 * c < D ? 8 * c : 0;
             load_lds_16((v ? Vg : K) + (int64_t)gr * D + col, (v ? nbuf + TILE : nbuf) + m * 512);
         };
-        const int t = (int)(g0 + i - qstart);
-        const int kbase = t * BN;
+        const int kbase = (qlo + (int)(g0 + i - qstart)) * BN;
         const int wrow0 = qt * BM + 32 * w, row = wrow0 + n;
-        if (wave_uniform(!(wrow0 >= S || (CAUSAL && kbase > wrow0 + 31)))) {
-        const bool need_mask = (CAUSAL && kbase + BN - 1 > wrow0) || (kbase + BN > S);
+        if (wave_uniform(wrow0 < S && vis.any(wrow0, min(wrow0 + 31, S - 1), kbase, kbase + BN - 1))) {
+        const bool need_mask = wave_uniform(!vis.all(wrow0, wrow0 + 31, kbase, kbase + BN - 1));
 #pragma unroll 1
         for (int kk = 0; kk < NKK; ++kk) {
             f32x16 s = zero16(), dp = zero16();
@@ -442,12 +449,14 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
 #pragma unroll
                 for (int j = NI / 2; j < PER; ++j) issue_part(kk, j);
             }
-            // lane column n = query row; register r = key kbase + 32kk + row_of_reg(r, hh)
-            const int lim = need_mask ? (CAUSAL ? min(row, S - 1) : S - 1) - kbase - 32 * kk : 64;
+            // lane column n = query row; register r = key kbase + 32kk + row_of_reg(r, hh),
+            // visible iff lo <= row_of_reg(r, hh) <= hi
+            const int hi = need_mask ? vis.hi(row) - kbase - 32 * kk : 64;
+            const int lo = need_mask ? vis.lo(row) - kbase - 32 * kk : -1;
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
                 float p = fast_exp2(s[q] * a.scale_log2 - lse2);
-                p = row_of_reg(q, hh) > lim ? 0.f : p;
+                p = (row_of_reg(q, hh) > hi || row_of_reg(q, hh) < lo) ? 0.f : p;
                 s[q] = p * (dp[q] - dlt);
             }
             {
@@ -508,8 +517,9 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
           break;
       }
       ++qt;
-      qstart = fast_q_start(S, CAUSAL, qt);
-      qn = fast_q_n(S, CAUSAL, qt);
+      qstart = fast_q_start(S, CAUSAL, W, qt);
+      qn = fast_q_n(S, CAUSAL, W, qt);
+      qlo = fast_q_lo(CAUSAL, W, qt);
 #pragma unroll
       for (int d = 0; d < NDT; ++d) dq[d] = zero16();
       load_rows(qt);
@@ -574,8 +584,8 @@ __global__ __launch_bounds__(256) void attn_bwd_fast_reduce(BwdArgs a) {
     const bool kv = blk < kv_blocks;
     if (!kv) blk -= kv_blocks;
     const int rg = (int)(blk % RG), t = (int)((blk / RG) % nt), bh = (int)(blk / (RG * nt));
-    const int64_t start = kv ? fast_kv_start(S, CAUSAL, a.group, t) : fast_q_start(S, CAUSAL, t);
-    const int n = kv ? fast_kv_n(S, CAUSAL, a.group, t) : fast_q_n(S, CAUSAL, t);
+    const int64_t start = kv ? fast_kv_start(S, CAUSAL, a.window, a.group, t) : fast_q_start(S, CAUSAL, a.window, t);
+    const int n = kv ? fast_kv_n(S, CAUSAL, a.window, a.group, t) : fast_q_n(S, CAUSAL, a.window, t);
     const int64_t chunk = kv ? a.kv_chunk : a.q_chunk;
     const int nsl = fast_slots(start, n, chunk);
     const int r0 = t * 128 + rg * kRedRows;

@@ -40,6 +40,11 @@ mft_status check_desc(const mft_attn_desc* d, mft::AttnShape* s) {
         return fail(MFT_ERR_UNSUPPORTED, "mft_attn: batch/head grid dimensions too large");
     if (!(std::isfinite(d->scale)))
         return fail(MFT_ERR_INVALID_ARG, "mft_attn: scale must be finite");
+    if (d->window < 0) return fail(MFT_ERR_INVALID_ARG, "mft_attn: window must be >= 0");
+    if (d->window > 0 && !d->causal)
+        return fail(MFT_ERR_INVALID_ARG, "mft_attn: a sliding window needs causal = 1 (j <= i && i - j < window)");
+    if ((reinterpret_cast<uintptr_t>(d->kv_len) & 3u) != 0)
+        return fail(MFT_ERR_INVALID_ARG, "mft_attn: kv_len must be 4-byte aligned");
     s->B = d->B;
     s->Hq = d->Hq;
     s->Hkv = d->Hkv;
@@ -48,6 +53,9 @@ mft_status check_desc(const mft_attn_desc* d, mft::AttnShape* s) {
     s->scale = d->scale > 0.f ? d->scale : 1.0f / std::sqrt(static_cast<float>(d->D));
     s->causal = d->causal != 0;
     s->bf16 = d->dtype == MFT_BF16;
+    // A window of S or more keys hides nothing beyond the causal mask.
+    s->window = d->window < d->S ? d->window : 0;
+    s->kv_len = d->kv_len;
     return MFT_OK;
 }
 
@@ -63,7 +71,7 @@ mft_status hip_status(hipError_t e, const char* what) {
 
 extern "C" {
 
-int mft_version(void) { return 1; }
+int mft_version(void) { return 2; }
 
 const char* mft_last_error(void) { return g_last_error.c_str(); }
 

@@ -126,6 +126,30 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 __device__ __forceinline__ float other_half(float x) { return __shfl_xor(x, 32); }
 
+// Keys visible to query row i: [lo(i), hi(i)], the reference's additive masks
+// (-1e10 entries, core/ops.cpp:2167-2180 and the Gemma sliding / padding masks
+// of graph/gemma_model.cpp:272-320) as ranges:
+//   hi(i) = min(causal ? i : S - 1, len - 1)   causal mask, key padding
+//   lo(i) = W > 0 ? i - W + 1 : 0              causal sliding window of W keys
+// len = valid keys of the batch (S without padding).  Both bounds are
+// non-decreasing in i, so a block of rows and a block of keys either
+// certainly never meet (!any), certainly always meet (all), or need the
+// per-element mask.
+struct KeyVis {
+    int S, W, len;
+    bool causal;
+    __device__ __forceinline__ int hi(int i) const { return min(causal ? i : S - 1, len - 1); }
+    __device__ __forceinline__ int lo(int i) const { return W > 0 ? i - W + 1 : 0; }
+    __device__ __forceinline__ bool visible(int i, int j) const { return j <= hi(i) && j >= lo(i); }
+    // Some row of [r0, r1] may see some key of [k0, k1].
+    __device__ __forceinline__ bool any(int r0, int r1, int k0, int k1) const { return k0 <= hi(r1) && k1 >= lo(r0); }
+    // Every row of [r0, r1] sees every key of [k0, k1].
+    __device__ __forceinline__ bool all(int r0, int r1, int k0, int k1) const { return k1 <= hi(r0) && k0 >= lo(r1); }
+    // The rows that see key j: [rlo(j), rhi(j)) (none for a padding key).
+    __device__ __forceinline__ int rlo(int j) const { return j >= len ? (1 << 30) : (causal ? j : -(1 << 30)); }
+    __device__ __forceinline__ int rhi(int j) const { return W > 0 ? j + W : (1 << 30); }
+};
+
 // ---------------------------------------------------------------------------
 // LDS staging primitives of the bf16 fast path (gfx950).
 //

@@ -40,6 +40,8 @@ struct FwdArgs {
     float scale_log2;  // softmax scale * log2(e)
     int vec_ok;        // D % (16 bytes / element size) == 0
     int vec4_ok;       // D % 4 == 0
+    int window;              // causal sliding window, 0 = none
+    const int* kv_len;       // [B] valid keys per batch, or null
     // balanced launch (bf16 fast path with a workspace; see FwdPlan)
     int chunk;               // iterations per unit
     int units;               // units per (batch, head)
@@ -95,10 +97,13 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
     float m_run = -INFINITY;  // running row max, log2-scaled units
     float l_run = 0.f;        // running sum over this half-wave's keys
 
+    const KeyVis vis{S, a.window, a.kv_len ? min(max(a.kv_len[b], 0), S) : S, CAUSAL};
     const int kend = CAUSAL ? min(S, m0 + BM) : S;
     const int ntiles = (kend + BN - 1) / BN;
+    // The causal window reaches no key before m0 - W + 1.
+    const int t0 = (CAUSAL && a.window > 0) ? max(0, m0 - a.window + 1) / BN : 0;
 
-    for (int t = 0; t < ntiles; ++t) {
+    for (int t = t0; t < ntiles; ++t) {
         const int kbase = t * BN;
         __syncthreads();
         {   // stage K (row-major)
@@ -140,8 +145,9 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
         }
         __syncthreads();
 
-        // A wave with no valid rows, or whose rows all precede this tile, skips it.
-        if (wrow0 >= S || (CAUSAL && kbase > wrow0 + 31)) continue;
+        // A wave with no valid rows, or none of whose rows sees a key of this
+        // tile, skips it.
+        if (wrow0 >= S || !vis.any(wrow0, min(wrow0 + 31, S - 1), kbase, kbase + BN - 1)) continue;
 
         f32x16 s[NKK];
 #pragma unroll
@@ -154,7 +160,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
             }
         }
 
-        const bool need_mask = (CAUSAL && kbase + BN - 1 > wrow0) || (kbase + BN > S);
+        const bool need_mask = !vis.all(wrow0, wrow0 + 31, kbase, kbase + BN - 1);
         float mx = -INFINITY;
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk) {
@@ -163,7 +169,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
                 float x = s[kk][r];
                 if (need_mask) {
                     const int key = kbase + 32 * kk + row_of_reg(r, hh);
-                    if (key >= S || (CAUSAL && key > row)) x = -INFINITY;
+                    if (!vis.visible(row, key)) x = -INFINITY;
                 }
                 s[kk][r] = x;
                 mx = fmaxf(mx, x);
@@ -223,7 +229,9 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
     if (wrow0 >= S) return;
     const float l_tot = l_run + other_half(l_run);
     if (row >= S) return;
-    const float inv = 1.f / l_tot;
+    // A row that sees no key at all (key padding) gets O = 0 and LSE = +inf
+    // here; attn_fwd_masked_rows then writes the reference's output for it.
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     T* O = (T*)a.o + (int64_t)(b * a.Hq + h) * S * D + (int64_t)row * D;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
@@ -231,7 +239,8 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
         for (int g = 0; g < 4; ++g)
             store4<T>(O, 32 * dt + 8 * g + 4 * hh, D, oacc[dt][4 * g] * inv, oacc[dt][4 * g + 1] * inv,
                       oacc[dt][4 * g + 2] * inv, oacc[dt][4 * g + 3] * inv, a.vec4_ok != 0);
-    if (a.lse && hh == 0) a.lse[(int64_t)(b * a.Hq + h) * S + row] = (m_run + log2f(l_tot)) * kLn2;
+    if (a.lse && hh == 0)
+        a.lse[(int64_t)(b * a.Hq + h) * S + row] = l_tot > 0.f ? (m_run + log2f(l_tot)) * kLn2 : INFINITY;
 }
 
 // ---------------------------------------------------------------------------
@@ -264,10 +273,11 @@ template <int DP> struct FwdLoads {
 // One 64-key tile for this wave's 32 rows: S^T = K Q^T, online softmax with
 // lazy rescale, O^T += V^T P^T.  Kb/Vb: the tile in LDS.  issue_part(j),
 // j < FwdLoads<DP>::NPARTS, issues the next tile's loads; they are spread
-// over the S^T steps.
-template <int DP, bool CAUSAL, class IssuePart>
+// over the S^T steps.  need_mask (wave-uniform): some key of the tile is
+// hidden from some row; this lane's row sees keys [vlo, vhi].
+template <int DP, class IssuePart>
 __device__ __forceinline__ void fwd_fast_tile(const FwdArgs& a, const bf16* Kb, const bf16* Vb, int kbase,
-                                              int wrow0, int row, const bf16x8 (&qf)[DP / 16],
+                                              bool need_mask, int vlo, int vhi, const bf16x8 (&qf)[DP / 16],
                                               f32x16 (&oacc)[DP / 32], float& m_run, float& l_run,
                                               const IssuePart& issue_part) {
     constexpr int NPARTS = FwdLoads<DP>::NPARTS;
@@ -275,7 +285,6 @@ __device__ __forceinline__ void fwd_fast_tile(const FwdArgs& a, const bf16* Kb, 
     constexpr int PF = 4;  // LDS operand prefetch depth
     const int lane = threadIdx.x & 63, n = lane & 31, hh = lane >> 5;
     const int i16 = lane & 15, nh = (lane >> 4) & 1;
-    const int S = a.S;
 
     // S^T = K Q^T: the NKK independent accumulator chains are interleaved
     // and the K operands stream through a PF-deep register ring, so LDS
@@ -303,14 +312,17 @@ __device__ __forceinline__ void fwd_fast_tile(const FwdArgs& a, const bf16* Kb, 
         for (int j = NI / 2; j < NPARTS; ++j) issue_part(j);
     }
 
-    // Keys past `lim` (causal: this lane's row; always: S-1) are masked,
-    // as selects so the hot loop stays branch-free.
-    if ((CAUSAL && kbase + BN - 1 > wrow0) || (kbase + BN > S)) {
-        const int lim = (CAUSAL ? min(row, S - 1) : S - 1) - kbase;
+    // Keys outside [vlo, vhi] are masked, as selects so the hot loop stays
+    // branch-free.
+    if (need_mask) {
+        const int hi = vhi - kbase, lo = vlo - kbase;
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) s[kk][r] = 32 * kk + row_of_reg(r, hh) > lim ? -INFINITY : s[kk][r];
+            for (int r = 0; r < 16; ++r) {
+                const int kl = 32 * kk + row_of_reg(r, hh);
+                s[kk][r] = (kl > hi || kl < lo) ? -INFINITY : s[kk][r];
+            }
     }
     float mx = -INFINITY;
 #pragma unroll
@@ -386,12 +398,14 @@ __device__ __forceinline__ void fwd_load_q(const bf16* Q, int row, int S, int D,
     for (int c = 0; c < DP / 16; ++c) qf[c] = load_chunk<bf16>(Q + (int64_t)rowc * D, 16 * c + 8 * hh, D, row < S, true);
 }
 
-// Normalised O row and its LSE (rows < S; call with the wave's l_tot).
+// Normalised O row and its LSE (rows < S; call with the wave's l_tot).  A
+// row that sees no key (key padding) gets O = 0 and LSE = +inf here, and the
+// reference's output from attn_fwd_masked_rows.
 template <int DP>
 __device__ __forceinline__ void fwd_store_row(const FwdArgs& a, int b, int h, int row, const f32x16 (&oacc)[DP / 32],
                                               float m_run, float l_tot) {
     const int hh = (threadIdx.x & 63) >> 5;
-    const float inv = 1.f / l_tot;
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     bf16* O = (bf16*)a.o + (int64_t)(b * a.Hq + h) * a.S * a.D + (int64_t)row * a.D;
 #pragma unroll
     for (int dt = 0; dt < DP / 32; ++dt)
@@ -399,7 +413,8 @@ __device__ __forceinline__ void fwd_store_row(const FwdArgs& a, int b, int h, in
         for (int g = 0; g < 4; ++g)
             store4<bf16>(O, 32 * dt + 8 * g + 4 * hh, a.D, oacc[dt][4 * g] * inv, oacc[dt][4 * g + 1] * inv,
                          oacc[dt][4 * g + 2] * inv, oacc[dt][4 * g + 3] * inv, true);
-    if (a.lse && hh == 0) a.lse[(int64_t)(b * a.Hq + h) * a.S + row] = (m_run + log2f(l_tot)) * kLn2;
+    if (a.lse && hh == 0)
+        a.lse[(int64_t)(b * a.Hq + h) * a.S + row] = l_tot > 0.f ? (m_run + log2f(l_tot)) * kLn2 : INFINITY;
 }
 
 template <int DP, bool CAUSAL>
@@ -422,10 +437,12 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_fast(FwdArgs a) {
     const bf16* __restrict__ K = (const bf16*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
     const bf16* __restrict__ Vg = (const bf16*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
 
-    const int kend = CAUSAL ? min(S, m0 + BM) : S;
-    const int ntiles = (kend + BN - 1) / BN;
-    issue_tile<DP, BN, NT, SWZ_ROW>(K, 0, S, D, smem);
-    issue_tile<DP, BN, NT, SWZ_TR>(Vg, 0, S, D, smem + TILE);
+    const KeyVis vis{S, a.window, a.kv_len ? min(max(a.kv_len[b], 0), S) : S, CAUSAL};
+    const int vlo = vis.lo(row), vhi = vis.hi(row);
+    const int t0 = fast_q_lo(CAUSAL, a.window, qt);
+    const int ntiles = t0 + fast_q_n(S, CAUSAL, a.window, qt);
+    issue_tile<DP, BN, NT, SWZ_ROW>(K, t0 * BN, S, D, smem);
+    issue_tile<DP, BN, NT, SWZ_TR>(Vg, t0 * BN, S, D, smem + TILE);
 
     bf16x8 qf[NC];
     fwd_load_q<DP>(Q, row, S, D, qf);
@@ -435,8 +452,8 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_fast(FwdArgs a) {
     for (int i = 0; i < NDT; ++i) oacc[i] = zero16();
     float m_run = -INFINITY, l_run = 0.f;
 
-    for (int t = 0; t < ntiles; ++t) {
-        const bf16* Kb = smem + (t & 1) * 2 * TILE;
+    for (int t = t0; t < ntiles; ++t) {
+        const bf16* Kb = smem + ((t - t0) & 1) * 2 * TILE;
         const bf16* Vb = Kb + TILE;
         // This wave's loads of tile t (issued one tile ago) have landed; after
         // the barrier every wave's have, and every wave is done with the
@@ -446,8 +463,8 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_fast(FwdArgs a) {
         // Next tile's loads, spread over this tile's S^T steps; the last
         // tile re-loads tile 0 into the idle buffer (no branch in the
         // schedule; waited for before the end).
-        bf16* const nb = smem + ((t + 1) & 1) * 2 * TILE;
-        const int nrow = t + 1 < ntiles ? (t + 1) * BN : 0;
+        bf16* const nb = smem + ((t - t0 + 1) & 1) * 2 * TILE;
+        const int nrow = t + 1 < ntiles ? (t + 1) * BN : t0 * BN;
         auto issue_part = [&](int j) {
             if (j < FwdLoads<DP>::PER)
                 issue_tile_part<DP, BN, NT, SWZ_ROW>(K, nrow, S, D, nb, j);
@@ -455,8 +472,9 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_fast(FwdArgs a) {
                 issue_tile_part<DP, BN, NT, SWZ_TR>(Vg, nrow, S, D, nb + TILE, j - FwdLoads<DP>::PER);
         };
         const int kbase = t * BN;
-        if (wave_uniform(!(wrow0 >= S || (CAUSAL && kbase > wrow0 + 31)))) {
-            fwd_fast_tile<DP, CAUSAL>(a, Kb, Vb, kbase, wrow0, row, qf, oacc, m_run, l_run, issue_part);
+        if (wave_uniform(wrow0 < S && vis.any(wrow0, min(wrow0 + 31, S - 1), kbase, kbase + BN - 1))) {
+            const bool need_mask = wave_uniform(!vis.all(wrow0, wrow0 + 31, kbase, kbase + BN - 1));
+            fwd_fast_tile<DP>(a, Kb, Vb, kbase, need_mask, vlo, vhi, qf, oacc, m_run, l_run, issue_part);
         } else {
 #pragma unroll
             for (int j = 0; j < FwdLoads<DP>::NPARTS; ++j) issue_part(j);
@@ -488,20 +506,24 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
     const bf16* __restrict__ K = (const bf16*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
     const bf16* __restrict__ Vg = (const bf16*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
 
+    const int W = a.window;
+    const KeyVis vis{S, W, a.kv_len ? min(max(a.kv_len[b], 0), S) : S, CAUSAL};
     // This unit's chunk of the flattened (query tile, key tile) iterations.
-    const int nqt = (S + BM - 1) / BM;
     const int64_t g0 = (int64_t)unit * a.chunk;
-    const int niter = (int)min((int64_t)a.chunk, fast_q_total(S, CAUSAL) - g0);
+    const int niter = (int)min((int64_t)a.chunk, fast_q_total(S, CAUSAL, W) - g0);
     int qt = 0;
-    while (fast_q_start(S, CAUSAL, qt + 1) <= g0) ++qt;
-    // Prefetch cursor: query tile and key tile of the next iteration to load.
-    int pf_qt = qt, pf_t = (int)(g0 - fast_q_start(S, CAUSAL, qt)), pf_n = fast_q_n(S, CAUSAL, qt);
+    while (fast_q_start(S, CAUSAL, W, qt + 1) <= g0) ++qt;
+    // Prefetch cursor: query tile and key tile of the next iteration to load
+    // (pf_t counts from the tile's first key tile pf_lo).
+    int pf_qt = qt, pf_t = (int)(g0 - fast_q_start(S, CAUSAL, W, qt)), pf_n = fast_q_n(S, CAUSAL, W, qt);
+    int pf_lo = fast_q_lo(CAUSAL, W, qt);
     auto next_key_tile = [&]() {
-        const int t = pf_t;
+        const int t = pf_lo + pf_t;
         if (++pf_t == pf_n) {
             ++pf_qt;
             pf_t = 0;
-            pf_n = fast_q_n(S, CAUSAL, pf_qt);
+            pf_n = fast_q_n(S, CAUSAL, W, pf_qt);
+            pf_lo = fast_q_lo(CAUSAL, W, pf_qt);
         }
         return t;
     };
@@ -514,8 +536,9 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
     bf16x8 qf[NC];
     f32x16 oacc[NDT];
     float m_run, l_run;
-    int64_t qstart = fast_q_start(S, CAUSAL, qt);
-    int qn = fast_q_n(S, CAUSAL, qt);
+    int64_t qstart = fast_q_start(S, CAUSAL, W, qt);
+    int qn = fast_q_n(S, CAUSAL, W, qt);
+    int qlo = fast_q_lo(CAUSAL, W, qt);
     fwd_load_q<DP>(Q, qt * BM + 32 * w + n, S, D, qf);
     wait_vmcnt<0>();  // Q complete before the loop (direct loads are untracked)
 
@@ -525,6 +548,7 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
         m_run = -INFINITY;
         l_run = 0.f;
         const int wrow0 = qt * BM + 32 * w, row = wrow0 + n;
+        const int vlo = vis.lo(row), vhi = vis.hi(row);
         // Iterations of query tile qt inside this unit, then its output.
         const int seg_end = (int)min((int64_t)niter, qstart + qn - g0);
         for (; i < seg_end; ++i) {
@@ -540,9 +564,10 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
                 else
                     issue_tile_part<DP, BN, NT, SWZ_TR>(Vg, nrow, S, D, nb + TILE, j - FwdLoads<DP>::PER);
             };
-            const int kbase = (int)(g0 + i - qstart) * BN;
-            if (wave_uniform(!(wrow0 >= S || (CAUSAL && kbase > wrow0 + 31)))) {
-                fwd_fast_tile<DP, CAUSAL>(a, Kb, Vb, kbase, wrow0, row, qf, oacc, m_run, l_run, issue_part);
+            const int kbase = (qlo + (int)(g0 + i - qstart)) * BN;
+            if (wave_uniform(wrow0 < S && vis.any(wrow0, min(wrow0 + 31, S - 1), kbase, kbase + BN - 1))) {
+                const bool need_mask = wave_uniform(!vis.all(wrow0, wrow0 + 31, kbase, kbase + BN - 1));
+                fwd_fast_tile<DP>(a, Kb, Vb, kbase, need_mask, vlo, vhi, qf, oacc, m_run, l_run, issue_part);
             } else {
 #pragma unroll
                 for (int j = 0; j < FwdLoads<DP>::NPARTS; ++j) issue_part(j);
@@ -577,8 +602,9 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
             break;
         }
         ++qt;
-        qstart = fast_q_start(S, CAUSAL, qt);
-        qn = fast_q_n(S, CAUSAL, qt);
+        qstart = fast_q_start(S, CAUSAL, W, qt);
+        qn = fast_q_n(S, CAUSAL, W, qt);
+        qlo = fast_q_lo(CAUSAL, W, qt);
         fwd_load_q<DP>(Q, qt * BM + 32 * w + n, S, D, qf);
         wait_vmcnt<0>();
     }
@@ -601,8 +627,8 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(FwdArgs a) {
     const int S = a.S, D = a.D;
     const int nqt = (S + BM - 1) / BM;
     const int rg = (int)blockIdx.x % RG, qt = ((int)blockIdx.x / RG) % nqt, bh = (int)blockIdx.x / (RG * nqt);
-    const int64_t qstart = fast_q_start(S, CAUSAL, qt);
-    const int nsl = fast_slots(qstart, fast_q_n(S, CAUSAL, qt), a.chunk);
+    const int64_t qstart = fast_q_start(S, CAUSAL, a.window, qt);
+    const int nsl = fast_slots(qstart, fast_q_n(S, CAUSAL, a.window, qt), a.chunk);
     const int r0 = qt * BM + rg * kCombRows;
     if (nsl <= 1 || r0 >= S) return;
     const int64_t u0 = qstart / a.chunk, head_slots = (int64_t)bh * 2 * a.units;
@@ -626,8 +652,9 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(FwdArgs a) {
             l += ml[p][tid].y * wp;
             wgt[p][tid] = wp;
         }
-        inv_l[tid] = 1.f / l;
-        if (a.lse) a.lse[(int64_t)bh * S + r0 + tid] = (m + log2f(l)) * kLn2;
+        // l = 0: the row sees no key (see fwd_store_row)
+        inv_l[tid] = l > 0.f ? 1.f / l : 0.f;
+        if (a.lse) a.lse[(int64_t)bh * S + r0 + tid] = l > 0.f ? (m + log2f(l)) * kLn2 : INFINITY;
     }
     __syncthreads();
     // Thread -> row tid / 16, 16-byte column chunks (tid % 16) + 16 j: the
@@ -722,21 +749,22 @@ hipError_t launch_fwd_dispatch(const AttnShape& s, FwdArgs a, hipStream_t st) {
 int fwd_rows_per_block(const AttnShape&) { return 128; }
 
 FwdPlan plan_fwd_split(const AttnShape& s) {
-    const int S = (int)s.S, causal = s.causal ? 1 : 0;
+    const int S = (int)s.S, causal = s.causal ? 1 : 0, W = s.window;
     const int nqt = (S + kFwdBM - 1) / kFwdBM;
-    const int64_t n = fast_q_total(S, causal);  // iterations per (batch, head)
+    const int64_t n = fast_q_total(S, causal, W);  // iterations per (batch, head)
     const int64_t pairs = s.B * s.Hq;
     const int64_t u = balanced_units(pairs, device_cus());
     FwdPlan p;
     // Units no shorter than 4 key tiles: a split costs one fp32 partial tile.
     // A query tile has at most 2*S/64 key tiles; keep its slots <= kCombMaxSlots.
-    const int64_t max_tile = fast_q_n(S, causal, nqt - 1);
+    int64_t max_tile = 0;
+    for (int t = 0; t < nqt; ++t) max_tile = std::max<int64_t>(max_tile, fast_q_n(S, causal, W, t));
     const int64_t min_chunk = std::max<int64_t>(4, (max_tile + kCombMaxSlots - 3) / (kCombMaxSlots - 2));
     p.chunk = (int)std::min<int64_t>(n, std::max<int64_t>(min_chunk, (n + u - 1) / u));
     p.units = (int)((n + p.chunk - 1) / p.chunk);
     p.any_split = false;
     for (int t = 0; t < nqt && !p.any_split; ++t)
-        p.any_split = fast_slots(fast_q_start(S, causal, t), fast_q_n(S, causal, t), p.chunk) > 1;
+        p.any_split = fast_slots(fast_q_start(S, causal, W, t), fast_q_n(S, causal, W, t), p.chunk) > 1;
     return p;
 }
 
@@ -768,6 +796,8 @@ hipError_t launch_attn_fwd(const AttnShape& s, const void* q, const void* k, con
     a.scale_log2 = s.scale * kLog2e;
     a.vec_ok = (s.D % (s.bf16 ? 8 : 4)) == 0;
     a.vec4_ok = (s.D % 4) == 0;
+    a.window = s.window;
+    a.kv_len = s.kv_len;
     a.chunk = 0;
     a.units = 0;
     a.part_o = nullptr;
@@ -779,7 +809,9 @@ hipError_t launch_attn_fwd(const AttnShape& s, const void* q, const void* k, con
         a.part_o = static_cast<float*>(workspace);
         a.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + ob);
     }
-    return s.bf16 ? launch_fwd_dispatch<bf16>(s, a, st) : launch_fwd_dispatch<float>(s, a, st);
+    const hipError_t e = s.bf16 ? launch_fwd_dispatch<bf16>(s, a, st) : launch_fwd_dispatch<float>(s, a, st);
+    if (e != hipSuccess) return e;
+    return launch_fwd_masked_rows(s, v, o, st);
 }
 
 }  // namespace mft

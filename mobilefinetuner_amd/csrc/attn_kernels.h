@@ -12,6 +12,8 @@ struct AttnShape {
     float scale;   // resolved (> 0)
     bool causal;
     bool bf16;     // element type of q, k, v, o, dO
+    int window;              // causal sliding window (keys), 0 = none; normalised: 0 < window < S
+    const int32_t* kv_len;   // device [B] valid keys per batch (right padding), or null
 };
 
 // Tile geometry of one kernel variant, exposed so that the C ABI can size
@@ -38,9 +40,10 @@ struct BwdPlan {
 BwdPlan plan_bwd_fast(const AttnShape& s);
 
 // Backward workspace layout in bytes: [delta or row-stat blocks][dK/dV
-// partials][dQ partials]; each region 256-byte aligned.
+// partials][dQ partials][masked-row terms (key padding only)]; each region
+// 256-byte aligned.
 struct BwdLayout {
-    size_t stats, kv_part, q_part, total;
+    size_t stats, kv_part, q_part, masked, total;
 };
 BwdLayout bwd_layout(const AttnShape& s);
 
@@ -66,13 +69,22 @@ hipError_t launch_attn_fwd(const AttnShape& s, const void* q, const void* k, con
 
 // Backward stages (bit mask, values of MFT_BWD_*): DELTA writes the per-row
 // terms; DKDV and DQ compute the gradients (writing fp32 partials for split
-// tiles); REDUCE sums the partials.
+// tiles); REDUCE sums the partials (and, with key padding, writes the
+// gradient terms of rows that see no key).
 enum { BWD_STAGE_DELTA = 1, BWD_STAGE_DKDV = 2, BWD_STAGE_REDUCE = 4, BWD_STAGE_DQ = 8, BWD_STAGE_ALL = 15 };
 
 // workspace: bwd_layout(s).total bytes.
 hipError_t launch_attn_bwd(const AttnShape& s, const void* q, const void* k, const void* v,
                            const void* o, const void* dO, const float* lse, float* dq,
                            float* dk, float* dv, void* workspace, int stages, hipStream_t st);
+
+// Rows that see no key (key padding; attn_masked_rows.hip): the forward
+// writes their O after the main pass, the backward their dQ and dK/dV terms
+// after REDUCE.  No-ops without key lengths.
+size_t masked_rows_workspace_bytes(const AttnShape& s);
+hipError_t launch_fwd_masked_rows(const AttnShape& s, const void* v, void* o, hipStream_t st);
+hipError_t launch_bwd_masked_rows(const AttnShape& s, const void* q, const void* k, const void* v, const void* o,
+                                  const void* dO, float* dq, float* dk, float* dv, void* scratch, hipStream_t st);
 
 hipError_t launch_repeat_kv_fwd(const void* kv, void* out, int64_t B, int64_t Hkv, int64_t S,
                                 int64_t D, int64_t r, int esize, hipStream_t st);

@@ -53,7 +53,7 @@ def test_every_header_symbol_is_exported(capi):
 def test_header_compiles_as_c(tmp_path):
     """The header is plain C (extern "C", C99 types, no torch types)."""
     src = tmp_path / "t.c"
-    src.write_text('#include "mft/attention.h"\nint main(void){return mft_version()==1?0:1;}\n')
+    src.write_text('#include "mft/attention.h"\nint main(void){return mft_version()==2?0:1;}\n')
     res = subprocess.run(["gcc", "-std=c99", "-fsyntax-only", "-D__HIP_PLATFORM_AMD__",
                           "-I", os.path.join(ROOT, "include"), "-I", "/opt/rocm/include", str(src)],
                          capture_output=True, text=True)
@@ -61,7 +61,7 @@ def test_header_compiles_as_c(tmp_path):
 
 
 def test_version(capi):
-    assert capi.lib().mft_version() == 1
+    assert capi.lib().mft_version() == 2
 
 
 def _err(capi, fn):
@@ -76,6 +76,9 @@ def _err(capi, fn):
     (dict(D=320), 2, "head_dim > 256"),
     (dict(dtype=1), 1, "dtype"),
     (dict(scale=float("nan")), 1, "scale"),
+    (dict(window=-1), 1, "window"),
+    (dict(window=16, causal=False), 1, "causal"),
+    (dict(kv_len=2), 1, "aligned"),
 ])
 def test_desc_validation(capi, kw, status, needle):
     args = dict(B=1, Hq=4, Hkv=1, S=64, D=64, scale=-1.0, causal=True, dtype=capi.MFT_BF16)
@@ -124,3 +127,16 @@ def test_workspace_is_aligned_and_subquadratic(capi):
         sizes.append(b)
         assert b < 4 * 4 * S * S * 4 or S <= 1024  # reference holds four S x S fp32 tensors per head
     assert sizes[2] < 16 * sizes[1]  # 4x longer sequence, far less than 16x the bytes
+
+
+def test_window_and_padding_workspace(capi):
+    """A window shrinks the backward's split-tile partials (fewer iterations
+    per tile); key lengths add the per-row scratch of the rows that see no
+    key (two fp32/int32 values per query row); a window >= S is no window."""
+    base = capi.workspace_size(capi.desc(1, 4, 1, 4096, 256, 1 / 16, True, capi.MFT_BF16))
+    same = capi.workspace_size(capi.desc(1, 4, 1, 4096, 256, 1 / 16, True, capi.MFT_BF16, window=4096))
+    assert same == base
+    win = capi.workspace_size(capi.desc(1, 4, 1, 4096, 256, 1 / 16, True, capi.MFT_BF16, window=512))
+    assert win[1] > 0
+    pad = capi.workspace_size(capi.desc(1, 4, 1, 4096, 256, 1 / 16, True, capi.MFT_BF16, kv_len=1 << 20))
+    assert pad[1] == base[1] + 2 * 4 * 4 * 4096 and pad[0] == base[0]
