@@ -21,15 +21,23 @@
 //     GQA callers materialise repeat_kv_heads first); q/k/v may be bf16
 //     (computed bf16 x bf16 -> fp32 on MFMA).  The output is fp32 as in the
 //     reference (.cpp:122).
-//   * Masks: nullptr, an all-zero [S,S] mask, or the canonical causal mask
+//   * Masks: nullptr, an all-zero [S,S] mask, the canonical causal mask
 //     (create_causal_mask, core/ops.cpp:2167-2180: 0 on/below the diagonal,
-//     <= -1e9 above) map to the kernels' causal flag with the reference's
-//     precedence.  Other additive masks are rejected with an error (there is
-//     no CPU fallback).
+//     <= -1e9 above) or a causal sliding-window mask (Gemma's
+//     build_sliding_mask, graph/gemma_model.cpp:272-285) map to the kernels'
+//     causal flag and window with the reference's precedence.  Other additive
+//     masks are rejected with an error (there is no CPU fallback).
+//   * Extension for the model graphs (fused_attention.h):
+//     memory_efficient_attention_masked(q, k, v, base_mask, pad_mask, cfg) is
+//     the Gemma / Qwen composite (graph/gemma_model.cpp:481-505,
+//     graph/qwen_model.cpp:302-318: scores + base_mask, then + pad_mask) in
+//     one op, with the [B,1,1,S] padding mask of a right-padded
+//     attention_mask passed to the kernels as per-batch key lengths.
 //   * Tensors are the reference's host tensors: inputs are copied to the GPU,
 //     results back (PCIe-inclusive).  Device-resident callers use the C ABI.
 #include "memory_efficient_attention.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <memory>
@@ -42,6 +50,7 @@
 
 #include "autograd_engine.h"
 #include "backward_functions.h"
+#include "fused_attention.h"
 #include "mft/attention.h"
 #include "ops.h"
 
@@ -122,37 +131,92 @@ TensorPtr download_f32(const DeviceBuffer& src, const std::vector<int64_t>& shap
     return out;
 }
 
-enum class MaskKind { kNone, kZero, kCausal, kOther };
+enum class MaskKind { kNone, kZero, kCausal, kSliding, kOther };
 
-// Classifies an additive [S,S] mask (the reference adds it to the scaled
-// scores, core/ops.cpp:415-442).  Entries <= -1e9 are "masked": exp(-1e9 - m)
+// An additive [S,S] mask (the reference adds it to the scaled scores,
+// core/ops.cpp:415-442).  Entries <= -1e9 are "masked": exp(-1e9 - m)
 // underflows to exactly 0 in fp32 for any score range the ops produce.
-MaskKind classify_mask(const TensorPtr& mask, int64_t S) {
-    if (!mask) return MaskKind::kNone;
+struct BaseMask {
+    MaskKind kind = MaskKind::kNone;
+    int64_t window = 0;                      // kSliding: i - j < window
+    float lo = 0.f, hi = 0.f;                // range of the masked entries' values
+};
+
+BaseMask classify_mask(const TensorPtr& mask, int64_t S) {
+    BaseMask r;
+    if (!mask) return r;
     if (mask->shape().size() != 2 || mask->shape()[0] != S || mask->shape()[1] != S)
         throw std::runtime_error("memory_efficient_attention: causal_mask must be [S,S]");
-    if (mask->dtype() != kFloat32) return MaskKind::kOther;
+    r.kind = MaskKind::kOther;
+    if (mask->dtype() != kFloat32) return r;
     const float* m = mask->data<float>();
-    bool zero = true, causal = true;
-    for (int64_t i = 0; i < S && (zero || causal); ++i) {
+    // Candidate window: the zeros at the end of the last row.
+    int64_t w = 0;
+    while (w < S && m[(S - 1) * S + (S - 1 - w)] == 0.0f) ++w;
+    bool zero = true, causal = true, sliding = w > 0;
+    r.lo = 0.f;
+    r.hi = -INFINITY;
+    for (int64_t i = 0; i < S && (zero || causal || sliding); ++i) {
         for (int64_t j = 0; j < S; ++j) {
             const float x = m[i * S + j];
-            if (j <= i) {
-                if (x != 0.0f) zero = causal = false;
-            } else {
-                if (x != 0.0f) zero = false;
-                if (!(x <= -1e9f)) causal = false;
+            const bool masked = x <= -1e9f;
+            if (!masked && x != 0.0f) return r;
+            if (masked) {
+                r.lo = std::min(r.lo, x);
+                r.hi = std::max(r.hi, x);
             }
+            if (x != 0.0f) zero = false;
+            if ((j > i) != masked) causal = false;
+            if ((j > i || i - j >= w) != masked) sliding = false;
         }
     }
-    return zero ? MaskKind::kZero : causal ? MaskKind::kCausal : MaskKind::kOther;
+    if (zero) r.kind = MaskKind::kZero;
+    else if (causal) r.kind = MaskKind::kCausal;
+    else if (sliding) {
+        r.kind = MaskKind::kSliding;
+        r.window = w;
+    }
+    return r;
+}
+
+// An additive padding mask [B,1,1,S] (graph/gemma_model.cpp:287-320,
+// graph/qwen_model.cpp:338-353): per batch 0 on the first len[b] keys and
+// masked (<= -1e9) after them, the right padding the datasets produce
+// (data/wikitext2_dataset.cpp:461-500, data/mmlu_dataset.cpp:285-305).
+struct PadMask {
+    std::vector<int32_t> len;
+    float lo = 0.f, hi = -INFINITY;  // range of the masked entries' values
+};
+
+PadMask classify_pad_mask(const TensorPtr& mask, int64_t B, int64_t S) {
+    PadMask r;
+    if (!mask) return r;
+    const auto& sh = mask->shape();
+    if (sh.size() != 4 || sh[0] != B || sh[1] != 1 || sh[2] != 1 || sh[3] != S || mask->dtype() != kFloat32)
+        throw std::runtime_error("memory_efficient_attention_masked: pad_mask must be float32 [B,1,1,S]");
+    const float* m = mask->data<float>();
+    r.len.resize(static_cast<size_t>(B));
+    for (int64_t b = 0; b < B; ++b) {
+        int64_t n = 0;
+        while (n < S && m[b * S + n] == 0.0f) ++n;
+        for (int64_t j = n; j < S; ++j) {
+            const float x = m[b * S + j];
+            if (!(x <= -1e9f))
+                throw std::runtime_error(
+                    "memory_efficient_attention_masked: pad_mask must mask a suffix of the keys (right padding)");
+            r.lo = std::min(r.lo, x);
+            r.hi = std::max(r.hi, x);
+        }
+        r.len[static_cast<size_t>(b)] = static_cast<int32_t>(n);
+    }
+    return r;
 }
 
 // What the kernels hold between forward and backward.
 struct SavedForBackward {
     mft_attn_desc desc{};
     std::vector<int64_t> q_shape, kv_shape;
-    std::unique_ptr<DeviceBuffer> q, k, v, o, lse;
+    std::unique_ptr<DeviceBuffer> q, k, v, o, lse, kv_len;
 };
 
 class FusedAttentionBackward : public BackwardFunction {
@@ -217,8 +281,17 @@ void online_softmax_weighted_sum(const float* logits, const float* values, int64
     }
 }
 
-TensorPtr memory_efficient_attention(const TensorPtr& q, const TensorPtr& k, const TensorPtr& v,
-                                     const TensorPtr& causal_mask, const MemoryEfficientAttentionConfig& config) {
+namespace {
+
+struct Checked {
+    int64_t B, Hq, Hkv, S, D;
+    DType dt;
+    float scale;
+    bool needs_grad;
+};
+
+Checked check_inputs(const TensorPtr& q, const TensorPtr& k, const TensorPtr& v,
+                     const MemoryEfficientAttentionConfig& config) {
     if (!q || !k || !v) throw std::runtime_error("memory_efficient_attention: null input");
     const auto& qs = q->shape();
     const auto& ks = k->shape();
@@ -236,29 +309,36 @@ TensorPtr memory_efficient_attention(const TensorPtr& q, const TensorPtr& k, con
         throw std::runtime_error("memory_efficient_attention: expects host tensors");
     const float scale = (config.scale > 0) ? config.scale : (1.0f / std::sqrt(static_cast<float>(D)));
     const bool needs_grad = q->requires_grad() || k->requires_grad() || v->requires_grad();
+    return {B, Hq, Hkv, S, D, dt, scale, needs_grad};
+}
 
-    // Causal flag with the reference's precedence: the grad path (composite,
-    // .cpp:23-43) uses the given mask instead of use_causal_mask; the no-grad
-    // path (.cpp:163-172) applies use_causal_mask and then adds the mask.
-    const MaskKind mk = classify_mask(causal_mask, S);
-    bool causal = config.use_causal_mask;
-    if (mk == MaskKind::kOther)
-        throw std::runtime_error(
-            "memory_efficient_attention: only the causal mask (or none) is supported on the GPU path");
-    if (mk == MaskKind::kCausal) causal = true;
-    if (mk == MaskKind::kZero && needs_grad) causal = false;
-
+// Forward on the device, and the autograd node when a grad is needed.
+TensorPtr run_fused(const TensorPtr& q, const TensorPtr& k, const TensorPtr& v, const Checked& c, bool causal,
+                    int64_t window, const std::vector<int32_t>& lengths) {
+    const auto& qs = q->shape();
+    const auto& ks = k->shape();
+    const DType dt = c.dt;
+    const bool needs_grad = c.needs_grad;
+    const int64_t B = c.B, Hq = c.Hq, S = c.S;
     mft_attn_desc d{};
-    d.B = B;
-    d.Hq = Hq;
-    d.Hkv = Hkv;
-    d.S = S;
-    d.D = D;
-    d.scale = scale;
+    d.B = c.B;
+    d.Hq = c.Hq;
+    d.Hkv = c.Hkv;
+    d.S = c.S;
+    d.D = c.D;
+    d.scale = c.scale;
     d.causal = causal ? 1 : 0;
     d.dtype = dt == kBFloat16 ? MFT_BF16 : MFT_F32;
+    d.window = static_cast<int32_t>(window < S ? window : 0);
 
     auto saved = std::make_shared<SavedForBackward>();
+    if (!lengths.empty()) {
+        saved->kv_len = std::make_unique<DeviceBuffer>(lengths.size() * sizeof(int32_t));
+        hip_check(hipMemcpyAsync(saved->kv_len->get(), lengths.data(), lengths.size() * sizeof(int32_t),
+                                 hipMemcpyHostToDevice, adapter_stream()),
+                  "copy kv_len");
+        d.kv_len = static_cast<const int32_t*>(saved->kv_len->get());
+    }
     saved->desc = d;
     saved->q_shape = qs;
     saved->kv_shape = ks;
@@ -281,6 +361,44 @@ TensorPtr memory_efficient_attention(const TensorPtr& q, const TensorPtr& k, con
                                                    std::make_shared<FusedAttentionBackward>(saved));
     }
     return out;
+}
+
+}  // namespace
+
+TensorPtr memory_efficient_attention(const TensorPtr& q, const TensorPtr& k, const TensorPtr& v,
+                                     const TensorPtr& causal_mask, const MemoryEfficientAttentionConfig& config) {
+    const Checked c = check_inputs(q, k, v, config);
+    // Causal flag with the reference's precedence: the grad path (composite,
+    // .cpp:23-43) uses the given mask instead of use_causal_mask; the no-grad
+    // path (.cpp:163-172) applies use_causal_mask and then adds the mask.
+    const BaseMask mk = classify_mask(causal_mask, c.S);
+    bool causal = config.use_causal_mask;
+    if (mk.kind == MaskKind::kOther)
+        throw std::runtime_error(
+            "memory_efficient_attention: only the causal or sliding-window mask (or none) is supported on the GPU "
+            "path");
+    if (mk.kind == MaskKind::kCausal || mk.kind == MaskKind::kSliding) causal = true;
+    if (mk.kind == MaskKind::kZero && c.needs_grad) causal = false;
+    return run_fused(q, k, v, c, causal, mk.kind == MaskKind::kSliding ? mk.window : 0, {});
+}
+
+TensorPtr memory_efficient_attention_masked(const TensorPtr& q, const TensorPtr& k, const TensorPtr& v,
+                                            const TensorPtr& base_mask, const TensorPtr& pad_mask,
+                                            const MemoryEfficientAttentionConfig& config) {
+    const Checked c = check_inputs(q, k, v, config);
+    const BaseMask bm = classify_mask(base_mask, c.S);
+    if (bm.kind == MaskKind::kOther)
+        throw std::runtime_error(
+            "memory_efficient_attention_masked: base_mask must be causal, sliding-window, all-zero or null");
+    const PadMask pm = classify_pad_mask(pad_mask, c.B, c.S);
+    // Rows that see no key follow the reference's -1e10 arithmetic, which the
+    // kernels reproduce when a window's and the padding's masked entries
+    // carry one value (Gemma: kMaskValue for both, graph/gemma_model.cpp:175).
+    if (bm.kind == MaskKind::kSliding && pad_mask && !(bm.lo == bm.hi && pm.lo == pm.hi && bm.lo == pm.lo))
+        throw std::runtime_error(
+            "memory_efficient_attention_masked: a sliding window with padding needs one masked value in both masks");
+    const bool causal = bm.kind == MaskKind::kCausal || bm.kind == MaskKind::kSliding;
+    return run_fused(q, k, v, c, causal, bm.kind == MaskKind::kSliding ? bm.window : 0, pm.len);
 }
 
 }  // namespace ops

@@ -20,6 +20,7 @@
 #include <vector>
 
 #include "autograd_engine.h"
+#include "fused_attention.h"
 #include "memory_efficient_attention.h"
 #include "ops.h"
 
@@ -119,6 +120,63 @@ Result run_case(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, float 
             max_rel(vf->grad(), vr->grad())};
 }
 
+// Gemma's build_sliding_mask (graph/gemma_model.cpp:272-285): j <= i and
+// i - j < window, else kMaskValue (-1e10).
+TensorPtr sliding_mask(int64_t S, int64_t window) {
+    auto m = zeros({S, S}, kFloat32, kCPU);
+    float* p = m->data<float>();
+    for (int64_t i = 0; i < S; ++i)
+        for (int64_t j = 0; j < S; ++j)
+            if (!(j <= i && i - j < window)) p[i * S + j] = -1e10f;
+    return m;
+}
+
+// The [B,1,1,S] padding mask of a right-padded attention_mask
+// (graph/gemma_model.cpp:287-320 with value -1e10; graph/qwen_model.cpp:338-353
+// with -1e9).
+TensorPtr pad_mask(int64_t B, int64_t S, const std::vector<int>& lengths, float value) {
+    auto m = zeros({B, 1, 1, S}, kFloat32, kCPU);
+    float* p = m->data<float>();
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t j = lengths[size_t(b)]; j < S; ++j) p[b * S + j] = value;
+    return m;
+}
+
+// The model graphs' composite (graph/gemma_model.cpp:481-505: repeat_kv_heads,
+// scores + base_mask, then + pad_mask) against memory_efficient_attention_masked
+// (or, without padding, memory_efficient_attention with the base mask).
+Result run_masked_case(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, int64_t window,
+                       const std::vector<int>& lengths, float pad_value, bool bf16, uint64_t seed) {
+    const int r = int(Hq / Hkv);
+    auto q0 = make({B, Hq, S, D}, seed, 1.0f, bf16, false);
+    auto k0 = make({B, Hkv, S, D}, seed + 1, 1.0f, bf16, false);
+    auto v0 = make({B, Hkv, S, D}, seed + 2, 1.0f, bf16, false);
+    auto g = make({B, Hq, S, D}, seed + 3, 0.1f, bf16, false);
+    auto base = window > 0 ? sliding_mask(S, window) : create_causal_mask(int(S), kFloat32, kCPU);
+    auto pad = lengths.empty() ? nullptr : pad_mask(B, S, lengths, pad_value);
+    const float scale = 1.0f / std::sqrt(float(D));
+
+    auto qr = copy_of(q0, true), kr = copy_of(k0, true), vr = copy_of(v0, true);
+    auto kk = r > 1 ? repeat_kv_heads(kr, r) : kr;
+    auto vv = r > 1 ? repeat_kv_heads(vr, r) : vr;
+    auto scores = add(mul(matmul(qr, transpose(kk, 2, 3)), scale), base);
+    if (pad) scores = add(scores, pad);
+    auto out_ref = matmul(softmax(scores, -1), vv);
+    autograd::Engine::instance().run_backward({out_ref}, {g});
+
+    auto qf = bf16 ? to_bf16(q0, true) : copy_of(q0, true);
+    auto kf = bf16 ? to_bf16(k0, true) : copy_of(k0, true);
+    auto vf = bf16 ? to_bf16(v0, true) : copy_of(v0, true);
+    MemoryEfficientAttentionConfig cfg;
+    cfg.scale = scale;
+    auto out = pad ? memory_efficient_attention_masked(qf, kf, vf, base, pad, cfg)
+                   : memory_efficient_attention(qf, kf, vf, base, cfg);
+    autograd::Engine::instance().run_backward({out}, {g});
+    if (!qf->grad() || !kf->grad() || !vf->grad()) throw std::runtime_error("missing fused grads");
+    return {max_rel(out, out_ref), max_rel(qf->grad(), qr->grad()), max_rel(kf->grad(), kr->grad()),
+            max_rel(vf->grad(), vr->grad())};
+}
+
 bool expect_throw(const char* what, const std::function<void()>& fn) {
     try {
         fn();
@@ -158,6 +216,32 @@ int main() {
                   << " dq=" << r.dq << " dk=" << r.dk << " dv=" << r.dv << (pass ? "  ok" : "  FAIL") << std::endl;
         ok = ok && pass;
     }
+    // The model graphs' masked composite: sliding window (Gemma) and padding
+    // (Gemma -1e10, Qwen -1e9), including rows left with no visible key.
+    struct MCase {
+        int64_t B, Hq, Hkv, S, D, window;
+        std::vector<int> lengths;
+        float pad_value;
+        bool bf16;
+    };
+    const MCase mcases[] = {
+        {1, 2, 2, 40, 32, 8, {}, 0.f, false},              // sliding mask via memory_efficient_attention
+        {2, 4, 1, 70, 64, 16, {70, 30}, -1e10f, false},    // Gemma: window + padding, rows 45.. see no key
+        {2, 4, 1, 96, 256, 32, {50, 96}, -1e10f, true},
+        {2, 14, 2, 33, 64, 0, {20, 33}, -1e9f, false},     // Qwen: causal + padding
+        {2, 2, 1, 24, 32, 0, {0, 24}, -1e9f, false},       // an all-padding sequence
+    };
+    for (const MCase& c : mcases) {
+        const Result r = run_masked_case(c.B, c.Hq, c.Hkv, c.S, c.D, c.window, c.lengths, c.pad_value, c.bf16,
+                                         seed += 17);
+        const float tol = c.bf16 ? 2e-2f : 1e-4f;
+        const bool pass = r.o <= tol && r.dq <= tol && r.dk <= tol && r.dv <= tol;
+        std::cout << "[dropin] masked B=" << c.B << " Hq=" << c.Hq << " Hkv=" << c.Hkv << " S=" << c.S
+                  << " D=" << c.D << " window=" << c.window << " padded=" << !c.lengths.empty()
+                  << (c.bf16 ? " bf16" : " fp32") << "  max-rel o=" << r.o << " dq=" << r.dq << " dk=" << r.dk
+                  << " dv=" << r.dv << (pass ? "  ok" : "  FAIL") << std::endl;
+        ok = ok && pass;
+    }
     // No-grad path equals the grad path's output (same kernels, no LSE kept).
     {
         auto q = make({1, 2, 20, 16}, 7, 1.0f, false, false);
@@ -177,6 +261,14 @@ int main() {
     auto mask = make({8, 8}, 3, 1.0f, false, false);
     ok = expect_throw("q 2 heads, k 3 heads", [&] { memory_efficient_attention(q, k3, k3, nullptr, {}); }) && ok;
     ok = expect_throw("non-causal additive mask", [&] { memory_efficient_attention(q, q, q, mask, {}); }) && ok;
+    ok = expect_throw("left padding", [&] {
+        auto pm = pad_mask(1, 8, {8}, -1e9f);
+        pm->data<float>()[0] = -1e9f;
+        memory_efficient_attention_masked(q, q, q, create_causal_mask(8, kFloat32, kCPU), pm, {});
+    }) && ok;
+    ok = expect_throw("window with padding of another value", [&] {
+        memory_efficient_attention_masked(q, q, q, sliding_mask(8, 3), pad_mask(1, 8, {5}, -1e9f), {});
+    }) && ok;
     ok = expect_throw("3-D input", [&] {
         auto t = zeros({2, 8, 16}, kFloat32, kCPU);
         memory_efficient_attention(t, t, t, nullptr, {});
