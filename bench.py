@@ -7,7 +7,9 @@
 A step is one forward plus one backward of the attention over the config's
 synthetic batch (inputs resident in HBM).  Prints ONE JSON line.  `value` is
 the algorithmic causal throughput  7*B*H*D*S*(S+1) / step time  in TFLOP/s
-The roofline object covers the dominant kernel,
+`mask_variants` adds the same measurement for the
+masks the model graphs use: Gemma's sliding window (c5w512) and right-padded
+batches (c4pad); their flops count the visible (query, key) pairs only.  The roofline object covers the dominant kernel,
 timed live with HIP events on the stream the kernels run on.  The
 cpu_baseline object times the reference CPU operators (oracle/_ref, compiled
 from the reference sources) on a bounded sample of the same workload.
@@ -39,12 +41,35 @@ CONFIGS = {
                name="Gemma-3-1B-shaped GQA attention fwd+bwd, bf16"),
     "c5f32": dict(B=1, Hq=4, Hkv=1, D=256, S=4096, dtype="f32", scale=1 / 16, do_sigma=0.1,
                   name="Gemma-3-1B-shaped GQA attention fwd+bwd, fp32 exactness variant"),
+    # Mask variants of the model graphs (not BASELINE configs): Gemma-3's
+    # sliding layers (sliding_window 512) at the c5 shape, and a right-padded
+    # batch (lengths per sequence) at the c4 shape.
+    "c5w512": dict(B=1, Hq=4, Hkv=1, D=256, S=4096, dtype="bf16", scale=1 / 16, do_sigma=0.1, window=512,
+                   name="Gemma-3-1B-shaped sliding-window layer (window 512) fwd+bwd, bf16"),
+    "c4pad": dict(B=4, Hq=4, Hkv=1, D=256, S=1024, dtype="bf16", scale=1 / 16, do_sigma=0.1,
+                  lengths=[1024, 700, 400, 130],
+                  name="Gemma-3-270M-shaped fwd+bwd with right-padded sequences, bf16"),
 }
 
 
+def visible_pairs(S, window=0, length=None):
+    """(query, key) pairs the causal mask, a sliding window and key padding
+    leave visible in one (batch, head)."""
+    n = S if length is None else length
+    w = window if window else S
+    # row i sees the keys j in [max(0, i - w + 1), min(i, n - 1)]
+    tot = 0
+    for i in range(S):
+        lo, hi = max(0, i - w + 1), min(i, n - 1)
+        tot += max(0, hi - lo + 1)
+    return tot
+
+
 def flop_units(c):
-    """One causal S x S x D contraction per query head: D*S*(S+1) flops."""
-    return c["B"] * c["Hq"] * c["D"] * c["S"] * (c["S"] + 1)
+    """2*D flops per visible (query, key) pair per query head: D*S*(S+1) for
+    the plain causal mask."""
+    lengths = c.get("lengths") or [None] * c["B"]
+    return c["Hq"] * c["D"] * 2 * sum(visible_pairs(c["S"], c.get("window", 0), n) for n in lengths)
 
 
 def saved_bytes(c):
@@ -67,22 +92,24 @@ def gpu_leg(cfg_id, steps, warmup):
     dev = torch.device("cuda:0")
     dt = torch.bfloat16 if c["dtype"] == "bf16" else torch.float32
     g = torch.Generator(device=dev)
-    g.manual_seed(1000 + int(cfg_id[1]))
+    g.manual_seed(1000 + sum(map(ord, cfg_id)))
     B, Hq, Hkv, S, D = c["B"], c["Hq"], c["Hkv"], c["S"], c["D"]
     q = torch.randn(B, Hq, S, D, device=dev, generator=g).to(dt)
     k = torch.randn(B, Hkv, S, D, device=dev, generator=g).to(dt)
     v = torch.randn(B, Hkv, S, D, device=dev, generator=g).to(dt)
     dO = (torch.randn(B, Hq, S, D, device=dev, generator=g) * c["do_sigma"]).to(dt)
     scale = c["scale"]
-    ws = torch.empty(max(A.workspace_bytes(q, k, scale, True), 1), dtype=torch.uint8, device=dev)
-    fws_n = A.fwd_workspace_bytes(q, k, scale, True)
+    window = c.get("window", 0)
+    kv_len = torch.tensor(c["lengths"], dtype=torch.int32, device=dev) if c.get("lengths") else None
+    ws = torch.empty(max(A.workspace_bytes(q, k, scale, True, window, kv_len), 1), dtype=torch.uint8, device=dev)
+    fws_n = A.fwd_workspace_bytes(q, k, scale, True, window, kv_len)
     fws = torch.empty(max(fws_n, 1), dtype=torch.uint8, device=dev)
     o = torch.empty_like(q)
     lse = torch.empty(B, Hq, S, dtype=torch.float32, device=dev)
     dq = torch.empty(q.shape, dtype=torch.float32, device=dev)
     dk = torch.empty(k.shape, dtype=torch.float32, device=dev)
     dv = torch.empty(v.shape, dtype=torch.float32, device=dev)
-    d = A._desc(q, k, scale, True)
+    d = A._desc(q, k, scale, True, window, kv_len)
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
     P = [t.data_ptr() for t in (q, k, v, o, dO, lse, dq, dk, dv, ws)]
@@ -186,6 +213,7 @@ def main():
     ap.add_argument("--config", default="c5", choices=sorted(CONFIGS))
     ap.add_argument("--all-configs", action="store_true", help="also report every config (extra key)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-variants", action="store_true", help="skip the mask variants (mask_variants key)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain copy of COPY_BYTES (for scaling rocprofv3 FETCH/WRITE_SIZE)")
     args = ap.parse_args()
@@ -237,6 +265,19 @@ def main():
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(ach, 2), "peak": peak,
                      "unit": "TFLOP/s", "frac": round(ach / peak, 4), "traffic": traffic},
     }
+    variants = {}
+    for cid in () if args.no_variants else ("c5w512", "c4pad"):
+        cc = CONFIGS[cid]
+        rr = gpu_leg(cid, max(10, args.steps // 2), 5)
+        u = rr["units"]
+        tf = 7 * u / (rr["step_ms"] * 1e-3) / 1e12
+        variants[cid] = {"workload": cc["name"], "window": cc.get("window", 0), "lengths": cc.get("lengths"),
+                         "ms_per_step": round(rr["step_ms"], 5), "fwd_ms": round(rr["fwd_ms"], 5),
+                         "bwd_ms": round(rr["bwd_ms"], 5), "tflops": round(tf, 2),
+                         "pct_peak": round(100 * tf / PEAK_TFLOPS[cc["dtype"]], 2),
+                         "tokens_per_s": round(cc["B"] * cc["S"] / (rr["step_ms"] * 1e-3), 1)}
+    if variants:
+        out["mask_variants"] = variants
     if args.all_configs:
         per = {}
         for cid in ("c1", "c2", "c3", "c4", "c5", "c5f32"):

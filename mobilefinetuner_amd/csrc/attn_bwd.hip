@@ -584,20 +584,22 @@ BwdPlan plan_bwd_fast(const AttnShape& s) {
     const int64_t n_q = fast_q_total(S, causal, W);                    // iterations per (batch, query head)
     const int64_t pairs_kv = s.B * s.Hkv, pairs_q = s.B * s.Hq;
     // The two roles run as separate launches: each is cut into about one
-    // unit per CU (units no shorter than 8 iterations).
+    // unit per CU.
     const int cus = device_cus();
     const int64_t u_kv = balanced_units(pairs_kv, cus);
     const int64_t u_q = balanced_units(pairs_q, cus);
     BwdPlan p;
-    // Units no shorter than 8 iterations, and long enough that no tile spans
-    // more than 63 units (REDUCE keeps a tile's slot list in LDS, 64 entries).
+    // Units no shorter than 4 iterations (shorter ones leave more idle CUs
+    // than they fill when a (batch, head) holds little work: windows, short
+    // sequences), and long enough that no tile spans more than 63 units
+    // (REDUCE keeps a tile's slot list in LDS, 64 entries).
     int64_t kv_tile_max = 0, q_tile_max = 0;
     for (int t = 0; t < nt; ++t) {
         kv_tile_max = std::max<int64_t>(kv_tile_max, bwd::fast_kv_n(S, causal, W, group, t));
         q_tile_max = std::max<int64_t>(q_tile_max, bwd::fast_q_n(S, causal, W, t));
     }
-    const int64_t kv_min = std::max<int64_t>(8, (kv_tile_max + 60) / 61);
-    const int64_t q_min = std::max<int64_t>(8, (q_tile_max + 60) / 61);
+    const int64_t kv_min = std::max<int64_t>(4, (kv_tile_max + 60) / 61);
+    const int64_t q_min = std::max<int64_t>(4, (q_tile_max + 60) / 61);
     p.kv_chunk = (int)std::min<int64_t>(n_kv, std::max<int64_t>(kv_min, (n_kv + u_kv - 1) / u_kv));
     p.q_chunk = (int)std::min<int64_t>(n_q, std::max<int64_t>(q_min, (n_q + u_q - 1) / u_q));
     p.kv_units = (int)((n_kv + p.kv_chunk - 1) / p.kv_chunk);

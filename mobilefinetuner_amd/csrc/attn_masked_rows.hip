@@ -102,20 +102,25 @@ __device__ __forceinline__ float dot4(const float (&x)[4], const float (&y)[4]) 
     return x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
 }
 
-// Backward, dQ of masked rows (and the row terms the dK/dV pass reads): one
-// wave per (row, batch x query head).
+// Backward, dQ of masked rows (and the row terms the dK/dV pass reads): a
+// workgroup per (64 rows, batch x query head), each wave 16 rows in turn.
+// Workgroups without masked rows return at once (the common case).
+template <typename T>
+__device__ void masked_dq_row(const MaskedArgs& a, const MaskedRows& mr, int b, int h, int i);
+
 template <typename T>
 __global__ __launch_bounds__(256) void attn_bwd_masked_dq(MaskedArgs a) {
-    const int S = a.S, D = a.D, lane = threadIdx.x & 63;
-    const int i = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
-    const int bh = blockIdx.y, b = bh / a.Hq, h = bh % a.Hq, hk = h / a.group;
-    if (i >= S) return;
+    const int bh = blockIdx.y, b = bh / a.Hq, h = bh % a.Hq;
     const MaskedRows mr = masked_rows(a, b);
-    const int64_t ri = (int64_t)bh * S + i;
-    if (i < mr.first()) {
-        if (lane == 0) a.row_active[ri] = 0;
-        return;
-    }
+    const int r0 = max((int)blockIdx.x * 64 + 16 * (int)(threadIdx.x >> 6), mr.first());
+    const int r1 = min((int)blockIdx.x * 64 + 16 * (int)(threadIdx.x >> 6) + 16, a.S);
+    for (int i = r0; i < r1; ++i) masked_dq_row<T>(a, mr, b, h, i);
+}
+
+template <typename T>
+__device__ void masked_dq_row(const MaskedArgs& a, const MaskedRows& mr, int b, int h, int i) {
+    const int S = a.S, D = a.D, lane = threadIdx.x & 63, hk = h / a.group;
+    const int64_t ri = ((int64_t)b * a.Hq + h) * S + i;
     float g[4], o[4];
     load_row4((const T*)a.dO + ri * D, D, g);
     load_row4((const T*)a.o + ri * D, D, o);
@@ -146,17 +151,26 @@ __global__ __launch_bounds__(256) void attn_bwd_masked_dq(MaskedArgs a) {
         if (lane + 64 * c < D) dq[lane + 64 * c] = acc[c] * a.scale;
 }
 
-// Backward, dK/dV contributions of masked rows: one wave per (key, batch x kv
-// head), adding to what the main pass wrote.  The rows that hold key j in
-// T_i: all masked rows for j < len, else rows j .. j + W - 1 (causal window)
-// among the masked ones; active rows are found 64 at a time by ballot.
+// Backward, dK/dV contributions of masked rows, added to what the main pass
+// wrote: a workgroup per (64 keys, batch x kv head), each wave 16 keys in
+// turn.  The rows that hold key j in T_i: all masked rows for j < len, else
+// rows j .. j + W - 1 (causal window) among the masked ones; active rows are
+// found 64 at a time by ballot.  Batches without masked rows return at once.
+template <typename T>
+__device__ void masked_dkdv_key(const MaskedArgs& a, const MaskedRows& mr, int b, int hk, int j);
+
 template <typename T>
 __global__ __launch_bounds__(256) void attn_bwd_masked_dkdv(MaskedArgs a) {
-    const int S = a.S, D = a.D, lane = threadIdx.x & 63;
-    const int j = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
     const int bk = blockIdx.y, b = bk / a.Hkv, hk = bk % a.Hkv;
-    if (j >= S) return;
     const MaskedRows mr = masked_rows(a, b);
+    if (mr.first() >= a.S) return;
+    const int j0 = (int)blockIdx.x * 64 + 16 * (int)(threadIdx.x >> 6);
+    for (int j = j0; j < min(j0 + 16, a.S); ++j) masked_dkdv_key<T>(a, mr, b, hk, j);
+}
+
+template <typename T>
+__device__ void masked_dkdv_key(const MaskedArgs& a, const MaskedRows& mr, int b, int hk, int j) {
+    const int S = a.S, D = a.D, lane = threadIdx.x & 63;
     int i_lo = mr.first(), i_hi = S - 1;
     if (j >= mr.len) {
         if (mr.causal) i_lo = max(i_lo, j);
@@ -251,8 +265,8 @@ hipError_t launch_bwd_masked_rows(const AttnShape& s, const void* q, const void*
     const size_t half = masked_rows_workspace_bytes(s) / 2;
     a.row_delta = static_cast<float*>(scratch);
     a.row_active = reinterpret_cast<int*>(static_cast<char*>(scratch) + half);
-    const dim3 gq((unsigned)((s.S + 3) / 4), (unsigned)(s.B * s.Hq));
-    const dim3 gk((unsigned)((s.S + 3) / 4), (unsigned)(s.B * s.Hkv));
+    const dim3 gq((unsigned)((s.S + 63) / 64), (unsigned)(s.B * s.Hq));
+    const dim3 gk((unsigned)((s.S + 63) / 64), (unsigned)(s.B * s.Hkv));
     if (s.bf16) {
         hipLaunchKernelGGL(attn_bwd_masked_dq<bf16>, gq, dim3(256), 0, st, a);
         hipLaunchKernelGGL(attn_bwd_masked_dkdv<bf16>, gk, dim3(256), 0, st, a);
