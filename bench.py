@@ -145,10 +145,9 @@ def gpu_leg(cfg_id, steps, warmup):
     fwd_ms = timed(fwd, n_phase)
     bwd_ms = timed(bwd, n_phase)
     stage(capi.MFT_BWD_DELTA)()  # row terms for the gradient stages
-    dkdv_ms = timed(stage(capi.MFT_BWD_DKDV), n_phase)
-    dq_ms = timed(stage(capi.MFT_BWD_DQ), n_phase)
+    main_ms = timed(stage(capi.MFT_BWD_MAIN), n_phase)
     units = flop_units(c)
-    return dict(step_ms=step_ms, fwd_ms=fwd_ms, bwd_ms=bwd_ms, dkdv_ms=dkdv_ms, dq_ms=dq_ms, units=units)
+    return dict(step_ms=step_ms, fwd_ms=fwd_ms, bwd_ms=bwd_ms, main_ms=main_ms, units=units)
 
 
 COPY_BYTES = 1 << 30
@@ -178,17 +177,18 @@ def hbm_traffic(cfg_id, kernel):
 
 
 def cpu_leg(cfg_id):
-    """Reference CPU operators on a bounded sample: one query head of the
-    workload (same S, D), fwd+bwd, single-threaded as the reference is."""
+    """Reference CPU operators (compiled from the reference sources) on a
+    bounded sample of the workload, fwd+bwd, single-threaded as the reference
+    is: the whole config when it is about 10-30 s of CPU work, else one query
+    head (and, if still too long, a shorter sequence)."""
     from oracle import oracle as O
     c = CONFIGS[cfg_id]
-    S, D = c["S"], c["D"]
-    # Keep the sample to roughly 10-30 s of CPU work: one head, and a shorter
-    # sequence when one head of the full length would be too long.
-    Ss = S
-    while 7 * D * Ss * (Ss + 1) > 1.2e11:
-        Ss //= 2
-    q, k, v, dO = O.make_inputs(1, 1, 1, Ss, D, 4242, c["dtype"], c["do_sigma"])
+    B, Hq, Hkv, S, D = c["B"], c["Hq"], c["Hkv"], c["S"], c["D"]
+    if 7 * B * Hq * D * S * (S + 1) > 1.6e11:
+        B, Hq, Hkv = 1, 1, 1
+        while 7 * D * S * (S + 1) > 1.2e11:
+            S //= 2
+    q, k, v, dO = O.make_inputs(B, Hq, Hkv, S, D, 4242, c["dtype"], c["do_sigma"])
     kind = "reference" if O.ref_available() else "port"
     t0 = time.time()
     if kind == "reference":
@@ -197,12 +197,12 @@ def cpu_leg(cfg_id):
     else:
         O.composite(q, k, v, dO, scale=c["scale"], causal=True)
         secs = time.time() - t0
-    units = D * Ss * (Ss + 1)
+    units = B * Hq * D * S * (S + 1)
     return dict(value=round(7 * units / secs / 1e12, 6), unit="TFLOP/s", cores=1, kind=kind,
                 seconds=round(secs, 3),
-                sample=f"1 query head of {cfg_id} (B=1,H=1,S={Ss},D={D}), fp32 composite fwd+bwd "
-                       f"(repeat/transpose/matmul/mul/add-mask/softmax/matmul + Engine backward), "
-                       f"pure C++ build, 1 thread")
+                sample=f"{cfg_id} sample B={B},Hq={Hq},Hkv={Hkv},S={S},D={D}: fp32 composite fwd+bwd "
+                       f"(repeat_kv/transpose/matmul/mul/add-mask/softmax/matmul + Engine backward), "
+                       f"reference sources built pure C++ (no BLAS), 1 thread")
 
 
 def main():
@@ -227,12 +227,14 @@ def main():
     units = r["units"]
     peak = PEAK_TFLOPS[c["dtype"]]
     tflops = 7 * units / (r["step_ms"] * 1e-3) / 1e12
-    # Dominant kernel: the longest of the forward, dK/dV and dQ launches;
-    # achieved = its algorithmic flops / its measured launch time.  Algorithmic
-    # work per launch in causal contraction units (D*S*(S+1) per query head):
-    # forward 2 (QK^T, PV); dK/dV 4 (QK^T recompute, dO V^T, P^T dO, dS^T Q);
-    # dQ 1 (dS K) - its QK^T and dO V^T recomputes are not counted.
-    kern = {"attn_fwd": (r["fwd_ms"], 2), "attn_bwd_dkdv": (r["dkdv_ms"], 4), "attn_bwd_dq": (r["dq_ms"], 1)}
+    # Dominant kernel: the longer of the forward and the backward's main
+    # launch (dK/dV and dQ work units in one grid); achieved = its algorithmic
+    # flops / its measured launch time.  Algorithmic work per launch in causal
+    # contraction units (D*S*(S+1) per query head): forward 2 (QK^T, PV; the
+    # forward call also holds the small partial-merge launch); backward main 5
+    # (QK^T recompute, dO V^T, P^T dO, dS^T Q, dS K) - the dQ units' second
+    # QK^T and dO V^T recomputes are not counted.
+    kern = {"attn_fwd": (r["fwd_ms"], 2), "attn_bwd_main": (r["main_ms"], 5)}
     dom = max(kern, key=lambda k: kern[k][0])
     ach = kern[dom][1] * units / (kern[dom][0] * 1e-3) / 1e12
     fwd_tf = 2 * units / (r["fwd_ms"] * 1e-3) / 1e12
@@ -257,8 +259,7 @@ def main():
         "tokens_per_s": round(c["B"] * c["S"] / (r["step_ms"] * 1e-3), 1),
         "fwd_ms": round(r["fwd_ms"], 5),
         "bwd_ms": round(r["bwd_ms"], 5),
-        "dkdv_ms": round(r["dkdv_ms"], 5),
-        "dq_ms": round(r["dq_ms"], 5),
+        "bwd_main_ms": round(r["main_ms"], 5),
         "fwd_tflops": round(fwd_tf, 2),
         "bwd_tflops": round(5 * units / (r["bwd_ms"] * 1e-3) / 1e12, 2),
         "saved_bytes": {"new": new_b, "reference": ref_b, "ratio": round(ref_b / new_b, 1)},

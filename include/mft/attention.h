@@ -117,8 +117,11 @@ mft_status mft_attn_bwd(const mft_attn_desc* desc, const void* q, const void* k,
 
 /* The backward's stages, as a bit mask for mft_attn_bwd_stage.
  *   DELTA : per-row softmax terms (delta_i = dO_i . O_i) into the workspace
- *   DKDV  : dK and dV (one launch)
- *   DQ    : dQ (one launch)
+ *   DKDV  : dK and dV
+ *   DQ    : dQ
+ *           (asked for together, DKDV and DQ run as one launch whose work
+ *           units of both kinds fill the GPU together; alone, each is one
+ *           launch of the same units)
  *   REDUCE: sums the fp32 partials of tiles split across work units, and
  *           with kv_len writes the terms of rows with no visible key
  * MAIN = DKDV | DQ.  mft_attn_bwd == mft_attn_bwd_stage(MFT_BWD_ALL).

@@ -583,16 +583,10 @@ BwdPlan plan_bwd_fast(const AttnShape& s) {
     const int64_t n_kv = bwd::fast_kv_start(S, causal, W, group, nt);  // iterations per (batch, kv head)
     const int64_t n_q = fast_q_total(S, causal, W);                    // iterations per (batch, query head)
     const int64_t pairs_kv = s.B * s.Hkv, pairs_q = s.B * s.Hq;
-    // The two roles run as separate launches: each is cut into about one
-    // unit per CU.
-    const int cus = device_cus();
-    const int64_t u_kv = balanced_units(pairs_kv, cus);
-    const int64_t u_q = balanced_units(pairs_q, cus);
+    const int64_t cus = device_cus();
     BwdPlan p;
-    // Units no shorter than 4 iterations (shorter ones leave more idle CUs
-    // than they fill when a (batch, head) holds little work: windows, short
-    // sequences), and long enough that no tile spans more than 63 units
-    // (REDUCE keeps a tile's slot list in LDS, 64 entries).
+    // Units no shorter than 4 iterations, and long enough that no tile spans
+    // more than 63 units (REDUCE keeps a tile's slot list in LDS, 64 entries).
     int64_t kv_tile_max = 0, q_tile_max = 0;
     for (int t = 0; t < nt; ++t) {
         kv_tile_max = std::max<int64_t>(kv_tile_max, bwd::fast_kv_n(S, causal, W, group, t));
@@ -600,8 +594,24 @@ BwdPlan plan_bwd_fast(const AttnShape& s) {
     }
     const int64_t kv_min = std::max<int64_t>(4, (kv_tile_max + 60) / 61);
     const int64_t q_min = std::max<int64_t>(4, (q_tile_max + 60) / 61);
-    p.kv_chunk = (int)std::min<int64_t>(n_kv, std::max<int64_t>(kv_min, (n_kv + u_kv - 1) / u_kv));
-    p.q_chunk = (int)std::min<int64_t>(n_q, std::max<int64_t>(q_min, (n_q + u_q - 1) / u_q));
+    // Both roles share one launch of about one workgroup per CU, with units
+    // of about equal duration: a dK/dV iteration (32 rows x 128 keys, four
+    // products) costs 2, a dQ iteration (128 rows x 64 keys, three products)
+    // 3.  The unit cost T is the smallest at which every unit fits in one
+    // round; fewer, longer units than one launch per role would take also
+    // mean fewer fp32 partial tiles for REDUCE.
+    const int64_t work = 2 * n_kv * pairs_kv + 3 * n_q * pairs_q;
+    auto kv_chunk = [&](int64_t T) { return std::min<int64_t>(n_kv, std::max<int64_t>(kv_min, T / 2)); };
+    auto q_chunk = [&](int64_t T) { return std::min<int64_t>(n_q, std::max<int64_t>(q_min, T / 3)); };
+    auto units = [&](int64_t T) {
+        return pairs_kv * ((n_kv + kv_chunk(T) - 1) / kv_chunk(T)) + pairs_q * ((n_q + q_chunk(T) - 1) / q_chunk(T));
+    };
+    int64_t T = std::max<int64_t>(6, (work + cus - 1) / cus);
+    // Longer units than both whole ranges change nothing; stop there.
+    const int64_t T_max = std::max(2 * n_kv, 3 * n_q);
+    while (T < T_max && units(T) > cus) T += std::max<int64_t>(1, T / 64);
+    p.kv_chunk = (int)kv_chunk(T);
+    p.q_chunk = (int)q_chunk(T);
     p.kv_units = (int)((n_kv + p.kv_chunk - 1) / p.kv_chunk);
     p.q_units = (int)((n_q + p.q_chunk - 1) / p.q_chunk);
     p.kv_parts_max = p.q_parts_max = 1;

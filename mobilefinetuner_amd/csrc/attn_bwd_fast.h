@@ -542,6 +542,23 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_bf16_fast(BwdArgs a) {
     dq_fast_body<DP, CAUSAL>(a, smem, i / bh, (i % bh) / a.Hq, (i % bh) % a.Hq);
 }
 
+// Both roles in one grid: the first kv_units * B * Hkv workgroups run dK/dV
+// units, the rest dQ units (the units of both are sized to take about equally
+// long, see plan_bwd_fast).
+template <int DP, bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_bwd_main_bf16_fast(BwdArgs a) {
+    __shared__ __attribute__((aligned(1024))) bf16 smem[BwdFastLds<DP>::ELEMS];
+    const int nkv = a.kv_units * a.B * a.Hkv;
+    const int i = (int)blockIdx.x;
+    if (i < nkv) {
+        const int bh = a.B * a.Hkv;
+        dkdv_fast_body<DP, CAUSAL>(a, smem, i / bh, (i % bh) / a.Hkv, (i % bh) % a.Hkv);
+    } else {
+        const int j = i - nkv, bh = a.B * a.Hq;
+        dq_fast_body<DP, CAUSAL>(a, smem, j / bh, (j % bh) / a.Hq, (j % bh) % a.Hq);
+    }
+}
+
 // REDUCE: sum the partial slots of every split tile in unit order.  One
 // workgroup per (batch, head, 128-row tile, 16-row group) of the dK/dV role
 // (rows = keys; dK and dV) and then of the dQ role (rows = queries);
@@ -615,14 +632,19 @@ hipError_t launch_bwd_fast(const AttnShape& s, BwdArgs a, int stages, hipStream_
                            st, a);
     }
     const BwdPlan pl = plan_bwd_fast(s);
-    if (stages & BWD_STAGE_DKDV) {
+    if ((stages & BWD_STAGE_MAIN) == BWD_STAGE_MAIN) {
+        const dim3 grid((unsigned)(pl.kv_units * s.B * s.Hkv + pl.q_units * s.B * s.Hq));
+        if (s.causal)
+            hipLaunchKernelGGL((attn_bwd_main_bf16_fast<DP, true>), grid, dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL((attn_bwd_main_bf16_fast<DP, false>), grid, dim3(256), 0, st, a);
+    } else if (stages & BWD_STAGE_DKDV) {
         const dim3 grid((unsigned)(pl.kv_units * s.B * s.Hkv));
         if (s.causal)
             hipLaunchKernelGGL((attn_bwd_dkdv_bf16_fast<DP, true>), grid, dim3(256), 0, st, a);
         else
             hipLaunchKernelGGL((attn_bwd_dkdv_bf16_fast<DP, false>), grid, dim3(256), 0, st, a);
-    }
-    if (stages & BWD_STAGE_DQ) {
+    } else if (stages & BWD_STAGE_DQ) {
         const dim3 grid((unsigned)(pl.q_units * s.B * s.Hq));
         if (s.causal)
             hipLaunchKernelGGL((attn_bwd_dq_bf16_fast<DP, true>), grid, dim3(256), 0, st, a);

@@ -71,7 +71,14 @@ hipError_t launch_attn_fwd(const AttnShape& s, const void* q, const void* k, con
 // terms; DKDV and DQ compute the gradients (writing fp32 partials for split
 // tiles); REDUCE sums the partials (and, with key padding, writes the
 // gradient terms of rows that see no key).
-enum { BWD_STAGE_DELTA = 1, BWD_STAGE_DKDV = 2, BWD_STAGE_REDUCE = 4, BWD_STAGE_DQ = 8, BWD_STAGE_ALL = 15 };
+enum {
+    BWD_STAGE_DELTA = 1,
+    BWD_STAGE_DKDV = 2,
+    BWD_STAGE_REDUCE = 4,
+    BWD_STAGE_DQ = 8,
+    BWD_STAGE_MAIN = 10,
+    BWD_STAGE_ALL = 15
+};
 
 // workspace: bwd_layout(s).total bytes.
 hipError_t launch_attn_bwd(const AttnShape& s, const void* q, const void* k, const void* v,

@@ -25,7 +25,9 @@ import sys
 
 # Kernel-name fragments -> short names used in bench.py's roofline object.
 KERNELS = {
+    "attn_fwd_combine": "attn_fwd_combine",
     "attn_fwd": "attn_fwd",
+    "attn_bwd_main": "attn_bwd_main",
     "attn_bwd_dkdv": "attn_bwd_dkdv",
     "attn_bwd_dq": "attn_bwd_dq",
     "attn_bwd_stats": "attn_bwd_stats",
