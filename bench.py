@@ -254,7 +254,9 @@ def main():
         "dtype": c["dtype"],
         "data": "synthetic: seeded Q,K,V ~ N(0,1), dO ~ N(0,0.1) (sigma), resident in HBM",
         "config": {"workload": f"{args.config}: {c['name']}", "B": c["B"], "Hq": c["Hq"], "Hkv": c["Hkv"],
-                   "S": c["S"], "D": c["D"], "causal": True, "scale": c["scale"]},
+                   "S": c["S"], "D": c["D"], "causal": True, "scale": c["scale"],
+                   **({"window": c["window"]} if c.get("window") else {}),
+                   **({"kv_len": c["lengths"]} if c.get("lengths") else {})},
         "pct_mfma_peak": round(100 * tflops / peak, 2),
         "tokens_per_s": round(c["B"] * c["S"] / (r["step_ms"] * 1e-3), 1),
         "fwd_ms": round(r["fwd_ms"], 5),

@@ -25,6 +25,9 @@ import sys
 
 # Kernel-name fragments -> short names used in bench.py's roofline object.
 KERNELS = {
+    "attn_fwd_masked_rows": "attn_fwd_masked_rows",
+    "attn_bwd_masked_dq": "attn_bwd_masked_dq",
+    "attn_bwd_masked_dkdv": "attn_bwd_masked_dkdv",
     "attn_fwd_combine": "attn_fwd_combine",
     "attn_fwd": "attn_fwd",
     "attn_bwd_main": "attn_bwd_main",
