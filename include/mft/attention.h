@@ -18,8 +18,9 @@
  *       core/ops.h:177, core/ops.cpp:2260-2335, core/backward_functions.cpp:693-726
  *
  * Conventions
- *   - Tensors are contiguous row-major [B, H, S, D] in device memory (the
- *     reference Tensor is contiguous row-major, core/tensor.h:78-237).
+ *   - Tensors are [B, H, S, D] in device memory: contiguous row-major (the
+ *     reference Tensor is contiguous row-major, core/tensor.h:78-237) unless the
+ *     descriptor gives strides (mft_strides), e.g. for [B, S, H, D] views.
  *   - q, o, dO have Hq heads; k, v, dk, dv have Hkv heads; Hq % Hkv == 0 and
  *     q-head h reads kv head h / (Hq / Hkv) (core/ops.cpp:2283-2284).
  *   - Element type of q, k, v, o, dO: MFT_F32 or MFT_BF16.  lse, dq, dk, dv
@@ -58,6 +59,16 @@ typedef enum {
 /* Values match ops::DType (core/dtype.h:9-18): kFloat32 = 0, kBFloat16 = 2. */
 typedef enum { MFT_F32 = 0, MFT_BF16 = 2 } mft_dtype;
 
+/* Element strides of an operand's batch, head and sequence dimensions; its head
+ * dim is contiguous, so element (b, h, s, d) lives at b*b + h*h + s*s + d.
+ * All zero = contiguous [B, H, S, D].  Strides let callers pass the models'
+ * [B, S, H, D] projection layout (graph/gemma_model.cpp:403-409, 506-508 and
+ * graph/qwen_model.cpp:290-299 permute it to [B, H, S, D] with a copy) as a view:
+ * b = S*H*D, h = D, s = H*D.  Every stride must be a multiple of 16 bytes. */
+typedef struct {
+    int64_t b, h, s;
+} mft_strides;
+
 typedef struct {
     int64_t B, Hq, Hkv, S, D; /* batch, query heads, kv heads, sequence, head dim     */
     float scale;              /* > 0: softmax scale; <= 0: 1/sqrt(D), as
@@ -77,6 +88,8 @@ typedef struct {
                                  graph/qwen_model.cpp:338-353; the datasets pad on
                                  the right, data/wikitext2_dataset.cpp:461-500).
                                  Values are clamped to [0, S].                        */
+    mft_strides q, k, v, o;   /* layouts of q, k, v, o (see mft_strides)              */
+    mft_strides dO, dq, dk, dv; /* layouts of dO and the gradients (backward)          */
 } mft_attn_desc;
 
 /* Rows with no visible key.  With kv_len a query row can see no key (every

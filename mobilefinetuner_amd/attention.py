@@ -20,12 +20,21 @@ def _check(t: torch.Tensor, name: str) -> None:
         raise ValueError(f"{name} must be a GPU tensor (the fused attention has no CPU path)")
     if t.dim() != 4:
         raise ValueError(f"{name} must be 4D [B,H,S,D]")
-    if not t.is_contiguous():
-        raise ValueError(f"{name} must be contiguous")
+    if t.stride(3) != 1:
+        raise ValueError(f"{name} must have a contiguous head dim (any [B,H,S] strides, e.g. a [B,S,H,D] view)")
 
 
-def _desc(q, k, scale, causal, window=0, kv_len=None):
-    """kv_len: None or an int32 [B] GPU tensor of valid keys per batch (key padding)."""
+def _strides(**ops):
+    """Element strides (b, h, s) of each non-contiguous operand for the
+    descriptor (contiguous operands take the descriptor's default)."""
+    return {n: (t.stride(0), t.stride(1), t.stride(2)) for n, t in ops.items()
+            if t is not None and not t.is_contiguous()}
+
+
+def _desc(q, k, scale, causal, window=0, kv_len=None, layouts=None):
+    """kv_len: None or an int32 [B] GPU tensor of valid keys per batch (key padding).
+    layouts: {name: tensor} of operands (q, k, v, o, dO, dq, dk, dv) whose strides
+    go into the descriptor (the others are contiguous)."""
     if q.dtype not in _DT:
         raise ValueError(f"unsupported dtype {q.dtype}")
     B, Hq, S, D = q.shape
@@ -34,7 +43,8 @@ def _desc(q, k, scale, causal, window=0, kv_len=None):
         if not kv_len.is_cuda or kv_len.dtype != torch.int32 or kv_len.shape != (B,) or not kv_len.is_contiguous():
             raise ValueError("kv_len must be a contiguous int32 GPU tensor of shape [B]")
         lp = kv_len.data_ptr()
-    return capi.desc(B, Hq, k.shape[1], S, D, scale, causal, _DT[q.dtype], window, lp)
+    return capi.desc(B, Hq, k.shape[1], S, D, scale, causal, _DT[q.dtype], window, lp,
+                     _strides(**(layouts or {})))
 
 
 def _stream():
@@ -52,22 +62,27 @@ def fwd_workspace_bytes(q, k, scale=-1.0, causal=True, window=0, kv_len=None):
 
 
 def attention_forward(q, k, v, scale: float = -1.0, causal: bool = True, want_lse: bool = True,
-                      workspace=None, balanced: bool = True, window: int = 0, kv_len=None):
+                      workspace=None, balanced: bool = True, window: int = 0, kv_len=None, out=None):
     """o, lse = fused attention forward (lse None when want_lse is False).
 
     balanced=True passes the forward workspace (allocated here unless given),
     which selects the launch that splits long query tiles across work units;
     balanced=False passes none (one workgroup per query tile).  window > 0:
     causal sliding window of that many keys; kv_len: int32 [B] GPU tensor of
-    valid (unpadded) keys per batch."""
+    valid (unpadded) keys per batch.  q, k, v (and out, the output buffer)
+    may be any [B,H,S,D] views with a contiguous head dim, e.g. transposed
+    [B,S,H,D] projections; by default o takes q's layout."""
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
         _check(t, n)
     if k.dtype != q.dtype or v.dtype != q.dtype or k.shape != v.shape:
         raise ValueError("q, k, v must share dtype and k, v must have equal shapes")
     if k.shape[0] != q.shape[0] or k.shape[2:] != q.shape[2:]:
         raise ValueError("k/v must be [B, Hkv, S, D] with q's B, S, D")
-    d = _desc(q, k, scale, causal, window, kv_len)
-    o = torch.empty_like(q)
+    o = torch.empty_like(q) if out is None else out
+    if o.shape != q.shape or o.dtype != q.dtype:
+        raise ValueError("out must have q's shape and dtype")
+    _check(o, "out")
+    d = _desc(q, k, scale, causal, window, kv_len, dict(q=q, k=k, v=v, o=o))
     lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device) if want_lse else None
     ws_ptr = None
     if balanced:
@@ -83,19 +98,21 @@ def attention_forward(q, k, v, scale: float = -1.0, causal: bool = True, want_ls
 
 def attention_backward(q, k, v, o, dO, lse, scale: float = -1.0, causal: bool = True, workspace=None,
                        window: int = 0, kv_len=None):
-    """dq, dk, dv (fp32; dk, dv already summed over the GQA group)."""
-    for t, n in ((q, "q"), (k, "k"), (v, "v"), (o, "o"), (dO, "dO"), (lse, "lse")):
-        if not t.is_cuda or not t.is_contiguous():
-            raise ValueError(f"{n} must be a contiguous GPU tensor")
+    """dq, dk, dv (fp32; dk, dv already summed over the GQA group), each in the
+    layout of q, k, v respectively (operands may be views as in attention_forward)."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (o, "o"), (dO, "dO")):
+        _check(t, n)
+    if not lse.is_cuda or not lse.is_contiguous():
+        raise ValueError("lse must be a contiguous GPU tensor")
     if dO.dtype != q.dtype or o.dtype != q.dtype or lse.dtype != torch.float32:
         raise ValueError("o and dO must have q's dtype; lse must be float32")
-    d = _desc(q, k, scale, causal, window, kv_len)
+    dq = torch.empty_like(q, dtype=torch.float32)
+    dk = torch.empty_like(k, dtype=torch.float32)
+    dv = torch.empty_like(v, dtype=torch.float32)
+    d = _desc(q, k, scale, causal, window, kv_len, dict(q=q, k=k, v=v, o=o, dO=dO, dq=dq, dk=dk, dv=dv))
     nbytes = capi.workspace_size(d)[1]
     if workspace is None or workspace.numel() < nbytes:
         workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
-    dq = torch.empty(q.shape, dtype=torch.float32, device=q.device)
-    dk = torch.empty(k.shape, dtype=torch.float32, device=q.device)
-    dv = torch.empty(v.shape, dtype=torch.float32, device=q.device)
     capi.attn_bwd(d, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dO.data_ptr(),
                   lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                   workspace.data_ptr(), _stream())

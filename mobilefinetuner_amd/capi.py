@@ -24,12 +24,20 @@ EXPORTS = (
 )
 
 
+class Strides(C.Structure):
+    """mft_strides: element strides of the batch, head and sequence dims (0,0,0 = contiguous)."""
+    _fields_ = [("b", C.c_int64), ("h", C.c_int64), ("s", C.c_int64)]
+
+
+LAYOUTS = ("q", "k", "v", "o", "dO", "dq", "dk", "dv")
+
+
 class AttnDesc(C.Structure):
     _fields_ = [
         ("B", C.c_int64), ("Hq", C.c_int64), ("Hkv", C.c_int64), ("S", C.c_int64), ("D", C.c_int64),
         ("scale", C.c_float), ("causal", C.c_int32), ("dtype", C.c_int32),
         ("window", C.c_int32), ("kv_len", C.c_void_p),
-    ]
+    ] + [(n, Strides) for n in LAYOUTS]
 
 
 class MftError(RuntimeError):
@@ -64,7 +72,7 @@ def lib():
     L.mft_repeat_kv_fwd.argtypes = [vp, vp, i64, i64, i64, i64, i64, C.c_int32, vp]
     L.mft_repeat_kv_bwd.restype = C.c_int
     L.mft_repeat_kv_bwd.argtypes = [vp, vp, i64, i64, i64, i64, i64, vp]
-    if L.mft_version() != 2:
+    if L.mft_version() != 3:
         raise RuntimeError("libmft_attn.so version mismatch")
     _lib = L
     return L
@@ -75,10 +83,18 @@ def check(status: int) -> None:
         raise MftError(status, lib().mft_last_error().decode())
 
 
-def desc(B, Hq, Hkv, S, D, scale=-1.0, causal=True, dtype=MFT_BF16, window=0, kv_len=None) -> AttnDesc:
-    """kv_len: device address of an int32 [B] array of valid keys per batch, or None."""
-    return AttnDesc(int(B), int(Hq), int(Hkv), int(S), int(D), float(scale), int(bool(causal)), int(dtype),
-                    int(window), kv_len)
+def desc(B, Hq, Hkv, S, D, scale=-1.0, causal=True, dtype=MFT_BF16, window=0, kv_len=None,
+         strides=None) -> AttnDesc:
+    """kv_len: device address of an int32 [B] array of valid keys per batch, or None.
+    strides: {name: (b, h, s)} element strides per operand (names in LAYOUTS);
+    missing operands are contiguous [B, H, S, D]."""
+    d = AttnDesc(int(B), int(Hq), int(Hkv), int(S), int(D), float(scale), int(bool(causal)), int(dtype),
+                 int(window), kv_len)
+    for name, st in (strides or {}).items():
+        if name not in LAYOUTS:
+            raise ValueError(f"unknown operand {name!r}")
+        setattr(d, name, Strides(*(int(x) for x in st)))
+    return d
 
 
 def workspace_size(d: AttnDesc):

@@ -52,8 +52,10 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(BwdArgs a) {
     const int c = threadIdx.x % TPR;
     float acc = 0.f;
     if (row < a.total_rows) {
-        const T* o = (const T*)a.o + row * a.D;
-        const T* g = (const T*)a.dO + row * a.D;
+        const int64_t bh = row / a.S, i = row % a.S;
+        const int bb = (int)(bh / a.Hq), hq = (int)(bh % a.Hq);
+        const T* o = (const T*)a.o + a.so.at(bb, hq) + i * a.so.s;
+        const T* g = (const T*)a.dO + a.sdo.at(bb, hq) + i * a.sdo.s;
         const V x = load_chunk<T>(o, c * VEC, a.D, true, a.vec_ok != 0);
         const V y = load_chunk<T>(g, c * VEC, a.D, true, a.vec_ok != 0);
 #pragma unroll
@@ -94,13 +96,13 @@ __device__ __forceinline__ void dkdv_bf16_body(const BwdArgs& a, char* smem, int
     const int key = wkey0 + n;
     const int keyc = key < S ? key : S - 1;
 
-    const bf16* K = (const bf16*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
-    const bf16* Vg = (const bf16*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
+    const bf16* K = (const bf16*)a.k + a.sk.at(b, hk);
+    const bf16* Vg = (const bf16*)a.v + a.sv.at(b, hk);
     bf16x8 kf[NC], vf[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-        kf[c] = load_chunk<bf16>(K + (int64_t)keyc * D, 16 * c + 8 * hh, D, key < S, vec_ok);
-        vf[c] = load_chunk<bf16>(Vg + (int64_t)keyc * D, 16 * c + 8 * hh, D, key < S, vec_ok);
+        kf[c] = load_chunk<bf16>(K + (int64_t)keyc * a.sk.s, 16 * c + 8 * hh, D, key < S, vec_ok);
+        vf[c] = load_chunk<bf16>(Vg + (int64_t)keyc * a.sv.s, 16 * c + 8 * hh, D, key < S, vec_ok);
     }
     f32x16 dk[NDT], dv[NDT];
 #pragma unroll
@@ -114,8 +116,8 @@ __device__ __forceinline__ void dkdv_bf16_body(const BwdArgs& a, char* smem, int
     const int qstart = CAUSAL ? j0 : 0;
     const int qend = (CAUSAL && a.window > 0) ? min(S, j0 + BNK - 1 + a.window) : S;
     for (int h = h_begin; h < h_end; ++h) {
-        const bf16* Q = (const bf16*)a.q + (int64_t)(b * a.Hq + h) * S * D;
-        const bf16* G = (const bf16*)a.dO + (int64_t)(b * a.Hq + h) * S * D;
+        const bf16* Q = (const bf16*)a.q + a.sq.at(b, h);
+        const bf16* G = (const bf16*)a.dO + a.sdo.at(b, h);
         const float* lse = a.lse + (int64_t)(b * a.Hq + h) * S;
         const float* dl = a.delta + (int64_t)(b * a.Hq + h) * S;
         for (int qb = qstart; qb < qend; qb += 32) {
@@ -129,8 +131,8 @@ __device__ __forceinline__ void dkdv_bf16_body(const BwdArgs& a, char* smem, int
                     for (int i = 0; i < 4; ++i) {
                         const int r = qb + 4 * rg + i;
                         const int rc = r < S ? r : S - 1;
-                        xq[i] = load_chunk<bf16>(Q + (int64_t)rc * D, 8 * c, D, r < S, vec_ok);
-                        xg[i] = load_chunk<bf16>(G + (int64_t)rc * D, 8 * c, D, r < S, vec_ok);
+                        xq[i] = load_chunk<bf16>(Q + (int64_t)rc * a.sq.s, 8 * c, D, r < S, vec_ok);
+                        xg[i] = load_chunk<bf16>(G + (int64_t)rc * a.sdo.s, 8 * c, D, r < S, vec_ok);
                         *reinterpret_cast<bf16x8*>(Qs + (4 * rg + i) * QSTR + 8 * c) = xq[i];
                         *reinterpret_cast<bf16x8*>(Gs + (4 * rg + i) * QSTR + 8 * c) = xg[i];
                     }
@@ -233,17 +235,17 @@ __device__ __forceinline__ void dkdv_f32_body(const BwdArgs& a, char* smem, int 
     const int wkey0 = j0 + 32 * w;
     const int key = wkey0 + n;
 
-    const float* K = (const float*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
-    const float* Vg = (const float*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
+    const float* K = (const float*)a.k + a.sk.at(b, hk);
+    const float* Vg = (const float*)a.v + a.sv.at(b, hk);
     {
         constexpr int CPR = DP / 4;
         for (int idx = tid; idx < BNK * CPR; idx += NT) {
             const int rr = idx / CPR, c = idx - rr * CPR;
             const int kr = j0 + rr, krc = kr < S ? kr : S - 1;
             *reinterpret_cast<f32x4*>(Ks + rr * STR + 4 * c) =
-                load_chunk<float>(K + (int64_t)krc * D, 4 * c, D, kr < S, vec_ok);
+                load_chunk<float>(K + (int64_t)krc * a.sk.s, 4 * c, D, kr < S, vec_ok);
             *reinterpret_cast<f32x4*>(Vs + rr * STR + 4 * c) =
-                load_chunk<float>(Vg + (int64_t)krc * D, 4 * c, D, kr < S, vec_ok);
+                load_chunk<float>(Vg + (int64_t)krc * a.sv.s, 4 * c, D, kr < S, vec_ok);
         }
     }
     f32x16 dk[NDT], dv[NDT];
@@ -259,8 +261,8 @@ __device__ __forceinline__ void dkdv_f32_body(const BwdArgs& a, char* smem, int 
     const int qstart = CAUSAL ? j0 : 0;
     const int qend = (CAUSAL && a.window > 0) ? min(S, j0 + BNK - 1 + a.window) : S;
     for (int h = h_begin; h < h_end; ++h) {
-        const float* Q = (const float*)a.q + (int64_t)(b * a.Hq + h) * S * D;
-        const float* G = (const float*)a.dO + (int64_t)(b * a.Hq + h) * S * D;
+        const float* Q = (const float*)a.q + a.sq.at(b, h);
+        const float* G = (const float*)a.dO + a.sdo.at(b, h);
         const float* lse = a.lse + (int64_t)(b * a.Hq + h) * S;
         const float* dl = a.delta + (int64_t)(b * a.Hq + h) * S;
         for (int qb = qstart; qb < qend; qb += 32) {
@@ -271,9 +273,9 @@ __device__ __forceinline__ void dkdv_f32_body(const BwdArgs& a, char* smem, int 
                     const int rr = idx / CPR, c = idx - rr * CPR;
                     const int r = qb + rr, rc = r < S ? r : S - 1;
                     *reinterpret_cast<f32x4*>(Qs + rr * STR + 4 * c) =
-                        load_chunk<float>(Q + (int64_t)rc * D, 4 * c, D, r < S, vec_ok);
+                        load_chunk<float>(Q + (int64_t)rc * a.sq.s, 4 * c, D, r < S, vec_ok);
                     *reinterpret_cast<f32x4*>(Gs + rr * STR + 4 * c) =
-                        load_chunk<float>(G + (int64_t)rc * D, 4 * c, D, r < S, vec_ok);
+                        load_chunk<float>(G + (int64_t)rc * a.sdo.s, 4 * c, D, r < S, vec_ok);
                 }
                 if (tid < 32) {
                     const int r = qb + tid;
@@ -354,15 +356,20 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int qt, in
     const int m0 = qt * BM, wrow0 = m0 + 32 * w, row = wrow0 + n;
     const int rowc = row < S ? row : S - 1;
 
-    const T* Q = (const T*)a.q + (int64_t)(b * a.Hq + h) * S * D;
-    const T* G = (const T*)a.dO + (int64_t)(b * a.Hq + h) * S * D;
-    const T* K = (const T*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
-    const T* Vg = (const T*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
-    V qf[NC], gf[NC];
+    const T* Q = (const T*)a.q + a.sq.at(b, h);
+    const T* G = (const T*)a.dO + a.sdo.at(b, h);
+    const T* K = (const T*)a.k + a.sk.at(b, hk);
+    const T* Vg = (const T*)a.v + a.sv.at(b, hk);
+    // fp32 at D > 128: this lane's dO row is re-read (L1/L2) per key tile
+    // instead of held in 128 more registers, which would spill most of the
+    // kernel's state.
+    constexpr bool GF_REG = !(sizeof(T) == 4 && DP > 128);
+    const T* grow = G + (int64_t)rowc * a.sdo.s;
+    V qf[NC], gf[GF_REG ? NC : 1];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-        qf[c] = load_chunk<T>(Q + (int64_t)rowc * D, 2 * VEC * c + VEC * hh, D, row < S, vec_ok);
-        gf[c] = load_chunk<T>(G + (int64_t)rowc * D, 2 * VEC * c + VEC * hh, D, row < S, vec_ok);
+        qf[c] = load_chunk<T>(Q + (int64_t)rowc * a.sq.s, 2 * VEC * c + VEC * hh, D, row < S, vec_ok);
+        if constexpr (GF_REG) gf[c] = load_chunk<T>(grow, 2 * VEC * c + VEC * hh, D, row < S, vec_ok);
     }
     const int64_t rbase = (int64_t)(b * a.Hq + h) * S;
     const float lse2 = row < S ? a.lse[rbase + row] * kLog2e : INFINITY;
@@ -385,9 +392,9 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int qt, in
                 const int rr = idx / CPR, c = idx - rr * CPR;
                 const int kr = kbase + rr, krc = kr < S ? kr : S - 1;
                 *reinterpret_cast<V*>(Ks + rr * L::STR + c * VEC) =
-                    load_chunk<T>(K + (int64_t)krc * D, c * VEC, D, kr < S, vec_ok);
+                    load_chunk<T>(K + (int64_t)krc * a.sk.s, c * VEC, D, kr < S, vec_ok);
                 *reinterpret_cast<V*>(Vs + rr * L::STR + c * VEC) =
-                    load_chunk<T>(Vg + (int64_t)krc * D, c * VEC, D, kr < S, vec_ok);
+                    load_chunk<T>(Vg + (int64_t)krc * a.sv.s, c * VEC, D, kr < S, vec_ok);
             }
         }
         if constexpr (L::KT) {
@@ -398,7 +405,7 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int qt, in
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int kr = kbase + 4 * kg + i, krc = kr < S ? kr : S - 1;
-                    x[i] = load_chunk<bf16>((const bf16*)K + (int64_t)krc * D, 8 * c, D, kr < S, vec_ok);
+                    x[i] = load_chunk<bf16>((const bf16*)K + (int64_t)krc * a.sk.s, 8 * c, D, kr < S, vec_ok);
                 }
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
@@ -419,7 +426,10 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int qt, in
                 const V ka = *reinterpret_cast<const V*>(Ks + (32 * kk + n) * L::STR + 2 * VEC * c + VEC * hh);
                 s = mfma_chunk(ka, qf[c], s);
                 const V va = *reinterpret_cast<const V*>(Vs + (32 * kk + n) * L::STR + 2 * VEC * c + VEC * hh);
-                dp = mfma_chunk(va, gf[c], dp);
+                if constexpr (GF_REG)
+                    dp = mfma_chunk(va, gf[c], dp);
+                else
+                    dp = mfma_chunk(va, load_chunk<T>(grow, 2 * VEC * c + VEC * hh, D, row < S, vec_ok), dp);
             }
             // lane column n = query row; register r = key kbase + 32kk + row_of_reg(r, hh)
 #pragma unroll
@@ -455,7 +465,7 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int qt, in
         }
     }
     if (row >= S) return;
-    float* dqp = a.dq + (rbase + row) * D;
+    float* dqp = a.dq + a.sdq.at(b, h) + (int64_t)row * a.sdq.s;
     const bool v4 = a.vec4_ok != 0;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
@@ -716,6 +726,14 @@ hipError_t launch_attn_bwd(const AttnShape& s, const void* q, const void* k, con
     a.causal = s.causal ? 1 : 0;
     a.window = s.window;
     a.kv_len = s.kv_len;
+    a.sq = s.q;
+    a.sk = s.k;
+    a.sv = s.v;
+    a.so = s.o;
+    a.sdo = s.dO;
+    a.sdq = s.dq;
+    a.sdk = s.dk;
+    a.sdv = s.dv;
     a.kv_part = part;
     a.q_part = lay.q_part ? reinterpret_cast<float*>(ws + lay.stats + lay.kv_part) : nullptr;
     a.q_part_stride = s.B * s.Hq * s.S * s.D;

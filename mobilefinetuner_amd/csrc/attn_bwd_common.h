@@ -32,6 +32,7 @@ struct BwdArgs {
     int vec_ok, vec4_ok;
     int window;         // causal sliding window, 0 = none
     const int* kv_len;  // [B] valid keys per batch, or null
+    Strides sq, sk, sv, so, sdo, sdq, sdk, sdv;  // operand layouts
     // fast path work units (see BwdPlan)
     int causal;
     int kv_chunk, q_chunk, kv_units, q_units;  // iterations per unit, units per (batch, head)
@@ -52,6 +53,19 @@ using ::mft::fast_q_total;
 using ::mft::fast_slots;
 using ::mft::split_slot;
 
+// Operand addressing of the fast kernels: STRIDED = false is the contiguous
+// [B, H, S, D] layout with offsets formed from the shape alone (no stride
+// state kept in registers); STRIDED = true follows the operand's Strides.
+template <bool STRIDED>
+__device__ __forceinline__ int64_t op_base(const Strides& st, int b, int h, int H, int S, int D) {
+    if constexpr (STRIDED) return st.at(b, h);
+    else return (int64_t)(b * H + h) * S * D;
+}
+template <bool STRIDED> __device__ __forceinline__ int op_ld(const Strides& st, int D) {
+    if constexpr (STRIDED) return st.s;
+    else return D;
+}
+
 // Key visibility of batch b (see KeyVis).
 __device__ __forceinline__ KeyVis key_vis(const BwdArgs& a, int b, bool causal) {
     return KeyVis{a.S, a.window, a.kv_len ? min(max(a.kv_len[b], 0), a.S) : a.S, causal};
@@ -60,10 +74,10 @@ __device__ __forceinline__ KeyVis key_vis(const BwdArgs& a, int b, bool causal) 
 // Output rows of dK / dV for a split.
 __device__ __forceinline__ void dkdv_out_rows(const BwdArgs& a, int b, int hk, int split, int key,
                                               float** dkp, float** dvp) {
-    const int64_t off = ((int64_t)(b * a.Hkv + hk) * a.S + key) * a.D;
+    const int64_t off = ((int64_t)(b * a.Hkv + hk) * a.S + key) * a.D;  // split partials: contiguous
     if (a.splits == 1) {
-        *dkp = a.dk + off;
-        *dvp = a.dv + off;
+        *dkp = a.dk + a.sdk.at(b, hk) + (int64_t)key * a.sdk.s;
+        *dvp = a.dv + a.sdv.at(b, hk) + (int64_t)key * a.sdv.s;
     } else {
         *dkp = a.part + (int64_t)split * a.part_stride + off;
         *dvp = a.part + (int64_t)(a.splits + split) * a.part_stride + off;
@@ -86,7 +100,8 @@ __device__ __forceinline__ void store_dkdv(const BwdArgs& a, float* dkp, float* 
 }
 
 // ----------------------------------------------------------------- REDUCE
-// dk = sum over splits of the dK partials (split order), same for dv.
+// dk = sum over splits of the dK partials (split order), same for dv.  The
+// partials are contiguous [B, Hkv, S, D]; dk, dv follow their layouts.
 static __global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(BwdArgs a) {
     const int64_t n = a.part_stride;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -96,8 +111,10 @@ static __global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(BwdArgs a) 
             sk += a.part[(int64_t)s * n + i];
             sv += a.part[(int64_t)(a.splits + s) * n + i];
         }
-        a.dk[i] = sk;
-        a.dv[i] = sv;
+        const int64_t d = i % a.D, row = (i / a.D) % a.S, bh = i / ((int64_t)a.D * a.S);
+        const int bb = (int)(bh / a.Hkv), hk = (int)(bh % a.Hkv);
+        a.dk[a.sdk.at(bb, hk) + row * a.sdk.s + d] = sk;
+        a.dv[a.sdv.at(bb, hk) + row * a.sdv.s + d] = sv;
     }
 }
 

@@ -37,9 +37,10 @@ __global__ __launch_bounds__(256) void attn_bwd_stats_kernel(BwdArgs a) {
     const bool valid = prow < total && i < a.S;
     float acc = 0.f;
     if (valid) {
-        const int64_t row = bh * a.S + i;
-        const V x = load_chunk<T>((const T*)a.o + row * a.D, c * VEC, a.D, true, a.vec_ok != 0);
-        const V y = load_chunk<T>((const T*)a.dO + row * a.D, c * VEC, a.D, true, a.vec_ok != 0);
+        const int bb = (int)(bh / a.Hq), hq = (int)(bh % a.Hq);
+        const V x = load_chunk<T>((const T*)a.o + a.so.at(bb, hq) + i * a.so.s, c * VEC, a.D, true, a.vec_ok != 0);
+        const V y = load_chunk<T>((const T*)a.dO + a.sdo.at(bb, hq) + i * a.sdo.s, c * VEC, a.D, true,
+                                  a.vec_ok != 0);
 #pragma unroll
         for (int k = 0; k < VEC; ++k) acc += (float)x[k] * (float)y[k];
     }
@@ -64,7 +65,7 @@ template <int DP> struct BwdFastLds {
     static constexpr int ELEMS = KV_ELEMS > Q_ELEMS ? KV_ELEMS : Q_ELEMS;
 };
 
-template <int DP, bool CAUSAL>
+template <int DP, bool CAUSAL, bool STRIDED>
 __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int unit, int b, int hk) {
     constexpr int NT = 256, BNK = 128, CPR = DP / 8, NC = DP / 16, NDT = DP / 32;
     constexpr int QT = 32 * DP;
@@ -76,8 +77,10 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
     const int i16 = lane & 15, nh = (lane >> 4) & 1;
     const int S = a.S, D = a.D, G = a.group, W = a.window;
     const KeyVis vis = key_vis(a, b, CAUSAL);
-    const bf16* K = (const bf16*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
-    const bf16* Vg = (const bf16*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
+    const bf16* K = (const bf16*)a.k + op_base<STRIDED>(a.sk, b, hk, a.Hkv, S, D);
+    const bf16* Vg = (const bf16*)a.v + op_base<STRIDED>(a.sv, b, hk, a.Hkv, S, D);
+    const int lk = op_ld<STRIDED>(a.sk, D), lv = op_ld<STRIDED>(a.sv, D);
+    const int lq = op_ld<STRIDED>(a.sq, D), lg = op_ld<STRIDED>(a.sdo, D);
 
     // This unit's chunk of the flattened (key tile, query head, query block)
     // iterations; it may start inside one key tile and end inside a later one.
@@ -118,15 +121,15 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
                 pf_nqb = fast_kv_nqb(S, CAUSAL, W, pf_kt);
             }
         }
-        const int64_t hoff = (int64_t)(b * a.Hq + h) * S * D;
-        return Pending{(const bf16*)a.q + hoff, (const bf16*)a.dO + hoff,
+        return Pending{(const bf16*)a.q + op_base<STRIDED>(a.sq, b, h, a.Hq, S, D),
+                       (const bf16*)a.dO + op_base<STRIDED>(a.sdo, b, h, a.Hq, S, D),
                        a.stats + ((int64_t)(b * a.Hq + h) * a.nqb_total + qb / 32) * 64, buf, qb};
     };
     auto issue_part = [&](const Pending& p, int j) {
         if (j < PER)
-            issue_tile_part<DP, 32, NT, SWZ_DUAL>(p.q, p.qb, S, D, p.buf, j);
+            issue_tile_part<DP, 32, NT, SWZ_DUAL>(p.q, p.qb, S, D, lq, p.buf, j);
         else if (j < 2 * PER)
-            issue_tile_part<DP, 32, NT, SWZ_DUAL>(p.g, p.qb, S, D, p.buf + QT, j - PER);
+            issue_tile_part<DP, 32, NT, SWZ_DUAL>(p.g, p.qb, S, D, lg, p.buf + QT, j - PER);
         else
             load_lds_16(p.st + 4 * i16, p.buf + 2 * QT + w * 512);
     };
@@ -144,11 +147,11 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
         const int key = t * BNK + 32 * w + n, keyc = key < S ? key : S - 1;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-            kf[c] = load_chunk<bf16>(K + (int64_t)keyc * D, 16 * c + 8 * hh, D, key < S, true);
-            if constexpr (!V_LDS) vf[c] = load_chunk<bf16>(Vg + (int64_t)keyc * D, 16 * c + 8 * hh, D, key < S, true);
+            kf[c] = load_chunk<bf16>(K + (int64_t)keyc * lk, 16 * c + 8 * hh, D, key < S, true);
+            if constexpr (!V_LDS) vf[c] = load_chunk<bf16>(Vg + (int64_t)keyc * lv, 16 * c + 8 * hh, D, key < S, true);
         }
         if constexpr (V_LDS) {
-            issue_tile<DP, BNK, NT, SWZ_ROW>(Vg, t * BNK, S, D, Vl);
+            issue_tile<DP, BNK, NT, SWZ_ROW>(Vg, t * BNK, S, D, lv, Vl);
             if (D < DP) {
                 // Staged columns >= D hold copies of column chunk 0, and so do
                 // those of the dO tiles: zero them so that dP = dO V^T sums
@@ -296,8 +299,8 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
       // tiles of 128 key rows.
       const int key = kt * BNK + 32 * w + n;
       if (key < S) {
-          const int64_t off = ((int64_t)(b * a.Hkv + hk) * S + key) * D;
-          float *dkp = a.dk + off, *dvp = a.dv + off;
+          float* dkp = a.dk + op_base<STRIDED>(a.sdk, b, hk, a.Hkv, S, D) + (int64_t)key * op_ld<STRIDED>(a.sdk, D);
+          float* dvp = a.dv + op_base<STRIDED>(a.sdv, b, hk, a.Hkv, S, D) + (int64_t)key * op_ld<STRIDED>(a.sdv, D);
           if (fast_slots(kstart, kn, a.kv_chunk) > 1) {
               const int64_t slot = (int64_t)(b * a.Hkv + hk) * 2 * a.kv_units + 2 * unit + (first ? 0 : 1);
               dkp = a.kv_part + (slot * 2 * BNK + (32 * w + n)) * D;
@@ -324,7 +327,7 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
     }
 }
 
-template <int DP, bool CAUSAL>
+template <int DP, bool CAUSAL, bool STRIDED>
 __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int unit, int b, int h) {
     constexpr int NT = 256, BN = 64, BM = 128, CPR = DP / 8, NC = DP / 16, NDT = DP / 32, NKK = BN / 32;
     constexpr int TILE = BN * DP;
@@ -340,10 +343,11 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
     const int S = a.S, D = a.D, W = a.window;
     const KeyVis vis = key_vis(a, b, CAUSAL);
     const int hk = h / a.group;
-    const bf16* K = (const bf16*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
-    const bf16* Vg = (const bf16*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
-    const bf16* Q = (const bf16*)a.q + (int64_t)(b * a.Hq + h) * S * D;
-    const bf16* G = (const bf16*)a.dO + (int64_t)(b * a.Hq + h) * S * D;
+    const bf16* K = (const bf16*)a.k + op_base<STRIDED>(a.sk, b, hk, a.Hkv, S, D);
+    const bf16* Vg = (const bf16*)a.v + op_base<STRIDED>(a.sv, b, hk, a.Hkv, S, D);
+    const bf16* Q = (const bf16*)a.q + op_base<STRIDED>(a.sq, b, h, a.Hq, S, D);
+    const bf16* G = (const bf16*)a.dO + op_base<STRIDED>(a.sdo, b, h, a.Hq, S, D);
+    const int lk = op_ld<STRIDED>(a.sk, D), lv = op_ld<STRIDED>(a.sv, D);
 
     // This unit's chunk of the flattened (query tile, key tile) iterations.
     const int64_t g0 = (int64_t)unit * a.q_chunk;
@@ -366,8 +370,8 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
     };
     {
         const int kt0 = next_key_tile();
-        issue_tile<DP, BN, NT, SWZ_DUAL>(K, kt0 * BN, S, D, smem);
-        issue_tile<DP, BN, NT, SWZ_ROW>(Vg, kt0 * BN, S, D, smem + TILE);
+        issue_tile<DP, BN, NT, SWZ_DUAL>(K, kt0 * BN, S, D, lk, smem);
+        issue_tile<DP, BN, NT, SWZ_ROW>(Vg, kt0 * BN, S, D, lv, smem + TILE);
     }
 
     bf16x8 qf[NC], gf[NC];
@@ -376,8 +380,8 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
         const int row = t * BM + 32 * w + n, rowc = row < S ? row : S - 1;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-            qf[c] = load_chunk<bf16>(Q + (int64_t)rowc * D, 16 * c + 8 * hh, D, row < S, true);
-            gf[c] = load_chunk<bf16>(G + (int64_t)rowc * D, 16 * c + 8 * hh, D, row < S, true);
+            qf[c] = load_chunk<bf16>(Q + (int64_t)rowc * op_ld<STRIDED>(a.sq, D), 16 * c + 8 * hh, D, row < S, true);
+            gf[c] = load_chunk<bf16>(G + (int64_t)rowc * op_ld<STRIDED>(a.sdo, D), 16 * c + 8 * hh, D, row < S, true);
         }
         const float* blk = a.stats + ((int64_t)(b * a.Hq + h) * a.nqb_total + rowc / 32) * 64;
         lse2 = row < S ? blk[rowc % 32] : INFINITY;
@@ -415,7 +419,10 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
             const int c = p ^ (v ? swz<CPR, SWZ_ROW>(r) : swz<CPR, SWZ_DUAL>(r));
             const int gr = min(ktn * BN + r, S - 1);
             const int col = 8 * c < D ? 8 * c : 0;
-            load_lds_16((v ? Vg : K) + (int64_t)gr * D + col, (v ? nbuf + TILE : nbuf) + m * 512);
+            if constexpr (STRIDED)
+                load_lds_16((v ? Vg : K) + (gr * (v ? lv : lk) + col), (v ? nbuf + TILE : nbuf) + m * 512);
+            else
+                load_lds_16((v ? Vg : K) + (int64_t)gr * D + col, (v ? nbuf + TILE : nbuf) + m * 512);
         };
         const int kbase = (qlo + (int)(g0 + i - qstart)) * BN;
         const int wrow0 = qt * BM + 32 * w, row = wrow0 + n;
@@ -498,8 +505,7 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
       // writes dQ, otherwise slot (unit - first unit of qt).
       const int row = qt * BM + 32 * w + n;
       if (row < S) {
-          const int64_t off = ((int64_t)(b * a.Hq + h) * S + row) * D;
-          float* dqp = a.dq + off;
+          float* dqp = a.dq + op_base<STRIDED>(a.sdq, b, h, a.Hq, S, D) + (int64_t)row * op_ld<STRIDED>(a.sdq, D);
           if (fast_slots(qstart, qn, a.q_chunk) > 1) {
               const int64_t slot = (int64_t)(b * a.Hq + h) * 2 * a.q_units + 2 * unit + (first ? 0 : 1);
               dqp = a.q_part + (slot * BM + 32 * w + n) * D;
@@ -528,34 +534,34 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
 }
 
 // One workgroup per unit; unit u of every (batch, head) precedes unit u+1.
-template <int DP, bool CAUSAL>
+template <int DP, bool CAUSAL, bool STRIDED>
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_bf16_fast(BwdArgs a) {
     __shared__ __attribute__((aligned(1024))) bf16 smem[BwdFastLds<DP>::KV_ELEMS];
     const int bh = a.B * a.Hkv, i = (int)blockIdx.x;
-    dkdv_fast_body<DP, CAUSAL>(a, smem, i / bh, (i % bh) / a.Hkv, (i % bh) % a.Hkv);
+    dkdv_fast_body<DP, CAUSAL, STRIDED>(a, smem, i / bh, (i % bh) / a.Hkv, (i % bh) % a.Hkv);
 }
 
-template <int DP, bool CAUSAL>
+template <int DP, bool CAUSAL, bool STRIDED>
 __global__ __launch_bounds__(256) void attn_bwd_dq_bf16_fast(BwdArgs a) {
     __shared__ __attribute__((aligned(1024))) bf16 smem[BwdFastLds<DP>::Q_ELEMS];
     const int bh = a.B * a.Hq, i = (int)blockIdx.x;
-    dq_fast_body<DP, CAUSAL>(a, smem, i / bh, (i % bh) / a.Hq, (i % bh) % a.Hq);
+    dq_fast_body<DP, CAUSAL, STRIDED>(a, smem, i / bh, (i % bh) / a.Hq, (i % bh) % a.Hq);
 }
 
 // Both roles in one grid: the first kv_units * B * Hkv workgroups run dK/dV
 // units, the rest dQ units (the units of both are sized to take about equally
 // long, see plan_bwd_fast).
-template <int DP, bool CAUSAL>
+template <int DP, bool CAUSAL, bool STRIDED>
 __global__ __launch_bounds__(256) void attn_bwd_main_bf16_fast(BwdArgs a) {
     __shared__ __attribute__((aligned(1024))) bf16 smem[BwdFastLds<DP>::ELEMS];
     const int nkv = a.kv_units * a.B * a.Hkv;
     const int i = (int)blockIdx.x;
     if (i < nkv) {
         const int bh = a.B * a.Hkv;
-        dkdv_fast_body<DP, CAUSAL>(a, smem, i / bh, (i % bh) / a.Hkv, (i % bh) % a.Hkv);
+        dkdv_fast_body<DP, CAUSAL, STRIDED>(a, smem, i / bh, (i % bh) / a.Hkv, (i % bh) % a.Hkv);
     } else {
         const int j = i - nkv, bh = a.B * a.Hq;
-        dq_fast_body<DP, CAUSAL>(a, smem, j / bh, (j % bh) / a.Hq, (j % bh) % a.Hq);
+        dq_fast_body<DP, CAUSAL, STRIDED>(a, smem, j / bh, (j % bh) / a.Hq, (j % bh) % a.Hq);
     }
 }
 
@@ -612,14 +618,18 @@ __global__ __launch_bounds__(256) void attn_bwd_fast_reduce(BwdArgs a) {
     __syncthreads();
     const int r = threadIdx.x / 16;
     if (r0 + r >= S) return;
-    const int64_t row = (int64_t)bh * S + r0 + r;
+    const int64_t row = r0 + r;
     const int64_t rit = rg * kRedRows + r;  // row inside the tile
     if (kv) {
         // slot layout [dK rows 0..127][dV rows 0..127]
-        reduce_rows(a.kv_part, slot_of, nsl, 2 * 128 * (int64_t)D, rit, D, a.dk + row * D);
-        reduce_rows(a.kv_part, slot_of, nsl, 2 * 128 * (int64_t)D, 128 + rit, D, a.dv + row * D);
+        const int bb = bh / a.Hkv, hk = bh % a.Hkv;
+        reduce_rows(a.kv_part, slot_of, nsl, 2 * 128 * (int64_t)D, rit, D,
+                    a.dk + a.sdk.at(bb, hk) + row * a.sdk.s);
+        reduce_rows(a.kv_part, slot_of, nsl, 2 * 128 * (int64_t)D, 128 + rit, D,
+                    a.dv + a.sdv.at(bb, hk) + row * a.sdv.s);
     } else {
-        reduce_rows(a.q_part, slot_of, nsl, 128 * (int64_t)D, rit, D, a.dq + row * D);
+        const int bb = bh / a.Hq, h = bh % a.Hq;
+        reduce_rows(a.q_part, slot_of, nsl, 128 * (int64_t)D, rit, D, a.dq + a.sdq.at(bb, h) + row * a.sdq.s);
     }
 }
 
@@ -632,25 +642,27 @@ hipError_t launch_bwd_fast(const AttnShape& s, BwdArgs a, int stages, hipStream_
                            st, a);
     }
     const BwdPlan pl = plan_bwd_fast(s);
+    const bool strided = !s.contiguous;
+    // (causal, strided) -> instantiation
+#define MFT_BWD_LAUNCH(KERNEL, GRID)                                                      \
+    do {                                                                                  \
+        if (s.causal && strided)                                                          \
+            hipLaunchKernelGGL((KERNEL<DP, true, true>), GRID, dim3(256), 0, st, a);      \
+        else if (s.causal)                                                                \
+            hipLaunchKernelGGL((KERNEL<DP, true, false>), GRID, dim3(256), 0, st, a);     \
+        else if (strided)                                                                 \
+            hipLaunchKernelGGL((KERNEL<DP, false, true>), GRID, dim3(256), 0, st, a);     \
+        else                                                                              \
+            hipLaunchKernelGGL((KERNEL<DP, false, false>), GRID, dim3(256), 0, st, a);    \
+    } while (0)
     if ((stages & BWD_STAGE_MAIN) == BWD_STAGE_MAIN) {
-        const dim3 grid((unsigned)(pl.kv_units * s.B * s.Hkv + pl.q_units * s.B * s.Hq));
-        if (s.causal)
-            hipLaunchKernelGGL((attn_bwd_main_bf16_fast<DP, true>), grid, dim3(256), 0, st, a);
-        else
-            hipLaunchKernelGGL((attn_bwd_main_bf16_fast<DP, false>), grid, dim3(256), 0, st, a);
+        MFT_BWD_LAUNCH(attn_bwd_main_bf16_fast, dim3((unsigned)(pl.kv_units * s.B * s.Hkv + pl.q_units * s.B * s.Hq)));
     } else if (stages & BWD_STAGE_DKDV) {
-        const dim3 grid((unsigned)(pl.kv_units * s.B * s.Hkv));
-        if (s.causal)
-            hipLaunchKernelGGL((attn_bwd_dkdv_bf16_fast<DP, true>), grid, dim3(256), 0, st, a);
-        else
-            hipLaunchKernelGGL((attn_bwd_dkdv_bf16_fast<DP, false>), grid, dim3(256), 0, st, a);
+        MFT_BWD_LAUNCH(attn_bwd_dkdv_bf16_fast, dim3((unsigned)(pl.kv_units * s.B * s.Hkv)));
     } else if (stages & BWD_STAGE_DQ) {
-        const dim3 grid((unsigned)(pl.q_units * s.B * s.Hq));
-        if (s.causal)
-            hipLaunchKernelGGL((attn_bwd_dq_bf16_fast<DP, true>), grid, dim3(256), 0, st, a);
-        else
-            hipLaunchKernelGGL((attn_bwd_dq_bf16_fast<DP, false>), grid, dim3(256), 0, st, a);
+        MFT_BWD_LAUNCH(attn_bwd_dq_bf16_fast, dim3((unsigned)(pl.q_units * s.B * s.Hq)));
     }
+#undef MFT_BWD_LAUNCH
     if ((stages & BWD_STAGE_REDUCE) && (pl.kv_parts_max > 1 || pl.q_parts_max > 1)) {
         const int64_t nt = (s.S + 127) / 128;
         const int64_t blocks = (s.B * s.Hkv + s.B * s.Hq) * nt * (128 / kRedRows);

@@ -45,6 +45,38 @@ mft_status check_desc(const mft_attn_desc* d, mft::AttnShape* s) {
         return fail(MFT_ERR_INVALID_ARG, "mft_attn: a sliding window needs causal = 1 (j <= i && i - j < window)");
     if ((reinterpret_cast<uintptr_t>(d->kv_len) & 3u) != 0)
         return fail(MFT_ERR_INVALID_ARG, "mft_attn: kv_len must be 4-byte aligned");
+    const int64_t esize = d->dtype == MFT_BF16 ? 2 : 4;
+    struct Named {
+        const mft_strides* st;
+        const char* name;
+        int64_t H;
+        int64_t esz;
+    };
+    const Named layouts[] = {{&d->q, "q", d->Hq, esize},  {&d->k, "k", d->Hkv, esize}, {&d->v, "v", d->Hkv, esize},
+                             {&d->o, "o", d->Hq, esize},  {&d->dO, "dO", d->Hq, esize}, {&d->dq, "dq", d->Hq, 4},
+                             {&d->dk, "dk", d->Hkv, 4},  {&d->dv, "dv", d->Hkv, 4}};
+    mft::Strides* out[] = {&s->q, &s->k, &s->v, &s->o, &s->dO, &s->dq, &s->dk, &s->dv};
+    s->contiguous = true;
+    for (int i = 0; i < 8; ++i) {
+        const mft_strides& st = *layouts[i].st;
+        const mft::Strides dense{layouts[i].H * d->S * d->D, d->S * d->D, (int)d->D};
+        if ((st.b == 0 && st.h == 0 && st.s == 0) || (st.b == dense.b && st.h == dense.h && st.s == dense.s)) {
+            *out[i] = dense;  // contiguous [B, H, S, D]
+            continue;
+        }
+        const int64_t unit = 16 / layouts[i].esz;  // 16-byte rows
+        if (st.b <= 0 || st.h <= 0 || st.s <= 0 || st.b % unit || st.h % unit || st.s % unit)
+            return fail(MFT_ERR_INVALID_ARG, std::string("mft_attn: strides of ") + layouts[i].name +
+                                                 " must be positive multiples of 16 bytes (or all zero)");
+        if (st.s < d->D)
+            return fail(MFT_ERR_INVALID_ARG, std::string("mft_attn: sequence stride of ") + layouts[i].name +
+                                                 " is shorter than a row (D)");
+        if ((d->S - 1) * st.s + d->D > (int64_t(1) << 31) - 1)
+            return fail(MFT_ERR_UNSUPPORTED, std::string("mft_attn: one (batch, head) block of ") + layouts[i].name +
+                                                 " spans 2^31 elements or more");
+        *out[i] = mft::Strides{st.b, st.h, (int)st.s};
+        s->contiguous = false;
+    }
     s->B = d->B;
     s->Hq = d->Hq;
     s->Hkv = d->Hkv;
@@ -71,7 +103,7 @@ mft_status hip_status(hipError_t e, const char* what) {
 
 extern "C" {
 
-int mft_version(void) { return 2; }
+int mft_version(void) { return 3; }
 
 const char* mft_last_error(void) { return g_last_error.c_str(); }
 

@@ -272,14 +272,14 @@ __device__ __forceinline__ int tile_off(int r, int col) {
 }
 
 // Issue the direct loads of a [ROWS x DP] bf16 tile whose first global row is
-// row0 (row stride D elements) into a swizzled LDS tile.  NT threads share
+// row0 (row stride ld elements, D valid columns) into a swizzled LDS tile.  NT threads share
 // the work; every thread issues ROWS*DP/8/NT loads (wave-uniform count).
 // Rows >= S read row S-1 and chunks >= D read chunk 0, so every address is
 // in bounds; callers mask such rows and never use such columns.
 // Load j (0 <= j < ROWS*DP/8/NT) of this thread's share of such a tile, so
 // that a tile's loads can be spread between other instructions.
 template <int DP, int ROWS, int NT, int SWZ>
-__device__ __forceinline__ void issue_tile_part(const bf16* __restrict__ src, int row0, int S, int D,
+__device__ __forceinline__ void issue_tile_part(const bf16* __restrict__ src, int row0, int S, int D, int ld,
                                                 bf16* lds_tile, int j) {
     constexpr int CPR = DP / 8;
     constexpr int PER_WAVE = ROWS * CPR / NT;
@@ -292,15 +292,15 @@ __device__ __forceinline__ void issue_tile_part(const bf16* __restrict__ src, in
     const int c = p ^ swz<CPR, SWZ>(r);
     const int gr = min(row0 + r, S - 1);
     const int col = 8 * c < D ? 8 * c : 0;
-    load_lds_16(src + (int64_t)gr * D + col, lds_tile + m * 512);
+    load_lds_16(src + (int64_t)gr * ld + col, lds_tile + m * 512);
 }
 
 template <int DP, int ROWS, int NT, int SWZ>
-__device__ __forceinline__ void issue_tile(const bf16* __restrict__ src, int row0, int S, int D,
+__device__ __forceinline__ void issue_tile(const bf16* __restrict__ src, int row0, int S, int D, int ld,
                                            bf16* lds_tile) {
     constexpr int PER_WAVE = ROWS * (DP / 8) / NT;
 #pragma unroll
-    for (int j = 0; j < PER_WAVE; ++j) issue_tile_part<DP, ROWS, NT, SWZ>(src, row0, S, D, lds_tile, j);
+    for (int j = 0; j < PER_WAVE; ++j) issue_tile_part<DP, ROWS, NT, SWZ>(src, row0, S, D, ld, lds_tile, j);
 }
 
 }  // namespace mft

@@ -42,6 +42,7 @@ struct FwdArgs {
     int vec4_ok;       // D % 4 == 0
     int window;              // causal sliding window, 0 = none
     const int* kv_len;       // [B] valid keys per batch, or null
+    Strides sq, sk, sv, so;  // layouts of q, k, v, o
     // balanced launch (bf16 fast path with a workspace; see FwdPlan)
     int chunk;               // iterations per unit
     int units;               // units per (batch, head)
@@ -82,14 +83,15 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
     const int row = wrow0 + n;
     const int rowc = row < S ? row : S - 1;
 
-    const T* __restrict__ Q = (const T*)a.q + (int64_t)(b * a.Hq + h) * S * D;
-    const T* __restrict__ K = (const T*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
-    const T* __restrict__ Vg = (const T*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
+    const T* __restrict__ Q = (const T*)a.q + a.sq.at(b, h);
+    const T* __restrict__ K = (const T*)a.k + a.sk.at(b, hk);
+    const T* __restrict__ Vg = (const T*)a.v + a.sv.at(b, hk);
+    const int lq = a.sq.s, lk = a.sk.s, lv = a.sv.s;
 
     V qf[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c)
-        qf[c] = load_chunk<T>(Q + (int64_t)rowc * D, 2 * VEC * c + VEC * hh, D, row < S, vec_ok);
+        qf[c] = load_chunk<T>(Q + (int64_t)rowc * lq, 2 * VEC * c + VEC * hh, D, row < S, vec_ok);
 
     f32x16 oacc[NDT];
 #pragma unroll
@@ -113,7 +115,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
                 const int key = kbase + rr;
                 const int keyc = key < S ? key : S - 1;
                 *reinterpret_cast<V*>(Ks + rr * L::KSTR + c * VEC) =
-                    load_chunk<T>(K + (int64_t)keyc * D, c * VEC, D, key < S, vec_ok);
+                    load_chunk<T>(K + (int64_t)keyc * lk, c * VEC, D, key < S, vec_ok);
             }
         }
         if constexpr (L::VT) {  // stage V transposed: 4 keys x 8 columns per item
@@ -125,7 +127,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
                 for (int i = 0; i < 4; ++i) {
                     const int key = kbase + 4 * kg + i;
                     const int keyc = key < S ? key : S - 1;
-                    x[i] = load_chunk<bf16>((const bf16*)Vg + (int64_t)keyc * D, 8 * c, D, key < S, vec_ok);
+                    x[i] = load_chunk<bf16>((const bf16*)Vg + (int64_t)keyc * lv, 8 * c, D, key < S, vec_ok);
                 }
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
@@ -140,7 +142,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
                 const int key = kbase + rr;
                 const int keyc = key < S ? key : S - 1;
                 *reinterpret_cast<V*>(Vs + rr * L::VSTR + c * VEC) =
-                    load_chunk<T>(Vg + (int64_t)keyc * D, c * VEC, D, key < S, vec_ok);
+                    load_chunk<T>(Vg + (int64_t)keyc * lv, c * VEC, D, key < S, vec_ok);
             }
         }
         __syncthreads();
@@ -232,7 +234,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
     // A row that sees no key at all (key padding) gets O = 0 and LSE = +inf
     // here; attn_fwd_masked_rows then writes the reference's output for it.
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    T* O = (T*)a.o + (int64_t)(b * a.Hq + h) * S * D + (int64_t)row * D;
+    T* O = (T*)a.o + a.so.at(b, h) + (int64_t)row * a.so.s;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -391,11 +393,12 @@ __device__ __forceinline__ void fwd_fast_tile(const FwdArgs& a, const bf16* Kb, 
 
 // This lane's query row: Q fragments (B operand of S^T).
 template <int DP>
-__device__ __forceinline__ void fwd_load_q(const bf16* Q, int row, int S, int D, bf16x8 (&qf)[DP / 16]) {
+__device__ __forceinline__ void fwd_load_q(const bf16* Q, int ld, int row, int S, int D, bf16x8 (&qf)[DP / 16]) {
     const int hh = (threadIdx.x & 63) >> 5;
     const int rowc = row < S ? row : S - 1;
 #pragma unroll
-    for (int c = 0; c < DP / 16; ++c) qf[c] = load_chunk<bf16>(Q + (int64_t)rowc * D, 16 * c + 8 * hh, D, row < S, true);
+    for (int c = 0; c < DP / 16; ++c)
+        qf[c] = load_chunk<bf16>(Q + (int64_t)rowc * ld, 16 * c + 8 * hh, D, row < S, true);
 }
 
 // Normalised O row and its LSE (rows < S; call with the wave's l_tot).  A
@@ -406,7 +409,7 @@ __device__ __forceinline__ void fwd_store_row(const FwdArgs& a, int b, int h, in
                                               float m_run, float l_tot) {
     const int hh = (threadIdx.x & 63) >> 5;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    bf16* O = (bf16*)a.o + (int64_t)(b * a.Hq + h) * a.S * a.D + (int64_t)row * a.D;
+    bf16* O = (bf16*)a.o + a.so.at(b, h) + (int64_t)row * a.so.s;
 #pragma unroll
     for (int dt = 0; dt < DP / 32; ++dt)
 #pragma unroll
@@ -433,19 +436,20 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_fast(FwdArgs a) {
     const int wrow0 = m0 + 32 * w;
     const int row = wrow0 + n;
 
-    const bf16* __restrict__ Q = (const bf16*)a.q + (int64_t)(b * a.Hq + h) * S * D;
-    const bf16* __restrict__ K = (const bf16*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
-    const bf16* __restrict__ Vg = (const bf16*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
+    const bf16* __restrict__ Q = (const bf16*)a.q + a.sq.at(b, h);
+    const bf16* __restrict__ K = (const bf16*)a.k + a.sk.at(b, hk);
+    const bf16* __restrict__ Vg = (const bf16*)a.v + a.sv.at(b, hk);
+    const int lq = a.sq.s, lk = a.sk.s, lv = a.sv.s;
 
     const KeyVis vis{S, a.window, a.kv_len ? min(max(a.kv_len[b], 0), S) : S, CAUSAL};
     const int vlo = vis.lo(row), vhi = vis.hi(row);
     const int t0 = fast_q_lo(CAUSAL, a.window, qt);
     const int ntiles = t0 + fast_q_n(S, CAUSAL, a.window, qt);
-    issue_tile<DP, BN, NT, SWZ_ROW>(K, t0 * BN, S, D, smem);
-    issue_tile<DP, BN, NT, SWZ_TR>(Vg, t0 * BN, S, D, smem + TILE);
+    issue_tile<DP, BN, NT, SWZ_ROW>(K, t0 * BN, S, D, lk, smem);
+    issue_tile<DP, BN, NT, SWZ_TR>(Vg, t0 * BN, S, D, lv, smem + TILE);
 
     bf16x8 qf[NC];
-    fwd_load_q<DP>(Q, row, S, D, qf);
+    fwd_load_q<DP>(Q, lq, row, S, D, qf);
     wait_vmcnt<0>();  // Q complete before the loop (direct loads are untracked)
     f32x16 oacc[NDT];
 #pragma unroll
@@ -467,9 +471,9 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_fast(FwdArgs a) {
         const int nrow = t + 1 < ntiles ? (t + 1) * BN : t0 * BN;
         auto issue_part = [&](int j) {
             if (j < FwdLoads<DP>::PER)
-                issue_tile_part<DP, BN, NT, SWZ_ROW>(K, nrow, S, D, nb, j);
+                issue_tile_part<DP, BN, NT, SWZ_ROW>(K, nrow, S, D, lk, nb, j);
             else
-                issue_tile_part<DP, BN, NT, SWZ_TR>(Vg, nrow, S, D, nb + TILE, j - FwdLoads<DP>::PER);
+                issue_tile_part<DP, BN, NT, SWZ_TR>(Vg, nrow, S, D, lv, nb + TILE, j - FwdLoads<DP>::PER);
         };
         const int kbase = t * BN;
         if (wave_uniform(wrow0 < S && vis.any(wrow0, min(wrow0 + 31, S - 1), kbase, kbase + BN - 1))) {
@@ -502,9 +506,10 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
     const int bh = a.B * a.Hq, blk = (int)blockIdx.x;
     const int unit = blk / bh, b = (blk % bh) / a.Hq, h = (blk % bh) % a.Hq, hk = h / a.group;
 
-    const bf16* __restrict__ Q = (const bf16*)a.q + (int64_t)(b * a.Hq + h) * S * D;
-    const bf16* __restrict__ K = (const bf16*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
-    const bf16* __restrict__ Vg = (const bf16*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
+    const bf16* __restrict__ Q = (const bf16*)a.q + a.sq.at(b, h);
+    const bf16* __restrict__ K = (const bf16*)a.k + a.sk.at(b, hk);
+    const bf16* __restrict__ Vg = (const bf16*)a.v + a.sv.at(b, hk);
+    const int lq = a.sq.s, lk = a.sk.s, lv = a.sv.s;
 
     const int W = a.window;
     const KeyVis vis{S, W, a.kv_len ? min(max(a.kv_len[b], 0), S) : S, CAUSAL};
@@ -529,8 +534,8 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
     };
     {
         const int t0 = next_key_tile();
-        issue_tile<DP, BN, NT, SWZ_ROW>(K, t0 * BN, S, D, smem);
-        issue_tile<DP, BN, NT, SWZ_TR>(Vg, t0 * BN, S, D, smem + TILE);
+        issue_tile<DP, BN, NT, SWZ_ROW>(K, t0 * BN, S, D, lk, smem);
+        issue_tile<DP, BN, NT, SWZ_TR>(Vg, t0 * BN, S, D, lv, smem + TILE);
     }
 
     bf16x8 qf[NC];
@@ -539,7 +544,7 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
     int64_t qstart = fast_q_start(S, CAUSAL, W, qt);
     int qn = fast_q_n(S, CAUSAL, W, qt);
     int qlo = fast_q_lo(CAUSAL, W, qt);
-    fwd_load_q<DP>(Q, qt * BM + 32 * w + n, S, D, qf);
+    fwd_load_q<DP>(Q, lq, qt * BM + 32 * w + n, S, D, qf);
     wait_vmcnt<0>();  // Q complete before the loop (direct loads are untracked)
 
     for (int i = 0, first = 1;; first = 0) {
@@ -560,9 +565,9 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
             const int nrow = i + 1 < niter ? next_key_tile() * BN : 0;
             auto issue_part = [&](int j) {
                 if (j < FwdLoads<DP>::PER)
-                    issue_tile_part<DP, BN, NT, SWZ_ROW>(K, nrow, S, D, nb, j);
+                    issue_tile_part<DP, BN, NT, SWZ_ROW>(K, nrow, S, D, lk, nb, j);
                 else
-                    issue_tile_part<DP, BN, NT, SWZ_TR>(Vg, nrow, S, D, nb + TILE, j - FwdLoads<DP>::PER);
+                    issue_tile_part<DP, BN, NT, SWZ_TR>(Vg, nrow, S, D, lv, nb + TILE, j - FwdLoads<DP>::PER);
             };
             const int kbase = (qlo + (int)(g0 + i - qstart)) * BN;
             if (wave_uniform(wrow0 < S && vis.any(wrow0, min(wrow0 + 31, S - 1), kbase, kbase + BN - 1))) {
@@ -605,7 +610,7 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
         qstart = fast_q_start(S, CAUSAL, W, qt);
         qn = fast_q_n(S, CAUSAL, W, qt);
         qlo = fast_q_lo(CAUSAL, W, qt);
-        fwd_load_q<DP>(Q, qt * BM + 32 * w + n, S, D, qf);
+        fwd_load_q<DP>(Q, lq, qt * BM + 32 * w + n, S, D, qf);
         wait_vmcnt<0>();
     }
 }
@@ -679,7 +684,7 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(FwdArgs a) {
         for (int j = 0; j < MAXJ; ++j) acc[j] += x[j] * wp;
     }
     const float il = inv_l[r];
-    bf16* O = (bf16*)a.o + (int64_t)bh * S * D + (int64_t)(r0 + r) * D;
+    bf16* O = (bf16*)a.o + a.so.at(bh / a.Hq, bh % a.Hq) + (int64_t)(r0 + r) * a.so.s;
 #pragma unroll
     for (int j = 0; j < MAXJ; ++j) {
         const int c = cl + 16 * j;
@@ -798,6 +803,10 @@ hipError_t launch_attn_fwd(const AttnShape& s, const void* q, const void* k, con
     a.vec4_ok = (s.D % 4) == 0;
     a.window = s.window;
     a.kv_len = s.kv_len;
+    a.sq = s.q;
+    a.sk = s.k;
+    a.sv = s.v;
+    a.so = s.o;
     a.chunk = 0;
     a.units = 0;
     a.part_o = nullptr;

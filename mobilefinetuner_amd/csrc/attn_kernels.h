@@ -7,6 +7,16 @@
 
 namespace mft {
 
+// Element strides of a [B, H, S, D] operand's batch, head and sequence
+// dimensions; the head dim is contiguous.  Element (b, h, s, d) lives at
+// b * b_ + h * h_ + s * s_ + d.  Offsets inside one (b, h) block fit in 32
+// bits (checked by the C ABI), so the row stride is an int.
+struct Strides {
+    int64_t b, h;
+    int s;
+    __host__ __device__ int64_t at(int64_t bi, int64_t hi) const { return bi * b + hi * h; }
+};
+
 struct AttnShape {
     int64_t B, Hq, Hkv, S, D;
     float scale;   // resolved (> 0)
@@ -14,6 +24,9 @@ struct AttnShape {
     bool bf16;     // element type of q, k, v, o, dO
     int window;              // causal sliding window (keys), 0 = none; normalised: 0 < window < S
     const int32_t* kv_len;   // device [B] valid keys per batch (right padding), or null
+    // Resolved layouts (contiguous [B, H, S, D] unless the caller gave strides).
+    Strides q, k, v, o, dO, dq, dk, dv;
+    bool contiguous;  // every operand contiguous [B, H, S, D]
 };
 
 // Tile geometry of one kernel variant, exposed so that the C ABI can size

@@ -40,6 +40,7 @@ struct MaskedArgs {
     const int* kv_len;
     int B, Hq, Hkv, S, D, group, window, causal;
     float scale;
+    Strides sq, sk, sv, so, sdo, sdq, sdk, sdv;  // operand layouts
 };
 
 // Rows [first, S) of a batch see no key; T_i as above.
@@ -75,19 +76,20 @@ __global__ __launch_bounds__(256) void attn_fwd_masked_rows(MaskedArgs a) {
     const MaskedRows mr = masked_rows(a, b);
     const int r0 = max((int)blockIdx.x * 64, mr.first()), r1 = min((int)blockIdx.x * 64 + 64, S);
     if (r0 >= r1 || d >= D) return;
-    const T* V = (const T*)a.v + (int64_t)(b * a.Hkv + hk) * S * D + d;
+    const T* V = (const T*)a.v + a.sv.at(b, hk) + d;
+    const int64_t lv = a.sv.s;
     double pre = 0.0;
-    for (int j = 0; j < mr.len; ++j) pre += ld(V + (int64_t)j * D);
+    for (int j = 0; j < mr.len; ++j) pre += ld(V + (int64_t)j * lv);
     int lo = mr.tlo(r0), hi = mr.thi(r0);
     double win = 0.0;
-    for (int j = lo; j <= hi; ++j) win += ld(V + (int64_t)j * D);
+    for (int j = lo; j <= hi; ++j) win += ld(V + (int64_t)j * lv);
     for (int i = r0; i < r1; ++i) {
         const int nlo = mr.tlo(i), nhi = mr.thi(i);
-        for (; hi < nhi; ++hi) win += ld(V + (int64_t)(hi + 1) * D);
-        for (; lo < nlo; ++lo) win -= ld(V + (int64_t)lo * D);
+        for (; hi < nhi; ++hi) win += ld(V + (int64_t)(hi + 1) * lv);
+        for (; lo < nlo; ++lo) win -= ld(V + (int64_t)lo * lv);
         const float o = (float)((pre + win) / (double)mr.count(i));
         for (int h = hk * a.group; h < (hk + 1) * a.group; ++h)
-            ((T*)a.o)[((int64_t)(b * a.Hq + h) * S + i) * D + d] = (T)o;
+            ((T*)a.o)[a.so.at(b, h) + (int64_t)i * a.so.s + d] = (T)o;
     }
 }
 
@@ -120,10 +122,10 @@ __global__ __launch_bounds__(256) void attn_bwd_masked_dq(MaskedArgs a) {
 template <typename T>
 __device__ void masked_dq_row(const MaskedArgs& a, const MaskedRows& mr, int b, int h, int i) {
     const int S = a.S, D = a.D, lane = threadIdx.x & 63, hk = h / a.group;
-    const int64_t ri = ((int64_t)b * a.Hq + h) * S + i;
+    const int64_t ri = ((int64_t)b * a.Hq + h) * S + i;  // row-term index (contiguous scratch)
     float g[4], o[4];
-    load_row4((const T*)a.dO + ri * D, D, g);
-    load_row4((const T*)a.o + ri * D, D, o);
+    load_row4((const T*)a.dO + a.sdo.at(b, h) + (int64_t)i * a.sdo.s, D, g);
+    load_row4((const T*)a.o + a.so.at(b, h) + (int64_t)i * a.so.s, D, o);
     const bool nz = __any(g[0] != 0.f || g[1] != 0.f || g[2] != 0.f || g[3] != 0.f);
     const float dl = wave_sum(dot4(g, o));
     if (lane == 0) {
@@ -131,21 +133,21 @@ __device__ void masked_dq_row(const MaskedArgs& a, const MaskedRows& mr, int b, 
         a.row_delta[ri] = dl;
     }
     if (!nz) return;  // dq_i = 0, as the main pass left it
-    const T* K = (const T*)a.k + (int64_t)(b * a.Hkv + hk) * S * D;
-    const T* V = (const T*)a.v + (int64_t)(b * a.Hkv + hk) * S * D;
+    const T* K = (const T*)a.k + a.sk.at(b, hk);
+    const T* V = (const T*)a.v + a.sv.at(b, hk);
     const float inv_c = 1.f / (float)mr.count(i);
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     auto key = [&](int j) {
         float vj[4], kj[4];
-        load_row4(V + (int64_t)j * D, D, vj);
-        load_row4(K + (int64_t)j * D, D, kj);
+        load_row4(V + (int64_t)j * a.sv.s, D, vj);
+        load_row4(K + (int64_t)j * a.sk.s, D, kj);
         const float ds = (wave_sum(dot4(g, vj)) - dl) * inv_c;
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[c] += ds * kj[c];
     };
     for (int j = 0; j < mr.len; ++j) key(j);
     for (int j = mr.tlo(i); j <= mr.thi(i); ++j) key(j);
-    float* dq = a.dq + ri * D;
+    float* dq = a.dq + a.sdq.at(b, h) + (int64_t)i * a.sdq.s;
 #pragma unroll
     for (int c = 0; c < 4; ++c)
         if (lane + 64 * c < D) dq[lane + 64 * c] = acc[c] * a.scale;
@@ -177,9 +179,8 @@ __device__ void masked_dkdv_key(const MaskedArgs& a, const MaskedRows& mr, int b
         if (mr.W > 0) i_hi = min(i_hi, j + mr.W - 1);
     }
     if (i_lo > i_hi) return;
-    const int64_t kvoff = ((int64_t)(b * a.Hkv + hk) * S + j) * D;
     float vj[4];
-    load_row4((const T*)a.v + kvoff, D, vj);
+    load_row4((const T*)a.v + a.sv.at(b, hk) + (int64_t)j * a.sv.s, D, vj);
     float ak[4] = {0.f, 0.f, 0.f, 0.f}, av[4] = {0.f, 0.f, 0.f, 0.f};
     bool any = false;
     for (int h = hk * a.group; h < (hk + 1) * a.group; ++h) {
@@ -193,8 +194,8 @@ __device__ void masked_dkdv_key(const MaskedArgs& a, const MaskedRows& mr, int b
                 any = true;
                 const int64_t ri = bh * S + i;
                 float g[4], q[4];
-                load_row4((const T*)a.dO + ri * D, D, g);
-                load_row4((const T*)a.q + ri * D, D, q);
+                load_row4((const T*)a.dO + a.sdo.at(b, h) + (int64_t)i * a.sdo.s, D, g);
+                load_row4((const T*)a.q + a.sq.at(b, h) + (int64_t)i * a.sq.s, D, q);
                 const float inv_c = 1.f / (float)mr.count(i);
                 const float ds = (wave_sum(dot4(g, vj)) - a.row_delta[ri]) * inv_c;
 #pragma unroll
@@ -206,11 +207,13 @@ __device__ void masked_dkdv_key(const MaskedArgs& a, const MaskedRows& mr, int b
         }
     }
     if (!any) return;
+    float* dk = a.dk + a.sdk.at(b, hk) + (int64_t)j * a.sdk.s;
+    float* dv = a.dv + a.sdv.at(b, hk) + (int64_t)j * a.sdv.s;
 #pragma unroll
     for (int c = 0; c < 4; ++c)
         if (lane + 64 * c < D) {
-            a.dk[kvoff + lane + 64 * c] += ak[c] * a.scale;
-            a.dv[kvoff + lane + 64 * c] += av[c];
+            dk[lane + 64 * c] += ak[c] * a.scale;
+            dv[lane + 64 * c] += av[c];
         }
 }
 
@@ -226,6 +229,14 @@ MaskedArgs masked_args(const AttnShape& s) {
     a.window = s.window;
     a.causal = s.causal ? 1 : 0;
     a.scale = s.scale;
+    a.sq = s.q;
+    a.sk = s.k;
+    a.sv = s.v;
+    a.so = s.o;
+    a.sdo = s.dO;
+    a.sdq = s.dq;
+    a.sdk = s.dk;
+    a.sdv = s.dv;
     return a;
 }
 

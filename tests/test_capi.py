@@ -53,7 +53,7 @@ def test_every_header_symbol_is_exported(capi):
 def test_header_compiles_as_c(tmp_path):
     """The header is plain C (extern "C", C99 types, no torch types)."""
     src = tmp_path / "t.c"
-    src.write_text('#include "mft/attention.h"\nint main(void){return mft_version()==2?0:1;}\n')
+    src.write_text('#include "mft/attention.h"\nint main(void){return mft_version()==3?0:1;}\n')
     res = subprocess.run(["gcc", "-std=c99", "-fsyntax-only", "-D__HIP_PLATFORM_AMD__",
                           "-I", os.path.join(ROOT, "include"), "-I", "/opt/rocm/include", str(src)],
                          capture_output=True, text=True)
@@ -61,7 +61,7 @@ def test_header_compiles_as_c(tmp_path):
 
 
 def test_version(capi):
-    assert capi.lib().mft_version() == 2
+    assert capi.lib().mft_version() == 3
 
 
 def _err(capi, fn):
@@ -140,3 +140,26 @@ def test_window_and_padding_workspace(capi):
     assert win[1] > 0
     pad = capi.workspace_size(capi.desc(1, 4, 1, 4096, 256, 1 / 16, True, capi.MFT_BF16, kv_len=1 << 20))
     assert pad[1] == base[1] + 2 * 4 * 4 * 4096 and pad[0] == base[0]
+
+
+@pytest.mark.parametrize("strides,needle", [
+    ({"q": (4096 * 64, 64, 64 * 4 + 4)}, "multiples of 16 bytes"),   # sequence stride 260 bf16 = 520 B
+    ({"k": (1, 0, 0)}, "multiples of 16 bytes"),
+    ({"dq": (4096 * 64, 64, 32)}, "shorter than a row"),
+])
+def test_stride_validation(capi, strides, needle):
+    """Operand layouts: every stride a positive multiple of 16 bytes, and a
+    sequence stride of at least one row; all-zero means contiguous."""
+    d = capi.desc(1, 4, 1, 4096, 64, 0.125, True, capi.MFT_BF16, strides=strides)
+    e = _err(capi, lambda: capi.workspace_size(d))
+    assert e.status == capi.MFT_ERR_INVALID_ARG and needle in str(e)
+
+
+def test_strided_layout_accepted(capi):
+    """[B,S,H,D] storage passed as [B,H,S,D] views (b = S*H*D, h = D, s = H*D)."""
+    B, H, S, D = 2, 4, 256, 64
+    st = (S * H * D, D, H * D)
+    d = capi.desc(B, H, 1, S, D, 0.125, True, capi.MFT_BF16,
+                  strides={n: st for n in ("q", "o", "dO")} | {"dq": st})
+    f, b = capi.workspace_size(d)
+    assert b == capi.workspace_size(capi.desc(B, H, 1, S, D, 0.125, True, capi.MFT_BF16))[1]
