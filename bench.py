@@ -7,9 +7,10 @@
 A step is one forward plus one backward of the attention over the config's
 synthetic batch (inputs resident in HBM).  Prints ONE JSON line.  `value` is
 the algorithmic causal throughput  7*B*H*D*S*(S+1) / step time  in TFLOP/s
-`mask_variants` adds the same measurement for the
-masks the model graphs use: Gemma's sliding window (c5w512) and right-padded
-batches (c4pad); their flops count the visible (query, key) pairs only.  The roofline object covers the dominant kernel,
+`variants` adds the same measurement for the
+masks the model graphs use - Gemma's sliding window (c5w512) and right-padded
+batches (c4pad); their flops count the visible (query, key) pairs only - and
+for the [B,S,H,D] operand layout (c5bshd).  The roofline object covers the dominant kernel,
 timed live with HIP events on the stream the kernels run on.  The
 cpu_baseline object times the reference CPU operators (oracle/_ref, compiled
 from the reference sources) on a bounded sample of the same workload.
@@ -49,6 +50,9 @@ CONFIGS = {
     "c4pad": dict(B=4, Hq=4, Hkv=1, D=256, S=1024, dtype="bf16", scale=1 / 16, do_sigma=0.1,
                   lengths=[1024, 700, 400, 130],
                   name="Gemma-3-270M-shaped fwd+bwd with right-padded sequences, bf16"),
+    # The models' [B,S,H,D] projection layout passed as strided views (no permute copies).
+    "c5bshd": dict(B=1, Hq=4, Hkv=1, D=256, S=4096, dtype="bf16", scale=1 / 16, do_sigma=0.1, layout="bshd",
+                   name="Gemma-3-1B-shaped GQA attention fwd+bwd on [B,S,H,D] views, bf16"),
 }
 
 
@@ -98,6 +102,8 @@ def gpu_leg(cfg_id, steps, warmup):
     k = torch.randn(B, Hkv, S, D, device=dev, generator=g).to(dt)
     v = torch.randn(B, Hkv, S, D, device=dev, generator=g).to(dt)
     dO = (torch.randn(B, Hq, S, D, device=dev, generator=g) * c["do_sigma"]).to(dt)
+    if c.get("layout") == "bshd":  # [B,S,H,D] storage, passed as [B,H,S,D] views
+        q, k, v, dO = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (q, k, v, dO))
     scale = c["scale"]
     window = c.get("window", 0)
     kv_len = torch.tensor(c["lengths"], dtype=torch.int32, device=dev) if c.get("lengths") else None
@@ -106,10 +112,10 @@ def gpu_leg(cfg_id, steps, warmup):
     fws = torch.empty(max(fws_n, 1), dtype=torch.uint8, device=dev)
     o = torch.empty_like(q)
     lse = torch.empty(B, Hq, S, dtype=torch.float32, device=dev)
-    dq = torch.empty(q.shape, dtype=torch.float32, device=dev)
-    dk = torch.empty(k.shape, dtype=torch.float32, device=dev)
-    dv = torch.empty(v.shape, dtype=torch.float32, device=dev)
-    d = A._desc(q, k, scale, True, window, kv_len)
+    dq = torch.empty_like(q, dtype=torch.float32)
+    dk = torch.empty_like(k, dtype=torch.float32)
+    dv = torch.empty_like(v, dtype=torch.float32)
+    d = A._desc(q, k, scale, True, window, kv_len, dict(q=q, k=k, v=v, o=o, dO=dO, dq=dq, dk=dk, dv=dv))
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
     P = [t.data_ptr() for t in (q, k, v, o, dO, lse, dq, dk, dv, ws)]
@@ -213,7 +219,7 @@ def main():
     ap.add_argument("--config", default="c5", choices=sorted(CONFIGS))
     ap.add_argument("--all-configs", action="store_true", help="also report every config (extra key)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-variants", action="store_true", help="skip the mask variants (mask_variants key)")
+    ap.add_argument("--no-variants", action="store_true", help="skip the mask and layout variants (variants key)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain copy of COPY_BYTES (for scaling rocprofv3 FETCH/WRITE_SIZE)")
     args = ap.parse_args()
@@ -256,7 +262,8 @@ def main():
         "config": {"workload": f"{args.config}: {c['name']}", "B": c["B"], "Hq": c["Hq"], "Hkv": c["Hkv"],
                    "S": c["S"], "D": c["D"], "causal": True, "scale": c["scale"],
                    **({"window": c["window"]} if c.get("window") else {}),
-                   **({"kv_len": c["lengths"]} if c.get("lengths") else {})},
+                   **({"kv_len": c["lengths"]} if c.get("lengths") else {}),
+                   **({"layout": c["layout"]} if c.get("layout") else {})},
         "pct_mfma_peak": round(100 * tflops / peak, 2),
         "tokens_per_s": round(c["B"] * c["S"] / (r["step_ms"] * 1e-3), 1),
         "fwd_ms": round(r["fwd_ms"], 5),
@@ -269,18 +276,19 @@ def main():
                      "unit": "TFLOP/s", "frac": round(ach / peak, 4), "traffic": traffic},
     }
     variants = {}
-    for cid in () if args.no_variants else ("c5w512", "c4pad"):
+    for cid in () if args.no_variants else ("c5w512", "c4pad", "c5bshd"):
         cc = CONFIGS[cid]
         rr = gpu_leg(cid, max(10, args.steps // 2), 5)
         u = rr["units"]
         tf = 7 * u / (rr["step_ms"] * 1e-3) / 1e12
         variants[cid] = {"workload": cc["name"], "window": cc.get("window", 0), "lengths": cc.get("lengths"),
+                         "layout": cc.get("layout", "bhsd"),
                          "ms_per_step": round(rr["step_ms"], 5), "fwd_ms": round(rr["fwd_ms"], 5),
                          "bwd_ms": round(rr["bwd_ms"], 5), "tflops": round(tf, 2),
                          "pct_peak": round(100 * tf / PEAK_TFLOPS[cc["dtype"]], 2),
                          "tokens_per_s": round(cc["B"] * cc["S"] / (rr["step_ms"] * 1e-3), 1)}
     if variants:
-        out["mask_variants"] = variants
+        out["variants"] = variants
     if args.all_configs:
         per = {}
         for cid in ("c1", "c2", "c3", "c4", "c5", "c5f32"):
