@@ -64,7 +64,11 @@ typedef enum { MFT_F32 = 0, MFT_BF16 = 2 } mft_dtype;
  * All zero = contiguous [B, H, S, D].  Strides let callers pass the models'
  * [B, S, H, D] projection layout (graph/gemma_model.cpp:403-409, 506-508 and
  * graph/qwen_model.cpp:290-299 permute it to [B, H, S, D] with a copy) as a view:
- * b = S*H*D, h = D, s = H*D.  Every stride must be a multiple of 16 bytes. */
+ * b = S*H*D, h = D, s = H*D.  Every stride must be a multiple of 16 bytes.
+ * The bf16 backward's fast kernels need k and v to share the sequence stride
+ * (as contiguous tensors, [B, S, Hkv, D] views and fused-QKV slices do);
+ * otherwise the general kernels run, with the same results to the tolerance
+ * and at lower speed. */
 typedef struct {
     int64_t b, h, s;
 } mft_strides;

@@ -573,7 +573,10 @@ int padded_d(int64_t D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 
 
 }  // namespace
 
-bool bwd_fast_path(const AttnShape& s) { return s.bf16 && s.D % 8 == 0 && s.D > 32; }
+// The fast bf16 kernels; they take K and V with one sequence stride (true of
+// contiguous operands, [B, S, Hkv, D] views and fused-QKV slices), other
+// layouts run the general kernels.
+bool bwd_fast_path(const AttnShape& s) { return s.bf16 && s.D % 8 == 0 && s.D > 32 && s.k.s == s.v.s; }
 
 // Compute units of the current device (256 on MI355X), cached per device.
 int device_cus() {

@@ -79,7 +79,10 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
     const KeyVis vis = key_vis(a, b, CAUSAL);
     const bf16* K = (const bf16*)a.k + op_base<STRIDED>(a.sk, b, hk, a.Hkv, S, D);
     const bf16* Vg = (const bf16*)a.v + op_base<STRIDED>(a.sv, b, hk, a.Hkv, S, D);
-    const int lk = op_ld<STRIDED>(a.sk, D), lv = op_ld<STRIDED>(a.sv, D);
+    // K and V share one sequence stride on this path (bwd_fast_path): a
+    // second stride live across the loop costs the dK/dV accumulators their
+    // registers (the compiler then shuffles them every block).
+    const int lk = op_ld<STRIDED>(a.sk, D), lv = lk;
     const int lq = op_ld<STRIDED>(a.sq, D), lg = op_ld<STRIDED>(a.sdo, D);
 
     // This unit's chunk of the flattened (key tile, query head, query block)
@@ -347,7 +350,7 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
     const bf16* Vg = (const bf16*)a.v + op_base<STRIDED>(a.sv, b, hk, a.Hkv, S, D);
     const bf16* Q = (const bf16*)a.q + op_base<STRIDED>(a.sq, b, h, a.Hq, S, D);
     const bf16* G = (const bf16*)a.dO + op_base<STRIDED>(a.sdo, b, h, a.Hq, S, D);
-    const int lk = op_ld<STRIDED>(a.sk, D), lv = op_ld<STRIDED>(a.sv, D);
+    const int lk = op_ld<STRIDED>(a.sk, D), lv = lk;  // one K/V sequence stride, as in dkdv_fast_body
 
     // This unit's chunk of the flattened (query tile, key tile) iterations.
     const int64_t g0 = (int64_t)unit * a.q_chunk;

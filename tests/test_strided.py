@@ -73,3 +73,32 @@ def test_fused_qkv_slices(orc, dev):
     assert torch.equal(o1, o2.contiguous()) and torch.equal(l1, l2)
     for a, b in zip(g1, g2):
         assert torch.equal(a, b.contiguous())
+
+
+@pytest.mark.parametrize("which", ["k", "v"])
+def test_kv_with_different_sequence_strides(orc, dev, which):
+    """k and v with different sequence strides (one a [B,S,Hkv,D] view, the
+    other contiguous): the bf16 backward then runs the general kernels (the
+    fast ones take one K/V sequence stride); held to the fp32 reference."""
+    import torch
+    from gpu_util import TOL, to_dev
+    from mobilefinetuner_amd import attention as A
+    B, Hq, Hkv, S, D = 2, 4, 2, 260, 128
+    print(f"[case] strided {which} only", flush=True)
+    q, k, v, dO = orc.make_inputs(B, Hq, Hkv, S, D, 77, "bf16", do_sigma=0.5)
+    scale = 1.0 / np.sqrt(D)
+    ref = orc.composite(q, k, v, dO, scale=scale, causal=True, want_lse=True)
+    cq, ck, cv, cg = (to_dev(x, "bf16", dev) for x in (q, k, v, dO))
+    if which == "k":
+        ck = _bshd(k, dev, "bf16")
+    else:
+        cv = _bshd(v, dev, "bf16")
+    assert ck.stride(2) != cv.stride(2)
+    o, lse = A.attention_forward(cq, ck, cv, scale, True)
+    dq, dk, dv = A.attention_backward(cq, ck, cv, o, cg, lse, scale, True)
+    torch.cuda.synchronize()
+    got = dict(o=o.float(), dq=dq, dk=dk, dv=dv)
+    for n in ("o", "dq", "dk", "dv"):
+        e = orc.max_rel(got[n].contiguous().cpu().numpy(), ref[n])
+        print(f"[errs] {n} {e:.2e}", flush=True)
+        assert e <= TOL["bf16"], (n, e)
