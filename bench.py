@@ -10,7 +10,9 @@ the algorithmic causal throughput  7*B*H*D*S*(S+1) / step time  in TFLOP/s
 `variants` adds the same measurement for the
 masks the model graphs use - Gemma's sliding window (c5w512) and right-padded
 batches (c4pad); their flops count the visible (query, key) pairs only - and
-for the [B,S,H,D] operand layout (c5bshd).  The roofline object covers the dominant kernel,
+for the [B,S,H,D] operand layout (c5bshd).  `prologue` times the fused q/k
+norm + RoPE pass at the config's q and k shapes against the HBM roofline.
+The roofline object covers the dominant kernel,
 timed live with HIP events on the stream the kernels run on.  The
 cpu_baseline object times the reference CPU operators (oracle/_ref, compiled
 from the reference sources) on a bounded sample of the same workload.
@@ -156,6 +158,70 @@ def gpu_leg(cfg_id, steps, warmup):
     return dict(step_ms=step_ms, fwd_ms=fwd_ms, bwd_ms=bwd_ms, main_ms=main_ms, units=units)
 
 
+def prologue_leg(cfg_id, steps, warmup):
+    """The fused q/k prologue (norm + RoPE) at a config's q and k shapes, on
+    [B,S,H,D] projection outputs viewed [B,H,S,D] (Gemma-3: rms_norm with
+    (1 + w), eps 1e-6, rope_theta 1e6), bf16 x/y, fp32 dy/dx.  HBM-bound:
+    algorithmic bytes per element are 2 (x) + 2 (y) forward and 2 (x) + 4 (dy)
+    + 4 (dx) backward, plus the [waves, D] dw partials written and re-read."""
+    import torch
+    from mobilefinetuner_amd import attention as A
+    from mobilefinetuner_amd import capi
+
+    c = CONFIGS[cfg_id]
+    dev = torch.device("cuda:0")
+    B, S, D = c["B"], c["S"], c["D"]
+    g = torch.Generator(device=dev)
+    g.manual_seed(77)
+    sp = torch.cuda.current_stream().cuda_stream
+    calls, fwd_bytes, bwd_bytes = [], 0, 0
+    for H in (c["Hq"], c["Hkv"]):
+        x = torch.randn(B, S, H, D, device=dev, generator=g).to(torch.bfloat16).transpose(1, 2)
+        w = 0.3 * torch.randn(D, device=dev, generator=g)
+        dy = torch.randn(B, S, H, D, device=dev, generator=g).transpose(1, 2)
+        y = torch.empty(B, H, S, D, dtype=torch.bfloat16, device=dev)
+        dx = torch.empty(B, H, S, D, dtype=torch.float32, device=dev)
+        dw = torch.empty(D, dtype=torch.float32, device=dev)
+        d = A._prologue_desc(x, "gemma", 1e-6, 1e6, dict(x=x, dy=dy))
+        wsb = capi.prologue_workspace_size(d)
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+        n = B * H * S * D
+        fwd_bytes += 4 * n
+        bwd_bytes += 10 * n + 2 * wsb
+        calls.append((d, x, w, y, dy, dx, dw, ws))
+
+    def fwd():
+        for d, x, w, y, *_ in calls:
+            capi.prologue_fwd(d, x.data_ptr(), w.data_ptr(), y.data_ptr(), sp)
+
+    def bwd():
+        for d, x, w, y, dy, dx, dw, ws in calls:
+            capi.prologue_bwd(d, x.data_ptr(), w.data_ptr(), dy.data_ptr(), dx.data_ptr(), dw.data_ptr(),
+                              ws.data_ptr(), sp)
+
+    def timed(fn, n):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    for _ in range(warmup):
+        fwd()
+        bwd()
+    f_ms, b_ms = timed(fwd, steps), timed(bwd, steps)
+    return {"workload": f"q/k rms_norm(1+w) + RoPE of {cfg_id} (Hq {c['Hq']} + Hkv {c['Hkv']} heads, S {S}, D {D}), "
+                        "[B,S,H,D] bf16 in, [B,H,S,D] out",
+            "fwd_us": round(f_ms * 1e3, 2), "bwd_us": round(b_ms * 1e3, 2),
+            "fwd_GBps": round(fwd_bytes / (f_ms * 1e-3) / 1e9, 1), "bwd_GBps": round(bwd_bytes / (b_ms * 1e-3) / 1e9, 1),
+            "fwd_frac_hbm": round(fwd_bytes / (f_ms * 1e-3) / 8e12, 4),
+            "bwd_frac_hbm": round(bwd_bytes / (b_ms * 1e-3) / 8e12, 4),
+            "fwd_bytes": fwd_bytes, "bwd_bytes": bwd_bytes, "launches": {"fwd": 2, "bwd": 4}}
+
+
 COPY_BYTES = 1 << 30
 
 
@@ -289,6 +355,8 @@ def main():
                          "tokens_per_s": round(cc["B"] * cc["S"] / (rr["step_ms"] * 1e-3), 1)}
     if variants:
         out["variants"] = variants
+    if not args.no_variants:
+        out["prologue"] = prologue_leg(args.config, max(20, args.steps), 5)
     if args.all_configs:
         per = {}
         for cid in ("c1", "c2", "c3", "c4", "c5", "c5f32"):

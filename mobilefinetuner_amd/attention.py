@@ -155,3 +155,70 @@ class FusedAttention(torch.autograd.Function):
         dq, dk, dv = attention_backward(q, k, v, o, dO.contiguous().to(q.dtype), lse, ctx.scale, ctx.causal,
                                         window=ctx.window, kv_len=ctx.kv_len)
         return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None
+
+
+# ------------------------------------------------------------ q/k prologue
+_NORMS = {"none": capi.MFT_NORM_NONE, "gemma": capi.MFT_NORM_GEMMA, "affine": capi.MFT_NORM_AFFINE}
+
+
+def _prologue_desc(x, norm, eps, theta, layouts):
+    if x.dtype not in _DT:
+        raise ValueError(f"unsupported dtype {x.dtype}")
+    if norm not in _NORMS:
+        raise ValueError(f"norm must be one of {sorted(_NORMS)}")
+    B, H, S, D = x.shape
+    return capi.prologue_desc(B, H, S, D, _DT[x.dtype], _NORMS[norm], eps, theta, _strides(**layouts))
+
+
+def prologue_forward(x, w=None, norm="gemma", eps=1e-6, theta=10000.0, out=None):
+    """y = rope(norm(x)) for x [B, H, S, D] (any [B, H, S] strides with a
+    contiguous head dim, e.g. the [B, S, H, D] projection output viewed as
+    [B, H, S, D]).  y is a new contiguous [B, H, S, D] tensor of x's dtype
+    unless `out` is given.  norm: "gemma" (ops::rms_norm, x / rms * (1 + w)),
+    "affine" (ops::rms_norm_affine) or "none"; theta 0 = no RoPE."""
+    _check(x, "x")
+    y = torch.empty(x.shape, dtype=x.dtype, device=x.device) if out is None else out
+    _check(y, "y")
+    if w is not None and (not w.is_cuda or w.dtype != torch.float32 or not w.is_contiguous()):
+        raise ValueError("w must be a contiguous fp32 GPU tensor [D]")
+    d = _prologue_desc(x, norm, eps, theta, dict(x=x, y=y))
+    capi.prologue_fwd(d, x.data_ptr(), None if w is None else w.data_ptr(), y.data_ptr(), _stream())
+    return y
+
+
+def prologue_backward(x, w, dy, norm="gemma", eps=1e-6, theta=10000.0, want_dw=True):
+    """(dx, dw) for y = rope(norm(x)): dx fp32 contiguous [B, H, S, D], dw fp32
+    [D] (None without a norm or when want_dw is False)."""
+    _check(x, "x")
+    _check(dy, "dy")
+    if dy.dtype != torch.float32:
+        raise ValueError("dy must be fp32")
+    dx = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+    d = _prologue_desc(x, norm, eps, theta, dict(x=x, dy=dy))
+    dw = ws = None
+    if norm != "none" and want_dw:
+        dw = torch.empty(x.shape[3], dtype=torch.float32, device=x.device)
+        ws = torch.empty(max(capi.prologue_workspace_size(d), 1), dtype=torch.uint8, device=x.device)
+    capi.prologue_bwd(d, x.data_ptr(), None if w is None else w.data_ptr(), dy.data_ptr(), dx.data_ptr(),
+                      None if dw is None else dw.data_ptr(), None if ws is None else ws.data_ptr(), _stream())
+    return dx, dw
+
+
+class QKPrologue(torch.autograd.Function):
+    """Autograd node of y = rope(norm(x)); saves x and w only (the row norms
+    are recomputed in the backward, as the reference's RMSNormBackward does)."""
+
+    @staticmethod
+    def forward(ctx, x, w=None, norm="gemma", eps=1e-6, theta=10000.0):
+        y = prologue_forward(x, w, norm, eps, theta)
+        ctx.save_for_backward(x, w)
+        ctx.cfg = (norm, eps, theta)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w = ctx.saved_tensors
+        norm, eps, theta = ctx.cfg
+        dx, dw = prologue_backward(x, w, dy.float(), norm, eps, theta,
+                                   want_dw=w is not None and ctx.needs_input_grad[1])
+        return dx.to(x.dtype), dw, None, None, None

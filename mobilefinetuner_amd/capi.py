@@ -1,4 +1,5 @@
-"""ctypes binding of the C ABI in ``include/mft/attention.h``.
+"""ctypes binding of the C ABI in ``include/mft/attention.h`` and
+``include/mft/prologue.h``.
 
 This is the binding a Python caller would use (the C++ finetune_ops adapter
 links the same library directly).  It raises when the library is missing: the
@@ -17,10 +18,13 @@ MFT_F32, MFT_BF16 = 0, 2
 MFT_BWD_DELTA, MFT_BWD_DKDV, MFT_BWD_REDUCE, MFT_BWD_DQ = 1, 2, 4, 8
 MFT_BWD_MAIN, MFT_BWD_ALL = 10, 15
 
-# Every symbol the header declares (checked by tests/test_capi.py).
+MFT_NORM_NONE, MFT_NORM_GEMMA, MFT_NORM_AFFINE = 0, 1, 2
+
+# Every symbol the headers declare (checked by tests/test_capi.py).
 EXPORTS = (
     "mft_attn_workspace_size", "mft_attn_fwd", "mft_attn_bwd", "mft_attn_bwd_stage",
     "mft_repeat_kv_fwd", "mft_repeat_kv_bwd", "mft_last_error", "mft_version",
+    "mft_prologue_fwd", "mft_prologue_workspace_size", "mft_prologue_bwd",
 )
 
 
@@ -38,6 +42,13 @@ class AttnDesc(C.Structure):
         ("scale", C.c_float), ("causal", C.c_int32), ("dtype", C.c_int32),
         ("window", C.c_int32), ("kv_len", C.c_void_p),
     ] + [(n, Strides) for n in LAYOUTS]
+
+
+class PrologueDesc(C.Structure):
+    _fields_ = [
+        ("B", C.c_int64), ("H", C.c_int64), ("S", C.c_int64), ("D", C.c_int64),
+        ("dtype", C.c_int32), ("norm", C.c_int32), ("eps", C.c_float), ("theta", C.c_float),
+    ] + [(n, Strides) for n in ("x", "y", "dy", "dx")]
 
 
 class MftError(RuntimeError):
@@ -72,6 +83,12 @@ def lib():
     L.mft_repeat_kv_fwd.argtypes = [vp, vp, i64, i64, i64, i64, i64, C.c_int32, vp]
     L.mft_repeat_kv_bwd.restype = C.c_int
     L.mft_repeat_kv_bwd.argtypes = [vp, vp, i64, i64, i64, i64, i64, vp]
+    L.mft_prologue_fwd.restype = C.c_int
+    L.mft_prologue_fwd.argtypes = [C.POINTER(PrologueDesc), vp, vp, vp, vp]
+    L.mft_prologue_workspace_size.restype = C.c_int
+    L.mft_prologue_workspace_size.argtypes = [C.POINTER(PrologueDesc), C.POINTER(C.c_size_t)]
+    L.mft_prologue_bwd.restype = C.c_int
+    L.mft_prologue_bwd.argtypes = [C.POINTER(PrologueDesc), vp, vp, vp, vp, vp, vp, vp]
     if L.mft_version() != 3:
         raise RuntimeError("libmft_attn.so version mismatch")
     _lib = L
@@ -121,3 +138,28 @@ def repeat_kv_fwd(kv, out, B, Hkv, S, D, r, dtype, stream) -> None:
 
 def repeat_kv_bwd(g, dkv, B, Hkv, S, D, r, stream) -> None:
     check(lib().mft_repeat_kv_bwd(g, dkv, B, Hkv, S, D, r, stream))
+
+
+def prologue_desc(B, H, S, D, dtype=MFT_BF16, norm=MFT_NORM_GEMMA, eps=1e-6, theta=10000.0,
+                  strides=None) -> PrologueDesc:
+    """strides: {name: (b, h, s)} element strides of x, y, dy, dx (missing = contiguous [B, H, S, D])."""
+    d = PrologueDesc(int(B), int(H), int(S), int(D), int(dtype), int(norm), float(eps), float(theta))
+    for name, st in (strides or {}).items():
+        if name not in ("x", "y", "dy", "dx"):
+            raise ValueError(f"unknown operand {name!r}")
+        setattr(d, name, Strides(*(int(v) for v in st)))
+    return d
+
+
+def prologue_workspace_size(d: PrologueDesc) -> int:
+    n = C.c_size_t()
+    check(lib().mft_prologue_workspace_size(C.byref(d), C.byref(n)))
+    return n.value
+
+
+def prologue_fwd(d: PrologueDesc, x, w, y, stream) -> None:
+    check(lib().mft_prologue_fwd(C.byref(d), x, w, y, stream))
+
+
+def prologue_bwd(d: PrologueDesc, x, w, dy, dx, dw, workspace, stream) -> None:
+    check(lib().mft_prologue_bwd(C.byref(d), x, w, dy, dx, dw, workspace, stream))

@@ -13,8 +13,10 @@
 #include <string>
 
 #include "attn_kernels.h"
+#include "capi_util.h"
 
-namespace {
+namespace mft {
+namespace capi {
 
 thread_local std::string g_last_error;
 
@@ -22,6 +24,44 @@ mft_status fail(mft_status st, const std::string& msg) {
     g_last_error = msg;
     return st;
 }
+
+mft_status resolve_layout(const mft_strides& st, int64_t H, int64_t S, int64_t D, int64_t esz, const char* who,
+                          const char* name, Strides* out, bool* dense_out) {
+    const Strides dense{H * S * D, S * D, (int)D};
+    if ((st.b == 0 && st.h == 0 && st.s == 0) || (st.b == dense.b && st.h == dense.h && st.s == dense.s)) {
+        *out = dense;  // contiguous [B, H, S, D]
+        *dense_out = true;
+        return MFT_OK;
+    }
+    const int64_t unit = 16 / esz;  // 16-byte rows
+    if (st.b <= 0 || st.h <= 0 || st.s <= 0 || st.b % unit || st.h % unit || st.s % unit)
+        return fail(MFT_ERR_INVALID_ARG, std::string(who) + ": strides of " + name +
+                                             " must be positive multiples of 16 bytes (or all zero)");
+    if (st.s < D)
+        return fail(MFT_ERR_INVALID_ARG, std::string(who) + ": sequence stride of " + name +
+                                             " is shorter than a row (D)");
+    if ((S - 1) * st.s + D > (int64_t(1) << 31) - 1)
+        return fail(MFT_ERR_UNSUPPORTED, std::string(who) + ": one (batch, head) block of " + name +
+                                             " spans 2^31 elements or more");
+    *out = Strides{st.b, st.h, (int)st.s};
+    *dense_out = false;
+    return MFT_OK;
+}
+
+// Tensors are read and written in 16-byte vectors.
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+mft_status hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return MFT_OK;
+    return fail(MFT_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+}  // namespace capi
+}  // namespace mft
+
+namespace {
+
+using namespace mft::capi;
 
 mft_status check_desc(const mft_attn_desc* d, mft::AttnShape* s) {
     if (!d) return fail(MFT_ERR_INVALID_ARG, "mft_attn: desc is NULL");
@@ -58,24 +98,11 @@ mft_status check_desc(const mft_attn_desc* d, mft::AttnShape* s) {
     mft::Strides* out[] = {&s->q, &s->k, &s->v, &s->o, &s->dO, &s->dq, &s->dk, &s->dv};
     s->contiguous = true;
     for (int i = 0; i < 8; ++i) {
-        const mft_strides& st = *layouts[i].st;
-        const mft::Strides dense{layouts[i].H * d->S * d->D, d->S * d->D, (int)d->D};
-        if ((st.b == 0 && st.h == 0 && st.s == 0) || (st.b == dense.b && st.h == dense.h && st.s == dense.s)) {
-            *out[i] = dense;  // contiguous [B, H, S, D]
-            continue;
-        }
-        const int64_t unit = 16 / layouts[i].esz;  // 16-byte rows
-        if (st.b <= 0 || st.h <= 0 || st.s <= 0 || st.b % unit || st.h % unit || st.s % unit)
-            return fail(MFT_ERR_INVALID_ARG, std::string("mft_attn: strides of ") + layouts[i].name +
-                                                 " must be positive multiples of 16 bytes (or all zero)");
-        if (st.s < d->D)
-            return fail(MFT_ERR_INVALID_ARG, std::string("mft_attn: sequence stride of ") + layouts[i].name +
-                                                 " is shorter than a row (D)");
-        if ((d->S - 1) * st.s + d->D > (int64_t(1) << 31) - 1)
-            return fail(MFT_ERR_UNSUPPORTED, std::string("mft_attn: one (batch, head) block of ") + layouts[i].name +
-                                                 " spans 2^31 elements or more");
-        *out[i] = mft::Strides{st.b, st.h, (int)st.s};
-        s->contiguous = false;
+        bool dense = true;
+        const mft_status r = resolve_layout(*layouts[i].st, layouts[i].H, d->S, d->D, layouts[i].esz, "mft_attn",
+                                            layouts[i].name, out[i], &dense);
+        if (r != MFT_OK) return r;
+        s->contiguous = s->contiguous && dense;
     }
     s->B = d->B;
     s->Hq = d->Hq;
@@ -91,21 +118,13 @@ mft_status check_desc(const mft_attn_desc* d, mft::AttnShape* s) {
     return MFT_OK;
 }
 
-// Tensors are read and written in 16-byte vectors.
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
-mft_status hip_status(hipError_t e, const char* what) {
-    if (e == hipSuccess) return MFT_OK;
-    return fail(MFT_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
-}
-
 }  // namespace
 
 extern "C" {
 
 int mft_version(void) { return 3; }
 
-const char* mft_last_error(void) { return g_last_error.c_str(); }
+const char* mft_last_error(void) { return mft::capi::g_last_error.c_str(); }
 
 mft_status mft_attn_workspace_size(const mft_attn_desc* desc, size_t* fwd_bytes, size_t* bwd_bytes) {
     mft::AttnShape s;

@@ -1,0 +1,406 @@
+// Fused q/k prologue of the attention: y = rope(norm(x)) per row, and its
+// backward (C ABI in include/mft/prologue.h).
+//
+// One wave per row (b, h, s) of D elements; each wave takes RPW rows and
+// issues all their loads before computing any.  A RoPE pair (p, p + D/2)
+// never leaves its lane: lane l owns the elements p = (l + 64 j) * V + e
+// (j < NJ, e < V) of each half.  With D/2 in {64, 128, 256} and aligned rows
+// one j and V = D/128 contiguous elements per lane give vector loads and
+// stores; other head dims take V = 1 and NJ = 1, 2 or 4 strided elements.
+// The row's sum of squares is a wave reduction.
+//
+// Arithmetic follows the reference operators step for step, without fused
+// multiply-adds (fp contract off):
+//   rms_norm         core/ops.cpp:1693-1705   double sum of squares, float
+//                                             rms, (x / rms) * (1 + w)
+//   rms_norm_affine  core/ops.cpp:1739-1744   float inv_rms, x * inv_rms * w
+//   apply_rope       core/ops.cpp:2360-2389   angle = float(pos) * freq,
+//                                             freq = 1 / theta^(2d/D) (host
+//                                             table, the same float powf)
+//   ApplyRoPEBackward core/backward_functions.cpp:757-768
+//   RMSNorm(Affine)Backward core/backward_functions.cpp:510-528, 548-567,
+//                                             in double, as there.
+// cosf/sinf are the device library's (the reference calls the host libm's);
+// both are faithfully rounded, so y agrees to a few ulp.
+//
+// dL/dw: each backward workgroup (4 waves) sums its rows' terms (float,
+// fixed order) into one [D] partial, and a second kernel adds the partials in
+// a fixed order (in double).  The partition depends only on the shape, so dw
+// is deterministic.
+#include <hip/hip_runtime.h>
+
+#include "attn_common.h"
+#include "prologue_kernels.h"
+
+namespace mft {
+namespace {
+
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// V consecutive elements of type T, converted to / from float.
+template <typename T, int V> struct Vec {
+    typedef T raw __attribute__((ext_vector_type(V)));
+    __device__ static void load(const T* p, float* out) {
+        if constexpr (V == 1) {
+            out[0] = (float)*p;
+        } else {
+            const raw r = *reinterpret_cast<const raw*>(p);
+#pragma unroll
+            for (int e = 0; e < V; ++e) out[e] = (float)r[e];
+        }
+    }
+    __device__ static void store(T* p, const float* in) {
+        if constexpr (V == 1) {
+            *p = (T)in[0];
+        } else {
+            raw r;
+#pragma unroll
+            for (int e = 0; e < V; ++e) r[e] = (T)in[e];
+            *reinterpret_cast<raw*>(p) = r;
+        }
+    }
+};
+
+struct RowAddr {
+    int64_t b, h;
+    int s;
+};
+
+__device__ __forceinline__ RowAddr row_addr(const PrologueArgs& a, int64_t r) {
+    const int s = (int)(r % a.S);
+    const int64_t bh = r / a.S;
+    return RowAddr{bh / a.H, bh % a.H, s};
+}
+
+// First element of chunk j of this lane in a half.
+template <int V> __device__ __forceinline__ int elem(int lane, int j) { return (lane + 64 * j) * V; }
+
+constexpr int FWD_RPW = 2;
+
+template <typename T, int NJ, int V>
+__global__ __launch_bounds__(256) void prologue_fwd_kernel(PrologueArgs a) {
+#pragma clang fp contract(off)
+    constexpr int E = NJ * V;  // elements per lane per half
+    constexpr int RPW = FWD_RPW;
+    const int lane = threadIdx.x & 63;
+    const int half = a.D / 2;
+    const int64_t r0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
+    float x1[RPW][E], x2[RPW][E];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        const int64_t r = r0 + i;
+        const RowAddr ra = row_addr(a, r < a.rows ? r : 0);
+        const T* xr = (const T*)a.x + a.sx.at(ra.b, ra.h) + (int64_t)ra.s * a.sx.s;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int p = elem<V>(lane, j);
+            if (r < a.rows && p < half) {
+                Vec<T, V>::load(xr + p, &x1[i][j * V]);
+                Vec<T, V>::load(xr + p + half, &x2[i][j * V]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < V; ++e) x1[i][j * V + e] = x2[i][j * V + e] = 0.f;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        const int64_t r = r0 + i;
+        if (r >= a.rows) break;  // wave-uniform
+        const RowAddr ra = row_addr(a, r);
+        T* yr = (T*)a.y + a.sy.at(ra.b, ra.h) + (int64_t)ra.s * a.sy.s;
+        if (a.norm != PROLOGUE_NORM_NONE) {
+            double ss = 0.0;
+#pragma unroll
+            for (int k = 0; k < E; ++k) ss += (double)x1[i][k] * (double)x1[i][k] + (double)x2[i][k] * (double)x2[i][k];
+            ss = wave_sum(ss);
+            if (a.norm == PROLOGUE_NORM_GEMMA) {
+                const float rms = (float)sqrt(ss / (double)a.D + (double)a.eps);
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                    for (int e = 0; e < V; ++e) {
+                        const int p = elem<V>(lane, j) + e, k = j * V + e;
+                        if (p < half) {
+                            x1[i][k] = (x1[i][k] / rms) * (1.0f + a.w[p]);
+                            x2[i][k] = (x2[i][k] / rms) * (1.0f + a.w[p + half]);
+                        }
+                    }
+            } else {
+                const float inv = (float)(1.0 / sqrt(ss / (double)a.D + (double)a.eps));
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                    for (int e = 0; e < V; ++e) {
+                        const int p = elem<V>(lane, j) + e, k = j * V + e;
+                        if (p < half) {
+                            x1[i][k] = x1[i][k] * inv * a.w[p];
+                            x2[i][k] = x2[i][k] * inv * a.w[p + half];
+                        }
+                    }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int p0 = elem<V>(lane, j);
+            if (p0 >= half) continue;
+            float y1[V], y2[V];
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                const int k = j * V + e;
+                y1[e] = x1[i][k];
+                y2[e] = x2[i][k];
+                if (a.rope) {
+                    const float ang = (float)ra.s * a.inv_freq[p0 + e];
+                    const float c = cosf(ang), sn = sinf(ang);
+                    y1[e] = x1[i][k] * c - x2[i][k] * sn;
+                    y2[e] = x1[i][k] * sn + x2[i][k] * c;
+                }
+            }
+            Vec<T, V>::store(yr + p0, y1);
+            Vec<T, V>::store(yr + p0 + half, y2);
+        }
+    }
+}
+
+// Backward: workgroup g (4 waves) owns rows [4 RPW g, 4 RPW (g + 1)), wave w
+// the rows 4 RPW g + w + 4 i (i < RPW), all loaded before any is computed.
+// The dL/dw terms are summed per wave in row order, then over the 4 waves in
+// wave order (LDS), giving one [D] partial per workgroup.
+template <typename T, int NJ, int V>
+__global__ __launch_bounds__(256) void prologue_bwd_kernel(PrologueArgs a) {
+#pragma clang fp contract(off)
+    constexpr int E = NJ * V;
+    constexpr int RPW = prologue_bwd_rows_per_wave(E);
+    __shared__ float red[3][PROLOGUE_MAX_D];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int half = a.D / 2;
+    const bool norm = a.norm != PROLOGUE_NORM_NONE;
+    const int64_t rbase = (int64_t)blockIdx.x * 4 * RPW + w;
+    float gw1[E], gw2[E];
+#pragma unroll
+    for (int k = 0; k < E; ++k) gw1[k] = gw2[k] = 0.f;
+    float g1[RPW][E], g2[RPW][E], x1[RPW][E], x2[RPW][E];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        const int64_t r = rbase + 4 * i;
+        const bool live = r < a.rows;
+        const RowAddr ra = row_addr(a, live ? r : 0);
+        const float* gr = a.dy + a.sdy.at(ra.b, ra.h) + (int64_t)ra.s * a.sdy.s;
+        const T* xr = norm ? (const T*)a.x + a.sx.at(ra.b, ra.h) + (int64_t)ra.s * a.sx.s : nullptr;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int p = elem<V>(lane, j);
+            if (live && p < half) {
+                Vec<float, V>::load(gr + p, &g1[i][j * V]);
+                Vec<float, V>::load(gr + p + half, &g2[i][j * V]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < V; ++e) g1[i][j * V + e] = g2[i][j * V + e] = 0.f;
+            }
+            if (norm && live && p < half) {
+                Vec<T, V>::load(xr + p, &x1[i][j * V]);
+                Vec<T, V>::load(xr + p + half, &x2[i][j * V]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < V; ++e) x1[i][j * V + e] = x2[i][j * V + e] = 0.f;
+            }
+        }
+    }
+    // effective weights: 1 + w for Gemma's rms_norm, w for the affine variant
+    double we1[E], we2[E];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+            const int p = elem<V>(lane, j) + e, k = j * V + e;
+            const bool ok = norm && p < half;
+            const double w1 = ok ? (double)a.w[p] : 0.0, w2 = ok ? (double)a.w[p + half] : 0.0;
+            we1[k] = a.norm == PROLOGUE_NORM_GEMMA ? 1.0 + w1 : w1;
+            we2[k] = a.norm == PROLOGUE_NORM_GEMMA ? 1.0 + w2 : w2;
+        }
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        const int64_t r = rbase + 4 * i;
+        if (r >= a.rows) break;  // wave-uniform
+        const RowAddr ra = row_addr(a, r);
+        float* dxr = a.dx + a.sdx.at(ra.b, ra.h) + (int64_t)ra.s * a.sdx.s;
+        // gradient at the norm's output: R^T dy
+        if (a.rope) {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int e = 0; e < V; ++e) {
+                    const int p = elem<V>(lane, j) + e, k = j * V + e;
+                    if (p >= half) continue;
+                    const float ang = (float)ra.s * a.inv_freq[p];
+                    const float c = cosf(ang), sn = sinf(ang);
+                    const float a1 = g1[i][k], a2 = g2[i][k];
+                    g1[i][k] = a1 * c + a2 * sn;
+                    g2[i][k] = -a1 * sn + a2 * c;
+                }
+        }
+        if (norm) {
+            double ss = 0.0, dot = 0.0;
+#pragma unroll
+            for (int k = 0; k < E; ++k) {
+                ss += (double)x1[i][k] * (double)x1[i][k] + (double)x2[i][k] * (double)x2[i][k];
+                dot += (double)g1[i][k] * we1[k] * (double)x1[i][k] + (double)g2[i][k] * we2[k] * (double)x2[i][k];
+            }
+            ss = wave_sum(ss);
+            dot = wave_sum(dot);
+            const double inv = 1.0 / sqrt(ss / (double)a.D + (double)a.eps);
+            const double coeff = (inv * inv * inv) / (double)a.D;
+#pragma unroll
+            for (int k = 0; k < E; ++k) {
+                const float d1 = (float)((double)g1[i][k] * we1[k] * inv - (double)x1[i][k] * coeff * dot);
+                const float d2 = (float)((double)g2[i][k] * we2[k] * inv - (double)x2[i][k] * coeff * dot);
+                gw1[k] += (float)((double)g1[i][k] * (double)x1[i][k] * inv);
+                gw2[k] += (float)((double)g2[i][k] * (double)x2[i][k] * inv);
+                g1[i][k] = d1;
+                g2[i][k] = d2;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int p = elem<V>(lane, j);
+            if (p < half) {
+                Vec<float, V>::store(dxr + p, &g1[i][j * V]);
+                Vec<float, V>::store(dxr + p + half, &g2[i][j * V]);
+            }
+        }
+    }
+    if (!norm || !a.dw_part) return;
+    // the workgroup's partial: waves 1..3 hand theirs to wave 0, which adds
+    // them in wave order
+    if (w > 0) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                const int p = elem<V>(lane, j) + e, k = j * V + e;
+                if (p < half) {
+                    red[w - 1][p] = gw1[k];
+                    red[w - 1][p + half] = gw2[k];
+                }
+            }
+    }
+    __syncthreads();
+    if (w == 0) {
+        float* part = a.dw_part + (int64_t)blockIdx.x * a.D;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                const int p = elem<V>(lane, j) + e, k = j * V + e;
+                if (p >= half) continue;
+                float s1 = gw1[k], s2 = gw2[k];
+                for (int q = 0; q < 3; ++q) {
+                    s1 += red[q][p];
+                    s2 += red[q][p + half];
+                }
+                part[p] = s1;
+                part[p + half] = s2;
+            }
+    }
+}
+
+// dw[c] = sum of the workgroup partials, in a fixed order: 64 slices per
+// column (slice t adds partials t, t + 64, ... in double, eight loads in
+// flight), then the slices in slice order.
+__global__ __launch_bounds__(1024) void prologue_dw_reduce_kernel(const float* part, int64_t nparts, int D,
+                                                                  float* dw) {
+    constexpr int NS = 64;
+    __shared__ double acc[NS][16];
+    const int cl = threadIdx.x & 15, sl = threadIdx.x >> 4;
+    const int c = blockIdx.x * 16 + cl;
+    double s = 0.0;
+    if (c < D) {
+        int64_t k = sl;
+        for (; k + 7 * NS < nparts; k += 8 * NS) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = part[(k + NS * u) * D + c];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s += (double)v[u];
+        }
+        for (; k < nparts; k += NS) s += (double)part[k * D + c];
+    }
+    acc[sl][cl] = s;
+    __syncthreads();
+    if (sl == 0 && c < D) {
+        double t = 0.0;
+        for (int k = 0; k < NS; ++k) t += acc[k][cl];
+        dw[c] = (float)t;
+    }
+}
+
+// Whether every row of a layout starts on a vbytes boundary.
+bool rows_aligned(const void* base, const Strides& st, int64_t esz, int vbytes) {
+    const int64_t m = vbytes / esz;
+    return (reinterpret_cast<uintptr_t>(base) % vbytes) == 0 && st.b % m == 0 && st.h % m == 0 && st.s % m == 0;
+}
+
+template <typename T, int NJ, int V>
+hipError_t launch_shape(const PrologueArgs& a, bool bwd, hipStream_t st) {
+    if (bwd) {
+        hipLaunchKernelGGL((prologue_bwd_kernel<T, NJ, V>), dim3((unsigned)prologue_bwd_blocks(a.rows, a.D)),
+                           dim3(256), 0, st, a);
+    } else {
+        const int64_t blocks = (a.rows + 4 * FWD_RPW - 1) / (4 * FWD_RPW);
+        hipLaunchKernelGGL((prologue_fwd_kernel<T, NJ, V>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+    }
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_t(const PrologueArgs& a, bool bwd, hipStream_t st) {
+    const int half = a.D / 2;
+    const int64_t esz = sizeof(T);
+    if (half == 64 || half == 128 || half == 256) {
+        const int V = half / 64;  // contiguous elements per lane
+        bool ok;
+        if (bwd) {
+            ok = rows_aligned(a.dy, a.sdy, 4, 4 * V) && rows_aligned(a.dx, a.sdx, 4, 4 * V);
+            if (a.norm != PROLOGUE_NORM_NONE) ok = ok && rows_aligned(a.x, a.sx, esz, V * (int)esz);
+        } else {
+            ok = rows_aligned(a.x, a.sx, esz, V * (int)esz) && rows_aligned(a.y, a.sy, esz, V * (int)esz);
+        }
+        if (ok) {
+            if (V == 1) return launch_shape<T, 1, 1>(a, bwd, st);
+            if (V == 2) return launch_shape<T, 1, 2>(a, bwd, st);
+            return launch_shape<T, 1, 4>(a, bwd, st);
+        }
+    }
+    if (half <= 64) return launch_shape<T, 1, 1>(a, bwd, st);
+    if (half <= 128) return launch_shape<T, 2, 1>(a, bwd, st);
+    return launch_shape<T, 4, 1>(a, bwd, st);
+}
+
+}  // namespace
+
+int64_t prologue_bwd_blocks(int64_t rows, int D) {
+    const int rows_per_wg = 4 * prologue_bwd_rows_per_wave(prologue_elems_per_lane(D));
+    return (rows + rows_per_wg - 1) / rows_per_wg;
+}
+
+hipError_t launch_prologue_fwd(const PrologueArgs& a, bool is_bf16, hipStream_t st) {
+    return is_bf16 ? launch_t<bf16>(a, false, st) : launch_t<float>(a, false, st);
+}
+
+hipError_t launch_prologue_bwd(const PrologueArgs& a, bool is_bf16, float* dw, hipStream_t st) {
+    const hipError_t e = is_bf16 ? launch_t<bf16>(a, true, st) : launch_t<float>(a, true, st);
+    if (e != hipSuccess) return e;
+    if (a.norm != PROLOGUE_NORM_NONE && dw && a.dw_part) {
+        hipLaunchKernelGGL(prologue_dw_reduce_kernel, dim3((unsigned)((a.D + 15) / 16)), dim3(1024), 0, st,
+                           (const float*)a.dw_part, prologue_bwd_blocks(a.rows, a.D), a.D, dw);
+        return hipGetLastError();
+    }
+    return hipSuccess;
+}
+
+}  // namespace mft

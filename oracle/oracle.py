@@ -71,6 +71,10 @@ def lib():
                                    opt_f32, opt_f32, opt_f32, opt_f32, opt_f32]
         L.orc_repeat_kv.argtypes = [_f32p, _f32p, _i64, _i64, _i64, _i64, _i64]
         L.orc_repeat_kv_backward.argtypes = [_f32p, _f32p, _i64, _i64, _i64, _i64, _i64]
+        L.orc_prologue_fwd.argtypes = [_f32p, C.c_void_p, _i64, _i64, _i64, _i64, C.c_int, C.c_float, C.c_float,
+                                       _f32p]
+        L.orc_prologue_bwd.argtypes = [_f32p, C.c_void_p, _f32p, _i64, _i64, _i64, _i64, C.c_int, C.c_float,
+                                       C.c_float, _f32p, C.c_void_p]
         _lib = L
     return _lib
 
@@ -99,6 +103,9 @@ def ref():
                                          C.c_float, C.c_int, _f32p, _f32p, _f32p, _f32p]
         R.mftref_repeat_kv.restype = C.c_int
         R.mftref_repeat_kv.argtypes = [_f32p, opt, _i64, _i64, _i64, _i64, _i64, _f32p, opt]
+        R.mftref_prologue.restype = C.c_int
+        R.mftref_prologue.argtypes = [_f32p, opt, opt, _i64, _i64, _i64, _i64, C.c_int, C.c_float, C.c_float,
+                                      _f32p, opt, opt]
         R.mftref_f32_to_bf16_bits.restype = C.c_uint16
         R.mftref_f32_to_bf16_bits.argtypes = [C.c_float]
         _ref = R
@@ -303,6 +310,29 @@ def repeat_kv_backward(g, r):
     return out
 
 
+NORMS = {"none": 0, "gemma": 1, "affine": 2}
+
+
+def prologue(x, w=None, dy=None, norm="gemma", eps=1e-6, theta=10000.0):
+    """y = rope(norm(x)) per row of x [B, H, S, D] (fp32), and with dy the
+    backward: dict(y, dx, dw).  norm: "none", "gemma" (ops::rms_norm,
+    x / rms * (1 + w)) or "affine" (ops::rms_norm_affine); theta 0 = no RoPE."""
+    B, H, S, D = x.shape
+    x = np.ascontiguousarray(x, np.float32)
+    nm = NORMS[norm]
+    wp = None if w is None else np.ascontiguousarray(w, np.float32)
+    y = np.empty_like(x)
+    lib().orc_prologue_fwd(x, _ptr(wp), B, H, S, D, nm, float(eps), float(theta), y)
+    out = dict(y=y)
+    if dy is not None:
+        dx = np.empty_like(x)
+        dw = np.empty(D, np.float32) if nm else None
+        lib().orc_prologue_bwd(x, _ptr(wp), np.ascontiguousarray(dy, np.float32), B, H, S, D, nm, float(eps),
+                               float(theta), dx, _ptr(dw))
+        out.update(dx=dx, dw=dw)
+    return out
+
+
 # ------------------------------------------------- reference (oracle/_ref)
 def ref_composite(q, k, v, dO=None, scale=None, causal=True):
     """The reference's own operators (compiled from its sources)."""
@@ -373,6 +403,26 @@ def ref_repeat_kv(kv, r, g=None):
     if rc != 0:
         raise RuntimeError("reference repeat_kv_heads raised")
     return out, dkv
+
+
+def ref_prologue(x, w=None, dy=None, norm="gemma", eps=1e-6, theta=10000.0):
+    """The reference's rms_norm / rms_norm_affine and apply_rope with their
+    Engine backward (compiled from its sources); same contract as prologue()."""
+    B, H, S, D = x.shape
+    x = np.ascontiguousarray(x, np.float32)
+    nm = NORMS[norm]
+    wp = None if w is None else np.ascontiguousarray(w, np.float32)
+    y = np.empty_like(x)
+    dx = np.empty_like(x) if dy is not None else None
+    dw = np.empty(D, np.float32) if (dy is not None and nm) else None
+    rc = ref().mftref_prologue(x, _ptr(wp), _ptr(None if dy is None else np.ascontiguousarray(dy, np.float32)),
+                               B, H, S, D, nm, float(eps), float(theta), y, _ptr(dx), _ptr(dw))
+    if rc != 0:
+        raise RuntimeError("reference rms_norm / apply_rope raised")
+    out = dict(y=y)
+    if dy is not None:
+        out.update(dx=dx, dw=dw)
+    return out
 
 
 # ------------------------------------------------------------------ metrics

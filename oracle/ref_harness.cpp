@@ -216,4 +216,33 @@ int mftref_repeat_kv(const float* kv, const float* g, int64_t B, int64_t Hkv, in
 // The reference's bf16 rounding (core/dtype.h:114-121), for pinning refcpu's.
 uint16_t mftref_f32_to_bf16_bits(float x) { return float32_to_bf16_bits(x); }
 
+// The q/k prologue of graph/gemma_model.cpp:459-471: ops::rms_norm (norm 1)
+// or ops::rms_norm_affine (norm 2) or nothing (norm 0), then ops::apply_rope
+// when theta > 0; backward by Engine::run_backward({y}, {dy}).  x is
+// [B, H, S, D]; w is [D]; dw, dx, dy may be NULL (dy NULL skips the backward).
+int mftref_prologue(const float* x, const float* w, const float* dy, int64_t B, int64_t H, int64_t S,
+                    int64_t D, int norm, float eps, float theta, float* y, float* dx, float* dw) {
+    try {
+        const bool grad = dy != nullptr;
+        auto xt = from_host(x, {B, H, S, D}, grad);
+        TensorPtr wt;
+        if (norm != 0) wt = from_host(w, {D}, grad);
+        TensorPtr t = xt;
+        if (norm == 1) t = rms_norm(t, wt, eps);
+        if (norm == 2) t = rms_norm_affine(t, wt, eps);
+        if (theta > 0.f) t = apply_rope(t, static_cast<int>(S), static_cast<int>(D), theta);
+        to_host(t, y);
+        if (grad) {
+            autograd::Engine::instance().run_backward({t}, {from_host(dy, {B, H, S, D}, false)});
+            to_host(xt->grad(), dx);
+            if (wt) to_host(wt->grad(), dw);
+        }
+        autograd::Engine::instance().clear_graph();
+        return 0;
+    } catch (const std::exception& e) {
+        std::cerr << "[mftref_prologue] " << e.what() << std::endl;
+        return -1;
+    }
+}
+
 }  // extern "C"

@@ -386,4 +386,97 @@ void orc_repeat_kv_backward(const float* g, float* dkv, int64_t B, int64_t Hkv,
             }
 }
 
+// ---- q/k prologue ----
+
+namespace {
+
+// RoPE of one row in place (core/ops.cpp:2363-2389): rotate-half pairs.
+void rope_row(float* r, int64_t pos, int64_t D, float theta) {
+    const int64_t half = D / 2;
+    for (int64_t d = 0; d < half; ++d) {
+        float freq = 1.0f / std::pow(theta, 2.0f * d / D);
+        float angle = pos * freq;
+        float c = std::cos(angle);
+        float s = std::sin(angle);
+        float x1 = r[d];
+        float x2 = r[half + d];
+        r[d] = x1 * c - x2 * s;
+        r[half + d] = x1 * s + x2 * c;
+    }
+}
+
+}  // namespace
+
+void orc_prologue_fwd(const float* x, const float* w, int64_t B, int64_t H, int64_t S, int64_t D,
+                      int norm, float eps, float theta, float* y) {
+    const int64_t rows = B * H * S;
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * D;
+        float* yr = y + r * D;
+        if (norm == 0) {
+            std::memcpy(yr, xr, sizeof(float) * D);
+        } else {
+            double ss = 0.0;
+            for (int64_t i = 0; i < D; ++i) ss += static_cast<double>(xr[i]) * static_cast<double>(xr[i]);
+            if (norm == 1) {
+                float rms = static_cast<float>(std::sqrt(ss / static_cast<double>(D) + static_cast<double>(eps)));
+                for (int64_t i = 0; i < D; ++i) {
+                    float scale = 1.0f + w[i];
+                    yr[i] = (xr[i] / rms) * scale;
+                }
+            } else {
+                float inv = static_cast<float>(1.0 / std::sqrt(ss / static_cast<double>(D) + static_cast<double>(eps)));
+                for (int64_t i = 0; i < D; ++i) yr[i] = xr[i] * inv * w[i];
+            }
+        }
+        if (theta > 0.f) rope_row(yr, r % S, D, theta);
+    }
+}
+
+void orc_prologue_bwd(const float* x, const float* w, const float* dy, int64_t B, int64_t H, int64_t S,
+                      int64_t D, int norm, float eps, float theta, float* dx, float* dw) {
+    const int64_t rows = B * H * S, half = D / 2;
+    std::vector<float> g(D);
+    if (dw) std::fill(dw, dw + D, 0.0f);
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* gy = dy + r * D;
+        if (theta > 0.f) {
+            const int64_t pos = r % S;
+            for (int64_t d = 0; d < half; ++d) {
+                float freq = 1.0f / std::pow(theta, 2.0f * static_cast<float>(d) / static_cast<float>(D));
+                float angle = static_cast<float>(pos) * freq;
+                float c = std::cos(angle);
+                float s = std::sin(angle);
+                float g1p = gy[d];
+                float g2p = gy[half + d];
+                g[d] = g1p * c + g2p * s;
+                g[half + d] = -g1p * s + g2p * c;
+            }
+        } else {
+            std::memcpy(g.data(), gy, sizeof(float) * D);
+        }
+        float* gx = dx + r * D;
+        if (norm == 0) {
+            std::memcpy(gx, g.data(), sizeof(float) * D);
+            continue;
+        }
+        const float* xb = x + r * D;
+        double sqsum = 0.0;
+        for (int64_t i = 0; i < D; ++i) sqsum += static_cast<double>(xb[i]) * static_cast<double>(xb[i]);
+        double inv_rms = 1.0 / std::sqrt(sqsum / static_cast<double>(D) + static_cast<double>(eps));
+        auto w_eff = [&](int64_t i) {
+            return norm == 1 ? 1.0 + static_cast<double>(w[i]) : static_cast<double>(w[i]);
+        };
+        double dot = 0.0;
+        for (int64_t i = 0; i < D; ++i) dot += static_cast<double>(g[i]) * w_eff(i) * static_cast<double>(xb[i]);
+        double coeff = (inv_rms * inv_rms * inv_rms) / static_cast<double>(D);
+        for (int64_t i = 0; i < D; ++i) {
+            double term1 = static_cast<double>(g[i]) * w_eff(i) * inv_rms;
+            double term2 = static_cast<double>(xb[i]) * coeff * dot;
+            gx[i] = static_cast<float>(term1 - term2);
+            if (dw) dw[i] += static_cast<float>(static_cast<double>(g[i]) * static_cast<double>(xb[i]) * inv_rms);
+        }
+    }
+}
+
 }  // extern "C"

@@ -92,6 +92,22 @@ void orc_repeat_kv(const float* kv, float* out, int64_t B, int64_t Hkv, int64_t 
 void orc_repeat_kv_backward(const float* g, float* dkv, int64_t B, int64_t Hkv,
                             int64_t S, int64_t D, int64_t r);
 
+/* ---- q/k prologue: norm then RoPE, per row of D (layout [B, H, S, D]) ----
+ * norm 0: none; 1: ops::rms_norm (core/ops.cpp:1677-1706), y = (x / rms) * (1 + w)
+ * with rms = float(sqrt(double sum x^2 / D + eps)); 2: ops::rms_norm_affine
+ * (core/ops.cpp:1728-1745), y = x * inv_rms * w.  Then, if theta > 0,
+ * ops::apply_rope (core/ops.cpp:2337-2391): pairs (d, d + D/2), freq =
+ * 1 / powf(theta, 2d/D), angle = pos * freq, cosf / sinf.  w may be NULL for
+ * norm 0. */
+void orc_prologue_fwd(const float* x, const float* w, int64_t B, int64_t H, int64_t S, int64_t D,
+                      int norm, float eps, float theta, float* y);
+/* Backward of the same chain, as the Engine runs it: ApplyRoPEBackward
+ * (core/backward_functions.cpp:728-774) gives g = R^T dy, then
+ * RMSNormBackward / RMSNormAffineBackward (core/backward_functions.cpp:492-575)
+ * in double; dw (may be NULL) = the float sum over rows in row order. */
+void orc_prologue_bwd(const float* x, const float* w, const float* dy, int64_t B, int64_t H, int64_t S,
+                      int64_t D, int norm, float eps, float theta, float* dx, float* dw);
+
 #ifdef __cplusplus
 }
 #endif

@@ -3,6 +3,8 @@
 Runs in the build container only (it needs oracle/_ref/libmftref.so, which is
 compiled from /root/reference by oracle/Makefile).  Outputs, all data:
 
+  tests/golden/prologue.npz  full tensors of the q/k prologue (rms_norm /
+                             rms_norm_affine + apply_rope, fwd and bwd)
   tests/golden/tiny.npz      full tensors of small cases: the deterministic
                              fills and shapes of the reference's four hot-path
                              unit tests plus seeded GQA cases
@@ -124,15 +126,56 @@ def make_config(cfg):
     np.savez_compressed(os.path.join(HERE, f"{cfg}.npz"), **out)
 
 
+# q/k prologue cases: (B, H, S, D, norm, eps, theta, seed).  Gemma-3's
+# rms_norm_eps and rope thetas (1e6 global, 1e4 local layers), Qwen's RoPE
+# without a norm, the affine variant, no RoPE, an odd half-dim, and positions
+# up to 4095 on a narrow head.
+PROLOGUE_CASES = [
+    (1, 2, 33, 64, "gemma", 1e-6, 10000.0, 1),
+    (2, 1, 17, 128, "gemma", 1e-6, 1000000.0, 2),
+    (1, 3, 20, 256, "none", 1e-6, 1000000.0, 3),
+    (1, 2, 12, 96, "affine", 1e-5, 10000.0, 4),
+    (1, 1, 9, 6, "gemma", 1e-6, 0.0, 5),
+    (1, 1, 4096, 4, "gemma", 1e-6, 10000.0, 6),
+]
+
+
+def make_prologue():
+    """tests/golden/prologue.npz: full tensors (x, w, dy -> y, dx, dw) of the
+    reference's rms_norm / rms_norm_affine + apply_rope and their backward."""
+    out = {}
+    ok = True
+    for i, (B, H, S, D, norm, eps, theta, seed) in enumerate(PROLOGUE_CASES):
+        n = B * H * S * D
+        x = (2.0 * O.normal(n, 3000 + seed, 0)).reshape(B, H, S, D).astype(np.float32)
+        w = (0.3 * O.normal(D, 3000 + seed, 1)).astype(np.float32)
+        dy = O.normal(n, 3000 + seed, 2).reshape(B, H, S, D).astype(np.float32)
+        r = O.ref_prologue(x, w if norm != "none" else None, dy, norm, eps, theta)
+        mine = O.prologue(x, w if norm != "none" else None, dy, norm, eps, theta)
+        ok = ok and all(bitwise(mine[k], r[k]) for k in r if r[k] is not None)
+        out[f"case{i}"] = np.array([B, H, S, D, seed], np.int64)
+        out[f"case{i}_cfg"] = np.array([O.NORMS[norm], eps, theta], np.float64)
+        for k, v in (("x", x), ("w", w), ("dy", dy), ("y", r["y"]), ("dx", r["dx"])):
+            out[f"case{i}_{k}"] = v
+        if r["dw"] is not None:
+            out[f"case{i}_dw"] = r["dw"]
+    out["refcpu_bitwise"] = np.array(ok)
+    path = os.path.join(HERE, "prologue.npz")
+    np.savez_compressed(path, **out)
+    print(f"prologue: {len(PROLOGUE_CASES)} cases, refcpu bitwise = {ok} -> {path}")
+
+
 def main(argv):
     if not O.ref_available():
         O.build()
     if not O.ref_available():
         raise SystemExit("oracle/_ref/libmftref.so could not be built (needs /root/reference)")
-    todo = argv or ["tiny", "c1", "c2", "c4", "c5", "c5f32", "c3"]
+    todo = argv or ["tiny", "prologue", "c1", "c2", "c4", "c5", "c5f32", "c3"]
     for t in todo:
         if t == "tiny":
             make_tiny()
+        elif t == "prologue":
+            make_prologue()
         else:
             make_config(t)
 

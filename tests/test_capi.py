@@ -11,6 +11,7 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "mft", "attention.h")
+HEADERS = [HEADER, os.path.join(ROOT, "include", "mft", "prologue.h")]
 
 
 @pytest.fixture(scope="module")
@@ -24,7 +25,7 @@ def capi():
 
 
 def header_functions():
-    text = open(HEADER).read()
+    text = "".join(open(h).read() for h in HEADERS)
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     text = re.sub(r"//[^\n]*", "", text)
     return sorted(set(re.findall(r"\b(mft_[a-z0-9_]+)\s*\(", text)))
@@ -53,7 +54,8 @@ def test_every_header_symbol_is_exported(capi):
 def test_header_compiles_as_c(tmp_path):
     """The header is plain C (extern "C", C99 types, no torch types)."""
     src = tmp_path / "t.c"
-    src.write_text('#include "mft/attention.h"\nint main(void){return mft_version()==3?0:1;}\n')
+    src.write_text('#include "mft/attention.h"\n#include "mft/prologue.h"\n'
+                   'int main(void){return mft_version()==3?0:1;}\n')
     res = subprocess.run(["gcc", "-std=c99", "-fsyntax-only", "-D__HIP_PLATFORM_AMD__",
                           "-I", os.path.join(ROOT, "include"), "-I", "/opt/rocm/include", str(src)],
                          capture_output=True, text=True)
@@ -163,3 +165,41 @@ def test_strided_layout_accepted(capi):
                   strides={n: st for n in ("q", "o", "dO")} | {"dq": st})
     f, b = capi.workspace_size(d)
     assert b == capi.workspace_size(capi.desc(B, H, 1, S, D, 0.125, True, capi.MFT_BF16))[1]
+
+
+@pytest.mark.parametrize("kw,status,needle", [
+    (dict(D=7), 1, "even head_dim"),
+    (dict(D=514), 2, "head_dim > 512"),
+    (dict(S=0), 1, "4D tensor"),
+    (dict(dtype=5), 1, "dtype"),
+    (dict(norm=3), 1, "norm must be"),
+    (dict(eps=-1.0), 1, "eps"),
+    (dict(theta=float("nan")), 1, "theta"),
+])
+def test_prologue_desc_validation(capi, kw, status, needle):
+    args = dict(B=1, H=2, S=8, D=64, dtype=capi.MFT_BF16, norm=capi.MFT_NORM_GEMMA, eps=1e-6, theta=1e4)
+    args.update(kw)
+    d = capi.prologue_desc(**args)
+    with pytest.raises(capi.MftError) as e:
+        capi.prologue_fwd(d, 16, 16, 16, None)
+    assert e.value.status == status and needle in str(e.value)
+
+
+def test_prologue_pointer_rules(capi):
+    d = capi.prologue_desc(1, 2, 8, 64)
+    for call, needle in ((lambda: capi.prologue_fwd(d, None, 16, 16, None), "non-NULL"),
+                         (lambda: capi.prologue_fwd(d, 16, None, 16, None), "weight"),
+                         (lambda: capi.prologue_fwd(d, 17, 16, 16, None), "element-aligned"),
+                         (lambda: capi.prologue_bwd(d, 16, 16, 32, 32, None, None, None), "alias"),
+                         (lambda: capi.prologue_bwd(d, 16, 16, 32, 48, 64, None, None), "workspace")):
+        with pytest.raises(capi.MftError) as e:
+            call()
+        assert needle in str(e.value)
+    bad = capi.prologue_desc(1, 2, 8, 64, strides=dict(x=(1024, 64, 100)))
+    with pytest.raises(capi.MftError) as e:
+        capi.prologue_fwd(bad, 16, 16, 16, None)
+    assert "multiples of 16 bytes" in str(e.value)
+    # workspace: [waves, D] fp32 partials, sized by the shape alone
+    assert capi.prologue_workspace_size(capi.prologue_desc(1, 4, 4096, 256)) == 16384 // 16 * 4 * 256
+    assert capi.prologue_workspace_size(capi.prologue_desc(1, 4, 4096, 256, norm=capi.MFT_NORM_NONE)) == 0
+
