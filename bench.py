@@ -11,7 +11,9 @@ the algorithmic causal throughput  7*B*H*D*S*(S+1) / step time  in TFLOP/s
 masks the model graphs use - Gemma's sliding window (c5w512) and right-padded
 batches (c4pad); their flops count the visible (query, key) pairs only - and
 for the [B,S,H,D] operand layout (c5bshd).  `prologue` times the fused q/k
-norm + RoPE pass at the config's q and k shapes against the HBM roofline.
+norm + RoPE pass at the config's q and k shapes against the HBM roofline,
+and `lm_loss` the LM cross-entropy at the Gemma-3-1B head over the config's
+positions (streaming: MFMA roofline; dense logits: HBM roofline).
 The roofline object covers the dominant kernel,
 timed live with HIP events on the stream the kernels run on.  The
 cpu_baseline object times the reference CPU operators (oracle/_ref, compiled
@@ -222,6 +224,74 @@ def prologue_leg(cfg_id, steps, warmup):
             "fwd_bytes": fwd_bytes, "bwd_bytes": bwd_bytes, "launches": {"fwd": 2, "bwd": 4}}
 
 
+def lm_loss_leg(cfg_id, steps, warmup):
+    """LM cross-entropy at the Gemma-3-1B head (H 1152, V 262144) over the
+    config's B*S positions, bf16.  Streaming (hidden, weight): four GEMMs of
+    2*N*V*H flop per step (forward logits; backward logits again, d hidden,
+    d weight), MFMA roofline.  Dense (given bf16 logits [B, S, V]): HBM
+    roofline, algorithmic bytes 2*N*V forward and 2*N*V + 4*N*V backward."""
+    import torch
+    from mobilefinetuner_amd import lm_loss as L
+
+    c = CONFIGS[cfg_id]
+    dev = torch.device("cuda:0")
+    B, S, H, V = c["B"], c["S"], 1152, 262144
+    N = B * S
+    g = torch.Generator(device=dev)
+    g.manual_seed(99)
+    hidden = (0.5 * torch.randn(B, S, H, device=dev, generator=g)).to(torch.bfloat16)
+    weight = (0.05 * torch.randn(V, H, device=dev, generator=g)).to(torch.bfloat16)
+    labels = torch.randint(0, V, (B, S), device=dev, generator=g, dtype=torch.int32)
+    one = torch.ones(1, device=dev)
+
+    def timed(fn, n):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    state = {}
+
+    def s_fwd():
+        state["lse"] = L.streaming_lm_cross_entropy(hidden, weight, labels, check_labels=False)[1]
+
+    s_fwd()
+
+    def s_bwd():
+        L.streaming_lm_cross_entropy_backward(hidden, weight, labels, state["lse"], one)
+
+    sf, sb = timed(s_fwd, steps), timed(s_bwd, steps)
+    flop = 2.0 * N * V * H
+    out = {"workload": f"Gemma-3-1B LM head (H {H}, V {V}) over the {cfg_id} batch ({N} positions), bf16",
+           "streaming": {"fwd_ms": round(sf, 4), "bwd_ms": round(sb, 4),
+                         "fwd_tflops": round(flop / (sf * 1e-3) / 1e12, 1),
+                         "bwd_tflops": round(3 * flop / (sb * 1e-3) / 1e12, 1),
+                         "frac_mfma_peak": round(4 * flop / ((sf + sb) * 1e-3) / 1e12 / PEAK_TFLOPS["bf16"], 4)}}
+    del state["lse"]
+    logits = torch.randn(B, S, V, device=dev, generator=g).to(torch.bfloat16)
+
+    def d_fwd():
+        state["lse"] = L.lm_cross_entropy(logits, labels, check_labels=False)[1]
+
+    d_fwd()
+
+    def d_bwd():
+        L.lm_cross_entropy_backward(logits, labels, state["lse"], one)
+
+    df, db = timed(d_fwd, steps), timed(d_bwd, steps)
+    fb, bb = 2.0 * N * V, 6.0 * N * V
+    out["dense"] = {"fwd_ms": round(df, 4), "bwd_ms": round(db, 4),
+                    "fwd_frac_hbm": round(fb / (df * 1e-3) / (HBM_GBS * 1e9), 4),
+                    "bwd_frac_hbm": round(bb / (db * 1e-3) / (HBM_GBS * 1e9), 4)}
+    return out
+
+
 COPY_BYTES = 1 << 30
 
 
@@ -357,6 +427,7 @@ def main():
         out["variants"] = variants
     if not args.no_variants:
         out["prologue"] = prologue_leg(args.config, max(20, args.steps), 5)
+        out["lm_loss"] = lm_loss_leg(args.config, 5, 2)
     if args.all_configs:
         per = {}
         for cid in ("c1", "c2", "c3", "c4", "c5", "c5f32"):

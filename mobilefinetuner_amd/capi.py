@@ -1,5 +1,5 @@
-"""ctypes binding of the C ABI in ``include/mft/attention.h`` and
-``include/mft/prologue.h``.
+"""ctypes binding of the C ABI in ``include/mft/attention.h``,
+``include/mft/prologue.h`` and ``include/mft/lm_loss.h``.
 
 This is the binding a Python caller would use (the C++ finetune_ops adapter
 links the same library directly).  It raises when the library is missing: the
@@ -25,7 +25,10 @@ EXPORTS = (
     "mft_attn_workspace_size", "mft_attn_fwd", "mft_attn_bwd", "mft_attn_bwd_stage",
     "mft_repeat_kv_fwd", "mft_repeat_kv_bwd", "mft_last_error", "mft_version",
     "mft_prologue_fwd", "mft_prologue_workspace_size", "mft_prologue_bwd",
+    "mft_lm_ce_workspace_size", "mft_lm_ce_fwd", "mft_lm_ce_bwd", "mft_lm_ce_streaming_fwd",
+    "mft_lm_ce_streaming_bwd",
 )
+MFT_REDUCE_MEAN, MFT_REDUCE_SUM, MFT_REDUCE_NONE = 0, 1, 2
 
 
 class Strides(C.Structure):
@@ -49,6 +52,11 @@ class PrologueDesc(C.Structure):
         ("B", C.c_int64), ("H", C.c_int64), ("S", C.c_int64), ("D", C.c_int64),
         ("dtype", C.c_int32), ("norm", C.c_int32), ("eps", C.c_float), ("theta", C.c_float),
     ] + [(n, Strides) for n in ("x", "y", "dy", "dx")]
+
+
+class LmLossDesc(C.Structure):
+    _fields_ = [("B", C.c_int64), ("S", C.c_int64), ("V", C.c_int64), ("H", C.c_int64),
+                ("dtype", C.c_int32), ("ignore_index", C.c_int32), ("reduction", C.c_int32), ("chunk", C.c_int32)]
 
 
 class MftError(RuntimeError):
@@ -89,6 +97,16 @@ def lib():
     L.mft_prologue_workspace_size.argtypes = [C.POINTER(PrologueDesc), C.POINTER(C.c_size_t)]
     L.mft_prologue_bwd.restype = C.c_int
     L.mft_prologue_bwd.argtypes = [C.POINTER(PrologueDesc), vp, vp, vp, vp, vp, vp, vp]
+    L.mft_lm_ce_workspace_size.restype = C.c_int
+    L.mft_lm_ce_workspace_size.argtypes = [C.POINTER(LmLossDesc), C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+    L.mft_lm_ce_fwd.restype = C.c_int
+    L.mft_lm_ce_fwd.argtypes = [C.POINTER(LmLossDesc)] + [vp] * 7
+    L.mft_lm_ce_bwd.restype = C.c_int
+    L.mft_lm_ce_bwd.argtypes = [C.POINTER(LmLossDesc)] + [vp] * 7
+    L.mft_lm_ce_streaming_fwd.restype = C.c_int
+    L.mft_lm_ce_streaming_fwd.argtypes = [C.POINTER(LmLossDesc)] + [vp] * 8
+    L.mft_lm_ce_streaming_bwd.restype = C.c_int
+    L.mft_lm_ce_streaming_bwd.argtypes = [C.POINTER(LmLossDesc)] + [vp] * 9
     if L.mft_version() != 3:
         raise RuntimeError("libmft_attn.so version mismatch")
     _lib = L
@@ -163,3 +181,31 @@ def prologue_fwd(d: PrologueDesc, x, w, y, stream) -> None:
 
 def prologue_bwd(d: PrologueDesc, x, w, dy, dx, dw, workspace, stream) -> None:
     check(lib().mft_prologue_bwd(C.byref(d), x, w, dy, dx, dw, workspace, stream))
+
+
+def lm_loss_desc(B, S, V, H=0, dtype=MFT_F32, ignore_index=-100, reduction=MFT_REDUCE_MEAN, chunk=0) -> LmLossDesc:
+    return LmLossDesc(int(B), int(S), int(V), int(H), int(dtype), int(ignore_index), int(reduction), int(chunk))
+
+
+def lm_ce_workspace_size(d: LmLossDesc):
+    f, b = C.c_size_t(), C.c_size_t()
+    check(lib().mft_lm_ce_workspace_size(C.byref(d), C.byref(f), C.byref(b)))
+    return f.value, b.value
+
+
+def lm_ce_fwd(d, logits, labels, loss, lse, status, workspace, stream) -> None:
+    check(lib().mft_lm_ce_fwd(C.byref(d), logits, labels, loss, lse, status, workspace, stream))
+
+
+def lm_ce_bwd(d, logits, labels, lse, grad_loss, grad_logits, workspace, stream) -> None:
+    check(lib().mft_lm_ce_bwd(C.byref(d), logits, labels, lse, grad_loss, grad_logits, workspace, stream))
+
+
+def lm_ce_streaming_fwd(d, hidden, weight, labels, loss, lse, status, workspace, stream) -> None:
+    check(lib().mft_lm_ce_streaming_fwd(C.byref(d), hidden, weight, labels, loss, lse, status, workspace, stream))
+
+
+def lm_ce_streaming_bwd(d, hidden, weight, labels, lse, grad_loss, grad_hidden, grad_weight, workspace,
+                        stream) -> None:
+    check(lib().mft_lm_ce_streaming_bwd(C.byref(d), hidden, weight, labels, lse, grad_loss, grad_hidden,
+                                        grad_weight, workspace, stream))

@@ -71,6 +71,11 @@ def lib():
                                    opt_f32, opt_f32, opt_f32, opt_f32, opt_f32]
         L.orc_repeat_kv.argtypes = [_f32p, _f32p, _i64, _i64, _i64, _i64, _i64]
         L.orc_repeat_kv_backward.argtypes = [_f32p, _f32p, _i64, _i64, _i64, _i64, _i64]
+        L.orc_lm_ce.restype = C.c_int
+        L.orc_lm_ce.argtypes = [_f32p, C.c_void_p, _i64, _i64, _i64, C.c_int, C.c_int, C.c_void_p, _f32p, C.c_void_p]
+        L.orc_selected_ce.restype = C.c_int
+        L.orc_selected_ce.argtypes = [_f32p, _f32p, C.c_void_p, _i64, _i64, _i64, _i64, C.c_int, C.c_int, C.c_float,
+                                      _f32p, C.c_void_p, C.c_void_p]
         L.orc_prologue_fwd.argtypes = [_f32p, C.c_void_p, _i64, _i64, _i64, _i64, C.c_int, C.c_float, C.c_float,
                                        _f32p]
         L.orc_prologue_bwd.argtypes = [_f32p, C.c_void_p, _f32p, _i64, _i64, _i64, _i64, C.c_int, C.c_float,
@@ -103,6 +108,11 @@ def ref():
                                          C.c_float, C.c_int, _f32p, _f32p, _f32p, _f32p]
         R.mftref_repeat_kv.restype = C.c_int
         R.mftref_repeat_kv.argtypes = [_f32p, opt, _i64, _i64, _i64, _i64, _i64, _f32p, opt]
+        R.mftref_lm_ce.restype = C.c_int
+        R.mftref_lm_ce.argtypes = [_f32p, opt, _i64, _i64, _i64, C.c_int, C.c_int, opt, _f32p, opt]
+        R.mftref_streaming_ce.restype = C.c_int
+        R.mftref_streaming_ce.argtypes = [_f32p, _f32p, opt, _i64, _i64, _i64, _i64, C.c_int, C.c_int, C.c_float,
+                                          _f32p, opt, opt]
         R.mftref_prologue.restype = C.c_int
         R.mftref_prologue.argtypes = [_f32p, opt, opt, _i64, _i64, _i64, _i64, C.c_int, C.c_float, C.c_float,
                                       _f32p, opt, opt]
@@ -117,6 +127,11 @@ def _ptr(a):
 
 
 # ---------------------------------------------------------------- generator
+def uniform(seed: int, stream: int, counter: int) -> float:
+    """The generator's 53-bit uniform in (0, 1) (splitmix64 of seed, stream, counter)."""
+    return float(lib().orc_uniform(seed, stream, counter))
+
+
 def normal(n: int, seed: int, stream: int, sigma: float = 1.0) -> np.ndarray:
     x = np.empty(n, dtype=np.float32)
     lib().orc_fill_normal(x, n, seed, stream, sigma)
@@ -333,6 +348,53 @@ def prologue(x, w=None, dy=None, norm="gemma", eps=1e-6, theta=10000.0):
     return out
 
 
+REDUCTIONS = {"mean": 0, "sum": 1, "none": 2}
+
+
+def _ce_dense(fn, logits, labels, ignore_index, reduction, grad_out):
+    B, S, V = logits.shape
+    logits = np.ascontiguousarray(logits, np.float32)
+    labels = np.ascontiguousarray(labels, np.int32)
+    red = REDUCTIONS[reduction]
+    loss = np.zeros((B, S) if red == 2 else (1,), np.float32)
+    g = None
+    if grad_out is not None:
+        g = np.ascontiguousarray(np.broadcast_to(np.float32(grad_out), loss.shape), np.float32)
+    grad = np.zeros_like(logits) if g is not None else None
+    rc = fn(logits, labels.ctypes.data, B, S, V, int(ignore_index), red, _ptr(g), loss, _ptr(grad))
+    if rc != 0:
+        raise ValueError("lm_cross_entropy: label out of range")
+    return dict(loss=loss, grad=grad)
+
+
+def lm_ce(logits, labels, ignore_index=-100, reduction="mean", grad_out=None):
+    """ops::lm_cross_entropy on logits [B, S, V] (fp32) and int32 labels [B, S];
+    with grad_out (scalar, or [B, S] for "none") also the logits gradient."""
+    return _ce_dense(lib().orc_lm_ce, logits, labels, ignore_index, reduction, grad_out)
+
+
+def _ce_stream(fn, hidden, weight, labels, ignore_index, reduction, grad_out):
+    B, S, H = hidden.shape
+    V = weight.shape[0]
+    hidden = np.ascontiguousarray(hidden, np.float32)
+    weight = np.ascontiguousarray(weight, np.float32)
+    labels = np.ascontiguousarray(labels, np.int32)
+    loss = np.zeros(1, np.float32)
+    gh = np.zeros_like(hidden) if grad_out is not None else None
+    gw = np.zeros_like(weight) if grad_out is not None else None
+    rc = fn(hidden, weight, labels.ctypes.data, B, S, H, V, int(ignore_index), REDUCTIONS[reduction],
+            float(1.0 if grad_out is None else grad_out), loss, _ptr(gh), _ptr(gw))
+    if rc != 0:
+        raise ValueError("lm_cross_entropy: label out of range")
+    return dict(loss=loss, grad_hidden=gh, grad_weight=gw)
+
+
+def selected_ce(hidden, weight, labels, ignore_index=-100, reduction="mean", grad_out=None):
+    """ops::selected_token_lm_cross_entropy (= streaming) on fp32 hidden
+    [B, S, H] and weight [V, H]; reduction "mean" or "sum"."""
+    return _ce_stream(lib().orc_selected_ce, hidden, weight, labels, ignore_index, reduction, grad_out)
+
+
 # ------------------------------------------------- reference (oracle/_ref)
 def ref_composite(q, k, v, dO=None, scale=None, causal=True):
     """The reference's own operators (compiled from its sources)."""
@@ -403,6 +465,16 @@ def ref_repeat_kv(kv, r, g=None):
     if rc != 0:
         raise RuntimeError("reference repeat_kv_heads raised")
     return out, dkv
+
+
+def ref_lm_ce(logits, labels, ignore_index=-100, reduction="mean", grad_out=None):
+    """The reference's lm_cross_entropy and Engine backward (same contract as lm_ce)."""
+    return _ce_dense(ref().mftref_lm_ce, logits, labels, ignore_index, reduction, grad_out)
+
+
+def ref_streaming_ce(hidden, weight, labels, ignore_index=-100, reduction="mean", grad_out=None):
+    """The reference's streaming_lm_cross_entropy and Engine backward."""
+    return _ce_stream(ref().mftref_streaming_ce, hidden, weight, labels, ignore_index, reduction, grad_out)
 
 
 def ref_prologue(x, w=None, dy=None, norm="gemma", eps=1e-6, theta=10000.0):

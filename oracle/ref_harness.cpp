@@ -13,6 +13,7 @@
 //   repeat_kv_heads -> transpose -> matmul -> mul(scale) -> add(causal mask)
 //   -> softmax -> matmul, then autograd::Engine::run_backward({out}, {dO}).
 #include "core/autograd_engine.h"
+#include "core/lm_loss.h"
 #include "core/memory_efficient_attention.h"
 #include "core/memory_manager.h"
 #include "core/ops.h"
@@ -241,6 +242,58 @@ int mftref_prologue(const float* x, const float* w, const float* dy, int64_t B, 
         return 0;
     } catch (const std::exception& e) {
         std::cerr << "[mftref_prologue] " << e.what() << std::endl;
+        return -1;
+    }
+}
+
+// ops::lm_cross_entropy with its Engine backward (core/lm_loss.cpp:268-382).
+// reduction 0 mean, 1 sum, 2 none; grad_out [1] or [B, S] (NULL: no
+// backward).  Returns -1 when the reference throws.
+int mftref_lm_ce(const float* logits, const int32_t* labels, int64_t B, int64_t S, int64_t V, int ignore_index,
+                 int reduction, const float* grad_out, float* loss, float* grad_logits) {
+    try {
+        static const char* red[] = {"mean", "sum", "none"};
+        auto lt = from_host(logits, {B, S, V}, grad_out != nullptr);
+        auto yt = std::make_shared<Tensor>(std::vector<int64_t>{B, S}, labels, kInt32, kCPU);
+        auto out = lm_cross_entropy(lt, yt, ignore_index, red[reduction]);
+        to_host(out, loss);
+        if (grad_out) {
+            auto g = reduction == 2 ? from_host(grad_out, {B, S}, false) : from_host(grad_out, {1}, false);
+            autograd::Engine::instance().run_backward({out}, {g});
+            to_host(lt->grad(), grad_logits);
+        }
+        autograd::Engine::instance().clear_graph();
+        return 0;
+    } catch (const std::exception& e) {
+        std::cerr << "[mftref_lm_ce] " << e.what() << std::endl;
+        autograd::Engine::instance().clear_graph();
+        return -1;
+    }
+}
+
+// ops::streaming_lm_cross_entropy (= selected_token_lm_cross_entropy) with its
+// Engine backward (core/lm_loss.cpp:165-266, 384-481); reduction 0 mean, 1 sum.
+int mftref_streaming_ce(const float* hidden, const float* weight, const int32_t* labels, int64_t B, int64_t S,
+                        int64_t H, int64_t V, int ignore_index, int reduction, float grad_out, float* loss,
+                        float* grad_hidden, float* grad_weight) {
+    try {
+        static const char* red[] = {"mean", "sum"};
+        const bool grad = grad_hidden || grad_weight;
+        auto ht = from_host(hidden, {B, S, H}, grad);
+        auto wt = from_host(weight, {V, H}, grad);
+        auto yt = std::make_shared<Tensor>(std::vector<int64_t>{B, S}, labels, kInt32, kCPU);
+        auto out = streaming_lm_cross_entropy(ht, wt, yt, ignore_index, red[reduction]);
+        to_host(out, loss);
+        if (grad) {
+            autograd::Engine::instance().run_backward({out}, {from_host(&grad_out, {1}, false)});
+            if (grad_hidden) to_host(ht->grad(), grad_hidden);
+            if (grad_weight) to_host(wt->grad(), grad_weight);
+        }
+        autograd::Engine::instance().clear_graph();
+        return 0;
+    } catch (const std::exception& e) {
+        std::cerr << "[mftref_streaming_ce] " << e.what() << std::endl;
+        autograd::Engine::instance().clear_graph();
         return -1;
     }
 }

@@ -17,6 +17,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <limits>
 #include <vector>
 
 namespace {
@@ -477,6 +478,140 @@ void orc_prologue_bwd(const float* x, const float* w, const float* dy, int64_t B
             if (dw) dw[i] += static_cast<float>(static_cast<double>(g[i]) * static_cast<double>(xb[i]) * inv_rms);
         }
     }
+}
+
+// ---- LM cross-entropy ----
+
+int orc_lm_ce(const float* logits, const int32_t* labels, int64_t B, int64_t S, int64_t V, int ignore_index,
+              int reduction, const float* grad_out, float* loss, float* grad_logits) {
+    // forward (core/lm_loss.cpp:291-313, 318-334)
+    double loss_sum = 0.0;
+    int64_t valid_cnt = 0;
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t s = 0; s < S; ++s) {
+            if (reduction == 2) loss[b * S + s] = 0.0f;
+            if (s + 1 >= S) continue;
+            int32_t cls = labels[b * S + (s + 1)];
+            if (cls == ignore_index) continue;
+            if (cls < 0 || cls >= V) return -1;
+            const float* row = logits + (b * S + s) * V;
+            float max_val = -std::numeric_limits<float>::infinity();
+            for (int64_t v = 0; v < V; ++v) max_val = std::max(max_val, row[v]);
+            double denom = 0.0;
+            for (int64_t v = 0; v < V; ++v) denom += std::exp(row[v] - max_val);
+            double log_sum_exp = max_val + std::log(denom);
+            loss_sum += (log_sum_exp - row[cls]);
+            valid_cnt++;
+            if (reduction == 2) loss[b * S + s] = static_cast<float>(log_sum_exp - row[cls]);
+        }
+    if (reduction == 1) loss[0] = static_cast<float>(loss_sum);
+    if (reduction == 0)
+        loss[0] = valid_cnt > 0 ? static_cast<float>(loss_sum / static_cast<double>(valid_cnt))
+                                : std::numeric_limits<float>::quiet_NaN();
+    if (!grad_out || !grad_logits) return 0;
+    // backward (core/lm_loss.cpp:85-158)
+    std::fill(grad_logits, grad_logits + B * S * V, 0.0f);
+    float scale_base = 1.0f;
+    if (reduction == 0) scale_base = (valid_cnt > 0) ? (1.0f / static_cast<float>(valid_cnt)) : 0.0f;
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t s = 0; s + 1 < S; ++s) {
+            int32_t y = labels[b * S + (s + 1)];
+            if (y == ignore_index) continue;
+            const float* logit_row = logits + (b * S + s) * V;
+            float max_val = -std::numeric_limits<float>::infinity();
+            for (int64_t v = 0; v < V; ++v) max_val = std::max(max_val, logit_row[v]);
+            float denom = 0.0f;
+            for (int64_t v = 0; v < V; ++v) denom += std::exp(logit_row[v] - max_val);
+            float inv_denom = 1.0f / denom;
+            float outer = reduction == 2 ? grad_out[b * S + s] : grad_out[0];
+            float coeff = outer * scale_base;
+            float* grad_row = grad_logits + (b * S + s) * V;
+            for (int64_t v = 0; v < V; ++v) {
+                float p = std::exp(logit_row[v] - max_val) * inv_denom;
+                float g = p;
+                if (v == y) g -= 1.0f;
+                grad_row[v] = g * coeff;
+            }
+        }
+    return 0;
+}
+
+int orc_selected_ce(const float* hidden, const float* weight, const int32_t* labels, int64_t B, int64_t S,
+                    int64_t H, int64_t V, int ignore_index, int reduction, float grad_out, float* loss,
+                    float* grad_hidden, float* grad_weight) {
+    struct Item {
+        int64_t b, s;
+        int32_t cls;
+    };
+    std::vector<Item> valid;  // core/lm_loss.cpp:28-47
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t s = 0; s + 1 < S; ++s) {
+            int32_t cls = labels[b * S + (s + 1)];
+            if (cls == ignore_index) continue;
+            if (cls < 0 || cls >= V) return -1;
+            valid.push_back({b, s, cls});
+        }
+    auto dot = [&](const float* hrow, int64_t v) {  // :63-70
+        float sum = 0.0f;
+        for (int64_t h = 0; h < H; ++h) sum += hrow[h] * weight[v * H + h];
+        return sum;
+    };
+    // forward (:420-451)
+    double loss_sum = 0.0;
+    for (const Item& it : valid) {
+        const float* hrow = hidden + (it.b * S + it.s) * H;
+        float max_val = -std::numeric_limits<float>::infinity();
+        float target_logit = 0.0f;
+        for (int64_t v = 0; v < V; ++v) {
+            const float z = dot(hrow, v);
+            if (v == it.cls) target_logit = z;
+            max_val = std::max(max_val, z);
+        }
+        double denom = 0.0;
+        for (int64_t v = 0; v < V; ++v) denom += std::exp(dot(hrow, v) - max_val);
+        const double log_sum_exp = max_val + std::log(denom);
+        loss_sum += (log_sum_exp - target_logit);
+    }
+    if (reduction == 1)
+        loss[0] = static_cast<float>(loss_sum);
+    else
+        loss[0] = valid.empty() ? std::numeric_limits<float>::quiet_NaN()
+                                : static_cast<float>(loss_sum / static_cast<double>(valid.size()));
+    if (!grad_hidden && !grad_weight) return 0;
+    // backward (:197-262)
+    if (grad_hidden) std::fill(grad_hidden, grad_hidden + B * S * H, 0.0f);
+    if (grad_weight) std::fill(grad_weight, grad_weight + V * H, 0.0f);
+    if (valid.empty()) return 0;
+    float scale_base = 1.0f;
+    if (reduction == 0) scale_base = 1.0f / static_cast<float>(valid.size());
+    const float coeff = grad_out * scale_base;
+    if (coeff == 0.0f) return 0;
+    std::vector<float> logits(static_cast<size_t>(V));
+    for (const Item& it : valid) {
+        const float* hrow = hidden + (it.b * S + it.s) * H;
+        float max_val = -std::numeric_limits<float>::infinity();
+        for (int64_t v = 0; v < V; ++v) {
+            const float z = dot(hrow, v);
+            logits[static_cast<size_t>(v)] = z;
+            max_val = std::max(max_val, z);
+        }
+        float denom = 0.0f;
+        for (int64_t v = 0; v < V; ++v) denom += std::exp(logits[static_cast<size_t>(v)] - max_val);
+        const float inv_denom = 1.0f / denom;
+        float* ghrow = grad_hidden ? grad_hidden + (it.b * S + it.s) * H : nullptr;
+        for (int64_t v = 0; v < V; ++v) {
+            float p = std::exp(logits[static_cast<size_t>(v)] - max_val) * inv_denom;
+            if (v == it.cls) p -= 1.0f;
+            const float g = p * coeff;
+            if (ghrow)
+                for (int64_t h = 0; h < H; ++h) ghrow[h] += g * weight[v * H + h];
+            if (grad_weight) {
+                float* gwrow = grad_weight + v * H;
+                for (int64_t h = 0; h < H; ++h) gwrow[h] += g * hrow[h];
+            }
+        }
+    }
+    return 0;
 }
 
 }  // extern "C"

@@ -108,6 +108,22 @@ void orc_prologue_fwd(const float* x, const float* w, int64_t B, int64_t H, int6
 void orc_prologue_bwd(const float* x, const float* w, const float* dy, int64_t B, int64_t H, int64_t S,
                       int64_t D, int norm, float eps, float theta, float* dx, float* dw);
 
+/* ---- LM cross-entropy (core/lm_loss.cpp) ----
+ * Dense ops::lm_cross_entropy (:268-382) and LMCrossEntropyBackward
+ * (:85-158): position (b, s) is scored against labels[b, s + 1] unless that
+ * is ignore_index; reduction 0 mean, 1 sum, 2 none ([B, S] losses).
+ * grad_out: [1] (mean, sum) or [B, S] (none); NULL skips the backward.
+ * Returns -1 on a label outside [0, V) (the reference throws). */
+int orc_lm_ce(const float* logits, const int32_t* labels, int64_t B, int64_t S, int64_t V, int ignore_index,
+              int reduction, const float* grad_out, float* loss, float* grad_logits);
+/* ops::selected_token_lm_cross_entropy (:384-472) and its backward
+ * (:165-266) on fp32 hidden [B, S, H] and weight [V, H]: logits are dot
+ * products in float, h order; reduction 0 mean, 1 sum.  grad_hidden and
+ * grad_weight may be NULL. */
+int orc_selected_ce(const float* hidden, const float* weight, const int32_t* labels, int64_t B, int64_t S,
+                    int64_t H, int64_t V, int ignore_index, int reduction, float grad_out, float* loss,
+                    float* grad_hidden, float* grad_weight);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,6 +5,8 @@ compiled from /root/reference by oracle/Makefile).  Outputs, all data:
 
   tests/golden/prologue.npz  full tensors of the q/k prologue (rms_norm /
                              rms_norm_affine + apply_rope, fwd and bwd)
+  tests/golden/lm_loss.npz   lm_cross_entropy and streaming_lm_cross_entropy
+                             (loss, gradients), incl. the reference test's case
   tests/golden/tiny.npz      full tensors of small cases: the deterministic
                              fills and shapes of the reference's four hot-path
                              unit tests plus seeded GQA cases
@@ -165,17 +167,63 @@ def make_prologue():
     print(f"prologue: {len(PROLOGUE_CASES)} cases, refcpu bitwise = {ok} -> {path}")
 
 
+def make_lm_loss():
+    """tests/golden/lm_loss.npz: the reference's lm_cross_entropy and
+    streaming_lm_cross_entropy (loss and gradients) on the hand-written case of
+    core/test_selected_token_lm_loss.cpp:49-76 and on seeded random cases."""
+    out = {}
+    ok = True
+    # the reference test's own values
+    hidden = np.array([0.10, -0.20, 0.30, 0.00, 0.25, -0.15, 0.40, -0.10, 0.05, -0.30, 0.20, 0.10,
+                       0.05, 0.15, -0.25, 0.30, 0.10, -0.05, -0.20, 0.35, 0.25, 0.12, -0.08, 0.18],
+                      np.float32).reshape(2, 4, 3)
+    weight = np.array([0.20, -0.10, 0.05, -0.30, 0.25, 0.10, 0.15, 0.05, -0.20, 0.40, -0.35, 0.12,
+                       -0.05, 0.18, 0.30], np.float32).reshape(5, 3)
+    labels = np.array([[-100, 2, -100, 1], [-100, -100, 4, -100]], np.int32)
+    cases = [("unit", hidden, weight, labels)]
+    for i, (B, S, H, V) in enumerate([(2, 17, 24, 300), (1, 33, 40, 1000)]):
+        h = (0.5 * O.normal(B * S * H, 5000 + i, 0)).reshape(B, S, H).astype(np.float32)
+        w = (0.5 * O.normal(V * H, 5000 + i, 1)).reshape(V, H).astype(np.float32)
+        u = np.array([O.uniform(5000 + i, 2, j) for j in range(B * S)])
+        y = np.minimum((u * V).astype(np.int64), V - 1).astype(np.int32).reshape(B, S)
+        y[u.reshape(B, S) < 0.15] = -100
+        cases.append((f"rand{i}", h, w, y))
+    for name, h, w, y in cases:
+        logits = np.einsum("bsh,vh->bsv", h.astype(np.float64), w.astype(np.float64)).astype(np.float32)
+        out[f"{name}_hidden"], out[f"{name}_weight"], out[f"{name}_labels"] = h, w, y
+        out[f"{name}_logits"] = logits
+        for red in ("mean", "sum", "none"):
+            g = 0.75 if red != "none" else (O.normal(y.size, 5100, 0).reshape(y.shape) + 1.0)
+            r = O.ref_lm_ce(logits, y, -100, red, g)
+            m = O.lm_ce(logits, y, -100, red, g)
+            ok = ok and bitwise(m["loss"], r["loss"]) and bitwise(m["grad"], r["grad"])
+            out[f"{name}_dense_{red}_gout"] = np.asarray(g, np.float32)
+            out[f"{name}_dense_{red}_loss"], out[f"{name}_dense_{red}_grad"] = r["loss"], r["grad"]
+        for red in ("mean", "sum"):
+            r = O.ref_streaming_ce(h, w, y, -100, red, 0.75)
+            m = O.selected_ce(h, w, y, -100, red, 0.75)
+            ok = ok and all(bitwise(m[k], r[k]) for k in r)
+            for k in r:
+                out[f"{name}_stream_{red}_{k}"] = r[k]
+    out["refcpu_bitwise"] = np.array(ok)
+    path = os.path.join(HERE, "lm_loss.npz")
+    np.savez_compressed(path, **out)
+    print(f"lm_loss: {len(cases)} cases, refcpu bitwise = {ok} -> {path}")
+
+
 def main(argv):
     if not O.ref_available():
         O.build()
     if not O.ref_available():
         raise SystemExit("oracle/_ref/libmftref.so could not be built (needs /root/reference)")
-    todo = argv or ["tiny", "prologue", "c1", "c2", "c4", "c5", "c5f32", "c3"]
+    todo = argv or ["tiny", "prologue", "lm_loss", "c1", "c2", "c4", "c5", "c5f32", "c3"]
     for t in todo:
         if t == "tiny":
             make_tiny()
         elif t == "prologue":
             make_prologue()
+        elif t == "lm_loss":
+            make_lm_loss()
         else:
             make_config(t)
 

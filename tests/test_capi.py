@@ -11,7 +11,7 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "mft", "attention.h")
-HEADERS = [HEADER, os.path.join(ROOT, "include", "mft", "prologue.h")]
+HEADERS = [HEADER, os.path.join(ROOT, "include", "mft", "prologue.h"), os.path.join(ROOT, "include", "mft", "lm_loss.h")]
 
 
 @pytest.fixture(scope="module")
@@ -54,7 +54,7 @@ def test_every_header_symbol_is_exported(capi):
 def test_header_compiles_as_c(tmp_path):
     """The header is plain C (extern "C", C99 types, no torch types)."""
     src = tmp_path / "t.c"
-    src.write_text('#include "mft/attention.h"\n#include "mft/prologue.h"\n'
+    src.write_text('#include "mft/attention.h"\n#include "mft/prologue.h"\n#include "mft/lm_loss.h"\n'
                    'int main(void){return mft_version()==3?0:1;}\n')
     res = subprocess.run(["gcc", "-std=c99", "-fsyntax-only", "-D__HIP_PLATFORM_AMD__",
                           "-I", os.path.join(ROOT, "include"), "-I", "/opt/rocm/include", str(src)],
@@ -202,4 +202,21 @@ def test_prologue_pointer_rules(capi):
     # workspace: [waves, D] fp32 partials, sized by the shape alone
     assert capi.prologue_workspace_size(capi.prologue_desc(1, 4, 4096, 256)) == 16384 // 16 * 4 * 256
     assert capi.prologue_workspace_size(capi.prologue_desc(1, 4, 4096, 256, norm=capi.MFT_NORM_NONE)) == 0
+
+
+def test_lm_loss_validation(capi):
+    for kw, needle in ((dict(B=0), "[B,S,V]"), (dict(dtype=7), "dtype"), (dict(reduction=5), "reduction"),
+                       (dict(H=3, reduction=2), "only mean and sum"), (dict(chunk=-1), "chunk")):
+        args = dict(B=1, S=4, V=5)
+        args.update(kw)
+        with pytest.raises(capi.MftError) as e:
+            capi.lm_ce_workspace_size(capi.lm_loss_desc(**args))
+        assert needle in str(e.value), (kw, str(e.value))
+    d = capi.lm_loss_desc(1, 4, 5)
+    with pytest.raises(capi.MftError) as e:
+        capi.lm_ce_fwd(d, None, 16, 16, 16, None, 16, None)
+    assert "non-NULL" in str(e.value)
+    # streaming workspace: one fp32 and one input-dtype logits chunk plus the GEMM workspace
+    f, b = capi.lm_ce_workspace_size(capi.lm_loss_desc(1, 4096, 262144, 1152, capi.MFT_BF16))
+    assert f == b and 4096 * 16384 * 6 < f < 4096 * 16384 * 6 + (80 << 20)
 

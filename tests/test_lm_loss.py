@@ -1,0 +1,151 @@
+"""GPU parity of the LM cross-entropy (mft_lm_ce_* through the C ABI) with the
+oracle restatement of ops::lm_cross_entropy / ops::streaming_lm_cross_entropy
+(pinned bit for bit to the reference by test_lm_loss_oracle.py).
+
+Bars: fp32 max-rel 1e-4 (loss, gradients); bf16 2e-2 against the fp32 oracle
+run on the same bf16-rounded inputs.  The streaming variant is held to the
+same bars, and to the dense one (the reference test's own check).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"f32": 1e-4, "bf16": 2e-2}
+
+
+def _labels(orc, B, S, V, seed, ignore_frac=0.15):
+    u = np.array([orc.uniform(seed, 7, j) for j in range(B * S)]).reshape(B, S)
+    y = np.minimum((u * V).astype(np.int64), V - 1).astype(np.int32)
+    y[u < ignore_frac] = -100
+    return y
+
+
+def _dev(x, dtype, dev):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    return t.to(torch.bfloat16) if dtype == "bf16" else t
+
+
+def _rel(orc, got, ref):
+    return orc.max_rel(np.asarray(got, np.float32), np.asarray(ref, np.float32))
+
+
+DENSE = [
+    # B, S, V, dtype, reduction
+    (2, 17, 300, "f32", "mean"),
+    (1, 64, 5000, "f32", "sum"),
+    (2, 9, 1000, "f32", "none"),
+    (1, 8, 50000, "bf16", "mean"),
+    (3, 5, 777, "bf16", "none"),
+]
+
+
+@pytest.mark.parametrize("case", DENSE, ids=lambda c: "B{}S{}V{}-{}-{}".format(*c))
+def test_dense_matches_oracle(orc, dev, case):
+    import torch
+    from mobilefinetuner_amd import lm_loss as L
+    B, S, V, dtype, red = case
+    print(f"[case] dense {case}", flush=True)
+    logits = (3.0 * orc.normal(B * S * V, 6000 + V, 0)).reshape(B, S, V)
+    if dtype == "bf16":
+        logits = orc.round_bf16(logits)
+    y = _labels(orc, B, S, V, 6000 + V)
+    g = (orc.normal(B * S, 6100, 0).reshape(B, S) + 1.0) if red == "none" else 0.75
+    ref = orc.lm_ce(logits, y, -100, red, g)
+    lt, yt = _dev(logits, dtype, dev), torch.from_numpy(y).to(dev)
+    loss, lse = L.lm_cross_entropy(lt, yt, -100, red)
+    gl = torch.from_numpy(np.asarray(g, np.float32).reshape(-1) if red == "none" else np.array([g], np.float32))
+    grad = L.lm_cross_entropy_backward(lt, yt, lse, gl.to(dev).reshape(loss.shape), -100, red)
+    torch.cuda.synchronize()
+    e = (_rel(orc, loss.cpu().numpy(), ref["loss"]), _rel(orc, grad.cpu().numpy(), ref["grad"]))
+    print(f"[errs] loss {e[0]:.2e} grad {e[1]:.2e}", flush=True)
+    assert max(e) <= TOL[dtype], e
+
+
+STREAM = [
+    # B, S, H, V, dtype, reduction, chunk
+    (2, 17, 24, 300, "f32", "mean", 0),
+    (1, 33, 64, 1000, "f32", "sum", 128),     # chunks that split V unevenly
+    (2, 40, 128, 5000, "bf16", "mean", 1024),
+    (1, 64, 1152, 4096, "bf16", "mean", 0),   # Gemma-3-1B hidden size
+    (1, 20, 40, 999, "f32", "mean", 250),     # rows off the 16-byte grid: element-wise passes
+]
+
+
+@pytest.mark.parametrize("case", STREAM, ids=lambda c: "B{}S{}H{}V{}-{}-{}-c{}".format(*c))
+def test_streaming_matches_oracle(orc, dev, case):
+    import torch
+    from mobilefinetuner_amd import lm_loss as L
+    B, S, H, V, dtype, red, chunk = case
+    print(f"[case] streaming {case}", flush=True)
+    h = (0.5 * orc.normal(B * S * H, 6200 + V, 0)).reshape(B, S, H)
+    w = (0.5 * orc.normal(V * H, 6200 + V, 1)).reshape(V, H)
+    if dtype == "bf16":
+        h, w = orc.round_bf16(h), orc.round_bf16(w)
+    y = _labels(orc, B, S, V, 6200 + V)
+    ref = orc.selected_ce(h, w, y, -100, red, 0.75)
+    ht, wt, yt = _dev(h, dtype, dev), _dev(w, dtype, dev), torch.from_numpy(y).to(dev)
+    loss, lse = L.streaming_lm_cross_entropy(ht, wt, yt, -100, red, chunk)
+    gh, gw = L.streaming_lm_cross_entropy_backward(ht, wt, yt, lse, torch.full((1,), 0.75, device=dev), -100, red,
+                                                   chunk)
+    torch.cuda.synchronize()
+    e = (_rel(orc, loss.cpu().numpy(), ref["loss"]), _rel(orc, gh.cpu().numpy(), ref["grad_hidden"]),
+         _rel(orc, gw.cpu().numpy(), ref["grad_weight"]))
+    print(f"[errs] loss {e[0]:.2e} gh {e[1]:.2e} gw {e[2]:.2e}", flush=True)
+    assert max(e) <= TOL[dtype], e
+
+
+def test_streaming_equals_dense_on_the_gpu(orc, dev):
+    """The reference test's check (core/test_selected_token_lm_loss.cpp:98-115):
+    streaming loss and gradients equal the dense ones chained through
+    logits = hidden . W^T."""
+    import torch
+    from mobilefinetuner_amd import lm_loss as L
+    B, S, H, V = 2, 30, 48, 2000
+    h = torch.from_numpy((0.5 * orc.normal(B * S * H, 6300, 0)).reshape(B, S, H)).to(dev)
+    w = torch.from_numpy((0.5 * orc.normal(V * H, 6300, 1)).reshape(V, H)).to(dev)
+    y = torch.from_numpy(_labels(orc, B, S, V, 6300)).to(dev)
+    logits = (h @ w.t()).contiguous()
+    dl, dlse = L.lm_cross_entropy(logits, y)
+    dg = L.lm_cross_entropy_backward(logits, y, dlse, torch.ones(1, device=dev))
+    sl, slse = L.streaming_lm_cross_entropy(h, w, y, chunk=300)
+    gh, gw = L.streaming_lm_cross_entropy_backward(h, w, y, slse, torch.ones(1, device=dev), chunk=300)
+    torch.cuda.synchronize()
+    assert abs(float(dl) - float(sl)) <= 1e-5 * abs(float(dl))
+    assert torch.allclose(gh, torch.einsum("bsv,vh->bsh", dg, w), atol=1e-5, rtol=1e-4)
+    assert torch.allclose(gw, torch.einsum("bsv,bsh->vh", dg, h), atol=1e-5, rtol=1e-4)
+
+
+def test_all_ignored_and_out_of_range_labels(orc, dev):
+    import torch
+    from mobilefinetuner_amd import lm_loss as L
+    B, S, H, V = 2, 4, 3, 5
+    h = torch.randn(B, S, H, device=dev)
+    w = torch.randn(V, H, device=dev)
+    y = torch.full((B, S), -100, dtype=torch.int32, device=dev)
+    loss, lse = L.streaming_lm_cross_entropy(h, w, y)
+    gh, gw = L.streaming_lm_cross_entropy_backward(h, w, y, lse, torch.ones(1, device=dev))
+    dl, _ = L.lm_cross_entropy(torch.randn(B, S, V, device=dev), y)
+    torch.cuda.synchronize()
+    assert torch.isnan(loss).all() and torch.isnan(dl).all()
+    assert torch.count_nonzero(gh) == 0 and torch.count_nonzero(gw) == 0
+    y[0, 2] = V  # out of range: the reference throws
+    with pytest.raises(ValueError, match="out of range"):
+        L.lm_cross_entropy(torch.randn(B, S, V, device=dev), y)
+    with pytest.raises(ValueError, match="out of range"):
+        L.streaming_lm_cross_entropy(h, w, y)
+
+
+def test_autograd_node(orc, dev):
+    import torch
+    from mobilefinetuner_amd import lm_loss as L
+    B, S, H, V = 1, 20, 32, 700
+    h = torch.from_numpy((0.5 * orc.normal(B * S * H, 6400, 0)).reshape(B, S, H)).to(dev).requires_grad_(True)
+    w = torch.from_numpy((0.5 * orc.normal(V * H, 6400, 1)).reshape(V, H)).to(dev).requires_grad_(True)
+    y = torch.from_numpy(_labels(orc, B, S, V, 6400)).to(dev)
+    loss = L.StreamingLMCrossEntropy.apply(h, w, y)
+    (2.0 * loss).sum().backward()
+    ref = orc.selected_ce(h.detach().cpu().numpy(), w.detach().cpu().numpy(), y.cpu().numpy(), -100, "mean", 2.0)
+    assert _rel(orc, h.grad.cpu().numpy(), ref["grad_hidden"]) <= 1e-4
+    assert _rel(orc, w.grad.cpu().numpy(), ref["grad_weight"]) <= 1e-4
