@@ -1,6 +1,6 @@
 """Summaries of rocprofv3 output for the attention kernels.
 
-    python -m mobilefinetuner_amd.profiling stats <dir> [--command "..."]
+    python -m mobilefinetuner_amd.profiling stats <dir> [--command "..."] [--only attn_,prologue_]
     python -m mobilefinetuner_amd.profiling traffic <fetch_dir> <write_dir> --config c5 \
         --copy-bytes N [--out profiles/hbm_traffic_c5.json] [--command "..."]
     python -m mobilefinetuner_amd.profiling counters <dir> [--command "..."]
@@ -36,6 +36,14 @@ KERNELS = {
     "attn_bwd_stats": "attn_bwd_stats",
     "attn_bwd_fast_reduce": "attn_bwd_reduce",
     "attn_bwd_reduce": "attn_bwd_reduce",
+    "prologue_fwd_kernel": "prologue_fwd",
+    "prologue_bwd_kernel": "prologue_bwd",
+    "prologue_dw_reduce": "prologue_dw_reduce",
+    "ce_row_stats": "ce_row_stats",
+    "ce_grad": "ce_grad",
+    "ce_finalize": "ce_finalize",
+    "ce_reduce": "ce_reduce",
+    "Cijk_": "rocblas_gemm",
 }
 COPY_TAG = "MulFunctor"  # torch.mul(x, 1.0, out=y): the calibration copy
 
@@ -43,6 +51,8 @@ COPY_TAG = "MulFunctor"  # torch.mul(x, 1.0, out=y): the calibration copy
 def short_name(full: str) -> str:
     for frag, short in KERNELS.items():
         if frag in full:
+            if short == "rocblas_gemm":  # keep the Tensile tile name: the GEMMs differ
+                return "rocblas_" + full.split("_UserArgs_")[-1][:24] if "_UserArgs_" in full else short
             return short
     if COPY_TAG in full:
         return "copy_calibration"
@@ -85,6 +95,9 @@ def cmd_stats(args):
         sys.exit(f"no *kernel_stats.csv under {args.dir}")
     if args.command:
         print(f"command: {args.command}\n")
+    if args.only:
+        keep = tuple(args.only.split(","))
+        rows = [r for r in rows if short_name(r["Name"]).startswith(keep)]
     print(f"{'kernel':40s} {'calls':>6s} {'avg_us':>10s} {'min_us':>10s} {'max_us':>10s} {'pct':>6s}")
     for r in rows:
         print(f"{short_name(r['Name']):40s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:10.2f} "
@@ -147,6 +160,7 @@ def main():
     a = sub.add_parser("stats")
     a.add_argument("dir")
     a.add_argument("--command", default="")
+    a.add_argument("--only", default="", help="comma-separated short-name prefixes to keep")
     b = sub.add_parser("traffic")
     b.add_argument("fetch_dir")
     b.add_argument("write_dir")
