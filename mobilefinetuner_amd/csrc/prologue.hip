@@ -1,13 +1,13 @@
 // Fused q/k prologue of the attention: y = rope(norm(x)) per row, and its
 // backward (C ABI in include/mft/prologue.h).
 //
-// One wave per row (b, h, s) of D elements; each wave takes RPW rows and
-// issues all their loads before computing any.  A RoPE pair (p, p + D/2)
-// never leaves its lane: lane l owns the elements p = (l + 64 j) * V + e
-// (j < NJ, e < V) of each half.  With D/2 in {64, 128, 256} and aligned rows
-// one j and V = D/128 contiguous elements per lane give vector loads and
-// stores; other head dims take V = 1 and NJ = 1, 2 or 4 strided elements.
-// The row's sum of squares is a wave reduction.
+// Two lane layouts.  Head dims 128, 256 and 512 with 16-byte-aligned rows take
+// the 16-byte-lane kernels (prologue_*_vec below): a row spans D*size/16
+// lanes and a RoPE pair's partner value arrives by shuffle.  Other head dims
+// and unaligned rows take one wave per row (b, h, s), each wave RPW rows with
+// all loads issued first; a RoPE pair (p, p + D/2) never leaves its lane:
+// lane l owns the elements p = (l + 64 j) * V + e (j < NJ, e < V) of each
+// half.  The row's sum of squares is a shuffle reduction either way.
 //
 // Arithmetic follows the reference operators step for step, without fused
 // multiply-adds (fp contract off):
@@ -339,6 +339,206 @@ __global__ __launch_bounds__(1024) void prologue_dw_reduce_kernel(const float* p
     }
 }
 
+// ---------------------------------------------------------------------------
+// 16-byte lanes (head dims 128, 256, 512): a row is LPR = D * sizeof / 16
+// consecutive lanes, each holding EPL contiguous elements, so every global
+// access is a 16-byte vector.  The first LPR/2 lanes of a row hold the first
+// half; a RoPE pair's partner element sits in lane ^ (LPR/2) at the same
+// slot and comes over by a shuffle.  Row sums are shuffles inside the row's
+// LPR-lane group.  Same arithmetic as the kernels above, element by element.
+
+template <int LPR> __device__ __forceinline__ double group_sum(double v) {
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// cos/sin of the angles of this lane's EPL pairs.  The two lanes holding a
+// pair split the work: the first-half lane evaluates slots [0, EPL/2), its
+// partner slots [EPL/2, EPL), and each takes the other half by shuffle.
+template <int EPL, int LPR>
+__device__ __forceinline__ void pair_trig(const PrologueArgs& a, int s, int q0, bool first, float* c, float* sn) {
+    float mc[EPL / 2], ms[EPL / 2];
+#pragma unroll
+    for (int k = 0; k < EPL / 2; ++k) {
+        const int e = first ? k : k + EPL / 2;
+        const float ang = (float)s * a.inv_freq[q0 + e];
+        mc[k] = cosf(ang);
+        ms[k] = sinf(ang);
+    }
+#pragma unroll
+    for (int k = 0; k < EPL / 2; ++k) {
+        const float oc = __shfl_xor(mc[k], LPR / 2, 64), os = __shfl_xor(ms[k], LPR / 2, 64);
+        c[first ? k : k + EPL / 2] = mc[k];
+        sn[first ? k : k + EPL / 2] = ms[k];
+        c[first ? k + EPL / 2 : k] = oc;
+        sn[first ? k + EPL / 2 : k] = os;
+    }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void prologue_fwd_vec(PrologueArgs a) {
+#pragma clang fp contract(off)
+    constexpr int EPL = 16 / (int)sizeof(T), LPR = D / EPL, RPI = 64 / LPR, HALF = D / 2;
+    static_assert(LPR >= 2 && LPR <= 64, "a row spans 2..64 lanes");
+    constexpr int GROUPS = 2;  // row groups per wave, all loaded before any is computed
+    const int lane = threadIdx.x & 63, gl = lane % LPR;
+    const int p = gl * EPL;  // this lane's first element
+    const bool first = p < HALF;
+    const int64_t wave_row0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * (RPI * GROUPS);
+    float v[GROUPS][EPL];
+    RowAddr ra[GROUPS];
+#pragma unroll
+    for (int g = 0; g < GROUPS; ++g) {
+        const int64_t r = wave_row0 + g * RPI + lane / LPR;
+        ra[g] = row_addr(a, r < a.rows ? r : 0);
+        if (r < a.rows) {
+            Vec<T, EPL>::load((const T*)a.x + a.sx.at(ra[g].b, ra[g].h) + (int64_t)ra[g].s * a.sx.s + p, v[g]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) v[g][e] = 0.f;
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < GROUPS; ++g) {
+        const int64_t r = wave_row0 + g * RPI + lane / LPR;
+        if (a.norm != PROLOGUE_NORM_NONE) {
+            double ss = 0.0;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) ss += (double)v[g][e] * (double)v[g][e];
+            ss = group_sum<LPR>(ss);
+            if (a.norm == PROLOGUE_NORM_GEMMA) {
+                const float rms = (float)sqrt(ss / (double)D + (double)a.eps);
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) v[g][e] = (v[g][e] / rms) * (1.0f + a.w[p + e]);
+            } else {
+                const float inv = (float)(1.0 / sqrt(ss / (double)D + (double)a.eps));
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) v[g][e] = v[g][e] * inv * a.w[p + e];
+            }
+        }
+        float y[EPL];
+        if (a.rope) {
+            float c[EPL], sn[EPL];
+            pair_trig<EPL, LPR>(a, ra[g].s, p % HALF, first, c, sn);
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                const float pv = __shfl_xor(v[g][e], LPR / 2, 64);
+                // first half: x1 * c - x2 * s; second half: x1 * s + x2 * c
+                y[e] = first ? v[g][e] * c[e] - pv * sn[e] : pv * sn[e] + v[g][e] * c[e];
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) y[e] = v[g][e];
+        }
+        if (r < a.rows) Vec<T, EPL>::store((T*)a.y + a.sy.at(ra[g].b, ra[g].h) + (int64_t)ra[g].s * a.sy.s + p, y);
+    }
+}
+
+// Backward with fp32 dy/dx rows as the lane grid (EPL = 4, LPR = D / 4; x is
+// read 4 elements per lane).  Rows per workgroup as prologue_bwd_blocks
+// counts them; dL/dw is summed per lane over its rows, then over the row
+// groups of the wave and the 4 waves in fixed order.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void prologue_bwd_vec(PrologueArgs a) {
+#pragma clang fp contract(off)
+    constexpr int EPL = 4, LPR = D / EPL, RPI = 64 / LPR, HALF = D / 2;
+    static_assert(LPR >= 2 && LPR <= 64, "a row spans 2..64 lanes");
+    constexpr int ROWS_WG = 4 * prologue_bwd_rows_per_wave(prologue_elems_per_lane(D));
+    constexpr int GROUPS = ROWS_WG / 4 / RPI;  // row groups per wave
+    static_assert(GROUPS * RPI * 4 == ROWS_WG, "workgroup rows split evenly");
+    __shared__ float red[3][D];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, gl = lane % LPR;
+    const int p = gl * EPL;
+    const bool first = p < HALF;
+    const bool norm = a.norm != PROLOGUE_NORM_NONE;
+    const int64_t wave_row0 = (int64_t)blockIdx.x * ROWS_WG + w * (RPI * GROUPS);
+    // every row group's loads first
+    float gv[GROUPS][EPL], xv[GROUPS][EPL];
+    RowAddr ra[GROUPS];
+#pragma unroll
+    for (int g = 0; g < GROUPS; ++g) {
+        const int64_t r = wave_row0 + g * RPI + lane / LPR;
+        const bool live = r < a.rows;
+        ra[g] = row_addr(a, live ? r : 0);
+        if (live) {
+            Vec<float, EPL>::load(a.dy + a.sdy.at(ra[g].b, ra[g].h) + (int64_t)ra[g].s * a.sdy.s + p, gv[g]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) gv[g][e] = 0.f;
+        }
+        if (norm && live) {
+            Vec<T, EPL>::load((const T*)a.x + a.sx.at(ra[g].b, ra[g].h) + (int64_t)ra[g].s * a.sx.s + p, xv[g]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) xv[g][e] = 0.f;
+        }
+    }
+    float gw[EPL];
+    double we[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        gw[e] = 0.f;
+        const double wv = norm ? (double)a.w[p + e] : 0.0;
+        we[e] = a.norm == PROLOGUE_NORM_GEMMA ? 1.0 + wv : wv;
+    }
+#pragma unroll
+    for (int g = 0; g < GROUPS; ++g) {
+        const int64_t r = wave_row0 + g * RPI + lane / LPR;
+        const bool live = r < a.rows;
+        // gradient at the norm's output: R^T dy
+        if (a.rope) {
+            float c[EPL], sn[EPL];
+            pair_trig<EPL, LPR>(a, ra[g].s, p % HALF, first, c, sn);
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                const float pg = __shfl_xor(gv[g][e], LPR / 2, 64);
+                // first half: g1 c + g2 s; second half: -g1 s + g2 c
+                gv[g][e] = first ? gv[g][e] * c[e] + pg * sn[e] : -pg * sn[e] + gv[g][e] * c[e];
+            }
+        }
+        if (norm) {
+            double ss = 0.0, dot = 0.0;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                ss += (double)xv[g][e] * (double)xv[g][e];
+                dot += (double)gv[g][e] * we[e] * (double)xv[g][e];
+            }
+            ss = group_sum<LPR>(ss);
+            dot = group_sum<LPR>(dot);
+            const double inv = 1.0 / sqrt(ss / (double)D + (double)a.eps);
+            const double coeff = (inv * inv * inv) / (double)D;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                const float d = (float)((double)gv[g][e] * we[e] * inv - (double)xv[g][e] * coeff * dot);
+                if (live) gw[e] += (float)((double)gv[g][e] * (double)xv[g][e] * inv);
+                gv[g][e] = d;
+            }
+        }
+        if (live) Vec<float, EPL>::store(a.dx + a.sdx.at(ra[g].b, ra[g].h) + (int64_t)ra[g].s * a.sdx.s + p, gv[g]);
+    }
+    if (!norm || !a.dw_part) return;
+    // the wave's row groups, then the workgroup's waves, in fixed order
+#pragma unroll
+    for (int o = LPR; o < 64; o <<= 1)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) gw[e] += __shfl_xor(gw[e], o, 64);
+    if (w > 0 && lane < LPR) {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) red[w - 1][p + e] = gw[e];
+    }
+    __syncthreads();
+    if (w == 0 && lane < LPR) {
+        float* part = a.dw_part + (int64_t)blockIdx.x * D;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            float t = gw[e];
+            for (int q = 0; q < 3; ++q) t += red[q][p + e];
+            part[p + e] = t;
+        }
+    }
+}
+
 // Whether every row of a layout starts on a vbytes boundary.
 bool rows_aligned(const void* base, const Strides& st, int64_t esz, int vbytes) {
     const int64_t m = vbytes / esz;
@@ -357,10 +557,42 @@ hipError_t launch_shape(const PrologueArgs& a, bool bwd, hipStream_t st) {
     return hipGetLastError();
 }
 
+// The 16-byte-lane kernels, when the head dim and every row allow them.
+template <typename T, int D>
+bool launch_vec(const PrologueArgs& a, bool bwd, hipStream_t st, hipError_t* e) {
+    const int64_t esz = sizeof(T);
+    if (bwd) {
+        if constexpr (D / 4 > 64) {
+            return false;
+        } else {
+            if (!rows_aligned(a.dy, a.sdy, 4, 16) || !rows_aligned(a.dx, a.sdx, 4, 16)) return false;
+            if (a.norm != PROLOGUE_NORM_NONE && !rows_aligned(a.x, a.sx, esz, 4 * (int)esz)) return false;
+            hipLaunchKernelGGL((prologue_bwd_vec<T, D>), dim3((unsigned)prologue_bwd_blocks(a.rows, D)), dim3(256), 0,
+                               st, a);
+        }
+    } else {
+        constexpr int LPR = D * (int)sizeof(T) / 16;
+        if constexpr (LPR > 64) {
+            return false;
+        } else {
+            if (!rows_aligned(a.x, a.sx, esz, 16) || !rows_aligned(a.y, a.sy, esz, 16)) return false;
+            const int64_t per_block = 4 * (64 / LPR) * 2;
+            hipLaunchKernelGGL((prologue_fwd_vec<T, D>), dim3((unsigned)((a.rows + per_block - 1) / per_block)),
+                               dim3(256), 0, st, a);
+        }
+    }
+    *e = hipGetLastError();
+    return true;
+}
+
 template <typename T>
 hipError_t launch_t(const PrologueArgs& a, bool bwd, hipStream_t st) {
     const int half = a.D / 2;
     const int64_t esz = sizeof(T);
+    hipError_t ve = hipSuccess;
+    if (a.D == 128 && launch_vec<T, 128>(a, bwd, st, &ve)) return ve;
+    if (a.D == 256 && launch_vec<T, 256>(a, bwd, st, &ve)) return ve;
+    if (a.D == 512 && launch_vec<T, 512>(a, bwd, st, &ve)) return ve;
     if (half == 64 || half == 128 || half == 256) {
         const int V = half / 64;  // contiguous elements per lane
         bool ok;

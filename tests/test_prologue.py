@@ -25,6 +25,7 @@ CASES = [
     (3, 2, 50, 128, "f32", "gemma", 1e-6, 0.0),    # norm only
     (1, 2, 64, 200, "f32", "gemma", 1e-6, 1e4),    # strided lanes, 2 per half
     (1, 2, 48, 300, "bf16", "affine", 1e-6, 1e6),  # strided lanes, 4 per half
+    (2, 3, 70, 128, "bf16", "gemma", 1e-6, 1e6),   # 16-byte lanes, 4 rows per wave access
 ]
 
 
