@@ -27,6 +27,7 @@ EXPORTS = (
     "mft_prologue_fwd", "mft_prologue_workspace_size", "mft_prologue_bwd",
     "mft_lm_ce_workspace_size", "mft_lm_ce_fwd", "mft_lm_ce_bwd", "mft_lm_ce_streaming_fwd",
     "mft_lm_ce_streaming_bwd",
+    "mft_lora_workspace_size", "mft_lora_fwd", "mft_lora_bwd", "mft_lora_merge",
 )
 MFT_REDUCE_MEAN, MFT_REDUCE_SUM, MFT_REDUCE_NONE = 0, 1, 2
 
@@ -57,6 +58,18 @@ class PrologueDesc(C.Structure):
 class LmLossDesc(C.Structure):
     _fields_ = [("B", C.c_int64), ("S", C.c_int64), ("V", C.c_int64), ("H", C.c_int64),
                 ("dtype", C.c_int32), ("ignore_index", C.c_int32), ("reduction", C.c_int32), ("chunk", C.c_int32)]
+
+
+class LoraSlice(C.Structure):
+    _fields_ = [("A", C.c_void_p), ("B", C.c_void_p), ("grad_A", C.c_void_p), ("grad_B", C.c_void_p),
+                ("scale", C.c_float), ("a_transposed", C.c_int32), ("b_transposed", C.c_int32),
+                ("rank", C.c_int64), ("col0", C.c_int64), ("cols", C.c_int64)]
+
+
+class LoraDesc(C.Structure):
+    _fields_ = [("N", C.c_int64), ("in_dim", C.c_int64), ("out_dim", C.c_int64), ("w_dtype", C.c_int32),
+                ("w_transposed", C.c_int32), ("n_slices", C.c_int32), ("grads_for_column_slices", C.c_int32),
+                ("slices", C.POINTER(LoraSlice))]
 
 
 class MftError(RuntimeError):
@@ -107,7 +120,15 @@ def lib():
     L.mft_lm_ce_streaming_fwd.argtypes = [C.POINTER(LmLossDesc)] + [vp] * 8
     L.mft_lm_ce_streaming_bwd.restype = C.c_int
     L.mft_lm_ce_streaming_bwd.argtypes = [C.POINTER(LmLossDesc)] + [vp] * 9
-    if L.mft_version() != 3:
+    L.mft_lora_workspace_size.restype = C.c_int
+    L.mft_lora_workspace_size.argtypes = [C.POINTER(LoraDesc), C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+    L.mft_lora_fwd.restype = C.c_int
+    L.mft_lora_fwd.argtypes = [C.POINTER(LoraDesc)] + [vp] * 7
+    L.mft_lora_bwd.restype = C.c_int
+    L.mft_lora_bwd.argtypes = [C.POINTER(LoraDesc)] + [vp] * 7
+    L.mft_lora_merge.restype = C.c_int
+    L.mft_lora_merge.argtypes = [C.POINTER(LoraDesc), vp, C.c_float, vp]
+    if L.mft_version() != 4:
         raise RuntimeError("libmft_attn.so version mismatch")
     _lib = L
     return L
@@ -209,3 +230,35 @@ def lm_ce_streaming_bwd(d, hidden, weight, labels, lse, grad_loss, grad_hidden, 
                         stream) -> None:
     check(lib().mft_lm_ce_streaming_bwd(C.byref(d), hidden, weight, labels, lse, grad_loss, grad_hidden,
                                         grad_weight, workspace, stream))
+
+
+def lora_desc(N, in_dim, out_dim, w_dtype=MFT_F32, w_transposed=False, slices=(), grads_for_column_slices=False):
+    """slices: sequence of dicts with A, B, grad_A, grad_B (device pointers or None), scale, rank, col0, cols,
+    a_transposed, b_transposed.  The returned desc keeps its slice array alive."""
+    arr = (LoraSlice * max(1, len(slices)))()
+    for i, s in enumerate(slices):
+        arr[i] = LoraSlice(s["A"], s["B"], s.get("grad_A"), s.get("grad_B"), float(s["scale"]),
+                           int(bool(s.get("a_transposed", False))), int(bool(s.get("b_transposed", False))),
+                           int(s["rank"]), int(s.get("col0", 0)), int(s["cols"]))
+    d = LoraDesc(int(N), int(in_dim), int(out_dim), int(w_dtype), int(bool(w_transposed)), len(slices),
+                 int(bool(grads_for_column_slices)), C.cast(arr, C.POINTER(LoraSlice)))
+    d._slices = arr
+    return d
+
+
+def lora_workspace_size(d: LoraDesc):
+    f, b = C.c_size_t(), C.c_size_t()
+    check(lib().mft_lora_workspace_size(C.byref(d), C.byref(f), C.byref(b)))
+    return f.value, b.value
+
+
+def lora_fwd(d, x, W, bias, y, u, workspace, stream) -> None:
+    check(lib().mft_lora_fwd(C.byref(d), x, W, bias, y, u, workspace, stream))
+
+
+def lora_bwd(d, x, W, dy, u, dx, workspace, stream) -> None:
+    check(lib().mft_lora_bwd(C.byref(d), x, W, dy, u, dx, workspace, stream))
+
+
+def lora_merge(d, W, sign, stream) -> None:
+    check(lib().mft_lora_merge(C.byref(d), W, float(sign), stream))

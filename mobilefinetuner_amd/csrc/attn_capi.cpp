@@ -122,7 +122,7 @@ mft_status check_desc(const mft_attn_desc* d, mft::AttnShape* s) {
 
 extern "C" {
 
-int mft_version(void) { return 3; }
+int mft_version(void) { return 4; }
 
 const char* mft_last_error(void) { return mft::capi::g_last_error.c_str(); }
 

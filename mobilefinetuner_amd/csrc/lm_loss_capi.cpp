@@ -12,11 +12,9 @@
 // so the [N, V] logits never exist at once.
 #include "mft/lm_loss.h"
 
-#include <rocblas/rocblas.h>
-
-#include <mutex>
 #include <string>
 
+#include "blas_util.h"
 #include "capi_util.h"
 #include "lm_loss_kernels.h"
 
@@ -97,42 +95,13 @@ mft::CeArgs args(const mft_lm_loss_desc* d, const Layout& l, void* ws, const int
     return a;
 }
 
-// rocBLAS handle per device (created on first use; rocBLAS owns it until the
-// process ends).  Calls on one handle are serialised by the mutex.
-std::mutex g_blas_mu;
-rocblas_handle g_blas[64] = {};
-
-mft_status blas_handle(rocblas_handle* h) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
-        return fail(MFT_ERR_HIP, "mft_lm_ce: no current HIP device");
-    if (!g_blas[dev] && rocblas_create_handle(&g_blas[dev]) != rocblas_status_success)
-        return fail(MFT_ERR_HIP, "mft_lm_ce: rocblas_create_handle failed");
-    *h = g_blas[dev];
-    return MFT_OK;
-}
-
-// Column-major D = op(A) op(B) (+ D if accumulate), fp32 output and compute.
-mft_status gemm(rocblas_handle h, bool ta, bool tb, int64_t m, int64_t n, int64_t k, const void* A, int64_t lda,
-                const void* B, int64_t ldb, float* D, int64_t ldd, bool accumulate, bool bf16) {
-    const float alpha = 1.f, beta = accumulate ? 1.f : 0.f;
-    const rocblas_datatype ab = bf16 ? rocblas_datatype_bf16_r : rocblas_datatype_f32_r;
-    const rocblas_status st = rocblas_gemm_ex(
-        h, ta ? rocblas_operation_transpose : rocblas_operation_none,
-        tb ? rocblas_operation_transpose : rocblas_operation_none, (rocblas_int)m, (rocblas_int)n, (rocblas_int)k,
-        &alpha, A, ab, (rocblas_int)lda, B, ab, (rocblas_int)ldb, &beta, D, rocblas_datatype_f32_r, (rocblas_int)ldd,
-        D, rocblas_datatype_f32_r, (rocblas_int)ldd, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-    if (st != rocblas_status_success)
-        return fail(MFT_ERR_HIP, std::string("mft_lm_ce: rocblas_gemm_ex failed: ") + rocblas_status_to_string(st));
-    return MFT_OK;
-}
-
 // Z[N, nc] (row-major, fp32) = hidden[N, H] . W[v0 : v0 + nc, :]^T
 mft_status logits_chunk(rocblas_handle h, const mft_lm_loss_desc* d, const void* hidden, const void* weight,
                         int64_t v0, int64_t nc, float* Z) {
     const bool bf = d->dtype == MFT_BF16;
     const char* W = static_cast<const char*>(weight) + v0 * d->H * (bf ? 2 : 4);
-    return gemm(h, true, false, nc, d->B * d->S, d->H, W, d->H, hidden, d->H, Z, nc, false, bf);
+    return mft::blas::gemm_rm("mft_lm_ce", h, d->B * d->S, nc, d->H, 1.f, hidden, d->H, false, W, d->H, true, 0.f, Z,
+                              nc, bf);
 }
 
 }  // namespace
@@ -199,12 +168,9 @@ mft_status mft_lm_ce_streaming_fwd(const mft_lm_loss_desc* desc, const void* hid
     char* w = static_cast<char*>(workspace);
     float* Z = reinterpret_cast<float*>(w + l.z);
     const int64_t chunk = chunk_of(desc);
-    std::lock_guard<std::mutex> lock(g_blas_mu);
+    auto lock = mft::blas::lock();
     rocblas_handle h;
-    if ((r = blas_handle(&h)) != MFT_OK) return r;
-    if (rocblas_set_stream(h, stream) != rocblas_status_success ||
-        rocblas_set_workspace(h, w + l.blas, kBlasWorkspace) != rocblas_status_success)
-        return fail(MFT_ERR_HIP, "mft_lm_ce_streaming_fwd: rocblas_set_stream / set_workspace failed");
+    if ((r = mft::blas::bind("mft_lm_ce_streaming_fwd", stream, w + l.blas, kBlasWorkspace, &h)) != MFT_OK) return r;
     for (int64_t v0 = 0; v0 < desc->V; v0 += chunk) {
         const int64_t nc = desc->V - v0 < chunk ? desc->V - v0 : chunk;
         if ((r = logits_chunk(h, desc, hidden, weight, v0, nc, Z)) != MFT_OK) return r;
@@ -234,12 +200,9 @@ mft_status mft_lm_ce_streaming_bwd(const mft_lm_loss_desc* desc, const void* hid
     const int64_t chunk = chunk_of(desc), N = desc->B * desc->S, H = desc->H;
     hipError_t e = mft::launch_ce_count(a, stream);
     if (e != hipSuccess) return hip_status(e, "mft_lm_ce_streaming_bwd launch");
-    std::lock_guard<std::mutex> lock(g_blas_mu);
+    auto lock = mft::blas::lock();
     rocblas_handle h;
-    if ((r = blas_handle(&h)) != MFT_OK) return r;
-    if (rocblas_set_stream(h, stream) != rocblas_status_success ||
-        rocblas_set_workspace(h, w + l.blas, kBlasWorkspace) != rocblas_status_success)
-        return fail(MFT_ERR_HIP, "mft_lm_ce_streaming_bwd: rocblas_set_stream / set_workspace failed");
+    if ((r = mft::blas::bind("mft_lm_ce_streaming_bwd", stream, w + l.blas, kBlasWorkspace, &h)) != MFT_OK) return r;
     for (int64_t v0 = 0; v0 < desc->V; v0 += chunk) {
         const int64_t nc = desc->V - v0 < chunk ? desc->V - v0 : chunk;
         if ((r = logits_chunk(h, desc, hidden, weight, v0, nc, Z)) != MFT_OK) return r;
@@ -247,11 +210,12 @@ mft_status mft_lm_ce_streaming_bwd(const mft_lm_loss_desc* desc, const void* hid
         if (e != hipSuccess) return hip_status(e, "mft_lm_ce_streaming_bwd launch");
         const char* Wc = static_cast<const char*>(weight) + v0 * H * (bf ? 2 : 4);
         // grad_hidden[N, H] (+)= G[N, nc] . W_c[nc, H]
-        if (grad_hidden && (r = gemm(h, false, false, H, N, nc, Wc, H, G, nc, grad_hidden, H, v0 > 0, bf)) != MFT_OK)
+        if (grad_hidden && (r = mft::blas::gemm_rm("mft_lm_ce_streaming_bwd", h, N, H, nc, 1.f, G, nc, false, Wc, H,
+                                                   false, v0 > 0 ? 1.f : 0.f, grad_hidden, H, bf)) != MFT_OK)
             return r;
         // grad_weight[v0 : v0 + nc, :] = G^T . hidden
-        if (grad_weight &&
-            (r = gemm(h, false, true, H, nc, N, hidden, H, G, nc, grad_weight + v0 * H, H, false, bf)) != MFT_OK)
+        if (grad_weight && (r = mft::blas::gemm_rm("mft_lm_ce_streaming_bwd", h, nc, H, N, 1.f, G, nc, true, hidden, H,
+                                                   false, 0.f, grad_weight + v0 * H, H, bf)) != MFT_OK)
             return r;
     }
     return MFT_OK;

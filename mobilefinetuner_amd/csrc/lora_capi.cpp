@@ -1,0 +1,263 @@
+// C ABI of the LoRA linear layer (declared in include/mft/lora.h).
+//
+// The layer is GEMMs plus element-wise staging.  Row-major throughout, R =
+// sum of the slices' ranks, s_i = scale_i:
+//   forward   y  = x . W (+ bias)                 rocBLAS; bf16 W: x staged
+//                                                  to bf16 (lora_round_bf16)
+//             u_i = x . A_i                        fp32, into u[:, ro_i ..]
+//             y[:, col0_i ..] += s_i u_i . B_i     fp32, beta = 1
+//   backward  g_i = s_i dy[:, col0_i ..] . B_i^T   fp32 (workspace [N, R])
+//             grad_B_i = s_i u_i^T . dy[:, col0_i ..]
+//             grad_A_i = x^T . g_i
+//             dx = dy . W^T + sum_i g_i . A_i^T     bf16 W: dy staged to bf16
+// which is the reference's autograd graph of matmul / mul / add
+// (nn/lora_linear.cpp:384-434 with MatmulBackward,
+// core/backward_functions.cpp:94-160).  Validation messages follow the
+// reference's (nn/lora_linear.cpp:52-88, 118-128, 397-404).
+#include "mft/lora.h"
+
+#include <cmath>
+#include <string>
+
+#include "blas_util.h"
+#include "capi_util.h"
+#include "lora_kernels.h"
+
+namespace {
+
+using namespace mft::capi;
+
+constexpr size_t kBlasWorkspace = size_t(32) << 20;
+constexpr int64_t kMaxInt = (int64_t(1) << 31) - 1;
+
+size_t up(size_t x) { return (x + 255) & ~size_t(255); }
+
+int64_t total_rank(const mft_lora_desc* d) {
+    int64_t r = 0;
+    for (int i = 0; i < d->n_slices; ++i) r += d->slices[i].rank;
+    return r;
+}
+
+mft_status check(const mft_lora_desc* d, const char* who) {
+    if (!d) return fail(MFT_ERR_INVALID_ARG, std::string(who) + ": desc is NULL");
+    if (d->N <= 0 || d->in_dim <= 0 || d->out_dim <= 0)
+        return fail(MFT_ERR_INVALID_ARG, "LoRALinear: x must be [N, in] and W [in, out] with positive sizes");
+    if (d->w_dtype != MFT_F32 && d->w_dtype != MFT_BF16)
+        return fail(MFT_ERR_INVALID_ARG, std::string(who) + ": w_dtype must be MFT_F32 or MFT_BF16");
+    if (d->n_slices < 0 || (d->n_slices > 0 && !d->slices))
+        return fail(MFT_ERR_INVALID_ARG, std::string(who) + ": n_slices > 0 needs a slices array");
+    if (d->N > kMaxInt || d->in_dim > kMaxInt || d->out_dim > kMaxInt)
+        return fail(MFT_ERR_UNSUPPORTED, std::string(who) + ": N, in and out must be below 2^31");
+    for (int i = 0; i < d->n_slices; ++i) {
+        const mft_lora_slice& s = d->slices[i];
+        if (!s.A || !s.B) return fail(MFT_ERR_INVALID_ARG, "LoRALinear::attach_lora: A and B must not be null");
+        if (s.rank <= 0) return fail(MFT_ERR_INVALID_ARG, "LoRALinear: LoRA rank must be positive");
+        if (s.cols <= 0) return fail(MFT_ERR_INVALID_ARG, "LoRALinear: LoRA slice cols must be positive");
+        if (s.col0 < 0 || s.col0 + s.cols > d->out_dim)
+            return fail(MFT_ERR_INVALID_ARG, "LoRALinear: LoRA slice range exceeds base weight width");
+        if (s.rank > kMaxInt) return fail(MFT_ERR_UNSUPPORTED, std::string(who) + ": rank must be below 2^31");
+    }
+    if (total_rank(d) > kMaxInt) return fail(MFT_ERR_UNSUPPORTED, std::string(who) + ": total rank too large");
+    return MFT_OK;
+}
+
+// A slice whose delta is part of the autograd graph (see mft/lora.h).
+bool has_grad(const mft_lora_desc* d, const mft_lora_slice& s) {
+    return d->grads_for_column_slices || (s.col0 == 0 && s.cols == d->out_dim);
+}
+
+struct FwdLayout {
+    size_t xb, u, blas, total;
+};
+struct BwdLayout {
+    size_t dyb, g, blas, total;
+};
+
+FwdLayout fwd_layout(const mft_lora_desc* d) {
+    FwdLayout l{};
+    size_t o = 0;
+    l.xb = o, o += d->w_dtype == MFT_BF16 ? up((size_t)d->N * d->in_dim * 2) : 0;
+    l.u = o, o += up((size_t)d->N * total_rank(d) * 4);
+    l.blas = o, o += kBlasWorkspace;
+    l.total = o;
+    return l;
+}
+
+BwdLayout bwd_layout(const mft_lora_desc* d) {
+    BwdLayout l{};
+    size_t o = 0;
+    l.dyb = o, o += d->w_dtype == MFT_BF16 ? up((size_t)d->N * d->out_dim * 2) : 0;
+    l.g = o, o += up((size_t)d->N * total_rank(d) * 4);
+    l.blas = o, o += kBlasWorkspace;
+    l.total = o;
+    return l;
+}
+
+// op(W) as the right operand of x . W ([in, out]) or of dy . W^T ([out, in]).
+struct WOperand {
+    int64_t ld;
+    bool t;
+};
+WOperand w_for_forward(const mft_lora_desc* d) {
+    return d->w_transposed ? WOperand{d->in_dim, true} : WOperand{d->out_dim, false};
+}
+WOperand w_for_backward(const mft_lora_desc* d) {
+    return d->w_transposed ? WOperand{d->in_dim, false} : WOperand{d->out_dim, true};
+}
+
+}  // namespace
+
+extern "C" {
+
+mft_status mft_lora_workspace_size(const mft_lora_desc* desc, size_t* fwd_bytes, size_t* bwd_bytes) {
+    mft_status r = check(desc, "mft_lora_workspace_size");
+    if (r != MFT_OK) return r;
+    if (fwd_bytes) *fwd_bytes = fwd_layout(desc).total;
+    if (bwd_bytes) *bwd_bytes = bwd_layout(desc).total;
+    return MFT_OK;
+}
+
+mft_status mft_lora_fwd(const mft_lora_desc* desc, const float* x, const void* W, const float* bias, float* y,
+                        float* u, void* workspace, hipStream_t stream) {
+    static const char* who = "mft_lora_fwd";
+    mft_status r = check(desc, who);
+    if (r != MFT_OK) return r;
+    if (!x || !W || !y || !workspace)
+        return fail(MFT_ERR_INVALID_ARG, "mft_lora_fwd: x, W, y and workspace must be non-NULL");
+    const FwdLayout l = fwd_layout(desc);
+    char* ws = static_cast<char*>(workspace);
+    const int64_t N = desc->N, in = desc->in_dim, out = desc->out_dim, R = total_rank(desc);
+    const bool bf = desc->w_dtype == MFT_BF16;
+    if (!u) u = reinterpret_cast<float*>(ws + l.u);
+
+    hipError_t e = hipSuccess;
+    if (bias) e = mft::launch_lora_fill_bias(y, bias, N, out, stream);
+    const void* xo = x;
+    if (e == hipSuccess && bf) {
+        e = mft::launch_lora_round_bf16(x, reinterpret_cast<uint16_t*>(ws + l.xb), N * in, stream);
+        xo = ws + l.xb;
+    }
+    if (e != hipSuccess) return hip_status(e, "mft_lora_fwd launch");
+
+    auto lock = mft::blas::lock();
+    rocblas_handle h;
+    if ((r = mft::blas::bind(who, stream, ws + l.blas, kBlasWorkspace, &h)) != MFT_OK) return r;
+    const WOperand wo = w_for_forward(desc);
+    if ((r = mft::blas::gemm_rm(who, h, N, out, in, 1.f, xo, in, false, W, wo.ld, wo.t, bias ? 1.f : 0.f, y, out,
+                                bf)) != MFT_OK)
+        return r;
+    int64_t ro = 0;
+    for (int i = 0; i < desc->n_slices; ++i) {
+        const mft_lora_slice& s = desc->slices[i];
+        // u_i[N, r] = x . A_i
+        if ((r = mft::blas::gemm_rm(who, h, N, s.rank, in, 1.f, x, in, false, s.A, s.a_transposed ? in : s.rank,
+                                    s.a_transposed != 0, 0.f, u + ro, R, false)) != MFT_OK)
+            return r;
+        // y[:, col0 .. col0 + cols] += scale * u_i . B_i
+        if ((r = mft::blas::gemm_rm(who, h, N, s.cols, s.rank, s.scale, u + ro, R, false, s.B,
+                                    s.b_transposed ? s.rank : s.cols, s.b_transposed != 0, 1.f, y + s.col0, out,
+                                    false)) != MFT_OK)
+            return r;
+        ro += s.rank;
+    }
+    return MFT_OK;
+}
+
+mft_status mft_lora_bwd(const mft_lora_desc* desc, const float* x, const void* W, const float* dy, const float* u,
+                        float* dx, void* workspace, hipStream_t stream) {
+    static const char* who = "mft_lora_bwd";
+    mft_status r = check(desc, who);
+    if (r != MFT_OK) return r;
+    if (!x || !W || !dy || !workspace || (desc->n_slices > 0 && !u))
+        return fail(MFT_ERR_INVALID_ARG, "mft_lora_bwd: x, W, dy, u (with slices) and workspace must be non-NULL");
+    const BwdLayout l = bwd_layout(desc);
+    char* ws = static_cast<char*>(workspace);
+    const int64_t N = desc->N, in = desc->in_dim, out = desc->out_dim, R = total_rank(desc);
+    const bool bf = desc->w_dtype == MFT_BF16;
+    float* g = reinterpret_cast<float*>(ws + l.g);
+
+    const void* dyo = dy;
+    if (dx && bf) {
+        const hipError_t e = mft::launch_lora_round_bf16(dy, reinterpret_cast<uint16_t*>(ws + l.dyb), N * out, stream);
+        if (e != hipSuccess) return hip_status(e, "mft_lora_bwd launch");
+        dyo = ws + l.dyb;
+    }
+
+    auto lock = mft::blas::lock();
+    rocblas_handle h;
+    if ((r = mft::blas::bind(who, stream, ws + l.blas, kBlasWorkspace, &h)) != MFT_OK) return r;
+    int64_t ro = 0;
+    for (int i = 0; i < desc->n_slices; ++i) {
+        const mft_lora_slice& s = desc->slices[i];
+        const int64_t rk = s.rank;
+        if (has_grad(desc, s)) {
+            const float* dys = dy + s.col0;
+            // g_i[N, r] = scale * dy_slice . B_i^T
+            if ((r = mft::blas::gemm_rm(who, h, N, rk, s.cols, s.scale, dys, out, false, s.B,
+                                        s.b_transposed ? rk : s.cols, s.b_transposed == 0, 0.f, g + ro, R, false)) !=
+                MFT_OK)
+                return r;
+            if (s.grad_B) {
+                // [r, cols] = scale * u_i^T . dy_slice, or its transpose for a [cols, r] B
+                r = s.b_transposed
+                        ? mft::blas::gemm_rm(who, h, s.cols, rk, N, s.scale, dys, out, true, u + ro, R, false, 0.f,
+                                             s.grad_B, rk, false)
+                        : mft::blas::gemm_rm(who, h, rk, s.cols, N, s.scale, u + ro, R, true, dys, out, false, 0.f,
+                                             s.grad_B, s.cols, false);
+                if (r != MFT_OK) return r;
+            }
+            if (s.grad_A) {
+                // [in, r] = x^T . g_i, or its transpose for an [r, in] A
+                r = s.a_transposed ? mft::blas::gemm_rm(who, h, rk, in, N, 1.f, g + ro, R, true, x, in, false, 0.f,
+                                                        s.grad_A, in, false)
+                                   : mft::blas::gemm_rm(who, h, in, rk, N, 1.f, x, in, true, g + ro, R, false, 0.f,
+                                                        s.grad_A, rk, false);
+                if (r != MFT_OK) return r;
+            }
+        }
+        ro += rk;
+    }
+    if (!dx) return MFT_OK;
+    const WOperand wo = w_for_backward(desc);
+    if ((r = mft::blas::gemm_rm(who, h, N, in, out, 1.f, dyo, out, false, W, wo.ld, wo.t, 0.f, dx, in, bf)) != MFT_OK)
+        return r;
+    ro = 0;
+    for (int i = 0; i < desc->n_slices; ++i) {
+        const mft_lora_slice& s = desc->slices[i];
+        // dx += g_i . A_i^T
+        if (has_grad(desc, s) &&
+            (r = mft::blas::gemm_rm(who, h, N, in, s.rank, 1.f, g + ro, R, false, s.A, s.a_transposed ? in : s.rank,
+                                    s.a_transposed == 0, 1.f, dx, in, false)) != MFT_OK)
+            return r;
+        ro += s.rank;
+    }
+    return MFT_OK;
+}
+
+mft_status mft_lora_merge(const mft_lora_desc* desc, void* W, float sign, hipStream_t stream) {
+    mft_status r = check(desc, "mft_lora_merge");
+    if (r != MFT_OK) return r;
+    if (!W) return fail(MFT_ERR_INVALID_ARG, "mft_lora_merge: W must be non-NULL");
+    for (int i = 0; i < desc->n_slices; ++i) {
+        const mft_lora_slice& s = desc->slices[i];
+        mft::LoraMergeArgs a{};
+        a.W = W;
+        a.A = s.A;
+        a.B = s.B;
+        a.sign_scale = sign * s.scale;
+        a.w_bf16 = desc->w_dtype == MFT_BF16;
+        a.w_transposed = desc->w_transposed;
+        a.a_transposed = s.a_transposed;
+        a.b_transposed = s.b_transposed;
+        a.in = desc->in_dim;
+        a.out = desc->out_dim;
+        a.rank = s.rank;
+        a.col0 = s.col0;
+        a.cols = s.cols;
+        const hipError_t e = mft::launch_lora_merge(a, stream);
+        if (e != hipSuccess) return hip_status(e, "mft_lora_merge launch");
+    }
+    return MFT_OK;
+}
+
+}  // extern "C"

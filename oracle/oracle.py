@@ -78,6 +78,10 @@ def lib():
                                       _f32p, C.c_void_p, C.c_void_p]
         L.orc_prologue_fwd.argtypes = [_f32p, C.c_void_p, _i64, _i64, _i64, _i64, C.c_int, C.c_float, C.c_float,
                                        _f32p]
+        L.orc_lora.argtypes = [_f32p, _f32p, C.c_void_p, _i64, _i64, _i64, C.c_int, C.c_int, C.c_int, C.c_void_p, _f32p,
+                               _f32p, _f32p, C.c_int, C.c_void_p, _f32p, C.c_void_p, _f32p, _f32p, C.c_void_p]
+        L.orc_lora_merge.argtypes = [_f32p, C.c_int, _i64, _i64, C.c_int, C.c_void_p, _f32p, _f32p, _f32p,
+                                     C.c_float]
         L.orc_prologue_bwd.argtypes = [_f32p, C.c_void_p, _f32p, _i64, _i64, _i64, _i64, C.c_int, C.c_float,
                                        C.c_float, _f32p, C.c_void_p]
         _lib = L
@@ -117,6 +121,10 @@ def ref():
         R.mftref_prologue.argtypes = [_f32p, opt, opt, _i64, _i64, _i64, _i64, C.c_int, C.c_float, C.c_float,
                                       _f32p, opt, opt]
         R.mftref_f32_to_bf16_bits.restype = C.c_uint16
+        R.mftref_lora.argtypes = [_f32p, _f32p, C.c_void_p, _i64, _i64, _i64, C.c_int, C.c_int, C.c_int,
+                                  C.c_void_p, _f32p, _f32p, _f32p, C.c_void_p, _f32p, C.c_void_p, _f32p, _f32p,
+                                  C.c_void_p]
+        R.mftref_lora_merge.argtypes = [_f32p, C.c_int, _i64, _i64, C.c_int, C.c_void_p, _f32p, _f32p, _f32p]
         R.mftref_f32_to_bf16_bits.argtypes = [C.c_float]
         _ref = R
     return _ref
@@ -515,3 +523,100 @@ def rel_l2(x, ref) -> float:
     nb = np.sum(ref * ref)
     nd = np.sum((x - ref) ** 2)
     return float(math.sqrt(nd / nb)) if nb > 0 else float(math.sqrt(nd))
+
+
+# ------------------------------------------------------------- LoRA linear
+def _lora_pack(slices, in_dim):
+    """slices: dicts with A, B (fp32 arrays in their stored layout), scale, col0,
+    a_transposed, b_transposed.  Returns (meta int64 [n, 5], scale, A_all, B_all)."""
+    meta, sc, As, Bs = [], [], [], []
+    for sl in slices:
+        A, B = np.asarray(sl["A"], np.float32), np.asarray(sl["B"], np.float32)
+        at, bt = bool(sl.get("a_transposed", False)), bool(sl.get("b_transposed", False))
+        r = A.shape[0] if at else A.shape[1]
+        cols = B.shape[0] if bt else B.shape[1]
+        meta.append([r, int(sl.get("col0", 0)), cols, int(at), int(bt)])
+        sc.append(float(sl["scale"]))
+        As.append(A.ravel())
+        Bs.append(B.ravel())
+    meta = np.ascontiguousarray(np.array(meta, np.int64).reshape(-1, 5))
+    cat = lambda xs: np.ascontiguousarray(np.concatenate(xs) if xs else np.zeros(1, np.float32), np.float32)
+    return meta, np.ascontiguousarray(np.array(sc or [0.0], np.float32)), cat(As), cat(Bs)
+
+
+def _lora_unpack(flat, slices, key):
+    out, o = [], 0
+    for sl in slices:
+        n = np.asarray(sl[key]).size
+        out.append(flat[o:o + n].reshape(np.asarray(sl[key]).shape))
+        o += n
+    return out
+
+
+def _lora_prep(x, W, bias, slices, w_transposed, dy):
+    x = np.ascontiguousarray(x, np.float32)
+    W = np.ascontiguousarray(W, np.float32)
+    N, in_dim = x.shape
+    out = W.shape[0] if w_transposed else W.shape[1]
+    meta, sc, A_all, B_all = _lora_pack(slices, in_dim)
+    y = np.zeros((N, out), np.float32)
+    dx = np.zeros_like(x) if dy is not None else None
+    dA = np.full(A_all.shape, np.nan, np.float32)
+    dB = np.full(B_all.shape, np.nan, np.float32)
+    has = np.zeros(max(1, len(slices)), np.int32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    dyc = None if dy is None else np.ascontiguousarray(dy, np.float32)
+    return x, W, N, in_dim, out, meta, sc, A_all, B_all, y, dx, dA, dB, has, b, dyc
+
+
+def lora(x, W, bias=None, slices=(), w_transposed=False, dy=None, all_grads=False, w_bf16=False):
+    """ops::LoRALinear forward (and, with dy, the Engine backward) on fp32 x
+    [N, in]; W [in, out] (or [out, in] with w_transposed) as fp32 values,
+    those of a bf16 weight with w_bf16.  Returns y, dx, grad_A / grad_B lists
+    (None where the slice has no gradient)."""
+    slices = list(slices)
+    x, W, N, in_dim, out, meta, sc, A_all, B_all, y, dx, dA, dB, has, b, dyc = _lora_prep(
+        x, W, bias, slices, w_transposed, dy)
+    lib().orc_lora(x, W, _ptr(b), N, in_dim, out, int(bool(w_transposed)), int(bool(w_bf16)), len(slices), meta.ctypes.data, sc, A_all,
+                   B_all, int(bool(all_grads)), _ptr(dyc), y, _ptr(dx), dA, dB, has.ctypes.data)
+    return _lora_result(y, dx, dA, dB, has, slices, dy is not None)
+
+
+def ref_lora(x, W, bias=None, slices=(), w_transposed=False, dy=None, w_bf16=False):
+    """The real ops::LoRALinear (oracle/_ref), same arguments as lora()."""
+    slices = list(slices)
+    x, W, N, in_dim, out, meta, sc, A_all, B_all, y, dx, dA, dB, has, b, dyc = _lora_prep(
+        x, W, bias, slices, w_transposed, dy)
+    rc = ref().mftref_lora(x, W, _ptr(b), N, in_dim, out, int(bool(w_transposed)), int(bool(w_bf16)), len(slices),
+                           meta.ctypes.data, sc, A_all, B_all, _ptr(dyc), y, _ptr(dx), dA, dB, has.ctypes.data)
+    if rc != 0:
+        raise RuntimeError("mftref_lora failed")
+    return _lora_result(y, dx, dA, dB, has, slices, dy is not None)
+
+
+def _lora_result(y, dx, dA, dB, has, slices, grad):
+    res = dict(y=y, dx=dx, grad_A=[], grad_B=[])
+    if grad:
+        for i, (a, bb) in enumerate(zip(_lora_unpack(dA, slices, "A"), _lora_unpack(dB, slices, "B"))):
+            res["grad_A"].append(a if has[i] else None)
+            res["grad_B"].append(bb if has[i] else None)
+    return res
+
+
+def lora_merge(W, slices, w_bf16=False, sign=1.0):
+    """apply_lora_delta_to_base of every slice on W [in, out] (values); returns the new W."""
+    W = np.array(W, np.float32, copy=True)
+    meta, sc, A_all, B_all = _lora_pack(list(slices), W.shape[0])
+    lib().orc_lora_merge(W, int(bool(w_bf16)), W.shape[0], W.shape[1], len(slices), meta.ctypes.data, sc, A_all,
+                         B_all, float(sign))
+    return W
+
+
+def ref_lora_merge(W, slices, w_bf16=False):
+    """The real LoRALinear::merge_to_base (oracle/_ref) on W [in, out]."""
+    W = np.array(W, np.float32, copy=True)
+    meta, sc, A_all, B_all = _lora_pack(list(slices), W.shape[0])
+    if ref().mftref_lora_merge(W, int(bool(w_bf16)), W.shape[0], W.shape[1], len(slices), meta.ctypes.data, sc,
+                               A_all, B_all) != 0:
+        raise RuntimeError("mftref_lora_merge failed")
+    return W

@@ -17,11 +17,13 @@
 #include "core/memory_efficient_attention.h"
 #include "core/memory_manager.h"
 #include "core/ops.h"
+#include "nn/lora_linear.h"
 
 #include <chrono>
 #include <cstring>
 #include <exception>
 #include <iostream>
+#include <vector>
 
 using namespace ops;
 
@@ -294,6 +296,99 @@ int mftref_streaming_ce(const float* hidden, const float* weight, const int32_t*
     } catch (const std::exception& e) {
         std::cerr << "[mftref_streaming_ce] " << e.what() << std::endl;
         autograd::Engine::instance().clear_graph();
+        return -1;
+    }
+}
+
+
+// ops::LoRALinear (nn/lora_linear.cpp) forward and Engine backward, slices
+// packed as in orc_lora (refcpu.h).  W is built fp32 or, with w_bf16, bf16
+// from its (bf16-exact) values; x, A, B require grad.  A slice without a
+// gradient (the reference gives column-range slices none) leaves its dA/dB
+// untouched and has_grad[i] = 0.
+int mftref_lora(const float* x, const float* W, const float* bias, int64_t N, int64_t in, int64_t out,
+                int w_transposed, int w_bf16, int n, const int64_t* meta, const float* scale, const float* A_all,
+                const float* B_all, const float* dy, float* y, float* dx, float* dA_all, float* dB_all,
+                int32_t* has_grad) {
+    try {
+        const std::vector<int64_t> wshape = w_transposed ? std::vector<int64_t>{out, in} : std::vector<int64_t>{in, out};
+        TensorPtr Wt;
+        if (w_bf16) {
+            Wt = std::make_shared<Tensor>(wshape, kBFloat16, kCPU);
+            for (int64_t i = 0; i < in * out; ++i) Wt->data<uint16_t>()[i] = float32_to_bf16_bits(W[i]);
+        } else {
+            Wt = from_host(W, wshape, false);
+        }
+        TensorPtr bt = bias ? from_host(bias, {out}, false) : nullptr;
+        LoRALinear layer(Wt, bt);
+        std::vector<TensorPtr> As, Bs;
+        const float* Ap = A_all;
+        const float* Bp = B_all;
+        for (int i = 0; i < n; ++i) {
+            const int64_t* m = meta + 5 * i;
+            const int64_t r = m[0], cols = m[2];
+            As.push_back(from_host(Ap, m[3] ? std::vector<int64_t>{r, in} : std::vector<int64_t>{in, r}, true));
+            Bs.push_back(from_host(Bp, m[4] ? std::vector<int64_t>{cols, r} : std::vector<int64_t>{r, cols}, true));
+            layer.attach_lora(As.back(), Bs.back(), scale[i], (int)m[1], (int)cols);
+            Ap += in * r;
+            Bp += r * cols;
+        }
+        auto xt = from_host(x, {1, N, in}, dy != nullptr);
+        auto yt = layer.forward(xt);
+        to_host(yt, y);
+        if (dy) {
+            autograd::Engine::instance().run_backward({yt}, {from_host(dy, {1, N, out}, false)});
+            if (dx) to_host(xt->grad(), dx);
+            float* dA = dA_all;
+            float* dB = dB_all;
+            for (int i = 0; i < n; ++i) {
+                const int64_t r = meta[5 * i], cols = meta[5 * i + 2];
+                if (has_grad) has_grad[i] = As[i]->grad() != nullptr;
+                to_host(As[i]->grad(), dA);
+                to_host(Bs[i]->grad(), dB);
+                dA += in * r;
+                dB += r * cols;
+            }
+        }
+        autograd::Engine::instance().clear_graph();
+        return 0;
+    } catch (const std::exception& e) {
+        std::cerr << "[mftref_lora] " << e.what() << std::endl;
+        autograd::Engine::instance().clear_graph();
+        return -1;
+    }
+}
+
+// LoRALinear::merge_to_base (nn/lora_linear.cpp:446-460) on W [in, out]
+// (fp32, or bf16 with w_bf16: values in and out as floats).
+int mftref_lora_merge(float* W, int w_bf16, int64_t in, int64_t out, int n, const int64_t* meta, const float* scale,
+                      const float* A_all, const float* B_all) {
+    try {
+        TensorPtr Wt;
+        if (w_bf16) {
+            Wt = std::make_shared<Tensor>(std::vector<int64_t>{in, out}, kBFloat16, kCPU);
+            for (int64_t i = 0; i < in * out; ++i) Wt->data<uint16_t>()[i] = float32_to_bf16_bits(W[i]);
+        } else {
+            Wt = from_host(W, {in, out}, false);
+        }
+        LoRALinear layer(Wt);
+        const float* Ap = A_all;
+        const float* Bp = B_all;
+        for (int i = 0; i < n; ++i) {
+            const int64_t* m = meta + 5 * i;
+            const int64_t r = m[0], cols = m[2];
+            layer.attach_lora(from_host(Ap, m[3] ? std::vector<int64_t>{r, in} : std::vector<int64_t>{in, r}, false),
+                              from_host(Bp, m[4] ? std::vector<int64_t>{cols, r} : std::vector<int64_t>{r, cols}, false),
+                              scale[i], (int)m[1], (int)cols);
+            Ap += in * r;
+            Bp += r * cols;
+        }
+        layer.merge_to_base();
+        for (int64_t i = 0; i < in * out; ++i)
+            W[i] = w_bf16 ? bf16_bits_to_float32(Wt->data<uint16_t>()[i]) : Wt->data<float>()[i];
+        return 0;
+    } catch (const std::exception& e) {
+        std::cerr << "[mftref_lora_merge] " << e.what() << std::endl;
         return -1;
     }
 }

@@ -614,4 +614,138 @@ int orc_selected_ce(const float* hidden, const float* weight, const int32_t* lab
     return 0;
 }
 
+
+// ---- LoRA linear ----
+
+// A_eff [in, r] and B_eff [r, cols] of slice i (materialised transposes, as
+// the reference's transpose() makes them), and the offsets of the next slice.
+static void lora_eff(const int64_t* m, int64_t in, const float* A, const float* B, std::vector<float>& Ae,
+                     std::vector<float>& Be) {
+    const int64_t r = m[0], cols = m[2];
+    Ae.assign(A, A + in * r);
+    Be.assign(B, B + r * cols);
+    if (m[3]) transpose2d(A, Ae.data(), r, in);
+    if (m[4]) transpose2d(B, Be.data(), cols, r);
+}
+
+// C[M,N] = A[M,K] . B[N,K]^T with the association of the reference's
+// matmul_fallback_nt_mixed_b (core/ops.cpp:211-246), its path for a bf16
+// right operand: per 64-wide block of k a fresh float sum in k order, added
+// to C[i][j] block by block.
+static void mm_nt_blocked64(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K) {
+    std::fill(C, C + M * N, 0.0f);
+    for (int64_t k0 = 0; k0 < K; k0 += 64) {
+        const int64_t k1 = std::min(K, k0 + 64);
+        for (int64_t i = 0; i < M; ++i)
+            for (int64_t j = 0; j < N; ++j) {
+                float sum = 0.0f;
+                for (int64_t k = k0; k < k1; ++k) sum += A[i * K + k] * B[j * K + k];
+                C[i * N + j] += sum;
+            }
+    }
+}
+
+void orc_lora(const float* x, const float* W, const float* bias, int64_t N, int64_t in, int64_t out, int w_transposed,
+              int w_lowp, int n, const int64_t* meta, const float* scale, const float* A_all, const float* B_all,
+              int all_grads, const float* dy, float* y, float* dx, float* dA_all, float* dB_all, int32_t* has_grad) {
+    // Base: y = matmul(x, W_eff), W_eff = W or its transpose [in, out].
+    std::vector<float> We(W, W + in * out);
+    if (w_transposed) transpose2d(W, We.data(), out, in);
+    mm_nn(x, We.data(), y, N, out, in);
+    if (bias)
+        for (int64_t i = 0; i < N; ++i)
+            for (int64_t o = 0; o < out; ++o) y[i * out + o] = y[i * out + o] + bias[o];
+    std::vector<float> Ae, Be, xa, delta, ds, g, tmp, tmp2;
+    const float* Ap = A_all;
+    const float* Bp = B_all;
+    std::vector<std::vector<float>> gs(n), Aes(n);
+    for (int i = 0; i < n; ++i) {
+        const int64_t* m = meta + 5 * i;
+        const int64_t r = m[0], col0 = m[1], cols = m[2];
+        lora_eff(m, in, Ap, Bp, Ae, Be);
+        xa.assign(N * r, 0.f);
+        mm_nn(x, Ae.data(), xa.data(), N, r, in);
+        delta.assign(N * cols, 0.f);
+        mm_nn(xa.data(), Be.data(), delta.data(), N, cols, r);
+        for (auto& v : delta) v = v * scale[i];
+        for (int64_t t = 0; t < N; ++t)
+            for (int64_t c = 0; c < cols; ++c) y[t * out + col0 + c] = y[t * out + col0 + c] + delta[t * cols + c];
+        const bool grad = all_grads || (col0 == 0 && cols == out);
+        if (has_grad) has_grad[i] = grad;
+        if (dy && grad) {
+            // d(delta2d) = mul backward: dy_slice * scale
+            ds.assign(N * cols, 0.f);
+            for (int64_t t = 0; t < N; ++t)
+                for (int64_t c = 0; c < cols; ++c) ds[t * cols + c] = dy[t * out + col0 + c] * scale[i];
+            // g = ds . B_eff^T  [N, r]
+            tmp.assign(cols * r, 0.f);
+            transpose2d(Be.data(), tmp.data(), r, cols);
+            gs[i].assign(N * r, 0.f);
+            mm_nn(ds.data(), tmp.data(), gs[i].data(), N, r, cols);
+            // grad_B_eff = xa^T . ds  [r, cols]
+            tmp.assign(r * N, 0.f);
+            transpose2d(xa.data(), tmp.data(), N, r);
+            tmp2.assign(r * cols, 0.f);
+            mm_nn(tmp.data(), ds.data(), tmp2.data(), r, cols, N);
+            float* dB = dB_all + (Bp - B_all);
+            if (m[4]) transpose2d(tmp2.data(), dB, r, cols);
+            else std::copy(tmp2.begin(), tmp2.end(), dB);
+            // grad_A_eff = x^T . g  [in, r]
+            tmp.assign(in * N, 0.f);
+            transpose2d(x, tmp.data(), N, in);
+            tmp2.assign(in * r, 0.f);
+            mm_nn(tmp.data(), gs[i].data(), tmp2.data(), in, r, N);
+            float* dA = dA_all + (Ap - A_all);
+            if (m[3]) transpose2d(tmp2.data(), dA, in, r);
+            else std::copy(tmp2.begin(), tmp2.end(), dA);
+            Aes[i] = Ae;
+        }
+        Ap += in * r;
+        Bp += r * cols;
+    }
+    if (!dy || !dx) return;
+    // dx = dy . W_eff^T (MatmulBackward: matmul_rhs_T, core/backward_functions.cpp:98-101), then each
+    // slice's g . A_eff^T added in slice order.
+    if (w_lowp) {
+        mm_nt_blocked64(dy, We.data(), dx, N, in, out);
+    } else {
+        tmp.assign(out * in, 0.f);
+        transpose2d(We.data(), tmp.data(), in, out);
+        mm_nn(dy, tmp.data(), dx, N, in, out);
+    }
+    for (int i = 0; i < n; ++i) {
+        if (gs[i].empty()) continue;
+        const int64_t r = meta[5 * i];
+        tmp.assign(r * in, 0.f);
+        transpose2d(Aes[i].data(), tmp.data(), in, r);
+        tmp2.assign(N * in, 0.f);
+        mm_nn(gs[i].data(), tmp.data(), tmp2.data(), N, in, r);
+        for (int64_t t = 0; t < N * in; ++t) dx[t] = dx[t] + tmp2[t];
+    }
+}
+
+void orc_lora_merge(float* W, int w_bf16, int64_t in, int64_t out, int n, const int64_t* meta, const float* scale,
+                    const float* A_all, const float* B_all, float sign) {
+    const float* Ap = A_all;
+    const float* Bp = B_all;
+    for (int s = 0; s < n; ++s) {
+        const int64_t* m = meta + 5 * s;
+        const int64_t r = m[0], col0 = m[1], cols = m[2];
+        for (int64_t i = 0; i < in; ++i)
+            for (int64_t o = 0; o < cols; ++o) {
+                double delta = 0.0;
+                for (int64_t k = 0; k < r; ++k) {
+                    const float a = m[3] ? Ap[k * in + i] : Ap[i * r + k];
+                    const float b = m[4] ? Bp[o * r + k] : Bp[k * cols + o];
+                    delta += static_cast<double>(a) * static_cast<double>(b);
+                }
+                float& w = W[i * out + col0 + o];
+                const float updated = w + sign * scale[s] * static_cast<float>(delta);
+                w = w_bf16 ? orc_bf16_bits_to_f32(orc_f32_to_bf16_bits(updated)) : updated;
+            }
+        Ap += in * r;
+        Bp += r * cols;
+    }
+}
+
 }  // extern "C"

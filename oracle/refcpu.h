@@ -124,6 +124,30 @@ int orc_selected_ce(const float* hidden, const float* weight, const int32_t* lab
                     int64_t H, int64_t V, int ignore_index, int reduction, float grad_out, float* loss,
                     float* grad_hidden, float* grad_weight);
 
+/* ---- LoRA linear (nn/lora_linear.cpp) ----
+ * n slices; meta holds 5 int64 per slice: rank, col0, cols, a_transposed,
+ * b_transposed; A_all / B_all hold the slices' A ([in, rank] or [rank, in])
+ * and B ([rank, cols] or [cols, rank]) back to back.  W holds the weight's
+ * values ([in, out], or [out, in] with w_transposed; bf16 weights as their
+ * exact fp32 values).
+ * Forward (:332-444): y = matmul(x, W) (+ bias) and per slice
+ * y[:, col0 ..] += mul(matmul(matmul(x, A), B), scale), each matmul with
+ * the arithmetic of matmul_fallback_nn.
+ * Backward (dy != NULL), the Engine's graph: g = matmul(mul(dy_slice,
+ * scale), B^T), grad_B = xA^T . (scale dy_slice), grad_A = x^T . g,
+ * dx = dy . W^T + sum g . A^T over the slices that have a gradient (full
+ * slices, or all with all_grads); has_grad[i] says which.  dx may be NULL.
+ * w_lowp: W is bf16 in the reference, whose dy . W^T then sums in 64-wide
+ * blocks of k (matmul_fallback_nt_mixed_b). */
+void orc_lora(const float* x, const float* W, const float* bias, int64_t N, int64_t in, int64_t out, int w_transposed,
+              int w_lowp, int n, const int64_t* meta, const float* scale, const float* A_all, const float* B_all,
+              int all_grads, const float* dy, float* y, float* dx, float* dA_all, float* dB_all, int32_t* has_grad);
+/* apply_lora_delta_to_base (:108-138) of every slice in order, W [in, out]:
+ * W[i, col0 + o] = W + (sign * scale) * float(sum_r double(A) * double(B)),
+ * rounded to bf16 (core/dtype.h:114-121) after each slice when w_bf16. */
+void orc_lora_merge(float* W, int w_bf16, int64_t in, int64_t out, int n, const int64_t* meta, const float* scale,
+                    const float* A_all, const float* B_all, float sign);
+
 #ifdef __cplusplus
 }
 #endif

@@ -211,12 +211,91 @@ def make_lm_loss():
     print(f"lm_loss: {len(cases)} cases, refcpu bitwise = {ok} -> {path}")
 
 
+def lora_cases():
+    """The LoRA fixture's cases: (name, x [N, in], W values, bias, slices,
+    w_transposed, w_bf16, dy).  "unit" is the hand-written case of
+    nn/test_lora_linear.cpp:51-92; "merge_bf16" and "clear" are the weights of
+    its other two tests (:94-141), whose checks are about merging."""
+    f32 = lambda a, *sh: np.array(a, np.float32).reshape(sh)
+    cases = [
+        ("unit", f32([1.0, -2.0, 0.5, -1.5, 0.25, 2.0], 2, 3),
+         f32([0.10, -0.20, 0.30, 0.40, -0.50, 0.60, -0.70, 0.80, 0.90, -1.00, 1.10, -1.20], 3, 4), None,
+         [dict(A=f32([0.10, -0.20, 0.30, 0.40, -0.50, 0.60], 3, 2), B=f32([0.70, -0.80, 0.90, 1.00], 2, 2),
+               scale=0.5, col0=1)], False, False),
+        ("merge_bf16", f32([0.5, -1.0], 1, 2), O.round_bf16(f32([0.10, -0.20, 0.30, 0.40, -0.50, 0.60], 2, 3)),
+         None, [dict(A=f32([0.25, -0.50, 0.75, 0.125], 2, 2), B=f32([0.40, -0.30, 0.20, 0.10], 2, 2), scale=1.0,
+                     col0=1)], False, True),
+        ("clear", f32([1.0, 2.0], 1, 2), O.round_bf16(f32([0.1, 0.2, 0.3, 0.4], 2, 2)), None,
+         [dict(A=f32([0.5, -0.25], 2, 1), B=f32([0.75, -0.5], 1, 2), scale=1.0)], False, True),
+    ]
+    for i, (N, I, Od, wt, wb, bias, specs) in enumerate([
+            (24, 40, 36, False, False, True, [(4, 0.5, 0, 36, False, False), (2, 2.0, 8, 12, True, True)]),
+            (17, 33, 48, True, True, False, [(8, 2.0, 0, 48, True, False)]),
+            (40, 64, 96, False, True, True, [(8, 0.25, 0, 32, False, False), (8, 0.25, 32, 32, False, False),
+                                             (8, 0.25, 64, 32, False, True)])]):
+        seed = 7000 + 10 * i
+        x = O.normal(N * I, seed, 0).reshape(N, I)
+        W = (0.2 * O.normal(I * Od, seed, 1)).reshape((Od, I) if wt else (I, Od))
+        if wb:
+            W = O.round_bf16(W)
+        b = O.normal(Od, seed, 2) if bias else None
+        sl = []
+        for j, (r, sc, c0, cols, at, bt) in enumerate(specs):
+            A = (0.3 * O.normal(I * r, seed, 10 + j)).reshape((r, I) if at else (I, r))
+            Bm = (0.3 * O.normal(r * cols, seed, 20 + j)).reshape((cols, r) if bt else (r, cols))
+            sl.append(dict(A=A, B=Bm, scale=sc, col0=c0, a_transposed=at, b_transposed=bt))
+        cases.append((f"rand{i}", x, W, b, sl, wt, wb))
+    out = []
+    for name, x, W, b, sl, wt, wb in cases:
+        out_dim = W.shape[0] if wt else W.shape[1]
+        dy = O.normal(x.shape[0] * out_dim, 7500 + len(out), 3).reshape(x.shape[0], out_dim)
+        out.append((name, x, W, b, sl, wt, wb, dy))
+    return out
+
+
+def make_lora():
+    """tests/golden/lora.npz: the reference's LoRALinear forward, Engine
+    backward (dx, grad_A, grad_B) and merge_to_base, and whether the oracle
+    matched each bit for bit."""
+    out = {}
+    ok = True
+    cases = lora_cases()
+    for name, x, W, b, sl, wt, wb, dy in cases:
+        r = O.ref_lora(x, W, b, sl, w_transposed=wt, dy=dy, w_bf16=wb)
+        m = O.lora(x, W, b, sl, w_transposed=wt, dy=dy, w_bf16=wb)
+        ok = ok and bitwise(m["y"], r["y"]) and bitwise(m["dx"], r["dx"])
+        out[f"{name}_x"], out[f"{name}_W"], out[f"{name}_dy"] = x, W, dy
+        out[f"{name}_flags"] = np.array([int(wt), int(wb), len(sl), int(b is not None)], np.int64)
+        if b is not None:
+            out[f"{name}_bias"] = b
+        out[f"{name}_y"], out[f"{name}_dx"] = r["y"], r["dx"]
+        for j, s in enumerate(sl):
+            out[f"{name}_s{j}_A"], out[f"{name}_s{j}_B"] = s["A"], s["B"]
+            out[f"{name}_s{j}_meta"] = np.array([s.get("col0", 0), int(s.get("a_transposed", False)),
+                                                 int(s.get("b_transposed", False))], np.int64)
+            out[f"{name}_s{j}_scale"] = np.float32(s["scale"])
+            has = r["grad_A"][j] is not None
+            ok = ok and has == (m["grad_A"][j] is not None)
+            if has:
+                out[f"{name}_s{j}_grad_A"], out[f"{name}_s{j}_grad_B"] = r["grad_A"][j], r["grad_B"][j]
+                ok = ok and bitwise(m["grad_A"][j], r["grad_A"][j]) and bitwise(m["grad_B"][j], r["grad_B"][j])
+        if not wt:
+            rm = O.ref_lora_merge(W, sl, w_bf16=wb)
+            ok = ok and bitwise(O.lora_merge(W, sl, w_bf16=wb), rm)
+            out[f"{name}_merged"] = rm
+    out["names"] = np.array([c[0] for c in cases])
+    out["refcpu_bitwise"] = np.array(ok)
+    path = os.path.join(HERE, "lora.npz")
+    np.savez_compressed(path, **out)
+    print(f"lora: {len(cases)} cases, refcpu bitwise = {ok} -> {path}")
+
+
 def main(argv):
     if not O.ref_available():
         O.build()
     if not O.ref_available():
         raise SystemExit("oracle/_ref/libmftref.so could not be built (needs /root/reference)")
-    todo = argv or ["tiny", "prologue", "lm_loss", "c1", "c2", "c4", "c5", "c5f32", "c3"]
+    todo = argv or ["tiny", "prologue", "lm_loss", "lora", "c1", "c2", "c4", "c5", "c5f32", "c3"]
     for t in todo:
         if t == "tiny":
             make_tiny()
@@ -224,6 +303,8 @@ def main(argv):
             make_prologue()
         elif t == "lm_loss":
             make_lm_loss()
+        elif t == "lora":
+            make_lora()
         else:
             make_config(t)
 

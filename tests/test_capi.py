@@ -11,7 +11,7 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "mft", "attention.h")
-HEADERS = [HEADER, os.path.join(ROOT, "include", "mft", "prologue.h"), os.path.join(ROOT, "include", "mft", "lm_loss.h")]
+HEADERS = [HEADER] + [os.path.join(ROOT, "include", "mft", h) for h in ("prologue.h", "lm_loss.h", "lora.h")]
 
 
 @pytest.fixture(scope="module")
@@ -55,7 +55,7 @@ def test_header_compiles_as_c(tmp_path):
     """The header is plain C (extern "C", C99 types, no torch types)."""
     src = tmp_path / "t.c"
     src.write_text('#include "mft/attention.h"\n#include "mft/prologue.h"\n#include "mft/lm_loss.h"\n'
-                   'int main(void){return mft_version()==3?0:1;}\n')
+                   'int main(void){return mft_version()==4?0:1;}\n')
     res = subprocess.run(["gcc", "-std=c99", "-fsyntax-only", "-D__HIP_PLATFORM_AMD__",
                           "-I", os.path.join(ROOT, "include"), "-I", "/opt/rocm/include", str(src)],
                          capture_output=True, text=True)
@@ -63,7 +63,7 @@ def test_header_compiles_as_c(tmp_path):
 
 
 def test_version(capi):
-    assert capi.lib().mft_version() == 3
+    assert capi.lib().mft_version() == 4
 
 
 def _err(capi, fn):
@@ -220,3 +220,26 @@ def test_lm_loss_validation(capi):
     f, b = capi.lm_ce_workspace_size(capi.lm_loss_desc(1, 4096, 262144, 1152, capi.MFT_BF16))
     assert f == b and 4096 * 16384 * 6 < f < 4096 * 16384 * 6 + (80 << 20)
 
+
+
+def test_lora_validation(capi):
+    A = dict(A=16, B=16, scale=0.5, rank=4, cols=32)
+    for kw, slices, needle in ((dict(N=0), [A], "positive sizes"), (dict(w_dtype=1), [A], "w_dtype"),
+                               ({}, [dict(A, col0=8)], "exceeds base weight width"),
+                               ({}, [dict(A, A=None)], "must not be null"), ({}, [dict(A, rank=0)], "rank")):
+        args = dict(N=8, in_dim=16, out_dim=32, w_dtype=capi.MFT_F32, slices=slices)
+        args.update(kw)
+        with pytest.raises(capi.MftError) as e:
+            capi.lora_workspace_size(capi.lora_desc(**args))
+        assert needle in str(e.value), (kw, str(e.value))
+    d = capi.lora_desc(8, 16, 32, capi.MFT_BF16, slices=[A])
+    with pytest.raises(capi.MftError) as e:
+        capi.lora_fwd(d, None, 16, None, 16, None, 16, None)
+    assert "non-NULL" in str(e.value)
+    with pytest.raises(capi.MftError) as e:
+        capi.lora_bwd(d, 16, 16, 16, None, None, 16, None)
+    assert "non-NULL" in str(e.value)
+    # workspace: bf16 staging of x (forward) / dy (backward), x . A or g [N, R] fp32, the GEMM workspace
+    f, b = capi.lora_workspace_size(capi.lora_desc(4096, 1152, 1024, capi.MFT_BF16, slices=[dict(A, rank=16)]))
+    assert f == 4096 * 1152 * 2 + 4096 * 16 * 4 + (32 << 20)
+    assert b == 4096 * 1024 * 2 + 4096 * 16 * 4 + (32 << 20)
