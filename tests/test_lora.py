@@ -85,11 +85,13 @@ CASES = [
     (512, 1152, 1024, False, True, False, [(16, 2.0, 0, 1024, False, False)], False),
     (300, 256, 768, False, True, True, [(8, 2.0, 0, 256, False, False), (8, 2.0, 256, 256, True, False),
                                         (8, 2.0, 512, 256, False, True)], True),
-    (64, 96, 96, True, True, True, [(4, 0.25, 0, 96, False, False)], False),
+    (64, 96, 112, True, True, True, [(4, 0.25, 0, 112, False, False)], False),
     (33, 17, 29, False, False, True, [(3, 1.0, 0, 29, True, False), (2, 3.0, 7, 9, False, True)], False),
 ]
 
 
+# A square W is always taken as [in, out], as the reference's matmul takes it
+# (it transposes W only when the inner dimensions disagree, core/ops.cpp:649-654).
 @pytest.mark.parametrize("case", CASES, ids=lambda c: "N{}i{}o{}-wt{:d}-bf{:d}-s{}-g{:d}".format(
     c[0], c[1], c[2], c[3], c[4], len(c[6]), c[7]))
 def test_matches_oracle(orc, dev, case):
