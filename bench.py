@@ -13,7 +13,9 @@ batches (c4pad); their flops count the visible (query, key) pairs only - and
 for the [B,S,H,D] operand layout (c5bshd).  `prologue` times the fused q/k
 norm + RoPE pass at the config's q and k shapes against the HBM roofline,
 and `lm_loss` the LM cross-entropy at the Gemma-3-1B head over the config's
-positions (streaming: MFMA roofline; dense logits: HBM roofline).
+positions (streaming: MFMA roofline; dense logits: HBM roofline); `lora`
+times the LoRA linear layers of Gemma-3-1B's q_proj and gate_proj (bf16 MFMA
+roofline of the products with W).
 The roofline object covers the dominant kernel,
 timed live with HIP events on the stream the kernels run on.  The
 cpu_baseline object times the reference CPU operators (oracle/_ref, compiled
@@ -292,6 +294,65 @@ def lm_loss_leg(cfg_id, steps, warmup):
     return out
 
 
+def lora_leg(cfg_id, steps, warmup):
+    """LoRA linear layers of Gemma-3-1B over the config's B*S positions, as
+    the reference's injector builds them (graph/gemma_lora_injector.cpp:80-150):
+    W bf16 [out, in] (frozen), x fp32, A [r, in], B [out, r] fp32, r = 8,
+    scale = 2.  Forward y = x W^T + 2 (x A^T) B^T; backward dx, grad_A,
+    grad_B.  The products with W run on the bf16 MFMA path: 2*N*in*out flop
+    each way (MFMA roofline); the rank-8 products are fp32 and counted too."""
+    import torch
+    from mobilefinetuner_amd import capi
+
+    c = CONFIGS[cfg_id]
+    dev = torch.device("cuda:0")
+    N, r = c["B"] * c["S"], 8
+    st = torch.cuda.current_stream().cuda_stream
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+
+    def timed(fn, n):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    out = {"workload": f"Gemma-3-1B LoRA projections (r {r}, W bf16 [out, in], x fp32) over the {cfg_id} batch "
+                       f"({N} positions)"}
+    for name, I, O in (("q_proj", 1152, 1024), ("gate_proj", 1152, 6912)):
+        x = torch.randn(N, I, device=dev, generator=g)
+        W = (0.03 * torch.randn(O, I, device=dev, generator=g)).to(torch.bfloat16)
+        A = 0.02 * torch.randn(r, I, device=dev, generator=g)
+        Bm = 0.02 * torch.randn(O, r, device=dev, generator=g)
+        dy = torch.randn(N, O, device=dev, generator=g)
+        y, u, dx = torch.empty(N, O, device=dev), torch.empty(N, r, device=dev), torch.empty_like(x)
+        gA, gB = torch.empty_like(A), torch.empty_like(Bm)
+        d = capi.lora_desc(N, I, O, capi.MFT_BF16, True,
+                           [dict(A=A.data_ptr(), B=Bm.data_ptr(), grad_A=gA.data_ptr(), grad_B=gB.data_ptr(),
+                                 scale=2.0, rank=r, col0=0, cols=O, a_transposed=True, b_transposed=True)])
+        fw, bw = capi.lora_workspace_size(d)
+        ws = torch.empty(max(fw, bw), dtype=torch.uint8, device=dev)
+        fwd = lambda: capi.lora_fwd(d, x.data_ptr(), W.data_ptr(), None, y.data_ptr(), u.data_ptr(), ws.data_ptr(),
+                                    st)
+        bwd = lambda: capi.lora_bwd(d, x.data_ptr(), W.data_ptr(), dy.data_ptr(), u.data_ptr(), dx.data_ptr(),
+                                    ws.data_ptr(), st)
+        fwd()
+        tf, tb = timed(fwd, steps), timed(bwd, steps)
+        base = 2.0 * N * I * O
+        low_f, low_b = 2.0 * N * r * (I + O), 2.0 * N * r * (2 * O + 2 * I)
+        out[name] = {"in": I, "out": O, "fwd_ms": round(tf, 4), "bwd_ms": round(tb, 4),
+                     "fwd_tflops": round((base + low_f) / (tf * 1e-3) / 1e12, 1),
+                     "bwd_tflops": round((base + low_b) / (tb * 1e-3) / 1e12, 1),
+                     "frac_mfma_peak": round(2 * base / ((tf + tb) * 1e-3) / 1e12 / PEAK_TFLOPS["bf16"], 4)}
+    return out
+
+
 COPY_BYTES = 1 << 30
 
 
@@ -358,11 +419,17 @@ def main():
     ap.add_argument("--no-variants", action="store_true", help="skip the mask and layout variants (variants key)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain copy of COPY_BYTES (for scaling rocprofv3 FETCH/WRITE_SIZE)")
+    ap.add_argument("--leg", choices=("prologue", "lm_loss", "lora"),
+                    help="run only this widened-path leg and print its JSON object (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the attention path is built and measured on a single "
               "MI355X (multi-GPU sharding is design-only); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.leg:
+        leg = {"prologue": prologue_leg, "lm_loss": lm_loss_leg, "lora": lora_leg}[args.leg]
+        print(json.dumps(leg(args.config, args.steps, args.warmup)), flush=True)
+        return
 
     c = CONFIGS[args.config]
     r = gpu_leg(args.config, args.steps, args.warmup)
@@ -428,6 +495,7 @@ def main():
     if not args.no_variants:
         out["prologue"] = prologue_leg(args.config, max(20, args.steps), 5)
         out["lm_loss"] = lm_loss_leg(args.config, 5, 2)
+        out["lora"] = lora_leg(args.config, 20, 3)
     if args.all_configs:
         per = {}
         for cid in ("c1", "c2", "c3", "c4", "c5", "c5f32"):

@@ -72,6 +72,153 @@ __global__ __launch_bounds__(256) void lora_merge_kernel(LoraMergeArgs a) {
     }
 }
 
+// ---- rank-r products (r is small, the inner dimension long) ----
+//
+// lora_rowdot: out[n, j] = alpha sum_k M[n, k] P(k, j).  A workgroup owns
+// kRowsPerWg rows; its 256 threads stride jointly over k (thread t: columns
+// VEC t + 256 VEC i) and each keeps kRowsPerWg x 8 partial sums (one 8-wide
+// block of j at a time), so each P(k, j) it loads serves kRowsPerWg rows.  The
+// 256 partials of each (row, j) are summed through LDS in a fixed order
+// (deterministic).  M is read once per 8-wide block of j: HBM-bound for r <= 8.
+constexpr int kRowsPerWg = 8, kJB = 8;
+
+template <int VEC>
+__global__ __launch_bounds__(256) void lora_rowdot_kernel(LoraRowDot a) {
+    constexpr int NV = kRowsPerWg * kJB;  // partial sums per thread
+    __shared__ float red[NV][257];
+    __shared__ float red2[4][NV];
+    const int t = threadIdx.x;
+    const int64_t n0 = (int64_t)blockIdx.x * kRowsPerWg;
+    for (int jb = 0; jb < a.r; jb += kJB) {
+        float acc[kRowsPerWg][kJB];
+#pragma unroll
+        for (int i = 0; i < kRowsPerWg; ++i)
+#pragma unroll
+            for (int j = 0; j < kJB; ++j) acc[i][j] = 0.f;
+        for (int64_t k = (int64_t)VEC * t; k < a.K; k += 256 * VEC) {
+            float p[VEC][kJB];
+#pragma unroll
+            for (int v = 0; v < VEC; ++v)
+#pragma unroll
+                for (int j = 0; j < kJB; ++j)
+                    p[v][j] = (jb + j < a.r) ? a.P[(k + v) * a.pk + (int64_t)(jb + j) * a.pj] : 0.f;
+            float mv[kRowsPerWg][VEC];
+#pragma unroll
+            for (int i = 0; i < kRowsPerWg; ++i) {
+                const int64_t n = n0 + i < a.rows ? n0 + i : a.rows - 1;
+                const float* m = a.M + n * a.ldm + k;
+                if (VEC == 4) {
+                    const float4 q = *reinterpret_cast<const float4*>(m);
+                    mv[i][0] = q.x, mv[i][1 % VEC] = q.y, mv[i][2 % VEC] = q.z, mv[i][3 % VEC] = q.w;
+                } else {
+                    mv[i][0] = m[0];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < kRowsPerWg; ++i)
+#pragma unroll
+                for (int v = 0; v < VEC; ++v)
+#pragma unroll
+                    for (int j = 0; j < kJB; ++j) acc[i][j] += mv[i][v] * p[v][j];
+        }
+#pragma unroll
+        for (int i = 0; i < kRowsPerWg; ++i)
+#pragma unroll
+            for (int j = 0; j < kJB; ++j) red[i * kJB + j][t] = acc[i][j];
+        __syncthreads();
+        {
+            // quarter q of the 256 partials of value e, then the 4 quarters
+            const int e = t % NV, q = t / NV;
+            float s = 0.f;
+            for (int l = 0; l < 64; ++l) s += red[e][64 * q + l];
+            red2[q][e] = s;
+        }
+        __syncthreads();
+        if (t < NV) {
+            const int i = t / kJB, j = t % kJB;
+            const float s = (red2[0][t] + red2[1][t]) + (red2[2][t] + red2[3][t]);
+            const int64_t n = n0 + i;
+            if (n < a.rows && jb + j < a.r) a.out[n * a.ldo + jb + j] = a.alpha * s;
+        }
+        __syncthreads();
+    }
+}
+
+// lora_coldot: per chunk c of rows and column k, partial[c][k][j] = sum over
+// the chunk's rows of M[n, k] V[n, j]; one wave per (64 VEC columns, chunk),
+// the row of V is the same for the whole wave.  The chunk height is chosen so
+// that about 2048 waves run (lora_coldot_chunk).  Then lora_coldot_reduce sums
+// the chunks in a fixed order.
+int64_t lora_coldot_chunk(int64_t rows, int64_t K) {
+    const int64_t col_waves = (K + 255) / 256;
+    int64_t chunk = 16;
+    while (chunk < 128 && col_waves * ((rows + chunk - 1) / chunk) > 2048) chunk *= 2;
+    return chunk;
+}
+
+template <int VEC>
+__global__ __launch_bounds__(64) void lora_coldot_kernel(LoraColDot a, int64_t chunk) {
+    const int64_t k = ((int64_t)blockIdx.x * 64 + threadIdx.x) * VEC;
+    const int64_t c = blockIdx.y;
+    const int64_t r0 = c * chunk, r1 = r0 + chunk < a.rows ? r0 + chunk : a.rows;
+    const bool live = k < a.K;
+    for (int jb = 0; jb < a.r; jb += kJB) {
+        float acc[VEC][kJB];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v)
+#pragma unroll
+            for (int j = 0; j < kJB; ++j) acc[v][j] = 0.f;
+#pragma unroll 8
+        for (int64_t n = r0; n < r1; ++n) {
+            float vv[kJB];
+#pragma unroll
+            for (int j = 0; j < kJB; ++j) vv[j] = jb + j < a.r ? a.V[n * a.ldv + jb + j] : 0.f;
+            float mv[VEC];
+            if (live) {
+                const float* m = a.M + n * a.ldm + k;
+                if (VEC == 4) {
+                    const float4 q = *reinterpret_cast<const float4*>(m);
+                    mv[0] = q.x, mv[1 % VEC] = q.y, mv[2 % VEC] = q.z, mv[3 % VEC] = q.w;
+                } else {
+                    mv[0] = m[0];
+                }
+            } else {
+#pragma unroll
+                for (int v = 0; v < VEC; ++v) mv[v] = 0.f;
+            }
+#pragma unroll
+            for (int v = 0; v < VEC; ++v)
+#pragma unroll
+                for (int j = 0; j < kJB; ++j) acc[v][j] += mv[v] * vv[j];
+        }
+        if (live) {
+            float* part = a.partial + (c * a.K + k) * a.r + jb;
+#pragma unroll
+            for (int v = 0; v < VEC; ++v)
+#pragma unroll
+                for (int j = 0; j < kJB; ++j)
+                    if (jb + j < a.r) part[v * a.r + j] = acc[v][j];
+        }
+    }
+}
+
+// Sixteen lanes per output value: lane l sums chunks l, l + 16, ... in order,
+// then the sixteen sums combine in a fixed butterfly (deterministic).
+__global__ __launch_bounds__(256) void lora_coldot_reduce(LoraColDot a, int64_t chunks) {
+    const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) / 16;
+    const int l = threadIdx.x % 16;
+    const int64_t total = a.K * a.r;
+    float s = 0.f;
+    if (e < total)
+        for (int64_t c = l; c < chunks; c += 16) s += a.partial[c * total + e];
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, 16);
+    if (e < total && l == 0) {
+        const int64_t k = e / a.r, j = e % a.r;
+        a.out[k * a.ok + j * a.oj] = a.alpha * s;
+    }
+}
+
 unsigned grid_for(int64_t work) {
     const int64_t g = (work + 255) / 256;
     return (unsigned)(g < 1 ? 1 : g > 8192 ? 8192 : g);
@@ -96,6 +243,38 @@ hipError_t launch_lora_round_bf16(const float* src, uint16_t* dst, int64_t n, hi
 hipError_t launch_lora_fill_bias(float* y, const float* bias, int64_t N, int64_t out, hipStream_t st) {
     if (N <= 0 || out <= 0) return hipSuccess;
     hipLaunchKernelGGL(lora_fill_bias_kernel, dim3(grid_for(N * out)), dim3(256), 0, st, y, bias, N, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_lora_rowdot(const LoraRowDot& a, hipStream_t st) {
+    if (a.rows <= 0 || a.r <= 0) return hipSuccess;
+    const dim3 grid((unsigned)((a.rows + kRowsPerWg - 1) / kRowsPerWg));
+    const bool vec = a.K % 4 == 0 && a.ldm % 4 == 0 && (uintptr_t)a.M % 16 == 0;
+    if (vec)
+        hipLaunchKernelGGL(lora_rowdot_kernel<4>, grid, dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL(lora_rowdot_kernel<1>, grid, dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+int64_t lora_coldot_partial_floats(int64_t rows, int64_t K, int r) {
+    const int64_t chunk = lora_coldot_chunk(rows, K);
+    return (rows + chunk - 1) / chunk * K * r;
+}
+
+hipError_t launch_lora_coldot(const LoraColDot& a, hipStream_t st) {
+    if (a.K <= 0 || a.r <= 0) return hipSuccess;
+    const int64_t chunk = lora_coldot_chunk(a.rows, a.K);
+    const int64_t chunks = (a.rows + chunk - 1) / chunk;
+    const bool vec = a.K % 4 == 0 && a.ldm % 4 == 0 && (uintptr_t)a.M % 16 == 0;
+    const int VEC = vec ? 4 : 1;
+    const dim3 grid((unsigned)((a.K + 64 * VEC - 1) / (64 * VEC)), (unsigned)chunks);
+    if (vec)
+        hipLaunchKernelGGL(lora_coldot_kernel<4>, grid, dim3(64), 0, st, a, chunk);
+    else
+        hipLaunchKernelGGL(lora_coldot_kernel<1>, grid, dim3(64), 0, st, a, chunk);
+    hipLaunchKernelGGL(lora_coldot_reduce, dim3((unsigned)((a.K * a.r * 16 + 255) / 256)), dim3(256), 0, st, a,
+                       chunks);
     return hipGetLastError();
 }
 

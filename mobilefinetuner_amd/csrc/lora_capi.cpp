@@ -4,16 +4,18 @@
 // sum of the slices' ranks, s_i = scale_i:
 //   forward   y  = x . W (+ bias)                 rocBLAS; bf16 W: x staged
 //                                                  to bf16 (lora_round_bf16)
-//             u_i = x . A_i                        fp32, into u[:, ro_i ..]
-//             y[:, col0_i ..] += s_i u_i . B_i     fp32, beta = 1
-//   backward  g_i = s_i dy[:, col0_i ..] . B_i^T   fp32 (workspace [N, R])
-//             grad_B_i = s_i u_i^T . dy[:, col0_i ..]
-//             grad_A_i = x^T . g_i
-//             dx = dy . W^T + sum_i g_i . A_i^T     bf16 W: dy staged to bf16
+//             u_i = x . A_i                        lora_rowdot, into u[:, ro_i ..]
+//             y[:, col0_i ..] += s_i u_i . B_i     rocBLAS fp32, beta = 1
+//   backward  g_i = s_i dy[:, col0_i ..] . B_i^T   lora_rowdot (workspace [N, R])
+//             grad_B_i = s_i u_i^T . dy[:, col0_i ..]   lora_coldot
+//             grad_A_i = x^T . g_i                      lora_coldot
+//             dx = dy . W^T + sum_i g_i . A_i^T     rocBLAS; bf16 W: dy staged to bf16
 // which is the reference's autograd graph of matmul / mul / add
 // (nn/lora_linear.cpp:384-434 with MatmulBackward,
-// core/backward_functions.cpp:94-160).  Validation messages follow the
-// reference's (nn/lora_linear.cpp:52-88, 118-128, 397-404).
+// core/backward_functions.cpp:94-160).  The rank-r products with a long inner
+// dimension (u, g, grad_A, grad_B) are this library's own HBM-bound kernels:
+// rocBLAS runs those shapes on a few workgroups.  Validation messages follow
+// the reference's (nn/lora_linear.cpp:52-88, 118-128, 397-404).
 #include "mft/lora.h"
 
 #include <cmath>
@@ -70,7 +72,7 @@ struct FwdLayout {
     size_t xb, u, blas, total;
 };
 struct BwdLayout {
-    size_t dyb, g, blas, total;
+    size_t dyb, g, part, blas, total;
 };
 
 FwdLayout fwd_layout(const mft_lora_desc* d) {
@@ -88,9 +90,36 @@ BwdLayout bwd_layout(const mft_lora_desc* d) {
     size_t o = 0;
     l.dyb = o, o += d->w_dtype == MFT_BF16 ? up((size_t)d->N * d->out_dim * 2) : 0;
     l.g = o, o += up((size_t)d->N * total_rank(d) * 4);
+    int64_t part = 0;
+    for (int i = 0; i < d->n_slices; ++i) {
+        const mft_lora_slice& s = d->slices[i];
+        // grad_B's reduction runs over cols columns, grad_A's over in (the chunk
+        // height depends on the width, so take both)
+        for (const int64_t k : {s.cols, d->in_dim}) {
+            const int64_t p = mft::lora_coldot_partial_floats(d->N, k, (int)s.rank);
+            part = p > part ? p : part;
+        }
+    }
+    l.part = o, o += up((size_t)part * 4);
     l.blas = o, o += kBlasWorkspace;
     l.total = o;
     return l;
+}
+
+// u_i = x . A_eff, or g_i = scale * dy_slice . B_eff^T: rank-r products over a
+// long inner dimension (lora_rowdot).
+mft_status rowdot(const float* M, int64_t ldm, int64_t rows, int64_t K, const float* P, int64_t pk, int64_t pj,
+                  float* out, int64_t ldo, int64_t r, float alpha, hipStream_t stream, const char* who) {
+    mft::LoraRowDot a{M, ldm, rows, K, P, pk, pj, out, ldo, (int)r, alpha};
+    return hip_status(mft::launch_lora_rowdot(a, stream), who);
+}
+
+// out(k, j) = alpha * M^T V over the N rows (lora_coldot), for grad_A / grad_B.
+mft_status coldot(const float* M, int64_t ldm, int64_t rows, int64_t K, const float* V, int64_t ldv, int64_t r,
+                  float alpha, float* partial, float* out, int64_t ok, int64_t oj, hipStream_t stream,
+                  const char* who) {
+    mft::LoraColDot a{M, ldm, rows, K, V, ldv, (int)r, alpha, partial, out, ok, oj};
+    return hip_status(mft::launch_lora_coldot(a, stream), who);
 }
 
 // op(W) as the right operand of x . W ([in, out]) or of dy . W^T ([out, in]).
@@ -149,9 +178,9 @@ mft_status mft_lora_fwd(const mft_lora_desc* desc, const float* x, const void* W
     int64_t ro = 0;
     for (int i = 0; i < desc->n_slices; ++i) {
         const mft_lora_slice& s = desc->slices[i];
-        // u_i[N, r] = x . A_i
-        if ((r = mft::blas::gemm_rm(who, h, N, s.rank, in, 1.f, x, in, false, s.A, s.a_transposed ? in : s.rank,
-                                    s.a_transposed != 0, 0.f, u + ro, R, false)) != MFT_OK)
+        // u_i[N, r] = x . A_eff, A_eff(k, j) = A[k, j] or A[j, k]
+        if ((r = rowdot(x, in, N, in, s.A, s.a_transposed ? 1 : s.rank, s.a_transposed ? in : 1, u + ro, R, s.rank,
+                        1.f, stream, "mft_lora_fwd launch")) != MFT_OK)
             return r;
         // y[:, col0 .. col0 + cols] += scale * u_i . B_i
         if ((r = mft::blas::gemm_rm(who, h, N, s.cols, s.rank, s.scale, u + ro, R, false, s.B,
@@ -175,6 +204,7 @@ mft_status mft_lora_bwd(const mft_lora_desc* desc, const float* x, const void* W
     const int64_t N = desc->N, in = desc->in_dim, out = desc->out_dim, R = total_rank(desc);
     const bool bf = desc->w_dtype == MFT_BF16;
     float* g = reinterpret_cast<float*>(ws + l.g);
+    float* part = reinterpret_cast<float*>(ws + l.part);
 
     const void* dyo = dy;
     if (dx && bf) {
@@ -192,28 +222,19 @@ mft_status mft_lora_bwd(const mft_lora_desc* desc, const float* x, const void* W
         const int64_t rk = s.rank;
         if (has_grad(desc, s)) {
             const float* dys = dy + s.col0;
-            // g_i[N, r] = scale * dy_slice . B_i^T
-            if ((r = mft::blas::gemm_rm(who, h, N, rk, s.cols, s.scale, dys, out, false, s.B,
-                                        s.b_transposed ? rk : s.cols, s.b_transposed == 0, 0.f, g + ro, R, false)) !=
-                MFT_OK)
+            // g_i[N, r] = scale * dy_slice . B_eff^T, B_eff(j, o) = B[j, o] or B[o, j]
+            if ((r = rowdot(dys, out, N, s.cols, s.B, s.b_transposed ? rk : 1, s.b_transposed ? 1 : s.cols, g + ro, R,
+                            rk, s.scale, stream, "mft_lora_bwd launch")) != MFT_OK)
                 return r;
-            if (s.grad_B) {
-                // [r, cols] = scale * u_i^T . dy_slice, or its transpose for a [cols, r] B
-                r = s.b_transposed
-                        ? mft::blas::gemm_rm(who, h, s.cols, rk, N, s.scale, dys, out, true, u + ro, R, false, 0.f,
-                                             s.grad_B, rk, false)
-                        : mft::blas::gemm_rm(who, h, rk, s.cols, N, s.scale, u + ro, R, true, dys, out, false, 0.f,
-                                             s.grad_B, s.cols, false);
-                if (r != MFT_OK) return r;
-            }
-            if (s.grad_A) {
-                // [in, r] = x^T . g_i, or its transpose for an [r, in] A
-                r = s.a_transposed ? mft::blas::gemm_rm(who, h, rk, in, N, 1.f, g + ro, R, true, x, in, false, 0.f,
-                                                        s.grad_A, in, false)
-                                   : mft::blas::gemm_rm(who, h, in, rk, N, 1.f, x, in, true, g + ro, R, false, 0.f,
-                                                        s.grad_A, rk, false);
-                if (r != MFT_OK) return r;
-            }
+            // grad_B(o, j) = scale * sum_n dy[n, col0 + o] u_i[n, j], stored [r, cols] or [cols, r]
+            if (s.grad_B && (r = coldot(dys, out, N, s.cols, u + ro, R, rk, s.scale, part, s.grad_B,
+                                        s.b_transposed ? rk : 1, s.b_transposed ? 1 : s.cols, stream,
+                                        "mft_lora_bwd launch")) != MFT_OK)
+                return r;
+            // grad_A(i, j) = sum_n x[n, i] g_i[n, j], stored [in, r] or [r, in]
+            if (s.grad_A && (r = coldot(x, in, N, in, g + ro, R, rk, 1.f, part, s.grad_A, s.a_transposed ? 1 : rk,
+                                        s.a_transposed ? in : 1, stream, "mft_lora_bwd launch")) != MFT_OK)
+                return r;
         }
         ro += rk;
     }

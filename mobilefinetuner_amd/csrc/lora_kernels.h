@@ -26,4 +26,36 @@ struct LoraMergeArgs {
 // W[i, col0 + o] = W + sign_scale * float(sum_r double(A[i, r]) * double(B[r, o])).
 hipError_t launch_lora_merge(const LoraMergeArgs& a, hipStream_t st);
 
+// Rank-r products with a long inner dimension, which library GEMMs run on a
+// handful of workgroups.  P(k, j) = P[k * pk + j * pj] describes A_eff / B_eff
+// in either stored layout.
+struct LoraRowDot {
+    const float* M;        // [rows, K] with leading dimension ldm
+    int64_t ldm, rows, K;
+    const float* P;
+    int64_t pk, pj;
+    float* out;            // [rows, r] with leading dimension ldo
+    int64_t ldo;
+    int r;
+    float alpha;
+};
+// out[n, j] = alpha * sum_k M[n, k] P(k, j)
+hipError_t launch_lora_rowdot(const LoraRowDot& a, hipStream_t st);
+
+struct LoraColDot {
+    const float* M;        // [rows, K] with leading dimension ldm
+    int64_t ldm, rows, K;
+    const float* V;        // [rows, r] with leading dimension ldv
+    int64_t ldv;
+    int r;
+    float alpha;
+    float* partial;        // workspace: lora_coldot_partial_floats(rows, K, r)
+    float* out;            // out[k * ok + j * oj]
+    int64_t ok, oj;
+};
+// out(k, j) = alpha * sum_n M[n, k] V[n, j]: per row-chunk partial sums, then
+// one fixed-order sum over the chunks (deterministic).
+hipError_t launch_lora_coldot(const LoraColDot& a, hipStream_t st);
+int64_t lora_coldot_partial_floats(int64_t rows, int64_t K, int r);
+
 }  // namespace mft
