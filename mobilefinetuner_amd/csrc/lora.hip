@@ -48,9 +48,10 @@ __global__ __launch_bounds__(256) void lora_fill_bias_kernel(float* __restrict__
 
 // One thread per (i, o) element of the slice's [in, cols] block; o runs
 // fastest so that B's row and W's row (untransposed layouts) are read in
-// consecutive addresses.
-#pragma clang fp contract(off)
+// consecutive addresses.  Every multiply and add is rounded on its own, as
+// the reference's are (fp contract off in this kernel only).
 __global__ __launch_bounds__(256) void lora_merge_kernel(LoraMergeArgs a) {
+#pragma clang fp contract(off)
     const int64_t total = a.in * a.cols;
     for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
         const int64_t i = e / a.cols, o = e % a.cols;
@@ -58,16 +59,16 @@ __global__ __launch_bounds__(256) void lora_merge_kernel(LoraMergeArgs a) {
         for (int64_t r = 0; r < a.rank; ++r) {
             const float av = a.a_transposed ? a.A[r * a.in + i] : a.A[i * a.rank + r];
             const float bv = a.b_transposed ? a.B[o * a.rank + r] : a.B[r * a.cols + o];
-            delta = __dadd_rn(delta, __dmul_rn((double)av, (double)bv));
+            delta += (double)av * (double)bv;
         }
         const int64_t c = a.col0 + o;
         const int64_t w = a.w_transposed ? c * a.in + i : i * a.out + c;
         if (a.w_bf16) {
             uint16_t* W = static_cast<uint16_t*>(a.W);
-            W[w] = bf16_bits_rne(__fadd_rn(bf16_bits_to_float(W[w]), __fmul_rn(a.sign_scale, (float)delta)));
+            W[w] = bf16_bits_rne(bf16_bits_to_float(W[w]) + a.sign_scale * (float)delta);
         } else {
             float* W = static_cast<float*>(a.W);
-            W[w] = __fadd_rn(W[w], __fmul_rn(a.sign_scale, (float)delta));
+            W[w] = W[w] + a.sign_scale * (float)delta;
         }
     }
 }
@@ -100,8 +101,12 @@ __global__ __launch_bounds__(256) void lora_rowdot_kernel(LoraRowDot a) {
 #pragma unroll
             for (int v = 0; v < VEC; ++v)
 #pragma unroll
-                for (int j = 0; j < kJB; ++j)
-                    p[v][j] = (jb + j < a.r) ? a.P[(k + v) * a.pk + (int64_t)(jb + j) * a.pj] : 0.f;
+                for (int j = 0; j < kJB; ++j) {
+                    // clamped index, so the load needs no branch; the select zeroes j >= r
+                    const int jj = jb + j < a.r ? jb + j : a.r - 1;
+                    const float pv = a.P[(k + v) * a.pk + (int64_t)jj * a.pj];
+                    p[v][j] = jb + j < a.r ? pv : 0.f;
+                }
             float mv[kRowsPerWg][VEC];
 #pragma unroll
             for (int i = 0; i < kRowsPerWg; ++i) {
@@ -172,7 +177,11 @@ __global__ __launch_bounds__(64) void lora_coldot_kernel(LoraColDot a, int64_t c
         for (int64_t n = r0; n < r1; ++n) {
             float vv[kJB];
 #pragma unroll
-            for (int j = 0; j < kJB; ++j) vv[j] = jb + j < a.r ? a.V[n * a.ldv + jb + j] : 0.f;
+            for (int j = 0; j < kJB; ++j) {
+                const int jj = jb + j < a.r ? jb + j : a.r - 1;
+                const float x = a.V[n * a.ldv + jj];
+                vv[j] = jb + j < a.r ? x : 0.f;
+            }
             float mv[VEC];
             if (live) {
                 const float* m = a.M + n * a.ldm + k;

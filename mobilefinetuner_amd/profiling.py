@@ -43,6 +43,12 @@ KERNELS = {
     "ce_grad": "ce_grad",
     "ce_finalize": "ce_finalize",
     "ce_reduce": "ce_reduce",
+    "lora_round_bf16": "lora_round_bf16",
+    "lora_fill_bias": "lora_fill_bias",
+    "lora_rowdot": "lora_rowdot",
+    "lora_coldot_reduce": "lora_coldot_reduce",
+    "lora_coldot_kernel": "lora_coldot",
+    "lora_merge": "lora_merge",
     "Cijk_": "rocblas_gemm",
 }
 COPY_TAG = "MulFunctor"  # torch.mul(x, 1.0, out=y): the calibration copy
@@ -52,7 +58,10 @@ def short_name(full: str) -> str:
     for frag, short in KERNELS.items():
         if frag in full:
             if short == "rocblas_gemm":  # keep the Tensile tile name: the GEMMs differ
-                return "rocblas_" + full.split("_UserArgs_")[-1][:24] if "_UserArgs_" in full else short
+                if "_UserArgs_" in full:
+                    return "rocblas_" + full.split("_UserArgs_")[-1][:24]
+                mt = full.find("_MT")
+                return "rocblas_f32_" + full[mt + 1:].split("_")[0] if mt >= 0 else short
             return short
     if COPY_TAG in full:
         return "copy_calibration"
