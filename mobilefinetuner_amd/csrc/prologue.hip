@@ -156,7 +156,8 @@ __global__ __launch_bounds__(256) void prologue_fwd_kernel(PrologueArgs a) {
                 y2[e] = x2[i][k];
                 if (a.rope) {
                     const float ang = (float)ra.s * a.inv_freq[p0 + e];
-                    const float c = cosf(ang), sn = sinf(ang);
+                    float c, sn;
+                    sincosf(ang, &sn, &c);
                     y1[e] = x1[i][k] * c - x2[i][k] * sn;
                     y2[e] = x1[i][k] * sn + x2[i][k] * c;
                 }
@@ -238,7 +239,8 @@ __global__ __launch_bounds__(256) void prologue_bwd_kernel(PrologueArgs a) {
                     const int p = elem<V>(lane, j) + e, k = j * V + e;
                     if (p >= half) continue;
                     const float ang = (float)ra.s * a.inv_freq[p];
-                    const float c = cosf(ang), sn = sinf(ang);
+                    float c, sn;
+                    sincosf(ang, &sn, &c);
                     const float a1 = g1[i][k], a2 = g2[i][k];
                     g1[i][k] = a1 * c + a2 * sn;
                     g2[i][k] = -a1 * sn + a2 * c;
@@ -353,50 +355,32 @@ template <int LPR> __device__ __forceinline__ double group_sum(double v) {
     return v;
 }
 
-// cos/sin of the angles of this lane's EPL pairs.  The two lanes holding a
-// pair split the work: the first-half lane evaluates slots [0, EPL/2), its
-// partner slots [EPL/2, EPL), and each takes the other half by shuffle.
-template <int EPL, int LPR>
-__device__ __forceinline__ void pair_trig(const PrologueArgs& a, int s, int q0, bool first, float* c, float* sn) {
-    float mc[EPL / 2], ms[EPL / 2];
-#pragma unroll
-    for (int k = 0; k < EPL / 2; ++k) {
-        const int e = first ? k : k + EPL / 2;
-        const float ang = (float)s * a.inv_freq[q0 + e];
-        mc[k] = cosf(ang);
-        ms[k] = sinf(ang);
-    }
-#pragma unroll
-    for (int k = 0; k < EPL / 2; ++k) {
-        const float oc = __shfl_xor(mc[k], LPR / 2, 64), os = __shfl_xor(ms[k], LPR / 2, 64);
-        c[first ? k : k + EPL / 2] = mc[k];
-        sn[first ? k : k + EPL / 2] = ms[k];
-        c[first ? k + EPL / 2 : k] = oc;
-        sn[first ? k + EPL / 2 : k] = os;
-    }
-}
-
+// Forward, 16 bytes per lane and row: a lane holds EPL / 2 elements of the
+// first half (d = q0 .. q0 + EPL/2 - 1) and their rotate-half partners
+// (d + D/2), so each RoPE pair is rotated inside one lane with one sincosf
+// per pair and no shuffle; only the norm's sum of squares crosses lanes.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void prologue_fwd_vec(PrologueArgs a) {
 #pragma clang fp contract(off)
-    constexpr int EPL = 16 / (int)sizeof(T), LPR = D / EPL, RPI = 64 / LPR, HALF = D / 2;
+    constexpr int EPL = 16 / (int)sizeof(T), H2 = EPL / 2, LPR = D / EPL, RPI = 64 / LPR, HALF = D / 2;
     static_assert(LPR >= 2 && LPR <= 64, "a row spans 2..64 lanes");
     constexpr int GROUPS = 2;  // row groups per wave, all loaded before any is computed
     const int lane = threadIdx.x & 63, gl = lane % LPR;
-    const int p = gl * EPL;  // this lane's first element
-    const bool first = p < HALF;
+    const int q0 = gl * H2;  // this lane's first element of the first half
     const int64_t wave_row0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * (RPI * GROUPS);
-    float v[GROUPS][EPL];
+    float v[GROUPS][2][H2];  // [group][half][element]
     RowAddr ra[GROUPS];
 #pragma unroll
     for (int g = 0; g < GROUPS; ++g) {
         const int64_t r = wave_row0 + g * RPI + lane / LPR;
         ra[g] = row_addr(a, r < a.rows ? r : 0);
         if (r < a.rows) {
-            Vec<T, EPL>::load((const T*)a.x + a.sx.at(ra[g].b, ra[g].h) + (int64_t)ra[g].s * a.sx.s + p, v[g]);
+            const T* x = (const T*)a.x + a.sx.at(ra[g].b, ra[g].h) + (int64_t)ra[g].s * a.sx.s + q0;
+            Vec<T, H2>::load(x, v[g][0]);
+            Vec<T, H2>::load(x + HALF, v[g][1]);
         } else {
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) v[g][e] = 0.f;
+            for (int e = 0; e < H2; ++e) v[g][0][e] = v[g][1][e] = 0.f;
         }
     }
 #pragma unroll
@@ -405,56 +389,68 @@ __global__ __launch_bounds__(256) void prologue_fwd_vec(PrologueArgs a) {
         if (a.norm != PROLOGUE_NORM_NONE) {
             double ss = 0.0;
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) ss += (double)v[g][e] * (double)v[g][e];
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                for (int e = 0; e < H2; ++e) ss += (double)v[g][hf][e] * (double)v[g][hf][e];
             ss = group_sum<LPR>(ss);
             if (a.norm == PROLOGUE_NORM_GEMMA) {
                 const float rms = (float)sqrt(ss / (double)D + (double)a.eps);
 #pragma unroll
-                for (int e = 0; e < EPL; ++e) v[g][e] = (v[g][e] / rms) * (1.0f + a.w[p + e]);
+                for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                    for (int e = 0; e < H2; ++e)
+                        v[g][hf][e] = (v[g][hf][e] / rms) * (1.0f + a.w[hf * HALF + q0 + e]);
             } else {
                 const float inv = (float)(1.0 / sqrt(ss / (double)D + (double)a.eps));
 #pragma unroll
-                for (int e = 0; e < EPL; ++e) v[g][e] = v[g][e] * inv * a.w[p + e];
+                for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                    for (int e = 0; e < H2; ++e) v[g][hf][e] = v[g][hf][e] * inv * a.w[hf * HALF + q0 + e];
             }
         }
-        float y[EPL];
+        float y[2][H2];
         if (a.rope) {
-            float c[EPL], sn[EPL];
-            pair_trig<EPL, LPR>(a, ra[g].s, p % HALF, first, c, sn);
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                const float pv = __shfl_xor(v[g][e], LPR / 2, 64);
+            for (int e = 0; e < H2; ++e) {
+                float c, sn;
+                sincosf((float)ra[g].s * a.inv_freq[q0 + e], &sn, &c);
+                const float x1 = v[g][0][e], x2 = v[g][1][e];
                 // first half: x1 * c - x2 * s; second half: x1 * s + x2 * c
-                y[e] = first ? v[g][e] * c[e] - pv * sn[e] : pv * sn[e] + v[g][e] * c[e];
+                y[0][e] = x1 * c - x2 * sn;
+                y[1][e] = x1 * sn + x2 * c;
             }
         } else {
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) y[e] = v[g][e];
+            for (int e = 0; e < H2; ++e) y[0][e] = v[g][0][e], y[1][e] = v[g][1][e];
         }
-        if (r < a.rows) Vec<T, EPL>::store((T*)a.y + a.sy.at(ra[g].b, ra[g].h) + (int64_t)ra[g].s * a.sy.s + p, y);
+        if (r < a.rows) {
+            T* yp = (T*)a.y + a.sy.at(ra[g].b, ra[g].h) + (int64_t)ra[g].s * a.sy.s + q0;
+            Vec<T, H2>::store(yp, y[0]);
+            Vec<T, H2>::store(yp + HALF, y[1]);
+        }
     }
 }
 
-// Backward with fp32 dy/dx rows as the lane grid (EPL = 4, LPR = D / 4; x is
-// read 4 elements per lane).  Rows per workgroup as prologue_bwd_blocks
-// counts them; dL/dw is summed per lane over its rows, then over the row
-// groups of the wave and the 4 waves in fixed order.
+// Backward with fp32 dy/dx rows as the lane grid (EPL = 4 per lane, LPR =
+// D / 4): a lane holds 2 elements of the first half and their rotate-half
+// partners, so R^T dy is applied inside the lane.  Rows per workgroup as
+// prologue_bwd_blocks counts them; dL/dw is summed per lane over its rows,
+// then over the row groups of the wave and the 4 waves in fixed order.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void prologue_bwd_vec(PrologueArgs a) {
 #pragma clang fp contract(off)
-    constexpr int EPL = 4, LPR = D / EPL, RPI = 64 / LPR, HALF = D / 2;
+    constexpr int EPL = 4, H2 = EPL / 2, LPR = D / EPL, RPI = 64 / LPR, HALF = D / 2;
     static_assert(LPR >= 2 && LPR <= 64, "a row spans 2..64 lanes");
     constexpr int ROWS_WG = 4 * prologue_bwd_rows_per_wave(prologue_elems_per_lane(D));
     constexpr int GROUPS = ROWS_WG / 4 / RPI;  // row groups per wave
     static_assert(GROUPS * RPI * 4 == ROWS_WG, "workgroup rows split evenly");
     __shared__ float red[3][D];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, gl = lane % LPR;
-    const int p = gl * EPL;
-    const bool first = p < HALF;
+    const int q0 = gl * H2;  // this lane's first element of the first half
     const bool norm = a.norm != PROLOGUE_NORM_NONE;
     const int64_t wave_row0 = (int64_t)blockIdx.x * ROWS_WG + w * (RPI * GROUPS);
-    // every row group's loads first
-    float gv[GROUPS][EPL], xv[GROUPS][EPL];
+    // every row group's loads first; [group][half][element]
+    float gv[GROUPS][2][H2], xv[GROUPS][2][H2];
     RowAddr ra[GROUPS];
 #pragma unroll
     for (int g = 0; g < GROUPS; ++g) {
@@ -462,80 +458,103 @@ __global__ __launch_bounds__(256) void prologue_bwd_vec(PrologueArgs a) {
         const bool live = r < a.rows;
         ra[g] = row_addr(a, live ? r : 0);
         if (live) {
-            Vec<float, EPL>::load(a.dy + a.sdy.at(ra[g].b, ra[g].h) + (int64_t)ra[g].s * a.sdy.s + p, gv[g]);
+            const float* dy = a.dy + a.sdy.at(ra[g].b, ra[g].h) + (int64_t)ra[g].s * a.sdy.s + q0;
+            Vec<float, H2>::load(dy, gv[g][0]);
+            Vec<float, H2>::load(dy + HALF, gv[g][1]);
         } else {
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) gv[g][e] = 0.f;
+            for (int e = 0; e < H2; ++e) gv[g][0][e] = gv[g][1][e] = 0.f;
         }
         if (norm && live) {
-            Vec<T, EPL>::load((const T*)a.x + a.sx.at(ra[g].b, ra[g].h) + (int64_t)ra[g].s * a.sx.s + p, xv[g]);
+            const T* x = (const T*)a.x + a.sx.at(ra[g].b, ra[g].h) + (int64_t)ra[g].s * a.sx.s + q0;
+            Vec<T, H2>::load(x, xv[g][0]);
+            Vec<T, H2>::load(x + HALF, xv[g][1]);
         } else {
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) xv[g][e] = 0.f;
+            for (int e = 0; e < H2; ++e) xv[g][0][e] = xv[g][1][e] = 0.f;
         }
     }
-    float gw[EPL];
-    double we[EPL];
+    float gw[2][H2];
+    double we[2][H2];
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-        gw[e] = 0.f;
-        const double wv = norm ? (double)a.w[p + e] : 0.0;
-        we[e] = a.norm == PROLOGUE_NORM_GEMMA ? 1.0 + wv : wv;
-    }
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int e = 0; e < H2; ++e) {
+            gw[hf][e] = 0.f;
+            const double wv = norm ? (double)a.w[hf * HALF + q0 + e] : 0.0;
+            we[hf][e] = a.norm == PROLOGUE_NORM_GEMMA ? 1.0 + wv : wv;
+        }
 #pragma unroll
     for (int g = 0; g < GROUPS; ++g) {
         const int64_t r = wave_row0 + g * RPI + lane / LPR;
         const bool live = r < a.rows;
         // gradient at the norm's output: R^T dy
         if (a.rope) {
-            float c[EPL], sn[EPL];
-            pair_trig<EPL, LPR>(a, ra[g].s, p % HALF, first, c, sn);
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                const float pg = __shfl_xor(gv[g][e], LPR / 2, 64);
+            for (int e = 0; e < H2; ++e) {
+                float c, sn;
+                sincosf((float)ra[g].s * a.inv_freq[q0 + e], &sn, &c);
+                const float g1 = gv[g][0][e], g2 = gv[g][1][e];
                 // first half: g1 c + g2 s; second half: -g1 s + g2 c
-                gv[g][e] = first ? gv[g][e] * c[e] + pg * sn[e] : -pg * sn[e] + gv[g][e] * c[e];
+                gv[g][0][e] = g1 * c + g2 * sn;
+                gv[g][1][e] = -g1 * sn + g2 * c;
             }
         }
         if (norm) {
             double ss = 0.0, dot = 0.0;
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                ss += (double)xv[g][e] * (double)xv[g][e];
-                dot += (double)gv[g][e] * we[e] * (double)xv[g][e];
-            }
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                for (int e = 0; e < H2; ++e) {
+                    ss += (double)xv[g][hf][e] * (double)xv[g][hf][e];
+                    dot += (double)gv[g][hf][e] * we[hf][e] * (double)xv[g][hf][e];
+                }
             ss = group_sum<LPR>(ss);
             dot = group_sum<LPR>(dot);
             const double inv = 1.0 / sqrt(ss / (double)D + (double)a.eps);
             const double coeff = (inv * inv * inv) / (double)D;
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                const float d = (float)((double)gv[g][e] * we[e] * inv - (double)xv[g][e] * coeff * dot);
-                if (live) gw[e] += (float)((double)gv[g][e] * (double)xv[g][e] * inv);
-                gv[g][e] = d;
-            }
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                for (int e = 0; e < H2; ++e) {
+                    const float d =
+                        (float)((double)gv[g][hf][e] * we[hf][e] * inv - (double)xv[g][hf][e] * coeff * dot);
+                    if (live) gw[hf][e] += (float)((double)gv[g][hf][e] * (double)xv[g][hf][e] * inv);
+                    gv[g][hf][e] = d;
+                }
         }
-        if (live) Vec<float, EPL>::store(a.dx + a.sdx.at(ra[g].b, ra[g].h) + (int64_t)ra[g].s * a.sdx.s + p, gv[g]);
+        if (live) {
+            float* dx = a.dx + a.sdx.at(ra[g].b, ra[g].h) + (int64_t)ra[g].s * a.sdx.s + q0;
+            Vec<float, H2>::store(dx, gv[g][0]);
+            Vec<float, H2>::store(dx + HALF, gv[g][1]);
+        }
     }
     if (!norm || !a.dw_part) return;
     // the wave's row groups, then the workgroup's waves, in fixed order
 #pragma unroll
     for (int o = LPR; o < 64; o <<= 1)
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) gw[e] += __shfl_xor(gw[e], o, 64);
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int e = 0; e < H2; ++e) gw[hf][e] += __shfl_xor(gw[hf][e], o, 64);
     if (w > 0 && lane < LPR) {
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) red[w - 1][p + e] = gw[e];
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int e = 0; e < H2; ++e) red[w - 1][hf * HALF + q0 + e] = gw[hf][e];
     }
     __syncthreads();
     if (w == 0 && lane < LPR) {
         float* part = a.dw_part + (int64_t)blockIdx.x * D;
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            float t = gw[e];
-            for (int q = 0; q < 3; ++q) t += red[q][p + e];
-            part[p + e] = t;
-        }
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int e = 0; e < H2; ++e) {
+                const int idx = hf * HALF + q0 + e;
+                float t = gw[hf][e];
+                for (int q = 0; q < 3; ++q) t += red[q][idx];
+                part[idx] = t;
+            }
     }
 }
 
