@@ -36,6 +36,8 @@ KERNELS = {
     "attn_bwd_stats": "attn_bwd_stats",
     "attn_bwd_fast_reduce": "attn_bwd_reduce",
     "attn_bwd_reduce": "attn_bwd_reduce",
+    "prologue_fwd_vec": "prologue_fwd_vec",
+    "prologue_bwd_vec": "prologue_bwd_vec",
     "prologue_fwd_kernel": "prologue_fwd",
     "prologue_bwd_kernel": "prologue_bwd",
     "prologue_dw_reduce": "prologue_dw_reduce",
