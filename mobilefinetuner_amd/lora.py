@@ -218,14 +218,17 @@ class LoRALinear:
     def _merge(self, sign):
         W = self._W
         in_dim = W.shape[0]
-        slices = []
+        slices, keep = [], []  # keep: the contiguous operands stay alive until the launch is enqueued
         for s in self._slices:
             rank, cols, at, bt = _effective_shape(s.A, s.B, in_dim)
             if s.cols != cols:
                 raise RuntimeError("LoRALinear: LoRA slice cols do not match B output dimension")
             if s.col0 < 0 or s.col0 + cols > W.shape[1]:
                 raise RuntimeError("LoRALinear: LoRA slice range exceeds base weight width")
-            slices.append(dict(A=s.A.detach().contiguous().data_ptr(), B=s.B.detach().contiguous().data_ptr(),
-                               scale=s.scale, rank=rank, col0=s.col0, cols=cols, a_transposed=at, b_transposed=bt))
+            A, B = s.A.detach().contiguous(), s.B.detach().contiguous()
+            keep += [A, B]
+            slices.append(dict(A=A.data_ptr(), B=B.data_ptr(), scale=s.scale, rank=rank, col0=s.col0, cols=cols,
+                               a_transposed=at, b_transposed=bt))
         d = capi.lora_desc(1, in_dim, W.shape[1], _w_dtype(W), False, slices)
         capi.lora_merge(d, W.data_ptr(), sign, _stream(W.device))
+        del keep  # the caching allocator reuses this memory only after the merge on this stream
