@@ -228,6 +228,14 @@ __global__ __launch_bounds__(256) void lora_coldot_reduce(LoraColDot a, int64_t 
     }
 }
 
+__global__ __launch_bounds__(256) void lora_pack_kmajor_kernel(const float* __restrict__ P, int64_t pk, int64_t pj,
+                                                               int64_t K, int r, float* __restrict__ dst) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= K * r) return;
+    const int64_t j = e / K, k = e % K;
+    dst[e] = P[k * pk + j * pj];
+}
+
 unsigned grid_for(int64_t work) {
     const int64_t g = (work + 255) / 256;
     return (unsigned)(g < 1 ? 1 : g > 8192 ? 8192 : g);
@@ -263,6 +271,14 @@ hipError_t launch_lora_rowdot(const LoraRowDot& a, hipStream_t st) {
         hipLaunchKernelGGL(lora_rowdot_kernel<4>, grid, dim3(256), 0, st, a);
     else
         hipLaunchKernelGGL(lora_rowdot_kernel<1>, grid, dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_lora_pack_kmajor(const float* P, int64_t pk, int64_t pj, int64_t K, int r, float* dst,
+                                   hipStream_t st) {
+    if (K <= 0 || r <= 0) return hipSuccess;
+    hipLaunchKernelGGL(lora_pack_kmajor_kernel, dim3((unsigned)((K * r + 255) / 256)), dim3(256), 0, st, P, pk, pj,
+                       K, r, dst);
     return hipGetLastError();
 }
 

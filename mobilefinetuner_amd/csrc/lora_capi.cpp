@@ -18,6 +18,7 @@
 // the reference's (nn/lora_linear.cpp:52-88, 118-128, 397-404).
 #include "mft/lora.h"
 
+#include <algorithm>
 #include <cmath>
 #include <string>
 
@@ -69,17 +70,29 @@ bool has_grad(const mft_lora_desc* d, const mft_lora_slice& s) {
 }
 
 struct FwdLayout {
-    size_t xb, u, blas, total;
+    size_t xb, u, pt, blas, total;
 };
 struct BwdLayout {
-    size_t dyb, g, part, blas, total;
+    size_t dyb, g, part, pt, blas, total;
 };
+
+// k-contiguous copy of a rank-r operand (see rowdot): the largest slice's.
+size_t pack_bytes(const mft_lora_desc* d) {
+    size_t m = 0;
+    for (int i = 0; i < d->n_slices; ++i) {
+        const mft_lora_slice& s = d->slices[i];
+        const size_t k = (size_t)(s.cols > d->in_dim ? s.cols : d->in_dim);
+        m = std::max(m, k * (size_t)s.rank * 4);
+    }
+    return up(m);
+}
 
 FwdLayout fwd_layout(const mft_lora_desc* d) {
     FwdLayout l{};
     size_t o = 0;
     l.xb = o, o += d->w_dtype == MFT_BF16 ? up((size_t)d->N * d->in_dim * 2) : 0;
     l.u = o, o += up((size_t)d->N * total_rank(d) * 4);
+    l.pt = o, o += pack_bytes(d);
     l.blas = o, o += kBlasWorkspace;
     l.total = o;
     return l;
@@ -101,6 +114,7 @@ BwdLayout bwd_layout(const mft_lora_desc* d) {
         }
     }
     l.part = o, o += up((size_t)part * 4);
+    l.pt = o, o += pack_bytes(d);
     l.blas = o, o += kBlasWorkspace;
     l.total = o;
     return l;
@@ -108,8 +122,16 @@ BwdLayout bwd_layout(const mft_lora_desc* d) {
 
 // u_i = x . A_eff, or g_i = scale * dy_slice . B_eff^T: rank-r products over a
 // long inner dimension (lora_rowdot).
+// A P that is not k-contiguous (pk != 1) is first copied k-major into
+// `pack` (K x r floats of workspace): rowdot's lanes stride over k, and a
+// j-contiguous P would put every lane of a load on its own cache line.
 mft_status rowdot(const float* M, int64_t ldm, int64_t rows, int64_t K, const float* P, int64_t pk, int64_t pj,
-                  float* out, int64_t ldo, int64_t r, float alpha, hipStream_t stream, const char* who) {
+                  float* out, int64_t ldo, int64_t r, float alpha, float* pack, hipStream_t stream, const char* who) {
+    if (pk != 1) {
+        const hipError_t e = mft::launch_lora_pack_kmajor(P, pk, pj, K, (int)r, pack, stream);
+        if (e != hipSuccess) return hip_status(e, who);
+        P = pack, pk = 1, pj = K;
+    }
     mft::LoraRowDot a{M, ldm, rows, K, P, pk, pj, out, ldo, (int)r, alpha};
     return hip_status(mft::launch_lora_rowdot(a, stream), who);
 }
@@ -180,7 +202,7 @@ mft_status mft_lora_fwd(const mft_lora_desc* desc, const float* x, const void* W
         const mft_lora_slice& s = desc->slices[i];
         // u_i[N, r] = x . A_eff, A_eff(k, j) = A[k, j] or A[j, k]
         if ((r = rowdot(x, in, N, in, s.A, s.a_transposed ? 1 : s.rank, s.a_transposed ? in : 1, u + ro, R, s.rank,
-                        1.f, stream, "mft_lora_fwd launch")) != MFT_OK)
+                        1.f, reinterpret_cast<float*>(ws + l.pt), stream, "mft_lora_fwd launch")) != MFT_OK)
             return r;
         // y[:, col0 .. col0 + cols] += scale * u_i . B_i
         if ((r = mft::blas::gemm_rm(who, h, N, s.cols, s.rank, s.scale, u + ro, R, false, s.B,
@@ -224,7 +246,7 @@ mft_status mft_lora_bwd(const mft_lora_desc* desc, const float* x, const void* W
             const float* dys = dy + s.col0;
             // g_i[N, r] = scale * dy_slice . B_eff^T, B_eff(j, o) = B[j, o] or B[o, j]
             if ((r = rowdot(dys, out, N, s.cols, s.B, s.b_transposed ? rk : 1, s.b_transposed ? 1 : s.cols, g + ro, R,
-                            rk, s.scale, stream, "mft_lora_bwd launch")) != MFT_OK)
+                            rk, s.scale, reinterpret_cast<float*>(ws + l.pt), stream, "mft_lora_bwd launch")) != MFT_OK)
                 return r;
             // grad_B(o, j) = scale * sum_n dy[n, col0 + o] u_i[n, j], stored [r, cols] or [cols, r]
             if (s.grad_B && (r = coldot(dys, out, N, s.cols, u + ro, R, rk, s.scale, part, s.grad_B,

@@ -41,6 +41,10 @@ struct LoraRowDot {
 };
 // out[n, j] = alpha * sum_k M[n, k] P(k, j)
 hipError_t launch_lora_rowdot(const LoraRowDot& a, hipStream_t st);
+// dst[j * K + k] = P(k, j) for k < K, j < r: the k-contiguous copy rowdot
+// reads with coalesced loads when P is not k-contiguous already.
+hipError_t launch_lora_pack_kmajor(const float* P, int64_t pk, int64_t pj, int64_t K, int r, float* dst,
+                                   hipStream_t st);
 
 struct LoraColDot {
     const float* M;        // [rows, K] with leading dimension ldm

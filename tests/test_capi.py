@@ -241,7 +241,9 @@ def test_lora_validation(capi):
     assert "non-NULL" in str(e.value)
     # workspace: bf16 staging of x (forward) / dy (backward), x . A or g [N, R] fp32, the GEMM workspace
     f, b = capi.lora_workspace_size(capi.lora_desc(4096, 1152, 1024, capi.MFT_BF16, slices=[dict(A, rank=16)]))
-    assert f == 4096 * 1152 * 2 + 4096 * 16 * 4 + (32 << 20)
+    # plus a k-major copy of the largest rank-r operand ([max(in, cols), r] fp32)
+    pack = 1152 * 16 * 4
+    assert f == 4096 * 1152 * 2 + 4096 * 16 * 4 + pack + (32 << 20)
     # backward adds the per-row-chunk partials of grad_A / grad_B ([chunks, max(in, cols), r] fp32;
     # 16-row chunks here: 5 x 256 column waves)
-    assert b == 4096 * 1024 * 2 + 4096 * 16 * 4 + 4096 // 16 * 1152 * 16 * 4 + (32 << 20)
+    assert b == 4096 * 1024 * 2 + 4096 * 16 * 4 + 4096 // 16 * 1152 * 16 * 4 + pack + (32 << 20)
