@@ -7,7 +7,8 @@
 A step is one forward plus one backward of the attention over the config's
 synthetic batch (inputs resident in HBM).  Prints ONE JSON line.  `value` is
 the algorithmic causal throughput  7*B*H*D*S*(S+1) / step time  in TFLOP/s
-`variants` adds the same measurement for the
+(forward 2 and backward 5 products over the causal triangle with its
+diagonal, per query head).  `variants` adds the same measurement for the
 masks the model graphs use - Gemma's sliding window (c5w512) and right-padded
 batches (c4pad); their flops count the visible (query, key) pairs only - and
 for the [B,S,H,D] operand layout (c5bshd).  `prologue` times the fused q/k
@@ -87,8 +88,9 @@ def saved_bytes(c):
     B, Hq, Hkv, S, D = c["B"], c["Hq"], c["Hkv"], c["S"], c["D"]
     new = esz * (2 * B * Hq * S * D + 2 * B * Hkv * S * D) + 4 * B * Hq * S
     # Reference: four S x S fp32 tensors per query head stay alive until
-    # backward, plus the transposed and (GQA) repeated K/V copies
-    # (measured formula).
+    # backward, plus the transposed and (GQA) repeated K/V copies (the
+    # MemoryManager bytes the reference's composite graph holds between
+    # forward and backward, measured with oracle/_ref's mftref_composite).
     ref = 4 * B * Hq * S * S * 4 + 2 * B * Hq * S * D * 4 + (2 * B * Hq * S * D * 4 if Hq != Hkv else 0)
     return new, ref
 
