@@ -8,7 +8,11 @@ container).  On the GPU:
     compiled unchanged against the drop-in, passes;
   * test_fused_attention_dropin.cpp compares the fused operator (GQA, bf16,
     no-grad path, error convention) with the reference composite through the
-    unchanged ops / autograd API.
+    unchanged ops / autograd API;
+  * with nn/lora_linear.cpp replaced by lora_linear_hip.cpp, the reference's
+    OWN nn/test_lora_linear.cpp (merge, unmerge, clear) passes unchanged, and
+    test_lora_dropin.cpp compares forward and Engine backward with the graph
+    of the reference's operators.
 """
 import os
 import subprocess
@@ -38,4 +42,14 @@ def test_reference_unit_test_passes_on_dropin(dev):
 
 def test_fused_attention_dropin_parity(dev):
     res = _run("test_fused_attention_dropin")
+    assert res.returncode == 0 and "[PASS]" in res.stdout
+
+
+def test_reference_lora_unit_test_passes_on_dropin(dev):
+    res = _run("test_lora_linear")
+    assert res.returncode == 0, res.stdout + res.stderr
+
+
+def test_lora_dropin_parity(dev):
+    res = _run("test_lora_dropin")
     assert res.returncode == 0 and "[PASS]" in res.stdout
