@@ -12,7 +12,12 @@ container).  On the GPU:
   * with nn/lora_linear.cpp replaced by lora_linear_hip.cpp, the reference's
     OWN nn/test_lora_linear.cpp (merge, unmerge, clear) passes unchanged, and
     test_lora_dropin.cpp compares forward and Engine backward with the graph
-    of the reference's operators.
+    of the reference's operators;
+  * with core/lm_loss.cpp replaced by lm_loss_hip.cpp, the reference's OWN
+    core/test_selected_token_lm_loss.cpp (dense vs selected vs streaming,
+    all-ignored NaN, out-of-range label) passes unchanged, and
+    test_lm_loss_dropin.cpp checks every reduction and both weight dtypes
+    against the reference formulas on a multi-chunk vocabulary.
 """
 import os
 import subprocess
@@ -52,4 +57,14 @@ def test_reference_lora_unit_test_passes_on_dropin(dev):
 
 def test_lora_dropin_parity(dev):
     res = _run("test_lora_dropin")
+    assert res.returncode == 0 and "[PASS]" in res.stdout
+
+
+def test_reference_lm_loss_unit_test_passes_on_dropin(dev):
+    res = _run("test_selected_token_lm_loss")
+    assert res.returncode == 0 and "[PASS]" in res.stdout
+
+
+def test_lm_loss_dropin_parity(dev):
+    res = _run("test_lm_loss_dropin")
     assert res.returncode == 0 and "[PASS]" in res.stdout
