@@ -28,7 +28,6 @@
 #include <cmath>
 #include <cstring>
 #include <memory>
-#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -39,64 +38,20 @@
 #include "backward_functions.h"
 #include "ops.h"
 #include "mft/lm_loss.h"
+#include "dropin_device.h"
 
 namespace ops {
 namespace {
 
-void hip_check(hipError_t e, const char* what) {
-    if (e != hipSuccess) throw std::runtime_error(std::string("lm_loss: ") + what + ": " + hipGetErrorString(e));
-}
-
-void mft_check(mft_status st) {
-    if (st != MFT_OK) throw std::runtime_error(std::string("lm_loss: ") + mft_last_error());
-}
-
-hipStream_t loss_stream() {
-    static std::once_flag once;
-    static hipStream_t s = nullptr;
-    std::call_once(once, [] { hip_check(hipStreamCreate(&s), "hipStreamCreate"); });
-    return s;
-}
-
-class DeviceBuffer {
-public:
-    explicit DeviceBuffer(size_t bytes) {
-        if (bytes) hip_check(hipMalloc(&ptr_, bytes), "hipMalloc");
-    }
-    ~DeviceBuffer() {
-        if (ptr_) (void)hipFree(ptr_);
-    }
-    DeviceBuffer(const DeviceBuffer&) = delete;
-    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
-    void* get() const { return ptr_; }
-    float* f() const { return static_cast<float*>(ptr_); }
-
-private:
-    void* ptr_ = nullptr;
-};
-using Buf = std::unique_ptr<DeviceBuffer>;
-
-Buf upload_bytes(const void* src, size_t n) {
-    auto buf = std::make_unique<DeviceBuffer>(n);
-    if (n) hip_check(hipMemcpyAsync(buf->get(), src, n, hipMemcpyHostToDevice, loss_stream()), "copy to device");
-    return buf;
-}
-
-// A floating-point host tensor as fp32 values on the device (the widening of
-// tensor_row_value, core/lm_loss.cpp:50-61, which is exact).
-Buf upload_f32(const TensorPtr& t, const char* who) {
-    const int64_t n = t->numel();
-    if (t->dtype() == kFloat32) return upload_bytes(t->data<float>(), static_cast<size_t>(n) * 4);
-    if (t->dtype() != kBFloat16 && t->dtype() != kFloat16)
-        throw std::runtime_error(std::string(who) + ": unsupported floating dtype " + DTypeUtils::to_string(t->dtype()));
-    std::vector<float> v(static_cast<size_t>(n));
-    const uint16_t* bits = t->data<uint16_t>();
-    for (int64_t i = 0; i < n; ++i)
-        v[static_cast<size_t>(i)] = t->dtype() == kBFloat16 ? bf16_bits_to_float32(bits[i]) : fp16_bits_to_float32(bits[i]);
-    auto buf = upload_bytes(v.data(), v.size() * 4);
-    hip_check(hipStreamSynchronize(loss_stream()), "synchronize");  // v is a local
-    return buf;
-}
+constexpr const char* kWho = "lm_loss";
+void hip_check(hipError_t e, const char* what) { dropin::hip_check(kWho, e, what); }
+void mft_check(mft_status st) { dropin::mft_check(kWho, st); }
+hipStream_t loss_stream() { return dropin::stream(); }
+using dropin::Buf;
+using dropin::DeviceBuffer;
+using dropin::download_f32;
+using dropin::upload_bytes;
+using dropin::upload_f32;
 
 Buf upload_labels(const TensorPtr& labels, const char* who) {
     if (labels->dtype() != kInt32) throw std::runtime_error(std::string(who) + ": labels must be int32");
@@ -115,14 +70,6 @@ Buf upload_grad_loss(const TensorPtr& grad_output, int64_t n) {
     auto buf = upload_bytes(g.data(), g.size() * 4);
     hip_check(hipStreamSynchronize(loss_stream()), "synchronize");  // g is a local
     return buf;
-}
-
-TensorPtr download_f32(const DeviceBuffer& src, const std::vector<int64_t>& shape) {
-    auto out = zeros(shape, kFloat32, kCPU);
-    hip_check(hipMemcpyAsync(out->data<float>(), src.get(), static_cast<size_t>(out->numel()) * 4,
-                             hipMemcpyDeviceToHost, loss_stream()),
-              "copy to host");
-    return out;
 }
 
 // The forward's device state, kept by the backward node.

@@ -25,7 +25,6 @@
 #include <algorithm>
 #include <cstring>
 #include <memory>
-#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -36,73 +35,23 @@
 #include "../core/backward_functions.h"
 #include "../core/ops.h"
 #include "mft/lora.h"
+#include "dropin_device.h"
 
 namespace ops {
 namespace {
 
-void hip_check(hipError_t e, const char* what) {
-    if (e != hipSuccess) throw std::runtime_error(std::string("LoRALinear: ") + what + ": " + hipGetErrorString(e));
-}
-
-void mft_check(mft_status st) {
-    if (st != MFT_OK) throw std::runtime_error(std::string("LoRALinear: ") + mft_last_error());
-}
-
-hipStream_t lora_stream() {
-    static std::once_flag once;
-    static hipStream_t s = nullptr;
-    std::call_once(once, [] { hip_check(hipStreamCreate(&s), "hipStreamCreate"); });
-    return s;
-}
-
-class DeviceBuffer {
-public:
-    explicit DeviceBuffer(size_t bytes) {
-        if (bytes) hip_check(hipMalloc(&ptr_, bytes), "hipMalloc");
-    }
-    ~DeviceBuffer() {
-        if (ptr_) (void)hipFree(ptr_);
-    }
-    DeviceBuffer(const DeviceBuffer&) = delete;
-    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
-    void* get() const { return ptr_; }
-    float* f() const { return static_cast<float*>(ptr_); }
-
-private:
-    void* ptr_ = nullptr;
-};
-
-std::unique_ptr<DeviceBuffer> upload_bytes(const void* src, size_t n) {
-    auto buf = std::make_unique<DeviceBuffer>(n);
-    if (n) hip_check(hipMemcpyAsync(buf->get(), src, n, hipMemcpyHostToDevice, lora_stream()), "copy to device");
-    return buf;
-}
+constexpr const char* kWho = "LoRALinear";
+void hip_check(hipError_t e, const char* what) { dropin::hip_check(kWho, e, what); }
+void mft_check(mft_status st) { dropin::mft_check(kWho, st); }
+hipStream_t lora_stream() { return dropin::stream(); }
+using dropin::DeviceBuffer;
+using dropin::download_f32;
+using dropin::upload_bytes;
 
 // Any floating-point host tensor as fp32 values on the device (the C ABI's
 // A, B, x and bias are fp32; the reference reads them through
 // read_tensor_float, nn/lora_linear.cpp:19-31).
-std::unique_ptr<DeviceBuffer> upload_f32(const TensorPtr& t) {
-    const int64_t n = t->numel();
-    if (t->dtype() == kFloat32) return upload_bytes(t->data<float>(), static_cast<size_t>(n) * 4);
-    std::vector<float> v(static_cast<size_t>(n));
-    for (int64_t i = 0; i < n; ++i) {
-        const uint16_t b = t->data<uint16_t>()[i];
-        if (t->dtype() == kBFloat16) v[static_cast<size_t>(i)] = bf16_bits_to_float32(b);
-        else if (t->dtype() == kFloat16) v[static_cast<size_t>(i)] = fp16_bits_to_float32(b);
-        else throw std::runtime_error("LoRALinear: expected floating-point tensor storage");
-    }
-    auto buf = upload_bytes(v.data(), v.size() * 4);
-    hip_check(hipStreamSynchronize(lora_stream()), "synchronize");  // v is a local
-    return buf;
-}
-
-TensorPtr download_f32(const DeviceBuffer& src, const std::vector<int64_t>& shape) {
-    auto out = zeros(shape, kFloat32, kCPU);
-    hip_check(hipMemcpyAsync(out->data<float>(), src.get(), static_cast<size_t>(out->numel()) * 4,
-                             hipMemcpyDeviceToHost, lora_stream()),
-              "copy to host");
-    return out;
-}
+std::unique_ptr<DeviceBuffer> upload_f32(const TensorPtr& t) { return dropin::upload_f32(t, kWho); }
 
 int32_t w_dtype(const TensorPtr& W) {
     if (W->dtype() == kFloat32) return MFT_F32;

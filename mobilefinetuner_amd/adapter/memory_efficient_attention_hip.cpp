@@ -41,7 +41,6 @@
 #include <cmath>
 #include <cstring>
 #include <memory>
-#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -52,47 +51,18 @@
 #include "backward_functions.h"
 #include "fused_attention.h"
 #include "mft/attention.h"
+#include "dropin_device.h"
 #include "ops.h"
 
 namespace ops {
 namespace {
 
-void hip_check(hipError_t e, const char* what) {
-    if (e != hipSuccess) throw std::runtime_error(std::string("memory_efficient_attention: ") + what + ": " +
-                                                  hipGetErrorString(e));
-}
-
-void mft_check(mft_status st) {
-    if (st != MFT_OK) throw std::runtime_error(std::string("memory_efficient_attention: ") + mft_last_error());
-}
-
-// One stream for the adapter's work (default priority), created on first use.
-hipStream_t adapter_stream() {
-    static std::once_flag once;
-    static hipStream_t s = nullptr;
-    std::call_once(once, [] { hip_check(hipStreamCreate(&s), "hipStreamCreate"); });
-    return s;
-}
-
-// Device buffer owned by the adapter (freed when the last owner goes away).
-class DeviceBuffer {
-public:
-    DeviceBuffer() = default;
-    explicit DeviceBuffer(size_t bytes) : bytes_(bytes) {
-        if (bytes) hip_check(hipMalloc(&ptr_, bytes), "hipMalloc");
-    }
-    ~DeviceBuffer() {
-        if (ptr_) (void)hipFree(ptr_);
-    }
-    DeviceBuffer(const DeviceBuffer&) = delete;
-    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
-    void* get() const { return ptr_; }
-    size_t bytes() const { return bytes_; }
-
-private:
-    void* ptr_ = nullptr;
-    size_t bytes_ = 0;
-};
+constexpr const char* kWho = "memory_efficient_attention";
+void hip_check(hipError_t e, const char* what) { dropin::hip_check(kWho, e, what); }
+void mft_check(mft_status st) { dropin::mft_check(kWho, st); }
+hipStream_t adapter_stream() { return dropin::stream(); }
+using dropin::DeviceBuffer;
+using dropin::download_f32;
 
 size_t elt_size(DType t) { return t == kBFloat16 ? 2 : 4; }
 
@@ -120,14 +90,6 @@ TensorPtr download_as_f32(const DeviceBuffer& src, const std::vector<int64_t>& s
         float* o = out->data<float>();
         for (size_t i = 0; i < n; ++i) o[i] = bf16_bits_to_float32(bits[i]);
     }
-    return out;
-}
-
-TensorPtr download_f32(const DeviceBuffer& src, const std::vector<int64_t>& shape) {
-    auto out = zeros(shape, kFloat32, kCPU);
-    hip_check(hipMemcpyAsync(out->data<float>(), src.get(), static_cast<size_t>(out->numel()) * 4,
-                             hipMemcpyDeviceToHost, adapter_stream()),
-              "copy to host");
     return out;
 }
 
