@@ -119,6 +119,20 @@ __global__ __launch_bounds__(256) void lora_rowdot_kernel(LoraRowDot a) {
                     mv[i][0] = m[0];
                 }
             }
+            if (a.mb && jb == 0) {  // the bf16 copy of M, from the first j-block's loads
+#pragma unroll
+                for (int i = 0; i < kRowsPerWg; ++i) {
+                    if (n0 + i >= a.rows) continue;
+                    uint16_t* d = a.mb + (n0 + i) * a.ldb + k;
+                    if (VEC == 4)
+                        *reinterpret_cast<uint2*>(d) =
+                            make_uint2((uint32_t)bf16_bits_rne(mv[i][0]) | ((uint32_t)bf16_bits_rne(mv[i][1 % VEC]) << 16),
+                                       (uint32_t)bf16_bits_rne(mv[i][2 % VEC]) |
+                                           ((uint32_t)bf16_bits_rne(mv[i][3 % VEC]) << 16));
+                    else
+                        d[0] = bf16_bits_rne(mv[i][0]);
+                }
+            }
 #pragma unroll
             for (int i = 0; i < kRowsPerWg; ++i)
 #pragma unroll
@@ -266,7 +280,8 @@ hipError_t launch_lora_fill_bias(float* y, const float* bias, int64_t N, int64_t
 hipError_t launch_lora_rowdot(const LoraRowDot& a, hipStream_t st) {
     if (a.rows <= 0 || a.r <= 0) return hipSuccess;
     const dim3 grid((unsigned)((a.rows + kRowsPerWg - 1) / kRowsPerWg));
-    const bool vec = a.K % 4 == 0 && a.ldm % 4 == 0 && (uintptr_t)a.M % 16 == 0;
+    const bool vec = a.K % 4 == 0 && a.ldm % 4 == 0 && (uintptr_t)a.M % 16 == 0 &&
+                     (!a.mb || (a.ldb % 4 == 0 && (uintptr_t)a.mb % 8 == 0));
     if (vec)
         hipLaunchKernelGGL(lora_rowdot_kernel<4>, grid, dim3(256), 0, st, a);
     else

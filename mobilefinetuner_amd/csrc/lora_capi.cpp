@@ -3,13 +3,14 @@
 // The layer is GEMMs plus element-wise staging.  Row-major throughout, R =
 // sum of the slices' ranks, s_i = scale_i:
 //   forward   y  = x . W (+ bias)                 rocBLAS; bf16 W: x staged
-//                                                  to bf16 (lora_round_bf16)
+//                                                  to bf16 by the first rowdot
 //             u_i = x . A_i                        lora_rowdot, into u[:, ro_i ..]
 //             y[:, col0_i ..] += s_i u_i . B_i     rocBLAS fp32, beta = 1
 //   backward  g_i = s_i dy[:, col0_i ..] . B_i^T   lora_rowdot (workspace [N, R])
 //             grad_B_i = s_i u_i^T . dy[:, col0_i ..]   lora_coldot
 //             grad_A_i = x^T . g_i                      lora_coldot
 //             dx = dy . W^T + sum_i g_i . A_i^T     rocBLAS; bf16 W: dy staged to bf16
+//                                                  by a full-width slice's rowdot
 // which is the reference's autograd graph of matmul / mul / add
 // (nn/lora_linear.cpp:384-434 with MatmulBackward,
 // core/backward_functions.cpp:94-160).  The rank-r products with a long inner
@@ -125,14 +126,17 @@ BwdLayout bwd_layout(const mft_lora_desc* d) {
 // A P that is not k-contiguous (pk != 1) is first copied k-major into
 // `pack` (K x r floats of workspace): rowdot's lanes stride over k, and a
 // j-contiguous P would put every lane of a load on its own cache line.
+// With mb, the same pass also writes the bf16 copy of M[:, :K] (row stride
+// K) that the MFMA GEMM reads, so M is read from HBM once.
 mft_status rowdot(const float* M, int64_t ldm, int64_t rows, int64_t K, const float* P, int64_t pk, int64_t pj,
-                  float* out, int64_t ldo, int64_t r, float alpha, float* pack, hipStream_t stream, const char* who) {
+                  float* out, int64_t ldo, int64_t r, float alpha, float* pack, hipStream_t stream, const char* who,
+                  uint16_t* mb = nullptr) {
     if (pk != 1) {
         const hipError_t e = mft::launch_lora_pack_kmajor(P, pk, pj, K, (int)r, pack, stream);
         if (e != hipSuccess) return hip_status(e, who);
         P = pack, pk = 1, pj = K;
     }
-    mft::LoraRowDot a{M, ldm, rows, K, P, pk, pj, out, ldo, (int)r, alpha};
+    mft::LoraRowDot a{M, ldm, rows, K, P, pk, pj, out, ldo, (int)r, alpha, mb, K};
     return hip_status(mft::launch_lora_rowdot(a, stream), who);
 }
 
@@ -183,27 +187,32 @@ mft_status mft_lora_fwd(const mft_lora_desc* desc, const float* x, const void* W
 
     hipError_t e = hipSuccess;
     if (bias) e = mft::launch_lora_fill_bias(y, bias, N, out, stream);
-    const void* xo = x;
-    if (e == hipSuccess && bf) {
-        e = mft::launch_lora_round_bf16(x, reinterpret_cast<uint16_t*>(ws + l.xb), N * in, stream);
-        xo = ws + l.xb;
-    }
+    // bf16 W: the GEMM reads x rounded to bf16, written by the first slice's
+    // rowdot (one read of x) or, without slices, by lora_round_bf16.
+    uint16_t* xb = bf ? reinterpret_cast<uint16_t*>(ws + l.xb) : nullptr;
+    if (e == hipSuccess && bf && desc->n_slices == 0) e = mft::launch_lora_round_bf16(x, xb, N * in, stream);
     if (e != hipSuccess) return hip_status(e, "mft_lora_fwd launch");
-
-    auto lock = mft::blas::lock();
-    rocblas_handle h;
-    if ((r = mft::blas::bind(who, stream, ws + l.blas, kBlasWorkspace, &h)) != MFT_OK) return r;
-    const WOperand wo = w_for_forward(desc);
-    if ((r = mft::blas::gemm_rm(who, h, N, out, in, 1.f, xo, in, false, W, wo.ld, wo.t, bias ? 1.f : 0.f, y, out,
-                                bf)) != MFT_OK)
-        return r;
     int64_t ro = 0;
     for (int i = 0; i < desc->n_slices; ++i) {
         const mft_lora_slice& s = desc->slices[i];
         // u_i[N, r] = x . A_eff, A_eff(k, j) = A[k, j] or A[j, k]
         if ((r = rowdot(x, in, N, in, s.A, s.a_transposed ? 1 : s.rank, s.a_transposed ? in : 1, u + ro, R, s.rank,
-                        1.f, reinterpret_cast<float*>(ws + l.pt), stream, "mft_lora_fwd launch")) != MFT_OK)
+                        1.f, reinterpret_cast<float*>(ws + l.pt), stream, "mft_lora_fwd launch",
+                        i == 0 ? xb : nullptr)) != MFT_OK)
             return r;
+        ro += s.rank;
+    }
+
+    auto lock = mft::blas::lock();
+    rocblas_handle h;
+    if ((r = mft::blas::bind(who, stream, ws + l.blas, kBlasWorkspace, &h)) != MFT_OK) return r;
+    const WOperand wo = w_for_forward(desc);
+    if ((r = mft::blas::gemm_rm(who, h, N, out, in, 1.f, bf ? static_cast<const void*>(xb) : x, in, false, W, wo.ld,
+                                wo.t, bias ? 1.f : 0.f, y, out, bf)) != MFT_OK)
+        return r;
+    ro = 0;
+    for (int i = 0; i < desc->n_slices; ++i) {
+        const mft_lora_slice& s = desc->slices[i];
         // y[:, col0 .. col0 + cols] += scale * u_i . B_i
         if ((r = mft::blas::gemm_rm(who, h, N, s.cols, s.rank, s.scale, u + ro, R, false, s.B,
                                     s.b_transposed ? s.rank : s.cols, s.b_transposed != 0, 1.f, y + s.col0, out,
@@ -228,12 +237,20 @@ mft_status mft_lora_bwd(const mft_lora_desc* desc, const float* x, const void* W
     float* g = reinterpret_cast<float*>(ws + l.g);
     float* part = reinterpret_cast<float*>(ws + l.part);
 
-    const void* dyo = dy;
-    if (dx && bf) {
-        const hipError_t e = mft::launch_lora_round_bf16(dy, reinterpret_cast<uint16_t*>(ws + l.dyb), N * out, stream);
-        if (e != hipSuccess) return hip_status(e, "mft_lora_bwd launch");
-        dyo = ws + l.dyb;
+    // bf16 W: the dx GEMM reads dy rounded to bf16, written by the rowdot of
+    // the first slice that spans all columns and gets gradients (one read of
+    // dy), or else by lora_round_bf16.
+    uint16_t* dyb = dx && bf ? reinterpret_cast<uint16_t*>(ws + l.dyb) : nullptr;
+    int fuse = -1;
+    for (int i = 0; dyb && fuse < 0 && i < desc->n_slices; ++i) {
+        const mft_lora_slice& s = desc->slices[i];
+        if (s.col0 == 0 && s.cols == out && has_grad(desc, s)) fuse = i;
     }
+    if (dyb && fuse < 0) {
+        const hipError_t e = mft::launch_lora_round_bf16(dy, dyb, N * out, stream);
+        if (e != hipSuccess) return hip_status(e, "mft_lora_bwd launch");
+    }
+    const void* dyo = dyb ? static_cast<const void*>(dyb) : dy;
 
     auto lock = mft::blas::lock();
     rocblas_handle h;
@@ -246,7 +263,8 @@ mft_status mft_lora_bwd(const mft_lora_desc* desc, const float* x, const void* W
             const float* dys = dy + s.col0;
             // g_i[N, r] = scale * dy_slice . B_eff^T, B_eff(j, o) = B[j, o] or B[o, j]
             if ((r = rowdot(dys, out, N, s.cols, s.B, s.b_transposed ? rk : 1, s.b_transposed ? 1 : s.cols, g + ro, R,
-                            rk, s.scale, reinterpret_cast<float*>(ws + l.pt), stream, "mft_lora_bwd launch")) != MFT_OK)
+                            rk, s.scale, reinterpret_cast<float*>(ws + l.pt), stream, "mft_lora_bwd launch",
+                            i == fuse ? dyb : nullptr)) != MFT_OK)
                 return r;
             // grad_B(o, j) = scale * sum_n dy[n, col0 + o] u_i[n, j], stored [r, cols] or [cols, r]
             if (s.grad_B && (r = coldot(dys, out, N, s.cols, u + ro, R, rk, s.scale, part, s.grad_B,

@@ -38,8 +38,11 @@ struct LoraRowDot {
     int64_t ldo;
     int r;
     float alpha;
+    uint16_t* mb;          // optional: bf16 (RNE) copy of M[:, :K], leading dimension ldb
+    int64_t ldb;
 };
-// out[n, j] = alpha * sum_k M[n, k] P(k, j)
+// out[n, j] = alpha * sum_k M[n, k] P(k, j); with mb, also mb[n * ldb + k] =
+// bf16(M[n, k]) from the same loads (M is read once).
 hipError_t launch_lora_rowdot(const LoraRowDot& a, hipStream_t st);
 // dst[j * K + k] = P(k, j) for k < K, j < r: the k-contiguous copy rowdot
 // reads with coalesced loads when P is not k-contiguous already.

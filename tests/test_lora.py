@@ -87,6 +87,10 @@ CASES = [
                                         (8, 2.0, 512, 256, False, True)], True),
     (64, 96, 112, True, True, True, [(4, 0.25, 0, 112, False, False)], False),
     (33, 17, 29, False, False, True, [(3, 1.0, 0, 29, True, False), (2, 3.0, 7, 9, False, True)], False),
+    # bf16 W with in and out not multiples of 4 (scalar loads and bf16 stores in the staging rowdot)
+    (45, 35, 50, False, True, False, [(3, 1.5, 0, 50, False, False)], False),
+    # bf16 W whose only slice is a column range without gradients (dy staged by lora_round_bf16)
+    (64, 128, 96, False, True, True, [(4, 1.0, 32, 32, False, False)], False),
 ]
 
 
