@@ -42,7 +42,7 @@ def hipcc() -> str:
 # Files whose MFMA accumulators should be allocated in VGPRs: their kernels
 # keep all live state within 256 VGPRs, and the VGPR form avoids copying the
 # loop-carried accumulators between AGPRs and VGPRs on every iteration.
-VGPR_FORM = {"attn_fwd.hip", "attn_bwd_fast64.hip"}
+VGPR_FORM = {"attn_fwd.hip", "attn_fwd_fast256.hip", "attn_bwd_fast64.hip"}
 
 
 def sources():

@@ -178,6 +178,50 @@ __device__ __forceinline__ void load_lds_16(const void* gptr, void* lds_base) {
                  : "memory", "m0");
 }
 
+// The same load with the address split into a wave-uniform 64-bit base (an
+// SGPR pair: the instruction's saddr form) and this lane's 32-bit byte offset,
+// so that a tile's loads need no per-lane 64-bit address arithmetic.
+// lds_addr: the wave-uniform LDS byte address of the 1 KiB destination.
+__device__ __forceinline__ void load_lds_16_s(const void* sbase, uint32_t voff, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
+                 "s"(lds_addr)
+                 : "memory", "m0");
+}
+
+// LDS byte address of a __shared__ pointer (wave-uniform where p is).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const lds_void_t*)p);
+}
+
+// ---------------------------------------------------------------------------
+// v_mfma_f32_32x32x16_bf16 with its accumulator in VGPRs, as inline asm.
+//
+// The builtin puts every MFMA accumulator of a function in AGPRs or every one
+// in VGPRs (the register form is chosen per compile).  The D = 256 kernels
+// need both at once: their loop-carried accumulators fill the 256 AGPRs, so
+// the per-tile score products (S, dP) run through these VGPR forms.
+//
+// The hazard recognizer does not look inside inline asm, so these carry the
+// wait states the compiler inserts around the builtin on gfx950:
+//   - 2 wait states between a VALU write of an operand and the MFMA
+//     (s_nop 1 in front of every MFMA);
+//   - after the last MFMA of a chain, mfma_v_drain: 16 wait states (the
+//     builtin gets 12 for this 8-pass MFMA) before any instruction reads or
+//     writes its result registers.  The drain takes the accumulators as
+//     operands, so nothing that uses them can be scheduled before it.
+// Back-to-back MFMAs accumulating into the same registers need none.  Early
+// clobber keeps the result registers apart from the operands.
+__device__ __forceinline__ void mfma_v_first(f32x16& c, const bf16x8& a, const bf16x8& b) {
+    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(c) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma_v(f32x16& c, const bf16x8& a, const bf16x8& b) {
+    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma_v_drain(f32x16& c0, f32x16& c1) {
+    asm volatile("s_nop 7\n\ts_nop 7" : "+v"(c0), "+v"(c1));
+}
+__device__ __forceinline__ void mfma_v_drain(f32x16& c0) { asm volatile("s_nop 7\n\ts_nop 7" : "+v"(c0)); }
+
 // Wave index in the workgroup as a wave-uniform (scalar) value, for LDS
 // addresses of the direct loads.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
@@ -230,13 +274,13 @@ __device__ __forceinline__ bf16x4 ds_read_tr4(const bf16* lds_elem_ptr) {
 //  swz_tr  : for transposing reads, where a wave reads 8 consecutive rows x
 //            64 bytes (ds_read_b64_tr_b16) -> 2 cycles, the minimum.
 //  swz_dual: both patterns at their minimum (tiles read both ways).
-template <int CPR> __device__ __forceinline__ int swz_row(int r) {
+template <int CPR> __host__ __device__ __forceinline__ constexpr int swz_row(int r) {
     return CPR >= 16 ? (r & 15) : ((r >> 1) & 7);
 }
-template <int CPR> __device__ __forceinline__ int swz_tr(int r) {
+template <int CPR> __host__ __device__ __forceinline__ constexpr int swz_tr(int r) {
     return (CPR >= 16 ? (r & 3) : ((r >> 1) & 1)) << 2;
 }
-template <int CPR> __device__ __forceinline__ int swz_dual(int r) {
+template <int CPR> __host__ __device__ __forceinline__ constexpr int swz_dual(int r) {
     return CPR >= 16 ? (4 * (r & 3) + ((r >> 2) & 3)) : (4 * ((r >> 1) & 1) + ((r >> 2) & 3));
 }
 
@@ -261,13 +305,13 @@ __device__ __forceinline__ void pin_read_ahead() {
     __builtin_amdgcn_sched_group_barrier(SG_MFMA, PF * M, 0);
 }
 
-template <int CPR, int SWZ> __device__ __forceinline__ int swz(int r) {
+template <int CPR, int SWZ> __host__ __device__ __forceinline__ constexpr int swz(int r) {
     return SWZ == SWZ_ROW ? swz_row<CPR>(r) : SWZ == SWZ_TR ? swz_tr<CPR>(r) : swz_dual<CPR>(r);
 }
 
 // Element offset of (row r, column col) in a swizzled bf16 tile.
 template <int CPR, int SWZ>
-__device__ __forceinline__ int tile_off(int r, int col) {
+__host__ __device__ __forceinline__ constexpr int tile_off(int r, int col) {
     return r * (CPR * 8) + (((col >> 3) ^ swz<CPR, SWZ>(r)) << 3) + (col & 7);
 }
 
@@ -293,6 +337,54 @@ __device__ __forceinline__ void issue_tile_part(const bf16* __restrict__ src, in
     const int gr = min(row0 + r, S - 1);
     const int col = 8 * c < D ? 8 * c : 0;
     load_lds_16(src + (int64_t)gr * ld + col, lds_tile + m * 512);
+}
+
+// The same loads with loop-invariant per-lane offsets.  Load j of wave w
+// (m = w * PER + j, PER loads per thread) covers the R = 64 / CPR tile rows
+// R*m .. R*m + R - 1 and fills LDS bytes m * 1024 ..; lane (q = lane / CPR,
+// p = lane % CPR) reads row R*m + q, chunk p ^ swz(R*m + q).  The swizzles
+// are XOR-linear over disjoint row bits and R*m + q = R*w*PER | R*j | q, so
+// that chunk is (p ^ swz(q) ^ swz(R*w*PER)) ^ swz(R*j): a per-lane part and a
+// compile-time part.  The lane's byte offset inside the rows of load j is
+//   q * ld * 2 + (lx ^ 16 * swz(R*j)),   lx = 16 * (p ^ swz(q) ^ swz(R*w*PER)).
+// The rows' base (row0 + R*m) goes into the instruction's scalar address.
+// Valid for D == DP (whole rows; no column clamp) and rows < S; callers
+// take issue_tile_part for a load that would cross S.
+template <int DP, int ROWS, int NT, int SWZ> struct TileDma {
+    static constexpr int CPR = DP / 8, R = 64 / CPR, PER = ROWS * CPR / NT;
+    static_assert(PER * NT == ROWS * CPR && R * CPR == 64, "tile must split evenly over the threads");
+    uint32_t lx, lrow;
+    // Row offset (within the tile) of this wave's first load.
+    static __host__ __device__ constexpr int row_w(int w) { return R * w * PER; }
+    static __host__ __device__ constexpr uint32_t cx(int j) { return 16u * (uint32_t)swz<CPR, SWZ>(R * j); }
+    __host__ __device__ void init(int lane, int w, int ld_elems) {
+        const int q = lane / CPR, p = lane % CPR;
+        lx = 16u * (uint32_t)(p ^ swz<CPR, SWZ>(q) ^ swz<CPR, SWZ>(row_w(w)));
+        lrow = (uint32_t)q * (uint32_t)ld_elems * 2u;
+    }
+    __host__ __device__ uint32_t voff(int j) const { return lrow + (lx ^ cx(j)); }
+};
+
+// Load j of this thread's share of a tile.  FAST: the tile uses TileDma,
+// which the launch may choose when every tile is whole (D == DP and S a
+// multiple of the tile's rows).  Otherwise issue_tile_part, which clamps rows
+// and columns per lane.
+template <bool FAST, int DP, int ROWS, int NT, int SWZ>
+__device__ __forceinline__ void issue_tile_j(const TileDma<DP, ROWS, NT, SWZ>& t, const bf16* __restrict__ src,
+                                             int row0, int S, int D, int ld, bf16* lds_tile, int j) {
+    typedef TileDma<DP, ROWS, NT, SWZ> TD;
+    if constexpr (FAST) {
+        const int w = wave_id();
+        // wave-uniform: the scalar base of this wave's rows, and M0
+        const char* base = reinterpret_cast<const char*>(src + (int64_t)(row0 + TD::row_w(w)) * ld) +
+                           (int64_t)(TD::R * j) * ld * 2;
+        const uint32_t m0 = lds_addr(lds_tile) + (uint32_t)(w * TD::PER) * 1024u;
+        asm volatile("s_add_u32 m0, %2, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(t.voff(j)),
+                     "s"(base), "s"(m0), "n"(j * 1024)
+                     : "memory", "m0");
+    } else {
+        issue_tile_part<DP, ROWS, NT, SWZ>(src, row0, S, D, ld, lds_tile, j);
+    }
 }
 
 template <int DP, int ROWS, int NT, int SWZ>
