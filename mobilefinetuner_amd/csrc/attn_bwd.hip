@@ -155,13 +155,18 @@ __device__ __forceinline__ void dkdv_bf16_body(const BwdArgs& a, char* smem, int
             // no row of the block sees a key of this wave
             if (!vis.any(qb, min(qb + 31, S - 1), wkey0, min(wkey0 + 31, S - 1))) continue;
 
-            f32x16 s = zero16(), dp = zero16();
+            f32x16 s, dp;
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
                 const bf16x8 qa = *reinterpret_cast<const bf16x8*>(Qs + n * QSTR + 16 * c + 8 * hh);
-                s = mfma_bf16(qa, kf[c], s);
                 const bf16x8 ga = *reinterpret_cast<const bf16x8*>(Gs + n * QSTR + 16 * c + 8 * hh);
-                dp = mfma_bf16(ga, vf[c], dp);
+                if (c == 0) {
+                    mfma_chunk_first<true>(s, qa, kf[c]);
+                    mfma_chunk_first<true>(dp, ga, vf[c]);
+                } else {
+                    s = mfma_bf16(qa, kf[c], s);
+                    dp = mfma_bf16(ga, vf[c], dp);
+                }
             }
             // lane column n = key; register r = query qb + row_of_reg(r, hh)
             const bool need_mask = !vis.all(qb, qb + 31, wkey0, wkey0 + 31);
@@ -287,15 +292,20 @@ __device__ __forceinline__ void dkdv_f32_body(const BwdArgs& a, char* smem, int 
             if (wkey0 >= S) continue;
             if (!vis.any(qb, min(qb + 31, S - 1), wkey0, min(wkey0 + 31, S - 1))) continue;
 
-            f32x16 s = zero16(), dp = zero16();
+            f32x16 s, dp;
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
                 const f32x4 qa = *reinterpret_cast<const f32x4*>(Qs + n * STR + 8 * c + 4 * hh);
                 const f32x4 kb = *reinterpret_cast<const f32x4*>(Kw + 8 * c + 4 * hh);
-                s = mfma_chunk(qa, kb, s);
                 const f32x4 ga = *reinterpret_cast<const f32x4*>(Gs + n * STR + 8 * c + 4 * hh);
                 const f32x4 vb = *reinterpret_cast<const f32x4*>(Vw + 8 * c + 4 * hh);
-                dp = mfma_chunk(ga, vb, dp);
+                if (c == 0) {
+                    mfma_chunk_first<true>(s, qa, kb);
+                    mfma_chunk_first<true>(dp, ga, vb);
+                } else {
+                    s = mfma_chunk(qa, kb, s);
+                    dp = mfma_chunk(ga, vb, dp);
+                }
             }
             const bool need_mask = !vis.all(qb, qb + 31, wkey0, wkey0 + 31);
 #pragma unroll
@@ -420,16 +430,23 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int qt, in
         const bool need_mask = !vis.all(wrow0, wrow0 + 31, kbase, kbase + BN - 1);
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk) {
-            f32x16 s = zero16(), dp = zero16();
+            f32x16 s, dp;
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
                 const V ka = *reinterpret_cast<const V*>(Ks + (32 * kk + n) * L::STR + 2 * VEC * c + VEC * hh);
-                s = mfma_chunk(ka, qf[c], s);
                 const V va = *reinterpret_cast<const V*>(Vs + (32 * kk + n) * L::STR + 2 * VEC * c + VEC * hh);
+                V gb;
                 if constexpr (GF_REG)
-                    dp = mfma_chunk(va, gf[c], dp);
+                    gb = gf[c];
                 else
-                    dp = mfma_chunk(va, load_chunk<T>(grow, 2 * VEC * c + VEC * hh, D, row < S, vec_ok), dp);
+                    gb = load_chunk<T>(grow, 2 * VEC * c + VEC * hh, D, row < S, vec_ok);
+                if (c == 0) {
+                    mfma_chunk_first<true>(s, ka, qf[c]);
+                    mfma_chunk_first<true>(dp, va, gb);
+                } else {
+                    s = mfma_chunk(ka, qf[c], s);
+                    dp = mfma_chunk(va, gb, dp);
+                }
             }
             // lane column n = query row; register r = key kbase + 32kk + row_of_reg(r, hh)
 #pragma unroll

@@ -56,25 +56,83 @@ __global__ __launch_bounds__(256) void attn_bwd_stats_kernel(BwdArgs a) {
 template <int DP> struct BwdFastLds {
     // V_LDS: at D = 256 the dK/dV role reads V of its 128 keys from LDS (B
     // operand of dP) instead of registers: K, dK and dV already take 320 of
-    // a wave's 512 registers and the LDS operand pipeline needs the rest.
+    // a wave's 512 registers.
     static constexpr bool V_LDS = DP >= 256;
-    static constexpr int KV_BUF = 2 * 32 * DP + 4 * 512;  // Q, dO tiles + 4 waves x 1 KiB stats (elements)
-    static constexpr int KV_ELEMS = 2 * KV_BUF + (V_LDS ? 128 * DP : 0);
-    static constexpr int Q_BUF = 2 * 64 * DP;             // K, V tiles
-    static constexpr int Q_ELEMS = 2 * Q_BUF;
+    // dK/dV role, in elements: [Q tile 0][Q tile 1][dO tile 0][dO tile 1]
+    // (32 x DP each), [stats 0][stats 1] (4 waves x 1 KiB each), then V of the
+    // key tile (128 x DP).  Keeping the four operand tiles first keeps every
+    // read's tile and step offsets inside the 16-bit immediate.
+    static constexpr int QT = 32 * DP;
+    static constexpr int ST_OFF = 4 * QT, ST = 4 * 512;
+    static constexpr int V_OFF = ST_OFF + 2 * ST;
+    static constexpr int KV_ELEMS = V_OFF + (V_LDS ? 128 * DP : 0);
+    // dQ role: [K tile 0][K tile 1][V tile 0][V tile 1], 64 x DP each.
+    static constexpr int KT = 64 * DP;
+    static constexpr int Q_ELEMS = 4 * KT;
     static constexpr int ELEMS = KV_ELEMS > Q_ELEMS ? KV_ELEMS : Q_ELEMS;
 };
 
-template <int DP, bool CAUSAL, bool STRIDED>
+// Per-lane, loop-invariant LDS read offsets (bytes) of the fast backward's
+// SWZ_DUAL tiles, shared by both roles (tests/native/offsets_check.cpp checks
+// them against tile_off):
+//  rr[j]: row reads.  Row 32k + n, column chunk 2c + hh:
+//         n*ROWB + (32c ^ 16 (hh ^ swz_dual(n))) + 32k*ROWB, and c, c + 8 differ
+//         by 256 bytes: rr[c % 8].
+//  tr[hi][j]: transposing reads (ds_read_b64_tr_b16) of rows
+//         32k + 16e + 8hi + 4hh + i16/4, columns 32dt + 16nh + 4 (i16 & 3):
+//         the row's swizzle depends on (hi, lane) only, so the offset is
+//         tr[hi][dt % 4] + (32k + 16e)*ROWB + 256 (dt / 4).
+template <int DP> struct BwdLane {
+    static constexpr int CPR = DP / 8, ROWB = DP * 2, NC = DP / 16, NDT = DP / 32;
+    static constexpr int KC = NC < 8 ? NC : 8;
+    static constexpr int VC = NDT < 4 ? NDT : 4;
+    uint32_t rr[KC];
+    uint32_t tr[2][VC];
+    __host__ __device__ void init(int lane) {
+        const int n = lane & 31, hh = lane >> 5, i16 = lane & 15, nh = (lane >> 4) & 1;
+        const uint32_t y16 = 16u * (uint32_t)(hh ^ swz_dual<CPR>(n));
+#pragma unroll
+        for (int j = 0; j < KC; ++j) rr[j] = (uint32_t)n * ROWB + ((32u * j) ^ y16);
+        const int W = 2 * nh + ((i16 & 3) >> 1);
+#pragma unroll
+        for (int hi = 0; hi < 2; ++hi) {
+            const int rlow = 8 * hi + 4 * hh + (i16 >> 2);
+            const int sw = swz_dual<CPR>(rlow);
+#pragma unroll
+            for (int j = 0; j < VC; ++j)
+                tr[hi][j] = (uint32_t)rlow * ROWB + 16u * (uint32_t)((4 * j + W) ^ sw) + 8u * (i16 & 1);
+        }
+    }
+    __host__ __device__ uint32_t row(int k, int c) const { return rr[c % KC] + k * 32 * ROWB + (c / KC) * 256; }
+    __host__ __device__ uint32_t trn(int k, int e, int dt, int hi) const {
+        return tr[hi][dt % VC] + (32 * k + 16 * e) * ROWB + (dt / VC) * 256;
+    }
+};
+
+// The score products S and dP of one step.  ASM: the VGPR-form inline-asm
+// MFMAs (attn_common.h), used where the loop-carried accumulators fill the
+// AGPRs (D = 256); otherwise the builtin.  The first product of a chain is
+// always the asm form (see mfma_v_first).
+template <bool ASM>
+__device__ __forceinline__ void mm_score(f32x16& c, const bf16x8& a, const bf16x8& b, bool first) {
+    if (first)
+        mfma_v_first(c, a, b);
+    else if constexpr (ASM)
+        mfma_v(c, a, b);
+    else
+        c = mfma_bf16(a, b, c);
+}
+
+template <int DP, bool CAUSAL, bool STRIDED, bool FAST>
 __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int unit, int b, int hk) {
+    typedef BwdFastLds<DP> L;
     constexpr int NT = 256, BNK = 128, CPR = DP / 8, NC = DP / 16, NDT = DP / 32;
-    constexpr int QT = 32 * DP;
-    constexpr int BUF = BwdFastLds<DP>::KV_BUF;
-    constexpr bool V_LDS = BwdFastLds<DP>::V_LDS;
-    constexpr int PF = 4;  // LDS operand prefetch depth
+    constexpr bool V_LDS = L::V_LDS, ASM = DP >= 256;
+    constexpr int PF = 2;  // LDS operand prefetch depth
+    constexpr int QTB = L::QT * 2;  // bytes of one Q or dO tile
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
-    const int i16 = lane & 15, nh = (lane >> 4) & 1;
+    const int i16 = lane & 15;
     const int S = a.S, D = a.D, G = a.group, W = a.window;
     const KeyVis vis = key_vis(a, b, CAUSAL);
     const bf16* K = (const bf16*)a.k + op_base<STRIDED>(a.sk, b, hk, a.Hkv, S, D);
@@ -84,6 +142,12 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
     // registers (the compiler then shuffles them every block).
     const int lk = op_ld<STRIDED>(a.sk, D), lv = lk;
     const int lq = op_ld<STRIDED>(a.sq, D), lg = op_ld<STRIDED>(a.sdo, D);
+    BwdLane<DP> ln;
+    ln.init(lane);
+    const uint32_t smem_addr = lds_addr(smem);
+    TileDma<DP, 32, NT, SWZ_DUAL> dmq, dmg;
+    dmq.init(lane, wave_id(), lq);
+    dmg.init(lane, wave_id(), lg);
 
     // This unit's chunk of the flattened (key tile, query head, query block)
     // iterations; it may start inside one key tile and end inside a later one.
@@ -111,10 +175,9 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
         const bf16* q;
         const bf16* g;
         const float* st;
-        bf16* buf;
-        int qb;
+        int par, qb;
     };
-    auto issue_begin = [&](bf16* buf) {
+    auto issue_begin = [&](int par) {
         const int h = hk * G + pf_h, qb = (CAUSAL ? pf_kt * BNK : 0) + pf_qi * 32;
         if (++pf_qi == pf_nqb) {
             pf_qi = 0;
@@ -126,24 +189,26 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
         }
         return Pending{(const bf16*)a.q + op_base<STRIDED>(a.sq, b, h, a.Hq, S, D),
                        (const bf16*)a.dO + op_base<STRIDED>(a.sdo, b, h, a.Hq, S, D),
-                       a.stats + ((int64_t)(b * a.Hq + h) * a.nqb_total + qb / 32) * 64, buf, qb};
+                       a.stats + ((int64_t)(b * a.Hq + h) * a.nqb_total + qb / 32) * 64, par, qb};
     };
     auto issue_part = [&](const Pending& p, int j) {
         if (j < PER)
-            issue_tile_part<DP, 32, NT, SWZ_DUAL>(p.q, p.qb, S, D, lq, p.buf, j);
+            issue_tile_j<FAST, DP, 32, NT, SWZ_DUAL>(dmq, p.q, p.qb, S, D, lq, smem + p.par * L::QT,
+                                                     smem_addr + 2u * p.par * L::QT, j);
         else if (j < 2 * PER)
-            issue_tile_part<DP, 32, NT, SWZ_DUAL>(p.g, p.qb, S, D, lg, p.buf + QT, j - PER);
+            issue_tile_j<FAST, DP, 32, NT, SWZ_DUAL>(dmg, p.g, p.qb, S, D, lg, smem + (2 + p.par) * L::QT,
+                                                     smem_addr + 2u * (2 + p.par) * L::QT, j - PER);
         else
-            load_lds_16(p.st + 4 * i16, p.buf + 2 * QT + w * 512);
+            load_lds_16(p.st + 4 * i16, smem + L::ST_OFF + p.par * L::ST + w * 512);
     };
-    auto issue = [&](bf16* buf) {
-        const Pending p = issue_begin(buf);
+    auto issue = [&](int par) {
+        const Pending p = issue_begin(par);
 #pragma unroll
         for (int j = 0; j < NPARTS; ++j) issue_part(p, j);
         return p.qb;
     };
 
-    bf16* Vl = smem + 2 * BUF;  // V rows of the current key tile (V_LDS only)
+    bf16* Vl = smem + L::V_OFF;  // V rows of the current key tile (V_LDS only)
     bf16x8 kf[NC], vf[V_LDS ? 1 : NC];
     // Per key tile: this lane's K (and V) fragments, and with V_LDS the V tile.
     auto load_keys = [&](int t) {
@@ -154,7 +219,7 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
             if constexpr (!V_LDS) vf[c] = load_chunk<bf16>(Vg + (int64_t)keyc * lv, 16 * c + 8 * hh, D, key < S, true);
         }
         if constexpr (V_LDS) {
-            issue_tile<DP, BNK, NT, SWZ_ROW>(Vg, t * BNK, S, D, lv, Vl);
+            issue_tile<DP, BNK, NT, SWZ_DUAL>(Vg, t * BNK, S, D, lv, Vl);
             if (D < DP) {
                 // Staged columns >= D hold copies of column chunk 0, and so do
                 // those of the dO tiles: zero them so that dP = dO V^T sums
@@ -163,13 +228,13 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
                 const bf16x8 z = zero_vec<bf16x8>();
                 for (int idx = tid; idx < BNK * CPR; idx += NT) {
                     const int r = idx / CPR, c = idx % CPR;
-                    if (8 * c >= D) *reinterpret_cast<bf16x8*>(Vl + r * DP + ((c ^ swz_row<CPR>(r)) << 3)) = z;
+                    if (8 * c >= D) *reinterpret_cast<bf16x8*>(Vl + r * DP + ((c ^ swz_dual<CPR>(r)) << 3)) = z;
                 }
             }
         }
     };
     load_keys(kt);
-    int cur_qb = issue(smem);  // query block of the block in the current buffer
+    int cur_qb = issue(0);  // query block of the block in the current buffer
     // The key fragments are complete before the loop (the compiler then sees
     // nothing pending inside it; the direct loads are untracked, see load_lds_16).
     wait_vmcnt<0>();
@@ -187,20 +252,19 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
       // Iterations of key tile kt inside this unit, then its dK/dV store.
       const int seg_end = (int)min((int64_t)niter, kstart + kn - g0);
       for (; i < seg_end; ++i) {
-        const bf16* Qb = smem + (i & 1) * BUF;
-        const bf16* Gb = Qb + QT;
-        const float* stt = reinterpret_cast<const float*>(Qb + 2 * QT + w * 512);
-        // This wave's loads of buffer i&1 (issued one iteration ago) have
+        const int par = i & 1;
+        const char* Qb = reinterpret_cast<const char*>(smem) + par * QTB;   // Q tile; dO tile at + 2 QTB
+        const float* stt = reinterpret_cast<const float*>(smem + L::ST_OFF + par * L::ST + w * 512);
+        // This wave's loads of buffer par (issued one iteration ago) have
         // landed; after the barrier every wave's have, and every wave is done
-        // with buffer (i+1)&1, which the next block then streams into.
+        // with buffer par ^ 1, which the next block then streams into.
         wait_vmcnt<0>();
         lds_barrier();
         // The last block prefetches a harmless copy of itself into the idle
         // buffer, so that the load schedule below needs no branch (the unit
         // waits for it before it ends).
-        const Pending pend = i + 1 < niter ? issue_begin(smem + ((i + 1) & 1) * BUF)
-                                           : Pending{(const bf16*)a.q, (const bf16*)a.dO, a.stats,
-                                                     smem + ((i + 1) & 1) * BUF, 0};
+        const Pending pend = i + 1 < niter ? issue_begin(par ^ 1)
+                                           : Pending{(const bf16*)a.q, (const bf16*)a.dO, a.stats, par ^ 1, 0};
         const int qb = cur_qb;
         cur_qb = pend.qb;
         const int wkey0 = kt * BNK + 32 * w;
@@ -210,17 +274,15 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
         if (wave_uniform(wkey0 < S && vis.any(qb, min(qb + 31, S - 1), wkey0, min(wkey0 + 31, S - 1)))) {
         // S = Q K^T and dP = dO V^T, one chunk of both per step; the steps'
         // LDS operands (Q, dO and, with V_LDS, V) are read PF steps ahead.
-        f32x16 s = zero16(), dp = zero16();
+        f32x16 s, dp;
         {
-            constexpr int R = V_LDS ? 3 : 2;
+            const char* Vw = reinterpret_cast<const char*>(Vl) + 32 * w * 2 * DP;  // this wave's 32 V rows
             struct Ops { bf16x8 q, g, v; };
             auto sread = [&](int c) {
-                const int col = 16 * c + 8 * hh;
                 Ops o;
-                o.q = *reinterpret_cast<const bf16x8*>(Qb + tile_off<CPR, SWZ_DUAL>(n, col));
-                o.g = *reinterpret_cast<const bf16x8*>(Gb + tile_off<CPR, SWZ_DUAL>(n, col));
-                if constexpr (V_LDS)
-                    o.v = *reinterpret_cast<const bf16x8*>(Vl + tile_off<CPR, SWZ_ROW>(32 * w + n, col));
+                o.q = *reinterpret_cast<const bf16x8*>(Qb + ln.row(0, c));
+                o.g = *reinterpret_cast<const bf16x8*>(Qb + 2 * QTB + ln.row(0, c));
+                if constexpr (V_LDS) o.v = *reinterpret_cast<const bf16x8*>(Vw + ln.row(0, c));
                 return o;
             };
             Ops ring[PF];
@@ -230,65 +292,82 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
             for (int c = 0; c < NC; ++c) {
                 const Ops o = ring[c % PF];
                 if (c + PF < NC) ring[c % PF] = sread(c + PF);
-                s = mfma_bf16(o.q, kf[c], s);
+                mm_score<ASM>(s, o.q, kf[c], c == 0);
                 if constexpr (V_LDS)
-                    dp = mfma_bf16(o.g, o.v, dp);
+                    mm_score<ASM>(dp, o.g, o.v, c == 0);
                 else
-                    dp = mfma_bf16(o.g, vf[c], dp);
+                    mm_score<ASM>(dp, o.g, vf[c], c == 0);
                 // next block's loads, one per step, behind this step's MFMAs
                 if (c < NPARTS) issue_part(pend, c);
             }
 #pragma unroll
             for (int j = NC; j < NPARTS; ++j) issue_part(pend, j);
+            if constexpr (ASM) mfma_v_drain(s, dp);
         }
         // lane column n = key; register r = query qb + row_of_reg(r, hh)
-        const bool need_mask = wave_uniform(!vis.all(qb, qb + 31, wkey0, wkey0 + 31));
-        // this lane's key is seen by rows qb + [r_lo, r_hi)
-        const int r_lo = need_mask ? vis.rlo(key) - qb : -64, r_hi = need_mask ? vis.rhi(key) - qb : 64;
+        float lse_r[16], dlt_r[16];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const f32x4 l4 = *reinterpret_cast<const f32x4*>(stt + 8 * g + 4 * hh);
             const f32x4 d4 = *reinterpret_cast<const f32x4*>(stt + 32 + 8 * g + 4 * hh);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = 4 * g + i;
-                float p = fast_exp2(s[r] * a.scale_log2 - l4[i]);
-                const int rr = 8 * g + 4 * hh + i;
-                p = (rr < r_lo || rr >= r_hi) ? 0.f : p;
-                dp[r] = p * (dp[r] - d4[i]);
-                s[r] = p;
+            for (int i2 = 0; i2 < 4; ++i2) {
+                lse_r[4 * g + i2] = l4[i2];
+                dlt_r[4 * g + i2] = d4[i2];
             }
         }
-#pragma unroll 1
-        for (int e = 0; e < 2; ++e) {
-            bf16x8 pb, db;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = fast_exp2(s[r] * a.scale_log2 - lse_r[r]);
+        if (wave_uniform(!vis.all(qb, qb + 31, wkey0, wkey0 + 31))) {
+            // this lane's key is seen by rows qb + [r_lo, r_hi); the bounds
+            // pass through an asm statement inside the branch so that the
+            // selects stay in it (blocks without masked pairs skip them)
+            int r_lo = vis.rlo(key) - qb, r_hi = vis.rhi(key) - qb;
+            asm volatile("" : "+v"(r_lo), "+v"(r_hi));
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int rr = row_of_reg(r, hh);
+                s[r] = (rr < r_lo || rr >= r_hi) ? 0.f : s[r];
+            }
+        }
+        bf16x8 pb[2], db[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                pb[j] = (bf16)s[8 * e + j];
-                db[j] = (bf16)dp[8 * e + j];
+                const int r = 8 * e + j;
+                pb[e][j] = (bf16)s[r];
+                db[e][j] = (bf16)(s[r] * (dp[r] - dlt_r[r]));
             }
-            // dV^T += dO^T P (even steps) and dK^T += Q^T dS (odd steps); the
-            // transposed A operands come two ds_read_b64_tr_b16 per step.
-            const int r0 = 16 * e + 4 * hh + (i16 >> 2);
-            constexpr int NI = 2 * NDT;
-            auto tread = [&](int it) {
-                const bf16* t = (it & 1) ? Qb : Gb;
-                const int col = 32 * (it >> 1) + 16 * nh + 4 * (i16 & 3);
-                const bf16x4 lo = ds_read_tr4(t + tile_off<CPR, SWZ_DUAL>(r0, col));
-                const bf16x4 hi = ds_read_tr4(t + tile_off<CPR, SWZ_DUAL>(r0 + 8, col));
-                return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        // dV^T += dO^T P (even steps) and dK^T += Q^T dS (odd steps); the
+        // transposed A operands come two ds_read_b64_tr_b16 per step, their
+        // halves through rings of their own (see the forward).
+        {
+            constexpr int NI = 4 * NDT;  // (e, dt, operand)
+            auto tread = [&](int it, int hi) {
+                const int e = it / (2 * NDT), dt = (it / 2) % NDT;
+                const char* t = (it & 1) ? Qb : Qb + 2 * QTB;
+                return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(t + ln.trn(0, e, dt, hi)));
             };
-            bf16x8 ring[PF];
+            v4i16 rl[PF], rh[PF];
 #pragma unroll
-            for (int it = 0; it < PF; ++it) ring[it] = tread(it);
+            for (int it = 0; it < PF; ++it) {
+                rl[it] = tread(it, 0);
+                rh[it] = tread(it, 1);
+            }
 #pragma unroll
             for (int it = 0; it < NI; ++it) {
-                const bf16x8 av = ring[it % PF];
-                if (it + PF < NI) ring[it % PF] = tread(it + PF);
+                const bf16x8 av =
+                    __builtin_bit_cast(bf16x8, __builtin_shufflevector(rl[it % PF], rh[it % PF], 0, 1, 2, 3, 4, 5, 6, 7));
+                if (it + PF < NI) {
+                    rl[it % PF] = tread(it + PF, 0);
+                    rh[it % PF] = tread(it + PF, 1);
+                }
+                const int e = it / (2 * NDT), dt = (it / 2) % NDT;
                 if (it & 1)
-                    dk[it >> 1] = mfma_bf16(av, db, dk[it >> 1]);
+                    dk[dt] = mfma_bf16(av, db[e], dk[dt]);
                 else
-                    dv[it >> 1] = mfma_bf16(av, pb, dv[it >> 1]);
+                    dv[dt] = mfma_bf16(av, pb[e], dv[dt]);
             }
             pin_read_ahead<NI, PF, 2>();
         }
@@ -330,19 +409,18 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
     }
 }
 
-template <int DP, bool CAUSAL, bool STRIDED>
+template <int DP, bool CAUSAL, bool STRIDED, bool FAST>
 __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int unit, int b, int h) {
+    typedef BwdFastLds<DP> L;
     constexpr int NT = 256, BN = 64, BM = 128, CPR = DP / 8, NC = DP / 16, NDT = DP / 32, NKK = BN / 32;
-    constexpr int TILE = BN * DP;
+    constexpr int KTB = L::KT * 2;  // bytes of one K or V tile
     constexpr int PER = BN * CPR / NT;  // loads per thread of a K (V) tile: the K tile's are spread
                                         // over the S/dP steps of kk = 0, the V tile's over kk = 1
     static_assert(NKK == 2, "one tile's loads per 32-key block");
-    constexpr int BUF = BwdFastLds<DP>::Q_BUF;
-    constexpr int PF = 4;  // LDS operand prefetch depth
+    constexpr bool ASM = DP >= 256;
+    constexpr int PF = 2;  // LDS operand prefetch depth
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
-    const int i16 = lane & 15, nh = (lane >> 4) & 1;
-    const int wu = wave_id();
     const int S = a.S, D = a.D, W = a.window;
     const KeyVis vis = key_vis(a, b, CAUSAL);
     const int hk = h / a.group;
@@ -351,6 +429,11 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
     const bf16* Q = (const bf16*)a.q + op_base<STRIDED>(a.sq, b, h, a.Hq, S, D);
     const bf16* G = (const bf16*)a.dO + op_base<STRIDED>(a.sdo, b, h, a.Hq, S, D);
     const int lk = op_ld<STRIDED>(a.sk, D), lv = lk;  // one K/V sequence stride, as in dkdv_fast_body
+    BwdLane<DP> ln;
+    ln.init(lane);
+    const uint32_t smem_addr = lds_addr(smem);
+    TileDma<DP, BN, NT, SWZ_DUAL> dmk;
+    dmk.init(lane, wave_id(), lk);
 
     // This unit's chunk of the flattened (query tile, key tile) iterations.
     const int64_t g0 = (int64_t)unit * a.q_chunk;
@@ -371,10 +454,23 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
         }
         return t;
     };
+    // Load j of the K tile (v = 0) or of the V tile (v = 1) of key tile ktn
+    // into buffer par.
+    auto issue_kv = [&](int v, int ktn, int par, int j) {
+        if (v)
+            issue_tile_j<FAST, DP, BN, NT, SWZ_DUAL>(dmk, Vg, ktn * BN, S, D, lv, smem + (2 + par) * L::KT,
+                                                     smem_addr + 2u * (2 + par) * L::KT, j);
+        else
+            issue_tile_j<FAST, DP, BN, NT, SWZ_DUAL>(dmk, K, ktn * BN, S, D, lk, smem + par * L::KT,
+                                                     smem_addr + 2u * par * L::KT, j);
+    };
     {
         const int kt0 = next_key_tile();
-        issue_tile<DP, BN, NT, SWZ_DUAL>(K, kt0 * BN, S, D, lk, smem);
-        issue_tile<DP, BN, NT, SWZ_ROW>(Vg, kt0 * BN, S, D, lv, smem + TILE);
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            issue_kv(0, kt0, 0, j);
+            issue_kv(1, kt0, 0, j);
+        }
     }
 
     bf16x8 qf[NC], gf[NC];
@@ -404,93 +500,83 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
       // Iterations of query tile qt inside this unit, then its dQ store.
       const int seg_end = (int)min((int64_t)niter, qstart + qn - g0);
       for (; i < seg_end; ++i) {
-        const bf16* Kb = smem + (i & 1) * BUF;
-        const bf16* Vb = Kb + TILE;
+        const int par = i & 1;
+        const char* Kb = reinterpret_cast<const char*>(smem) + par * KTB;  // K tile; V tile at + 2 KTB
         wait_vmcnt<0>();  // see dkdv_fast_body
         lds_barrier();
-        // Next key tile's loads (K then V, NPARTS per thread), spread over the
-        // S/dP steps below; the last block re-loads key tile 0 into the idle
-        // buffer so that the schedule has no branch (waited for at the end).
-        bf16* const nbuf = smem + ((i + 1) & 1) * BUF;
+        // Next key tile's loads (K then V, PER each per thread), spread over
+        // the S/dP steps below; the last block re-loads key tile 0 into the
+        // idle buffer so that the schedule has no branch (waited for at the end).
         const int ktn = i + 1 < niter ? next_key_tile() : 0;
-        // Load j of the K tile (v = 0) or of the V tile (v = 1; v may be a
-        // runtime value: the two tiles differ only in source, destination
-        // and swizzle, which are selected without a branch).
-        auto issue_part = [&](int v, int j) {
-            const int m = wu * PER + j, P = m * 64 + lane;
-            const int r = P / CPR, p = P % CPR;
-            const int c = p ^ (v ? swz<CPR, SWZ_ROW>(r) : swz<CPR, SWZ_DUAL>(r));
-            const int gr = min(ktn * BN + r, S - 1);
-            const int col = 8 * c < D ? 8 * c : 0;
-            if constexpr (STRIDED)
-                load_lds_16((v ? Vg : K) + (gr * (v ? lv : lk) + col), (v ? nbuf + TILE : nbuf) + m * 512);
-            else
-                load_lds_16((v ? Vg : K) + (int64_t)gr * D + col, (v ? nbuf + TILE : nbuf) + m * 512);
-        };
         const int kbase = (qlo + (int)(g0 + i - qstart)) * BN;
         const int wrow0 = qt * BM + 32 * w, row = wrow0 + n;
         if (wave_uniform(wrow0 < S && vis.any(wrow0, min(wrow0 + 31, S - 1), kbase, kbase + BN - 1))) {
         const bool need_mask = wave_uniform(!vis.all(wrow0, wrow0 + 31, kbase, kbase + BN - 1));
-#pragma unroll 1
+#pragma unroll
         for (int kk = 0; kk < NKK; ++kk) {
-            f32x16 s = zero16(), dp = zero16();
-            const int r = 32 * kk + n;
+            f32x16 s, dp;
             {
-                // S^T = K Q^T (even steps), dP^T = V dO^T (odd steps)
-                constexpr int NI = 2 * NC;
-                auto aread = [&](int it) {
-                    const int col = 16 * (it >> 1) + 8 * hh;
-                    return (it & 1) ? *reinterpret_cast<const bf16x8*>(Vb + tile_off<CPR, SWZ_ROW>(r, col))
-                                    : *reinterpret_cast<const bf16x8*>(Kb + tile_off<CPR, SWZ_DUAL>(r, col));
+                // S^T = K Q^T and dP^T = V dO^T, one chunk of both per step
+                struct Ops { bf16x8 k, v; };
+                auto aread = [&](int c) {
+                    Ops o;
+                    o.k = *reinterpret_cast<const bf16x8*>(Kb + ln.row(kk, c));
+                    o.v = *reinterpret_cast<const bf16x8*>(Kb + 2 * KTB + ln.row(kk, c));
+                    return o;
                 };
-                bf16x8 ring[PF];
+                Ops ring[PF];
 #pragma unroll
-                for (int it = 0; it < PF; ++it) ring[it] = aread(it);
+                for (int c = 0; c < PF; ++c) ring[c] = aread(c);
 #pragma unroll
-                for (int it = 0; it < NI; ++it) {
-                    const bf16x8 av = ring[it % PF];
-                    if (it + PF < NI) ring[it % PF] = aread(it + PF);
-                    if (it & 1)
-                        dp = mfma_bf16(av, gf[it >> 1], dp);
-                    else
-                        s = mfma_bf16(av, qf[it >> 1], s);
-                    if ((it & 1) && (it >> 1) < PER) issue_part(kk, it >> 1);
+                for (int c = 0; c < NC; ++c) {
+                    const Ops o = ring[c % PF];
+                    if (c + PF < NC) ring[c % PF] = aread(c + PF);
+                    mm_score<ASM>(s, o.k, qf[c], c == 0);
+                    mm_score<ASM>(dp, o.v, gf[c], c == 0);
+                    if (c < PER) issue_kv(kk, ktn, par ^ 1, c);
                 }
 #pragma unroll
-                for (int j = NI / 2; j < PER; ++j) issue_part(kk, j);
+                for (int j = NC; j < PER; ++j) issue_kv(kk, ktn, par ^ 1, j);
+                if constexpr (ASM) mfma_v_drain(s, dp);
             }
-            // lane column n = query row; register r = key kbase + 32kk + row_of_reg(r, hh),
-            // visible iff lo <= row_of_reg(r, hh) <= hi
-            const int hi = need_mask ? vis.hi(row) - kbase - 32 * kk : 64;
-            const int lo = need_mask ? vis.lo(row) - kbase - 32 * kk : -1;
+            // lane column n = query row; register r = key kbase + 32kk + row_of_reg(r, hh)
 #pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                float p = fast_exp2(s[q] * a.scale_log2 - lse2);
-                p = (row_of_reg(q, hh) > hi || row_of_reg(q, hh) < lo) ? 0.f : p;
-                s[q] = p * (dp[q] - dlt);
+            for (int q = 0; q < 16; ++q) s[q] = fast_exp2(s[q] * a.scale_log2 - lse2);
+            if (need_mask) {
+                // visible iff lo <= row_of_reg(r, hh) <= hi; the bounds pass
+                // through an asm statement so that the selects stay in the branch
+                int hi = vis.hi(row) - kbase - 32 * kk, lo = vis.lo(row) - kbase - 32 * kk;
+                asm volatile("" : "+v"(hi), "+v"(lo));
+#pragma unroll
+                for (int q = 0; q < 16; ++q)
+                    s[q] = (row_of_reg(q, hh) > hi || row_of_reg(q, hh) < lo) ? 0.f : s[q];
             }
+            bf16x8 db[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) db[e][j] = (bf16)(s[8 * e + j] * (dp[8 * e + j] - dlt));
             {
                 // dQ^T += K^T dS^T over the two 16-key halves (e) of this block
-                bf16x8 db[2];
-#pragma unroll
-                for (int e = 0; e < 2; ++e)
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) db[e][j] = (bf16)s[8 * e + j];
                 constexpr int NI = 2 * NDT;
-                auto tread = [&](int it) {
-                    const int r0 = 32 * kk + 16 * (it / NDT) + 4 * hh + (i16 >> 2);
-                    const int col = 32 * (it % NDT) + 16 * nh + 4 * (i16 & 3);
-                    const bf16x4 lo = ds_read_tr4(Kb + tile_off<CPR, SWZ_DUAL>(r0, col));
-                    const bf16x4 hi = ds_read_tr4(Kb + tile_off<CPR, SWZ_DUAL>(r0 + 8, col));
-                    return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                auto tread = [&](int it, int hi) {
+                    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_v4i16_t*)(Kb + ln.trn(kk, it / NDT, it % NDT, hi)));
                 };
-                bf16x8 ring[PF];
+                v4i16 rl[PF], rh[PF];
 #pragma unroll
-                for (int it = 0; it < PF; ++it) ring[it] = tread(it);
+                for (int it = 0; it < PF; ++it) {
+                    rl[it] = tread(it, 0);
+                    rh[it] = tread(it, 1);
+                }
 #pragma unroll
                 for (int it = 0; it < NI; ++it) {
-                    const bf16x8 av = ring[it % PF];
-                    if (it + PF < NI) ring[it % PF] = tread(it + PF);
+                    const bf16x8 av = __builtin_bit_cast(
+                        bf16x8, __builtin_shufflevector(rl[it % PF], rh[it % PF], 0, 1, 2, 3, 4, 5, 6, 7));
+                    if (it + PF < NI) {
+                        rl[it % PF] = tread(it + PF, 0);
+                        rh[it % PF] = tread(it + PF, 1);
+                    }
                     dq[it % NDT] = mfma_bf16(av, db[it / NDT], dq[it % NDT]);
                 }
                 pin_read_ahead<NI, PF, 2>();
@@ -499,8 +585,8 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
         } else {
 #pragma unroll
             for (int j = 0; j < PER; ++j) {
-                issue_part(0, j);
-                issue_part(1, j);
+                issue_kv(0, ktn, par ^ 1, j);
+                issue_kv(1, ktn, par ^ 1, j);
             }
         }  // active wave
       }
@@ -541,30 +627,31 @@ template <int DP, bool CAUSAL, bool STRIDED>
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_bf16_fast(BwdArgs a) {
     __shared__ __attribute__((aligned(1024))) bf16 smem[BwdFastLds<DP>::KV_ELEMS];
     const int bh = a.B * a.Hkv, i = (int)blockIdx.x;
-    dkdv_fast_body<DP, CAUSAL, STRIDED>(a, smem, i / bh, (i % bh) / a.Hkv, (i % bh) % a.Hkv);
+    dkdv_fast_body<DP, CAUSAL, STRIDED, false>(a, smem, i / bh, (i % bh) / a.Hkv, (i % bh) % a.Hkv);
 }
 
 template <int DP, bool CAUSAL, bool STRIDED>
 __global__ __launch_bounds__(256) void attn_bwd_dq_bf16_fast(BwdArgs a) {
     __shared__ __attribute__((aligned(1024))) bf16 smem[BwdFastLds<DP>::Q_ELEMS];
     const int bh = a.B * a.Hq, i = (int)blockIdx.x;
-    dq_fast_body<DP, CAUSAL, STRIDED>(a, smem, i / bh, (i % bh) / a.Hq, (i % bh) % a.Hq);
+    dq_fast_body<DP, CAUSAL, STRIDED, false>(a, smem, i / bh, (i % bh) / a.Hq, (i % bh) % a.Hq);
 }
 
 // Both roles in one grid: the first kv_units * B * Hkv workgroups run dK/dV
 // units, the rest dQ units (the units of both are sized to take about equally
-// long, see plan_bwd_fast).
-template <int DP, bool CAUSAL, bool STRIDED>
+// long, see plan_bwd_fast).  FAST: every operand tile is whole (D == DP and S
+// a multiple of 64), so the direct loads take TileDma's precomputed offsets.
+template <int DP, bool CAUSAL, bool STRIDED, bool FAST>
 __global__ __launch_bounds__(256) void attn_bwd_main_bf16_fast(BwdArgs a) {
     __shared__ __attribute__((aligned(1024))) bf16 smem[BwdFastLds<DP>::ELEMS];
     const int nkv = a.kv_units * a.B * a.Hkv;
     const int i = (int)blockIdx.x;
     if (i < nkv) {
         const int bh = a.B * a.Hkv;
-        dkdv_fast_body<DP, CAUSAL, STRIDED>(a, smem, i / bh, (i % bh) / a.Hkv, (i % bh) % a.Hkv);
+        dkdv_fast_body<DP, CAUSAL, STRIDED, FAST>(a, smem, i / bh, (i % bh) / a.Hkv, (i % bh) % a.Hkv);
     } else {
         const int j = i - nkv, bh = a.B * a.Hq;
-        dq_fast_body<DP, CAUSAL, STRIDED>(a, smem, j / bh, (j % bh) / a.Hq, (j % bh) % a.Hq);
+        dq_fast_body<DP, CAUSAL, STRIDED, FAST>(a, smem, j / bh, (j % bh) / a.Hq, (j % bh) % a.Hq);
     }
 }
 
@@ -659,7 +746,29 @@ hipError_t launch_bwd_fast(const AttnShape& s, BwdArgs a, int stages, hipStream_
             hipLaunchKernelGGL((KERNEL<DP, false, false>), GRID, dim3(256), 0, st, a);    \
     } while (0)
     if ((stages & BWD_STAGE_MAIN) == BWD_STAGE_MAIN) {
-        MFT_BWD_LAUNCH(attn_bwd_main_bf16_fast, dim3((unsigned)(pl.kv_units * s.B * s.Hkv + pl.q_units * s.B * s.Hq)));
+        const dim3 grid((unsigned)(pl.kv_units * s.B * s.Hkv + pl.q_units * s.B * s.Hq));
+        if (s.D == DP && s.S % 64 == 0) {
+#define MFT_MAIN_FAST(CAUSAL, STRIDED, FAST) \
+    hipLaunchKernelGGL((attn_bwd_main_bf16_fast<DP, CAUSAL, STRIDED, FAST>), grid, dim3(256), 0, st, a)
+            if (s.causal && strided)
+                MFT_MAIN_FAST(true, true, true);
+            else if (s.causal)
+                MFT_MAIN_FAST(true, false, true);
+            else if (strided)
+                MFT_MAIN_FAST(false, true, true);
+            else
+                MFT_MAIN_FAST(false, false, true);
+        } else {
+            if (s.causal && strided)
+                MFT_MAIN_FAST(true, true, false);
+            else if (s.causal)
+                MFT_MAIN_FAST(true, false, false);
+            else if (strided)
+                MFT_MAIN_FAST(false, true, false);
+            else
+                MFT_MAIN_FAST(false, false, false);
+#undef MFT_MAIN_FAST
+        }
     } else if (stages & BWD_STAGE_DKDV) {
         MFT_BWD_LAUNCH(attn_bwd_dkdv_bf16_fast, dim3((unsigned)(pl.kv_units * s.B * s.Hkv)));
     } else if (stages & BWD_STAGE_DQ) {

@@ -161,6 +161,14 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
 
+// LDS byte address of a __shared__ pointer (wave-uniform where p is).  A
+// generic pointer into LDS carries the LDS offset in its low 32 bits (the
+// high half is the shared aperture), so this is a truncation; an address-space
+// cast would add a null check.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
+}
+
 // global_load_lds_dwordx4: lane l copies 16 bytes from gptr (its own address)
 // to LDS byte address M0 + 16 l, without a VGPR round trip.  Issued as inline
 // asm so that the compiler does not track it as an LDS write: it would
@@ -173,7 +181,7 @@ typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
 // M0 needs one wait state (the s_nop), which the compiler's hazard pass
 // cannot insert inside an asm block.
 __device__ __forceinline__ void load_lds_16(const void* gptr, void* lds_base) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds_base);
+    const uint32_t m0 = lds_addr(lds_base);
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(m0)
                  : "memory", "m0");
 }
@@ -188,10 +196,6 @@ __device__ __forceinline__ void load_lds_16_s(const void* sbase, uint32_t voff, 
                  : "memory", "m0");
 }
 
-// LDS byte address of a __shared__ pointer (wave-uniform where p is).
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const lds_void_t*)p);
-}
 
 // ---------------------------------------------------------------------------
 // v_mfma_f32_32x32x16_bf16 with its accumulator in VGPRs, as inline asm.
@@ -211,6 +215,11 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 //     operands, so nothing that uses them can be scheduled before it.
 // Back-to-back MFMAs accumulating into the same registers need none.  Early
 // clobber keeps the result registers apart from the operands.
+//
+// mfma_v_first also starts every builtin accumulation chain: for the builtin
+// with a literal-zero accumulator the compiler (ROCm 7.2) may place the
+// result registers over the A/B operands, which gave NaN results on gfx950
+// (the scan in tests/test_geometry.py checks the built code for it).
 __device__ __forceinline__ void mfma_v_first(f32x16& c, const bf16x8& a, const bf16x8& b) {
     asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(c) : "v"(a), "v"(b));
 }
@@ -221,6 +230,26 @@ __device__ __forceinline__ void mfma_v_drain(f32x16& c0, f32x16& c1) {
     asm volatile("s_nop 7\n\ts_nop 7" : "+v"(c0), "+v"(c1));
 }
 __device__ __forceinline__ void mfma_v_drain(f32x16& c0) { asm volatile("s_nop 7\n\ts_nop 7" : "+v"(c0)); }
+
+// First chunk of an accumulation chain (accumulator in AGPRs where AGPR,
+// else VGPRs), the rest through the builtins: keeps the result registers
+// apart from the operands (see mfma_v_first).  The chain must continue with
+// at least one builtin MFMA before its result is read.
+template <bool AGPR> __device__ __forceinline__ void mfma_chunk_first(f32x16& c, const bf16x8& a, const bf16x8& b) {
+    if constexpr (AGPR)
+        asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&a"(c) : "v"(a), "v"(b));
+    else
+        mfma_v_first(c, a, b);
+}
+template <bool AGPR> __device__ __forceinline__ void mfma_chunk_first(f32x16& c, const f32x4& a, const f32x4& b) {
+    if constexpr (AGPR)
+        asm volatile("s_nop 1\n\tv_mfma_f32_32x32x2_f32 %0, %1, %2, 0" : "=&a"(c) : "v"(a[0]), "v"(b[0]));
+    else
+        asm volatile("s_nop 1\n\tv_mfma_f32_32x32x2_f32 %0, %1, %2, 0" : "=&v"(c) : "v"(a[0]), "v"(b[0]));
+    c = mfma_f32(a[1], b[1], c);
+    c = mfma_f32(a[2], b[2], c);
+    c = mfma_f32(a[3], b[3], c);
+}
 
 // Wave index in the workgroup as a wave-uniform (scalar) value, for LDS
 // addresses of the direct loads.
@@ -365,22 +394,26 @@ template <int DP, int ROWS, int NT, int SWZ> struct TileDma {
     __host__ __device__ uint32_t voff(int j) const { return lrow + (lx ^ cx(j)); }
 };
 
-// Load j of this thread's share of a tile.  FAST: the tile uses TileDma,
-// which the launch may choose when every tile is whole (D == DP and S a
-// multiple of the tile's rows).  Otherwise issue_tile_part, which clamps rows
-// and columns per lane.
+// Load j of this thread's share of a tile (at lds_tile, LDS byte address
+// lds_tile_addr).  FAST: the tile uses TileDma, which the launch may choose
+// when every tile is whole (D == DP and S a multiple of the tile's rows).
+// Otherwise issue_tile_part, which clamps rows and columns per lane.
 template <bool FAST, int DP, int ROWS, int NT, int SWZ>
 __device__ __forceinline__ void issue_tile_j(const TileDma<DP, ROWS, NT, SWZ>& t, const bf16* __restrict__ src,
-                                             int row0, int S, int D, int ld, bf16* lds_tile, int j) {
+                                             int row0, int S, int D, int ld, bf16* lds_tile, uint32_t lds_tile_addr,
+                                             int j) {
     typedef TileDma<DP, ROWS, NT, SWZ> TD;
     if constexpr (FAST) {
         const int w = wave_id();
-        // wave-uniform: the scalar base of this wave's rows, and M0
+        // wave-uniform: the scalar base of this wave's rows, and M0 (the
+        // tile's LDS byte address, passed as an integer)
         const char* base = reinterpret_cast<const char*>(src + (int64_t)(row0 + TD::row_w(w)) * ld) +
                            (int64_t)(TD::R * j) * ld * 2;
-        const uint32_t m0 = lds_addr(lds_tile) + (uint32_t)(w * TD::PER) * 1024u;
-        asm volatile("s_add_u32 m0, %2, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(t.voff(j)),
-                     "s"(base), "s"(m0), "n"(j * 1024)
+        const uint32_t m0 = lds_tile_addr + (uint32_t)(w * TD::PER) * 1024u;
+        // M0 is set with s_mov (no SCC write inside the asm statement; the
+        // address arithmetic stays with the compiler, which knows SCC).
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(t.voff(j)),
+                     "s"(base), "s"(m0 + (uint32_t)(j * 1024))
                      : "memory", "m0");
     } else {
         issue_tile_part<DP, ROWS, NT, SWZ>(src, row0, S, D, ld, lds_tile, j);

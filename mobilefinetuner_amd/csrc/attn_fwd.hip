@@ -144,11 +144,13 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
         f32x16 s[NKK];
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk) {
-            s[kk] = zero16();
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
                 const V ka = *reinterpret_cast<const V*>(Ks + (32 * kk + n) * L::KSTR + 2 * VEC * c + VEC * hh);
-                s[kk] = mfma_chunk(ka, qf[c], s[kk]);
+                if (c == 0)
+                    mfma_chunk_first<false>(s[kk], ka, qf[c]);  // VGPR-form translation unit
+                else
+                    s[kk] = mfma_chunk(ka, qf[c], s[kk]);
             }
         }
 

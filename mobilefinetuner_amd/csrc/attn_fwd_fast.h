@@ -151,7 +151,10 @@ __device__ __forceinline__ void fwd_tile(const FwdArgs& a, const char* smem, con
         for (int it = 0; it < NI; ++it) {
             const bf16x8 ka = ring[it % PF];
             if (it + PF < NI) ring[it % PF] = kread(it + PF);
-            s[it % NKK] = mfma_bf16(ka, qf[it / NKK], it < NKK ? zero16() : s[it % NKK]);
+            if (it < NKK)
+                mfma_v_first(s[it], ka, qf[0]);
+            else
+                s[it % NKK] = mfma_bf16(ka, qf[it / NKK], s[it % NKK]);
             if ((it & 1) && (it >> 1) < NPARTS) issue_part(it >> 1);
         }
 #pragma unroll
@@ -277,14 +280,16 @@ struct FwdIssue {
     const bf16* K;
     const bf16* V;
     bf16* smem;
+    uint32_t smem_addr;  // LDS byte address of smem
     int lk, lv, nrow, npar;
     __device__ __forceinline__ void operator()(int j) const {
         constexpr int PER = FwdLoads<DP>::PER, TILE = kFwdBN * DP;
         if (j < PER)
-            issue_tile_j<FAST, DP, kFwdBN, 256, SWZ_ROW>(ln.dk, K, nrow, a.S, a.D, lk, smem + npar * TILE, j);
+            issue_tile_j<FAST, DP, kFwdBN, 256, SWZ_ROW>(ln.dk, K, nrow, a.S, a.D, lk, smem + npar * TILE,
+                                                         smem_addr + 2u * npar * TILE, j);
         else
             issue_tile_j<FAST, DP, kFwdBN, 256, SWZ_TR>(ln.dv, V, nrow, a.S, a.D, lv, smem + (2 + npar) * TILE,
-                                                     j - PER);
+                                                        smem_addr + 2u * (2 + npar) * TILE, j - PER);
     }
 };
 
@@ -316,7 +321,7 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_fast(FwdArgs a) {
     const int t0 = fast_q_lo(CAUSAL, a.window, qt);
     const int ntiles = t0 + fast_q_n(S, CAUSAL, a.window, qt);
     {
-        const FwdIssue<DP, FAST> first{a, ln, K, Vg, smem, lk, lv, t0 * BN, 0};
+        const FwdIssue<DP, FAST> first{a, ln, K, Vg, smem, lds_addr(smem), lk, lv, t0 * BN, 0};
 #pragma unroll
         for (int j = 0; j < FwdLoads<DP>::NPARTS; ++j) first(j);
     }
@@ -340,7 +345,7 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_fast(FwdArgs a) {
         // Next tile's loads, spread over this tile's S^T steps; the last
         // tile re-loads tile t0 into the idle buffer (no branch in the
         // schedule; waited for before the end).
-        const FwdIssue<DP, FAST> issue{a, ln, K, Vg, smem, lk, lv, t + 1 < ntiles ? (t + 1) * BN : t0 * BN, par ^ 1};
+        const FwdIssue<DP, FAST> issue{a, ln, K, Vg, smem, lds_addr(smem), lk, lv, t + 1 < ntiles ? (t + 1) * BN : t0 * BN, par ^ 1};
         const int kbase = t * BN;
         if (wave_uniform(wrow0 < S && vis.any(wrow0, min(wrow0 + 31, S - 1), kbase, kbase + BN - 1))) {
             const bool need_mask = wave_uniform(!vis.all(wrow0, wrow0 + 31, kbase, kbase + BN - 1));
@@ -405,7 +410,7 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
         return t;
     };
     {
-        const FwdIssue<DP, FAST> first{a, ln, K, Vg, smem, lk, lv, next_key_tile() * BN, 0};
+        const FwdIssue<DP, FAST> first{a, ln, K, Vg, smem, lds_addr(smem), lk, lv, next_key_tile() * BN, 0};
 #pragma unroll
         for (int j = 0; j < FwdLoads<DP>::NPARTS; ++j) first(j);
     }
@@ -433,7 +438,7 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
             const int par = i & 1;
             wait_vmcnt<0>();  // as in attn_fwd_bf16_fast
             lds_barrier();
-            const FwdIssue<DP, FAST> issue{a, ln, K, Vg, smem, lk, lv, i + 1 < niter ? next_key_tile() * BN : 0, par ^ 1};
+            const FwdIssue<DP, FAST> issue{a, ln, K, Vg, smem, lds_addr(smem), lk, lv, i + 1 < niter ? next_key_tile() * BN : 0, par ^ 1};
             const int kbase = (qlo + (int)(g0 + i - qstart)) * BN;
             if (wave_uniform(wrow0 < S && vis.any(wrow0, min(wrow0 + 31, S - 1), kbase, kbase + BN - 1))) {
                 const bool need_mask = wave_uniform(!vis.all(wrow0, wrow0 + 31, kbase, kbase + BN - 1));

@@ -1,8 +1,10 @@
 // Host check of the fast kernels' precomputed LDS and direct-load offsets: the
-// per-lane closed forms of TileDma (attn_common.h) and FwdLane (attn_fwd_fast.h)
+// per-lane closed forms of TileDma (attn_common.h), FwdLane (attn_fwd_fast.h) and
+// BwdLane (attn_bwd_fast.h)
 // against the swizzled tile addressing they replace (tile_off, and the per-lane
 // address arithmetic of issue_tile_part), for every lane, wave and load.
 #include "attn_fwd_fast.h"
+#include "attn_bwd_fast.h"
 #include <cstdio>
 using namespace mft;
 static int bad = 0;
@@ -37,6 +39,23 @@ template <int DP> void check_fwd() {
     }
   }
 }
+template <int DP> void check_bwd() {
+  constexpr int CPR = DP / 8, NC = DP / 16, NDT = DP / 32;
+  for (int lane = 0; lane < 64; ++lane) {
+    const int n = lane & 31, hh = lane >> 5, i16 = lane & 15, nh = (lane >> 4) & 1;
+    bwd::BwdLane<DP> ln; ln.init(lane);
+    for (int k = 0; k < 4; ++k) for (int c = 0; c < NC; ++c) {
+      const int old_b = 2 * tile_off<CPR, SWZ_DUAL>(32 * k + n, 16 * c + 8 * hh);
+      CHECK(old_b == (int)ln.row(k, c), "bwd row DP%d lane%d k%d c%d: %d vs %d\n", DP, lane, k, c, old_b, (int)ln.row(k, c));
+    }
+    for (int k = 0; k < 2; ++k) for (int e = 0; e < 2; ++e) for (int dt = 0; dt < NDT; ++dt) for (int hi = 0; hi < 2; ++hi) {
+      const int r0 = 32 * k + 16 * e + 4 * hh + (i16 >> 2) + 8 * hi;
+      const int col = 32 * dt + 16 * nh + 4 * (i16 & 3);
+      const int old_b = 2 * tile_off<CPR, SWZ_DUAL>(r0, col);
+      CHECK(old_b == (int)ln.trn(k, e, dt, hi), "bwd tr DP%d lane%d k%d e%d dt%d hi%d: %d vs %d\n", DP, lane, k, e, dt, hi, old_b, (int)ln.trn(k, e, dt, hi));
+    }
+  }
+}
 int main() {
   for (int ld : {64, 128, 256, 1024, 3584}) {
     check_dma<64, 64, SWZ_ROW>(ld); check_dma<64, 64, SWZ_TR>(ld); check_dma<64, 64, SWZ_DUAL>(ld);
@@ -46,6 +65,7 @@ int main() {
     check_dma<64, 128, SWZ_ROW>(ld); check_dma<128, 128, SWZ_ROW>(ld); check_dma<256, 128, SWZ_ROW>(ld);
   }
   check_fwd<64>(); check_fwd<128>(); check_fwd<256>();
+  check_bwd<64>(); check_bwd<128>(); check_bwd<256>();
   printf("%s %d mismatches\n", bad ? "FAIL" : "ok", bad);
   return bad != 0;
 }

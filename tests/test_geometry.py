@@ -33,3 +33,54 @@ def test_precomputed_offsets_match_swizzled_addressing(tmp_path):
                    check=True, capture_output=True, text=True)
     out = subprocess.run([str(exe)], capture_output=True, text=True)
     assert out.returncode == 0 and out.stdout.startswith("ok 0"), out.stdout + out.stderr
+
+
+def _mfma_overlaps(asm_text):
+    """MFMAs whose result registers overlap their A or B operand registers."""
+    import re
+
+    def rng(t):
+        m = re.match(r"([va])\[(\d+):(\d+)\]", t) or re.match(r"([va])(\d+)()$", t)
+        if not m:
+            return None
+        lo = int(m.group(2))
+        return m.group(1), lo, int(m.group(3)) if m.group(3) else lo
+
+    bad = []
+    for line in asm_text.splitlines():
+        m = re.match(r"\s+v_mfma\S*\s+(\S+),\s*(\S+),\s*(\S+),\s*(\S+)", line)
+        if not m:
+            continue
+        d = rng(m.group(1))
+        for src in (rng(m.group(2)), rng(m.group(3))):
+            if d and src and d[0] == src[0] and not (src[2] < d[1] or src[1] > d[2]):
+                bad.append(line.strip())
+    return bad
+
+
+def test_no_mfma_result_overlaps_its_operands(tmp_path):
+    """The compiler (ROCm 7.2) may give an MFMA with a literal-zero
+    accumulator result registers that overlap its A/B operands, which gave
+    NaN gradients on gfx950; the kernels start every chain with the
+    early-clobber form instead.  Compile the attention translation units to
+    assembly, with the build's flags, and check that no MFMA does this."""
+    import concurrent.futures as cf
+    import sys
+    sys.path.insert(0, ROOT)
+    from mobilefinetuner_amd import build as B
+    units = ["attn_fwd.hip", "attn_fwd_fast256.hip", "attn_bwd.hip", "attn_bwd_fast64.hip", "attn_bwd_fast256.hip"]
+
+    def asm(name):
+        out = tmp_path / (name + ".s")
+        cmd = [B.hipcc(), *B.HIP_FLAGS, "-I", os.path.join(ROOT, "include"), "-I", B.CSRC, "--cuda-device-only",
+               "-S", os.path.join(B.CSRC, name), "-o", str(out)]
+        if name in B.VGPR_FORM:
+            cmd[1:1] = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+        subprocess.run(cmd, check=True, capture_output=True, text=True)
+        return out.read_text()
+
+    with cf.ThreadPoolExecutor(len(units)) as ex:
+        texts = list(ex.map(asm, units))
+    bad = [b for t in texts for b in _mfma_overlaps(t)]
+    assert sum(t.count("v_mfma") for t in texts) > 1000
+    assert not bad, bad[:5]
