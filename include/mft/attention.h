@@ -132,6 +132,19 @@ mft_status mft_attn_bwd(const mft_attn_desc* desc, const void* q, const void* k,
                         float* dq, float* dk, float* dv, void* workspace,
                         hipStream_t stream);
 
+/* Backward that allocates nothing and takes no workspace: the same kernels as
+ * mft_attn_bwd, with the workspace in a library-owned device array of a fixed
+ * 128 MiB per GPU (held until the process ends).  Shapes whose backward
+ * workspace (mft_attn_workspace_size) exceeds that return MFT_ERR_UNSUPPORTED
+ * with a message.  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams, other threads) race.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). */
+mft_status mft_attn_bwd_noalloc(const mft_attn_desc* desc, const void* q, const void* k,
+                                const void* v, const void* o, const void* dO, const float* lse,
+                                float* dq, float* dk, float* dv, hipStream_t stream);
+
 /* The backward's stages, as a bit mask for mft_attn_bwd_stage.
  *   DELTA : per-row softmax terms (delta_i = dO_i . O_i) into the workspace
  *   DKDV  : dK and dV

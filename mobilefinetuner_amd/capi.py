@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(_PKG, "lib", "libmft_attn.so")
 
 MFT_OK, MFT_ERR_INVALID_ARG, MFT_ERR_UNSUPPORTED, MFT_ERR_HIP = 0, 1, 2, 3
 MFT_F32, MFT_BF16 = 0, 2
+NOALLOC_SCRATCH_BYTES = 128 << 20  # device scratch of mft_attn_bwd_noalloc, per GPU
 MFT_BWD_DELTA, MFT_BWD_DKDV, MFT_BWD_REDUCE, MFT_BWD_DQ = 1, 2, 4, 8
 MFT_BWD_MAIN, MFT_BWD_ALL = 10, 15
 
@@ -22,7 +23,7 @@ MFT_NORM_NONE, MFT_NORM_GEMMA, MFT_NORM_AFFINE = 0, 1, 2
 
 # Every symbol the headers declare (checked by tests/test_capi.py).
 EXPORTS = (
-    "mft_attn_workspace_size", "mft_attn_fwd", "mft_attn_bwd", "mft_attn_bwd_stage",
+    "mft_attn_workspace_size", "mft_attn_fwd", "mft_attn_bwd", "mft_attn_bwd_stage", "mft_attn_bwd_noalloc",
     "mft_repeat_kv_fwd", "mft_repeat_kv_bwd", "mft_last_error", "mft_version",
     "mft_prologue_fwd", "mft_prologue_workspace_size", "mft_prologue_bwd",
     "mft_lm_ce_workspace_size", "mft_lm_ce_fwd", "mft_lm_ce_bwd", "mft_lm_ce_streaming_fwd",
@@ -100,6 +101,8 @@ def lib():
     L.mft_attn_bwd.argtypes = [C.POINTER(AttnDesc), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
     L.mft_attn_bwd_stage.restype = C.c_int
     L.mft_attn_bwd_stage.argtypes = [C.POINTER(AttnDesc), C.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    L.mft_attn_bwd_noalloc.restype = C.c_int
+    L.mft_attn_bwd_noalloc.argtypes = [C.POINTER(AttnDesc), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
     L.mft_repeat_kv_fwd.restype = C.c_int
     L.mft_repeat_kv_fwd.argtypes = [vp, vp, i64, i64, i64, i64, i64, C.c_int32, vp]
     L.mft_repeat_kv_bwd.restype = C.c_int
@@ -128,7 +131,7 @@ def lib():
     L.mft_lora_bwd.argtypes = [C.POINTER(LoraDesc)] + [vp] * 7
     L.mft_lora_merge.restype = C.c_int
     L.mft_lora_merge.argtypes = [C.POINTER(LoraDesc), vp, C.c_float, vp]
-    if L.mft_version() != 4:
+    if L.mft_version() != 5:
         raise RuntimeError("libmft_attn.so version mismatch")
     _lib = L
     return L
@@ -169,6 +172,10 @@ def attn_bwd(d: AttnDesc, q, k, v, o, dO, lse, dq, dk, dv, workspace, stream) ->
 
 def attn_bwd_stage(d: AttnDesc, stages: int, q, k, v, o, dO, lse, dq, dk, dv, workspace, stream) -> None:
     check(lib().mft_attn_bwd_stage(C.byref(d), int(stages), q, k, v, o, dO, lse, dq, dk, dv, workspace, stream))
+
+
+def attn_bwd_noalloc(d: AttnDesc, q, k, v, o, dO, lse, dq, dk, dv, stream) -> None:
+    check(lib().mft_attn_bwd_noalloc(C.byref(d), q, k, v, o, dO, lse, dq, dk, dv, stream))
 
 
 def repeat_kv_fwd(kv, out, B, Hkv, S, D, r, dtype, stream) -> None:

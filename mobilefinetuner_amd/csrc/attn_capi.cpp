@@ -10,6 +10,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "attn_kernels.h"
@@ -118,11 +119,42 @@ mft_status check_desc(const mft_attn_desc* d, mft::AttnShape* s) {
     return MFT_OK;
 }
 
+// Scratch of mft_attn_bwd_noalloc: the backward workspace (row terms, fp32
+// partial tiles) of callers that cannot allocate.  One copy per GPU, held
+// until the process ends; the host only ever uses its per-device address.
+constexpr size_t kNoAllocScratchBytes = size_t(128) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's copy of `scratch`, looked up once per device (with
+// that device current) on its first use.
+mft_status scratch_for_current_device(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e, "mft_attn_bwd_noalloc: hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(MFT_ERR_UNSUPPORTED, "mft_attn_bwd_noalloc: device index " + std::to_string(dev) +
+                                             " is beyond the " + std::to_string(kMaxDevices) + " supported");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_status(e, "mft_attn_bwd_noalloc: hipGetSymbolAddress(scratch)");
+        if (!p) return fail(MFT_ERR_HIP, "mft_attn_bwd_noalloc: hipGetSymbolAddress(scratch) returned NULL");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return MFT_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
-int mft_version(void) { return 4; }
+int mft_version(void) { return 5; }
 
 const char* mft_last_error(void) { return mft::capi::g_last_error.c_str(); }
 
@@ -168,6 +200,28 @@ mft_status mft_attn_bwd(const mft_attn_desc* desc, const void* q, const void* k,
                         const void* dO, const float* lse, float* dq, float* dk, float* dv, void* workspace,
                         hipStream_t stream) {
     return mft_attn_bwd_stage(desc, MFT_BWD_ALL, q, k, v, o, dO, lse, dq, dk, dv, workspace, stream);
+}
+
+mft_status mft_attn_bwd_noalloc(const mft_attn_desc* desc, const void* q, const void* k, const void* v,
+                                const void* o, const void* dO, const float* lse, float* dq, float* dk, float* dv,
+                                hipStream_t stream) {
+    mft::AttnShape s;
+    const mft_status st = check_desc(desc, &s);
+    if (st != MFT_OK) return st;
+    const size_t need = mft::bwd_layout(s).total;
+    if (need > kNoAllocScratchBytes)
+        return fail(MFT_ERR_UNSUPPORTED,
+                    "mft_attn_bwd_noalloc: this shape needs " + std::to_string(need) +
+                        " bytes of backward workspace, more than the library's fixed scratch of " +
+                        std::to_string(kNoAllocScratchBytes) +
+                        " bytes; call mft_attn_bwd with a workspace of mft_attn_workspace_size bytes");
+    void* ws = nullptr;
+    const mft_status sp = scratch_for_current_device(&ws);
+    if (sp != MFT_OK) return sp;
+    // Every workspace byte the backward reads is written earlier in the same
+    // call (row terms by DELTA, partial tiles by their work units), so
+    // nothing has to start at zero.
+    return mft_attn_bwd_stage(desc, MFT_BWD_ALL, q, k, v, o, dO, lse, dq, dk, dv, ws, stream);
 }
 
 mft_status mft_repeat_kv_fwd(const void* kv, void* out, int64_t B, int64_t Hkv, int64_t S, int64_t D, int64_t r,
