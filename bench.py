@@ -1,26 +1,34 @@
 #!/usr/bin/env python3
 """Benchmark of the fused causal GQA attention fwd+bwd on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c5] [--all-configs]
-                    [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c5] [--headline-only]
+                    [--no-cpu-baseline] [--no-variants]
 
 A step is one forward plus one backward of the attention over the config's
 synthetic batch (inputs resident in HBM).  Prints ONE JSON line.  `value` is
 the algorithmic causal throughput  7*B*H*D*S*(S+1) / step time  in TFLOP/s
 (forward 2 and backward 5 products over the causal triangle with its
-diagonal, per query head).  `variants` adds the same measurement for the
-masks the model graphs use - Gemma's sliding window (c5w512) and right-padded
-batches (c4pad); their flops count the visible (query, key) pairs only - and
-for the [B,S,H,D] operand layout (c5bshd).  `prologue` times the fused q/k
-norm + RoPE pass at the config's q and k shapes against the HBM roofline,
-and `lm_loss` the LM cross-entropy at the Gemma-3-1B head over the config's
-positions (streaming: MFMA roofline; dense logits: HBM roofline); `lora`
-times the LoRA linear layers of Gemma-3-1B's q_proj and gate_proj (bf16 MFMA
-roofline of the products with W).
-The roofline object covers the dominant kernel,
-timed live with HIP events on the stream the kernels run on.  The
-cpu_baseline object times the reference CPU operators (oracle/_ref, compiled
-from the reference sources) on a bounded sample of the same workload.
+diagonal, per query head) of the --config workload (C5 by default).
+
+Also on the line:
+  per_config    every BASELINE config (C1-C5 and the C5 fp32 variant): step
+                time, TFLOP/s, tokens/s, % of the dtype's MFMA peak, and the
+                roofline object of its dominant kernel;
+  saved_bytes   bytes held from forward to backward, measured on both sides:
+                the reference composite graph's MemoryManager bytes, and the
+                drop-in autograd node's device bytes (its allocator) and host
+                bytes (MemoryManager);
+  dropin_step   forward + backward through the finetune_ops drop-in with host
+                tensors in and out (PCIe copies included) at C1, C2 and C5;
+  variants      Gemma's sliding window (c5w512), right-padded batches (c4pad)
+                and the [B,S,H,D] operand layout (c5bshd); their flops count
+                the visible (query, key) pairs only;
+  prologue / lm_loss / lora   the widened-path kernels (HBM or MFMA roofline);
+  cpu_baseline  the reference's own CPU operators (oracle/_ref, compiled from
+                the reference sources) over the config, one (batch, head)
+                slice per host core.
+The roofline objects cover the dominant kernel, timed live with HIP events
+on the stream the kernels run on.
 """
 from __future__ import annotations
 
@@ -81,18 +89,6 @@ def flop_units(c):
     the plain causal mask."""
     lengths = c.get("lengths") or [None] * c["B"]
     return c["Hq"] * c["D"] * 2 * sum(visible_pairs(c["S"], c.get("window", 0), n) for n in lengths)
-
-
-def saved_bytes(c):
-    esz = 2 if c["dtype"] == "bf16" else 4
-    B, Hq, Hkv, S, D = c["B"], c["Hq"], c["Hkv"], c["S"], c["D"]
-    new = esz * (2 * B * Hq * S * D + 2 * B * Hkv * S * D) + 4 * B * Hq * S
-    # Reference: four S x S fp32 tensors per query head stay alive until
-    # backward, plus the transposed and (GQA) repeated K/V copies (the
-    # MemoryManager bytes the reference's composite graph holds between
-    # forward and backward, measured with oracle/_ref's mftref_composite).
-    ref = 4 * B * Hq * S * S * 4 + 2 * B * Hq * S * D * 4 + (2 * B * Hq * S * D * 4 if Hq != Hkv else 0)
-    return new, ref
 
 
 def gpu_leg(cfg_id, steps, warmup):
@@ -381,42 +377,139 @@ def hbm_traffic(cfg_id, kernel):
         return None
 
 
-def cpu_leg(cfg_id):
-    """Reference CPU operators (compiled from the reference sources) on a
-    bounded sample of the workload, fwd+bwd, single-threaded as the reference
-    is: the whole config when it is about 10-30 s of CPU work, else one query
-    head (and, if still too long, a shorter sequence)."""
+def _cpu_share():
+    """Host cores this process may use, capped at one GPU's CPU share (16)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_slice(task):
+    """Worker process: one (batch, query head) slice of a config through the
+    reference composite, forward + Engine backward; returns its seconds."""
+    cfg_id, b, h, S, kind = task
     from oracle import oracle as O
     c = CONFIGS[cfg_id]
-    B, Hq, Hkv, S, D = c["B"], c["Hq"], c["Hkv"], c["S"], c["D"]
-    if 7 * B * Hq * D * S * (S + 1) > 1.6e11:
-        B, Hq, Hkv = 1, 1, 1
-        while 7 * D * S * (S + 1) > 1.2e11:
-            S //= 2
-    q, k, v, dO = O.make_inputs(B, Hq, Hkv, S, D, 4242, c["dtype"], c["do_sigma"])
-    kind = "reference" if O.ref_available() else "port"
-    t0 = time.time()
+    q, k, v, dO = O.make_inputs(1, 1, 1, S, c["D"], 4242 + 97 * b + h, c["dtype"], c["do_sigma"])
     if kind == "reference":
         r = O.ref_composite(q, k, v, dO, scale=c["scale"], causal=True)
-        secs = r["t_fwd"] + r["t_bwd"]
-    else:
-        O.composite(q, k, v, dO, scale=c["scale"], causal=True)
-        secs = time.time() - t0
-    units = B * Hq * D * S * (S + 1)
-    return dict(value=round(7 * units / secs / 1e12, 6), unit="TFLOP/s", cores=1, kind=kind,
-                seconds=round(secs, 3),
-                sample=f"{cfg_id} sample B={B},Hq={Hq},Hkv={Hkv},S={S},D={D}: fp32 composite fwd+bwd "
-                       f"(repeat_kv/transpose/matmul/mul/add-mask/softmax/matmul + Engine backward), "
-                       f"reference sources built pure C++ (no BLAS), 1 thread")
+        return r["t_fwd"] + r["t_bwd"]
+    t0 = time.perf_counter()
+    O.composite(q, k, v, dO, scale=c["scale"], causal=True)
+    return time.perf_counter() - t0
+
+
+def _cpu_saved(cfg_id):
+    """Worker process: bytes the reference composite's autograd graph holds
+    from forward to backward (MemoryManager::get_memory_usage() after the
+    forward minus before it, core/memory_manager.h:144) for the whole config."""
+    from oracle import oracle as O
+    c = CONFIGS[cfg_id]
+    q, k, v, _ = O.make_inputs(c["B"], c["Hq"], c["Hkv"], c["S"], c["D"], 4242, c["dtype"], c["do_sigma"])
+    return O.ref_saved_bytes(q, k, v, scale=c["scale"], causal=True)
+
+
+def cpu_leg(cfg_id, saved_cfgs=()):
+    """The reference CPU path on the host's cores, run before the GPU is
+    touched.  The reference operators are single-threaded, so the config is
+    cut into (batch, query head) slices, each run by its own worker process
+    (one core each) through the reference composite built from its own
+    sources; value = the slices' flops / the slowest slice's seconds.  The
+    reference's CMake links BLAS only when find_package(BLAS) finds one
+    (operator/CMakeLists.txt:164-190); this image has none, so the build is
+    its pure-C++ GEMM (DISABLE_BLAS_COMPLETELY, core/ops.cpp:768-794).  Also
+    measures the reference's saved-activation bytes for `saved_cfgs`."""
+    import multiprocessing as mp
+    from oracle import oracle as O
+    c = CONFIGS[cfg_id]
+    B, Hq, S, D = c["B"], c["Hq"], c["S"], c["D"]
+    while 7 * D * S * (S + 1) > 1.5e11:  # keep one slice within ~30 s
+        S //= 2
+    kind = "reference" if O.ref_available() else "port"
+    cores = _cpu_share()
+    slices = [(cfg_id, b, h, S, kind) for b in range(B) for h in range(Hq)]
+    if len(slices) > cores:  # whole rounds of one slice per worker
+        slices = slices[:cores * (len(slices) // cores)]
+    workers = min(cores, len(slices))
+    ctx = mp.get_context("spawn")
+    with ctx.Pool(workers) as pool:
+        t0 = time.perf_counter()
+        secs = pool.map(_cpu_slice, slices, chunksize=1)
+        wall = time.perf_counter() - t0
+        saved = dict(zip(saved_cfgs, pool.map(_cpu_saved, saved_cfgs, chunksize=1))) if kind == "reference" else {}
+    busiest = max(secs) if len(slices) <= workers else wall
+    flops = 7.0 * D * S * (S + 1) * len(slices)
+    return dict(value=round(flops / busiest / 1e12, 6), unit="TFLOP/s", cores=workers, kind=kind,
+                seconds=round(busiest, 3), cpu_seconds=round(sum(secs), 3), wall_seconds=round(wall, 3),
+                nproc=os.cpu_count(), cpu_share=cores, cpu_model=_cpu_model(), blas="none (pure C++ GEMM)",
+                sample=f"{cfg_id}: {len(slices)} (batch, query head) slices of S={S}, D={D}, one per worker "
+                       f"process: fp32 reference composite fwd+bwd (transpose/matmul/mul/add-mask/softmax/"
+                       f"matmul + Engine backward; a slice has one kv head, so no repeat_kv), reference "
+                       f"sources built pure C++ (no BLAS in the image), 1 thread per slice"), saved
+
+
+DROPIN_PROBE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "mobilefinetuner_amd", "adapter", "_dropin",
+                            "dropin_probe")
+
+
+def dropin_probe(mode, cfg_id, *extra):
+    """Run the drop-in probe (reference API over the HIP kernels, host tensors
+    in and out) as a child process; its JSON object, or None when the drop-in
+    is not built."""
+    import subprocess
+    if not os.path.exists(DROPIN_PROBE):
+        return None
+    c = CONFIGS[cfg_id]
+    cmd = [DROPIN_PROBE, mode, *(str(c[x]) for x in ("B", "Hq", "Hkv", "S", "D")), c["dtype"], *map(str, extra)]
+    res = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+    if res.returncode != 0:
+        raise RuntimeError(f"dropin_probe {mode} {cfg_id} failed: {res.stderr[-2000:]}")
+    return json.loads(res.stdout.strip().splitlines()[-1])
+
+
+def roofline_of(cfg_id, r):
+    """Roofline object of a config's dominant kernel: the longer of the
+    forward and the backward's main launch (dK/dV and dQ work units in one
+    grid); achieved = its algorithmic flops / its measured launch time.
+    Algorithmic work per launch in causal contraction units (D*S*(S+1) per
+    query head): forward 2 (QK^T, PV; the forward call also holds the small
+    partial-merge launch); backward main 5 (QK^T recompute, dO V^T, P^T dO,
+    dS^T Q, dS K) - the dQ units' second QK^T and dO V^T recomputes are not
+    counted."""
+    c = CONFIGS[cfg_id]
+    peak = PEAK_TFLOPS[c["dtype"]]
+    kern = {"attn_fwd": (r["fwd_ms"], 2), "attn_bwd_main": (r["main_ms"], 5)}
+    dom = max(kern, key=lambda k: kern[k][0])
+    ach = kern[dom][1] * r["units"] / (kern[dom][0] * 1e-3) / 1e12
+    traffic = hbm_traffic(cfg_id, dom)
+    out = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s",
+           "frac": round(ach / peak, 4), "traffic": traffic}
+    if traffic:
+        out["hbm_GBps"] = round(traffic / (kern[dom][0] * 1e-3) / 1e9, 1)
+    return out
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="c5", choices=sorted(CONFIGS))
-    ap.add_argument("--all-configs", action="store_true", help="also report every config (extra key)")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="skip the per_config report (C1-C5, C5 fp32) and measure the --config workload only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-variants", action="store_true", help="skip the mask and layout variants (variants key)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -434,23 +527,19 @@ def main():
         return
 
     c = CONFIGS[args.config]
+    per_ids = () if args.headline_only else ("c1", "c2", "c3", "c4", "c5", "c5f32")
+    cpu, ref_saved = None, {}
+    if not args.no_cpu_baseline:  # before the GPU is touched: it spawns worker processes
+        saved_ids = sorted({args.config, *(i for i in per_ids if i != "c5f32")})
+        cpu, ref_saved = cpu_leg(args.config, saved_ids)
+        if "c5" in ref_saved:  # the reference composite runs fp32 for either input rounding
+            ref_saved.setdefault("c5f32", ref_saved["c5"])
+
     r = gpu_leg(args.config, args.steps, args.warmup)
     units = r["units"]
     peak = PEAK_TFLOPS[c["dtype"]]
     tflops = 7 * units / (r["step_ms"] * 1e-3) / 1e12
-    # Dominant kernel: the longer of the forward and the backward's main
-    # launch (dK/dV and dQ work units in one grid); achieved = its algorithmic
-    # flops / its measured launch time.  Algorithmic work per launch in causal
-    # contraction units (D*S*(S+1) per query head): forward 2 (QK^T, PV; the
-    # forward call also holds the small partial-merge launch); backward main 5
-    # (QK^T recompute, dO V^T, P^T dO, dS^T Q, dS K) - the dQ units' second
-    # QK^T and dO V^T recomputes are not counted.
-    kern = {"attn_fwd": (r["fwd_ms"], 2), "attn_bwd_main": (r["main_ms"], 5)}
-    dom = max(kern, key=lambda k: kern[k][0])
-    ach = kern[dom][1] * units / (kern[dom][0] * 1e-3) / 1e12
     fwd_tf = 2 * units / (r["fwd_ms"] * 1e-3) / 1e12
-    new_b, ref_b = saved_bytes(c)
-    traffic = hbm_traffic(args.config, dom)
     out = {
         "metric": METRIC,
         "value": round(tflops, 3),
@@ -476,10 +565,44 @@ def main():
         "bwd_main_ms": round(r["main_ms"], 5),
         "fwd_tflops": round(fwd_tf, 2),
         "bwd_tflops": round(5 * units / (r["bwd_ms"] * 1e-3) / 1e12, 2),
-        "saved_bytes": {"new": new_b, "reference": ref_b, "ratio": round(ref_b / new_b, 1)},
-        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(ach, 2), "peak": peak,
-                     "unit": "TFLOP/s", "frac": round(ach / peak, 4), "traffic": traffic},
+        "roofline": roofline_of(args.config, r),
     }
+    per = {}
+    for cid in per_ids:
+        cc = CONFIGS[cid]
+        rr = r if cid == args.config else gpu_leg(cid, max(10, args.steps // 2), 5)
+        u = rr["units"]
+        tf = 7 * u / (rr["step_ms"] * 1e-3) / 1e12
+        per[cid] = {"workload": cc["name"], "dtype": cc["dtype"], "ms_per_step": round(rr["step_ms"], 5),
+                    "fwd_ms": round(rr["fwd_ms"], 5), "bwd_ms": round(rr["bwd_ms"], 5),
+                    "bwd_main_ms": round(rr["main_ms"], 5), "tflops": round(tf, 2),
+                    "pct_peak": round(100 * tf / PEAK_TFLOPS[cc["dtype"]], 2),
+                    "tokens_per_s": round(cc["B"] * cc["S"] / (rr["step_ms"] * 1e-3), 1),
+                    "roofline": roofline_of(cid, rr)}
+    if per:
+        out["per_config"] = per
+    # Saved-activation bytes, measured on both sides: the reference composite
+    # graph's MemoryManager bytes, and the drop-in's autograd node (device
+    # bytes from its allocator, host bytes from MemoryManager).
+    saved = {}
+    for cid in sorted({args.config, *per_ids}):
+        ent = {"reference": ref_saved.get(cid)}
+        d = dropin_probe("saved", cid)
+        if d is not None:
+            ent.update(dropin_device=d["device_bytes"], dropin_host=d["host_bytes"])
+            if ent["reference"]:
+                ent["ratio"] = round(ent["reference"] / (d["device_bytes"] + d["host_bytes"]), 1)
+        saved[cid] = ent
+    out["saved_bytes"] = saved
+    # The PCIe-inclusive step through the drop-in (host tensors in, host
+    # gradients out, reference Engine), steady state with cached device memory.
+    pcie = {}
+    for cid in ("c1", "c2", args.config):
+        d = dropin_probe("step", cid, 2, 5)
+        if d is not None:
+            pcie[cid] = d
+    if pcie:
+        out["dropin_step"] = pcie
     variants = {}
     for cid in () if args.no_variants else ("c5w512", "c4pad", "c5bshd"):
         cc = CONFIGS[cid]
@@ -498,24 +621,10 @@ def main():
         out["prologue"] = prologue_leg(args.config, max(20, args.steps), 5)
         out["lm_loss"] = lm_loss_leg(args.config, 5, 2)
         out["lora"] = lora_leg(args.config, 20, 3)
-    if args.all_configs:
-        per = {}
-        for cid in ("c1", "c2", "c3", "c4", "c5", "c5f32"):
-            cc = CONFIGS[cid]
-            rr = gpu_leg(cid, max(10, args.steps // 2), 5)
-            u = rr["units"]
-            tf = 7 * u / (rr["step_ms"] * 1e-3) / 1e12
-            nb, rb = saved_bytes(cc)
-            per[cid] = {"ms_per_step": round(rr["step_ms"], 5), "fwd_ms": round(rr["fwd_ms"], 5),
-                        "bwd_ms": round(rr["bwd_ms"], 5), "tflops": round(tf, 2),
-                        "pct_peak": round(100 * tf / PEAK_TFLOPS[cc["dtype"]], 2),
-                        "tokens_per_s": round(cc["B"] * cc["S"] / (rr["step_ms"] * 1e-3), 1),
-                        "saved_bytes_new": nb, "saved_bytes_ref": rb}
-        out["per_config"] = per
     if args.copy_calibration:
         copy_calibration()
-    if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_leg(args.config)
+    if cpu is not None:
+        out["cpu_baseline"] = cpu
     print(json.dumps(out), flush=True)
 
 

@@ -1,8 +1,9 @@
 // Host-side device plumbing shared by the finetune_ops drop-in adapters
 // (memory_efficient_attention_hip.cpp, lora_linear_hip.cpp, lm_loss_hip.cpp):
 // error checks that throw std::runtime_error with the operator's name, one
-// process-wide HIP stream at default priority, an owning device buffer, and
-// copies between the reference's host tensors and device memory.
+// process-wide HIP stream at default priority, a caching device allocator
+// behind an owning device buffer, and copies between the reference's host
+// tensors and device memory.
 #ifndef MFT_DROPIN_DEVICE_H
 #define MFT_DROPIN_DEVICE_H
 
@@ -11,6 +12,7 @@
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include <hip/hip_runtime.h>
@@ -39,15 +41,93 @@ inline hipStream_t stream() {
     return s;
 }
 
-// Device memory owned by one adapter object (freed with it).
+// Caching device allocator of the adapters.  A request is rounded up to a
+// size class; a released block goes onto its class's free list and the next
+// request of that class takes it, so a training loop's per-step buffers
+// (saved operands, gradients, workspaces) stop costing a hipMalloc/hipFree
+// pair per buffer per call.  Blocks are reused without waiting: every
+// adapter enqueues all of its device work on the one stream(), so work that
+// touches a reused block is ordered after the stream's earlier uses of it.
+// Cached blocks are returned to the device only when a hipMalloc fails (after
+// draining the stream) and are otherwise held until the process ends.
+class DevicePool {
+public:
+    static DevicePool& instance() {
+        static DevicePool* pool = new DevicePool();  // never destroyed: HIP may be torn down first
+        return *pool;
+    }
+
+    // Bytes of the class a request of `bytes` is served from: multiples of
+    // 4 KiB up to 1 MiB, then quarter steps between powers of two (at most
+    // 25% rounding).
+    static size_t size_class(size_t bytes) {
+        if (bytes <= (size_t(1) << 20)) return (bytes + 4095) & ~size_t(4095);
+        size_t p = size_t(1) << 20;
+        while (p * 2 < bytes) p *= 2;
+        const size_t step = p / 4;
+        return (bytes + step - 1) / step * step;
+    }
+
+    void* get(size_t bytes) {
+        const size_t cls = size_class(bytes);
+        std::lock_guard<std::mutex> lock(mu_);
+        auto& fl = free_[cls];
+        void* p = nullptr;
+        if (!fl.empty()) {
+            p = fl.back();
+            fl.pop_back();
+            cached_ -= cls;
+        } else {
+            hipError_t e = hipMalloc(&p, cls);
+            if (e == hipErrorOutOfMemory && cached_) {
+                (void)hipGetLastError();
+                release_cached_locked();
+                e = hipMalloc(&p, cls);
+            }
+            hip_check("drop-in", e, "hipMalloc");
+            ++mallocs_;
+        }
+        live_ += cls;
+        return p;
+    }
+
+    void put(void* p, size_t bytes) {
+        const size_t cls = size_class(bytes);
+        std::lock_guard<std::mutex> lock(mu_);
+        free_[cls].push_back(p);
+        live_ -= cls;
+        cached_ += cls;
+    }
+
+    size_t live_bytes() {
+        std::lock_guard<std::mutex> lock(mu_);
+        return live_;
+    }
+    size_t cached_bytes() {
+        std::lock_guard<std::mutex> lock(mu_);
+        return cached_;
+    }
+    size_t device_mallocs() {
+        std::lock_guard<std::mutex> lock(mu_);
+        return mallocs_;
+    }
+
+private:
+    void release_cached_locked();
+    std::mutex mu_;
+    std::unordered_map<size_t, std::vector<void*>> free_;
+    size_t live_ = 0, cached_ = 0, mallocs_ = 0;
+};
+
+// Device memory owned by one adapter object (back to the pool with it).
 class DeviceBuffer {
 public:
     DeviceBuffer() = default;
     explicit DeviceBuffer(size_t bytes) : bytes_(bytes) {
-        if (bytes) hip_check("drop-in", hipMalloc(&ptr_, bytes), "hipMalloc");
+        if (bytes) ptr_ = DevicePool::instance().get(bytes);
     }
     ~DeviceBuffer() {
-        if (ptr_) (void)hipFree(ptr_);
+        if (ptr_) DevicePool::instance().put(ptr_, bytes_);
     }
     DeviceBuffer(const DeviceBuffer&) = delete;
     DeviceBuffer& operator=(const DeviceBuffer&) = delete;
@@ -60,6 +140,15 @@ private:
     size_t bytes_ = 0;
 };
 using Buf = std::unique_ptr<DeviceBuffer>;
+
+inline void DevicePool::release_cached_locked() {
+    (void)hipStreamSynchronize(stream());  // the stream may still read freed blocks
+    for (auto& kv : free_) {
+        for (void* p : kv.second) (void)hipFree(p);
+        kv.second.clear();
+    }
+    cached_ = 0;
+}
 
 // n bytes of host memory into a new device buffer (ordered on stream(); the
 // source must stay alive until the stream reaches the copy).

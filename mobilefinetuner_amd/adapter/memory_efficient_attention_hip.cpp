@@ -364,3 +364,13 @@ TensorPtr memory_efficient_attention_masked(const TensorPtr& q, const TensorPtr&
 }
 
 }  // namespace ops
+
+// Counters of the adapters' caching device allocator (dropin_device.h), for
+// measurement harnesses: bytes in live buffers, bytes cached for reuse, and
+// the hipMalloc calls made so far.
+extern "C" void mft_dropin_pool_stats(size_t* live_bytes, size_t* cached_bytes, size_t* device_mallocs) {
+    auto& p = ops::dropin::DevicePool::instance();
+    if (live_bytes) *live_bytes = p.live_bytes();
+    if (cached_bytes) *cached_bytes = p.cached_bytes();
+    if (device_mallocs) *device_mallocs = p.device_mallocs();
+}

@@ -104,6 +104,9 @@ def ref():
                                        C.c_float, C.c_int, opt, opt, opt, opt,
                                        C.POINTER(C.c_double), C.POINTER(C.c_double),
                                        C.POINTER(C.c_int64)]
+        R.mftref_composite_saved.restype = C.c_int
+        R.mftref_composite_saved.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, _i64,
+                                             C.c_float, C.c_int, _f32p, C.POINTER(C.c_int64)]
         R.mftref_memeff_nograd.restype = C.c_int
         R.mftref_memeff_nograd.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64,
                                            C.c_float, C.c_int, _f32p]
@@ -225,6 +228,40 @@ def composite(q, k, v, dO=None, scale=None, causal=True, want_lse=False):
                                   _ptr(o), _ptr(lse), _ptr(dq), _ptr(dk), _ptr(dv))
     if rc != 0:
         raise ValueError("orc_attn_composite rejected its arguments")
+    return dict(o=o, lse=lse, dq=dq, dk=dk, dv=dv)
+
+
+def composite_sliced(q, k, v, dO, scale=None, causal=True, threads=16):
+    """composite() computed one (batch, query head) at a time on `threads`
+    threads, bit-identical to composite() on the whole tensors: every head's
+    arithmetic is independent of the others, and the kv-head gradients are
+    summed over the query heads of their group in head order starting from 0,
+    ((0 + g_0) + g_1) + ..., as RepeatKVHeadsBackward::apply does
+    (core/backward_functions.cpp:693-726).  For the full config sizes."""
+    from concurrent.futures import ThreadPoolExecutor
+    B, Hq, S, D = q.shape
+    Hkv = k.shape[1]
+    r = Hq // Hkv
+
+    def one(bh):
+        b, h = bh
+        g = h // r
+        return composite(q[b:b + 1, h:h + 1], k[b:b + 1, g:g + 1], v[b:b + 1, g:g + 1], dO[b:b + 1, h:h + 1],
+                         scale=scale, causal=causal, want_lse=True)
+
+    jobs = [(b, h) for b in range(B) for h in range(Hq)]
+    with ThreadPoolExecutor(max(1, min(threads, len(jobs)))) as ex:
+        parts = list(ex.map(one, jobs))
+    o = np.empty_like(q, dtype=np.float32)
+    lse = np.empty((B, Hq, S), np.float32)
+    dq = np.empty_like(q, dtype=np.float32)
+    dk = np.zeros(k.shape, np.float32)
+    dv = np.zeros(v.shape, np.float32)
+    for (b, h), p in zip(jobs, parts):
+        g = h // r
+        o[b, h], lse[b, h], dq[b, h] = p["o"][0, 0], p["lse"][0, 0], p["dq"][0, 0]
+        dk[b, g] = dk[b, g] + p["dk"][0, 0]
+        dv[b, g] = dv[b, g] + p["dv"][0, 0]
     return dict(o=o, lse=lse, dq=dq, dk=dk, dv=dv)
 
 
@@ -423,6 +460,23 @@ def ref_composite(q, k, v, dO=None, scale=None, causal=True):
     if rc != 0:
         raise RuntimeError("reference composite raised")
     return dict(o=o, dq=dq, dk=dk, dv=dv, t_fwd=tf.value, t_bwd=tb.value, held_bytes=held.value)
+
+
+def ref_saved_bytes(q, k, v, scale=None, causal=True):
+    """MemoryManager bytes the reference composite's autograd graph holds
+    after its forward (inputs requiring grad; no backward is run)."""
+    B, Hq, S, D = q.shape
+    Hkv = k.shape[1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    q, k, v = (np.ascontiguousarray(t, dtype=np.float32) for t in (q, k, v))
+    o = np.empty_like(q)
+    held = C.c_int64()
+    rc = ref().mftref_composite_saved(q, k, v, B, Hq, Hkv, S, D, float(scale), int(causal), o,
+                                      C.byref(held))
+    if rc != 0:
+        raise RuntimeError("reference composite raised")
+    return held.value
 
 
 def ref_composite_masked(q, k, v, dO=None, scale=None, base_mask=None, pad_mask=None):

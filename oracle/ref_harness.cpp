@@ -53,18 +53,18 @@ extern "C" {
 // Returns 0 on success.  Timings in seconds; held_bytes = MemoryManager bytes
 // in use after the forward minus before it (what the autograd graph keeps
 // alive until backward), the reference's saved-activation measure.
-int mftref_composite(const float* q, const float* k, const float* v, const float* dO,
-                     int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
-                     float scale, int causal,
-                     float* o, float* dq, float* dk, float* dv,
-                     double* t_fwd, double* t_bwd, int64_t* held_bytes) {
+static int composite_impl(const float* q, const float* k, const float* v, const float* dO,
+                          int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
+                          float scale, int causal,
+                          float* o, float* dq, float* dk, float* dv,
+                          double* t_fwd, double* t_bwd, int64_t* held_bytes, bool keep_graph_only) {
     try {
-        const bool grad = dO != nullptr;
+        const bool grad = dO != nullptr || keep_graph_only;
         auto qt = from_host(q, {B, Hq, S, D}, grad);
         auto kt = from_host(k, {B, Hkv, S, D}, grad);
         auto vt = from_host(v, {B, Hkv, S, D}, grad);
         TensorPtr gt;
-        if (grad) gt = from_host(dO, {B, Hq, S, D}, false);
+        if (dO) gt = from_host(dO, {B, Hq, S, D}, false);
         const size_t before = MemoryManager::instance().get_memory_usage();
 
         const double t0 = now_s();
@@ -88,7 +88,7 @@ int mftref_composite(const float* q, const float* k, const float* v, const float
         if (t_fwd) *t_fwd = t1 - t0;
         if (held_bytes) *held_bytes = static_cast<int64_t>(after) - static_cast<int64_t>(before);
 
-        if (grad) {
+        if (dO) {
             const double t2 = now_s();
             autograd::Engine::instance().run_backward({out}, {gt});
             const double t3 = now_s();
@@ -105,6 +105,26 @@ int mftref_composite(const float* q, const float* k, const float* v, const float
         std::cerr << "[mftref_composite] " << e.what() << std::endl;
         return -1;
     }
+}
+
+int mftref_composite(const float* q, const float* k, const float* v, const float* dO,
+                     int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
+                     float scale, int causal,
+                     float* o, float* dq, float* dk, float* dv,
+                     double* t_fwd, double* t_bwd, int64_t* held_bytes) {
+    return composite_impl(q, k, v, dO, B, Hq, Hkv, S, D, scale, causal, o, dq, dk, dv, t_fwd, t_bwd, held_bytes,
+                          false);
+}
+
+// The forward of mftref_composite with inputs that require grad, so that the
+// autograd graph is built, and no backward: held_bytes is what that graph
+// keeps for the backward (the saved-activation figure) at a fraction of the
+// cost of the full step.
+int mftref_composite_saved(const float* q, const float* k, const float* v,
+                           int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
+                           float scale, int causal, float* o, int64_t* held_bytes) {
+    return composite_impl(q, k, v, nullptr, B, Hq, Hkv, S, D, scale, causal, o, nullptr, nullptr, nullptr,
+                          nullptr, nullptr, held_bytes, true);
 }
 
 // The composite with explicit additive masks, as graph/gemma_model.cpp:481-505

@@ -91,6 +91,20 @@ def test_fixtures_record_refcpu_bitwise():
         assert int(z[f"{n}/refcpu_bitwise"]) == 1, n
 
 
+@pytest.mark.parametrize("shape,causal", [((2, 4, 1, 37, 16), True), ((1, 6, 2, 64, 32), False),
+                                          ((2, 3, 3, 20, 8), True), ((1, 7, 1, 33, 64), True)])
+def test_sliced_composite_is_bit_identical(orc, shape, causal):
+    """composite_sliced (one (batch, head) per thread, kv gradients summed in
+    head order) gives the whole-tensor composite's bits, so the full-config
+    GPU parity compares against exactly the restated reference."""
+    B, Hq, Hkv, S, D = shape
+    q, k, v, dO = orc.make_inputs(B, Hq, Hkv, S, D, 9 + S, "f32", 0.5)
+    a = orc.composite(q, k, v, dO, scale=0.3, causal=causal, want_lse=True)
+    b = orc.composite_sliced(q, k, v, dO, scale=0.3, causal=causal, threads=4)
+    for t in ("o", "lse", "dq", "dk", "dv"):
+        assert np.array_equal(_bits(a[t]), _bits(b[t])), t
+
+
 # ------------------------------------------------------- live reference
 def _need_ref(orc):
     if not orc.ref_available():
