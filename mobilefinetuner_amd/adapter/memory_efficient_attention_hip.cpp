@@ -147,7 +147,8 @@ BaseMask classify_mask(const TensorPtr& mask, int64_t S) {
 // (data/wikitext2_dataset.cpp:461-500, data/mmlu_dataset.cpp:285-305).
 struct PadMask {
     std::vector<int32_t> len;
-    float lo = 0.f, hi = -INFINITY;  // range of the masked entries' values
+    float lo = INFINITY, hi = -INFINITY;  // range of the masked entries' values (empty: none masked)
+    bool masks_any() const { return lo <= hi; }
 };
 
 PadMask classify_pad_mask(const TensorPtr& mask, int64_t B, int64_t S) {
@@ -356,7 +357,7 @@ TensorPtr memory_efficient_attention_masked(const TensorPtr& q, const TensorPtr&
     // Rows that see no key follow the reference's -1e10 arithmetic, which the
     // kernels reproduce when a window's and the padding's masked entries
     // carry one value (Gemma: kMaskValue for both, graph/gemma_model.cpp:175).
-    if (bm.kind == MaskKind::kSliding && pad_mask && !(bm.lo == bm.hi && pm.lo == pm.hi && bm.lo == pm.lo))
+    if (bm.kind == MaskKind::kSliding && pm.masks_any() && !(bm.lo == bm.hi && pm.lo == pm.hi && bm.lo == pm.lo))
         throw std::runtime_error(
             "memory_efficient_attention_masked: a sliding window with padding needs one masked value in both masks");
     const bool causal = bm.kind == MaskKind::kCausal || bm.kind == MaskKind::kSliding;

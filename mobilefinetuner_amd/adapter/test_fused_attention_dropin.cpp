@@ -230,6 +230,7 @@ int main() {
         {2, 4, 1, 96, 256, 32, {50, 96}, -1e10f, true},
         {2, 14, 2, 33, 64, 0, {20, 33}, -1e9f, false},     // Qwen: causal + padding
         {2, 2, 1, 24, 32, 0, {0, 24}, -1e9f, false},       // an all-padding sequence
+        {2, 2, 1, 40, 32, 8, {40, 40}, -1e10f, false},     // window + an all-ones attention_mask (pad mask of zeros)
     };
     for (const MCase& c : mcases) {
         const Result r = run_masked_case(c.B, c.Hq, c.Hkv, c.S, c.D, c.window, c.lengths, c.pad_value, c.bf16,
