@@ -8,8 +8,10 @@
 //   * lm_cross_entropy (core/lm_loss.cpp:268-382): the HF shift, ignore_index,
 //     "mean" (NaN with nothing scored), "sum", "sum_debug" (scored like
 //     "sum"; its backward, like "sum"'s, is not normalised) and "none" ([B, S]
-//     per-position NLL) — any other reduction string means "mean", as in the
-//     reference.  The backward node (inputs {logits}) runs mft_lm_ce_bwd.
+//     per-position NLL).  Any other reduction string scores like "mean" but,
+//     as in the reference (LMCrossEntropyBackward normalises only for exactly
+//     "mean", core/lm_loss.cpp:96-100), its backward is not normalised.  The
+//     backward node (inputs {logits}) runs mft_lm_ce_bwd.
 //   * selected_token_lm_cross_entropy / streaming_lm_cross_entropy
 //     (core/lm_loss.cpp:384-481): the loss from hidden and lm_head_weight
 //     without a [B, S, V] logits tensor, "mean" or "sum" only; the backward
@@ -75,6 +77,7 @@ Buf upload_grad_loss(const TensorPtr& grad_output, int64_t n) {
 // The forward's device state, kept by the backward node.
 struct Saved {
     mft_lm_loss_desc desc{};
+    int32_t bwd_reduction = MFT_REDUCE_MEAN;  // the backward's scaling (MEAN: 1 / scored count)
     std::vector<int64_t> in_shape, w_shape;
     Buf x, w, labels, lse;  // x: logits (dense) or hidden (streaming)
     bool grad_x = false, grad_w = false;
@@ -112,7 +115,9 @@ public:
 
     std::vector<TensorPtr> apply(const TensorPtr& grad_output) override {
         if (!s_) throw std::runtime_error("LMCrossEntropyBackwardHip: applied twice");
-        const mft_lm_loss_desc* d = &s_->desc;
+        mft_lm_loss_desc bwd_desc = s_->desc;
+        bwd_desc.reduction = s_->bwd_reduction;
+        const mft_lm_loss_desc* d = &bwd_desc;
         const int64_t n_loss = d->reduction == MFT_REDUCE_NONE ? d->B * d->S : 1;
         Buf g = upload_grad_loss(grad_output, n_loss);
         size_t fwd_ws = 0, bwd_ws = 0;
@@ -177,6 +182,9 @@ TensorPtr lm_cross_entropy(const TensorPtr& logits, const TensorPtr& labels, int
     s->desc.reduction = reduction == "none" ? MFT_REDUCE_NONE
                         : (reduction == "sum" || reduction == "sum_debug") ? MFT_REDUCE_SUM
                                                                            : MFT_REDUCE_MEAN;
+    s->bwd_reduction = reduction == "mean" ? MFT_REDUCE_MEAN
+                       : reduction == "none" ? MFT_REDUCE_NONE
+                                             : MFT_REDUCE_SUM;
     s->in_shape = shape;
     s->x = upload_f32(logits, "lm_cross_entropy");
     s->labels = upload_labels(labels, "lm_cross_entropy");

@@ -143,7 +143,11 @@ void run_selected(const std::string& tag, const Problem& p, const std::string& r
     check(tag + " " + red + " grad_weight", w->grad()->data<float>(), e.dweight, 1e-4);
 }
 
+// Dense lm_cross_entropy.  The reference scores "sum" and "sum_debug" as a
+// sum and any other string but "none" as a mean, and normalises the gradient
+// only for exactly "mean" (core/lm_loss.cpp:96-100, 318-364).
 void run_dense(const std::string& tag, const Problem& p, const std::string& red) {
+    const bool sum_loss = red == "sum" || red == "sum_debug";
     const Expected e = expected(p, red == "mean", 1.0);
     std::vector<float> z(e.logits.begin(), e.logits.end());
     auto logits = std::make_shared<Tensor>(std::vector<int64_t>{p.B, p.S, p.V}, z.data(), kFloat32, kCPU);
@@ -156,7 +160,7 @@ void run_dense(const std::string& tag, const Problem& p, const std::string& red)
         return;
     }
     loss->backward();
-    const std::vector<double> want{red == "mean" ? e.sum / double(e.count) : e.sum};
+    const std::vector<double> want{sum_loss ? e.sum : e.sum / double(e.count)};
     check(tag + " dense " + red + " loss", loss->data<float>(), want, 1e-5);
     check(tag + " dense " + red + " grad_logits", logits->grad()->data<float>(), e.dlogits, 1e-4);
 }
@@ -186,7 +190,7 @@ int main() {
         run_selected("fp32 B2 S37 H64 V20000", a, red);
         run_selected("bf16w B3 S19 H96 V1537", b, red);
     }
-    for (const char* red : {"mean", "sum", "none"}) run_dense("B3 S19 V1537", b, red);
+    for (const char* red : {"mean", "sum", "none", "sum_debug", "avg"}) run_dense("B3 S19 V1537", b, red);
 
     Problem bad = b;
     bad.labels[1] = static_cast<int32_t>(bad.V);

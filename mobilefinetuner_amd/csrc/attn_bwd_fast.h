@@ -659,7 +659,7 @@ __global__ __launch_bounds__(256) void attn_bwd_main_bf16_fast(BwdArgs a) {
 // workgroup per (batch, head, 128-row tile, 16-row group) of the dK/dV role
 // (rows = keys; dK and dV) and then of the dQ role (rows = queries);
 // workgroups of unsplit tiles return at once.
-constexpr int kRedRows = 16, kRedMaxSlots = 64;
+constexpr int kRedRows = 16, kRedMaxSlots = kSplitMaxSlots;
 
 __device__ __forceinline__ void reduce_rows(const float* part, const int64_t* slot_of, int nsl, int64_t tile_elems,
                                             int64_t row_in_tile, int D, float* dst) {

@@ -7,6 +7,7 @@
 // nothing is allocated here.
 #include "mft/attention.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -119,6 +120,30 @@ mft_status check_desc(const mft_attn_desc* d, mft::AttnShape* s) {
     return MFT_OK;
 }
 
+// The split plans keep at most kSplitMaxSlots partial slots per tile (the
+// merge kernels hold the slot list in LDS); a shape whose plan would need
+// more is refused instead of launched.
+mft_status check_fwd_plan(const mft::AttnShape& s, const char* who) {
+    if (mft::fwd_workspace_bytes(s) == 0) return MFT_OK;
+    const mft::FwdPlan p = mft::plan_fwd_split(s);
+    if (p.parts_max > mft::kSplitMaxSlots)
+        return fail(MFT_ERR_UNSUPPORTED, std::string(who) + ": the balanced forward would split a query tile into " +
+                                             std::to_string(p.parts_max) + " parts, more than " +
+                                             std::to_string(mft::kSplitMaxSlots));
+    return MFT_OK;
+}
+
+mft_status check_bwd_plan(const mft::AttnShape& s, const char* who) {
+    if (!mft::bwd_fast_path(s)) return MFT_OK;
+    const mft::BwdPlan p = mft::plan_bwd_fast(s);
+    const int parts = std::max(p.kv_parts_max, p.q_parts_max);
+    if (parts > mft::kSplitMaxSlots)
+        return fail(MFT_ERR_UNSUPPORTED, std::string(who) + ": the backward plan would split a tile into " +
+                                             std::to_string(parts) + " parts, more than " +
+                                             std::to_string(mft::kSplitMaxSlots));
+    return MFT_OK;
+}
+
 // Scratch of mft_attn_bwd_noalloc: the backward workspace (row terms, fp32
 // partial tiles) of callers that cannot allocate.  One copy per GPU, held
 // until the process ends; the host only ever uses its per-device address.
@@ -175,6 +200,10 @@ mft_status mft_attn_fwd(const mft_attn_desc* desc, const void* q, const void* k,
     if (!q || !k || !v || !o) return fail(MFT_ERR_INVALID_ARG, "mft_attn_fwd: q, k, v, o must be non-NULL");
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(lse) || !aligned16(workspace))
         return fail(MFT_ERR_INVALID_ARG, "mft_attn_fwd: buffers must be 16-byte aligned");
+    if (workspace) {
+        const mft_status pl = check_fwd_plan(s, "mft_attn_fwd");
+        if (pl != MFT_OK) return pl;
+    }
     return hip_status(mft::launch_attn_fwd(s, q, k, v, o, lse, workspace, stream), "mft_attn_fwd launch");
 }
 
@@ -192,6 +221,8 @@ mft_status mft_attn_bwd_stage(const mft_attn_desc* desc, int stages, const void*
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(dO) || !aligned16(lse) ||
         !aligned16(dq) || !aligned16(dk) || !aligned16(dv) || !aligned16(workspace))
         return fail(MFT_ERR_INVALID_ARG, "mft_attn_bwd: buffers must be 16-byte aligned");
+    const mft_status pl = check_bwd_plan(s, "mft_attn_bwd");
+    if (pl != MFT_OK) return pl;
     return hip_status(mft::launch_attn_bwd(s, q, k, v, o, dO, lse, dq, dk, dv, workspace, stages, stream),
                       "mft_attn_bwd launch");
 }

@@ -373,9 +373,11 @@ FwdPlan plan_fwd_split(const AttnShape& s) {
     const int64_t min_chunk = std::max<int64_t>(4, (max_tile + kCombMaxSlots - 3) / (kCombMaxSlots - 2));
     p.chunk = (int)std::min<int64_t>(n, std::max<int64_t>(min_chunk, (n + u - 1) / u));
     p.units = (int)((n + p.chunk - 1) / p.chunk);
-    p.any_split = false;
-    for (int t = 0; t < nqt && !p.any_split; ++t)
-        p.any_split = fast_slots(fast_q_start(S, causal, W, t), fast_q_n(S, causal, W, t), p.chunk) > 1;
+    p.parts_max = 1;
+    for (int t = 0; t < nqt; ++t)
+        p.parts_max = std::max(p.parts_max, fast_slots(fast_q_start(S, causal, W, t), fast_q_n(S, causal, W, t),
+                                                       p.chunk));
+    p.any_split = p.parts_max > 1;
     return p;
 }
 

@@ -51,7 +51,7 @@ struct FwdArgs {
 };
 
 constexpr int kFwdBM = 128, kFwdBN = 64;
-constexpr int kCombRows = 16, kCombMaxSlots = 64;
+constexpr int kCombRows = 16, kCombMaxSlots = kSplitMaxSlots;
 
 // The launches of the fast path for one padded head dim (attn_fwd.hip,
 // attn_fwd_fast256.hip).

@@ -45,6 +45,12 @@ bool bwd_fast_path(const AttnShape& s);
 // CU in total, so the causal triangle no longer sets the critical path.  A
 // tile touched by several units gets fp32 partials (at most kv_parts_max /
 // q_parts_max slots) that REDUCE sums in slot order.
+// The most partial slots one split tile may have: REDUCE and the forward
+// combine keep a tile's slot list (and the combine its per-slot weights) in
+// LDS arrays of this length.  The planners size units so that no tile goes
+// past it; the C ABI rejects a shape whose plan would (MFT_ERR_UNSUPPORTED).
+constexpr int kSplitMaxSlots = 64;
+
 struct BwdPlan {
     int kv_chunk, q_chunk;
     int kv_parts_max, q_parts_max;
@@ -70,6 +76,7 @@ int device_cus();
 struct FwdPlan {
     int chunk, units;
     bool any_split;
+    int parts_max;  // most slots of one query tile
 };
 FwdPlan plan_fwd_split(const AttnShape& s);
 // Forward workspace bytes (0 where the forward takes no workspace).  With a

@@ -166,14 +166,8 @@ __global__ __launch_bounds__(256) void lora_rowdot_kernel(LoraRowDot a) {
 // lora_coldot: per chunk c of rows and column k, partial[c][k][j] = sum over
 // the chunk's rows of M[n, k] V[n, j]; one wave per (64 VEC columns, chunk),
 // the row of V is the same for the whole wave.  The chunk height is chosen so
-// that about 2048 waves run (lora_coldot_chunk).  Then lora_coldot_reduce sums
-// the chunks in a fixed order.
-int64_t lora_coldot_chunk(int64_t rows, int64_t K) {
-    const int64_t col_waves = (K + 255) / 256;
-    int64_t chunk = 16;
-    while (chunk < 128 && col_waves * ((rows + chunk - 1) / chunk) > 2048) chunk *= 2;
-    return chunk;
-}
+// that about 2048 waves run (lora_coldot_chunk, lora_kernels.h).  Then
+// lora_coldot_reduce sums the chunks in a fixed order.
 
 template <int VEC>
 __global__ __launch_bounds__(64) void lora_coldot_kernel(LoraColDot a, int64_t chunk) {

@@ -49,6 +49,8 @@ hipError_t launch_lora_rowdot(const LoraRowDot& a, hipStream_t st);
 hipError_t launch_lora_pack_kmajor(const float* P, int64_t pk, int64_t pj, int64_t K, int r, float* dst,
                                    hipStream_t st);
 
+constexpr int64_t kLoraMaxGridY = 65535;  // a launch's grid limit in y (and z)
+
 struct LoraColDot {
     const float* M;        // [rows, K] with leading dimension ldm
     int64_t ldm, rows, K;
@@ -64,5 +66,17 @@ struct LoraColDot {
 // one fixed-order sum over the chunks (deterministic).
 hipError_t launch_lora_coldot(const LoraColDot& a, hipStream_t st);
 int64_t lora_coldot_partial_floats(int64_t rows, int64_t K, int r);
+
+// Rows per chunk of lora_coldot (one grid row, blockIdx.y, per chunk): 16 to
+// 128, doubled while more than about 2048 waves would run, and never so few
+// that the chunk count passes the grid's 65535 limit in y (rows beyond
+// 65535 * 128 = ~8.4M take taller chunks).
+inline int64_t lora_coldot_chunk(int64_t rows, int64_t K) {
+    const int64_t col_waves = (K + 255) / 256;
+    int64_t chunk = 16;
+    while (chunk < 128 && col_waves * ((rows + chunk - 1) / chunk) > 2048) chunk *= 2;
+    const int64_t min_chunk = (rows + kLoraMaxGridY - 1) / kLoraMaxGridY;
+    return chunk > min_chunk ? chunk : min_chunk;
+}
 
 }  // namespace mft

@@ -35,6 +35,38 @@ def test_precomputed_offsets_match_swizzled_addressing(tmp_path):
     assert out.returncode == 0 and out.stdout.startswith("ok 0"), out.stdout + out.stderr
 
 
+def test_lora_coldot_grid_stays_within_launch_limits(tmp_path):
+    """lora_coldot launches one grid row per chunk of rows: past ~8.4M rows the
+    chunks grow so that grid.y stays within 65535 (the C ABI accepts N up to
+    2^31 - 1)."""
+    exe = tmp_path / "lora_grid_check"
+    subprocess.run(["/opt/rocm/bin/hipcc", "-x", "hip", "--offload-arch=gfx950", "--cuda-host-only", "-O1",
+                    "-std=c++17", "-I", os.path.join(ROOT, "mobilefinetuner_amd", "csrc"),
+                    os.path.join(ROOT, "tests", "native", "lora_grid_check.cpp"), "-o", str(exe)],
+                   check=True, capture_output=True, text=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert out.returncode == 0 and out.stdout.startswith("ok"), out.stdout + out.stderr
+
+
+def test_split_plans_stay_within_slot_limit(tmp_path):
+    """The forward and backward split planners never give a tile more
+    partial slots than the merge kernels hold (kSplitMaxSlots), over a sweep
+    of shapes up to S = 2^20, GQA groups, windows and head dims."""
+    lib = os.path.join(ROOT, "mobilefinetuner_amd", "lib")
+    if not os.path.exists(os.path.join(lib, "libmft_attn.so")):
+        import pytest
+        pytest.skip("libmft_attn.so not built")
+    exe = tmp_path / "plan_check"
+    subprocess.run(["/opt/rocm/bin/hipcc", "-x", "hip", "--offload-arch=gfx950", "--cuda-host-only", "-O1",
+                    "-std=c++17", "-I", os.path.join(ROOT, "include"),
+                    "-I", os.path.join(ROOT, "mobilefinetuner_amd", "csrc"),
+                    os.path.join(ROOT, "tests", "native", "plan_check.cpp"), "-o", str(exe),
+                    "-L", lib, "-lmft_attn", f"-Wl,-rpath,{lib}"],
+                   check=True, capture_output=True, text=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, env={**os.environ, "HIP_VISIBLE_DEVICES": ""})
+    assert out.returncode == 0 and out.stdout.startswith("ok"), out.stdout + out.stderr
+
+
 def _mfma_overlaps(asm_text):
     """MFMAs whose result registers overlap their A or B operand registers."""
     import re
