@@ -51,6 +51,10 @@ struct FwdArgs {
 };
 
 constexpr int kFwdBM = 128, kFwdBN = 64;
+// Fewest vector stores a wave issues for a segment's output (32 per lane
+// for D = 256: the fp32 partial O or the bf16 O); smaller head dims use
+// vmcnt(0) (see attn_fwd_bf16_split).
+constexpr int kEpilogueStores = 32;
 constexpr int kCombRows = 16, kCombMaxSlots = kSplitMaxSlots;
 
 // The launches of the fast path for one padded head dim (attn_fwd.hip,
@@ -424,6 +428,9 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
     fwd_load_q<DP>(Q, lq, qt * BM + 32 * w + n, S, D, qf);
     wait_vmcnt<0>();  // Q complete before the loop (direct loads are untracked)
 
+    // After a segment whose outputs this wave stored, the first tile's wait
+    // leaves those stores in flight (see the end of the segment loop).
+    bool stores_in_flight = false;
     for (int i = 0, first = 1;; first = 0) {
 #pragma unroll
         for (int d = 0; d < NDT; ++d) oacc[d] = zero16();
@@ -436,7 +443,17 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
         const int seg_end = (int)min((int64_t)niter, qstart + qn - g0);
         for (; i < seg_end; ++i) {
             const int par = i & 1;
-            wait_vmcnt<0>();  // as in attn_fwd_bf16_fast
+            // This wave's loads of buffer par have landed (as in
+            // attn_fwd_bf16_fast).  Vector memory operations complete in
+            // issue order, and the previous segment's epilogue issued at
+            // least kEpilogueStores stores after this tile's loads and after
+            // the Q reload: waiting until at most that many remain leaves the
+            // stores draining behind this tile's work.
+            if (stores_in_flight)
+                wait_vmcnt<kEpilogueStores>();
+            else
+                wait_vmcnt<0>();
+            stores_in_flight = false;
             lds_barrier();
             const FwdIssue<DP, FAST> issue{a, ln, K, Vg, smem, lds_addr(smem), lk, lv, i + 1 < niter ? next_key_tile() * BN : 0, par ^ 1};
             const int kbase = (qlo + (int)(g0 + i - qstart)) * BN;
@@ -449,12 +466,25 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
                 for (int j = 0; j < FwdLoads<DP>::NPARTS; ++j) issue(j);
             }
         }
-        // End of this unit's part of query tile qt: a tile inside one unit is
-        // written normalised; otherwise this unit's slot gets the unnormalised
-        // partial (O, running max, sum) for attn_fwd_combine.
+        // The next segment's Q rows load first (qf is dead here), so that
+        // they land while this segment's outputs are stored.
+        const bool more = i < niter;
+        const int nsl = fast_slots(qstart, qn, a.chunk);  // of the segment just finished
+        if (more) {
+            ++qt;
+            qstart = fast_q_start(S, CAUSAL, W, qt);
+            qn = fast_q_n(S, CAUSAL, W, qt);
+            qlo = fast_q_lo(CAUSAL, W, qt);
+            fwd_load_q<DP>(Q, lq, qt * BM + 32 * w + n, S, D, qf);
+        }
+        // End of this unit's part of the query tile: a tile inside one unit
+        // is written normalised; otherwise this unit's slot gets the
+        // unnormalised partial (O, running max, sum) for attn_fwd_combine.
+        // Every path below issues at least kEpilogueStores vector stores per
+        // wave whose first row is in range (rows of a wave are all in range
+        // or all out of range when FAST).
         if (wrow0 < S) {
             const float l_tot = l_run + other_half(l_run);
-            const int nsl = fast_slots(qstart, qn, a.chunk);
             if (nsl <= 1) {
                 if (row < S) fwd_store_row<DP>(a, b, h, row, oacc, m_run, l_tot);
             } else if (row < S) {
@@ -473,16 +503,11 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
                 }
             }
         }
-        if (i >= niter) {
+        if (!more) {
             wait_vmcnt<0>();  // the last tile's re-load has landed before the unit ends
             break;
         }
-        ++qt;
-        qstart = fast_q_start(S, CAUSAL, W, qt);
-        qn = fast_q_n(S, CAUSAL, W, qt);
-        qlo = fast_q_lo(CAUSAL, W, qt);
-        fwd_load_q<DP>(Q, lq, qt * BM + 32 * w + n, S, D, qf);
-        wait_vmcnt<0>();
+        stores_in_flight = FAST && DP == 256 && wave_uniform(wrow0 < S);
     }
 }
 
