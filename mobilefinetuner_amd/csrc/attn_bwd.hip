@@ -613,7 +613,7 @@ BwdPlan plan_bwd_fast(const AttnShape& s) {
     const int64_t n_kv = bwd::fast_kv_start(S, causal, W, group, nt);  // iterations per (batch, kv head)
     const int64_t n_q = fast_q_total(S, causal, W);                    // iterations per (batch, query head)
     const int64_t pairs_kv = s.B * s.Hkv, pairs_q = s.B * s.Hq;
-    const int64_t cus = device_cus();
+    const int64_t cus = (int64_t)device_cus() * bwd_wgs_per_cu(s.D);  // resident workgroups
     BwdPlan p;
     // Units no shorter than 4 iterations, and long enough that no tile spans
     // more than 63 units (REDUCE keeps a tile's slot list in LDS, 64 entries).

@@ -364,7 +364,7 @@ FwdPlan plan_fwd_split(const AttnShape& s) {
     const int nqt = (S + kFwdBM - 1) / kFwdBM;
     const int64_t n = fast_q_total(S, causal, W);  // iterations per (batch, head)
     const int64_t pairs = s.B * s.Hq;
-    const int64_t u = balanced_units(pairs, device_cus());
+    const int64_t u = balanced_units(pairs, (int64_t)device_cus() * fwd_wgs_per_cu(s.D));
     FwdPlan p;
     // Units no shorter than 4 key tiles: a split costs one fp32 partial tile.
     // A query tile has at most 2*S/64 key tiles; keep its slots <= kCombMaxSlots.

@@ -69,6 +69,14 @@ BwdLayout bwd_layout(const AttnShape& s);
 // Compute units of the current device (cached; 256 when the query fails).
 int device_cus();
 
+// Workgroups of the bf16 fast kernels that one CU holds at once, which the
+// planners size their launches for.  Registers decide it (LDS allows more):
+// the forward needs at most 256 per lane up to D = 128 and the backward up
+// to D = 64, so two workgroups - two waves per SIMD - share a CU there; the
+// wider kernels keep one wave per SIMD.
+inline int fwd_wgs_per_cu(int64_t D) { return D <= 128 ? 2 : 1; }
+inline int bwd_wgs_per_cu(int64_t D) { return D <= 64 ? 2 : 1; }
+
 // Balanced forward (bf16 fast path): per (batch, head) the iterations
 // (128-row query tile, 64-key tile) are cut into `units` chunks of `chunk`
 // iterations; a query tile split across units leaves fp32 partials in the
