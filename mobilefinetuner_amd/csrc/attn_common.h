@@ -226,6 +226,20 @@ __device__ __forceinline__ void mfma_v_first(f32x16& c, const bf16x8& a, const b
 __device__ __forceinline__ void mfma_v(f32x16& c, const bf16x8& a, const bf16x8& b) {
     asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
 }
+// The first step of a 16x16x32 accumulator chain (srcC = 0), early-clobber
+// like mfma_v_first.
+__device__ __forceinline__ void mfma16_first(f32x4& c, const bf16x8& a, const bf16x8& b) {
+    asm volatile("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=&v"(c) : "v"(a), "v"(b));
+}
+// A 16x16x32 step whose A operand stays live past the instruction, so that
+// its result registers cannot take the A operand's (the compiler would
+// otherwise reuse a dead operand's registers for the result).
+__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+    const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    asm volatile("" ::"v"(a));
+    return d;
+}
+
 __device__ __forceinline__ void mfma_v_drain(f32x16& c0, f32x16& c1) {
     asm volatile("s_nop 7\n\ts_nop 7" : "+v"(c0), "+v"(c1));
 }
@@ -313,7 +327,12 @@ template <int CPR> __host__ __device__ __forceinline__ constexpr int swz_dual(in
     return CPR >= 16 ? (4 * (r & 3) + ((r >> 2) & 3)) : (4 * ((r >> 1) & 1) + ((r >> 2) & 3));
 }
 
-enum { SWZ_ROW = 0, SWZ_TR = 1, SWZ_DUAL = 2 };
+//  swz_tr16: for transposing reads where a wave reads 16 consecutive rows x
+//            32 bytes (ds_read_b64_tr_b16 in the 16x16x32 MFMA layout): rows
+//            r..r+7 land in distinct 32-byte windows (CPR >= 16).
+template <int CPR> __host__ __device__ __forceinline__ constexpr int swz_tr16(int r) { return 2 * (r & 7); }
+
+enum { SWZ_ROW = 0, SWZ_TR = 1, SWZ_DUAL = 2, SWZ_TR16 = 3 };
 
 // Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
 enum { SG_MFMA = 0x008, SG_DS_READ = 0x100 };
@@ -335,7 +354,10 @@ __device__ __forceinline__ void pin_read_ahead() {
 }
 
 template <int CPR, int SWZ> __host__ __device__ __forceinline__ constexpr int swz(int r) {
-    return SWZ == SWZ_ROW ? swz_row<CPR>(r) : SWZ == SWZ_TR ? swz_tr<CPR>(r) : swz_dual<CPR>(r);
+    return SWZ == SWZ_ROW ? swz_row<CPR>(r)
+           : SWZ == SWZ_TR ? swz_tr<CPR>(r)
+           : SWZ == SWZ_TR16 ? swz_tr16<CPR>(r)
+                             : swz_dual<CPR>(r);
 }
 
 // Element offset of (row r, column col) in a swizzled bf16 tile.
