@@ -99,6 +99,59 @@ __device__ __forceinline__ void store_dkdv(const BwdArgs& a, float* dkp, float* 
         }
 }
 
+// A wave's 32-row fp32 accumulator tile in the 32x32 MFMA layout (lane
+// n = l % 32 holds row n; register 4g + i of column tile dt holds column
+// 32dt + 8g + 4hh + i, hh = l / 32), stored row-contiguously through a
+// per-wave LDS staging area of 32 rows x 32*DTR columns (4 KiB x DTR).
+// Stored from the registers directly, each vector store writes 32 rows x 32
+// bytes; after the staging each writes 64 / (8 DTR) whole row runs of
+// 128 DTR bytes.  Row r goes to dst + r*ld for all 32 rows and 32*NDT
+// columns (16-byte aligned rows; callers take another path for partial
+// tiles).  The staging area's 16-byte chunks are XOR-swizzled by row, so
+// that the 32 rows of one register write reach distinct chunks.
+// Wave-local: the caller makes the area free (a barrier, when other waves
+// used it) and keeps other waves out of it until the call returns.
+template <int NDT, int DTR>
+__device__ __forceinline__ void store_acc32_staged(char* stage, float* dst, int64_t ld, const f32x16 (&acc)[NDT],
+                                                   float scale) {
+    static_assert(NDT % DTR == 0 && (DTR == 1 || DTR == 2 || DTR == 4), "staging rounds");
+    constexpr int CPRR = 8 * DTR, RB = 16 * CPRR, RPI = 64 / CPRR;  // chunks, bytes per row; rows per store
+    constexpr int NB = 4;                                            // reads in flight before their stores
+    // The lane's offsets are formed here: left to itself, the compiler hoists
+    // them out of the caller's loops into registers it then has to spill.
+    int lane = threadIdx.x & 63;
+    asm volatile("" : "+v"(lane));
+    const int n = lane & 31, hh = lane >> 5;
+    const int rrow = lane / CPRR, c = lane % CPRR;
+    char* wr = stage + n * RB;
+    const char* rd = stage + rrow * RB;
+    float* out = dst + rrow * ld + 4 * c;
+#pragma unroll
+    for (int r0 = 0; r0 < NDT / DTR; ++r0) {
+        asm volatile("" ::: "memory");  // the last round's reads precede these writes
+#pragma unroll
+        for (int dl = 0; dl < DTR; ++dl)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x16& t = acc[DTR * r0 + dl];
+                const f32x4 v = {t[4 * g] * scale, t[4 * g + 1] * scale, t[4 * g + 2] * scale, t[4 * g + 3] * scale};
+                *reinterpret_cast<f32x4*>(wr + 16 * ((8 * dl + 2 * g + hh) ^ (n & (CPRR - 1)))) = v;
+            }
+        asm volatile("" ::: "memory");  // LDS executes a wave's operations in order
+#pragma unroll
+        for (int k0 = 0; k0 < 32 / RPI; k0 += NB) {
+            f32x4 v[NB];
+#pragma unroll
+            for (int k = 0; k < NB; ++k)
+                v[k] = *reinterpret_cast<const f32x4*>(rd + (k0 + k) * RPI * RB +
+                                                        16 * (c ^ ((RPI * (k0 + k) + rrow) & (CPRR - 1))));
+#pragma unroll
+            for (int k = 0; k < NB; ++k) *reinterpret_cast<f32x4*>(out + (k0 + k) * RPI * ld + 32 * DTR * r0) = v[k];
+        }
+    }
+    asm volatile("" ::: "memory");
+}
+
 // ----------------------------------------------------------------- REDUCE
 // dk = sum over splits of the dK partials (split order), same for dv.  The
 // partials are contiguous [B, Hkv, S, D]; dk, dv follow their layouts.

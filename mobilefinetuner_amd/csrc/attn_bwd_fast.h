@@ -379,13 +379,34 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
       // End of this unit's part of key tile kt: a tile covered by one unit
       // writes dK/dV, otherwise this unit's slot (split_slot): [dK | dV]
       // tiles of 128 key rows.
-      const int key = kt * BNK + 32 * w + n;
-      if (key < S) {
+      const int key0 = kt * BNK + 32 * w;
+      if constexpr (V_LDS && FAST) {
+          // Whole tiles (FAST: D == DP, 16-byte rows, and key0 < S means all
+          // 32 rows are): through LDS (store_acc32_staged), this wave's
+          // quarter of the V tile as its staging area once every wave is done
+          // with V.
+          lds_barrier();
+          if (wave_uniform(key0 < S)) {
+              float* dkp = a.dk + op_base<STRIDED>(a.sdk, b, hk, a.Hkv, S, D) + (int64_t)key0 * op_ld<STRIDED>(a.sdk, D);
+              float* dvp = a.dv + op_base<STRIDED>(a.sdv, b, hk, a.Hkv, S, D) + (int64_t)key0 * op_ld<STRIDED>(a.sdv, D);
+              int64_t ldk = op_ld<STRIDED>(a.sdk, D), ldv = op_ld<STRIDED>(a.sdv, D);
+              if (fast_slots(kstart, kn, a.kv_chunk) > 1) {
+                  const int64_t slot = (int64_t)(b * a.Hkv + hk) * 2 * a.kv_units + 2 * unit + (first ? 0 : 1);
+                  dkp = a.kv_part + (slot * 2 * BNK + 32 * w) * D;
+                  dvp = dkp + BNK * D;
+                  ldk = ldv = D;
+              }
+              char* stage = reinterpret_cast<char*>(Vl) + w * (32 * DP * 2);
+              store_acc32_staged<NDT, 4>(stage, dkp, ldk, dk, a.scale);
+              store_acc32_staged<NDT, 4>(stage, dvp, ldv, dv, 1.f);
+          }
+      } else if (key0 + n < S) {
+          const int key = key0 + n;
           float* dkp = a.dk + op_base<STRIDED>(a.sdk, b, hk, a.Hkv, S, D) + (int64_t)key * op_ld<STRIDED>(a.sdk, D);
           float* dvp = a.dv + op_base<STRIDED>(a.sdv, b, hk, a.Hkv, S, D) + (int64_t)key * op_ld<STRIDED>(a.sdv, D);
           if (fast_slots(kstart, kn, a.kv_chunk) > 1) {
               const int64_t slot = (int64_t)(b * a.Hkv + hk) * 2 * a.kv_units + 2 * unit + (first ? 0 : 1);
-              dkp = a.kv_part + (slot * 2 * BNK + (32 * w + n)) * D;
+              dkp = a.kv_part + (slot * 2 * BNK + key - kt * BNK) * D;
               dvp = dkp + BNK * D;
           }
           store_dkdv<NDT>(a, dkp, dvp, hh, dk, dv);
@@ -592,9 +613,28 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
       }
       // End of this unit's part of query tile qt: a tile covered by one unit
       // writes dQ, otherwise slot (unit - first unit of qt).
-      const int row = qt * BM + 32 * w + n;
-      if (row < S) {
-          float* dqp = a.dq + op_base<STRIDED>(a.sdq, b, h, a.Hq, S, D) + (int64_t)row * op_ld<STRIDED>(a.sdq, D);
+      const int row0 = qt * BM + 32 * w;
+      if constexpr (FAST) {
+          // Whole tiles (FAST: D == DP, 16-byte rows, and row0 < S means all
+          // 32 rows are): through LDS
+          // (store_acc32_staged), the buffer of the segment's last tile is
+          // idle (the next tile streams into the other); waves 0 and 1 stage
+          // in its K tile, waves 2 and 3 in its V tile.
+          lds_barrier();
+          if (wave_uniform(row0 < S)) {
+              float* dqp = a.dq + op_base<STRIDED>(a.sdq, b, h, a.Hq, S, D) + (int64_t)row0 * op_ld<STRIDED>(a.sdq, D);
+              int64_t ldq = op_ld<STRIDED>(a.sdq, D);
+              if (fast_slots(qstart, qn, a.q_chunk) > 1) {
+                  const int64_t slot = (int64_t)(b * a.Hq + h) * 2 * a.q_units + 2 * unit + (first ? 0 : 1);
+                  dqp = a.q_part + (slot * BM + 32 * w) * D;
+                  ldq = D;
+              }
+              constexpr int SB = KTB / 2;  // staging bytes per wave
+              char* stage = reinterpret_cast<char*>(smem) + (((i - 1) & 1) + 2 * (w >> 1)) * KTB + (w & 1) * SB;
+              store_acc32_staged<NDT, SB / 4096 < NDT ? SB / 4096 : NDT>(stage, dqp, ldq, dq, a.scale);
+          }
+      } else if (row0 + n < S) {
+          float* dqp = a.dq + op_base<STRIDED>(a.sdq, b, h, a.Hq, S, D) + (int64_t)(row0 + n) * op_ld<STRIDED>(a.sdq, D);
           if (fast_slots(qstart, qn, a.q_chunk) > 1) {
               const int64_t slot = (int64_t)(b * a.Hq + h) * 2 * a.q_units + 2 * unit + (first ? 0 : 1);
               dqp = a.q_part + (slot * BM + 32 * w + n) * D;
