@@ -609,49 +609,29 @@ int device_cus() {
 
 BwdPlan plan_bwd_fast(const AttnShape& s) {
     const int S = (int)s.S, causal = s.causal ? 1 : 0, group = (int)(s.Hq / s.Hkv), W = s.window;
-    const int nt = (S + 127) / 128;
-    const int64_t n_kv = bwd::fast_kv_start(S, causal, W, group, nt);  // iterations per (batch, kv head)
-    const int64_t n_q = fast_q_total(S, causal, W);                    // iterations per (batch, query head)
+    const FastTiles gkv{S, causal, W, group, 1}, gq{S, causal, W, group, 0};
     const int64_t pairs_kv = s.B * s.Hkv, pairs_q = s.B * s.Hq;
     const int64_t cus = (int64_t)device_cus() * bwd_wgs_per_cu(s.D);  // resident workgroups
-    BwdPlan p;
-    // Units no shorter than 4 iterations, and long enough that no tile spans
-    // more than 63 units (REDUCE keeps a tile's slot list in LDS, 64 entries).
-    int64_t kv_tile_max = 0, q_tile_max = 0;
-    for (int t = 0; t < nt; ++t) {
-        kv_tile_max = std::max<int64_t>(kv_tile_max, bwd::fast_kv_n(S, causal, W, group, t));
-        q_tile_max = std::max<int64_t>(q_tile_max, bwd::fast_q_n(S, causal, W, t));
-    }
-    const int64_t kv_min = std::max<int64_t>(4, (kv_tile_max + 60) / 61);
-    const int64_t q_min = std::max<int64_t>(4, (q_tile_max + 60) / 61);
     // Both roles share one launch of about one workgroup per CU, with units
-    // of about equal duration: a dK/dV iteration (32 rows x 128 keys, four
-    // products) costs 2, a dQ iteration (128 rows x 64 keys, three products)
-    // 3.  The unit cost T is the smallest at which every unit fits in one
-    // round; fewer, longer units than one launch per role would take also
-    // mean fewer fp32 partial tiles for REDUCE.
-    const int64_t work = 2 * n_kv * pairs_kv + 3 * n_q * pairs_q;
-    auto kv_chunk = [&](int64_t T) { return std::min<int64_t>(n_kv, std::max<int64_t>(kv_min, T / 2)); };
-    auto q_chunk = [&](int64_t T) { return std::min<int64_t>(n_q, std::max<int64_t>(q_min, T / 3)); };
-    auto units = [&](int64_t T) {
-        return pairs_kv * ((n_kv + kv_chunk(T) - 1) / kv_chunk(T)) + pairs_q * ((n_q + q_chunk(T) - 1) / q_chunk(T));
-    };
-    int64_t T = std::max<int64_t>(6, (work + cus - 1) / cus);
+    // of about equal cost (the iteration and tile costs price the two roles'
+    // work on one scale).  The unit cost T is the smallest
+    // at which every unit fits in one round; fewer, longer units than one
+    // launch per role would take also mean fewer fp32 partial tiles for
+    // REDUCE.
+    const int kvc = kv_tile_cost(s.D), qc = q_tile_cost(s.D);
+    const int64_t c_kv = make_unit_split(gkv, 1, kKvIterCost, kvc).ctot;  // one (batch, kv head)
+    const int64_t c_q = make_unit_split(gq, 1, kQIterCost, qc).ctot;      // one (batch, query head)
+    const int64_t work = c_kv * pairs_kv + c_q * pairs_q;
+    auto units = [&](int64_t T) { return pairs_kv * ((c_kv + T - 1) / T) + pairs_q * ((c_q + T - 1) / T); };
+    int64_t T = std::max<int64_t>(1, (work + cus - 1) / cus);
     // Longer units than both whole ranges change nothing; stop there.
-    const int64_t T_max = std::max(2 * n_kv, 3 * n_q);
+    const int64_t T_max = std::max(c_kv, c_q);
     while (T < T_max && units(T) > cus) T += std::max<int64_t>(1, T / 64);
-    p.kv_chunk = (int)kv_chunk(T);
-    p.q_chunk = (int)q_chunk(T);
-    p.kv_units = (int)((n_kv + p.kv_chunk - 1) / p.kv_chunk);
-    p.q_units = (int)((n_q + p.q_chunk - 1) / p.q_chunk);
-    p.kv_parts_max = p.q_parts_max = 1;
-    for (int t = 0; t < nt; ++t) {
-        p.kv_parts_max = std::max(p.kv_parts_max,
-                                  bwd::fast_slots(bwd::fast_kv_start(S, causal, W, group, t),
-                                                  bwd::fast_kv_n(S, causal, W, group, t), p.kv_chunk));
-        p.q_parts_max = std::max(p.q_parts_max, bwd::fast_slots(bwd::fast_q_start(S, causal, W, t),
-                                                                bwd::fast_q_n(S, causal, W, t), p.q_chunk));
-    }
+    // Units no shorter than kMinUnitIters iterations, and no tile over
+    // kSplitMaxSlots units (REDUCE keeps a tile's slot list in LDS).
+    BwdPlan p;
+    p.kv = fit_unit_split(gkv, (c_kv + T - 1) / T, kKvIterCost, kvc, kMinUnitIters, kSplitMaxSlots, &p.kv_parts_max);
+    p.q = fit_unit_split(gq, (c_q + T - 1) / T, kQIterCost, qc, kMinUnitIters, kSplitMaxSlots, &p.q_parts_max);
     return p;
 }
 
@@ -669,8 +649,8 @@ BwdLayout bwd_layout(const AttnShape& s) {
         // two slots per unit (split_slot), each one 128-row tile: dK and dV
         // tiles for the dK/dV role, a dQ tile for the dQ role
         const size_t tile = static_cast<size_t>(128 * s.D);
-        l.kv_part = p.kv_parts_max > 1 ? up(sizeof(float) * 2 * tile * 2 * p.kv_units * s.B * s.Hkv) : 0;
-        l.q_part = p.q_parts_max > 1 ? up(sizeof(float) * tile * 2 * p.q_units * s.B * s.Hq) : 0;
+        l.kv_part = p.kv_parts_max > 1 ? up(sizeof(float) * 2 * tile * 2 * p.kv.units * s.B * s.Hkv) : 0;
+        l.q_part = p.q_parts_max > 1 ? up(sizeof(float) * tile * 2 * p.q.units * s.B * s.Hq) : 0;
     } else {
         const int splits = dkdv_splits(s);
         l.kv_part = splits > 1 ? up(sizeof(float) * 2 * splits * kv_elems) : 0;
@@ -759,12 +739,10 @@ hipError_t launch_attn_bwd(const AttnShape& s, const void* q, const void* k, con
     a.q_part_stride = s.B * s.Hq * s.S * s.D;
     if (bwd_fast_path(s)) {
         const BwdPlan p = plan_bwd_fast(s);
-        a.kv_chunk = p.kv_chunk;
-        a.q_chunk = p.q_chunk;
-        a.kv_units = p.kv_units;
-        a.q_units = p.q_units;
+        a.kv_us = p.kv;
+        a.q_us = p.q;
     } else {
-        a.kv_chunk = a.q_chunk = a.kv_units = a.q_units = 0;
+        a.kv_us = a.q_us = UnitSplit{0, 0, 0, 0};
     }
     const hipError_t e =
         s.bf16 ? launch_bwd_dispatch<bf16>(s, a, stages, st) : launch_bwd_dispatch<float>(s, a, stages, st);

@@ -35,9 +35,9 @@ struct BwdArgs {
     Strides sq, sk, sv, so, sdo, sdq, sdk, sdv;  // operand layouts
     // fast path work units (see BwdPlan)
     int causal;
-    int kv_chunk, q_chunk, kv_units, q_units;  // iterations per unit, units per (batch, head)
-    float* kv_part;   // [B*Hkv][2*kv_units][dK, dV][128][D] partial tiles (split_slot)
-    float* q_part;    // [B*Hq][2*q_units][128][D] partial dQ tiles (split_slot)
+    UnitSplit kv_us, q_us;  // work units per (batch, kv head), per (batch, query head)
+    float* kv_part;   // [B*Hkv][2*kv_us.units][dK, dV][128][D] partial tiles (split_slot)
+    float* q_part;    // [B*Hq][2*q_us.units][128][D] partial dQ tiles (split_slot)
     int64_t q_part_stride;  // B*Hq*S*D
 };
 
@@ -50,8 +50,11 @@ using ::mft::fast_q_lo;
 using ::mft::fast_q_n;
 using ::mft::fast_q_start;
 using ::mft::fast_q_total;
-using ::mft::fast_slots;
+using ::mft::FastTiles;
 using ::mft::split_slot;
+using ::mft::tile_units;
+using ::mft::unit_first;
+using ::mft::UnitSplit;
 
 // Operand addressing of the fast kernels: STRIDED = false is the contiguous
 // [B, H, S, D] layout with offsets formed from the shape alone (no stride

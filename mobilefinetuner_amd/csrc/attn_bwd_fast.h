@@ -151,9 +151,9 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
 
     // This unit's chunk of the flattened (key tile, query head, query block)
     // iterations; it may start inside one key tile and end inside a later one.
-    const int nkt = (S + BNK - 1) / BNK;
-    const int64_t g0 = (int64_t)unit * a.kv_chunk;
-    const int niter = (int)min((int64_t)a.kv_chunk, fast_kv_start(S, CAUSAL, W, G, nkt) - g0);
+    const FastTiles tiles{S, CAUSAL, W, G, 1};
+    const int64_t g0 = unit_first(tiles, a.kv_us, unit);
+    const int niter = (int)(unit_first(tiles, a.kv_us, unit + 1) - g0);
     int kt = 0;
     while (fast_kv_start(S, CAUSAL, W, G, kt + 1) <= g0) ++kt;
 
@@ -390,8 +390,8 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
               float* dkp = a.dk + op_base<STRIDED>(a.sdk, b, hk, a.Hkv, S, D) + (int64_t)key0 * op_ld<STRIDED>(a.sdk, D);
               float* dvp = a.dv + op_base<STRIDED>(a.sdv, b, hk, a.Hkv, S, D) + (int64_t)key0 * op_ld<STRIDED>(a.sdv, D);
               int64_t ldk = op_ld<STRIDED>(a.sdk, D), ldv = op_ld<STRIDED>(a.sdv, D);
-              if (fast_slots(kstart, kn, a.kv_chunk) > 1) {
-                  const int64_t slot = (int64_t)(b * a.Hkv + hk) * 2 * a.kv_units + 2 * unit + (first ? 0 : 1);
+              if (tile_units(tiles, a.kv_us, kt) > 1) {
+                  const int64_t slot = (int64_t)(b * a.Hkv + hk) * 2 * a.kv_us.units + 2 * unit + (first ? 0 : 1);
                   dkp = a.kv_part + (slot * 2 * BNK + 32 * w) * D;
                   dvp = dkp + BNK * D;
                   ldk = ldv = D;
@@ -404,8 +404,8 @@ __device__ __forceinline__ void dkdv_fast_body(const BwdArgs& a, bf16* smem, int
           const int key = key0 + n;
           float* dkp = a.dk + op_base<STRIDED>(a.sdk, b, hk, a.Hkv, S, D) + (int64_t)key * op_ld<STRIDED>(a.sdk, D);
           float* dvp = a.dv + op_base<STRIDED>(a.sdv, b, hk, a.Hkv, S, D) + (int64_t)key * op_ld<STRIDED>(a.sdv, D);
-          if (fast_slots(kstart, kn, a.kv_chunk) > 1) {
-              const int64_t slot = (int64_t)(b * a.Hkv + hk) * 2 * a.kv_units + 2 * unit + (first ? 0 : 1);
+          if (tile_units(tiles, a.kv_us, kt) > 1) {
+              const int64_t slot = (int64_t)(b * a.Hkv + hk) * 2 * a.kv_us.units + 2 * unit + (first ? 0 : 1);
               dkp = a.kv_part + (slot * 2 * BNK + key - kt * BNK) * D;
               dvp = dkp + BNK * D;
           }
@@ -456,9 +456,10 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
     TileDma<DP, BN, NT, SWZ_DUAL> dmk;
     dmk.init(lane, wave_id(), lk);
 
-    // This unit's chunk of the flattened (query tile, key tile) iterations.
-    const int64_t g0 = (int64_t)unit * a.q_chunk;
-    const int niter = (int)min((int64_t)a.q_chunk, fast_q_total(S, CAUSAL, W) - g0);
+    // This unit's range of the flattened (query tile, key tile) iterations.
+    const FastTiles tiles{S, CAUSAL, W, a.group, 0};
+    const int64_t g0 = unit_first(tiles, a.q_us, unit);
+    const int niter = (int)(unit_first(tiles, a.q_us, unit + 1) - g0);
     int qt = 0;
     while (fast_q_start(S, CAUSAL, W, qt + 1) <= g0) ++qt;
     // Prefetch cursor: query tile and key tile of the next iteration to load
@@ -624,8 +625,8 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
           if (wave_uniform(row0 < S)) {
               float* dqp = a.dq + op_base<STRIDED>(a.sdq, b, h, a.Hq, S, D) + (int64_t)row0 * op_ld<STRIDED>(a.sdq, D);
               int64_t ldq = op_ld<STRIDED>(a.sdq, D);
-              if (fast_slots(qstart, qn, a.q_chunk) > 1) {
-                  const int64_t slot = (int64_t)(b * a.Hq + h) * 2 * a.q_units + 2 * unit + (first ? 0 : 1);
+              if (tile_units(tiles, a.q_us, qt) > 1) {
+                  const int64_t slot = (int64_t)(b * a.Hq + h) * 2 * a.q_us.units + 2 * unit + (first ? 0 : 1);
                   dqp = a.q_part + (slot * BM + 32 * w) * D;
                   ldq = D;
               }
@@ -635,8 +636,8 @@ __device__ __forceinline__ void dq_fast_body(const BwdArgs& a, bf16* smem, int u
           }
       } else if (row0 + n < S) {
           float* dqp = a.dq + op_base<STRIDED>(a.sdq, b, h, a.Hq, S, D) + (int64_t)(row0 + n) * op_ld<STRIDED>(a.sdq, D);
-          if (fast_slots(qstart, qn, a.q_chunk) > 1) {
-              const int64_t slot = (int64_t)(b * a.Hq + h) * 2 * a.q_units + 2 * unit + (first ? 0 : 1);
+          if (tile_units(tiles, a.q_us, qt) > 1) {
+              const int64_t slot = (int64_t)(b * a.Hq + h) * 2 * a.q_us.units + 2 * unit + (first ? 0 : 1);
               dqp = a.q_part + (slot * BM + 32 * w + n) * D;
           }
 #pragma unroll
@@ -677,14 +678,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_bf16_fast(BwdArgs a) {
     dq_fast_body<DP, CAUSAL, STRIDED, false>(a, smem, i / bh, (i % bh) / a.Hq, (i % bh) % a.Hq);
 }
 
-// Both roles in one grid: the first kv_units * B * Hkv workgroups run dK/dV
+// Both roles in one grid: the first kv_us.units * B * Hkv workgroups run dK/dV
 // units, the rest dQ units (the units of both are sized to take about equally
 // long, see plan_bwd_fast).  FAST: every operand tile is whole (D == DP and S
 // a multiple of 64), so the direct loads take TileDma's precomputed offsets.
 template <int DP, bool CAUSAL, bool STRIDED, bool FAST>
 __global__ __launch_bounds__(256) void attn_bwd_main_bf16_fast(BwdArgs a) {
     __shared__ __attribute__((aligned(1024))) bf16 smem[BwdFastLds<DP>::ELEMS];
-    const int nkv = a.kv_units * a.B * a.Hkv;
+    const int nkv = a.kv_us.units * a.B * a.Hkv;
     const int i = (int)blockIdx.x;
     if (i < nkv) {
         const int bh = a.B * a.Hkv;
@@ -737,14 +738,15 @@ __global__ __launch_bounds__(256) void attn_bwd_fast_reduce(BwdArgs a) {
     const bool kv = blk < kv_blocks;
     if (!kv) blk -= kv_blocks;
     const int rg = (int)(blk % RG), t = (int)((blk / RG) % nt), bh = (int)(blk / (RG * nt));
-    const int64_t start = kv ? fast_kv_start(S, CAUSAL, a.window, a.group, t) : fast_q_start(S, CAUSAL, a.window, t);
-    const int n = kv ? fast_kv_n(S, CAUSAL, a.window, a.group, t) : fast_q_n(S, CAUSAL, a.window, t);
-    const int64_t chunk = kv ? a.kv_chunk : a.q_chunk;
-    const int nsl = fast_slots(start, n, chunk);
+    const FastTiles tiles{S, CAUSAL, a.window, a.group, kv ? 1 : 0};
+    const UnitSplit us = kv ? a.kv_us : a.q_us;
+    int u0;
+    const int nsl = tile_units(tiles, us, t, &u0);
     const int r0 = t * 128 + rg * kRedRows;
     if (nsl <= 1 || r0 >= S) return;
-    const int64_t u0 = start / chunk, head_slots = (int64_t)bh * 2 * (kv ? a.kv_units : a.q_units);
-    if ((int)threadIdx.x < nsl) slot_of[threadIdx.x] = head_slots + split_slot(start, chunk, u0 + threadIdx.x, u0);
+    const bool starts = unit_first(tiles, us, u0) == tiles.start(t);
+    const int64_t head_slots = (int64_t)bh * 2 * us.units;
+    if ((int)threadIdx.x < nsl) slot_of[threadIdx.x] = head_slots + split_slot(u0 + threadIdx.x, u0, starts);
     __syncthreads();
     const int r = threadIdx.x / 16;
     if (r0 + r >= S) return;
@@ -786,7 +788,7 @@ hipError_t launch_bwd_fast(const AttnShape& s, BwdArgs a, int stages, hipStream_
             hipLaunchKernelGGL((KERNEL<DP, false, false>), GRID, dim3(256), 0, st, a);    \
     } while (0)
     if ((stages & BWD_STAGE_MAIN) == BWD_STAGE_MAIN) {
-        const dim3 grid((unsigned)(pl.kv_units * s.B * s.Hkv + pl.q_units * s.B * s.Hq));
+        const dim3 grid((unsigned)(pl.kv.units * s.B * s.Hkv + pl.q.units * s.B * s.Hq));
         if (s.D == DP && s.S % 64 == 0) {
 #define MFT_MAIN_FAST(CAUSAL, STRIDED, FAST) \
     hipLaunchKernelGGL((attn_bwd_main_bf16_fast<DP, CAUSAL, STRIDED, FAST>), grid, dim3(256), 0, st, a)
@@ -810,9 +812,9 @@ hipError_t launch_bwd_fast(const AttnShape& s, BwdArgs a, int stages, hipStream_
 #undef MFT_MAIN_FAST
         }
     } else if (stages & BWD_STAGE_DKDV) {
-        MFT_BWD_LAUNCH(attn_bwd_dkdv_bf16_fast, dim3((unsigned)(pl.kv_units * s.B * s.Hkv)));
+        MFT_BWD_LAUNCH(attn_bwd_dkdv_bf16_fast, dim3((unsigned)(pl.kv.units * s.B * s.Hkv)));
     } else if (stages & BWD_STAGE_DQ) {
-        MFT_BWD_LAUNCH(attn_bwd_dq_bf16_fast, dim3((unsigned)(pl.q_units * s.B * s.Hq)));
+        MFT_BWD_LAUNCH(attn_bwd_dq_bf16_fast, dim3((unsigned)(pl.q.units * s.B * s.Hq)));
     }
 #undef MFT_BWD_LAUNCH
     if ((stages & BWD_STAGE_REDUCE) && (pl.kv_parts_max > 1 || pl.q_parts_max > 1)) {

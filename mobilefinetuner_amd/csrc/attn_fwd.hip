@@ -252,15 +252,17 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(FwdArgs a) {
     const int S = a.S, D = a.D;
     const int nqt = (S + BM - 1) / BM;
     const int rg = (int)blockIdx.x % RG, qt = ((int)blockIdx.x / RG) % nqt, bh = (int)blockIdx.x / (RG * nqt);
-    const int64_t qstart = fast_q_start(S, CAUSAL, a.window, qt);
-    const int nsl = fast_slots(qstart, fast_q_n(S, CAUSAL, a.window, qt), a.chunk);
+    const FastTiles tiles{S, CAUSAL, a.window, a.group, 0};
+    int u0;
+    const int nsl = tile_units(tiles, a.us, qt, &u0);
     const int r0 = qt * BM + rg * kCombRows;
     if (nsl <= 1 || r0 >= S) return;
-    const int64_t u0 = qstart / a.chunk, head_slots = (int64_t)bh * 2 * a.units;
+    const bool starts = unit_first(tiles, a.us, u0) == tiles.start(qt);
+    const int64_t head_slots = (int64_t)bh * 2 * a.us.units;
     __shared__ int64_t slot_of[kCombMaxSlots];
     const int rows = min(kCombRows, S - r0);
     const int tid = threadIdx.x;
-    if (tid < nsl) slot_of[tid] = head_slots + split_slot(qstart, a.chunk, u0 + tid, u0);
+    if (tid < nsl) slot_of[tid] = head_slots + split_slot(u0 + tid, u0, starts);
     __syncthreads();
     // (running max, sum) of every (slot, row), loaded in parallel.
     for (int i = tid; i < nsl * kCombRows; i += 256) {
@@ -361,22 +363,13 @@ int fwd_rows_per_block(const AttnShape&) { return 128; }
 
 FwdPlan plan_fwd_split(const AttnShape& s) {
     const int S = (int)s.S, causal = s.causal ? 1 : 0, W = s.window;
-    const int nqt = (S + kFwdBM - 1) / kFwdBM;
-    const int64_t n = fast_q_total(S, causal, W);  // iterations per (batch, head)
     const int64_t pairs = s.B * s.Hq;
     const int64_t u = balanced_units(pairs, (int64_t)device_cus() * fwd_wgs_per_cu(s.D));
     FwdPlan p;
-    // Units no shorter than 4 key tiles: a split costs one fp32 partial tile.
-    // A query tile has at most 2*S/64 key tiles; keep its slots <= kCombMaxSlots.
-    int64_t max_tile = 0;
-    for (int t = 0; t < nqt; ++t) max_tile = std::max<int64_t>(max_tile, fast_q_n(S, causal, W, t));
-    const int64_t min_chunk = std::max<int64_t>(4, (max_tile + kCombMaxSlots - 3) / (kCombMaxSlots - 2));
-    p.chunk = (int)std::min<int64_t>(n, std::max<int64_t>(min_chunk, (n + u - 1) / u));
-    p.units = (int)((n + p.chunk - 1) / p.chunk);
-    p.parts_max = 1;
-    for (int t = 0; t < nqt; ++t)
-        p.parts_max = std::max(p.parts_max, fast_slots(fast_q_start(S, causal, W, t), fast_q_n(S, causal, W, t),
-                                                       p.chunk));
+    // Units of about equal cost, no shorter than kMinUnitIters key tiles (a
+    // split costs one fp32 partial tile), no query tile over kCombMaxSlots.
+    const FastTiles g{S, causal, W, (int)(s.Hq / s.Hkv), 0};
+    p.us = fit_unit_split(g, u, kFwdIterCost, fwd_tile_cost(s.D), kMinUnitIters, kCombMaxSlots, &p.parts_max);
     p.any_split = p.parts_max > 1;
     return p;
 }
@@ -384,7 +377,7 @@ FwdPlan plan_fwd_split(const AttnShape& s) {
 size_t fwd_workspace_bytes(const AttnShape& s) {
     if (!(s.bf16 && s.D % 8 == 0 && s.D > 32)) return 0;
     const FwdPlan p = plan_fwd_split(s);
-    const size_t rows = p.any_split ? static_cast<size_t>(s.B * s.Hq) * 2 * p.units * kFwdBM : 0;
+    const size_t rows = p.any_split ? static_cast<size_t>(s.B * s.Hq) * 2 * p.us.units * kFwdBM : 0;
     auto up = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
     // Always non-zero for this path, so that a caller that passes the queried
     // workspace gets the balanced launch.
@@ -415,13 +408,12 @@ hipError_t launch_attn_fwd(const AttnShape& s, const void* q, const void* k, con
     a.sk = s.k;
     a.sv = s.v;
     a.so = s.o;
-    a.chunk = 0;
-    a.units = 0;
+    a.us = UnitSplit{0, 0, 0, 0};
     a.part_o = nullptr;
     a.part_ml = nullptr;
     if (workspace && fwd_workspace_bytes(s) > 0) {
         const FwdPlan p = plan_fwd_split(s);
-        const size_t rows = p.any_split ? static_cast<size_t>(s.B * s.Hq) * 2 * p.units * kFwdBM : 0;
+        const size_t rows = p.any_split ? static_cast<size_t>(s.B * s.Hq) * 2 * p.us.units * kFwdBM : 0;
         const size_t ob = (rows * static_cast<size_t>(s.D) * 4 + 255) & ~static_cast<size_t>(255);
         a.part_o = static_cast<float*>(workspace);
         a.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + ob);

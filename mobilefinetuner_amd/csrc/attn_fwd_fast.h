@@ -44,9 +44,8 @@ struct FwdArgs {
     const int* kv_len;       // [B] valid keys per batch, or null
     Strides sq, sk, sv, so;  // layouts of q, k, v, o
     // balanced launch (bf16 fast path with a workspace; see FwdPlan)
-    int chunk;               // iterations per unit
-    int units;               // units per (batch, head)
-    float* part_o;           // [B*Hq][2*units][128][D] unnormalised O (split_slot)
+    UnitSplit us;            // work units per (batch, head)
+    float* part_o;           // [B*Hq][2*us.units][128][D] unnormalised O (split_slot)
     float* part_ml;          // [B*Hq][2*units][128][2] running max (log2 units), sum
 };
 
@@ -394,9 +393,10 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
 
     const int W = a.window;
     const KeyVis vis{S, W, a.kv_len ? min(max(a.kv_len[b], 0), S) : S, CAUSAL};
-    // This unit's chunk of the flattened (query tile, key tile) iterations.
-    const int64_t g0 = (int64_t)unit * a.chunk;
-    const int niter = (int)min((int64_t)a.chunk, fast_q_total(S, CAUSAL, W) - g0);
+    // This unit's range of the flattened (query tile, key tile) iterations.
+    const FastTiles tiles{S, CAUSAL, W, a.group, 0};
+    const int64_t g0 = unit_first(tiles, a.us, unit);
+    const int niter = (int)(unit_first(tiles, a.us, unit + 1) - g0);
     int qt = 0;
     while (fast_q_start(S, CAUSAL, W, qt + 1) <= g0) ++qt;
     // Prefetch cursor: query tile and key tile of the next iteration to load
@@ -469,7 +469,7 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
         // The next segment's Q rows load first (qf is dead here), so that
         // they land while this segment's outputs are stored.
         const bool more = i < niter;
-        const int nsl = fast_slots(qstart, qn, a.chunk);  // of the segment just finished
+        const int nsl = tile_units(tiles, a.us, qt);  // of the segment just finished
         if (more) {
             ++qt;
             qstart = fast_q_start(S, CAUSAL, W, qt);
@@ -488,7 +488,7 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
             if (nsl <= 1) {
                 if (row < S) fwd_store_row<DP>(a, b, h, row, oacc, m_run, l_tot);
             } else if (row < S) {
-                const int64_t slot = (int64_t)(b * a.Hq + h) * 2 * a.units + 2 * unit + (first ? 0 : 1);
+                const int64_t slot = (int64_t)(b * a.Hq + h) * 2 * a.us.units + 2 * unit + (first ? 0 : 1);
                 float* po = a.part_o + (slot * BM + 32 * w + n) * D;
 #pragma unroll
                 for (int dt = 0; dt < NDT; ++dt)
@@ -534,20 +534,19 @@ hipError_t launch_fwd_fast_t(const AttnShape& s, FwdArgs a, hipStream_t st) {
     FwdPlan p{};
     if (split) {
         p = plan_fwd_split(s);
-        a.chunk = p.chunk;
-        a.units = p.units;
+        a.us = p.us;
     }
     const bool fast = fwd_fast_dma<DP>(s);
     if (s.causal) {
         if (fast)
-            launch_fwd_fast_k<DP, true, true>(s, a, split, p.units, st);
+            launch_fwd_fast_k<DP, true, true>(s, a, split, p.us.units, st);
         else
-            launch_fwd_fast_k<DP, true, false>(s, a, split, p.units, st);
+            launch_fwd_fast_k<DP, true, false>(s, a, split, p.us.units, st);
     } else {
         if (fast)
-            launch_fwd_fast_k<DP, false, true>(s, a, split, p.units, st);
+            launch_fwd_fast_k<DP, false, true>(s, a, split, p.us.units, st);
         else
-            launch_fwd_fast_k<DP, false, false>(s, a, split, p.units, st);
+            launch_fwd_fast_k<DP, false, false>(s, a, split, p.us.units, st);
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || !(split && p.any_split)) return e;

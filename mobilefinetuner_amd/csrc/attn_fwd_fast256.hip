@@ -11,9 +11,8 @@ hipError_t launch_fwd_fast256(const AttnShape& s, FwdArgs a, hipStream_t st) {
     if (a.part_o == nullptr || !fwd_fast_dma<256>(s)) return launch_fwd_fast_t<256>(s, a, st);
     a.n_qtiles = (int)((s.S + kFwdBM - 1) / kFwdBM);
     const FwdPlan p = plan_fwd_split(s);
-    a.chunk = p.chunk;
-    a.units = p.units;
-    const dim3 grid((unsigned)(p.units * s.B * s.Hq));
+    a.us = p.us;
+    const dim3 grid((unsigned)(p.us.units * s.B * s.Hq));
     if (s.causal)
         hipLaunchKernelGGL((attn_fwd_bf16_split16<256, true>), grid, dim3(kW16Threads), 0, st, a);
     else

@@ -238,8 +238,9 @@ __global__ __launch_bounds__(kW16Threads) void attn_fwd_bf16_split16(FwdArgs a) 
 
     const int W = a.window;
     const KeyVis vis{S, W, a.kv_len ? min(max(a.kv_len[b], 0), S) : S, CAUSAL};
-    const int64_t g0 = (int64_t)unit * a.chunk;
-    const int niter = (int)min((int64_t)a.chunk, fast_q_total(S, CAUSAL, W) - g0);
+    const FastTiles tiles{S, CAUSAL, W, a.group, 0};
+    const int64_t g0 = unit_first(tiles, a.us, unit);
+    const int niter = (int)(unit_first(tiles, a.us, unit + 1) - g0);
     int qt = 0;
     while (fast_q_start(S, CAUSAL, W, qt + 1) <= g0) ++qt;
     int pf_qt = qt, pf_t = (int)(g0 - fast_q_start(S, CAUSAL, W, qt)), pf_n = fast_q_n(S, CAUSAL, W, qt);
@@ -307,7 +308,7 @@ __global__ __launch_bounds__(kW16Threads) void attn_fwd_bf16_split16(FwdArgs a) 
             }
         }
         const bool more = i < niter;
-        const int nsl = fast_slots(qstart, qn, a.chunk);
+        const int nsl = tile_units(tiles, a.us, qt);
         if (more) {
             ++qt;
             qstart = fast_q_start(S, CAUSAL, W, qt);
@@ -321,7 +322,7 @@ __global__ __launch_bounds__(kW16Threads) void attn_fwd_bf16_split16(FwdArgs a) 
             if (nsl <= 1) {
                 fwd16_store_row<DP>(a, b, h, row, oacc, m_run, l_tot);
             } else {
-                const int64_t slot = (int64_t)(b * a.Hq + h) * 2 * a.units + 2 * unit + (first ? 0 : 1);
+                const int64_t slot = (int64_t)(b * a.Hq + h) * 2 * a.us.units + 2 * unit + (first ? 0 : 1);
                 float* po = a.part_o + (slot * BM + 16 * w + n) * D;
 #pragma unroll
                 for (int dt = 0; dt < NDT; ++dt)

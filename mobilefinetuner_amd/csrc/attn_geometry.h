@@ -21,7 +21,8 @@ namespace mft {
 // tile).  dQ and forward: per (batch, query head) the iterations (128-row
 // query tile qt, 64-key tile) are flattened qt-major; tile qt holds
 // fast_q_n(qt) key tiles fast_q_lo(qt) .. + fast_q_n(qt) - 1 starting at
-// iteration fast_q_start(qt).  Work units are equal chunks of these ranges.
+// iteration fast_q_start(qt).  Work units are contiguous ranges of these
+// iterations of about equal cost (UnitSplit).
 __host__ __device__ inline int fast_nb(int S) { return (S + 31) / 32; }
 
 // 64-key tiles a 128-row query tile reaches back beyond its own two:
@@ -94,20 +95,104 @@ __host__ __device__ inline int64_t balanced_units(int64_t pairs, int64_t cus) {
     }
     return best;
 }
-// Units [first, last] of chunk size `chunk` that touch the range [start, start + n).
-__host__ __device__ inline int fast_slots(int64_t start, int n, int64_t chunk) {
-    return (int)((start + n - 1) / chunk - start / chunk + 1);
+// The tiles of one (batch, head)'s flattened iterations: 128-key tiles of the
+// dK/dV role (kv = 1), or 128-row query tiles of the dQ role and the forward.
+struct FastTiles {
+    int S, causal, W, group, kv;
+    __host__ __device__ int nt() const { return (S + 127) / 128; }
+    __host__ __device__ int64_t start(int t) const {
+        return kv ? fast_kv_start(S, causal, W, group, t) : fast_q_start(S, causal, W, t);
+    }
+    __host__ __device__ int n(int t) const {
+        return kv ? fast_kv_n(S, causal, W, group, t) : fast_q_n(S, causal, W, t);
+    }
+    __host__ __device__ int64_t total() const { return start(nt() - 1) + n(nt() - 1); }
+};
+
+// Work units sized by cost rather than by iteration count.  An iteration
+// costs w and each tile costs c more, for what a tile's segment adds
+// (loading its rows, storing its outputs or partial, restarting the
+// pipeline), so that units covering many short tiles get fewer iterations.
+// F(i) = w (i + 1) + c (t(i) + 1) is the cost through iteration i of tile
+// t(i), ctot = F(last); unit u of `units` holds the iterations i with
+// ceil(F(i) units / ctot) - 1 == u, a contiguous range.
+struct UnitSplit {
+    int units, w, c;
+    int64_t ctot;
+};
+__host__ __device__ inline UnitSplit make_unit_split(const FastTiles& g, int units, int w, int c) {
+    return UnitSplit{units, w, c, (int64_t)w * g.total() + (int64_t)c * g.nt()};
+}
+// Unit of iteration i, which lies in tile t.
+__host__ __device__ inline int unit_of(const UnitSplit& u, int64_t i, int t) {
+    const int64_t F = (int64_t)u.w * (i + 1) + (int64_t)u.c * (t + 1);
+    return (int)((F * u.units + u.ctot - 1) / u.ctot - 1);
+}
+// First iteration of unit k (k = units: one past the last iteration): the
+// smallest i with F(i) units > k ctot, found in the first tile whose last
+// iteration passes the bound.
+__host__ __device__ inline int64_t unit_first(const FastTiles& g, const UnitSplit& u, int k) {
+    if (k <= 0) return 0;
+    if (k >= u.units) return g.total();
+    const int64_t target = (int64_t)k * u.ctot;
+    int lo = 0, hi = g.nt() - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi) / 2;
+        const int64_t end_cost = (int64_t)u.w * (g.start(mid) + g.n(mid)) + (int64_t)u.c * (mid + 1);
+        if (end_cost * u.units > target)
+            hi = mid;
+        else
+            lo = mid + 1;
+    }
+    const int64_t s0 = g.start(lo);
+    const int64_t num = target - (int64_t)u.c * (lo + 1) * u.units;
+    const int64_t i = num < 0 ? 0 : num / ((int64_t)u.w * u.units);
+    return i > s0 ? i : s0;
+}
+// Units that touch tile t (first: *u0).
+__host__ __device__ inline int tile_units(const FastTiles& g, const UnitSplit& u, int t, int* u0) {
+    const int64_t s = g.start(t);
+    *u0 = unit_of(u, s, t);
+    return unit_of(u, s + g.n(t) - 1, t) - *u0 + 1;
+}
+__host__ __device__ inline int tile_units(const FastTiles& g, const UnitSplit& u, int t) {
+    int u0;
+    return tile_units(g, u, t, &u0);
+}
+// A split over `units` units with the planners' limits: every unit at least
+// kMin iterations and no tile over kMaxSlots units; units is lowered until
+// both hold (one unit always does).  *parts_max: the most units of a tile.
+inline UnitSplit fit_unit_split(const FastTiles& g, int64_t units, int w, int c, int kMin, int kMaxSlots,
+                                int* parts_max) {
+    const int64_t n = g.total();
+    if (units > n / kMin) units = n / kMin;
+    if (units < 1) units = 1;
+    for (;; units = units * 15 / 16 < units - 1 ? units * 15 / 16 : units - 1) {
+        const UnitSplit u = make_unit_split(g, (int)units, w, c);
+        int pm = 1;
+        for (int t = 0; t < g.nt(); ++t) {
+            const int k = tile_units(g, u, t);
+            pm = k > pm ? k : pm;
+        }
+        bool ok = pm <= kMaxSlots;
+        for (int k = 0; ok && k < u.units; ++k) ok = unit_first(g, u, k + 1) - unit_first(g, u, k) >= kMin;
+        if (ok || units == 1) {
+            *parts_max = pm;
+            return u;
+        }
+    }
 }
 
 // Partial slots.  A work unit has at most two segments in split tiles: the
 // tile holding its first iteration and the tile holding its last.  Unit u of
 // a (batch, head) keeps their partials in slots 2u (first segment) and 2u + 1
-// (last segment, when it differs from the first).  For a split tile starting
-// at iteration `start`, touched by units u0 = start / chunk .. u1, unit u's
-// partial is in slot split_slot(start, chunk, u, u0): the tile is the first
-// segment of every unit except possibly u0 (when the tile starts inside u0).
-__host__ __device__ inline int64_t split_slot(int64_t start, int64_t chunk, int64_t u, int64_t u0) {
-    return 2 * u + ((u == u0 && start % chunk != 0) ? 1 : 0);
+// (last segment, when it differs from the first).  For a split tile touched
+// by units u0 .. u1, unit u's partial is in slot split_slot(u, u0, starts):
+// the tile is the first segment of every unit except possibly u0, whose last
+// segment it is when the tile starts inside u0 (starts: the tile begins at
+// u0's first iteration).
+__host__ __device__ inline int64_t split_slot(int64_t u, int64_t u0, bool starts) {
+    return 2 * u + ((u == u0 && !starts) ? 1 : 0);
 }
 
 }  // namespace mft

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "attn_geometry.h"
+
 namespace mft {
 
 // Element strides of a [B, H, S, D] operand's batch, head and sequence
@@ -41,10 +43,10 @@ bool bwd_fast_path(const AttnShape& s);
 // Work decomposition of the bf16 fast backward.  Per (batch, kv head) the
 // dK/dV iterations (128-key tile, query head, 32-row query block) and per
 // (batch, query head) the dQ iterations (128-row query tile, 64-key tile) are
-// cut into equal chunks (kv_chunk / q_chunk iterations), about one unit per
-// CU in total, so the causal triangle no longer sets the critical path.  A
-// tile touched by several units gets fp32 partials (at most kv_parts_max /
-// q_parts_max slots) that REDUCE sums in slot order.
+// cut into units of about equal cost (UnitSplit, attn_geometry.h), about one
+// unit per CU in total, so the causal triangle no longer sets the critical
+// path.  A tile touched by several units gets fp32 partials (at most
+// kv_parts_max / q_parts_max slots) that REDUCE sums in slot order.
 // The most partial slots one split tile may have: REDUCE and the forward
 // combine keep a tile's slot list (and the combine its per-slot weights) in
 // LDS arrays of this length.  The planners size units so that no tile goes
@@ -52,10 +54,23 @@ bool bwd_fast_path(const AttnShape& s);
 constexpr int kSplitMaxSlots = 64;
 
 struct BwdPlan {
-    int kv_chunk, q_chunk;
+    UnitSplit kv, q;  // units per (batch, kv head) and per (batch, query head)
     int kv_parts_max, q_parts_max;
-    int kv_units, q_units;  // units per (batch, kv head) and per (batch, query head)
 };
+
+// Costs of the unit splits (UnitSplit): an iteration's and a tile's extra
+// (its rows loaded, its outputs or partial stored, the pipeline restarted),
+// from per-unit cycle counts of the D = 256 kernels.  Backward iterations
+// are priced against each other: a dK/dV one (32 rows x 128 keys, four
+// products) 2, a dQ one (128 rows x 64 keys, three products) 3.  The tile
+// costs were measured at D = 256 only; narrower heads split by iteration
+// count (tile cost 0), which measured faster there than the D = 256 costs.
+constexpr int kFwdIterCost = 1, kKvIterCost = 2, kQIterCost = 3;
+inline int fwd_tile_cost(int64_t D) { return D >= 256 ? 2 : 0; }
+inline int kv_tile_cost(int64_t D) { return D >= 256 ? 11 : 0; }
+inline int q_tile_cost(int64_t D) { return D >= 256 ? 13 : 0; }
+// The fewest iterations the planners give a unit.
+constexpr int kMinUnitIters = 4;
 BwdPlan plan_bwd_fast(const AttnShape& s);
 
 // Backward workspace layout in bytes: [delta or row-stat blocks][dK/dV
@@ -78,11 +93,11 @@ inline int fwd_wgs_per_cu(int64_t D) { return D <= 128 ? 2 : 1; }
 inline int bwd_wgs_per_cu(int64_t D) { return D <= 64 ? 2 : 1; }
 
 // Balanced forward (bf16 fast path): per (batch, head) the iterations
-// (128-row query tile, 64-key tile) are cut into `units` chunks of `chunk`
-// iterations; a query tile split across units leaves fp32 partials in the
-// units' slots (split_slot, attn_geometry.h).
+// (128-row query tile, 64-key tile) are cut into units of about equal cost
+// (UnitSplit, attn_geometry.h); a query tile split across units leaves fp32
+// partials in the units' slots (split_slot).
 struct FwdPlan {
-    int chunk, units;
+    UnitSplit us;
     bool any_split;
     int parts_max;  // most slots of one query tile
 };
