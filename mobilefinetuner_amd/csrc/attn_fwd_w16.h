@@ -93,40 +93,40 @@ struct W16Issue {
     }
 };
 
-// One 64-key tile for this wave's 16 rows (see the header comment).
+// S^T = K Q^T of one 64-key tile for this wave's 16 rows: the four 16-key
+// blocks' chains interleaved, K through a ring; issue(j) for the next tile's
+// loads j < Issue::NPARTS go between the steps.
 template <int DP, class Issue>
-__device__ __forceinline__ void fwd16_tile(const FwdArgs& a, const char* smem, const W16Lane<DP>& ln, int par,
-                                           bool need_mask, int kbase, int vlo, int vhi, const bf16x8 (&qf)[DP / 32],
-                                           f32x4 (&oacc)[DP / 16], float& m_run, float& l_run, const Issue& issue) {
-    constexpr int NJ = DP / 32, NDT = DP / 16, NKB = kFwdBN / 16;
-    constexpr int TILEB = kFwdBN * DP * 2;
-    constexpr int PF = 4;
+__device__ __forceinline__ void fwd16_s(const char* kb_, const W16Lane<DP>& ln, const bf16x8 (&qf)[DP / 32],
+                                        f32x4 (&s)[kFwdBN / 16], const Issue& issue) {
+    constexpr int NJ = DP / 32, NKB = kFwdBN / 16, PF = 4;
     constexpr int NPARTS = Issue::NPARTS;
-    const int g = (threadIdx.x & 63) >> 4;
-    const char* kb_ = smem + par * TILEB;
-    const char* vb_ = smem + (2 + par) * TILEB;
-
-    // S^T: the four 16-key blocks' chains interleaved, K through a ring.
-    f32x4 s[NKB];
-    {
-        constexpr int NI = NKB * NJ;
-        auto kread = [&](int it) { return *reinterpret_cast<const bf16x8*>(kb_ + ln.k_off(it % NKB, it / NKB)); };
-        bf16x8 ring[PF];
+    constexpr int NI = NKB * NJ;
+    auto kread = [&](int it) { return *reinterpret_cast<const bf16x8*>(kb_ + ln.k_off(it % NKB, it / NKB)); };
+    bf16x8 ring[PF];
 #pragma unroll
-        for (int it = 0; it < PF; ++it) ring[it] = kread(it);
+    for (int it = 0; it < PF; ++it) ring[it] = kread(it);
 #pragma unroll
-        for (int it = 0; it < NI; ++it) {
-            const bf16x8 ka = ring[it % PF];
-            if (it + PF < NI) ring[it % PF] = kread(it + PF);
-            if (it < NKB)
-                mfma16_first(s[it], ka, qf[0]);
-            else
-                s[it % NKB] = mfma16(ka, qf[it / NKB], s[it % NKB]);
-            if ((it & 3) == 3 && (it >> 2) < NPARTS) issue(it >> 2);
-        }
-#pragma unroll
-        for (int j = NI / 4; j < NPARTS; ++j) issue(j);
+    for (int it = 0; it < NI; ++it) {
+        const bf16x8 ka = ring[it % PF];
+        if (it + PF < NI) ring[it % PF] = kread(it + PF);
+        if (it < NKB)
+            mfma16_first(s[it], ka, qf[0]);
+        else
+            s[it % NKB] = mfma16(ka, qf[it / NKB], s[it % NKB]);
+        if ((it & 3) == 3 && (it >> 2) < NPARTS) issue(it >> 2);
     }
+#pragma unroll
+    for (int j = NI / 4; j < NPARTS; ++j) issue(j);
+}
+
+// Mask, online softmax and O^T += V^T P^T of one tile whose S^T is in s.
+template <int DP>
+__device__ __forceinline__ void fwd16_pv(const FwdArgs& a, const char* vb_, const W16Lane<DP>& ln, bool need_mask,
+                                         int kbase, int vlo, int vhi, f32x4 (&s)[kFwdBN / 16], f32x4 (&oacc)[DP / 16],
+                                         float& m_run, float& l_run) {
+    constexpr int NDT = DP / 16, NKB = kFwdBN / 16, PF = 4;
+    const int g = (threadIdx.x & 63) >> 4;
     if (need_mask) {  // keys outside [vlo, vhi]
         int hi = vhi - kbase, lo = vlo - kbase;
         asm volatile("" : "+v"(hi), "+v"(lo));
@@ -196,6 +196,17 @@ __device__ __forceinline__ void fwd16_tile(const FwdArgs& a, const char* smem, c
         }
         pin_read_ahead<NI, PF, 2>();
     }
+}
+
+// One 64-key tile for this wave's 16 rows (see the header comment).
+template <int DP, class Issue>
+__device__ __forceinline__ void fwd16_tile(const FwdArgs& a, const char* smem, const W16Lane<DP>& ln, int par,
+                                           bool need_mask, int kbase, int vlo, int vhi, const bf16x8 (&qf)[DP / 32],
+                                           f32x4 (&oacc)[DP / 16], float& m_run, float& l_run, const Issue& issue) {
+    constexpr int TILEB = kFwdBN * DP * 2;
+    f32x4 s[kFwdBN / 16];
+    fwd16_s<DP>(smem + par * TILEB, ln, qf, s, issue);
+    fwd16_pv<DP>(a, smem + (2 + par) * TILEB, ln, need_mask, kbase, vlo, vhi, s, oacc, m_run, l_run);
 }
 
 // Normalised O row and LSE of this lane's query (row < S): lane group g
