@@ -700,7 +700,7 @@ __global__ __launch_bounds__(256) void attn_bwd_main_bf16_fast(BwdArgs a) {
 // workgroup per (batch, head, 128-row tile, 16-row group) of the dK/dV role
 // (rows = keys; dK and dV) and then of the dQ role (rows = queries);
 // workgroups of unsplit tiles return at once.
-constexpr int kRedRows = 16, kRedMaxSlots = kSplitMaxSlots;
+constexpr int kRedRows = 16, kRedMaxSlots = kSplitMaxSlots, kRedBatch = 4;
 
 __device__ __forceinline__ void reduce_rows(const float* part, const int64_t* slot_of, int nsl, int64_t tile_elems,
                                             int64_t row_in_tile, int D, float* dst) {
@@ -710,16 +710,26 @@ __device__ __forceinline__ void reduce_rows(const float* part, const int64_t* sl
     f32x4 acc[MAXJ];
 #pragma unroll
     for (int j = 0; j < MAXJ; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int p = 0; p < nsl; ++p) {
-        const float* src = part + slot_of[p] * tile_elems + row_in_tile * D;
-        f32x4 x[MAXJ];
+    // kRedBatch slots' loads in flight before they are summed (in slot order):
+    // one memory round trip per batch instead of one per slot.
+    for (int p0 = 0; p0 < nsl; p0 += kRedBatch) {
+        f32x4 x[kRedBatch][MAXJ];
 #pragma unroll
-        for (int j = 0; j < MAXJ; ++j) {
-            const int c = cl + 16 * j;
-            x[j] = c < cg ? *reinterpret_cast<const f32x4*>(src + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < kRedBatch; ++q) {
+            if (p0 + q >= nsl) break;
+            const float* src = part + slot_of[p0 + q] * tile_elems + row_in_tile * D;
+#pragma unroll
+            for (int j = 0; j < MAXJ; ++j) {
+                const int c = cl + 16 * j;
+                x[q][j] = c < cg ? *reinterpret_cast<const f32x4*>(src + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
         }
 #pragma unroll
-        for (int j = 0; j < MAXJ; ++j) acc[j] += x[j];
+        for (int q = 0; q < kRedBatch; ++q) {
+            if (p0 + q >= nsl) break;
+#pragma unroll
+            for (int j = 0; j < MAXJ; ++j) acc[j] += x[q][j];
+        }
     }
 #pragma unroll
     for (int j = 0; j < MAXJ; ++j) {

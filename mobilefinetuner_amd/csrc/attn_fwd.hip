@@ -32,6 +32,7 @@ namespace mft {
 using fwd::FwdArgs;
 using fwd::kFwdBM;
 using fwd::kFwdBN;
+using fwd::kCombBatch;
 using fwd::kCombRows;
 using fwd::kCombMaxSlots;
 using fwd::launch_fwd_fast64;
@@ -293,17 +294,27 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(FwdArgs a) {
     f32x4 acc[MAXJ];
 #pragma unroll
     for (int j = 0; j < MAXJ; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int p = 0; p < nsl; ++p) {
-        const float* src = a.part_o + (slot_of[p] * BM + rr) * D;
-        const float wp = wgt[p][r];
-        f32x4 x[MAXJ];
+    // kCombBatch slots' loads in flight before they are summed (in slot
+    // order): one memory round trip per batch instead of one per slot.
+    for (int p0 = 0; p0 < nsl; p0 += kCombBatch) {
+        f32x4 x[kCombBatch][MAXJ];
 #pragma unroll
-        for (int j = 0; j < MAXJ; ++j) {
-            const int c = cl + 16 * j;
-            x[j] = c < cg ? *reinterpret_cast<const f32x4*>(src + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < kCombBatch; ++q) {
+            if (p0 + q >= nsl) break;
+            const float* src = a.part_o + (slot_of[p0 + q] * BM + rr) * D;
+#pragma unroll
+            for (int j = 0; j < MAXJ; ++j) {
+                const int c = cl + 16 * j;
+                x[q][j] = c < cg ? *reinterpret_cast<const f32x4*>(src + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
         }
 #pragma unroll
-        for (int j = 0; j < MAXJ; ++j) acc[j] += x[j] * wp;
+        for (int q = 0; q < kCombBatch; ++q) {
+            if (p0 + q >= nsl) break;
+            const float wp = wgt[p0 + q][r];
+#pragma unroll
+            for (int j = 0; j < MAXJ; ++j) acc[j] += x[q][j] * wp;
+        }
     }
     const float il = inv_l[r];
     bf16* O = (bf16*)a.o + a.so.at(bh / a.Hq, bh % a.Hq) + (int64_t)(r0 + r) * a.so.s;
