@@ -41,6 +41,26 @@ import time
 
 METRIC = "causal GQA attn fwd+bwd TFLOP/s & % MFMA peak (1 GPU); saved-act bytes"
 PEAK_TFLOPS = {"bf16": 2500.0, "f32": 157.3}  # MI355X dense MFMA (published)
+# Warm-up floor: W warm-up steps are a minimum; warm-up continues until this
+# much wall time of them has run.  A cold MI355X ramps its clocks over the
+# first ~100 C5 steps (~25 ms): successive 50-step rounds from a cold start
+# measured 303, 223, 217, 215, 215 ... us per step.
+WARM_FLOOR_S = 0.15
+
+
+def warm_up(fn, warmup):
+    """Run fn untimed at least `warmup` times and for at least WARM_FLOOR_S
+    (synchronizing every 10 calls, so that the wall time is the GPU's);
+    returns the number of calls."""
+    import torch
+    n, t0 = 0, time.perf_counter()
+    while n < warmup or time.perf_counter() - t0 < WARM_FLOOR_S:
+        fn()
+        n += 1
+        if n % 10 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return n
 HBM_GBS = 8000.0
 
 # BASELINE.json configs (shapes, dtype, scale, dO sigma); all causal.
@@ -146,10 +166,7 @@ def gpu_leg(cfg_id, steps, warmup):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / n  # ms
 
-    for _ in range(warmup):
-        fwd()
-        bwd()
-    torch.cuda.synchronize()
+    warm_n = warm_up(lambda: (fwd(), bwd()), warmup)
     step_ms = timed(lambda: (fwd(), bwd()), steps)
     n_phase = max(steps, 10)
     fwd_ms = timed(fwd, n_phase)
@@ -157,7 +174,7 @@ def gpu_leg(cfg_id, steps, warmup):
     stage(capi.MFT_BWD_DELTA)()  # row terms for the gradient stages
     main_ms = timed(stage(capi.MFT_BWD_MAIN), n_phase)
     units = flop_units(c)
-    return dict(step_ms=step_ms, fwd_ms=fwd_ms, bwd_ms=bwd_ms, main_ms=main_ms, units=units)
+    return dict(step_ms=step_ms, fwd_ms=fwd_ms, bwd_ms=bwd_ms, main_ms=main_ms, units=units, warm_n=warm_n)
 
 
 def prologue_leg(cfg_id, steps, warmup):
@@ -211,9 +228,7 @@ def prologue_leg(cfg_id, steps, warmup):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / n
 
-    for _ in range(warmup):
-        fwd()
-        bwd()
+    warm_up(lambda: (fwd(), bwd()), warmup)
     f_ms, b_ms = timed(fwd, steps), timed(bwd, steps)
     return {"workload": f"q/k rms_norm(1+w) + RoPE of {cfg_id} (Hq {c['Hq']} + Hkv {c['Hkv']} heads, S {S}, D {D}), "
                         "[B,S,H,D] bf16 in, [B,H,S,D] out",
@@ -246,9 +261,7 @@ def lm_loss_leg(cfg_id, steps, warmup):
 
     def timed(fn, n):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        for _ in range(warmup):
-            fn()
-        torch.cuda.synchronize()
+        warm_up(fn, warmup)
         e0.record()
         for _ in range(n):
             fn()
@@ -311,9 +324,7 @@ def lora_leg(cfg_id, steps, warmup):
 
     def timed(fn, n):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        for _ in range(warmup):
-            fn()
-        torch.cuda.synchronize()
+        warm_up(fn, warmup)
         e0.record()
         for _ in range(n):
             fn()
@@ -547,6 +558,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_steps_run": r["warm_n"],  # W is a minimum; see WARM_FLOOR_S
         "ms_per_step": round(r["step_ms"], 5),
         "higher_is_better": True,
         "scaling": "weak",
