@@ -576,6 +576,7 @@ hipError_t launch_bwd_t(const AttnShape& s, BwdArgs a, int stages, hipStream_t s
 template <typename T>
 hipError_t launch_bwd_dispatch(const AttnShape& s, const BwdArgs& a, int stages, hipStream_t st) {
     if (bwd_fast_path(s)) {
+        if (!s.bf16) return f32::launch_bwd_fast(s, a, stages, st);
         if (s.D <= 64) return launch_bwd_fast_64(s, a, stages, st);
         if (s.D <= 128) return launch_bwd_fast_128(s, a, stages, st);
         return launch_bwd_fast_256(s, a, stages, st);
@@ -590,10 +591,12 @@ int padded_d(int64_t D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 
 
 }  // namespace
 
-// The fast bf16 kernels; they take K and V with one sequence stride (true of
-// contiguous operands, [B, S, Hkv, D] views and fused-QKV slices), other
-// layouts run the general kernels.
-bool bwd_fast_path(const AttnShape& s) { return s.bf16 && s.D % 8 == 0 && s.D > 32 && s.k.s == s.v.s; }
+// The fast kernels: bf16 (they take K and V with one sequence stride, true
+// of contiguous operands, [B, S, Hkv, D] views and fused-QKV slices; other
+// layouts run the general kernels) and fp32 (any layout).
+bool bwd_fast_path(const AttnShape& s) {
+    return (s.bf16 && s.D % 8 == 0 && s.D > 32 && s.k.s == s.v.s) || f32::fast_path(s);
+}
 
 // Compute units of the current device (256 on MI355X), cached per device.
 int device_cus() {
@@ -611,14 +614,14 @@ BwdPlan plan_bwd_fast(const AttnShape& s) {
     const int S = (int)s.S, causal = s.causal ? 1 : 0, group = (int)(s.Hq / s.Hkv), W = s.window;
     const FastTiles gkv{S, causal, W, group, 1}, gq{S, causal, W, group, 0};
     const int64_t pairs_kv = s.B * s.Hkv, pairs_q = s.B * s.Hq;
-    const int64_t cus = (int64_t)device_cus() * bwd_wgs_per_cu(s.D);  // resident workgroups
+    const int64_t cus = bwd_unit_slots(s);  // units resident at once
     // Both roles share one launch of about one workgroup per CU, with units
     // of about equal cost (the iteration and tile costs price the two roles'
     // work on one scale).  The unit cost T is the smallest
     // at which every unit fits in one round; fewer, longer units than one
     // launch per role would take also mean fewer fp32 partial tiles for
     // REDUCE.
-    const int kvc = kv_tile_cost(s.D), qc = q_tile_cost(s.D);
+    const int kvc = kv_tile_cost(s), qc = q_tile_cost(s);
     const int64_t c_kv = make_unit_split(gkv, 1, kKvIterCost, kvc).ctot;  // one (batch, kv head)
     const int64_t c_q = make_unit_split(gq, 1, kQIterCost, qc).ctot;      // one (batch, query head)
     const int64_t work = c_kv * pairs_kv + c_q * pairs_q;

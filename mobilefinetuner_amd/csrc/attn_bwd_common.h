@@ -181,4 +181,13 @@ hipError_t launch_bwd_fast_128(const AttnShape& s, const BwdArgs& a, int stages,
 hipError_t launch_bwd_fast_256(const AttnShape& s, const BwdArgs& a, int stages, hipStream_t st);
 
 }  // namespace bwd
+
+namespace f32 {
+// The fp32 fast backward (attn_f32_fast.hip).
+hipError_t launch_bwd_fast(const AttnShape& s, const bwd::BwdArgs& a, int stages, hipStream_t st);
+}  // namespace f32
+
+namespace bwd {
+
+}  // namespace bwd
 }  // namespace mft

@@ -244,7 +244,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
 // 16-row group); workgroups of tiles that were not split return at once.
 // The per-(slot, row) weights go through LDS, then each thread sums 16-byte
 // column chunks over the slots.
-template <bool CAUSAL>
+template <bool CAUSAL, typename T>
 __global__ __launch_bounds__(256) void attn_fwd_combine(FwdArgs a) {
     constexpr int BM = kFwdBM, RG = BM / kCombRows;
     __shared__ float wgt[kCombMaxSlots][kCombRows];
@@ -317,11 +317,11 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(FwdArgs a) {
         }
     }
     const float il = inv_l[r];
-    bf16* O = (bf16*)a.o + a.so.at(bh / a.Hq, bh % a.Hq) + (int64_t)(r0 + r) * a.so.s;
+    T* O = (T*)a.o + a.so.at(bh / a.Hq, bh % a.Hq) + (int64_t)(r0 + r) * a.so.s;
 #pragma unroll
     for (int j = 0; j < MAXJ; ++j) {
         const int c = cl + 16 * j;
-        if (c < cg) store4<bf16>(O, 4 * c, D, acc[j][0] * il, acc[j][1] * il, acc[j][2] * il, acc[j][3] * il, true);
+        if (c < cg) store4<T>(O, 4 * c, D, acc[j][0] * il, acc[j][1] * il, acc[j][2] * il, acc[j][3] * il, true);
     }
 }
 
@@ -346,6 +346,9 @@ hipError_t launch_fwd_dispatch(const AttnShape& s, FwdArgs a, hipStream_t st) {
             if (s.D <= 128) return launch_fwd_fast128(s, a, st);
             return launch_fwd_fast256(s, a, st);
         }
+    } else {
+        // the fp32 fast kernels run the balanced launch only (with a workspace)
+        if (f32::fast_path(s) && a.part_o != nullptr) return f32::launch_fwd_fast(s, a, st);
     }
     if (s.D <= 32) return launch_fwd_t<T, 32, 4, 64>(s, a, st);
     if (s.D <= 64) return launch_fwd_t<T, 64, 4, 64>(s, a, st);
@@ -358,10 +361,17 @@ hipError_t launch_fwd_dispatch(const AttnShape& s, FwdArgs a, hipStream_t st) {
 namespace fwd {
 hipError_t launch_fwd_combine(const AttnShape& s, const FwdArgs& a, hipStream_t st) {
     const dim3 cgrid((unsigned)(s.B * s.Hq * a.n_qtiles * (kFwdBM / kCombRows)));
-    if (s.causal)
-        hipLaunchKernelGGL(attn_fwd_combine<true>, cgrid, dim3(256), 0, st, a);
-    else
-        hipLaunchKernelGGL(attn_fwd_combine<false>, cgrid, dim3(256), 0, st, a);
+    if (s.bf16) {
+        if (s.causal)
+            hipLaunchKernelGGL((attn_fwd_combine<true, bf16>), cgrid, dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL((attn_fwd_combine<false, bf16>), cgrid, dim3(256), 0, st, a);
+    } else {
+        if (s.causal)
+            hipLaunchKernelGGL((attn_fwd_combine<true, float>), cgrid, dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL((attn_fwd_combine<false, float>), cgrid, dim3(256), 0, st, a);
+    }
     return hipGetLastError();
 }
 hipError_t launch_fwd_fast64(const AttnShape& s, FwdArgs a, hipStream_t st) { return launch_fwd_fast_t<64>(s, a, st); }
@@ -375,18 +385,18 @@ int fwd_rows_per_block(const AttnShape&) { return 128; }
 FwdPlan plan_fwd_split(const AttnShape& s) {
     const int S = (int)s.S, causal = s.causal ? 1 : 0, W = s.window;
     const int64_t pairs = s.B * s.Hq;
-    const int64_t u = balanced_units(pairs, (int64_t)device_cus() * fwd_wgs_per_cu(s.D));
+    const int64_t u = balanced_units(pairs, fwd_unit_slots(s));
     FwdPlan p;
     // Units of about equal cost, no shorter than kMinUnitIters key tiles (a
     // split costs one fp32 partial tile), no query tile over kCombMaxSlots.
     const FastTiles g{S, causal, W, (int)(s.Hq / s.Hkv), 0};
-    p.us = fit_unit_split(g, u, kFwdIterCost, fwd_tile_cost(s.D), kMinUnitIters, kCombMaxSlots, &p.parts_max);
+    p.us = fit_unit_split(g, u, kFwdIterCost, fwd_tile_cost(s), kMinUnitIters, kCombMaxSlots, &p.parts_max);
     p.any_split = p.parts_max > 1;
     return p;
 }
 
 size_t fwd_workspace_bytes(const AttnShape& s) {
-    if (!(s.bf16 && s.D % 8 == 0 && s.D > 32)) return 0;
+    if (!((s.bf16 && s.D % 8 == 0 && s.D > 32) || f32::fast_path(s))) return 0;
     const FwdPlan p = plan_fwd_split(s);
     const size_t rows = p.any_split ? static_cast<size_t>(s.B * s.Hq) * 2 * p.us.units * kFwdBM : 0;
     auto up = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };

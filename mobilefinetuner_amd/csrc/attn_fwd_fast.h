@@ -63,6 +63,14 @@ hipError_t launch_fwd_fast128(const AttnShape& s, FwdArgs a, hipStream_t st);
 hipError_t launch_fwd_fast256(const AttnShape& s, FwdArgs a, hipStream_t st);
 // The split launch's merge of partial query tiles (attn_fwd.hip).
 hipError_t launch_fwd_combine(const AttnShape& s, const FwdArgs& a, hipStream_t st);
+}  // namespace fwd
+
+namespace f32 {
+// The fp32 fast forward (attn_f32_fast.hip): the balanced launch (a.part_o set).
+hipError_t launch_fwd_fast(const AttnShape& s, const fwd::FwdArgs& a, hipStream_t st);
+}  // namespace f32
+
+namespace fwd {
 
 namespace {
 

@@ -37,7 +37,9 @@ int fwd_rows_per_block(const AttnShape& s);
 int dkdv_keys_per_block(const AttnShape& s);
 // Number of head groups the dK/dV pass is split into (1 = no partials).
 int dkdv_splits(const AttnShape& s);
-// bf16 with D % 8 == 0 and 32 < D <= 256 takes the direct-to-LDS kernels.
+// The direct-to-LDS kernels with work units: bf16 with D % 8 == 0,
+// 32 < D <= 256 and one K/V sequence stride, and fp32 with D % 4 == 0,
+// 32 < D <= 256 (f32::fast_path).
 bool bwd_fast_path(const AttnShape& s);
 
 // Work decomposition of the bf16 fast backward.  Per (batch, kv head) the
@@ -52,6 +54,9 @@ bool bwd_fast_path(const AttnShape& s);
 // LDS arrays of this length.  The planners size units so that no tile goes
 // past it; the C ABI rejects a shape whose plan would (MFT_ERR_UNSUPPORTED).
 constexpr int kSplitMaxSlots = 64;
+
+// Compute units of the current device (cached; 256 when the query fails).
+int device_cus();
 
 struct BwdPlan {
     UnitSplit kv, q;  // units per (batch, kv head) and per (batch, query head)
@@ -69,6 +74,11 @@ constexpr int kFwdIterCost = 1, kKvIterCost = 2, kQIterCost = 3;
 inline int fwd_tile_cost(int64_t D) { return D >= 256 ? 2 : 0; }
 inline int kv_tile_cost(int64_t D) { return D >= 256 ? 11 : 0; }
 inline int q_tile_cost(int64_t D) { return D >= 256 ? 13 : 0; }
+// fp32 iterations take about 16 times as long as bf16 ones (the fp32 MFMA
+// rate), so a tile's fixed costs are left out for fp32.
+inline int fwd_tile_cost(const AttnShape& s) { return s.bf16 ? fwd_tile_cost(s.D) : 0; }
+inline int kv_tile_cost(const AttnShape& s) { return s.bf16 ? kv_tile_cost(s.D) : 0; }
+inline int q_tile_cost(const AttnShape& s) { return s.bf16 ? q_tile_cost(s.D) : 0; }
 // The fewest iterations the planners give a unit.
 constexpr int kMinUnitIters = 4;
 BwdPlan plan_bwd_fast(const AttnShape& s);
@@ -81,8 +91,6 @@ struct BwdLayout {
 };
 BwdLayout bwd_layout(const AttnShape& s);
 
-// Compute units of the current device (cached; 256 when the query fails).
-int device_cus();
 
 // Workgroups of the bf16 fast kernels that one CU holds at once, which the
 // planners size their launches for.  Registers decide it (LDS allows more):
@@ -91,6 +99,23 @@ int device_cus();
 // wider kernels keep one wave per SIMD.
 inline int fwd_wgs_per_cu(int64_t D) { return D <= 128 ? 2 : 1; }
 inline int bwd_wgs_per_cu(int64_t D) { return D <= 64 ? 2 : 1; }
+
+// fp32 fast path (attn_f32_fast.hip): fp32 operands with D % 4 == 0 and
+// 32 < D <= 256 run the same work units, each unit as kF32Halves workgroups
+// (one per 64-row or 64-key half of its 128-row tiles).  Registers decide
+// how many share a CU as for bf16 (the forward fits 256 per lane up to
+// D = 128, the backward up to D = 64; LDS, 128 KiB at D = 256, allows as many).
+namespace f32 {
+bool fast_path(const AttnShape& s);
+}
+constexpr int kF32Halves = 2;
+// Units a launch of the fast forward / backward holds at once (one round).
+inline int64_t fwd_unit_slots(const AttnShape& s) {
+    return (int64_t)device_cus() * fwd_wgs_per_cu(s.D) / (s.bf16 ? 1 : kF32Halves);
+}
+inline int64_t bwd_unit_slots(const AttnShape& s) {
+    return (int64_t)device_cus() * bwd_wgs_per_cu(s.D) / (s.bf16 ? 1 : kF32Halves);
+}
 
 // Balanced forward (bf16 fast path): per (batch, head) the iterations
 // (128-row query tile, 64-key tile) are cut into units of about equal cost
