@@ -697,30 +697,33 @@ __global__ __launch_bounds__(256) void attn_bwd_main_bf16_fast(BwdArgs a) {
 }
 
 // REDUCE: sum the partial slots of every split tile in unit order.  One
-// workgroup per (batch, head, 128-row tile, 16-row group) of the dK/dV role
-// (rows = keys; dK and dV) and then of the dQ role (rows = queries);
-// workgroups of unsplit tiles return at once.
-constexpr int kRedRows = 16, kRedMaxSlots = kSplitMaxSlots, kRedBatch = 4;
+// workgroup per (batch, head, 128-row tile, group of merge_rows(D) rows) of
+// the dK/dV role (rows = keys; dK and dV) and then of the dQ role (rows =
+// queries); workgroups of unsplit tiles return at once.
+constexpr int kRedMaxSlots = kSplitMaxSlots, kRedBatch = 4;
 
+// dst row r (r < rows, row stride ld) = sum over the slots, in slot order, of
+// row row0 + r of the slot tiles (rows <= RW = merge_rows(D)).  256 / RW
+// threads share a row: thread t sums its row's 16-byte chunks
+// t % (256 / RW) + (256 / RW) j (j < 4), kRedBatch slots' loads in flight
+// together.
 __device__ __forceinline__ void reduce_rows(const float* part, const int64_t* slot_of, int nsl, int64_t tile_elems,
-                                            int64_t row_in_tile, int D, float* dst) {
-    // thread -> 16-byte column chunks (tid % 16) + 16 j of row tid / 16
-    const int cl = threadIdx.x % 16, cg = D / 4;
-    constexpr int MAXJ = 256 / 4 / 16;
+                                            int row0, int rows, int D, float* dst, int64_t ld) {
+    constexpr int MAXJ = 4;
+    const int tpr = 256 / merge_rows(D), r = (int)threadIdx.x / tpr, cl = (int)threadIdx.x % tpr, cg = D / 4;
+    if (r >= rows) return;
     f32x4 acc[MAXJ];
 #pragma unroll
     for (int j = 0; j < MAXJ; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // kRedBatch slots' loads in flight before they are summed (in slot order):
-    // one memory round trip per batch instead of one per slot.
     for (int p0 = 0; p0 < nsl; p0 += kRedBatch) {
         f32x4 x[kRedBatch][MAXJ];
 #pragma unroll
         for (int q = 0; q < kRedBatch; ++q) {
             if (p0 + q >= nsl) break;
-            const float* src = part + slot_of[p0 + q] * tile_elems + row_in_tile * D;
+            const float* src = part + slot_of[p0 + q] * tile_elems + (int64_t)(row0 + r) * D;
 #pragma unroll
             for (int j = 0; j < MAXJ; ++j) {
-                const int c = cl + 16 * j;
+                const int c = cl + tpr * j;
                 x[q][j] = c < cg ? *reinterpret_cast<const f32x4*>(src + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
             }
         }
@@ -731,18 +734,18 @@ __device__ __forceinline__ void reduce_rows(const float* part, const int64_t* sl
             for (int j = 0; j < MAXJ; ++j) acc[j] += x[q][j];
         }
     }
+    float* out = dst + (int64_t)r * ld;
 #pragma unroll
     for (int j = 0; j < MAXJ; ++j) {
-        const int c = cl + 16 * j;
-        if (c < cg) *reinterpret_cast<f32x4*>(dst + 4 * c) = acc[j];
+        const int c = cl + tpr * j;
+        if (c < cg) *reinterpret_cast<f32x4*>(out + 4 * c) = acc[j];
     }
 }
 
 template <bool CAUSAL>
 __global__ __launch_bounds__(256) void attn_bwd_fast_reduce(BwdArgs a) {
-    constexpr int RG = 128 / kRedRows;
     __shared__ int64_t slot_of[kRedMaxSlots];
-    const int S = a.S, D = a.D, nt = (S + 127) / 128;
+    const int S = a.S, D = a.D, nt = (S + 127) / 128, RW = merge_rows(D), RG = 128 / RW;
     const int64_t kv_blocks = (int64_t)a.B * a.Hkv * nt * RG;
     int64_t blk = blockIdx.x;
     const bool kv = blk < kv_blocks;
@@ -752,26 +755,24 @@ __global__ __launch_bounds__(256) void attn_bwd_fast_reduce(BwdArgs a) {
     const UnitSplit us = kv ? a.kv_us : a.q_us;
     int u0;
     const int nsl = tile_units(tiles, us, t, &u0);
-    const int r0 = t * 128 + rg * kRedRows;
+    const int r0 = t * 128 + rg * RW;
     if (nsl <= 1 || r0 >= S) return;
     const bool starts = unit_first(tiles, us, u0) == tiles.start(t);
     const int64_t head_slots = (int64_t)bh * 2 * us.units;
     if ((int)threadIdx.x < nsl) slot_of[threadIdx.x] = head_slots + split_slot(u0 + threadIdx.x, u0, starts);
     __syncthreads();
-    const int r = threadIdx.x / 16;
-    if (r0 + r >= S) return;
-    const int64_t row = r0 + r;
-    const int64_t rit = rg * kRedRows + r;  // row inside the tile
+    const int rows = min(RW, S - r0), rit = rg * RW;  // rows, first row inside the tile
     if (kv) {
         // slot layout [dK rows 0..127][dV rows 0..127]
         const int bb = bh / a.Hkv, hk = bh % a.Hkv;
-        reduce_rows(a.kv_part, slot_of, nsl, 2 * 128 * (int64_t)D, rit, D,
-                    a.dk + a.sdk.at(bb, hk) + row * a.sdk.s);
-        reduce_rows(a.kv_part, slot_of, nsl, 2 * 128 * (int64_t)D, 128 + rit, D,
-                    a.dv + a.sdv.at(bb, hk) + row * a.sdv.s);
+        reduce_rows(a.kv_part, slot_of, nsl, 2 * 128 * (int64_t)D, rit, rows, D,
+                    a.dk + a.sdk.at(bb, hk) + (int64_t)r0 * a.sdk.s, a.sdk.s);
+        reduce_rows(a.kv_part, slot_of, nsl, 2 * 128 * (int64_t)D, 128 + rit, rows, D,
+                    a.dv + a.sdv.at(bb, hk) + (int64_t)r0 * a.sdv.s, a.sdv.s);
     } else {
         const int bb = bh / a.Hq, h = bh % a.Hq;
-        reduce_rows(a.q_part, slot_of, nsl, 128 * (int64_t)D, rit, D, a.dq + a.sdq.at(bb, h) + row * a.sdq.s);
+        reduce_rows(a.q_part, slot_of, nsl, 128 * (int64_t)D, rit, rows, D,
+                    a.dq + a.sdq.at(bb, h) + (int64_t)r0 * a.sdq.s, a.sdq.s);
     }
 }
 
@@ -829,7 +830,7 @@ hipError_t launch_bwd_fast(const AttnShape& s, BwdArgs a, int stages, hipStream_
 #undef MFT_BWD_LAUNCH
     if ((stages & BWD_STAGE_REDUCE) && (pl.kv_parts_max > 1 || pl.q_parts_max > 1)) {
         const int64_t nt = (s.S + 127) / 128;
-        const int64_t blocks = (s.B * s.Hkv + s.B * s.Hq) * nt * (128 / kRedRows);
+        const int64_t blocks = (s.B * s.Hkv + s.B * s.Hq) * nt * (128 / merge_rows(s.D));
         if (s.causal)
             hipLaunchKernelGGL(attn_bwd_fast_reduce<true>, dim3((unsigned)blocks), dim3(256), 0, st, a);
         else

@@ -811,7 +811,7 @@ hipError_t launch_bwd(const AttnShape& s, const BwdArgs& a, int stages, hipStrea
 #undef MFT_F32_LAUNCH
     if ((stages & BWD_STAGE_REDUCE) && (pl.kv_parts_max > 1 || pl.q_parts_max > 1)) {
         const int64_t nt = (s.S + 127) / 128;
-        const int64_t blocks = (s.B * s.Hkv + s.B * s.Hq) * nt * (128 / bwd::kRedRows);
+        const int64_t blocks = (s.B * s.Hkv + s.B * s.Hq) * nt * (128 / merge_rows(s.D));
         if (s.causal)
             hipLaunchKernelGGL(bwd::attn_bwd_fast_reduce<true>, dim3((unsigned)blocks), dim3(256), 0, st, a);
         else

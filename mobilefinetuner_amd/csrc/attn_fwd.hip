@@ -33,7 +33,6 @@ using fwd::FwdArgs;
 using fwd::kFwdBM;
 using fwd::kFwdBN;
 using fwd::kCombBatch;
-using fwd::kCombRows;
 using fwd::kCombMaxSlots;
 using fwd::launch_fwd_fast64;
 using fwd::launch_fwd_fast128;
@@ -241,34 +240,36 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
 // Merge the partial slots of every split query tile, in slot order:
 // m = max_i m_i, l = sum_i l_i 2^(m_i - m), O = sum_i O_i 2^(m_i - m) / l,
 // LSE = (m + log2 l) ln 2.  One workgroup per (batch, head, query tile,
-// 16-row group); workgroups of tiles that were not split return at once.
-// The per-(slot, row) weights go through LDS, then each thread sums 16-byte
-// column chunks over the slots.
-template <bool CAUSAL, typename T>
+// group of RW = merge_rows(D) rows); workgroups of tiles that were not split
+// return at once.  The per-(slot, row) weights go through LDS (sized by RW),
+// then 256 / RW threads share a row: thread t sums its row's 16-byte chunks
+// t % (256 / RW) + (256 / RW) j over the slots, kCombBatch slots' loads in
+// flight together.
+template <bool CAUSAL, typename T, int RW>
 __global__ __launch_bounds__(256) void attn_fwd_combine(FwdArgs a) {
-    constexpr int BM = kFwdBM, RG = BM / kCombRows;
-    __shared__ float wgt[kCombMaxSlots][kCombRows];
-    __shared__ float2 ml[kCombMaxSlots][kCombRows];
-    __shared__ float inv_l[kCombRows];
+    constexpr int BM = kFwdBM, RG = BM / RW, TPR = 256 / RW, MAXJ = 4;
+    __shared__ float wgt[kCombMaxSlots][RW];
+    __shared__ float2 ml[kCombMaxSlots][RW];
+    __shared__ float inv_l[RW];
+    __shared__ int64_t slot_of[kCombMaxSlots];
     const int S = a.S, D = a.D;
     const int nqt = (S + BM - 1) / BM;
     const int rg = (int)blockIdx.x % RG, qt = ((int)blockIdx.x / RG) % nqt, bh = (int)blockIdx.x / (RG * nqt);
     const FastTiles tiles{S, CAUSAL, a.window, a.group, 0};
     int u0;
     const int nsl = tile_units(tiles, a.us, qt, &u0);
-    const int r0 = qt * BM + rg * kCombRows;
+    const int r0 = qt * BM + rg * RW;
     if (nsl <= 1 || r0 >= S) return;
     const bool starts = unit_first(tiles, a.us, u0) == tiles.start(qt);
     const int64_t head_slots = (int64_t)bh * 2 * a.us.units;
-    __shared__ int64_t slot_of[kCombMaxSlots];
-    const int rows = min(kCombRows, S - r0);
+    const int rows = min(RW, S - r0), rit = rg * RW;  // rows, first row inside the tile
     const int tid = threadIdx.x;
     if (tid < nsl) slot_of[tid] = head_slots + split_slot(u0 + tid, u0, starts);
     __syncthreads();
     // (running max, sum) of every (slot, row), loaded in parallel.
-    for (int i = tid; i < nsl * kCombRows; i += 256) {
-        const int p = i / kCombRows, r = i % kCombRows;
-        ml[p][r] = *reinterpret_cast<const float2*>(a.part_ml + (slot_of[p] * BM + rg * kCombRows + r) * 2);
+    for (int i = tid; i < nsl * rows; i += 256) {
+        const int p = i / rows, r = i - p * rows;
+        ml[p][r] = *reinterpret_cast<const float2*>(a.part_ml + (slot_of[p] * BM + rit + r) * 2);
     }
     __syncthreads();
     if (tid < rows) {
@@ -285,17 +286,12 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(FwdArgs a) {
         if (a.lse) a.lse[(int64_t)bh * S + r0 + tid] = l > 0.f ? (m + log2f(l)) * kLn2 : INFINITY;
     }
     __syncthreads();
-    // Thread -> row tid / 16, 16-byte column chunks (tid % 16) + 16 j: the
-    // chunks' loads of one slot are independent and issued together.
-    const int r = tid / 16, cl = tid % 16, cg = D / 4;  // fast path: D % 8 == 0
+    const int r = tid / TPR, cl = tid % TPR, cg = D / 4;  // fast path: D % 4 == 0
     if (r >= rows) return;
-    constexpr int MAXJ = 256 / 4 / 16;
-    const int64_t rr = rg * kCombRows + r;
+    const int64_t rr = rit + r;
     f32x4 acc[MAXJ];
 #pragma unroll
     for (int j = 0; j < MAXJ; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // kCombBatch slots' loads in flight before they are summed (in slot
-    // order): one memory round trip per batch instead of one per slot.
     for (int p0 = 0; p0 < nsl; p0 += kCombBatch) {
         f32x4 x[kCombBatch][MAXJ];
 #pragma unroll
@@ -304,7 +300,7 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(FwdArgs a) {
             const float* src = a.part_o + (slot_of[p0 + q] * BM + rr) * D;
 #pragma unroll
             for (int j = 0; j < MAXJ; ++j) {
-                const int c = cl + 16 * j;
+                const int c = cl + TPR * j;
                 x[q][j] = c < cg ? *reinterpret_cast<const f32x4*>(src + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
             }
         }
@@ -320,7 +316,7 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(FwdArgs a) {
     T* O = (T*)a.o + a.so.at(bh / a.Hq, bh % a.Hq) + (int64_t)(r0 + r) * a.so.s;
 #pragma unroll
     for (int j = 0; j < MAXJ; ++j) {
-        const int c = cl + 16 * j;
+        const int c = cl + TPR * j;
         if (c < cg) store4<T>(O, 4 * c, D, acc[j][0] * il, acc[j][1] * il, acc[j][2] * il, acc[j][3] * il, true);
     }
 }
@@ -360,18 +356,25 @@ hipError_t launch_fwd_dispatch(const AttnShape& s, FwdArgs a, hipStream_t st) {
 
 namespace fwd {
 hipError_t launch_fwd_combine(const AttnShape& s, const FwdArgs& a, hipStream_t st) {
-    const dim3 cgrid((unsigned)(s.B * s.Hq * a.n_qtiles * (kFwdBM / kCombRows)));
+    const int rw = merge_rows(s.D);
+    const dim3 cgrid((unsigned)(s.B * s.Hq * a.n_qtiles * (kFwdBM / rw)));
+#define MFT_COMBINE(T, RW)                                                                      \
+    do {                                                                                        \
+        if (s.causal)                                                                           \
+            hipLaunchKernelGGL((attn_fwd_combine<true, T, RW>), cgrid, dim3(256), 0, st, a);    \
+        else                                                                                    \
+            hipLaunchKernelGGL((attn_fwd_combine<false, T, RW>), cgrid, dim3(256), 0, st, a);   \
+    } while (0)
     if (s.bf16) {
-        if (s.causal)
-            hipLaunchKernelGGL((attn_fwd_combine<true, bf16>), cgrid, dim3(256), 0, st, a);
-        else
-            hipLaunchKernelGGL((attn_fwd_combine<false, bf16>), cgrid, dim3(256), 0, st, a);
+        if (rw == 16) MFT_COMBINE(bf16, 16);
+        else if (rw == 32) MFT_COMBINE(bf16, 32);
+        else MFT_COMBINE(bf16, 64);
     } else {
-        if (s.causal)
-            hipLaunchKernelGGL((attn_fwd_combine<true, float>), cgrid, dim3(256), 0, st, a);
-        else
-            hipLaunchKernelGGL((attn_fwd_combine<false, float>), cgrid, dim3(256), 0, st, a);
+        if (rw == 16) MFT_COMBINE(float, 16);
+        else if (rw == 32) MFT_COMBINE(float, 32);
+        else MFT_COMBINE(float, 64);
     }
+#undef MFT_COMBINE
     return hipGetLastError();
 }
 hipError_t launch_fwd_fast64(const AttnShape& s, FwdArgs a, hipStream_t st) { return launch_fwd_fast_t<64>(s, a, st); }

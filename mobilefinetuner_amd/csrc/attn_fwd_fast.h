@@ -54,7 +54,7 @@ constexpr int kFwdBM = 128, kFwdBN = 64;
 // for D = 256: the fp32 partial O or the bf16 O); smaller head dims use
 // vmcnt(0) (see attn_fwd_bf16_split).
 constexpr int kEpilogueStores = 32;
-constexpr int kCombRows = 16, kCombMaxSlots = kSplitMaxSlots, kCombBatch = 4;
+constexpr int kCombMaxSlots = kSplitMaxSlots, kCombBatch = 4;
 
 // The launches of the fast path for one padded head dim (attn_fwd.hip,
 // attn_fwd_fast256.hip).

@@ -54,6 +54,12 @@ bool bwd_fast_path(const AttnShape& s);
 // LDS arrays of this length.  The planners size units so that no tile goes
 // past it; the C ABI rejects a shape whose plan would (MFT_ERR_UNSUPPORTED).
 constexpr int kSplitMaxSlots = 64;
+// Rows of a split tile that one workgroup of the merge kernels (REDUCE and
+// the forward combine) takes: 16 KiB of fp32 row data per slot, so 16 rows
+// at a padded head dim of 256, 32 at 128 and 64 below.  Each of its 256
+// threads then sums four 16-byte chunks of the rows, and narrow heads do not
+// pay one workgroup's fixed cost per 4 KiB.
+__host__ __device__ inline int merge_rows(int64_t D) { return D > 128 ? 16 : D > 64 ? 32 : 64; }
 
 // Compute units of the current device (cached; 256 when the query fails).
 int device_cus();

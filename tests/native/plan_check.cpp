@@ -71,7 +71,8 @@ int main() {
         for (const auto& sh : shapes)
             for (int W : windows)
                 for (int causal = 0; causal < 2; ++causal)
-                    for (int D : dims) {
+                    for (int D : dims)
+                    for (int bf = 0; bf < 2; ++bf) {
                         if (W && !causal) continue;
                         mft::AttnShape s{};
                         s.B = sh[0];
@@ -81,15 +82,15 @@ int main() {
                         s.D = D;
                         s.scale = 0.1f;
                         s.causal = causal != 0;
-                        s.bf16 = true;
+                        s.bf16 = bf != 0;  // fp32: the fp32 fast path's units (two workgroups each)
                         s.window = W < S ? W : 0;
                         s.contiguous = true;
                         const mft::FwdPlan f = mft::plan_fwd_split(s);
                         const mft::BwdPlan b = mft::plan_bwd_fast(s);
                         if (f.parts_max > mft::kSplitMaxSlots || b.kv_parts_max > mft::kSplitMaxSlots ||
                             b.q_parts_max > mft::kSplitMaxSlots) {
-                            std::printf("OVER S=%lld B=%d Hq=%d Hkv=%d D=%d causal=%d W=%d fwd=%d kv=%d q=%d\n", S,
-                                        sh[0], sh[1], sh[2], D, causal, W, f.parts_max, b.kv_parts_max,
+                            std::printf("OVER S=%lld B=%d Hq=%d Hkv=%d D=%d bf16=%d causal=%d W=%d fwd=%d kv=%d q=%d\n", S,
+                                        sh[0], sh[1], sh[2], D, bf, causal, W, f.parts_max, b.kv_parts_max,
                                         b.q_parts_max);
                             return 1;
                         }
