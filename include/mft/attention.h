@@ -105,9 +105,11 @@ typedef struct {
 
 /* Workspace bytes of the calls.
  *   fwd: fp32 partial output tiles of query tiles whose key range is split
- *        across work units (bf16 fast path; 0 for the other paths).  The
- *        forward also accepts workspace = NULL and then runs one workgroup per
- *        query tile (same results, no cross-unit load balancing).
+ *        across work units (the fast paths: bf16 with D % 8 == 0 and fp32
+ *        with D % 4 == 0, 32 < D <= 256; 0 for the others).  The forward also
+ *        accepts workspace = NULL and then runs one workgroup per query tile
+ *        (same results within the dtype's tolerance; no cross-unit load
+ *        balancing, and for fp32 the general kernels).
  *   bwd: per-row softmax terms and the fp32 partials of split tiles.
  * Replaces: nothing (the reference allocates from its pool implicitly). */
 mft_status mft_attn_workspace_size(const mft_attn_desc* desc, size_t* fwd_bytes,

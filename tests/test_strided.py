@@ -14,7 +14,9 @@ CASES = [
     (2, 4, 1, 300, 256, "bf16", True, 0, None),      # fast path, split tiles
     (1, 8, 2, 520, 128, "bf16", True, 64, None),     # window geometry
     (2, 4, 2, 200, 64, "bf16", True, 0, [200, 77]),  # padding
-    (1, 4, 4, 130, 96, "f32", True, 0, None),        # general fp32 path
+    (1, 4, 4, 130, 96, "f32", True, 0, None),        # fp32 fast path, partial tiles
+    (1, 4, 1, 256, 256, "f32", True, 0, None),       # fp32 fast path, whole tiles (direct-load offsets)
+    (2, 2, 2, 100, 20, "f32", True, 0, [100, 37]),   # general fp32 path (D <= 32), padding
     (2, 2, 1, 96, 40, "bf16", False, 0, [96, 0]),    # general bf16 path, rows with no key
 ]
 
