@@ -272,13 +272,22 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_split(FwdArgs a) {
                     }
                 mx = fmaxf(mx, __shfl_xor(mx, 16));
                 mx = fmaxf(mx, __shfl_xor(mx, 32));
-                const float m_new = fmaxf(m_run, mx);
-                const float msub = m_new == -INFINITY ? 0.f : m_new;
-                const float alpha = fast_exp2(m_run - msub);
-                m_run = m_new;
-                l_run *= alpha;
+                // Lazy rescaling (as the bf16 kernels): the reference point
+                // m_run moves, and O and l are rescaled, only when some row
+                // of the wave sees a max above m_run + 8, so exp2 arguments
+                // stay <= 8.  O = acc / l and LSE = m_run + log2(l) are the
+                // same for any reference point; most tiles skip the rescale
+                // of the accumulators (which live in AGPRs: a read, a
+                // multiply and a write each).
+                if (__any(mx > m_run + kLazyRescale)) {
+                    const float m_new = fmaxf(m_run, mx);
+                    const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.f : m_new));
+                    m_run = m_new;
+                    l_run *= alpha;
 #pragma unroll
-                for (int t = 0; t < 4 * NU; ++t) oacc[t] *= alpha;
+                    for (int t = 0; t < 4 * NU; ++t) oacc[t] *= alpha;
+                }
+                const float msub = m_run == -INFINITY ? 0.f : m_run;
 #pragma unroll
                 for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
