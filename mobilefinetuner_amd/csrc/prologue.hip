@@ -349,6 +349,17 @@ __global__ __launch_bounds__(1024) void prologue_dw_reduce_kernel(const float* p
 // slot and comes over by a shuffle.  Row sums are shuffles inside the row's
 // LPR-lane group.  Same arithmetic as the kernels above, element by element.
 
+// Row order of the 16-byte-lane kernels: head fastest, r -> (b, s, h) with
+// h = r % H, so that a lane's consecutive row groups are heads of one
+// position and share its RoPE angles (sincosf once per position and pair).
+__device__ __forceinline__ RowAddr row_addr_hf(const PrologueArgs& a, int64_t r) {
+    const int h = (int)(r % a.H);
+    const int64_t bs = r / a.H;
+    return RowAddr{bs / a.S, h, (int)(bs % a.S)};
+}
+// Row groups per lane of the forward (all loaded before any is computed).
+constexpr int kFwdVecGroups = 2;
+
 template <int LPR> __device__ __forceinline__ double group_sum(double v) {
 #pragma unroll
     for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
@@ -357,23 +368,26 @@ template <int LPR> __device__ __forceinline__ double group_sum(double v) {
 
 // Forward, 16 bytes per lane and row: a lane holds EPL / 2 elements of the
 // first half (d = q0 .. q0 + EPL/2 - 1) and their rotate-half partners
-// (d + D/2), so each RoPE pair is rotated inside one lane with one sincosf
-// per pair and no shuffle; only the norm's sum of squares crosses lanes.
+// (d + D/2), so each RoPE pair is rotated inside one lane and no shuffle;
+// only the norm's sum of squares crosses lanes.  A lane takes GROUPS
+// consecutive rows (row_addr_hf order) and evaluates sincosf only when a
+// row's position differs from the previous row's.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void prologue_fwd_vec(PrologueArgs a) {
 #pragma clang fp contract(off)
     constexpr int EPL = 16 / (int)sizeof(T), H2 = EPL / 2, LPR = D / EPL, RPI = 64 / LPR, HALF = D / 2;
     static_assert(LPR >= 2 && LPR <= 64, "a row spans 2..64 lanes");
-    constexpr int GROUPS = 2;  // row groups per wave, all loaded before any is computed
+    constexpr int GROUPS = kFwdVecGroups;
     const int lane = threadIdx.x & 63, gl = lane % LPR;
     const int q0 = gl * H2;  // this lane's first element of the first half
-    const int64_t wave_row0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * (RPI * GROUPS);
+    // the lane's rows: lane_row0 + g, g < GROUPS
+    const int64_t lane_row0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * (RPI * GROUPS) + (lane / LPR) * GROUPS;
     float v[GROUPS][2][H2];  // [group][half][element]
     RowAddr ra[GROUPS];
 #pragma unroll
     for (int g = 0; g < GROUPS; ++g) {
-        const int64_t r = wave_row0 + g * RPI + lane / LPR;
-        ra[g] = row_addr(a, r < a.rows ? r : 0);
+        const int64_t r = lane_row0 + g;
+        ra[g] = row_addr_hf(a, r < a.rows ? r : 0);
         if (r < a.rows) {
             const T* x = (const T*)a.x + a.sx.at(ra[g].b, ra[g].h) + (int64_t)ra[g].s * a.sx.s + q0;
             Vec<T, H2>::load(x, v[g][0]);
@@ -383,9 +397,11 @@ __global__ __launch_bounds__(256) void prologue_fwd_vec(PrologueArgs a) {
             for (int e = 0; e < H2; ++e) v[g][0][e] = v[g][1][e] = 0.f;
         }
     }
+    float cs[H2], sn[H2];
+    int s_cur = -1;  // position whose angles cs, sn hold
 #pragma unroll
     for (int g = 0; g < GROUPS; ++g) {
-        const int64_t r = wave_row0 + g * RPI + lane / LPR;
+        const int64_t r = lane_row0 + g;
         if (a.norm != PROLOGUE_NORM_NONE) {
             double ss = 0.0;
 #pragma unroll
@@ -410,14 +426,17 @@ __global__ __launch_bounds__(256) void prologue_fwd_vec(PrologueArgs a) {
         }
         float y[2][H2];
         if (a.rope) {
+            if (ra[g].s != s_cur) {
+                s_cur = ra[g].s;
+#pragma unroll
+                for (int e = 0; e < H2; ++e) sincosf((float)s_cur * a.inv_freq[q0 + e], &sn[e], &cs[e]);
+            }
 #pragma unroll
             for (int e = 0; e < H2; ++e) {
-                float c, sn;
-                sincosf((float)ra[g].s * a.inv_freq[q0 + e], &sn, &c);
                 const float x1 = v[g][0][e], x2 = v[g][1][e];
                 // first half: x1 * c - x2 * s; second half: x1 * s + x2 * c
-                y[0][e] = x1 * c - x2 * sn;
-                y[1][e] = x1 * sn + x2 * c;
+                y[0][e] = x1 * cs[e] - x2 * sn[e];
+                y[1][e] = x1 * sn[e] + x2 * cs[e];
             }
         } else {
 #pragma unroll
@@ -434,8 +453,10 @@ __global__ __launch_bounds__(256) void prologue_fwd_vec(PrologueArgs a) {
 // Backward with fp32 dy/dx rows as the lane grid (EPL = 4 per lane, LPR =
 // D / 4): a lane holds 2 elements of the first half and their rotate-half
 // partners, so R^T dy is applied inside the lane.  Rows per workgroup as
-// prologue_bwd_blocks counts them; dL/dw is summed per lane over its rows,
-// then over the row groups of the wave and the 4 waves in fixed order.
+// prologue_bwd_blocks counts them, GROUPS consecutive rows per lane in
+// row_addr_hf order (sincosf once per position, as in the forward); dL/dw is
+// summed per lane over its rows, then over the lanes of the wave that share
+// its columns and the 4 waves in fixed order.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void prologue_bwd_vec(PrologueArgs a) {
 #pragma clang fp contract(off)
@@ -448,15 +469,16 @@ __global__ __launch_bounds__(256) void prologue_bwd_vec(PrologueArgs a) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, gl = lane % LPR;
     const int q0 = gl * H2;  // this lane's first element of the first half
     const bool norm = a.norm != PROLOGUE_NORM_NONE;
-    const int64_t wave_row0 = (int64_t)blockIdx.x * ROWS_WG + w * (RPI * GROUPS);
+    // the lane's rows: lane_row0 + g, g < GROUPS
+    const int64_t lane_row0 = (int64_t)blockIdx.x * ROWS_WG + w * (RPI * GROUPS) + (lane / LPR) * GROUPS;
     // every row group's loads first; [group][half][element]
     float gv[GROUPS][2][H2], xv[GROUPS][2][H2];
     RowAddr ra[GROUPS];
 #pragma unroll
     for (int g = 0; g < GROUPS; ++g) {
-        const int64_t r = wave_row0 + g * RPI + lane / LPR;
+        const int64_t r = lane_row0 + g;
         const bool live = r < a.rows;
-        ra[g] = row_addr(a, live ? r : 0);
+        ra[g] = row_addr_hf(a, live ? r : 0);
         if (live) {
             const float* dy = a.dy + a.sdy.at(ra[g].b, ra[g].h) + (int64_t)ra[g].s * a.sdy.s + q0;
             Vec<float, H2>::load(dy, gv[g][0]);
@@ -484,20 +506,25 @@ __global__ __launch_bounds__(256) void prologue_bwd_vec(PrologueArgs a) {
             const double wv = norm ? (double)a.w[hf * HALF + q0 + e] : 0.0;
             we[hf][e] = a.norm == PROLOGUE_NORM_GEMMA ? 1.0 + wv : wv;
         }
+    float cs[H2], sn[H2];
+    int s_cur = -1;  // position whose angles cs, sn hold
 #pragma unroll
     for (int g = 0; g < GROUPS; ++g) {
-        const int64_t r = wave_row0 + g * RPI + lane / LPR;
+        const int64_t r = lane_row0 + g;
         const bool live = r < a.rows;
         // gradient at the norm's output: R^T dy
         if (a.rope) {
+            if (ra[g].s != s_cur) {
+                s_cur = ra[g].s;
+#pragma unroll
+                for (int e = 0; e < H2; ++e) sincosf((float)s_cur * a.inv_freq[q0 + e], &sn[e], &cs[e]);
+            }
 #pragma unroll
             for (int e = 0; e < H2; ++e) {
-                float c, sn;
-                sincosf((float)ra[g].s * a.inv_freq[q0 + e], &sn, &c);
                 const float g1 = gv[g][0][e], g2 = gv[g][1][e];
                 // first half: g1 c + g2 s; second half: -g1 s + g2 c
-                gv[g][0][e] = g1 * c + g2 * sn;
-                gv[g][1][e] = -g1 * sn + g2 * c;
+                gv[g][0][e] = g1 * cs[e] + g2 * sn[e];
+                gv[g][1][e] = -g1 * sn[e] + g2 * cs[e];
             }
         }
         if (norm) {
@@ -595,7 +622,7 @@ bool launch_vec(const PrologueArgs& a, bool bwd, hipStream_t st, hipError_t* e) 
             return false;
         } else {
             if (!rows_aligned(a.x, a.sx, esz, 16) || !rows_aligned(a.y, a.sy, esz, 16)) return false;
-            const int64_t per_block = 4 * (64 / LPR) * 2;
+            const int64_t per_block = 4 * (64 / LPR) * kFwdVecGroups;
             hipLaunchKernelGGL((prologue_fwd_vec<T, D>), dim3((unsigned)((a.rows + per_block - 1) / per_block)),
                                dim3(256), 0, st, a);
         }
