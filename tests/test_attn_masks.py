@@ -38,6 +38,9 @@ CASES = [
     (2, 4, 1, 512, 128, "bf16", True, 96, [100, 512]),
     (1, 2, 1, 260, 256, "bf16", True, 32, [40]),
     (2, 2, 2, 190, 64, "f32", True, 20, [30, 0]),
+    # fp32 whole tiles (S a multiple of 64, D = 256 / 128): the direct loads' fixed offsets
+    (1, 4, 1, 512, 256, "f32", True, 100, None),
+    (2, 2, 1, 256, 128, "f32", True, 0, [256, 100]),
 ]
 
 
