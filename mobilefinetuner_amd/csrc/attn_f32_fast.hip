@@ -510,9 +510,8 @@ __device__ __forceinline__ void dkdv_f32_body(const BwdArgs& a, float* smem, int
                     dp[qa][r] = p * (dp[qa][r] - d4[r]);
                 }
             }
-            // dV(u, j) += P^T dO, dK(u, j) += dS^T Q: step (qa, r, u) takes query
-            // row 16 qa + 4 g + r of the block and the d-range of tiles (u, *)
-            // step (qa, r, u): [dO, Q] of row 16 qa + 4 g + r, chunk 16 u + i
+            // dV(u, j) += P^T dO, dK(u, j) += dS^T Q: step (qa, r, u) reads dO and
+            // Q of block row 16 qa + 4 g + r, chunk 16 u + i (the d-range of tiles (u, *))
             chain<8 * NU, kPF, 2, 8, Ops<2>>(
                 [&](int st8) {
                     const int row = 16 * (st8 / (4 * NU)) + 4 * g + ((st8 / NU) & 3), u = st8 % NU;
