@@ -183,7 +183,7 @@ hipError_t launch_bwd_fast_256(const AttnShape& s, const BwdArgs& a, int stages,
 }  // namespace bwd
 
 namespace f32 {
-// The fp32 fast backward (attn_f32_fast.hip).
+// The fp32 fast backward (attn_f32_fast.h).
 hipError_t launch_bwd_fast(const AttnShape& s, const bwd::BwdArgs& a, int stages, hipStream_t st);
 }  // namespace f32
 

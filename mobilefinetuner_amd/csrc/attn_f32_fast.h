@@ -30,12 +30,15 @@
 // patterns (16 rows x one chunk, one row x 16 chunks per 16 lanes) then hit
 // 16 distinct bank groups.  They are filled with global_load_lds_dwordx4 by
 // the bf16 path's TileDma, viewing an fp32 row as 2 * DPF bf16 columns.
+//
+// The kernels are instantiated per padded head dim in attn_f32_fast64.hip,
+// attn_f32_fast128.hip and attn_f32_fast256.hip, so they compile in parallel.
+#pragma once
 #include "attn_bwd_fast.h"
 #include "attn_fwd_fast.h"
 
 namespace mft {
 namespace f32 {
-namespace {
 
 using bwd::BwdArgs;
 using fwd::FwdArgs;
@@ -828,21 +831,21 @@ hipError_t launch_bwd(const AttnShape& s, const BwdArgs& a, int stages, hipStrea
     return hipGetLastError();
 }
 
-}  // namespace
-
-bool fast_path(const AttnShape& s) { return !s.bf16 && s.D % 4 == 0 && s.D > 32 && s.D <= 256; }
-
-hipError_t launch_fwd_fast(const AttnShape& s, const FwdArgs& a, hipStream_t st) {
-    if (s.D <= 64) return launch_fwd<64>(s, a, st);
-    if (s.D <= 128) return launch_fwd<128>(s, a, st);
-    return launch_fwd<256>(s, a, st);
+// Launchers for one padded head dim (DPF = 64, 128, 256).  Each is
+// instantiated in its own translation unit (attn_f32_fast<DPF>.hip).
+template <int DPF> hipError_t launch_fwd_dpf(const AttnShape& s, const FwdArgs& a, hipStream_t st) {
+    return launch_fwd<DPF>(s, a, st);
 }
-
-hipError_t launch_bwd_fast(const AttnShape& s, const BwdArgs& a, int stages, hipStream_t st) {
-    if (s.D <= 64) return launch_bwd<64>(s, a, stages, st);
-    if (s.D <= 128) return launch_bwd<128>(s, a, stages, st);
-    return launch_bwd<256>(s, a, stages, st);
+template <int DPF> hipError_t launch_bwd_dpf(const AttnShape& s, const BwdArgs& a, int stages, hipStream_t st) {
+    return launch_bwd<DPF>(s, a, stages, st);
 }
+#define MFT_F32_EXTERN(DPF)                                                                         \
+    extern template hipError_t launch_fwd_dpf<DPF>(const AttnShape&, const FwdArgs&, hipStream_t); \
+    extern template hipError_t launch_bwd_dpf<DPF>(const AttnShape&, const BwdArgs&, int, hipStream_t);
+MFT_F32_EXTERN(64)
+MFT_F32_EXTERN(128)
+MFT_F32_EXTERN(256)
+#undef MFT_F32_EXTERN
 
 }  // namespace f32
 }  // namespace mft

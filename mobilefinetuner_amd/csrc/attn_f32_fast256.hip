@@ -1,0 +1,9 @@
+// fp32 fast-path instantiations for padded head dim 256.
+#include "attn_f32_fast.h"
+
+namespace mft {
+namespace f32 {
+template hipError_t launch_fwd_dpf<256>(const AttnShape&, const FwdArgs&, hipStream_t);
+template hipError_t launch_bwd_dpf<256>(const AttnShape&, const BwdArgs&, int, hipStream_t);
+}  // namespace f32
+}  // namespace mft

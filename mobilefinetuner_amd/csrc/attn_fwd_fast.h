@@ -66,7 +66,7 @@ hipError_t launch_fwd_combine(const AttnShape& s, const FwdArgs& a, hipStream_t 
 }  // namespace fwd
 
 namespace f32 {
-// The fp32 fast forward (attn_f32_fast.hip): the balanced launch (a.part_o set).
+// The fp32 fast forward (attn_f32_fast.h): the balanced launch (a.part_o set).
 hipError_t launch_fwd_fast(const AttnShape& s, const fwd::FwdArgs& a, hipStream_t st);
 }  // namespace f32
 

@@ -106,7 +106,7 @@ BwdLayout bwd_layout(const AttnShape& s);
 inline int fwd_wgs_per_cu(int64_t D) { return D <= 128 ? 2 : 1; }
 inline int bwd_wgs_per_cu(int64_t D) { return D <= 64 ? 2 : 1; }
 
-// fp32 fast path (attn_f32_fast.hip): fp32 operands with D % 4 == 0 and
+// fp32 fast path (attn_f32_fast.h): fp32 operands with D % 4 == 0 and
 // 32 < D <= 256 run the same work units, each unit as kF32Halves workgroups
 // (one per 64-row or 64-key half of its 128-row tiles).  Registers decide
 // how many share a CU as for bf16 (the forward fits 256 per lane up to
