@@ -611,6 +611,9 @@ int device_cus() {
 }
 
 BwdPlan plan_bwd_fast(const AttnShape& s) {
+    BwdPlan p{};
+    p.fast = bwd_fast_path(s);
+    if (!p.fast) return p;
     const int S = (int)s.S, causal = s.causal ? 1 : 0, group = (int)(s.Hq / s.Hkv), W = s.window;
     const FastTiles gkv{S, causal, W, group, 1}, gq{S, causal, W, group, 0};
     const int64_t pairs_kv = s.B * s.Hkv, pairs_q = s.B * s.Hq;
@@ -632,13 +635,12 @@ BwdPlan plan_bwd_fast(const AttnShape& s) {
     while (T < T_max && units(T) > cus) T += std::max<int64_t>(1, T / 64);
     // Units no shorter than kMinUnitIters iterations, and no tile over
     // kSplitMaxSlots units (REDUCE keeps a tile's slot list in LDS).
-    BwdPlan p;
     p.kv = fit_unit_split(gkv, (c_kv + T - 1) / T, kKvIterCost, kvc, kMinUnitIters, kSplitMaxSlots, &p.kv_parts_max);
     p.q = fit_unit_split(gq, (c_q + T - 1) / T, kQIterCost, qc, kMinUnitIters, kSplitMaxSlots, &p.q_parts_max);
     return p;
 }
 
-BwdLayout bwd_layout(const AttnShape& s) {
+BwdLayout bwd_layout(const AttnShape& s, const BwdPlan& p) {
     auto up = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
     const size_t rows = static_cast<size_t>(s.B * s.Hq);
     const size_t stat_floats = rows * static_cast<size_t>((s.S + 31) / 32) * 64;
@@ -647,8 +649,7 @@ BwdLayout bwd_layout(const AttnShape& s) {
     const size_t q_elems = static_cast<size_t>(s.B * s.Hq * s.S * s.D);
     BwdLayout l;
     l.stats = up(sizeof(float) * std::max(stat_floats, delta_floats));
-    if (bwd_fast_path(s)) {
-        const BwdPlan p = plan_bwd_fast(s);
+    if (p.fast) {
         // two slots per unit (split_slot), each one 128-row tile: dK and dV
         // tiles for the dK/dV role, a dQ tile for the dQ role
         const size_t tile = static_cast<size_t>(128 * s.D);
@@ -686,10 +687,10 @@ int dkdv_splits(const AttnShape& s) {
     return (int)best;
 }
 
-hipError_t launch_attn_bwd(const AttnShape& s, const void* q, const void* k, const void* v,
+hipError_t launch_attn_bwd(const AttnShape& s, const BwdPlan& p, const void* q, const void* k, const void* v,
                            const void* o, const void* dO, const float* lse, float* dq, float* dk,
                            float* dv, void* workspace, int stages, hipStream_t st) {
-    const BwdLayout lay = bwd_layout(s);
+    const BwdLayout lay = bwd_layout(s, p);
     char* ws = static_cast<char*>(workspace);
     float* delta = reinterpret_cast<float*>(ws);
     float* part = lay.kv_part ? reinterpret_cast<float*>(ws + lay.stats) : nullptr;
@@ -740,13 +741,10 @@ hipError_t launch_attn_bwd(const AttnShape& s, const void* q, const void* k, con
     a.kv_part = part;
     a.q_part = lay.q_part ? reinterpret_cast<float*>(ws + lay.stats + lay.kv_part) : nullptr;
     a.q_part_stride = s.B * s.Hq * s.S * s.D;
-    if (bwd_fast_path(s)) {
-        const BwdPlan p = plan_bwd_fast(s);
-        a.kv_us = p.kv;
-        a.q_us = p.q;
-    } else {
-        a.kv_us = a.q_us = UnitSplit{0, 0, 0, 0};
-    }
+    a.kv_us = p.kv;
+    a.q_us = p.q;
+    a.kv_parts_max = p.kv_parts_max;
+    a.q_parts_max = p.q_parts_max;
     const hipError_t e =
         s.bf16 ? launch_bwd_dispatch<bf16>(s, a, stages, st) : launch_bwd_dispatch<float>(s, a, stages, st);
     if (e != hipSuccess || !(stages & BWD_STAGE_REDUCE)) return e;

@@ -39,6 +39,7 @@ struct BwdArgs {
     float* kv_part;   // [B*Hkv][2*kv_us.units][dK, dV][128][D] partial tiles (split_slot)
     float* q_part;    // [B*Hq][2*q_us.units][128][D] partial dQ tiles (split_slot)
     int64_t q_part_stride;  // B*Hq*S*D
+    int kv_parts_max, q_parts_max;  // most units of one tile (REDUCE runs when either is > 1)
 };
 
 // Work geometry of the fast path (attn_geometry.h), shared with the forward.

@@ -680,13 +680,16 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_bf16_fast(BwdArgs a) {
 
 // Both roles in one grid: the first kv_us.units * B * Hkv workgroups run dK/dV
 // units, the rest dQ units (the units of both are sized to take about equally
-// long, see plan_bwd_fast).  FAST: every operand tile is whole (D == DP and S
+// long, see plan_bwd_fast).  Block ids are renumbered XCD-major (xcd_block):
+// units with neighbouring ids, which read the same K/V tiles (the group's
+// query heads' units of one index) or the same query blocks, then share one
+// XCD's L2.  FAST: every operand tile is whole (D == DP and S
 // a multiple of 64), so the direct loads take TileDma's precomputed offsets.
 template <int DP, bool CAUSAL, bool STRIDED, bool FAST>
 __global__ __launch_bounds__(256) void attn_bwd_main_bf16_fast(BwdArgs a) {
     __shared__ __attribute__((aligned(1024))) bf16 smem[BwdFastLds<DP>::ELEMS];
     const int nkv = a.kv_us.units * a.B * a.Hkv;
-    const int i = (int)blockIdx.x;
+    const int i = xcd_block((int)blockIdx.x, (int)gridDim.x);
     if (i < nkv) {
         const int bh = a.B * a.Hkv;
         dkdv_fast_body<DP, CAUSAL, STRIDED, FAST>(a, smem, i / bh, (i % bh) / a.Hkv, (i % bh) % a.Hkv);
@@ -784,7 +787,6 @@ hipError_t launch_bwd_fast(const AttnShape& s, BwdArgs a, int stages, hipStream_
         hipLaunchKernelGGL((attn_bwd_stats_kernel<bf16, DP>), dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256), 0,
                            st, a);
     }
-    const BwdPlan pl = plan_bwd_fast(s);
     const bool strided = !s.contiguous;
     // (causal, strided) -> instantiation
 #define MFT_BWD_LAUNCH(KERNEL, GRID)                                                      \
@@ -799,7 +801,7 @@ hipError_t launch_bwd_fast(const AttnShape& s, BwdArgs a, int stages, hipStream_
             hipLaunchKernelGGL((KERNEL<DP, false, false>), GRID, dim3(256), 0, st, a);    \
     } while (0)
     if ((stages & BWD_STAGE_MAIN) == BWD_STAGE_MAIN) {
-        const dim3 grid((unsigned)(pl.kv.units * s.B * s.Hkv + pl.q.units * s.B * s.Hq));
+        const dim3 grid((unsigned)(a.kv_us.units * s.B * s.Hkv + a.q_us.units * s.B * s.Hq));
         if (s.D == DP && s.S % 64 == 0) {
 #define MFT_MAIN_FAST(CAUSAL, STRIDED, FAST) \
     hipLaunchKernelGGL((attn_bwd_main_bf16_fast<DP, CAUSAL, STRIDED, FAST>), grid, dim3(256), 0, st, a)
@@ -823,12 +825,12 @@ hipError_t launch_bwd_fast(const AttnShape& s, BwdArgs a, int stages, hipStream_
 #undef MFT_MAIN_FAST
         }
     } else if (stages & BWD_STAGE_DKDV) {
-        MFT_BWD_LAUNCH(attn_bwd_dkdv_bf16_fast, dim3((unsigned)(pl.kv.units * s.B * s.Hkv)));
+        MFT_BWD_LAUNCH(attn_bwd_dkdv_bf16_fast, dim3((unsigned)(a.kv_us.units * s.B * s.Hkv)));
     } else if (stages & BWD_STAGE_DQ) {
-        MFT_BWD_LAUNCH(attn_bwd_dq_bf16_fast, dim3((unsigned)(pl.q.units * s.B * s.Hq)));
+        MFT_BWD_LAUNCH(attn_bwd_dq_bf16_fast, dim3((unsigned)(a.q_us.units * s.B * s.Hq)));
     }
 #undef MFT_BWD_LAUNCH
-    if ((stages & BWD_STAGE_REDUCE) && (pl.kv_parts_max > 1 || pl.q_parts_max > 1)) {
+    if ((stages & BWD_STAGE_REDUCE) && (a.kv_parts_max > 1 || a.q_parts_max > 1)) {
         const int64_t nt = (s.S + 127) / 128;
         const int64_t blocks = (s.B * s.Hkv + s.B * s.Hq) * nt * (128 / merge_rows(s.D));
         if (s.causal)

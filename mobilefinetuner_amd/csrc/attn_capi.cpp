@@ -120,29 +120,11 @@ mft_status check_desc(const mft_attn_desc* d, mft::AttnShape* s) {
     return MFT_OK;
 }
 
-// The split plans keep at most kSplitMaxSlots partial slots per tile (the
-// merge kernels hold the slot list in LDS); a shape whose plan would need
-// more is refused instead of launched.
-mft_status check_fwd_plan(const mft::AttnShape& s, const char* who) {
-    if (mft::fwd_workspace_bytes(s) == 0) return MFT_OK;
-    const mft::FwdPlan p = mft::plan_fwd_split(s);
-    if (p.parts_max > mft::kSplitMaxSlots)
-        return fail(MFT_ERR_UNSUPPORTED, std::string(who) + ": the balanced forward would split a query tile into " +
-                                             std::to_string(p.parts_max) + " parts, more than " +
-                                             std::to_string(mft::kSplitMaxSlots));
-    return MFT_OK;
-}
-
-mft_status check_bwd_plan(const mft::AttnShape& s, const char* who) {
-    if (!mft::bwd_fast_path(s)) return MFT_OK;
-    const mft::BwdPlan p = mft::plan_bwd_fast(s);
-    const int parts = std::max(p.kv_parts_max, p.q_parts_max);
-    if (parts > mft::kSplitMaxSlots)
-        return fail(MFT_ERR_UNSUPPORTED, std::string(who) + ": the backward plan would split a tile into " +
-                                             std::to_string(parts) + " parts, more than " +
-                                             std::to_string(mft::kSplitMaxSlots));
-    return MFT_OK;
-}
+// Each call plans its work once (plan_fwd_split / plan_bwd_fast) and passes
+// the plan to the workspace layout and the launches.  The planners keep at
+// most kSplitMaxSlots partial slots per tile (fit_unit_split lowers the unit
+// count until that holds; tests/native/plan_check.cpp sweeps it), which the
+// merge kernels' LDS slot lists rely on.
 
 // Scratch of mft_attn_bwd_noalloc: the backward workspace (row terms, fp32
 // partial tiles) of callers that cannot allocate.  One copy per GPU, held
@@ -187,8 +169,8 @@ mft_status mft_attn_workspace_size(const mft_attn_desc* desc, size_t* fwd_bytes,
     mft::AttnShape s;
     const mft_status st = check_desc(desc, &s);
     if (st != MFT_OK) return st;
-    if (fwd_bytes) *fwd_bytes = mft::fwd_workspace_bytes(s);
-    if (bwd_bytes) *bwd_bytes = mft::bwd_layout(s).total;
+    if (fwd_bytes) *fwd_bytes = mft::fwd_workspace_bytes(s, mft::plan_fwd_split(s));
+    if (bwd_bytes) *bwd_bytes = mft::bwd_layout(s, mft::plan_bwd_fast(s)).total;
     return MFT_OK;
 }
 
@@ -200,19 +182,18 @@ mft_status mft_attn_fwd(const mft_attn_desc* desc, const void* q, const void* k,
     if (!q || !k || !v || !o) return fail(MFT_ERR_INVALID_ARG, "mft_attn_fwd: q, k, v, o must be non-NULL");
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(lse) || !aligned16(workspace))
         return fail(MFT_ERR_INVALID_ARG, "mft_attn_fwd: buffers must be 16-byte aligned");
-    if (workspace) {
-        const mft_status pl = check_fwd_plan(s, "mft_attn_fwd");
-        if (pl != MFT_OK) return pl;
-    }
-    return hip_status(mft::launch_attn_fwd(s, q, k, v, o, lse, workspace, stream), "mft_attn_fwd launch");
+    return hip_status(mft::launch_attn_fwd(s, mft::plan_fwd_split(s), q, k, v, o, lse, workspace, stream),
+                      "mft_attn_fwd launch");
 }
 
-mft_status mft_attn_bwd_stage(const mft_attn_desc* desc, int stages, const void* q, const void* k,
-                              const void* v, const void* o, const void* dO, const float* lse, float* dq,
-                              float* dk, float* dv, void* workspace, hipStream_t stream) {
-    mft::AttnShape s;
-    const mft_status st = check_desc(desc, &s);
-    if (st != MFT_OK) return st;
+}  // extern "C"
+
+namespace {
+
+// mft_attn_bwd_stage for a checked shape and its plan.
+mft_status bwd_stage(const mft::AttnShape& s, const mft::BwdPlan& p, int stages, const void* q, const void* k,
+                     const void* v, const void* o, const void* dO, const float* lse, float* dq, float* dk, float* dv,
+                     void* workspace, hipStream_t stream) {
     if (stages <= 0 || (stages & ~MFT_BWD_ALL) != 0)
         return fail(MFT_ERR_INVALID_ARG, "mft_attn_bwd_stage: stages must be a non-empty mask of MFT_BWD_*");
     if (!q || !k || !v || !o || !dO || !lse || !dq || !dk || !dv)
@@ -221,10 +202,21 @@ mft_status mft_attn_bwd_stage(const mft_attn_desc* desc, int stages, const void*
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(dO) || !aligned16(lse) ||
         !aligned16(dq) || !aligned16(dk) || !aligned16(dv) || !aligned16(workspace))
         return fail(MFT_ERR_INVALID_ARG, "mft_attn_bwd: buffers must be 16-byte aligned");
-    const mft_status pl = check_bwd_plan(s, "mft_attn_bwd");
-    if (pl != MFT_OK) return pl;
-    return hip_status(mft::launch_attn_bwd(s, q, k, v, o, dO, lse, dq, dk, dv, workspace, stages, stream),
+    return hip_status(mft::launch_attn_bwd(s, p, q, k, v, o, dO, lse, dq, dk, dv, workspace, stages, stream),
                       "mft_attn_bwd launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+mft_status mft_attn_bwd_stage(const mft_attn_desc* desc, int stages, const void* q, const void* k,
+                              const void* v, const void* o, const void* dO, const float* lse, float* dq,
+                              float* dk, float* dv, void* workspace, hipStream_t stream) {
+    mft::AttnShape s;
+    const mft_status st = check_desc(desc, &s);
+    if (st != MFT_OK) return st;
+    return bwd_stage(s, mft::plan_bwd_fast(s), stages, q, k, v, o, dO, lse, dq, dk, dv, workspace, stream);
 }
 
 mft_status mft_attn_bwd(const mft_attn_desc* desc, const void* q, const void* k, const void* v, const void* o,
@@ -239,7 +231,8 @@ mft_status mft_attn_bwd_noalloc(const mft_attn_desc* desc, const void* q, const 
     mft::AttnShape s;
     const mft_status st = check_desc(desc, &s);
     if (st != MFT_OK) return st;
-    const size_t need = mft::bwd_layout(s).total;
+    const mft::BwdPlan plan = mft::plan_bwd_fast(s);
+    const size_t need = mft::bwd_layout(s, plan).total;
     if (need > kNoAllocScratchBytes)
         return fail(MFT_ERR_UNSUPPORTED,
                     "mft_attn_bwd_noalloc: this shape needs " + std::to_string(need) +
@@ -252,7 +245,7 @@ mft_status mft_attn_bwd_noalloc(const mft_attn_desc* desc, const void* q, const 
     // Every workspace byte the backward reads is written earlier in the same
     // call (row terms by DELTA, partial tiles by their work units), so
     // nothing has to start at zero.
-    return mft_attn_bwd_stage(desc, MFT_BWD_ALL, q, k, v, o, dO, lse, dq, dk, dv, ws, stream);
+    return bwd_stage(s, plan, MFT_BWD_ALL, q, k, v, o, dO, lse, dq, dk, dv, ws, stream);
 }
 
 mft_status mft_repeat_kv_fwd(const void* kv, void* out, int64_t B, int64_t Hkv, int64_t S, int64_t D, int64_t r,

@@ -779,9 +779,7 @@ template <int DPF> bool whole_tiles(const AttnShape& s) { return s.D == DPF && s
 template <int DPF>
 hipError_t launch_fwd(const AttnShape& s, FwdArgs a, hipStream_t st) {
     a.n_qtiles = (int)((s.S + kFwdBM - 1) / kFwdBM);
-    const FwdPlan p = plan_fwd_split(s);
-    a.us = p.us;
-    const dim3 grid((unsigned)(2 * p.us.units * s.B * s.Hq));
+    const dim3 grid((unsigned)(2 * a.us.units * s.B * s.Hq));
     const bool fast = whole_tiles<DPF>(s);
     if (s.causal) {
         if (fast) hipLaunchKernelGGL((attn_fwd_f32_split<DPF, true, true>), grid, dim3(256), 0, st, a);
@@ -791,7 +789,7 @@ hipError_t launch_fwd(const AttnShape& s, FwdArgs a, hipStream_t st) {
         else hipLaunchKernelGGL((attn_fwd_f32_split<DPF, false, false>), grid, dim3(256), 0, st, a);
     }
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess || !p.any_split) return e;
+    if (e != hipSuccess || !a.any_split) return e;
     return fwd::launch_fwd_combine(s, a, st);
 }
 
@@ -803,7 +801,6 @@ hipError_t launch_bwd(const AttnShape& s, const BwdArgs& a, int stages, hipStrea
         hipLaunchKernelGGL((bwd::attn_bwd_stats_kernel<float, DPF>), dim3((unsigned)((rows + RPB - 1) / RPB)),
                            dim3(256), 0, st, a);
     }
-    const BwdPlan pl = plan_bwd_fast(s);
     const bool fast = whole_tiles<DPF>(s);
 #define MFT_F32_LAUNCH(KERNEL, GRID)                                                                         \
     do {                                                                                                     \
@@ -812,7 +809,7 @@ hipError_t launch_bwd(const AttnShape& s, const BwdArgs& a, int stages, hipStrea
         else if (fast) hipLaunchKernelGGL((KERNEL<DPF, false, true>), GRID, dim3(256), 0, st, a);            \
         else hipLaunchKernelGGL((KERNEL<DPF, false, false>), GRID, dim3(256), 0, st, a);                     \
     } while (0)
-    const unsigned nkv = (unsigned)(2 * pl.kv.units * s.B * s.Hkv), nq = (unsigned)(2 * pl.q.units * s.B * s.Hq);
+    const unsigned nkv = (unsigned)(2 * a.kv_us.units * s.B * s.Hkv), nq = (unsigned)(2 * a.q_us.units * s.B * s.Hq);
     if ((stages & BWD_STAGE_MAIN) == BWD_STAGE_MAIN)
         MFT_F32_LAUNCH(attn_bwd_main_f32, dim3(nkv + nq));
     else if (stages & BWD_STAGE_DKDV)
@@ -820,7 +817,7 @@ hipError_t launch_bwd(const AttnShape& s, const BwdArgs& a, int stages, hipStrea
     else if (stages & BWD_STAGE_DQ)
         MFT_F32_LAUNCH(attn_bwd_dq_f32_fast, dim3(nq));
 #undef MFT_F32_LAUNCH
-    if ((stages & BWD_STAGE_REDUCE) && (pl.kv_parts_max > 1 || pl.q_parts_max > 1)) {
+    if ((stages & BWD_STAGE_REDUCE) && (a.kv_parts_max > 1 || a.q_parts_max > 1)) {
         const int64_t nt = (s.S + 127) / 128;
         const int64_t blocks = (s.B * s.Hkv + s.B * s.Hq) * nt * (128 / merge_rows(s.D));
         if (s.causal)

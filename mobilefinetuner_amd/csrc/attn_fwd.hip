@@ -386,10 +386,12 @@ hipError_t launch_fwd_fast128(const AttnShape& s, FwdArgs a, hipStream_t st) {
 int fwd_rows_per_block(const AttnShape&) { return 128; }
 
 FwdPlan plan_fwd_split(const AttnShape& s) {
+    FwdPlan p{};
+    p.balanced = (s.bf16 && s.D % 8 == 0 && s.D > 32) || f32::fast_path(s);
+    if (!p.balanced) return p;
     const int S = (int)s.S, causal = s.causal ? 1 : 0, W = s.window;
     const int64_t pairs = s.B * s.Hq;
     const int64_t u = balanced_units(pairs, fwd_unit_slots(s));
-    FwdPlan p;
     // Units of about equal cost, no shorter than kMinUnitIters key tiles (a
     // split costs one fp32 partial tile), no query tile over kCombMaxSlots.
     const FastTiles g{S, causal, W, (int)(s.Hq / s.Hkv), 0};
@@ -398,9 +400,8 @@ FwdPlan plan_fwd_split(const AttnShape& s) {
     return p;
 }
 
-size_t fwd_workspace_bytes(const AttnShape& s) {
-    if (!((s.bf16 && s.D % 8 == 0 && s.D > 32) || f32::fast_path(s))) return 0;
-    const FwdPlan p = plan_fwd_split(s);
+size_t fwd_workspace_bytes(const AttnShape& s, const FwdPlan& p) {
+    if (!p.balanced) return 0;
     const size_t rows = p.any_split ? static_cast<size_t>(s.B * s.Hq) * 2 * p.us.units * kFwdBM : 0;
     auto up = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
     // Always non-zero for this path, so that a caller that passes the queried
@@ -408,7 +409,7 @@ size_t fwd_workspace_bytes(const AttnShape& s) {
     return up(rows * static_cast<size_t>(s.D) * 4) + up(rows * 2 * 4) + 256;
 }
 
-hipError_t launch_attn_fwd(const AttnShape& s, const void* q, const void* k, const void* v, void* o,
+hipError_t launch_attn_fwd(const AttnShape& s, const FwdPlan& p, const void* q, const void* k, const void* v, void* o,
                            float* lse, void* workspace, hipStream_t st) {
     FwdArgs a;
     a.q = q;
@@ -433,10 +434,12 @@ hipError_t launch_attn_fwd(const AttnShape& s, const void* q, const void* k, con
     a.sv = s.v;
     a.so = s.o;
     a.us = UnitSplit{0, 0, 0, 0};
+    a.any_split = 0;
     a.part_o = nullptr;
     a.part_ml = nullptr;
-    if (workspace && fwd_workspace_bytes(s) > 0) {
-        const FwdPlan p = plan_fwd_split(s);
+    if (workspace && p.balanced) {
+        a.us = p.us;
+        a.any_split = p.any_split ? 1 : 0;
         const size_t rows = p.any_split ? static_cast<size_t>(s.B * s.Hq) * 2 * p.us.units * kFwdBM : 0;
         const size_t ob = (rows * static_cast<size_t>(s.D) * 4 + 255) & ~static_cast<size_t>(255);
         a.part_o = static_cast<float*>(workspace);

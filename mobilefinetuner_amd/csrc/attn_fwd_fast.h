@@ -45,6 +45,7 @@ struct FwdArgs {
     Strides sq, sk, sv, so;  // layouts of q, k, v, o
     // balanced launch (bf16 fast path with a workspace; see FwdPlan)
     UnitSplit us;            // work units per (batch, head)
+    int any_split;           // some query tile spans several units (the combine runs)
     float* part_o;           // [B*Hq][2*us.units][128][D] unnormalised O (split_slot)
     float* part_ml;          // [B*Hq][2*units][128][2] running max (log2 units), sum
 };
@@ -539,25 +540,21 @@ template <int DP>
 hipError_t launch_fwd_fast_t(const AttnShape& s, FwdArgs a, hipStream_t st) {
     a.n_qtiles = (int)((s.S + kFwdBM - 1) / kFwdBM);
     const bool split = a.part_o != nullptr;
-    FwdPlan p{};
-    if (split) {
-        p = plan_fwd_split(s);
-        a.us = p.us;
-    }
+    const unsigned units = split ? (unsigned)a.us.units : 0u;
     const bool fast = fwd_fast_dma<DP>(s);
     if (s.causal) {
         if (fast)
-            launch_fwd_fast_k<DP, true, true>(s, a, split, p.us.units, st);
+            launch_fwd_fast_k<DP, true, true>(s, a, split, units, st);
         else
-            launch_fwd_fast_k<DP, true, false>(s, a, split, p.us.units, st);
+            launch_fwd_fast_k<DP, true, false>(s, a, split, units, st);
     } else {
         if (fast)
-            launch_fwd_fast_k<DP, false, true>(s, a, split, p.us.units, st);
+            launch_fwd_fast_k<DP, false, true>(s, a, split, units, st);
         else
-            launch_fwd_fast_k<DP, false, false>(s, a, split, p.us.units, st);
+            launch_fwd_fast_k<DP, false, false>(s, a, split, units, st);
     }
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess || !(split && p.any_split)) return e;
+    if (e != hipSuccess || !(split && a.any_split)) return e;
     return launch_fwd_combine(s, a, st);
 }
 

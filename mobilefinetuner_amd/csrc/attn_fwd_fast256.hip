@@ -10,15 +10,13 @@ namespace fwd {
 hipError_t launch_fwd_fast256(const AttnShape& s, FwdArgs a, hipStream_t st) {
     if (a.part_o == nullptr || !fwd_fast_dma<256>(s)) return launch_fwd_fast_t<256>(s, a, st);
     a.n_qtiles = (int)((s.S + kFwdBM - 1) / kFwdBM);
-    const FwdPlan p = plan_fwd_split(s);
-    a.us = p.us;
-    const dim3 grid((unsigned)(p.us.units * s.B * s.Hq));
+    const dim3 grid((unsigned)(a.us.units * s.B * s.Hq));
     if (s.causal)
         hipLaunchKernelGGL((attn_fwd_bf16_split16<256, true>), grid, dim3(kW16Threads), 0, st, a);
     else
         hipLaunchKernelGGL((attn_fwd_bf16_split16<256, false>), grid, dim3(kW16Threads), 0, st, a);
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess || !p.any_split) return e;
+    if (e != hipSuccess || !a.any_split) return e;
     return launch_fwd_combine(s, a, st);
 }
 }  // namespace fwd

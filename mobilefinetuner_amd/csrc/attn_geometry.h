@@ -195,4 +195,16 @@ __host__ __device__ inline int64_t split_slot(int64_t u, int64_t u0, bool starts
     return 2 * u + ((u == u0 && !starts) ? 1 : 0);
 }
 
+// XCD-aware block order.  The dispatcher hands workgroup i of a launch to
+// XCD i % kXcds, and each XCD has its own L2.  xcd_block(i, n) renumbers the
+// n workgroups so that XCD x runs one contiguous range of logical indices:
+// work units with neighbouring indices (which read the same K/V or Q tiles)
+// then share one L2.  A bijection of [0, n) whatever the dispatch order, so
+// only the cache behaviour depends on it.
+constexpr int kXcds = 8;
+__host__ __device__ inline int xcd_block(int i, int n) {
+    const int x = i % kXcds, k = i / kXcds, q = n / kXcds, r = n % kXcds;
+    return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + k;
+}
+
 }  // namespace mft

@@ -65,6 +65,7 @@ __host__ __device__ inline int merge_rows(int64_t D) { return D > 128 ? 16 : D >
 int device_cus();
 
 struct BwdPlan {
+    bool fast;        // the work-unit kernels (bwd_fast_path)
     UnitSplit kv, q;  // units per (batch, kv head) and per (batch, query head)
     int kv_parts_max, q_parts_max;
 };
@@ -87,6 +88,8 @@ inline int kv_tile_cost(const AttnShape& s) { return s.bf16 ? kv_tile_cost(s.D) 
 inline int q_tile_cost(const AttnShape& s) { return s.bf16 ? q_tile_cost(s.D) : 0; }
 // The fewest iterations the planners give a unit.
 constexpr int kMinUnitIters = 4;
+// The plan of one backward call, computed once per call and passed to the
+// workspace layout and the launches.
 BwdPlan plan_bwd_fast(const AttnShape& s);
 
 // Backward workspace layout in bytes: [delta or row-stat blocks][dK/dV
@@ -95,7 +98,7 @@ BwdPlan plan_bwd_fast(const AttnShape& s);
 struct BwdLayout {
     size_t stats, kv_part, q_part, masked, total;
 };
-BwdLayout bwd_layout(const AttnShape& s);
+BwdLayout bwd_layout(const AttnShape& s, const BwdPlan& p);
 
 
 // Workgroups of the bf16 fast kernels that one CU holds at once, which the
@@ -128,17 +131,19 @@ inline int64_t bwd_unit_slots(const AttnShape& s) {
 // (UnitSplit, attn_geometry.h); a query tile split across units leaves fp32
 // partials in the units' slots (split_slot).
 struct FwdPlan {
+    bool balanced;  // the shape has a balanced launch (it takes a workspace)
     UnitSplit us;
     bool any_split;
     int parts_max;  // most slots of one query tile
 };
+// Computed once per call and passed to the workspace size and the launch.
 FwdPlan plan_fwd_split(const AttnShape& s);
 // Forward workspace bytes (0 where the forward takes no workspace).  With a
 // workspace of this size the forward uses the balanced launch; without one
 // (NULL) it runs one workgroup per query tile.
-size_t fwd_workspace_bytes(const AttnShape& s);
+size_t fwd_workspace_bytes(const AttnShape& s, const FwdPlan& p);
 
-hipError_t launch_attn_fwd(const AttnShape& s, const void* q, const void* k, const void* v,
+hipError_t launch_attn_fwd(const AttnShape& s, const FwdPlan& p, const void* q, const void* k, const void* v,
                            void* o, float* lse, void* workspace, hipStream_t st);
 
 // Backward stages (bit mask, values of MFT_BWD_*): DELTA writes the per-row
@@ -154,8 +159,8 @@ enum {
     BWD_STAGE_ALL = 15
 };
 
-// workspace: bwd_layout(s).total bytes.
-hipError_t launch_attn_bwd(const AttnShape& s, const void* q, const void* k, const void* v,
+// workspace: bwd_layout(s, p).total bytes.
+hipError_t launch_attn_bwd(const AttnShape& s, const BwdPlan& p, const void* q, const void* k, const void* v,
                            const void* o, const void* dO, const float* lse, float* dq,
                            float* dk, float* dv, void* workspace, int stages, hipStream_t st);
 

@@ -22,6 +22,10 @@ CASES = [
     # sliding window, no padding
     (1, 4, 1, 1000, 256, "bf16", True, 128, None),
     (1, 2, 1, 700, 64, "bf16", True, 1, None),
+    # D = 256 with a window that leaves the last 64-key tile of each query
+    # tile invisible to its upper half (W = 65), and with window + padding
+    (1, 4, 1, 704, 256, "bf16", True, 65, None),
+    (2, 2, 1, 448, 256, "bf16", True, 200, [448, 333]),
     (2, 2, 1, 300, 128, "bf16", True, 64, None),
     (1, 4, 2, 520, 128, "bf16", True, 65, None),
     (1, 2, 2, 333, 96, "f32", True, 50, None),
