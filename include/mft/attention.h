@@ -29,8 +29,11 @@
  *   - lse[b, h, i] = log(sum_j exp(scale * q_i . k_j)) over the visible keys
  *     (natural log, fp32, [B, Hq, S]).  The backward recomputes the softmax
  *     from it; no S x S tensor is ever stored.
- *   - All pointers are caller-owned device memory, 16-byte aligned; the
- *     library allocates nothing.  Work is enqueued on `stream` (NULL = the null stream) and is
+ *   - All pointers are caller-owned device memory, 16-byte aligned; no call
+ *     allocates device memory.  Loading the library takes a fixed 128 MiB
+ *     per GPU it runs on (the workspace of mft_attn_bwd_noalloc, a
+ *     __device__ array of its code object), whether or not that entry point
+ *     is called.  Work is enqueued on `stream` (NULL = the null stream) and is
  *     ordered there; the calls return before the GPU finishes.
  *   - Errors: a non-zero mft_status, and mft_last_error() returns a
  *     thread-local message.  The C++ adapter rethrows it as the reference's
