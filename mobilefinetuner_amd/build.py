@@ -50,8 +50,24 @@ def sources():
                   if f.endswith((".hip", ".cpp")))
 
 
+def _stale(src: str, obj: str) -> bool:
+    """The object is older than its source or any header of csrc/ and include/."""
+    if not os.path.exists(obj):
+        return True
+    heads = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
+    inc = os.path.join(ROOT, "include", "mft")
+    heads += [os.path.join(inc, f) for f in os.listdir(inc)]
+    newest = max(os.path.getmtime(p) for p in heads + [src])
+    return os.path.getmtime(obj) < newest
+
+
+INCREMENTAL = False
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+    if INCREMENTAL and not _stale(src, obj):
+        return obj
     cmd = [hipcc(), *HIP_FLAGS, "-I", os.path.join(ROOT, "include"), "-I", CSRC, "-c", src, "-o", obj]
     if os.path.basename(src) in VGPR_FORM:
         cmd[1:1] = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
@@ -87,5 +103,8 @@ def build(verbose: bool = True) -> str:
 
 
 if __name__ == "__main__":
+    # --incremental: recompile only sources older than their object's inputs
+    # (a development shortcut; build() with no flag compiles everything).
+    INCREMENTAL = "--incremental" in sys.argv
     build()
     sys.exit(0)
