@@ -32,7 +32,8 @@
 // the bf16 path's TileDma, viewing an fp32 row as 2 * DPF bf16 columns.
 //
 // The kernels are instantiated per padded head dim in attn_f32_fast64.hip,
-// attn_f32_fast128.hip and attn_f32_fast256.hip, so they compile in parallel.
+// attn_f32_fast128.hip and, split by role and causal mode,
+// attn_f32_fast256*.hip, so they compile in parallel.
 #pragma once
 #include "attn_bwd_fast.h"
 #include "attn_fwd_fast.h"
@@ -178,7 +179,7 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_split(FwdArgs a) {
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, i16 = lane & 15, g = lane >> 4;
     const int S = a.S, D = a.D, W = a.window;
-    const int bh = a.B * a.Hq, blk = (int)blockIdx.x;
+    const int bh = a.B * a.Hq, blk = xcd_block((int)blockIdx.x, (int)gridDim.x);  // XCD-major order
     const int unit = blk / (2 * bh), half = (blk / bh) & 1, b = (blk % bh) / a.Hq, h = (blk % bh) % a.Hq;
     const int hk = h / a.group;
     const float* Q = (const float*)a.q + a.sq.at(b, h);
@@ -751,7 +752,7 @@ __device__ __forceinline__ void dq_f32_body(const BwdArgs& a, float* smem, int u
 template <int DPF, bool CAUSAL, bool FAST>
 __global__ __launch_bounds__(256) void attn_bwd_main_f32(BwdArgs a) {
     __shared__ __attribute__((aligned(1024))) float smem[main_lds_floats<DPF>()];
-    const int nkv = 2 * a.kv_us.units * a.B * a.Hkv, i = (int)blockIdx.x;
+    const int nkv = 2 * a.kv_us.units * a.B * a.Hkv, i = xcd_block((int)blockIdx.x, (int)gridDim.x);
     if (i < nkv) {
         const int bh = a.B * a.Hkv;
         dkdv_f32_body<DPF, CAUSAL, FAST>(a, smem, i / (2 * bh), (i / bh) & 1, (i % bh) / a.Hkv, (i % bh) % a.Hkv);
@@ -793,30 +794,67 @@ hipError_t launch_fwd(const AttnShape& s, FwdArgs a, hipStream_t st) {
     return fwd::launch_fwd_combine(s, a, st);
 }
 
-template <int DPF>
-hipError_t launch_bwd(const AttnShape& s, const BwdArgs& a, int stages, hipStream_t st) {
-    if (stages & BWD_STAGE_DELTA) {
-        constexpr int RPB = 256 / (DPF / 4);
-        const int64_t rows = s.B * s.Hq * (int64_t)a.nqb_total * 32;
-        hipLaunchKernelGGL((bwd::attn_bwd_stats_kernel<float, DPF>), dim3((unsigned)((rows + RPB - 1) / RPB)),
-                           dim3(256), 0, st, a);
-    }
+// The work-unit kernels of one causal mode: MAIN = the combined launch of
+// both roles, otherwise the DKDV or DQ stage alone (stages).  Instantiated
+// per (DPF, CAUSAL, MAIN) in the attn_f32_fast*.hip translation units, so
+// that the D = 256 kernels compile in parallel.
+template <int DPF, bool CAUSAL, bool MAIN>
+hipError_t launch_bwd_units(const AttnShape& s, const BwdArgs& a, int stages, hipStream_t st) {
     const bool fast = whole_tiles<DPF>(s);
-#define MFT_F32_LAUNCH(KERNEL, GRID)                                                                         \
-    do {                                                                                                     \
-        if (s.causal && fast) hipLaunchKernelGGL((KERNEL<DPF, true, true>), GRID, dim3(256), 0, st, a);      \
-        else if (s.causal) hipLaunchKernelGGL((KERNEL<DPF, true, false>), GRID, dim3(256), 0, st, a);        \
-        else if (fast) hipLaunchKernelGGL((KERNEL<DPF, false, true>), GRID, dim3(256), 0, st, a);            \
-        else hipLaunchKernelGGL((KERNEL<DPF, false, false>), GRID, dim3(256), 0, st, a);                     \
-    } while (0)
     const unsigned nkv = (unsigned)(2 * a.kv_us.units * s.B * s.Hkv), nq = (unsigned)(2 * a.q_us.units * s.B * s.Hq);
-    if ((stages & BWD_STAGE_MAIN) == BWD_STAGE_MAIN)
+#define MFT_F32_LAUNCH(KERNEL, GRID)                                                       \
+    do {                                                                                   \
+        if (fast) hipLaunchKernelGGL((KERNEL<DPF, CAUSAL, true>), GRID, dim3(256), 0, st, a); \
+        else hipLaunchKernelGGL((KERNEL<DPF, CAUSAL, false>), GRID, dim3(256), 0, st, a);     \
+    } while (0)
+    if constexpr (MAIN)
         MFT_F32_LAUNCH(attn_bwd_main_f32, dim3(nkv + nq));
     else if (stages & BWD_STAGE_DKDV)
         MFT_F32_LAUNCH(attn_bwd_dkdv_f32_fast, dim3(nkv));
     else if (stages & BWD_STAGE_DQ)
         MFT_F32_LAUNCH(attn_bwd_dq_f32_fast, dim3(nq));
 #undef MFT_F32_LAUNCH
+    return hipGetLastError();
+}
+
+// Launchers for one padded head dim (DPF = 64, 128, 256), instantiated in the
+// attn_f32_fast*.hip translation units.
+template <int DPF> hipError_t launch_fwd_dpf(const AttnShape& s, const FwdArgs& a, hipStream_t st) {
+    return launch_fwd<DPF>(s, a, st);
+}
+#define MFT_F32_EXTERN(DPF)                                                                                  \
+    extern template hipError_t launch_fwd_dpf<DPF>(const AttnShape&, const FwdArgs&, hipStream_t);          \
+    extern template hipError_t launch_bwd_units<DPF, true, true>(const AttnShape&, const BwdArgs&, int,     \
+                                                                 hipStream_t);                               \
+    extern template hipError_t launch_bwd_units<DPF, false, true>(const AttnShape&, const BwdArgs&, int,    \
+                                                                  hipStream_t);                              \
+    extern template hipError_t launch_bwd_units<DPF, true, false>(const AttnShape&, const BwdArgs&, int,    \
+                                                                  hipStream_t);                              \
+    extern template hipError_t launch_bwd_units<DPF, false, false>(const AttnShape&, const BwdArgs&, int,   \
+                                                                   hipStream_t);
+MFT_F32_EXTERN(64)
+MFT_F32_EXTERN(128)
+MFT_F32_EXTERN(256)
+#undef MFT_F32_EXTERN
+
+// DELTA, the work-unit launch of the stages asked for, then REDUCE.
+template <int DPF>
+hipError_t launch_bwd_dpf(const AttnShape& s, const BwdArgs& a, int stages, hipStream_t st) {
+    if (stages & BWD_STAGE_DELTA) {
+        constexpr int RPB = 256 / (DPF / 4);
+        const int64_t rows = s.B * s.Hq * (int64_t)a.nqb_total * 32;
+        hipLaunchKernelGGL((bwd::attn_bwd_stats_kernel<float, DPF>), dim3((unsigned)((rows + RPB - 1) / RPB)),
+                           dim3(256), 0, st, a);
+    }
+    hipError_t e = hipSuccess;
+    const bool main = (stages & BWD_STAGE_MAIN) == BWD_STAGE_MAIN;
+    if (main)
+        e = s.causal ? launch_bwd_units<DPF, true, true>(s, a, stages, st)
+                     : launch_bwd_units<DPF, false, true>(s, a, stages, st);
+    else if (stages & BWD_STAGE_MAIN)
+        e = s.causal ? launch_bwd_units<DPF, true, false>(s, a, stages, st)
+                     : launch_bwd_units<DPF, false, false>(s, a, stages, st);
+    if (e != hipSuccess) return e;
     if ((stages & BWD_STAGE_REDUCE) && (a.kv_parts_max > 1 || a.q_parts_max > 1)) {
         const int64_t nt = (s.S + 127) / 128;
         const int64_t blocks = (s.B * s.Hkv + s.B * s.Hq) * nt * (128 / merge_rows(s.D));
@@ -827,22 +865,6 @@ hipError_t launch_bwd(const AttnShape& s, const BwdArgs& a, int stages, hipStrea
     }
     return hipGetLastError();
 }
-
-// Launchers for one padded head dim (DPF = 64, 128, 256).  Each is
-// instantiated in its own translation unit (attn_f32_fast<DPF>.hip).
-template <int DPF> hipError_t launch_fwd_dpf(const AttnShape& s, const FwdArgs& a, hipStream_t st) {
-    return launch_fwd<DPF>(s, a, st);
-}
-template <int DPF> hipError_t launch_bwd_dpf(const AttnShape& s, const BwdArgs& a, int stages, hipStream_t st) {
-    return launch_bwd<DPF>(s, a, stages, st);
-}
-#define MFT_F32_EXTERN(DPF)                                                                         \
-    extern template hipError_t launch_fwd_dpf<DPF>(const AttnShape&, const FwdArgs&, hipStream_t); \
-    extern template hipError_t launch_bwd_dpf<DPF>(const AttnShape&, const BwdArgs&, int, hipStream_t);
-MFT_F32_EXTERN(64)
-MFT_F32_EXTERN(128)
-MFT_F32_EXTERN(256)
-#undef MFT_F32_EXTERN
 
 }  // namespace f32
 }  // namespace mft

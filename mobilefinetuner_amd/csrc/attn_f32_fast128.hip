@@ -4,6 +4,9 @@
 namespace mft {
 namespace f32 {
 template hipError_t launch_fwd_dpf<128>(const AttnShape&, const FwdArgs&, hipStream_t);
-template hipError_t launch_bwd_dpf<128>(const AttnShape&, const BwdArgs&, int, hipStream_t);
+template hipError_t launch_bwd_units<128, true, true>(const AttnShape&, const BwdArgs&, int, hipStream_t);
+template hipError_t launch_bwd_units<128, false, true>(const AttnShape&, const BwdArgs&, int, hipStream_t);
+template hipError_t launch_bwd_units<128, true, false>(const AttnShape&, const BwdArgs&, int, hipStream_t);
+template hipError_t launch_bwd_units<128, false, false>(const AttnShape&, const BwdArgs&, int, hipStream_t);
 }  // namespace f32
 }  // namespace mft

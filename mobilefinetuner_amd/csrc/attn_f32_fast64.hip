@@ -5,7 +5,10 @@
 namespace mft {
 namespace f32 {
 template hipError_t launch_fwd_dpf<64>(const AttnShape&, const FwdArgs&, hipStream_t);
-template hipError_t launch_bwd_dpf<64>(const AttnShape&, const BwdArgs&, int, hipStream_t);
+template hipError_t launch_bwd_units<64, true, true>(const AttnShape&, const BwdArgs&, int, hipStream_t);
+template hipError_t launch_bwd_units<64, false, true>(const AttnShape&, const BwdArgs&, int, hipStream_t);
+template hipError_t launch_bwd_units<64, true, false>(const AttnShape&, const BwdArgs&, int, hipStream_t);
+template hipError_t launch_bwd_units<64, false, false>(const AttnShape&, const BwdArgs&, int, hipStream_t);
 
 bool fast_path(const AttnShape& s) { return !s.bf16 && s.D % 4 == 0 && s.D > 32 && s.D <= 256; }
 

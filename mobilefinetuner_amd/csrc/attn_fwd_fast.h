@@ -390,7 +390,7 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
     const int S = a.S, D = a.D;
-    const int bh = a.B * a.Hq, blk = (int)blockIdx.x;
+    const int bh = a.B * a.Hq, blk = xcd_block((int)blockIdx.x, (int)gridDim.x);  // XCD-major (see split16)
     const int unit = blk / bh, b = (blk % bh) / a.Hq, h = (blk % bh) % a.Hq, hk = h / a.group;
 
     const bf16* __restrict__ Q = (const bf16*)a.q + a.sq.at(b, h);

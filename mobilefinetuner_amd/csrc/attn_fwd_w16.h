@@ -236,7 +236,9 @@ __global__ __launch_bounds__(kW16Threads) void attn_fwd_bf16_split16(FwdArgs a) 
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
     const int S = a.S, D = a.D;
-    const int bh = a.B * a.Hq, blk = (int)blockIdx.x;
+    // XCD-major block order (xcd_block): the query heads of one unit index,
+    // which read the same K/V tiles, and neighbouring units share one L2.
+    const int bh = a.B * a.Hq, blk = xcd_block((int)blockIdx.x, (int)gridDim.x);
     const int unit = blk / bh, b = (blk % bh) / a.Hq, h = (blk % bh) % a.Hq, hk = h / a.group;
 
     const bf16* __restrict__ Q = (const bf16*)a.q + a.sq.at(b, h);

@@ -100,8 +100,7 @@ def test_no_mfma_result_overlaps_its_operands(tmp_path):
     import sys
     sys.path.insert(0, ROOT)
     from mobilefinetuner_amd import build as B
-    units = ["attn_fwd.hip", "attn_fwd_fast256.hip", "attn_bwd.hip", "attn_bwd_fast64.hip", "attn_bwd_fast256.hip",
-             "attn_f32_fast64.hip", "attn_f32_fast128.hip", "attn_f32_fast256.hip"]
+    units = sorted(f for f in os.listdir(B.CSRC) if f.startswith("attn_") and f.endswith(".hip"))
 
     def asm(name):
         out = tmp_path / (name + ".s")
