@@ -76,6 +76,16 @@ typedef struct {
     int64_t b, h, s;
 } mft_strides;
 
+/* An additive mask (mask mode): element (b, h, i, j) - batch, query head,
+ * query row, key - is ptr[b*sb + h*sh + i*si + j*sj], fp32 device memory
+ * (4-byte aligned); a zero stride broadcasts that dimension, so an [S, S] mask
+ * is (0, 0, S, 1) and a [B, 1, 1, S] padding mask (S, 0, 0, 1).  ptr = NULL:
+ * no mask. */
+typedef struct {
+    const float* ptr;
+    int64_t sb, sh, si, sj;
+} mft_mask;
+
 typedef struct {
     int64_t B, Hq, Hkv, S, D; /* batch, query heads, kv heads, sequence, head dim     */
     float scale;              /* > 0: softmax scale; <= 0: 1/sqrt(D), as
@@ -97,6 +107,22 @@ typedef struct {
                                  Values are clamped to [0, S].                        */
     mft_strides q, k, v, o;   /* layouts of q, k, v, o (see mft_strides)              */
     mft_strides dO, dq, dk, dv; /* layouts of dO and the gradients (backward)          */
+    mft_mask mask0, mask1;    /* Mask mode (either non-NULL): the scores are
+                                 x = (causal && j > i ? -1e10 : scale * q_i.k_j),
+                                 then x += mask0, then x += mask1 (float adds, in
+                                 that order), and the softmax runs over every key.
+                                 causal = 1 is the no-grad operator's rule
+                                 (core/memory_efficient_attention.cpp:163-172:
+                                 -1e10 above the diagonal, then the mask added);
+                                 the grad path's composite (:29-38) ignores the
+                                 causal flag when given a mask, i.e. causal = 0
+                                 here.  Any mask values are taken (rows masked
+                                 everywhere by one value get a uniform softmax, as
+                                 in the reference).  window must be 0 and kv_len
+                                 NULL (the masks express them).  The general
+                                 kernels run (no fast path).  lse then holds two
+                                 floats per row: [B, Hq, S, 2] = (max of the row's
+                                 scores, ln of the sum of exp(x - max)).          */
 } mft_attn_desc;
 
 /* Rows with no visible key.  With kv_len a query row can see no key (every

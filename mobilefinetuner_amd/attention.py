@@ -31,10 +31,24 @@ def _strides(**ops):
             if t is not None and not t.is_contiguous()}
 
 
-def _desc(q, k, scale, causal, window=0, kv_len=None, layouts=None):
+def _mask_spec(m, B, Hq, S):
+    """(device address, (sb, sh, si, sj)) of an additive fp32 mask: [S, S] or
+    4-D [1|B, 1|Hq, 1|S, S] (size-1 dims broadcast)."""
+    if not isinstance(m, torch.Tensor) or not m.is_cuda or m.dtype != torch.float32:
+        raise ValueError("masks must be float32 GPU tensors")
+    if m.dim() == 2:
+        m = m.view(1, 1, *m.shape)
+    if m.dim() != 4 or m.shape[3] != S or any(m.shape[i] not in (1, n) for i, n in enumerate((B, Hq, S))):
+        raise ValueError(f"a mask must be [S,S] or [1|B, 1|Hq, 1|S, S] (S={S}), got {tuple(m.shape)}")
+    st = tuple(0 if m.shape[i] == 1 else m.stride(i) for i in range(4))
+    return m.data_ptr(), st
+
+
+def _desc(q, k, scale, causal, window=0, kv_len=None, layouts=None, masks=()):
     """kv_len: None or an int32 [B] GPU tensor of valid keys per batch (key padding).
     layouts: {name: tensor} of operands (q, k, v, o, dO, dq, dk, dv) whose strides
-    go into the descriptor (the others are contiguous)."""
+    go into the descriptor (the others are contiguous).  masks: up to two
+    additive fp32 masks (mask mode; see attention_forward)."""
     if q.dtype not in _DT:
         raise ValueError(f"unsupported dtype {q.dtype}")
     B, Hq, S, D = q.shape
@@ -44,7 +58,7 @@ def _desc(q, k, scale, causal, window=0, kv_len=None, layouts=None):
             raise ValueError("kv_len must be a contiguous int32 GPU tensor of shape [B]")
         lp = kv_len.data_ptr()
     return capi.desc(B, Hq, k.shape[1], S, D, scale, causal, _DT[q.dtype], window, lp,
-                     _strides(**(layouts or {})))
+                     _strides(**(layouts or {})), [_mask_spec(m, B, Hq, S) for m in masks])
 
 
 def _stream():
@@ -62,7 +76,8 @@ def fwd_workspace_bytes(q, k, scale=-1.0, causal=True, window=0, kv_len=None):
 
 
 def attention_forward(q, k, v, scale: float = -1.0, causal: bool = True, want_lse: bool = True,
-                      workspace=None, balanced: bool = True, window: int = 0, kv_len=None, out=None):
+                      workspace=None, balanced: bool = True, window: int = 0, kv_len=None, out=None,
+                      masks=()):
     """o, lse = fused attention forward (lse None when want_lse is False).
 
     balanced=True passes the forward workspace (allocated here unless given),
@@ -71,7 +86,12 @@ def attention_forward(q, k, v, scale: float = -1.0, causal: bool = True, want_ls
     causal sliding window of that many keys; kv_len: int32 [B] GPU tensor of
     valid (unpadded) keys per batch.  q, k, v (and out, the output buffer)
     may be any [B,H,S,D] views with a contiguous head dim, e.g. transposed
-    [B,S,H,D] projections; by default o takes q's layout."""
+    [B,S,H,D] projections; by default o takes q's layout.
+
+    masks: up to two additive fp32 masks ([S,S] or [1|B, 1|Hq, 1|S, S]), added
+    to the scaled scores in order (mask mode, mft_mask: every key is visited;
+    causal=True replaces the scores above the diagonal by -1e10 first, the
+    reference's no-grad rule).  lse is then [B, Hq, S, 2]: (row max, ln sum)."""
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
         _check(t, n)
     if k.dtype != q.dtype or v.dtype != q.dtype or k.shape != v.shape:
@@ -82,8 +102,9 @@ def attention_forward(q, k, v, scale: float = -1.0, causal: bool = True, want_ls
     if o.shape != q.shape or o.dtype != q.dtype:
         raise ValueError("out must have q's shape and dtype")
     _check(o, "out")
-    d = _desc(q, k, scale, causal, window, kv_len, dict(q=q, k=k, v=v, o=o))
-    lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device) if want_lse else None
+    d = _desc(q, k, scale, causal, window, kv_len, dict(q=q, k=k, v=v, o=o), masks)
+    lse_shape = tuple(q.shape[:3]) + ((2,) if masks else ())
+    lse = torch.empty(lse_shape, dtype=torch.float32, device=q.device) if want_lse else None
     ws_ptr = None
     if balanced:
         nbytes = capi.workspace_size(d)[0]
@@ -97,7 +118,7 @@ def attention_forward(q, k, v, scale: float = -1.0, causal: bool = True, want_ls
 
 
 def attention_backward(q, k, v, o, dO, lse, scale: float = -1.0, causal: bool = True, workspace=None,
-                       window: int = 0, kv_len=None):
+                       window: int = 0, kv_len=None, masks=()):
     """dq, dk, dv (fp32; dk, dv already summed over the GQA group), each in the
     layout of q, k, v respectively (operands may be views as in attention_forward)."""
     for t, n in ((q, "q"), (k, "k"), (v, "v"), (o, "o"), (dO, "dO")):
@@ -109,7 +130,7 @@ def attention_backward(q, k, v, o, dO, lse, scale: float = -1.0, causal: bool = 
     dq = torch.empty_like(q, dtype=torch.float32)
     dk = torch.empty_like(k, dtype=torch.float32)
     dv = torch.empty_like(v, dtype=torch.float32)
-    d = _desc(q, k, scale, causal, window, kv_len, dict(q=q, k=k, v=v, o=o, dO=dO, dq=dq, dk=dk, dv=dv))
+    d = _desc(q, k, scale, causal, window, kv_len, dict(q=q, k=k, v=v, o=o, dO=dO, dq=dq, dk=dk, dv=dv), masks)
     nbytes = capi.workspace_size(d)[1]
     if workspace is None or workspace.numel() < nbytes:
         workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)

@@ -41,12 +41,18 @@ class Strides(C.Structure):
 LAYOUTS = ("q", "k", "v", "o", "dO", "dq", "dk", "dv")
 
 
+class Mask(C.Structure):
+    """mft_mask: an additive fp32 mask, element (b, h, i, j) at
+    ptr[b*sb + h*sh + i*si + j*sj] (zero strides broadcast); ptr NULL = none."""
+    _fields_ = [("ptr", C.c_void_p), ("sb", C.c_int64), ("sh", C.c_int64), ("si", C.c_int64), ("sj", C.c_int64)]
+
+
 class AttnDesc(C.Structure):
     _fields_ = [
         ("B", C.c_int64), ("Hq", C.c_int64), ("Hkv", C.c_int64), ("S", C.c_int64), ("D", C.c_int64),
         ("scale", C.c_float), ("causal", C.c_int32), ("dtype", C.c_int32),
         ("window", C.c_int32), ("kv_len", C.c_void_p),
-    ] + [(n, Strides) for n in LAYOUTS]
+    ] + [(n, Strides) for n in LAYOUTS] + [("mask0", Mask), ("mask1", Mask)]
 
 
 class PrologueDesc(C.Structure):
@@ -131,7 +137,7 @@ def lib():
     L.mft_lora_bwd.argtypes = [C.POINTER(LoraDesc)] + [vp] * 7
     L.mft_lora_merge.restype = C.c_int
     L.mft_lora_merge.argtypes = [C.POINTER(LoraDesc), vp, C.c_float, vp]
-    if L.mft_version() != 5:
+    if L.mft_version() != 6:
         raise RuntimeError("libmft_attn.so version mismatch")
     _lib = L
     return L
@@ -143,16 +149,22 @@ def check(status: int) -> None:
 
 
 def desc(B, Hq, Hkv, S, D, scale=-1.0, causal=True, dtype=MFT_BF16, window=0, kv_len=None,
-         strides=None) -> AttnDesc:
+         strides=None, masks=()) -> AttnDesc:
     """kv_len: device address of an int32 [B] array of valid keys per batch, or None.
     strides: {name: (b, h, s)} element strides per operand (names in LAYOUTS);
-    missing operands are contiguous [B, H, S, D]."""
+    missing operands are contiguous [B, H, S, D].
+    masks: up to two (device address, (sb, sh, si, sj)) additive fp32 masks
+    (mask mode, see mft_mask; lse then holds two floats per row)."""
     d = AttnDesc(int(B), int(Hq), int(Hkv), int(S), int(D), float(scale), int(bool(causal)), int(dtype),
                  int(window), kv_len)
     for name, st in (strides or {}).items():
         if name not in LAYOUTS:
             raise ValueError(f"unknown operand {name!r}")
         setattr(d, name, Strides(*(int(x) for x in st)))
+    if len(masks) > 2:
+        raise ValueError("at most two masks")
+    for i, (ptr, st) in enumerate(masks):
+        setattr(d, f"mask{i}", Mask(ptr, *(int(x) for x in st)))
     return d
 
 

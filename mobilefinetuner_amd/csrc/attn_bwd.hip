@@ -41,6 +41,23 @@ namespace mft {
 namespace {
 using namespace bwd;
 
+// Row terms of a query row for the P recompute, in log2 units:
+// P = exp2(x * lc - t0 - t1).  Plain: x is the raw dot product, lc =
+// scale * log2(e), t0 = lse * log2(e), t1 = 0.  Mask mode: x is the
+// mask_score (natural units), lc = log2(e), (t0, t1) = (row max, ln sum) *
+// log2(e) from the forward's lse pair; x * lc - t0 is exactly 0 at the row
+// max, so a uniform row (all scores equal and huge) still gets P = 1 / n.
+template <bool MASK>
+__device__ __forceinline__ void row_terms(const float* lse, int64_t ri, bool valid, float* t0, float* t1) {
+    if constexpr (MASK) {
+        *t0 = valid ? lse[2 * ri] * kLog2e : INFINITY;
+        *t1 = valid ? lse[2 * ri + 1] * kLog2e : 0.f;
+    } else {
+        *t0 = valid ? lse[ri] * kLog2e : INFINITY;
+        *t1 = 0.f;
+    }
+}
+
 // ------------------------------------------------------------------ DELTA
 template <typename T, int DP>
 __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(BwdArgs a) {
@@ -70,10 +87,10 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(BwdArgs a) {
 template <int DP> struct DkdvBf16Lds {
     static constexpr int QSTR = DP + 8;  // row-major 32-row tiles of Q and dO
     static constexpr int TSTR = 32 + 4;  // transposed tiles Q^T, dO^T: [DP][32 + 4]
-    static constexpr int BYTES = 2 * (2 * 32 * QSTR + 2 * DP * TSTR) + 2 * 32 * 4;
+    static constexpr int BYTES = 2 * (2 * 32 * QSTR + 2 * DP * TSTR) + 3 * 32 * 4;  // + row terms
 };
 
-template <int DP, int NW, bool CAUSAL>
+template <int DP, int NW, bool CAUSAL, bool MASK>
 __device__ __forceinline__ void dkdv_bf16_body(const BwdArgs& a, char* smem, int kt, int ysplit, int b) {
     typedef DkdvBf16Lds<DP> L;
     constexpr int NC = DP / 16, NDT = DP / 32, NT = NW * 64, BNK = 32 * NW;
@@ -84,6 +101,7 @@ __device__ __forceinline__ void dkdv_bf16_body(const BwdArgs& a, char* smem, int
     bf16* Gt = Qt + DP * TSTR;
     float* Ls = reinterpret_cast<float*>(Gt + DP * TSTR);
     float* Dl = Ls + 32;
+    float* L1 = Dl + 32;  // second row term (mask mode)
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
     const int S = a.S, D = a.D;
@@ -118,7 +136,7 @@ __device__ __forceinline__ void dkdv_bf16_body(const BwdArgs& a, char* smem, int
     for (int h = h_begin; h < h_end; ++h) {
         const bf16* Q = (const bf16*)a.q + a.sq.at(b, h);
         const bf16* G = (const bf16*)a.dO + a.sdo.at(b, h);
-        const float* lse = a.lse + (int64_t)(b * a.Hq + h) * S;
+        const float* lse = a.lse + (int64_t)(b * a.Hq + h) * S * (MASK ? 2 : 1);
         const float* dl = a.delta + (int64_t)(b * a.Hq + h) * S;
         for (int qb = qstart; qb < qend; qb += 32) {
             __syncthreads();
@@ -146,7 +164,7 @@ __device__ __forceinline__ void dkdv_bf16_body(const BwdArgs& a, char* smem, int
                 }
                 if (tid < 32) {
                     const int r = qb + tid;
-                    Ls[tid] = r < S ? lse[r] * kLog2e : INFINITY;
+                    row_terms<MASK>(lse, r, r < S, &Ls[tid], &L1[tid]);
                     Dl[tid] = r < S ? dl[r] : 0.f;
                 }
             }
@@ -174,11 +192,21 @@ __device__ __forceinline__ void dkdv_bf16_body(const BwdArgs& a, char* smem, int
             for (int g = 0; g < 4; ++g) {
                 const f32x4 l4 = *reinterpret_cast<const f32x4*>(Ls + 8 * g + 4 * hh);
                 const f32x4 d4 = *reinterpret_cast<const f32x4*>(Dl + 8 * g + 4 * hh);
+                const f32x4 e4 = MASK ? *reinterpret_cast<const f32x4*>(L1 + 8 * g + 4 * hh) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int r = 4 * g + i;
-                    float p = fast_exp2(s[r] * a.scale_log2 - l4[i]);
-                    if (need_mask && !vis.visible(qb + 8 * g + 4 * hh + i, key)) p = 0.f;
+                    float p;
+                    if constexpr (MASK) {
+                        const int qr = qb + 8 * g + 4 * hh + i;
+                        const float x = qr < S && key < S
+                                            ? mask_score(s[r], a.scale, a.mask_causal, a.m0, a.m1, b, h, qr, key)
+                                            : -INFINITY;
+                        p = fast_exp2((x * kLog2e - l4[i]) - e4[i]);
+                    } else {
+                        p = fast_exp2(s[r] * a.scale_log2 - l4[i]);
+                        if (need_mask && !vis.visible(qb + 8 * g + 4 * hh + i, key)) p = 0.f;
+                    }
                     dp[r] = p * (dp[r] - d4[i]);
                     s[r] = p;
                 }
@@ -216,10 +244,10 @@ __device__ __forceinline__ void dkdv_bf16_body(const BwdArgs& a, char* smem, int
 // ------------------------------------------------------- dK/dV role (fp32)
 template <int DP, int NW> struct DkdvF32Lds {
     static constexpr int STR = DP + 4;
-    static constexpr int BYTES = 4 * (2 * 32 * NW * STR + 2 * 32 * STR + 64);
+    static constexpr int BYTES = 4 * (2 * 32 * NW * STR + 2 * 32 * STR + 96);
 };
 
-template <int DP, int NW, bool CAUSAL>
+template <int DP, int NW, bool CAUSAL, bool MASK>
 __device__ __forceinline__ void dkdv_f32_body(const BwdArgs& a, char* smem, int kt, int ysplit, int b) {
     constexpr int NC = DP / 8, NDT = DP / 32, NT = NW * 64, BNK = 32 * NW;
     constexpr int STR = DkdvF32Lds<DP, NW>::STR;
@@ -229,6 +257,7 @@ __device__ __forceinline__ void dkdv_f32_body(const BwdArgs& a, char* smem, int 
     float* Gs = Qs + 32 * STR;
     float* Ls = Gs + 32 * STR;
     float* Dl = Ls + 32;
+    float* L1 = Dl + 32;  // second row term (mask mode)
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
     const int S = a.S, D = a.D;
@@ -268,7 +297,7 @@ __device__ __forceinline__ void dkdv_f32_body(const BwdArgs& a, char* smem, int 
     for (int h = h_begin; h < h_end; ++h) {
         const float* Q = (const float*)a.q + a.sq.at(b, h);
         const float* G = (const float*)a.dO + a.sdo.at(b, h);
-        const float* lse = a.lse + (int64_t)(b * a.Hq + h) * S;
+        const float* lse = a.lse + (int64_t)(b * a.Hq + h) * S * (MASK ? 2 : 1);
         const float* dl = a.delta + (int64_t)(b * a.Hq + h) * S;
         for (int qb = qstart; qb < qend; qb += 32) {
             __syncthreads();
@@ -284,7 +313,7 @@ __device__ __forceinline__ void dkdv_f32_body(const BwdArgs& a, char* smem, int 
                 }
                 if (tid < 32) {
                     const int r = qb + tid;
-                    Ls[tid] = r < S ? lse[r] * kLog2e : INFINITY;
+                    row_terms<MASK>(lse, r, r < S, &Ls[tid], &L1[tid]);
                     Dl[tid] = r < S ? dl[r] : 0.f;
                 }
             }
@@ -312,11 +341,21 @@ __device__ __forceinline__ void dkdv_f32_body(const BwdArgs& a, char* smem, int 
             for (int g = 0; g < 4; ++g) {
                 const f32x4 l4 = *reinterpret_cast<const f32x4*>(Ls + 8 * g + 4 * hh);
                 const f32x4 d4 = *reinterpret_cast<const f32x4*>(Dl + 8 * g + 4 * hh);
+                const f32x4 e4 = MASK ? *reinterpret_cast<const f32x4*>(L1 + 8 * g + 4 * hh) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int r = 4 * g + i;
-                    float p = fast_exp2(s[r] * a.scale_log2 - l4[i]);
-                    if (need_mask && !vis.visible(qb + 8 * g + 4 * hh + i, key)) p = 0.f;
+                    float p;
+                    if constexpr (MASK) {
+                        const int qr = qb + 8 * g + 4 * hh + i;
+                        const float x = qr < S && key < S
+                                            ? mask_score(s[r], a.scale, a.mask_causal, a.m0, a.m1, b, h, qr, key)
+                                            : -INFINITY;
+                        p = fast_exp2((x * kLog2e - l4[i]) - e4[i]);
+                    } else {
+                        p = fast_exp2(s[r] * a.scale_log2 - l4[i]);
+                        if (need_mask && !vis.visible(qb + 8 * g + 4 * hh + i, key)) p = 0.f;
+                    }
                     dp[r] = p * (dp[r] - d4[i]);
                     s[r] = p;
                 }
@@ -348,7 +387,7 @@ template <typename T, int DP, int BN> struct DqLds {
     static constexpr int BYTES = (int)sizeof(T) * (2 * KV_ELEMS + KT_ELEMS);
 };
 
-template <typename T, int DP, int NW, int BN, bool CAUSAL>
+template <typename T, int DP, int NW, int BN, bool CAUSAL, bool MASK>
 __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int qt, int h, int b) {
     typedef typename Elt<T>::vec V;
     typedef DqLds<T, DP, BN> L;
@@ -382,7 +421,8 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int qt, in
         if constexpr (GF_REG) gf[c] = load_chunk<T>(grow, 2 * VEC * c + VEC * hh, D, row < S, vec_ok);
     }
     const int64_t rbase = (int64_t)(b * a.Hq + h) * S;
-    const float lse2 = row < S ? a.lse[rbase + row] * kLog2e : INFINITY;
+    float lse2, lse2b;
+    row_terms<MASK>(a.lse, rbase + row, row < S, &lse2, &lse2b);
     const float dlt = row < S ? a.delta[rbase + row] : 0.f;
 
     f32x16 dq[NDT];
@@ -451,8 +491,17 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int qt, in
             // lane column n = query row; register r = key kbase + 32kk + row_of_reg(r, hh)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                float p = fast_exp2(s[r] * a.scale_log2 - lse2);
-                if (need_mask && !vis.visible(row, kbase + 32 * kk + row_of_reg(r, hh))) p = 0.f;
+                const int key = kbase + 32 * kk + row_of_reg(r, hh);
+                float p;
+                if constexpr (MASK) {
+                    const float x = row < S && key < S
+                                        ? mask_score(s[r], a.scale, a.mask_causal, a.m0, a.m1, b, h, row, key)
+                                        : -INFINITY;
+                    p = fast_exp2((x * kLog2e - lse2) - lse2b);
+                } else {
+                    p = fast_exp2(s[r] * a.scale_log2 - lse2);
+                    if (need_mask && !vis.visible(row, key)) p = 0.f;
+                }
                 s[r] = p * (dp[r] - dlt);
             }
             if constexpr (L::KT) {
@@ -494,41 +543,42 @@ __device__ __forceinline__ void dq_body(const BwdArgs& a, char* smem, int qt, in
 }
 
 // bf16 (head dims the fast path does not take): one launch per role.
-template <int DP, bool CAUSAL>
+// MASK: mask mode (AttnShape::masked; CAUSAL false, every key).
+template <int DP, bool CAUSAL, bool MASK>
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_bf16(BwdArgs a) {
     __shared__ __attribute__((aligned(16))) char smem[DkdvBf16Lds<DP>::BYTES];
     const int i = blockIdx.x;
     const int yb = a.Hkv * a.splits * a.B;
     const int t = i / yb, rest = i - t * yb;
-    dkdv_bf16_body<DP, 4, CAUSAL>(a, smem, t, rest % (a.Hkv * a.splits), rest / (a.Hkv * a.splits));
+    dkdv_bf16_body<DP, 4, CAUSAL, MASK>(a, smem, t, rest % (a.Hkv * a.splits), rest / (a.Hkv * a.splits));
 }
 
-template <int DP, bool CAUSAL>
+template <int DP, bool CAUSAL, bool MASK>
 __global__ __launch_bounds__(256) void attn_bwd_dq_bf16(BwdArgs a) {
     __shared__ __attribute__((aligned(16))) char smem[DqLds<bf16, DP, 64>::BYTES];
     const int i = blockIdx.x;
     const int yb = a.Hq * a.B;
     const int ti = i / yb, rest = i - ti * yb;
-    dq_body<bf16, DP, 4, 64, CAUSAL>(a, smem, a.n_qtiles - 1 - ti, rest % a.Hq, rest / a.Hq);
+    dq_body<bf16, DP, 4, 64, CAUSAL, MASK>(a, smem, a.n_qtiles - 1 - ti, rest % a.Hq, rest / a.Hq);
 }
 
 // fp32: the roles use different block sizes, so they are two launches.
-template <int DP, int NW, bool CAUSAL>
+template <int DP, int NW, bool CAUSAL, bool MASK>
 __global__ __launch_bounds__(NW * 64) void attn_bwd_dkdv_f32(BwdArgs a) {
     __shared__ __attribute__((aligned(16))) char smem[DkdvF32Lds<DP, NW>::BYTES];
     const int i = blockIdx.x;
     const int yb = a.Hkv * a.splits * a.B;
     const int t = i / yb, rest = i - t * yb;
-    dkdv_f32_body<DP, NW, CAUSAL>(a, smem, t, rest % (a.Hkv * a.splits), rest / (a.Hkv * a.splits));
+    dkdv_f32_body<DP, NW, CAUSAL, MASK>(a, smem, t, rest % (a.Hkv * a.splits), rest / (a.Hkv * a.splits));
 }
 
-template <int DP, int BN, bool CAUSAL>
+template <int DP, int BN, bool CAUSAL, bool MASK>
 __global__ __launch_bounds__(256) void attn_bwd_dq_f32(BwdArgs a) {
     __shared__ __attribute__((aligned(16))) char smem[DqLds<float, DP, BN>::BYTES];
     const int i = blockIdx.x;
     const int yb = a.Hq * a.B;
     const int ti = i / yb, rest = i - ti * yb;
-    dq_body<float, DP, 4, BN, CAUSAL>(a, smem, a.n_qtiles - 1 - ti, rest % a.Hq, rest / a.Hq);
+    dq_body<float, DP, 4, BN, CAUSAL, MASK>(a, smem, a.n_qtiles - 1 - ti, rest % a.Hq, rest / a.Hq);
 }
 
 
@@ -547,23 +597,26 @@ hipError_t launch_bwd_t(const AttnShape& s, BwdArgs a, int stages, hipStream_t s
     if (stages & (BWD_STAGE_DKDV | BWD_STAGE_DQ)) {
         constexpr int NW = BF ? 4 : f32_dkdv_warps(DP), BN = BF ? 64 : f32_dq_bn(DP);
         const bool kv = stages & BWD_STAGE_DKDV, q = stages & BWD_STAGE_DQ;
-        if constexpr (BF) {
-            if (s.causal) {
-                if (kv) hipLaunchKernelGGL((attn_bwd_dkdv_bf16<DP, true>), dim3(a.n_kv_blocks), dim3(256), 0, st, a);
-                if (q) hipLaunchKernelGGL((attn_bwd_dq_bf16<DP, true>), dim3(a.n_q_blocks), dim3(256), 0, st, a);
-            } else {
-                if (kv) hipLaunchKernelGGL((attn_bwd_dkdv_bf16<DP, false>), dim3(a.n_kv_blocks), dim3(256), 0, st, a);
-                if (q) hipLaunchKernelGGL((attn_bwd_dq_bf16<DP, false>), dim3(a.n_q_blocks), dim3(256), 0, st, a);
-            }
-        } else {
-            if (s.causal) {
-                if (kv) hipLaunchKernelGGL((attn_bwd_dkdv_f32<DP, NW, true>), dim3(a.n_kv_blocks), dim3(NW * 64), 0, st, a);
-                if (q) hipLaunchKernelGGL((attn_bwd_dq_f32<DP, BN, true>), dim3(a.n_q_blocks), dim3(256), 0, st, a);
-            } else {
-                if (kv) hipLaunchKernelGGL((attn_bwd_dkdv_f32<DP, NW, false>), dim3(a.n_kv_blocks), dim3(NW * 64), 0, st, a);
-                if (q) hipLaunchKernelGGL((attn_bwd_dq_f32<DP, BN, false>), dim3(a.n_q_blocks), dim3(256), 0, st, a);
-            }
-        }
+        // (causal, mask mode) -> instantiation; mask mode applies the causal
+        // flag per element (mask_score) and visits every key
+#define MFT_BWD_ROLES(C, M)                                                                                     \
+    do {                                                                                                        \
+        if constexpr (BF) {                                                                                     \
+            if (kv) hipLaunchKernelGGL((attn_bwd_dkdv_bf16<DP, C, M>), dim3(a.n_kv_blocks), dim3(256), 0, st, a); \
+            if (q) hipLaunchKernelGGL((attn_bwd_dq_bf16<DP, C, M>), dim3(a.n_q_blocks), dim3(256), 0, st, a);    \
+        } else {                                                                                                \
+            if (kv)                                                                                             \
+                hipLaunchKernelGGL((attn_bwd_dkdv_f32<DP, NW, C, M>), dim3(a.n_kv_blocks), dim3(NW * 64), 0, st, a); \
+            if (q) hipLaunchKernelGGL((attn_bwd_dq_f32<DP, BN, C, M>), dim3(a.n_q_blocks), dim3(256), 0, st, a); \
+        }                                                                                                       \
+    } while (0)
+        if (s.masked)
+            MFT_BWD_ROLES(false, true);
+        else if (s.causal)
+            MFT_BWD_ROLES(true, false);
+        else
+            MFT_BWD_ROLES(false, false);
+#undef MFT_BWD_ROLES
     }
     if ((stages & BWD_STAGE_REDUCE) && a.splits > 1) {
         int64_t blocks = (a.part_stride + 255) / 256;
@@ -595,6 +648,7 @@ int padded_d(int64_t D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 
 // of contiguous operands, [B, S, Hkv, D] views and fused-QKV slices; other
 // layouts run the general kernels) and fp32 (any layout).
 bool bwd_fast_path(const AttnShape& s) {
+    if (s.masked) return false;  // mask mode: the general kernels
     return (s.bf16 && s.D % 8 == 0 && s.D > 32 && s.k.s == s.v.s) || f32::fast_path(s);
 }
 
@@ -730,6 +784,9 @@ hipError_t launch_attn_bwd(const AttnShape& s, const BwdPlan& p, const void* q, 
     a.causal = s.causal ? 1 : 0;
     a.window = s.window;
     a.kv_len = s.kv_len;
+    a.m0 = s.m0;
+    a.m1 = s.m1;
+    a.mask_causal = s.causal ? 1 : 0;
     a.sq = s.q;
     a.sk = s.k;
     a.sv = s.v;

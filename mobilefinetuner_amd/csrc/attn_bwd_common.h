@@ -40,6 +40,10 @@ struct BwdArgs {
     float* q_part;    // [B*Hq][2*q_us.units][128][D] partial dQ tiles (split_slot)
     int64_t q_part_stride;  // B*Hq*S*D
     int kv_parts_max, q_parts_max;  // most units of one tile (REDUCE runs when either is > 1)
+    // mask mode (AttnShape::masked; general kernels only): lse holds (row max,
+    // ln sum) pairs
+    MaskView m0, m1;
+    int mask_causal;
 };
 
 // Work geometry of the fast path (attn_geometry.h), shared with the forward.

@@ -117,6 +117,22 @@ mft_status check_desc(const mft_attn_desc* d, mft::AttnShape* s) {
     // A window of S or more keys hides nothing beyond the causal mask.
     s->window = d->window < d->S ? d->window : 0;
     s->kv_len = d->kv_len;
+    // Mask mode.
+    const mft_mask* masks[2] = {&d->mask0, &d->mask1};
+    mft::MaskView* views[2] = {&s->m0, &s->m1};
+    for (int i = 0; i < 2; ++i) {
+        const mft_mask& m = *masks[i];
+        *views[i] = mft::MaskView{m.ptr, m.sb, m.sh, m.si, m.sj};
+        if (!m.ptr) continue;
+        if ((reinterpret_cast<uintptr_t>(m.ptr) & 3u) != 0)
+            return fail(MFT_ERR_INVALID_ARG, "mft_attn: masks must be 4-byte aligned fp32");
+        if (m.sb < 0 || m.sh < 0 || m.si < 0 || m.sj < 0)
+            return fail(MFT_ERR_INVALID_ARG, "mft_attn: mask strides must be >= 0");
+    }
+    s->masked = d->mask0.ptr || d->mask1.ptr;
+    if (s->masked && (d->window != 0 || d->kv_len))
+        return fail(MFT_ERR_UNSUPPORTED, "mft_attn: with mask0/mask1, window must be 0 and kv_len NULL "
+                                         "(express them in the masks)");
     return MFT_OK;
 }
 
@@ -161,7 +177,7 @@ mft_status scratch_for_current_device(void** out) {
 
 extern "C" {
 
-int mft_version(void) { return 5; }
+int mft_version(void) { return 6; }
 
 const char* mft_last_error(void) { return mft::capi::g_last_error.c_str(); }
 

@@ -48,8 +48,13 @@ template <typename T, int DP, int BN> struct FwdLds {
     static constexpr int V_ELEMS = VT ? DP * VSTR : BN * VSTR;
 };
 
-template <typename T, int DP, int NW, int BN, bool CAUSAL>
+// MASK: mask mode (AttnShape::masked, CAUSAL false): every key, scores from
+// mask_score, the running max in natural units, and lse written as the pair
+// (row max, ln sum), which keeps the row's sum exact when its scores are
+// huge (a row masked by -1e10 everywhere is a uniform softmax).
+template <typename T, int DP, int NW, int BN, bool CAUSAL, bool MASK = false>
 __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
+    static_assert(!(MASK && CAUSAL), "mask mode visits every key");
     typedef typename Elt<T>::vec V;
     typedef FwdLds<T, DP, BN> L;
     constexpr int VEC = Elt<T>::VEC;
@@ -161,24 +166,27 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 float x = s[kk][r];
-                if (need_mask) {
-                    const int key = kbase + 32 * kk + row_of_reg(r, hh);
-                    if (!vis.visible(row, key)) x = -INFINITY;
-                }
+                const int key = kbase + 32 * kk + row_of_reg(r, hh);
+                if constexpr (MASK)
+                    x = key < S ? mask_score(x, a.scale, a.mask_causal, a.m0, a.m1, b, h, rowc, key) : -INFINITY;
+                else if (need_mask && !vis.visible(row, key))
+                    x = -INFINITY;
                 s[kk][r] = x;
                 mx = fmaxf(mx, x);
             }
         }
         mx = fmaxf(mx, other_half(mx));
-        const float m_new = fmaxf(m_run, mx * a.scale_log2);
+        // log2 units (MASK: natural units, scaled into the exponent below)
+        const float m_new = fmaxf(m_run, MASK ? mx : mx * a.scale_log2);
         const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = fast_exp2(m_run - m_use);
+        const float alpha = MASK ? fast_exp2((m_run - m_use) * kLog2e) : fast_exp2(m_run - m_use);
         float psum = 0.f;
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float p = fast_exp2(s[kk][r] * a.scale_log2 - m_use);
+                const float p = MASK ? fast_exp2((s[kk][r] - m_use) * kLog2e)
+                                     : fast_exp2(s[kk][r] * a.scale_log2 - m_use);
                 s[kk][r] = p;
                 psum += p;
             }
@@ -233,8 +241,15 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
         for (int g = 0; g < 4; ++g)
             store4<T>(O, 32 * dt + 8 * g + 4 * hh, D, oacc[dt][4 * g] * inv, oacc[dt][4 * g + 1] * inv,
                       oacc[dt][4 * g + 2] * inv, oacc[dt][4 * g + 3] * inv, a.vec4_ok != 0);
-    if (a.lse && hh == 0)
-        a.lse[(int64_t)(b * a.Hq + h) * S + row] = l_tot > 0.f ? (m_run + log2f(l_tot)) * kLn2 : INFINITY;
+    if (a.lse && hh == 0) {
+        const int64_t ri = (int64_t)(b * a.Hq + h) * S + row;
+        if constexpr (MASK) {
+            a.lse[2 * ri] = l_tot > 0.f ? m_run : INFINITY;
+            a.lse[2 * ri + 1] = l_tot > 0.f ? logf(l_tot) : 0.f;
+        } else {
+            a.lse[ri] = l_tot > 0.f ? (m_run + log2f(l_tot)) * kLn2 : INFINITY;
+        }
+    }
 }
 
 // Merge the partial slots of every split query tile, in slot order:
@@ -326,7 +341,9 @@ hipError_t launch_fwd_t(const AttnShape& s, FwdArgs a, hipStream_t st) {
     constexpr int BM = 32 * NW;
     a.n_qtiles = (int)((s.S + BM - 1) / BM);
     dim3 grid(a.n_qtiles, (unsigned)s.Hq, (unsigned)s.B);
-    if (s.causal)
+    if (s.masked)  // causal or not: mask_score applies the flag per element
+        hipLaunchKernelGGL((attn_fwd_kernel<T, DP, NW, BN, false, true>), grid, dim3(NW * 64), 0, st, a);
+    else if (s.causal)
         hipLaunchKernelGGL((attn_fwd_kernel<T, DP, NW, BN, true>), grid, dim3(NW * 64), 0, st, a);
     else
         hipLaunchKernelGGL((attn_fwd_kernel<T, DP, NW, BN, false>), grid, dim3(NW * 64), 0, st, a);
@@ -336,7 +353,9 @@ hipError_t launch_fwd_t(const AttnShape& s, FwdArgs a, hipStream_t st) {
 template <typename T>
 hipError_t launch_fwd_dispatch(const AttnShape& s, FwdArgs a, hipStream_t st) {
     constexpr bool F32 = sizeof(T) == 4;
-    if constexpr (!F32) {
+    if (s.masked) {
+        // mask mode: the general kernel only
+    } else if constexpr (!F32) {
         if (s.D % 8 == 0 && s.D > 32) {
             if (s.D <= 64) return launch_fwd_fast64(s, a, st);
             if (s.D <= 128) return launch_fwd_fast128(s, a, st);
@@ -387,7 +406,7 @@ int fwd_rows_per_block(const AttnShape&) { return 128; }
 
 FwdPlan plan_fwd_split(const AttnShape& s) {
     FwdPlan p{};
-    p.balanced = (s.bf16 && s.D % 8 == 0 && s.D > 32) || f32::fast_path(s);
+    p.balanced = !s.masked && ((s.bf16 && s.D % 8 == 0 && s.D > 32) || f32::fast_path(s));
     if (!p.balanced) return p;
     const int S = (int)s.S, causal = s.causal ? 1 : 0, W = s.window;
     const int64_t pairs = s.B * s.Hq;
@@ -437,6 +456,10 @@ hipError_t launch_attn_fwd(const AttnShape& s, const FwdPlan& p, const void* q, 
     a.any_split = 0;
     a.part_o = nullptr;
     a.part_ml = nullptr;
+    a.m0 = s.m0;
+    a.m1 = s.m1;
+    a.mask_causal = s.causal ? 1 : 0;
+    a.scale = s.scale;
     if (workspace && p.balanced) {
         a.us = p.us;
         a.any_split = p.any_split ? 1 : 0;

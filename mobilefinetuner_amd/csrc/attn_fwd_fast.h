@@ -48,6 +48,10 @@ struct FwdArgs {
     int any_split;           // some query tile spans several units (the combine runs)
     float* part_o;           // [B*Hq][2*us.units][128][D] unnormalised O (split_slot)
     float* part_ml;          // [B*Hq][2*units][128][2] running max (log2 units), sum
+    // mask mode (AttnShape::masked; general kernel only)
+    MaskView m0, m1;
+    int mask_causal;
+    float scale;
 };
 
 constexpr int kFwdBM = 128, kFwdBN = 64;

@@ -19,6 +19,32 @@ struct Strides {
     __host__ __device__ int64_t at(int64_t bi, int64_t hi) const { return bi * b + hi * h; }
 };
 
+// An additive mask operand (mask mode; see mft_mask in include/mft/attention.h):
+// element (b, h, i, j) - batch, query head, query row, key - at
+// p[b*sb + h*sh + i*si + j*sj], fp32; p null = none.  Zero strides broadcast.
+struct MaskView {
+    const float* p;
+    int64_t sb, sh, si, sj;
+    __host__ __device__ float at(int64_t b, int64_t h, int64_t i, int64_t j) const {
+        return p[b * sb + h * sh + i * si + j * sj];
+    }
+};
+
+// The score of (query row i, key j) of batch b, query head h in mask mode,
+// with the reference's float operations in their order: dot * scale, replaced
+// by -1e10 above the diagonal when causal (the no-grad operator,
+// core/memory_efficient_attention.cpp:160-172), then + mask0 and + mask1 (the
+// composite's mul then add, :29-38; the model graphs' base then padding mask,
+// graph/gemma_model.cpp:494-499).  No fused multiply-add: the reference rounds
+// each step.
+__device__ __forceinline__ float mask_score(float dot, float scale, int causal, const MaskView& m0,
+                                            const MaskView& m1, int b, int h, int i, int j) {
+    float x = (causal && j > i) ? -1e10f : __fmul_rn(dot, scale);
+    if (m0.p) x = __fadd_rn(x, m0.at(b, h, i, j));
+    if (m1.p) x = __fadd_rn(x, m1.at(b, h, i, j));
+    return x;
+}
+
 struct AttnShape {
     int64_t B, Hq, Hkv, S, D;
     float scale;   // resolved (> 0)
@@ -29,6 +55,11 @@ struct AttnShape {
     // Resolved layouts (contiguous [B, H, S, D] unless the caller gave strides).
     Strides q, k, v, o, dO, dq, dk, dv;
     bool contiguous;  // every operand contiguous [B, H, S, D]
+    // Mask mode (mft_mask): additive masks, general kernels only, every key
+    // visited (causal = the -1e10 replacement above the diagonal); lse holds
+    // two floats per row (the row max of the scores, ln of the sum).
+    MaskView m0, m1;
+    bool masked;
 };
 
 // Tile geometry of one kernel variant, exposed so that the C ABI can size

@@ -65,6 +65,14 @@ def lib():
         L.orc_attn_streaming.restype = C.c_int
         L.orc_attn_streaming.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64,
                                          C.c_float, C.c_int, _f32p]
+        L.orc_attn_streaming_mask.restype = C.c_int
+        L.orc_attn_streaming_mask.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64,
+                                              C.c_float, C.c_int, opt_f32, _f32p]
+        L.orc_attn_composite_masks.restype = C.c_int
+        L.orc_attn_composite_masks.argtypes = [_f32p, _f32p, _f32p, opt_f32,
+                                               _i64, _i64, _i64, _i64, _i64, C.c_float, C.c_int,
+                                               opt_f32, opt_f32, opt_f32, opt_f32,
+                                               opt_f32, opt_f32, opt_f32, opt_f32, opt_f32, opt_f32]
         L.orc_attn_f64.restype = C.c_int
         L.orc_attn_f64.argtypes = [_f32p, _f32p, _f32p, opt_f32,
                                    _i64, _i64, _i64, _i64, _i64, C.c_double, C.c_int,
@@ -323,6 +331,62 @@ def composite_masked(q, k, v, dO=None, scale=None, base_mask=None, pad_mask=None
     return dict(o=o, lse=lse, dq=dq, dk=dk, dv=dv)
 
 
+def mask_strides(m, B, Hq, S):
+    """Element strides (sb, sh, si, sj) of an additive mask array [S,S] or
+    [1|B, 1|Hq, 1|S, S] broadcast over [B, Hq, S, S] (0 for broadcast dims),
+    and the array as a C-contiguous 4-D float32 array."""
+    m = np.ascontiguousarray(m, dtype=np.float32)
+    if m.ndim == 2:
+        m = m.reshape(1, 1, *m.shape)
+    if m.ndim != 4 or m.shape[3] != S or any(m.shape[i] not in (1, n) for i, n in enumerate((B, Hq, S))):
+        raise ValueError(f"mask shape {m.shape} does not broadcast to [B, Hq, S, S]")
+    st = [0 if m.shape[i] == 1 else m.strides[i] // 4 for i in range(4)]
+    return m, np.asarray(st, dtype=np.int64)
+
+
+def composite_masks(q, k, v, dO=None, scale=None, mode=0, masks=(), want_lse=False):
+    """Reference composite with the mask mode of the C ABI: mode 0 (no causal
+    rule), 1 (-1e10 replaces the scores above the diagonal: the no-grad
+    operator's rule) or 2 (create_causal_mask added), then up to two additive
+    masks ([S,S] or [1|B, 1|Hq, 1|S, S]) in order.  lse2 (want_lse): [B,Hq,S,2]
+    row max and ln of the row sum."""
+    B, Hq, S, D = q.shape
+    Hkv = k.shape[1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    q, k, v = (np.ascontiguousarray(t, dtype=np.float32) for t in (q, k, v))
+    ms = [mask_strides(m, B, Hq, S) for m in masks]
+    if len(ms) > 2:
+        raise ValueError("at most two masks")
+    (m0, s0), (m1, s1) = (ms + [(None, None)] * 2)[:2]
+    o = np.empty_like(q)
+    lse2 = np.empty((B, Hq, S, 2), dtype=np.float32) if want_lse else None
+    dq = dk = dv = None
+    if dO is not None:
+        dO = np.ascontiguousarray(dO, dtype=np.float32)
+        dq, dk, dv = np.empty_like(q), np.empty_like(k), np.empty_like(v)
+    rc = lib().orc_attn_composite_masks(q, k, v, _ptr(dO), B, Hq, Hkv, S, D, float(scale), int(mode),
+                                        _ptr(m0), _ptr(s0), _ptr(m1), _ptr(s1),
+                                        _ptr(o), None, _ptr(lse2), _ptr(dq), _ptr(dk), _ptr(dv))
+    if rc != 0:
+        raise ValueError("orc_attn_composite_masks rejected its arguments")
+    return dict(o=o, lse2=lse2, dq=dq, dk=dk, dv=dv)
+
+
+def streaming_mask(q, k, v, mask, scale=None, causal=True):
+    """The no-grad operator with its [S,S] mask (core/memory_efficient_attention.cpp:110-200)."""
+    B, H, S, D = q.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    o = np.empty_like(q)
+    m = None if mask is None else np.ascontiguousarray(mask, np.float32)
+    rc = lib().orc_attn_streaming_mask(np.ascontiguousarray(q), np.ascontiguousarray(k), np.ascontiguousarray(v),
+                                       B, H, S, D, float(scale), int(causal), _ptr(m), o)
+    if rc != 0:
+        raise ValueError("orc_attn_streaming_mask rejected its arguments")
+    return o
+
+
 def streaming(q, k, v, scale=None, causal=True):
     B, H, S, D = q.shape
     if scale is None:
@@ -503,6 +567,57 @@ def ref_composite_masked(q, k, v, dO=None, scale=None, base_mask=None, pad_mask=
     if rc != 0:
         raise RuntimeError("reference composite (masked) raised")
     return dict(o=o, dq=dq, dk=dk, dv=dv)
+
+
+def ref_composite_mask4(q, k, v, dO=None, scale=None, masks=()):
+    """The reference composite with up to two dense masks [1|B, 1|Hq, 1|S, S]
+    added by its own broadcasting ops::add (ref_harness.cpp)."""
+    B, Hq, S, D = q.shape
+    Hkv = k.shape[1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    q, k, v = (np.ascontiguousarray(t, dtype=np.float32) for t in (q, k, v))
+    dense = []
+    for m in masks:
+        m = np.ascontiguousarray(m, np.float32)
+        if m.ndim == 2:
+            m = m.reshape(1, 1, *m.shape)
+        dense.append(m)
+    dense += [None] * (2 - len(dense))
+    o = np.empty_like(q)
+    dq = dk = dv = None
+    if dO is not None:
+        dO = np.ascontiguousarray(dO, dtype=np.float32)
+        dq, dk, dv = np.empty_like(q), np.empty_like(k), np.empty_like(v)
+    R = ref()
+    R.mftref_composite_mask4.restype = C.c_int
+    R.mftref_composite_mask4.argtypes = [_f32p, _f32p, _f32p, C.c_void_p, _i64, _i64, _i64, _i64, _i64, C.c_float,
+                                         C.c_void_p, _i64, _i64, _i64, C.c_void_p, _i64, _i64, _i64,
+                                         C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+    shp = [(m.shape[0], m.shape[1], m.shape[2]) if m is not None else (1, 1, 1) for m in dense]
+    rc = R.mftref_composite_mask4(q, k, v, _ptr(dO), B, Hq, Hkv, S, D, float(scale),
+                                  _ptr(dense[0]), *shp[0], _ptr(dense[1]), *shp[1],
+                                  _ptr(o), _ptr(dq), _ptr(dk), _ptr(dv))
+    if rc != 0:
+        raise RuntimeError("reference composite (mask4) raised")
+    return dict(o=o, dq=dq, dk=dk, dv=dv)
+
+
+def ref_memeff_nograd_mask(q, k, v, mask, scale=None, causal=True):
+    B, H, S, D = q.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    o = np.empty_like(q)
+    R = ref()
+    R.mftref_memeff_nograd_mask.restype = C.c_int
+    R.mftref_memeff_nograd_mask.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, C.c_float, C.c_int,
+                                            _f32p, _f32p]
+    rc = R.mftref_memeff_nograd_mask(np.ascontiguousarray(q), np.ascontiguousarray(k), np.ascontiguousarray(v),
+                                     B, H, S, D, float(scale), int(causal),
+                                     np.ascontiguousarray(mask, np.float32), o)
+    if rc != 0:
+        raise RuntimeError("reference memory_efficient_attention (mask) raised")
+    return o
 
 
 def ref_memeff_nograd(q, k, v, scale=None, causal=True):

@@ -166,6 +166,70 @@ int mftref_composite_masked(const float* q, const float* k, const float* v, cons
     }
 }
 
+// The composite with up to two additive masks given as dense tensors of
+// shape [mb, mh, mi, S] (mb in {1, B}, mh in {1, Hq}, mi in {1, S}), added to
+// the scaled scores by ops::add with its broadcasting (core/ops.cpp:299-377),
+// mask 0 first; no causal mask (the composite of
+// core/memory_efficient_attention.cpp:23-43 with a mask given).
+int mftref_composite_mask4(const float* q, const float* k, const float* v, const float* dO,
+                           int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, float scale,
+                           const float* m0, int64_t m0b, int64_t m0h, int64_t m0i,
+                           const float* m1, int64_t m1b, int64_t m1h, int64_t m1i,
+                           float* o, float* dq, float* dk, float* dv) {
+    try {
+        const bool grad = dO != nullptr;
+        auto qt = from_host(q, {B, Hq, S, D}, grad);
+        auto kt = from_host(k, {B, Hkv, S, D}, grad);
+        auto vt = from_host(v, {B, Hkv, S, D}, grad);
+        TensorPtr gt;
+        if (grad) gt = from_host(dO, {B, Hq, S, D}, false);
+        TensorPtr k_use = kt, v_use = vt;
+        if (Hq != Hkv) {
+            const int rep = static_cast<int>(Hq / Hkv);
+            k_use = repeat_kv_heads(kt, rep);
+            v_use = repeat_kv_heads(vt, rep);
+        }
+        auto scores = mul(matmul(qt, transpose(k_use, 2, 3)), scale);
+        if (m0) scores = add(scores, from_host(m0, {m0b, m0h, m0i, S}, false));
+        if (m1) scores = add(scores, from_host(m1, {m1b, m1h, m1i, S}, false));
+        auto out = matmul(softmax(scores, -1), v_use);
+        to_host(out, o);
+        if (grad) {
+            autograd::Engine::instance().run_backward({out}, {gt});
+            to_host(qt->grad(), dq);
+            to_host(kt->grad(), dk);
+            to_host(vt->grad(), dv);
+        }
+        autograd::Engine::instance().clear_graph();
+        return 0;
+    } catch (const std::exception& e) {
+        std::cerr << "[mftref_composite_mask4] " << e.what() << std::endl;
+        return -1;
+    }
+}
+
+// ops::memory_efficient_attention without grad and with an [S,S] mask: the
+// streaming path applies the causal rule, then adds the mask
+// (core/memory_efficient_attention.cpp:160-172).
+int mftref_memeff_nograd_mask(const float* q, const float* k, const float* v,
+                              int64_t B, int64_t H, int64_t S, int64_t D,
+                              float scale, int causal, const float* mask, float* o) {
+    try {
+        auto qt = from_host(q, {B, H, S, D}, false);
+        auto kt = from_host(k, {B, H, S, D}, false);
+        auto vt = from_host(v, {B, H, S, D}, false);
+        MemoryEfficientAttentionConfig cfg;
+        cfg.use_causal_mask = causal != 0;
+        cfg.scale = scale;
+        auto out = memory_efficient_attention(qt, kt, vt, from_host(mask, {S, S}, false), cfg);
+        to_host(out, o);
+        return 0;
+    } catch (const std::exception& e) {
+        std::cerr << "[mftref_memeff_nograd_mask] " << e.what() << std::endl;
+        return -1;
+    }
+}
+
 // ops::memory_efficient_attention with no input requiring grad: the
 // reference's streaming path (core/memory_efficient_attention.cpp:110-200).
 int mftref_memeff_nograd(const float* q, const float* k, const float* v,

@@ -145,7 +145,20 @@ int orc_attn_composite_masked(const float* q, const float* k, const float* v, co
                               int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
                               float scale, int causal, const float* base_mask, const float* pad_mask,
                               float* o, float* lse, float* dq, float* dk, float* dv) {
+    // The [S,S] base mask replaces the causal mask; the [B,1,1,S] padding
+    // mask is added after it (graph/gemma_model.cpp:494-499).
+    const int64_t sbase[4] = {0, 0, S, 1}, spad[4] = {S, 0, 0, 1};
+    return orc_attn_composite_masks(q, k, v, dO, B, Hq, Hkv, S, D, scale, base_mask ? 0 : (causal ? 2 : 0),
+                                    base_mask, sbase, pad_mask, spad, o, lse, nullptr, dq, dk, dv);
+}
+
+int orc_attn_composite_masks(const float* q, const float* k, const float* v, const float* dO,
+                             int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
+                             float scale, int mode, const float* m0, const int64_t* s0,
+                             const float* m1, const int64_t* s1,
+                             float* o, float* lse, float* lse2, float* dq, float* dk, float* dv) {
     if (!q || !k || !v || B <= 0 || Hq <= 0 || Hkv <= 0 || S <= 0 || D <= 0) return -1;
+    if (mode < 0 || mode > 2 || (m0 && !s0) || (m1 && !s1)) return -1;
     if (Hq % Hkv != 0) return -1;
     const int64_t r = Hq / Hkv;
     const int64_t SS = S * S, SD = S * D;
@@ -170,20 +183,18 @@ int orc_attn_composite_masked(const float* q, const float* k, const float* v, co
             // scores = mul(matmul(q, transpose(k, 2, 3)), scale) [+ causal mask]
             transpose2d(K, kt.data(), S, D);
             mm_nn(Q, kt.data(), sc.data(), S, S, D);
-            // Additive masks, one float add each as the reference graphs apply
-            // them (graph/gemma_model.cpp:494-499): the [S,S] base mask
-            // (causal: create_causal_mask, core/ops.cpp:2167-2180; or any
-            // given one, e.g. build_sliding_mask, graph/gemma_model.cpp:272-285),
-            // then the [B,1,1,S] padding mask (build_padding_mask, :287-321).
-            const float* pm = pad_mask ? pad_mask + b * S : nullptr;
+            // The causal rule of the mode, then the additive masks, one float
+            // add each as the reference graphs apply them
+            // (graph/gemma_model.cpp:494-499: the [S,S] base mask, e.g.
+            // build_sliding_mask :272-285, then the [B,1,1,S] padding mask
+            // build_padding_mask :287-321).
             for (int64_t i = 0; i < S; ++i) {
                 for (int64_t j = 0; j < S; ++j) {
                     float x = sc[i * S + j] * scale;
-                    if (base_mask)
-                        x = x + base_mask[i * S + j];
-                    else if (causal)
-                        x = x + (j > i ? -1e10f : 0.0f);
-                    if (pm) x = x + pm[j];
+                    if (mode == 1 && j > i) x = -1e10f;
+                    if (mode == 2) x = x + (j > i ? -1e10f : 0.0f);
+                    if (m0) x = x + m0[b * s0[0] + h * s0[1] + i * s0[2] + j * s0[3]];
+                    if (m1) x = x + m1[b * s1[0] + h * s1[1] + i * s1[2] + j * s1[3]];
                     sc[i * S + j] = x;
                 }
             }
@@ -203,6 +214,10 @@ int orc_attn_composite_masked(const float* q, const float* k, const float* v, co
                     // the same max and sum, for checking the kernel's saved LSE.
                     lse[(b * Hq + h) * S + i] =
                         static_cast<float>(static_cast<double>(mx) + std::log(static_cast<double>(sum)));
+                }
+                if (lse2) {  // the same as (row max, ln sum)
+                    lse2[2 * ((b * Hq + h) * S + i)] = mx;
+                    lse2[2 * ((b * Hq + h) * S + i) + 1] = static_cast<float>(std::log(static_cast<double>(sum)));
                 }
             }
             // context = matmul(probs, v)
@@ -252,6 +267,12 @@ int orc_attn_composite_masked(const float* q, const float* k, const float* v, co
 int orc_attn_streaming(const float* q, const float* k, const float* v,
                        int64_t B, int64_t H, int64_t S, int64_t D,
                        float scale, int causal, float* o) {
+    return orc_attn_streaming_mask(q, k, v, B, H, S, D, scale, causal, nullptr, o);
+}
+
+int orc_attn_streaming_mask(const float* q, const float* k, const float* v,
+                            int64_t B, int64_t H, int64_t S, int64_t D,
+                            float scale, int causal, const float* mask, float* o) {
     if (!q || !k || !v || !o || B <= 0 || H <= 0 || S <= 0 || D <= 0) return -1;
     std::vector<float> scores(static_cast<size_t>(S));
     for (int64_t bh = 0; bh < B * H; ++bh) {
@@ -268,6 +289,7 @@ int orc_attn_streaming(const float* q, const float* k, const float* v,
                 for (int64_t d = 0; d < D; ++d) dot += qr[d] * kr[d];
                 float s = dot * scale;
                 if (causal && j > i) s = -1e10f;
+                if (mask) s += mask[i * S + j];
                 scores[j] = s;
                 mx = std::max(mx, s);
             }

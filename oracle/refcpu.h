@@ -72,12 +72,35 @@ int orc_attn_composite_masked(const float* q, const float* k, const float* v, co
                               float scale, int causal, const float* base_mask, const float* pad_mask,
                               float* o, float* lse, float* dq, float* dk, float* dv);
 
+/* The composite with general additive masks (the mask mode of the C ABI):
+ *   mode 0: x = s * scale
+ *   mode 1: x = j > i ? -1e10 : s * scale   (the no-grad operator's causal rule,
+ *           core/memory_efficient_attention.cpp:163-167)
+ *   mode 2: x = s * scale + (j > i ? -1e10 : 0)   (create_causal_mask added,
+ *           core/ops.cpp:2167-2180)
+ * then x = x + m0[b*s0[0] + h*s0[1] + i*s0[2] + j*s0[3]] and the same for m1
+ * (each may be NULL; float adds in that order, ops::add's broadcast,
+ * core/ops.cpp:299-377), then the composite's softmax, matmul and Engine
+ * backward as orc_attn_composite.  lse2, if given, is [B,Hq,S,2]: the row max
+ * and ln of the float row sum (not reference outputs: for checking the
+ * kernels' row terms). */
+int orc_attn_composite_masks(const float* q, const float* k, const float* v, const float* dO,
+                             int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
+                             float scale, int mode, const float* m0, const int64_t* s0,
+                             const float* m1, const int64_t* s1,
+                             float* o, float* lse, float* lse2, float* dq, float* dk, float* dv);
+
 /* The no-grad streaming path of ops::memory_efficient_attention
  * (core/memory_efficient_attention.cpp:110-200): double sum_exp, float
  * inv_sum, float context accumulation.  MHA only (Hq == Hkv), as there. */
 int orc_attn_streaming(const float* q, const float* k, const float* v,
                        int64_t B, int64_t H, int64_t S, int64_t D,
                        float scale, int causal, float* o);
+/* The same with the operator's optional [S,S] mask added after the causal
+ * replacement (core/memory_efficient_attention.cpp:169-172). */
+int orc_attn_streaming_mask(const float* q, const float* k, const float* v,
+                            int64_t B, int64_t H, int64_t S, int64_t D,
+                            float scale, int causal, const float* mask, float* o);
 
 /* Independent fp64 brute-force attention (textbook formula, no reference
  * op order) used as a third check.  Outputs are double. */

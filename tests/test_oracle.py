@@ -283,3 +283,77 @@ def test_mask_builders_and_invariants(orc):
     assert np.all(r["dk"][0, :, 7:] == 0) and np.all(r["dv"][0, :, 7:] == 0)
     ref7 = orc.composite(q[:, :, :7], k[:, :, :7], v[:, :, :7], dO[:, :, :7], scale=0.3, causal=True)
     assert np.allclose(r["o"][:, :, :7], ref7["o"], atol=1e-6)
+
+
+# ------------------------------------ general additive masks (the mask mode)
+def _general_masks(B, Hq, S, seed):
+    rng = np.random.default_rng(seed)
+    ss = rng.normal(size=(S, S)).astype(np.float32)
+    ss[rng.random((S, S)) < 0.3] = -1e10
+    ss[S // 2, :] = -1e10  # a row masked everywhere: uniform softmax
+    bss = rng.normal(size=(B, 1, S, S)).astype(np.float32)
+    bss[:, :, 1, :] = -1e9
+    left = np.zeros((B, 1, 1, S), np.float32)
+    left[:, :, :, :3] = -1e10  # left padding (not a suffix)
+    head = (-0.25 * np.arange(1, Hq + 1)[None, :, None, None] * np.arange(S)[None, None, None, :]).astype(np.float32)
+    return ss, bss, left, head
+
+
+@pytest.mark.parametrize("which", [(0,), (1,), (2,), (3,), (0, 2), (1, 3)])
+def test_general_mask_composite_equals_live_reference(orc, which):
+    """orc.composite_masks (mode 0) bit-exact against the reference composite
+    with the same dense masks added by its own broadcasting ops::add
+    (ref_harness.cpp mftref_composite_mask4): [S,S], [B,1,S,S], [B,1,1,S] and
+    [1,Hq,1,S] masks, alone and two in order."""
+    _need_ref(orc)
+    B, Hq, Hkv, S, D = 2, 4, 2, 41, 24
+    q, k, v, dO = orc.make_inputs(B, Hq, Hkv, S, D, 83, "f32", 0.5)
+    all_m = _general_masks(B, Hq, S, 5)
+    masks = [all_m[i] for i in which]
+    a = orc.composite_masks(q, k, v, dO, scale=0.3, mode=0, masks=masks)
+    b = orc.ref_composite_mask4(q, k, v, dO, scale=0.3, masks=masks)
+    for t in ("o", "dq", "dk", "dv"):
+        assert np.array_equal(_bits(a[t]), _bits(b[t])), t
+
+
+def test_mask_streaming_equals_live_reference(orc):
+    """The no-grad operator with an [S,S] mask (core/memory_efficient_attention.cpp:
+    160-172: causal replacement by -1e10, then + mask), bit-exact; the mask
+    mode's composite arithmetic with the same rule (mode 1) is within 1e-6."""
+    _need_ref(orc)
+    B, H, S, D = 2, 3, 37, 32
+    q, k, v, _ = orc.make_inputs(B, H, H, S, D, 19, "f32")
+    ss = _general_masks(B, H, S, 9)[0]
+    for causal in (True, False):
+        a = orc.streaming_mask(q, k, v, ss, 0.2, causal)
+        b = orc.ref_memeff_nograd_mask(q, k, v, ss, 0.2, causal)
+        assert np.array_equal(_bits(a), _bits(b)), causal
+        c = orc.composite_masks(q, k, v, None, scale=0.2, mode=1 if causal else 0, masks=[ss])["o"]
+        assert orc.max_rel(c, b) <= 1e-6, causal
+
+
+def test_general_mask_invariants(orc):
+    """What the mathematics fixes for additive masks: a row masked everywhere
+    by one value is a uniform softmax (O = mean of V); adding a constant to a
+    whole row of the mask changes nothing; an all-zero mask is the unmasked
+    composite; mode 2 equals mode 0 with create_causal_mask as the mask."""
+    B, Hq, Hkv, S, D = 1, 2, 1, 30, 16
+    q, k, v, dO = orc.make_inputs(B, Hq, Hkv, S, D, 23, "f32", 0.5)
+    full = np.full((S, S), -1e10, np.float32)
+    o = orc.composite_masks(q, k, v, None, scale=0.25, masks=[full])["o"]
+    assert np.allclose(o[0, 0], v[0, 0].mean(axis=0), atol=1e-6)
+    rng = np.random.default_rng(3)
+    m = rng.normal(size=(S, S)).astype(np.float32)
+    shift = (m + 3.0 * np.arange(S, dtype=np.float32)[:, None]).astype(np.float32)
+    a = orc.composite_masks(q, k, v, dO, scale=0.25, masks=[m])
+    b = orc.composite_masks(q, k, v, dO, scale=0.25, masks=[shift])
+    for t in ("o", "dq", "dk", "dv"):
+        assert orc.max_rel(a[t], b[t]) <= 1e-5, t
+    z = orc.composite_masks(q, k, v, dO, scale=0.25, masks=[np.zeros((S, S), np.float32)])
+    p = orc.composite(q, k, v, dO, scale=0.25, causal=False)
+    for t in ("o", "dq", "dk", "dv"):
+        assert np.array_equal(_bits(z[t]), _bits(p[t])), t
+    c2 = orc.composite_masks(q, k, v, dO, scale=0.25, mode=2)
+    c0 = orc.composite_masks(q, k, v, dO, scale=0.25, mode=0, masks=[orc.causal_mask(S)])
+    for t in ("o", "dq", "dk", "dv"):
+        assert np.array_equal(_bits(c2[t]), _bits(c0[t])), t
