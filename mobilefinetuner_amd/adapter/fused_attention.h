@@ -19,14 +19,15 @@
 namespace ops {
 
 // q [B,Hq,S,D]; k, v [B,Hkv,S,D] with Hkv | Hq; float32 or bfloat16 host
-// tensors.  base_mask: nullptr, all-zero, causal (create_causal_mask) or a
-// causal sliding window (build_sliding_mask), [S,S].  pad_mask: nullptr or
-// the [B,1,1,S] additive mask of a right-padded attention_mask (0 on the
-// first len[b] keys, <= -1e9 after).  Scale: cfg.scale > 0, else 1/sqrt(D);
-// cfg.use_causal_mask is not used (the masks say it).  Returns fp32
-// [B,Hq,S,D]; with grad, one autograd node whose backward returns
-// {dQ, dK, dV} (dK, dV summed over each kv head's query heads).  Other masks
-// throw std::runtime_error.
+// tensors.  base_mask: nullptr or an fp32 [S,S] additive mask; pad_mask:
+// nullptr or an fp32 [B,1,1,S] additive mask.  A causal / sliding base
+// (create_causal_mask, build_sliding_mask) with right padding (0 on the first
+// len[b] keys, <= -1e9 after) runs the fast kernels; any other masks run the
+// kernels' mask mode (scores + base_mask, then + pad_mask).  Scale:
+// cfg.scale > 0, else 1/sqrt(D); cfg.use_causal_mask is not used (the masks
+// say it).  Returns fp32 [B,Hq,S,D]; with grad, one autograd node whose
+// backward returns {dQ, dK, dV} (dK, dV summed over each kv head's query
+// heads).
 TensorPtr memory_efficient_attention_masked(const TensorPtr& q, const TensorPtr& k, const TensorPtr& v,
                                             const TensorPtr& base_mask, const TensorPtr& pad_mask,
                                             const MemoryEfficientAttentionConfig& config = {});

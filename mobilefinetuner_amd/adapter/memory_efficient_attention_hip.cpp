@@ -25,14 +25,19 @@
 //     (create_causal_mask, core/ops.cpp:2167-2180: 0 on/below the diagonal,
 //     <= -1e9 above) or a causal sliding-window mask (Gemma's
 //     build_sliding_mask, graph/gemma_model.cpp:272-285) map to the kernels'
-//     causal flag and window with the reference's precedence.  Other additive
-//     masks are rejected with an error (there is no CPU fallback).
+//     causal flag and window with the reference's precedence (the fast
+//     kernels).  Any other fp32 additive mask runs the kernels' mask mode
+//     (mft_mask, the general kernels): [S,S] on both paths, and on the grad
+//     path also the 4-D masks the composite's ops::add broadcasts,
+//     [1|B, 1|Hq, 1|S, S].
 //   * Extension for the model graphs (fused_attention.h):
 //     memory_efficient_attention_masked(q, k, v, base_mask, pad_mask, cfg) is
 //     the Gemma / Qwen composite (graph/gemma_model.cpp:481-505,
 //     graph/qwen_model.cpp:302-318: scores + base_mask, then + pad_mask) in
 //     one op, with the [B,1,1,S] padding mask of a right-padded
-//     attention_mask passed to the kernels as per-batch key lengths.
+//     attention_mask passed to the kernels as per-batch key lengths; other
+//     masks (any base, padding that is not a suffix) run the mask mode with
+//     both masks added in the composite's order.
 //   * Tensors are the reference's host tensors: inputs are copied to the GPU,
 //     results back (PCIe-inclusive).  Device-resident callers use the C ABI.
 #include "memory_efficient_attention.h"
@@ -107,9 +112,8 @@ struct BaseMask {
 BaseMask classify_mask(const TensorPtr& mask, int64_t S) {
     BaseMask r;
     if (!mask) return r;
-    if (mask->shape().size() != 2 || mask->shape()[0] != S || mask->shape()[1] != S)
-        throw std::runtime_error("memory_efficient_attention: causal_mask must be [S,S]");
     r.kind = MaskKind::kOther;
+    if (mask->shape().size() != 2 || mask->shape()[0] != S || mask->shape()[1] != S) return r;
     if (mask->dtype() != kFloat32) return r;
     const float* m = mask->data<float>();
     // Candidate window: the zeros at the end of the last row.
@@ -148,6 +152,7 @@ BaseMask classify_mask(const TensorPtr& mask, int64_t S) {
 struct PadMask {
     std::vector<int32_t> len;
     float lo = INFINITY, hi = -INFINITY;  // range of the masked entries' values (empty: none masked)
+    bool suffix = true;                   // masks a suffix of the keys (right padding): len is valid
     bool masks_any() const { return lo <= hi; }
 };
 
@@ -164,9 +169,10 @@ PadMask classify_pad_mask(const TensorPtr& mask, int64_t B, int64_t S) {
         while (n < S && m[b * S + n] == 0.0f) ++n;
         for (int64_t j = n; j < S; ++j) {
             const float x = m[b * S + j];
-            if (!(x <= -1e9f))
-                throw std::runtime_error(
-                    "memory_efficient_attention_masked: pad_mask must mask a suffix of the keys (right padding)");
+            if (!(x <= -1e9f)) {  // not a masked suffix: the mask mode takes it as it is
+                r.suffix = false;
+                return r;
+            }
             r.lo = std::min(r.lo, x);
             r.hi = std::max(r.hi, x);
         }
@@ -175,11 +181,54 @@ PadMask classify_pad_mask(const TensorPtr& mask, int64_t B, int64_t S) {
     return r;
 }
 
+// A mask of the mask mode: the fp32 host mask, copied to the device, and its
+// element strides over (batch, query head, query row, key); size-1 dims of a
+// 4-D [1|B, 1|Hq, 1|S, S] mask, and the leading dims of an [S,S] one,
+// broadcast (stride 0), as ops::add broadcasts them (core/ops.cpp:299-377).
+struct DeviceMask {
+    std::unique_ptr<DeviceBuffer> buf;
+    mft_mask m{};
+};
+
+DeviceMask upload_mask(const TensorPtr& mask, int64_t B, int64_t Hq, int64_t S, bool allow_4d, const char* who) {
+    if (mask->dtype() != kFloat32) throw std::runtime_error(std::string(who) + ": masks must be float32");
+    const auto& sh = mask->shape();
+    int64_t dims[4] = {1, 1, 0, 0};
+    if (sh.size() == 2) {
+        dims[2] = sh[0];
+        dims[3] = sh[1];
+    } else if (sh.size() == 4 && allow_4d) {
+        for (int i = 0; i < 4; ++i) dims[i] = sh[static_cast<size_t>(i)];
+    } else {
+        throw std::runtime_error(std::string(who) + (allow_4d ? ": mask must be [S,S] or [1|B, 1|Hq, 1|S, S]"
+                                                               : ": causal_mask must be [S,S]"));
+    }
+    const int64_t full[4] = {B, Hq, S, S};
+    for (int i = 0; i < 4; ++i)
+        if (dims[i] != full[i] && !(dims[i] == 1 && i < 3))
+            throw std::runtime_error(std::string(who) + ": mask shape does not broadcast to [B, Hq, S, S]");
+    DeviceMask d;
+    const size_t n = static_cast<size_t>(mask->numel());
+    d.buf = std::make_unique<DeviceBuffer>(n * 4);
+    hip_check(hipMemcpyAsync(d.buf->get(), mask->data<float>(), n * 4, hipMemcpyHostToDevice, adapter_stream()),
+              "copy mask");
+    int64_t st[4];
+    st[3] = 1;
+    for (int i = 2; i >= 0; --i) st[i] = st[i + 1] * dims[i + 1];
+    d.m.ptr = static_cast<const float*>(d.buf->get());
+    d.m.sb = dims[0] == 1 ? 0 : st[0];
+    d.m.sh = dims[1] == 1 ? 0 : st[1];
+    d.m.si = dims[2] == 1 ? 0 : st[2];
+    d.m.sj = 1;
+    return d;
+}
+
 // What the kernels hold between forward and backward.
 struct SavedForBackward {
     mft_attn_desc desc{};
     std::vector<int64_t> q_shape, kv_shape;
     std::unique_ptr<DeviceBuffer> q, k, v, o, lse, kv_len;
+    DeviceMask mask0, mask1;  // mask mode: the masks the backward re-reads
 };
 
 class FusedAttentionBackward : public BackwardFunction {
@@ -276,8 +325,10 @@ Checked check_inputs(const TensorPtr& q, const TensorPtr& k, const TensorPtr& v,
 }
 
 // Forward on the device, and the autograd node when a grad is needed.
+// mask0 / mask1: the mask mode's masks (moved into the saved state).
 TensorPtr run_fused(const TensorPtr& q, const TensorPtr& k, const TensorPtr& v, const Checked& c, bool causal,
-                    int64_t window, const std::vector<int32_t>& lengths) {
+                    int64_t window, const std::vector<int32_t>& lengths, DeviceMask mask0 = {},
+                    DeviceMask mask1 = {}) {
     const auto& qs = q->shape();
     const auto& ks = k->shape();
     const DType dt = c.dt;
@@ -302,6 +353,11 @@ TensorPtr run_fused(const TensorPtr& q, const TensorPtr& k, const TensorPtr& v, 
                   "copy kv_len");
         d.kv_len = static_cast<const int32_t*>(saved->kv_len->get());
     }
+    d.mask0 = mask0.m;
+    d.mask1 = mask1.m;
+    const bool mask_mode = d.mask0.ptr || d.mask1.ptr;
+    saved->mask0 = std::move(mask0);
+    saved->mask1 = std::move(mask1);
     saved->desc = d;
     saved->q_shape = qs;
     saved->kv_shape = ks;
@@ -309,7 +365,8 @@ TensorPtr run_fused(const TensorPtr& q, const TensorPtr& k, const TensorPtr& v, 
     saved->k = upload(k);
     saved->v = upload(v);
     saved->o = std::make_unique<DeviceBuffer>(static_cast<size_t>(q->numel()) * elt_size(dt));
-    if (needs_grad) saved->lse = std::make_unique<DeviceBuffer>(static_cast<size_t>(B * Hq * S) * 4);
+    // (mask mode: two floats per row, the row max and ln of the sum)
+    if (needs_grad) saved->lse = std::make_unique<DeviceBuffer>(static_cast<size_t>(B * Hq * S) * (mask_mode ? 8 : 4));
     size_t fwd_ws = 0, bwd_ws = 0;
     mft_check(mft_attn_workspace_size(&d, &fwd_ws, &bwd_ws));
     DeviceBuffer ws(fwd_ws);
@@ -336,10 +393,13 @@ TensorPtr memory_efficient_attention(const TensorPtr& q, const TensorPtr& k, con
     // path (.cpp:163-172) applies use_causal_mask and then adds the mask.
     const BaseMask mk = classify_mask(causal_mask, c.S);
     bool causal = config.use_causal_mask;
-    if (mk.kind == MaskKind::kOther)
-        throw std::runtime_error(
-            "memory_efficient_attention: only the causal or sliding-window mask (or none) is supported on the GPU "
-            "path");
+    if (mk.kind == MaskKind::kOther) {
+        // Mask mode.  Grad path: the composite adds the mask and ignores
+        // use_causal_mask (.cpp:29-38); no-grad path: -1e10 above the diagonal
+        // when use_causal_mask, then the [S,S] mask added (.cpp:160-172).
+        DeviceMask m = upload_mask(causal_mask, c.B, c.Hq, c.S, c.needs_grad, "memory_efficient_attention");
+        return run_fused(q, k, v, c, c.needs_grad ? false : causal, 0, {}, std::move(m));
+    }
     if (mk.kind == MaskKind::kCausal || mk.kind == MaskKind::kSliding) causal = true;
     if (mk.kind == MaskKind::kZero && c.needs_grad) causal = false;
     return run_fused(q, k, v, c, causal, mk.kind == MaskKind::kSliding ? mk.window : 0, {});
@@ -350,16 +410,21 @@ TensorPtr memory_efficient_attention_masked(const TensorPtr& q, const TensorPtr&
                                             const MemoryEfficientAttentionConfig& config) {
     const Checked c = check_inputs(q, k, v, config);
     const BaseMask bm = classify_mask(base_mask, c.S);
-    if (bm.kind == MaskKind::kOther)
-        throw std::runtime_error(
-            "memory_efficient_attention_masked: base_mask must be causal, sliding-window, all-zero or null");
     const PadMask pm = classify_pad_mask(pad_mask, c.B, c.S);
-    // Rows that see no key follow the reference's -1e10 arithmetic, which the
-    // kernels reproduce when a window's and the padding's masked entries
-    // carry one value (Gemma: kMaskValue for both, graph/gemma_model.cpp:175).
-    if (bm.kind == MaskKind::kSliding && pm.masks_any() && !(bm.lo == bm.hi && pm.lo == pm.hi && bm.lo == pm.lo))
-        throw std::runtime_error(
-            "memory_efficient_attention_masked: a sliding window with padding needs one masked value in both masks");
+    // The fast kernels take a causal or sliding base mask with right padding;
+    // their rows that see no key follow the reference's -1e10 arithmetic when
+    // a window's and the padding's masked entries carry one value (Gemma:
+    // kMaskValue for both, graph/gemma_model.cpp:175).  Anything else runs the
+    // mask mode: scores + base_mask, then + pad_mask, as the composite adds them.
+    if (bm.kind == MaskKind::kOther || !pm.suffix ||
+        (bm.kind == MaskKind::kSliding && pm.masks_any() && !(bm.lo == bm.hi && pm.lo == pm.hi && bm.lo == pm.lo))) {
+        const char* who = "memory_efficient_attention_masked";
+        DeviceMask m0, m1;
+        if (base_mask) m0 = upload_mask(base_mask, c.B, c.Hq, c.S, false, who);
+        if (pad_mask) m1 = upload_mask(pad_mask, c.B, c.Hq, c.S, true, who);
+        if (!m0.m.ptr) std::swap(m0, m1);
+        return run_fused(q, k, v, c, false, 0, {}, std::move(m0), std::move(m1));
+    }
     const bool causal = bm.kind == MaskKind::kCausal || bm.kind == MaskKind::kSliding;
     return run_fused(q, k, v, c, causal, bm.kind == MaskKind::kSliding ? bm.window : 0, pm.len);
 }

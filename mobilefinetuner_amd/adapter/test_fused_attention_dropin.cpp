@@ -177,6 +177,73 @@ Result run_masked_case(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
             max_rel(vf->grad(), vr->grad())};
 }
 
+// Any additive masks (the kernels' mask mode): the composite adds base, then
+// pad (core/memory_efficient_attention.cpp:29-38 with ops::add's broadcast)
+// against memory_efficient_attention(q, k, v, base) (pad null) or
+// memory_efficient_attention_masked(q, k, v, base, pad).
+Result run_any_mask_case(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, const TensorPtr& base,
+                         const TensorPtr& pad, bool bf16, uint64_t seed) {
+    const int r = int(Hq / Hkv);
+    auto q0 = make({B, Hq, S, D}, seed, 1.0f, bf16, false);
+    auto k0 = make({B, Hkv, S, D}, seed + 1, 1.0f, bf16, false);
+    auto v0 = make({B, Hkv, S, D}, seed + 2, 1.0f, bf16, false);
+    auto g = make({B, Hq, S, D}, seed + 3, 0.1f, bf16, false);
+    const float scale = 1.0f / std::sqrt(float(D));
+    auto qr = copy_of(q0, true), kr = copy_of(k0, true), vr = copy_of(v0, true);
+    auto kk = r > 1 ? repeat_kv_heads(kr, r) : kr;
+    auto vv = r > 1 ? repeat_kv_heads(vr, r) : vr;
+    auto scores = mul(matmul(qr, transpose(kk, 2, 3)), scale);
+    if (base) scores = add(scores, base);
+    if (pad) scores = add(scores, pad);
+    auto out_ref = matmul(softmax(scores, -1), vv);
+    autograd::Engine::instance().run_backward({out_ref}, {g});
+
+    auto qf = bf16 ? to_bf16(q0, true) : copy_of(q0, true);
+    auto kf = bf16 ? to_bf16(k0, true) : copy_of(k0, true);
+    auto vf = bf16 ? to_bf16(v0, true) : copy_of(v0, true);
+    MemoryEfficientAttentionConfig cfg;
+    cfg.scale = scale;
+    auto out = pad ? memory_efficient_attention_masked(qf, kf, vf, base, pad, cfg)
+                   : memory_efficient_attention(qf, kf, vf, base, cfg);
+    autograd::Engine::instance().run_backward({out}, {g});
+    if (!qf->grad() || !kf->grad() || !vf->grad()) throw std::runtime_error("missing fused grads");
+    return {max_rel(out, out_ref), max_rel(qf->grad(), qr->grad()), max_rel(kf->grad(), kr->grad()),
+            max_rel(vf->grad(), vr->grad())};
+}
+
+// No grad with an [S,S] mask: the operator's rule (.cpp:160-172), -1e10
+// above the diagonal when use_causal_mask, then + mask, against the same
+// scores through the composite's ops (the operator's double row sum differs
+// from the composite's float sum by rounding only).
+float run_nograd_mask_case(int64_t B, int64_t H, int64_t S, int64_t D, const TensorPtr& mask, bool causal,
+                           uint64_t seed) {
+    auto q = make({B, H, S, D}, seed, 1.0f, false, false);
+    auto k = make({B, H, S, D}, seed + 1, 1.0f, false, false);
+    auto v = make({B, H, S, D}, seed + 2, 1.0f, false, false);
+    const float scale = 1.0f / std::sqrt(float(D));
+    auto scores = mul(matmul(q, transpose(k, 2, 3)), scale);
+    if (causal) {
+        float* p = scores->data<float>();
+        for (int64_t bh = 0; bh < B * H; ++bh)
+            for (int64_t i = 0; i < S; ++i)
+                for (int64_t j = i + 1; j < S; ++j) p[(bh * S + i) * S + j] = -1e10f;
+    }
+    auto ref = matmul(softmax(add(scores, mask), -1), v);
+    MemoryEfficientAttentionConfig cfg;
+    cfg.use_causal_mask = causal;
+    cfg.scale = scale;
+    auto out = memory_efficient_attention(q, k, v, mask, cfg);
+    return max_rel(out, ref);
+}
+
+TensorPtr random_mask(const std::vector<int64_t>& shape, uint64_t seed, float hole_every) {
+    auto m = make(shape, seed, 1.0f, false, false);
+    float* p = m->data<float>();
+    for (int64_t i = 0; i < m->numel(); ++i)
+        if (std::fmod(float(i) * 0.618034f, 1.0f) < hole_every) p[i] = -1e10f;
+    return m;
+}
+
 bool expect_throw(const char* what, const std::function<void()>& fn) {
     try {
         fn();
@@ -243,6 +310,44 @@ int main() {
                   << " dv=" << r.dv << (pass ? "  ok" : "  FAIL") << std::endl;
         ok = ok && pass;
     }
+    // Any other additive mask (the kernels' mask mode): an arbitrary [S,S]
+    // mask with -1e10 holes and a row masked everywhere, a 4-D [B,1,S,S]
+    // mask, left padding, and a window with padding of another value.
+    {
+        struct AnyCase {
+            const char* what;
+            int64_t B, Hq, Hkv, S, D;
+            TensorPtr base, pad;
+            bool bf16;
+        };
+        auto ss = random_mask({40, 40}, 91, 0.3f);
+        for (int64_t j = 0; j < 40; ++j) ss->data<float>()[7 * 40 + j] = -1e10f;
+        auto left = pad_mask(2, 36, {36, 36}, 0.f);
+        for (int64_t j = 0; j < 5; ++j) left->data<float>()[36 + j] = -1e10f;  // batch 1: the first keys masked
+        const AnyCase any[] = {
+            {"[S,S] mask", 2, 4, 2, 40, 64, ss, nullptr, false},
+            {"[S,S] mask bf16", 1, 4, 1, 40, 256, ss, nullptr, true},
+            {"[B,1,S,S] mask", 2, 2, 1, 33, 32, random_mask({2, 1, 33, 33}, 92, 0.2f), nullptr, false},
+            {"left padding", 2, 4, 2, 36, 64, create_causal_mask(36, kFloat32, kCPU), left, false},
+            {"window + padding of another value", 1, 2, 2, 24, 32, sliding_mask(24, 3), pad_mask(1, 24, {17}, -1e9f),
+             false},
+        };
+        for (const AnyCase& c : any) {
+            const Result r = run_any_mask_case(c.B, c.Hq, c.Hkv, c.S, c.D, c.base, c.pad, c.bf16, seed += 17);
+            const float tol = c.bf16 ? 2e-2f : 1e-4f;
+            const bool pass = r.o <= tol && r.dq <= tol && r.dk <= tol && r.dv <= tol;
+            std::cout << "[dropin] mask mode, " << c.what << "  max-rel o=" << r.o << " dq=" << r.dq
+                      << " dk=" << r.dk << " dv=" << r.dv << (pass ? "  ok" : "  FAIL") << std::endl;
+            ok = ok && pass;
+        }
+        for (bool causal : {false, true}) {
+            const float e = run_nograd_mask_case(2, 3, 40, 32, ss, causal, seed += 17);
+            std::cout << "[dropin] mask mode, no grad" << (causal ? " causal" : "") << "  max-rel o=" << e
+                      << (e <= 1e-5f ? "  ok" : "  FAIL") << std::endl;
+            ok = ok && e <= 1e-5f;
+        }
+        autograd::Engine::instance().clear_graph();
+    }
     // No-grad path equals the grad path's output (same kernels, no LSE kept).
     {
         auto q = make({1, 2, 20, 16}, 7, 1.0f, false, false);
@@ -259,16 +364,12 @@ int main() {
     // Errors keep the reference's exception convention.
     auto q = make({1, 2, 8, 16}, 1, 1.0f, false, false);
     auto k3 = make({1, 3, 8, 16}, 2, 1.0f, false, false);
-    auto mask = make({8, 8}, 3, 1.0f, false, false);
+    auto mask4 = make({1, 1, 8, 8}, 3, 1.0f, false, false);
     ok = expect_throw("q 2 heads, k 3 heads", [&] { memory_efficient_attention(q, k3, k3, nullptr, {}); }) && ok;
-    ok = expect_throw("non-causal additive mask", [&] { memory_efficient_attention(q, q, q, mask, {}); }) && ok;
-    ok = expect_throw("left padding", [&] {
-        auto pm = pad_mask(1, 8, {8}, -1e9f);
-        pm->data<float>()[0] = -1e9f;
-        memory_efficient_attention_masked(q, q, q, create_causal_mask(8, kFloat32, kCPU), pm, {});
-    }) && ok;
-    ok = expect_throw("window with padding of another value", [&] {
-        memory_efficient_attention_masked(q, q, q, sliding_mask(8, 3), pad_mask(1, 8, {5}, -1e9f), {});
+    // the reference's no-grad operator takes only [S,S] masks (.cpp:114-120)
+    ok = expect_throw("4-D mask without grad", [&] { memory_efficient_attention(q, q, q, mask4, {}); }) && ok;
+    ok = expect_throw("mask of another length", [&] {
+        memory_efficient_attention(q, q, q, make({9, 9}, 4, 1.0f, false, false), {});
     }) && ok;
     ok = expect_throw("3-D input", [&] {
         auto t = zeros({2, 8, 16}, kFloat32, kCPU);
