@@ -19,7 +19,10 @@ Also on the line:
                 drop-in autograd node's device bytes (its allocator) and host
                 bytes (MemoryManager);
   dropin_step   forward + backward through the finetune_ops drop-in with host
-                tensors in and out (PCIe copies included) at C1, C2 and C5;
+                tensors in and out (PCIe copies included) at C1, C2 and C5
+                (C5 also with an [S,S] causal mask tensor, as GPT-2 passes
+                one), beside its transfer floor: the step's host<->device
+                bytes over the box's measured pinned-copy rates;
   variants      Gemma's sliding window (c5w512), right-padded batches (c4pad)
                 and the [B,S,H,D] operand layout (c5bshd); their flops count
                 the visible (query, key) pairs only;
@@ -609,10 +612,10 @@ def main():
     # The PCIe-inclusive step through the drop-in (host tensors in, host
     # gradients out, reference Engine), steady state with cached device memory.
     pcie = {}
-    for cid in ("c1", "c2", args.config):
-        d = dropin_probe("step", cid, 2, 5)
+    for cid, mask, iters in (("c1", "", 40), ("c2", "", 20), (args.config, "", 20), (args.config, "mask", 20)):
+        d = dropin_probe("step", cid, 5, iters, *([mask] if mask else []))
         if d is not None:
-            pcie[cid] = d
+            pcie[cid + ("_mask" if mask else "")] = d
     if pcie:
         out["dropin_step"] = pcie
     variants = {}

@@ -220,6 +220,16 @@ mft_status mft_repeat_kv_bwd(const float* g, float* dkv, int64_t B, int64_t Hkv,
 /* Message of the last failing call on this thread ("" if none). */
 const char* mft_last_error(void);
 
+/* Element conversion on the device: MFT_BF16 -> MFT_F32 (exact) or MFT_F32 ->
+ * MFT_BF16 with the reference's round-to-nearest-even
+ * (float32_to_bf16_bits, core/dtype.h:114-121).  n elements; src and dst
+ * 16-byte aligned device memory.  No counterpart in the reference, which
+ * converts on the host (ops::cast, core/ops.cpp:2894-2952, and the adapters'
+ * tensor reads): it lets the drop-in widen the bf16 output and round the fp32
+ * incoming gradient on the GPU instead of in host loops. */
+mft_status mft_convert(const void* src, mft_dtype src_dtype, void* dst, mft_dtype dst_dtype,
+                       int64_t n, hipStream_t stream);
+
 /* Library version, for the bindings' sanity check. */
 int mft_version(void);
 

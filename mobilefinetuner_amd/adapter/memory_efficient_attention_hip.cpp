@@ -46,6 +46,7 @@
 #include <cmath>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -71,31 +72,15 @@ using dropin::download_f32;
 
 size_t elt_size(DType t) { return t == kBFloat16 ? 2 : 4; }
 
-std::unique_ptr<DeviceBuffer> upload(const TensorPtr& t) {
-    const size_t n = static_cast<size_t>(t->numel()) * elt_size(t->dtype());
-    auto buf = std::make_unique<DeviceBuffer>(n);
-    hip_check(hipMemcpyAsync(buf->get(), t->data_ptr(), n, hipMemcpyHostToDevice, adapter_stream()),
-              "copy to device");
-    return buf;
-}
-
-// Device O (input dtype) -> a new fp32 host tensor.
+// Device O (input dtype) -> a new fp32 host tensor; bf16 is widened on the
+// device (exact), so the host only copies.
 TensorPtr download_as_f32(const DeviceBuffer& src, const std::vector<int64_t>& shape, DType dtype) {
-    auto out = zeros(shape, kFloat32, kCPU);
-    const size_t n = static_cast<size_t>(out->numel());
-    if (dtype == kFloat32) {
-        hip_check(hipMemcpyAsync(out->data<float>(), src.get(), n * 4, hipMemcpyDeviceToHost, adapter_stream()),
-                  "copy to host");
-        hip_check(hipStreamSynchronize(adapter_stream()), "synchronize");
-    } else {
-        std::vector<uint16_t> bits(n);
-        hip_check(hipMemcpyAsync(bits.data(), src.get(), n * 2, hipMemcpyDeviceToHost, adapter_stream()),
-                  "copy to host");
-        hip_check(hipStreamSynchronize(adapter_stream()), "synchronize");
-        float* o = out->data<float>();
-        for (size_t i = 0; i < n; ++i) o[i] = bf16_bits_to_float32(bits[i]);
-    }
-    return out;
+    int64_t n = 1;
+    for (int64_t x : shape) n *= x;
+    if (dtype == kFloat32) return download_f32(src, shape);
+    DeviceBuffer wide(static_cast<size_t>(n) * 4);
+    mft_check(mft_convert(src.get(), MFT_BF16, wide.get(), MFT_F32, n, adapter_stream()));
+    return download_f32(wide, shape);
 }
 
 enum class MaskKind { kNone, kZero, kCausal, kSliding, kOther };
@@ -109,9 +94,8 @@ struct BaseMask {
     float lo = 0.f, hi = 0.f;                // range of the masked entries' values
 };
 
-BaseMask classify_mask(const TensorPtr& mask, int64_t S) {
+BaseMask scan_mask(const TensorPtr& mask, int64_t S) {
     BaseMask r;
-    if (!mask) return r;
     r.kind = MaskKind::kOther;
     if (mask->shape().size() != 2 || mask->shape()[0] != S || mask->shape()[1] != S) return r;
     if (mask->dtype() != kFloat32) return r;
@@ -143,6 +127,81 @@ BaseMask classify_mask(const TensorPtr& mask, int64_t S) {
         r.window = w;
     }
     return r;
+}
+
+// Whether entry (i, j) of an [S,S] mask agrees with the answer r.
+bool agrees(const BaseMask& r, const float* m, int64_t S, int64_t i, int64_t j) {
+    const float x = m[i * S + j];
+    bool masked = false;
+    if (r.kind == MaskKind::kCausal) masked = j > i;
+    if (r.kind == MaskKind::kSliding) masked = j > i || i - j >= r.window;
+    return masked ? (x <= -1e9f && x >= r.lo && x <= r.hi) : x == 0.0f;
+}
+
+// classify_mask's answers for the masks seen last.  A model builds its [S,S]
+// causal mask once per forward and passes that tensor to every layer
+// (graph/gpt2_model.cpp:388, 623), so the full scan runs once per forward.
+// An answer is reused while the same tensor object is alive with the same
+// data pointer and shape, and a sample of its entries agrees with it: the
+// whole last row, and in 256 rows spread over the mask the diagonal, the
+// entry right of it, the window edge and one entry at a column that moves
+// from row to row (a few thousand reads where the full scan makes S*S).  A
+// mask edited in place only outside that sample keeps its old answer.
+class MaskCache {
+public:
+    BaseMask classify(const TensorPtr& mask, int64_t S) {
+        if (mask->shape().size() != 2 || mask->shape()[0] != S || mask->shape()[1] != S ||
+            mask->dtype() != kFloat32)
+            return scan_mask(mask, S);  // kOther: the mask mode reads the values themselves
+        std::lock_guard<std::mutex> lock(mu_);
+        const void* data = mask->data_ptr();
+        for (auto& e : entries_) {
+            if (e.owner.lock() != mask || e.data != data || e.S != S) continue;
+            if (e.answer.kind == MaskKind::kOther || sample_agrees(e.answer, mask->data<float>(), S)) {
+                ++hits_;
+                return e.answer;
+            }
+        }
+        BaseMask r = scan_mask(mask, S);
+        entries_[next_] = Entry{mask, data, S, r};
+        next_ = (next_ + 1) % kEntries;
+        return r;
+    }
+    uint64_t hits() const { return hits_; }
+    static MaskCache& instance() {
+        static MaskCache* c = new MaskCache();
+        return *c;
+    }
+
+private:
+    static bool sample_agrees(const BaseMask& r, const float* m, int64_t S) {
+        for (int64_t j = 0; j < S; ++j)
+            if (!agrees(r, m, S, S - 1, j)) return false;
+        const int64_t step = std::max<int64_t>(1, S / 256);
+        for (int64_t i = (S - 1) % step; i < S; i += step) {
+            const int64_t cols[4] = {i, std::min(i + 1, S - 1), std::max<int64_t>(i - r.window, 0),
+                                     (i * 7919 + 13) % S};
+            for (int64_t j : cols)
+                if (!agrees(r, m, S, i, j)) return false;
+        }
+        return true;
+    }
+    struct Entry {
+        std::weak_ptr<Tensor> owner;
+        const void* data = nullptr;
+        int64_t S = 0;
+        BaseMask answer;
+    };
+    static constexpr int kEntries = 4;
+    std::mutex mu_;
+    Entry entries_[kEntries];
+    int next_ = 0;
+    uint64_t hits_ = 0;
+};
+
+BaseMask classify_mask(const TensorPtr& mask, int64_t S) {
+    if (!mask) return BaseMask{};
+    return MaskCache::instance().classify(mask, S);
 }
 
 // An additive padding mask [B,1,1,S] (graph/gemma_model.cpp:287-320,
@@ -209,9 +268,7 @@ DeviceMask upload_mask(const TensorPtr& mask, int64_t B, int64_t Hq, int64_t S, 
             throw std::runtime_error(std::string(who) + ": mask shape does not broadcast to [B, Hq, S, S]");
     DeviceMask d;
     const size_t n = static_cast<size_t>(mask->numel());
-    d.buf = std::make_unique<DeviceBuffer>(n * 4);
-    hip_check(hipMemcpyAsync(d.buf->get(), mask->data<float>(), n * 4, hipMemcpyHostToDevice, adapter_stream()),
-              "copy mask");
+    d.buf = dropin::upload_bytes(mask->data<float>(), n * 4);
     int64_t st[4];
     st[3] = 1;
     for (int i = 2; i >= 0; --i) st[i] = st[i + 1] * dims[i + 1];
@@ -246,31 +303,23 @@ public:
         const size_t n_kv = static_cast<size_t>(d.B * d.Hkv * d.S * d.D);
         hipStream_t st = adapter_stream();
 
-        DeviceBuffer dO(n_q * (d.dtype == MFT_BF16 ? 2 : 4));
-        std::vector<uint16_t> bits;
+        auto dO = dropin::upload_bytes(grad_output->data<float>(), n_q * 4);
         if (d.dtype == MFT_BF16) {
             // dO enters the bf16 kernels rounded like every other bf16 operand
-            // (core/dtype.h:114-121).
-            bits.resize(n_q);
-            const float* g = grad_output->data<float>();
-            for (size_t i = 0; i < n_q; ++i) bits[i] = float32_to_bf16_bits(g[i]);
-            hip_check(hipMemcpyAsync(dO.get(), bits.data(), n_q * 2, hipMemcpyHostToDevice, st), "copy dO");
-        } else {
-            hip_check(hipMemcpyAsync(dO.get(), grad_output->data<float>(), n_q * 4, hipMemcpyHostToDevice, st),
-                      "copy dO");
+            // (core/dtype.h:114-121), on the device.
+            auto bits = std::make_unique<DeviceBuffer>(n_q * 2);
+            mft_check(mft_convert(dO->get(), MFT_F32, bits->get(), MFT_BF16, static_cast<int64_t>(n_q), st));
+            dO = std::move(bits);
         }
         size_t fwd_ws = 0, bwd_ws = 0;
         mft_check(mft_attn_workspace_size(&d, &fwd_ws, &bwd_ws));
         DeviceBuffer ws(bwd_ws), dq(n_q * 4), dk(n_kv * 4), dv(n_kv * 4);
-        mft_check(mft_attn_bwd(&d, s_->q->get(), s_->k->get(), s_->v->get(), s_->o->get(), dO.get(),
+        mft_check(mft_attn_bwd(&d, s_->q->get(), s_->k->get(), s_->v->get(), s_->o->get(), dO->get(),
                                static_cast<const float*>(s_->lse->get()), static_cast<float*>(dq.get()),
                                static_cast<float*>(dk.get()), static_cast<float*>(dv.get()), ws.get(), st));
-        auto gq = download_f32(dq, s_->q_shape);
-        auto gk = download_f32(dk, s_->kv_shape);
-        auto gv = download_f32(dv, s_->kv_shape);
-        hip_check(hipStreamSynchronize(st), "synchronize");
+        auto g = dropin::download_f32_all({{&dq, &s_->q_shape}, {&dk, &s_->kv_shape}, {&dv, &s_->kv_shape}});
         s_.reset();  // the graph is single-use (Engine::clear_graph, core/autograd_engine.cpp:275-287)
-        return {gq, gk, gv};
+        return g;
     }
 
 private:
@@ -347,10 +396,7 @@ TensorPtr run_fused(const TensorPtr& q, const TensorPtr& k, const TensorPtr& v, 
 
     auto saved = std::make_shared<SavedForBackward>();
     if (!lengths.empty()) {
-        saved->kv_len = std::make_unique<DeviceBuffer>(lengths.size() * sizeof(int32_t));
-        hip_check(hipMemcpyAsync(saved->kv_len->get(), lengths.data(), lengths.size() * sizeof(int32_t),
-                                 hipMemcpyHostToDevice, adapter_stream()),
-                  "copy kv_len");
+        saved->kv_len = dropin::upload_bytes(lengths.data(), lengths.size() * sizeof(int32_t));
         d.kv_len = static_cast<const int32_t*>(saved->kv_len->get());
     }
     d.mask0 = mask0.m;
@@ -361,9 +407,12 @@ TensorPtr run_fused(const TensorPtr& q, const TensorPtr& k, const TensorPtr& v, 
     saved->desc = d;
     saved->q_shape = qs;
     saved->kv_shape = ks;
-    saved->q = upload(q);
-    saved->k = upload(k);
-    saved->v = upload(v);
+    saved->q = std::make_unique<DeviceBuffer>(static_cast<size_t>(q->numel()) * elt_size(dt));
+    saved->k = std::make_unique<DeviceBuffer>(static_cast<size_t>(k->numel()) * elt_size(dt));
+    saved->v = std::make_unique<DeviceBuffer>(static_cast<size_t>(v->numel()) * elt_size(dt));
+    dropin::Stager::instance().upload({{saved->q->get(), q->data_ptr(), saved->q->bytes()},
+                                       {saved->k->get(), k->data_ptr(), saved->k->bytes()},
+                                       {saved->v->get(), v->data_ptr(), saved->v->bytes()}});
     saved->o = std::make_unique<DeviceBuffer>(static_cast<size_t>(q->numel()) * elt_size(dt));
     // (mask mode: two floats per row, the row max and ln of the sum)
     if (needs_grad) saved->lse = std::make_unique<DeviceBuffer>(static_cast<size_t>(B * Hq * S) * (mask_mode ? 8 : 4));
@@ -440,3 +489,7 @@ extern "C" void mft_dropin_pool_stats(size_t* live_bytes, size_t* cached_bytes, 
     if (cached_bytes) *cached_bytes = p.cached_bytes();
     if (device_mallocs) *device_mallocs = p.device_mallocs();
 }
+
+// Bytes of pinned host memory the adapters hold for result tensors
+// (dropin_device.h, PinnedPool): blocks in use and blocks kept for reuse.
+extern "C" size_t mft_dropin_pinned_bytes() { return ops::dropin::PinnedPool::instance().held_bytes(); }

@@ -340,6 +340,26 @@ int main() {
                       << " dk=" << r.dk << " dv=" << r.dv << (pass ? "  ok" : "  FAIL") << std::endl;
             ok = ok && pass;
         }
+        // One mask tensor passed again and again (a model passes its mask to
+        // every layer), edited in place between calls: causal, then a sliding
+        // window, then arbitrary values.  Each call must see the current values.
+        {
+            const int64_t S = 48;
+            auto m = create_causal_mask(int(S), kFloat32, kCPU);
+            float* p = m->data<float>();
+            for (int step = 0; step < 4; ++step) {
+                if (step == 2)
+                    for (int64_t i = 0; i < S; ++i)
+                        for (int64_t j = 0; j <= i; ++j) p[i * S + j] = (i - j < 5) ? 0.f : -1e10f;
+                if (step == 3)
+                    for (int64_t i = 0; i < S * S; ++i) p[i] = std::fmod(float(i) * 0.618034f, 1.0f) - 0.5f;
+                const Result r = run_any_mask_case(1, 2, 1, S, 32, m, nullptr, false, seed += 17);
+                const bool pass = r.o <= 1e-4f && r.dq <= 1e-4f && r.dk <= 1e-4f && r.dv <= 1e-4f;
+                std::cout << "[dropin] reused mask tensor, call " << step << "  max-rel o=" << r.o << " dq=" << r.dq
+                          << " dk=" << r.dk << " dv=" << r.dv << (pass ? "  ok" : "  FAIL") << std::endl;
+                ok = ok && pass;
+            }
+        }
         for (bool causal : {false, true}) {
             const float e = run_nograd_mask_case(2, 3, 40, 32, ss, causal, seed += 17);
             std::cout << "[dropin] mask mode, no grad" << (causal ? " causal" : "") << "  max-rel o=" << e

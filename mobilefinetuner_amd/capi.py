@@ -24,7 +24,7 @@ MFT_NORM_NONE, MFT_NORM_GEMMA, MFT_NORM_AFFINE = 0, 1, 2
 # Every symbol the headers declare (checked by tests/test_capi.py).
 EXPORTS = (
     "mft_attn_workspace_size", "mft_attn_fwd", "mft_attn_bwd", "mft_attn_bwd_stage", "mft_attn_bwd_noalloc",
-    "mft_repeat_kv_fwd", "mft_repeat_kv_bwd", "mft_last_error", "mft_version",
+    "mft_repeat_kv_fwd", "mft_repeat_kv_bwd", "mft_convert", "mft_last_error", "mft_version",
     "mft_prologue_fwd", "mft_prologue_workspace_size", "mft_prologue_bwd",
     "mft_lm_ce_workspace_size", "mft_lm_ce_fwd", "mft_lm_ce_bwd", "mft_lm_ce_streaming_fwd",
     "mft_lm_ce_streaming_bwd",
@@ -113,6 +113,8 @@ def lib():
     L.mft_repeat_kv_fwd.argtypes = [vp, vp, i64, i64, i64, i64, i64, C.c_int32, vp]
     L.mft_repeat_kv_bwd.restype = C.c_int
     L.mft_repeat_kv_bwd.argtypes = [vp, vp, i64, i64, i64, i64, i64, vp]
+    L.mft_convert.restype = C.c_int
+    L.mft_convert.argtypes = [vp, C.c_int, vp, C.c_int, i64, vp]
     L.mft_prologue_fwd.restype = C.c_int
     L.mft_prologue_fwd.argtypes = [C.POINTER(PrologueDesc), vp, vp, vp, vp]
     L.mft_prologue_workspace_size.restype = C.c_int
@@ -281,3 +283,8 @@ def lora_bwd(d, x, W, dy, u, dx, workspace, stream) -> None:
 
 def lora_merge(d, W, sign, stream) -> None:
     check(lib().mft_lora_merge(C.byref(d), W, float(sign), stream))
+
+
+def convert(src, src_dtype, dst, dst_dtype, n, stream) -> None:
+    """mft_convert: bf16 -> fp32 (exact) or fp32 -> bf16 (the reference's RNE) on the device."""
+    check(lib().mft_convert(src, int(src_dtype), dst, int(dst_dtype), int(n), stream))
