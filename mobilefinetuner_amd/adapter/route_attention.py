@@ -1,6 +1,7 @@
 #!/usr/bin/env python3
 """Generate the drop-in build's Gemma and Qwen model graphs with their
-attention composite routed through ops::memory_efficient_attention_masked.
+attention composite routed through ops::memory_efficient_attention_masked,
+and its GPT-2 graph with a flag for an autograd-preserving Q/K/V split.
 
     python route_attention.py <REF_DIR>/finetune_ops/graph <OUT_DIR>
 
@@ -20,6 +21,12 @@ per head are the same) and lets the fused op index each query head's kv
 head.  The debug dumps of scores/probs inside Gemma's block go with it: the
 fused op never materialises them (as the GPT-2 graph's own
 memory-efficient branch, graph/gpt2_model.cpp:616-625).
+
+GPT-2 already calls memory_efficient_attention; its Q/K/V split by memcpy
+(graph/gpt2_model.cpp:559-581) drops the autograd edge to c_attn.  The
+routed copy keeps that split and adds, behind ops::gpt2_qkv_grad()
+(gpt2_qkv_split.h, off by default), the split by the reference's own
+Tensor::slice, which keeps it.
 """
 from __future__ import annotations
 
@@ -73,12 +80,43 @@ def route_qwen(src):
     return "".join(_add_include(lines[:a] + body + lines[b + 1:], "qwen_model.cpp"))
 
 
+def route_gpt2(src):
+    lines = src.splitlines(keepends=True)
+    a, b = _span(lines, "const float* qkv_data = qkv->data<float>();", "std::memcpy(v_ptr, qkv_ptr + 2 * C",
+                 "gpt2_model.cpp")
+    # the split ends with the two loops' closing braces
+    if [l.strip() for l in lines[b + 1:b + 3]] != ["}", "}"]:
+        raise SystemExit("route_attention: unexpected end of the Q/K/V split in gpt2_model.cpp")
+    b += 2
+    decl = [l for l in lines[a:b + 1] if "= zeros({B, S, C}, kFloat32, kCPU);" in l]
+    if len(decl) != 3:
+        raise SystemExit("route_attention: expected the q, k, v allocations in gpt2_model.cpp's split")
+    indent = lines[a][:len(lines[a]) - len(lines[a].lstrip())]
+    inner = [("    " + l if l.strip() else l).replace("auto q = zeros", "q = zeros").replace(
+        "auto k = zeros", "k = zeros").replace("auto v = zeros", "v = zeros") for l in lines[a:b + 1]]
+    body = [
+        f"{indent}// drop-in build: with ops::gpt2_qkv_grad() the split keeps the autograd edge to c_attn\n",
+        f"{indent}TensorPtr q, k, v;\n",
+        f"{indent}if (gpt2_qkv_grad()) {{\n",
+        f"{indent}    q = qkv->slice(2, 0, C);\n",
+        f"{indent}    k = qkv->slice(2, C, 2 * C);\n",
+        f"{indent}    v = qkv->slice(2, 2 * C, 3 * C);\n",
+        f"{indent}}} else {{\n",
+    ] + inner + [f"{indent}}}\n"]
+    out = lines[:a] + body + lines[b + 1:]
+    for i, l in enumerate(out):
+        if l.startswith('#include "../core/ops.h"'):
+            return "".join(out[:i + 1] + ['#include "gpt2_qkv_split.h"  // drop-in build: the Q/K/V split flag\n']
+                           + out[i + 1:])
+    raise SystemExit("route_attention: no ops.h include in gpt2_model.cpp")
+
+
 def main():
     if len(sys.argv) != 3:
         raise SystemExit(__doc__)
     graph, out = sys.argv[1], sys.argv[2]
     os.makedirs(out, exist_ok=True)
-    for name, fn in (("gemma_model.cpp", route_gemma), ("qwen_model.cpp", route_qwen)):
+    for name, fn in (("gemma_model.cpp", route_gemma), ("qwen_model.cpp", route_qwen), ("gpt2_model.cpp", route_gpt2)):
         with open(os.path.join(graph, name)) as fh:
             text = fn(fh.read())
         with open(os.path.join(out, name), "w") as fh:

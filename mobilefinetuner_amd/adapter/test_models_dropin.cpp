@@ -8,7 +8,10 @@
 //                       by route_attention.py; GPT-2 with
 //                       use_memory_efficient_attention);
 //   test_models_ref     against the reference's own CPU operators and the
-//                       unmodified model sources.
+//                       unmodified Gemma and Qwen sources.
+// Both take GPT-2 from route_attention.py's copy, whose Q/K/V split flag
+// (gpt2_qkv_split.h) is off except in the gpt2_mha_d4_qkv_grad case; with
+// it off the copy computes what the unmodified source does.
 // tests/test_models_dropin.py runs both and compares the lines.
 //
 // Models and fills are the reference's synthetic-smoke ones
@@ -27,6 +30,7 @@
 #include "../graph/gpt2_model.h"
 #include "../graph/qwen_model.h"
 #include "autograd_engine.h"
+#include "gpt2_qkv_split.h"
 #include "lm_loss.h"
 #include "smoke_utils.h"
 
@@ -72,9 +76,12 @@ void run_case(const char* name, const std::vector<TensorPtr>& params, int vocab,
 
 int main() {
     try {
-        {
+        for (bool qkv_grad : {false, true}) {
             // optim/test_gpt2_lora_two_step_smoke.cpp's model (no padding:
-            // GPT2Model takes the memory-efficient branch only without one)
+            // GPT2Model takes the memory-efficient branch only without one).
+            // With the split flag the attention's gradient reaches c_attn
+            // and runs the fused backward.
+            set_gpt2_qkv_grad(qkv_grad);
             GPT2Config cfg;
             cfg.vocab_size = 64;
             cfg.n_positions = 16;
@@ -86,8 +93,9 @@ int main() {
             std::mt19937 rng(7);
             smoke::initialize_tiny_gpt2(model, rng);
             model.tie_weights();
-            run_case("gpt2_mha_d4", model.parameters(), cfg.vocab_size, 2, 12,
+            run_case(qkv_grad ? "gpt2_mha_d4_qkv_grad" : "gpt2_mha_d4", model.parameters(), cfg.vocab_size, 2, 12,
                      [&](const TensorPtr& ids) { return model.forward(ids); });
+            set_gpt2_qkv_grad(false);
         }
         for (int variant = 0; variant < 3; ++variant) {
             // Gemma synthetic smoke (examples/gemma_3_270m_lora_finetune):

@@ -16,7 +16,12 @@ Makefile from the reference sources in the build container).
 
 GPT-2's graph copies Q, K and V out of the fused projection into fresh
 tensors (graph/gpt2_model.cpp:560-581), so its attention runs the no-grad
-path; the Gemma and Qwen cases run the fused backward.
+path and c_attn gets no gradient from it.  Both builds take GPT-2 from
+route_attention.py's copy, which adds a flag (gpt2_qkv_split.h) to split with
+the reference's autograd-preserving Tensor::slice instead: the
+gpt2_mha_d4_qkv_grad case sets it, so GPT-2's attention runs the fused
+backward there, and its c_attn gradients (zero without the flag) match the
+CPU build's.  The Gemma and Qwen cases run the fused backward.
 """
 import json
 import os
@@ -49,7 +54,7 @@ def _cases(out):
 def test_model_graphs_match_reference_cpu(dev):
     ref = _cases(_run("test_models_ref"))
     got = _cases(_run("test_models_dropin"))
-    assert set(got) == set(ref) and len(ref) == 6
+    assert set(got) == set(ref) and len(ref) == 7
     for name, r in ref.items():
         g = got[name]
         assert abs(g["loss"] - r["loss"]) <= TOL * abs(r["loss"]), (name, g["loss"], r["loss"])
@@ -59,6 +64,18 @@ def test_model_graphs_match_reference_cpu(dev):
         worst = max(abs(a - b) for a, b in zip(g["grad_l2"], r["grad_l2"])) / scale
         print(f"[models] {name}: loss {g['loss']:.7f} vs {r['loss']:.7f}, grad-norm max rel {worst:.2e}", flush=True)
         assert worst <= TOL, (name, worst)
+
+
+def test_gpt2_qkv_flag_carries_attention_gradient_to_c_attn(dev):
+    got = _cases(_run("test_models_dropin"))
+    off, on = got["gpt2_mha_d4"]["grad_l2"], got["gpt2_mha_d4_qkv_grad"]["grad_l2"]
+    assert got["gpt2_mha_d4"]["loss"] == got["gpt2_mha_d4_qkv_grad"]["loss"] or \
+        abs(got["gpt2_mha_d4"]["loss"] - got["gpt2_mha_d4_qkv_grad"]["loss"]) <= 1e-6
+    # parameters with no gradient without the flag (c_attn's) get one with it
+    gained = [i for i, (a, b) in enumerate(zip(off, on)) if a == 0.0 and b > 0.0]
+    assert gained, (off, on)
+    # and no parameter loses its gradient
+    assert all(b > 0.0 for a, b in zip(off, on) if a > 0.0)
 
 
 def _smoke_numbers(out):
