@@ -411,10 +411,11 @@ FwdPlan plan_fwd_split(const AttnShape& s) {
     const int S = (int)s.S, causal = s.causal ? 1 : 0, W = s.window;
     const int64_t pairs = s.B * s.Hq;
     const int64_t u = balanced_units(pairs, fwd_unit_slots(s));
-    // Units of about equal cost, no shorter than kMinUnitIters key tiles (a
-    // split costs one fp32 partial tile), no query tile over kCombMaxSlots.
+    // Units of about equal cost, no shorter than kMinFwdUnitIters key tiles
+    // (a split costs one fp32 partial tile), no query tile over kCombMaxSlots.
     const FastTiles g{S, causal, W, (int)(s.Hq / s.Hkv), 0};
-    p.us = fit_unit_split(g, u, kFwdIterCost, fwd_tile_cost(s), kMinUnitIters, kCombMaxSlots, &p.parts_max);
+    p.us = fit_unit_split(g, u, kFwdIterCost, fwd_tile_cost(s), kMinFwdUnitIters, kCombMaxSlots,
+                          &p.parts_max);
     p.any_split = p.parts_max > 1;
     return p;
 }

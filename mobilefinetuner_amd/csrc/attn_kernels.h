@@ -117,8 +117,12 @@ inline int q_tile_cost(int64_t D) { return D >= 256 ? 13 : 0; }
 inline int fwd_tile_cost(const AttnShape& s) { return s.bf16 ? fwd_tile_cost(s.D) : 0; }
 inline int kv_tile_cost(const AttnShape& s) { return s.bf16 ? kv_tile_cost(s.D) : 0; }
 inline int q_tile_cost(const AttnShape& s) { return s.bf16 ? q_tile_cost(s.D) : 0; }
-// The fewest iterations the planners give a unit.
-constexpr int kMinUnitIters = 4;
+// The fewest iterations the planners give a unit: backward units 4, forward
+// units 2.  A forward unit's fixed costs (its Q rows, a partial tile) are
+// smaller; at C4 (B 4, Hq 4, S 1024, D 256) 2 gives 16 units per (batch,
+// head) instead of 11 and a 1.5 us shorter forward, and no other config
+// moved (1, 2 and 4 measured for each role on C1-C5).
+constexpr int kMinUnitIters = 4, kMinFwdUnitIters = 2;
 // The plan of one backward call, computed once per call and passed to the
 // workspace layout and the launches.
 BwdPlan plan_bwd_fast(const AttnShape& s);

@@ -11,11 +11,11 @@
 
 // The unit split of one role covers its iterations exactly once, in order:
 // unit k holds [unit_first(k), unit_first(k + 1)), nonempty (at least
-// kMinUnitIters iterations when there are several units), unit_of agrees at
+// min_iters iterations when there are several units), unit_of agrees at
 // both ends, and for every split tile the slot REDUCE / combine read for
 // each unit (split_slot) is the slot the unit writes (2u for its first
 // segment, 2u + 1 for its last).
-static bool check_split(const mft::FastTiles& g, const mft::UnitSplit& u, const char* role) {
+static bool check_split(const mft::FastTiles& g, const mft::UnitSplit& u, const char* role, int min_iters) {
     const int nt = g.nt();
     auto tile_of = [&](int64_t i, int t) {  // from a tile at or before i's
         while (t + 1 < nt && g.start(t + 1) <= i) ++t;
@@ -28,7 +28,7 @@ static bool check_split(const mft::FastTiles& g, const mft::UnitSplit& u, const 
     int t = 0;
     for (int k = 0; k < u.units; ++k) {
         const int64_t f0 = mft::unit_first(g, u, k), f1 = mft::unit_first(g, u, k + 1);
-        if (f1 <= f0 || (u.units > 1 && f1 - f0 < mft::kMinUnitIters)) {
+        if (f1 <= f0 || (u.units > 1 && f1 - f0 < min_iters)) {
             std::printf("BAD %s: unit %d holds [%lld, %lld)\n", role, k, (long long)f0, (long long)f1);
             return false;
         }
@@ -95,9 +95,9 @@ int main() {
                             return 1;
                         }
                         const int G = sh[1] / sh[2], Wv = (int)s.window, Si = (int)S;
-                        if (!check_split(mft::FastTiles{Si, causal, Wv, G, 0}, f.us, "fwd") ||
-                            !check_split(mft::FastTiles{Si, causal, Wv, G, 1}, b.kv, "kv") ||
-                            !check_split(mft::FastTiles{Si, causal, Wv, G, 0}, b.q, "q")) {
+                        if (!check_split(mft::FastTiles{Si, causal, Wv, G, 0}, f.us, "fwd", mft::kMinFwdUnitIters) ||
+                            !check_split(mft::FastTiles{Si, causal, Wv, G, 1}, b.kv, "kv", mft::kMinUnitIters) ||
+                            !check_split(mft::FastTiles{Si, causal, Wv, G, 0}, b.q, "q", mft::kMinUnitIters)) {
                             std::printf("  at S=%lld B=%d Hq=%d Hkv=%d D=%d causal=%d W=%d\n", S, sh[0], sh[1],
                                         sh[2], D, causal, W);
                             return 1;
