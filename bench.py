@@ -185,7 +185,9 @@ def prologue_leg(cfg_id, steps, warmup):
     [B,S,H,D] projection outputs viewed [B,H,S,D] (Gemma-3: rms_norm with
     (1 + w), eps 1e-6, rope_theta 1e6), bf16 x/y, fp32 dy/dx.  HBM-bound:
     algorithmic bytes per element are 2 (x) + 2 (y) forward and 2 (x) + 4 (dy)
-    + 4 (dx) backward, plus the [waves, D] dw partials written and re-read."""
+    + 4 (dx) backward, plus the [waves, D] dw partials written and re-read.
+    The q and k heads run as one batch (mft_prologue_fwd_n / _bwd_n: one
+    launch forward, two backward); "separate" times one call per tensor."""
     import torch
     from mobilefinetuner_amd import attention as A
     from mobilefinetuner_amd import capi
@@ -212,14 +214,24 @@ def prologue_leg(cfg_id, steps, warmup):
         bwd_bytes += 10 * n + 2 * wsb
         calls.append((d, x, w, y, dy, dx, dw, ws))
 
-    def fwd():
+    def fwd1():
         for d, x, w, y, *_ in calls:
             capi.prologue_fwd(d, x.data_ptr(), w.data_ptr(), y.data_ptr(), sp)
 
-    def bwd():
+    def bwd1():
         for d, x, w, y, dy, dx, dw, ws in calls:
             capi.prologue_bwd(d, x.data_ptr(), w.data_ptr(), dy.data_ptr(), dx.data_ptr(), dw.data_ptr(),
                               ws.data_ptr(), sp)
+
+    ds = [cl[0] for cl in calls]
+    ptr = lambda i: [cl[i].data_ptr() for cl in calls]
+    wsn = torch.empty(max(capi.prologue_workspace_size_n(ds), 1), dtype=torch.uint8, device=dev)
+
+    def fwd():
+        capi.prologue_fwd_n(ds, ptr(1), ptr(2), ptr(3), sp)
+
+    def bwd():
+        capi.prologue_bwd_n(ds, ptr(1), ptr(2), ptr(4), ptr(5), ptr(6), wsn.data_ptr(), sp)
 
     def timed(fn, n):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -231,15 +243,18 @@ def prologue_leg(cfg_id, steps, warmup):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / n
 
-    warm_up(lambda: (fwd(), bwd()), warmup)
+    warm_up(lambda: (fwd(), bwd(), fwd1(), bwd1()), warmup)
     f_ms, b_ms = timed(fwd, steps), timed(bwd, steps)
+    f1_ms, b1_ms = timed(fwd1, steps), timed(bwd1, steps)
     return {"workload": f"q/k rms_norm(1+w) + RoPE of {cfg_id} (Hq {c['Hq']} + Hkv {c['Hkv']} heads, S {S}, D {D}), "
                         "[B,S,H,D] bf16 in, [B,H,S,D] out",
             "fwd_us": round(f_ms * 1e3, 2), "bwd_us": round(b_ms * 1e3, 2),
             "fwd_GBps": round(fwd_bytes / (f_ms * 1e-3) / 1e9, 1), "bwd_GBps": round(bwd_bytes / (b_ms * 1e-3) / 1e9, 1),
             "fwd_frac_hbm": round(fwd_bytes / (f_ms * 1e-3) / 8e12, 4),
             "bwd_frac_hbm": round(bwd_bytes / (b_ms * 1e-3) / 8e12, 4),
-            "fwd_bytes": fwd_bytes, "bwd_bytes": bwd_bytes, "launches": {"fwd": 2, "bwd": 4}}
+            "fwd_bytes": fwd_bytes, "bwd_bytes": bwd_bytes, "launches": {"fwd": 1, "bwd": 2},
+            "separate": {"fwd_us": round(f1_ms * 1e3, 2), "bwd_us": round(b1_ms * 1e3, 2),
+                         "launches": {"fwd": 2, "bwd": 4}}}
 
 
 def lm_loss_leg(cfg_id, steps, warmup):

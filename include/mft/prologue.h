@@ -67,6 +67,23 @@ mft_status mft_prologue_workspace_size(const mft_prologue_desc* desc, size_t* by
 mft_status mft_prologue_bwd(const mft_prologue_desc* desc, const void* x, const float* w, const float* dy,
                             float* dx, float* dw, void* workspace, hipStream_t stream);
 
+/* Batched forms: n (1 or 2) independent prologues in one launch per
+ * direction, such as a layer's q heads and k heads (graph/gemma_model.cpp:
+ * 459-471 runs rms_norm and apply_rope on each).  Tensor i has descs[i] and
+ * the i-th pointer of every array; the results are those of n calls of
+ * mft_prologue_fwd / mft_prologue_bwd, bit for bit.  Every tensor of a batch
+ * has one dtype; they run as one launch when they share a head dim of 128,
+ * 256 or 512 with 16-byte-aligned rows, else one launch each.  The backward
+ * workspace (mft_prologue_workspace_size_n) holds every tensor's dw
+ * partials; dw[i] may be NULL.  No counterpart in the reference, which runs
+ * the two chains one after the other. */
+mft_status mft_prologue_fwd_n(int n, const mft_prologue_desc* descs, const void* const* x, const float* const* w,
+                              void* const* y, hipStream_t stream);
+mft_status mft_prologue_workspace_size_n(int n, const mft_prologue_desc* descs, size_t* bytes);
+mft_status mft_prologue_bwd_n(int n, const mft_prologue_desc* descs, const void* const* x, const float* const* w,
+                              const float* const* dy, float* const* dx, float* const* dw, void* workspace,
+                              hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -225,6 +225,44 @@ def prologue_backward(x, w, dy, norm="gemma", eps=1e-6, theta=10000.0, want_dw=T
     return dx, dw
 
 
+def prologue_forward_n(xs, ws, norm="gemma", eps=1e-6, theta=10000.0):
+    """prologue_forward of up to two tensors (a layer's q and k heads) in one
+    launch (mft_prologue_fwd_n): xs, ws lists; returns the list of y."""
+    ys, ds = [], []
+    for x, w in zip(xs, ws):
+        _check(x, "x")
+        if w is not None and (not w.is_cuda or w.dtype != torch.float32 or not w.is_contiguous()):
+            raise ValueError("w must be a contiguous fp32 GPU tensor [D]")
+        y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+        ys.append(y)
+        ds.append(_prologue_desc(x, norm, eps, theta, dict(x=x, y=y)))
+    capi.prologue_fwd_n(ds, [x.data_ptr() for x in xs], [0 if w is None else w.data_ptr() for w in ws],
+                        [y.data_ptr() for y in ys], _stream())
+    return ys
+
+
+def prologue_backward_n(xs, ws, dys, norm="gemma", eps=1e-6, theta=10000.0, want_dw=True):
+    """prologue_backward of up to two tensors in one launch per kernel
+    (mft_prologue_bwd_n): returns the list of (dx, dw)."""
+    ds, dxs, dws = [], [], []
+    for x, dy in zip(xs, dys):
+        _check(x, "x")
+        _check(dy, "dy")
+        if dy.dtype != torch.float32:
+            raise ValueError("dy must be fp32")
+        dxs.append(torch.empty(x.shape, dtype=torch.float32, device=x.device))
+        dws.append(torch.empty(x.shape[3], dtype=torch.float32, device=x.device)
+                   if norm != "none" and want_dw else None)
+        ds.append(_prologue_desc(x, norm, eps, theta, dict(x=x, dy=dy)))
+    ws_bytes = capi.prologue_workspace_size_n(ds)
+    wsp = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=xs[0].device)
+    capi.prologue_bwd_n(ds, [x.data_ptr() for x in xs], [0 if w is None else w.data_ptr() for w in ws],
+                        [dy.data_ptr() for dy in dys], [dx.data_ptr() for dx in dxs],
+                        [0 if dw is None else dw.data_ptr() for dw in dws], wsp.data_ptr() if ws_bytes else None,
+                        _stream())
+    return list(zip(dxs, dws))
+
+
 class QKPrologue(torch.autograd.Function):
     """Autograd node of y = rope(norm(x)); saves x and w only (the row norms
     are recomputed in the backward, as the reference's RMSNormBackward does)."""

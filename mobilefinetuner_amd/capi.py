@@ -26,6 +26,7 @@ EXPORTS = (
     "mft_attn_workspace_size", "mft_attn_fwd", "mft_attn_bwd", "mft_attn_bwd_stage", "mft_attn_bwd_noalloc",
     "mft_repeat_kv_fwd", "mft_repeat_kv_bwd", "mft_convert", "mft_last_error", "mft_version",
     "mft_prologue_fwd", "mft_prologue_workspace_size", "mft_prologue_bwd",
+    "mft_prologue_fwd_n", "mft_prologue_workspace_size_n", "mft_prologue_bwd_n",
     "mft_lm_ce_workspace_size", "mft_lm_ce_fwd", "mft_lm_ce_bwd", "mft_lm_ce_streaming_fwd",
     "mft_lm_ce_streaming_bwd",
     "mft_lora_workspace_size", "mft_lora_fwd", "mft_lora_bwd", "mft_lora_merge",
@@ -121,6 +122,12 @@ def lib():
     L.mft_prologue_workspace_size.argtypes = [C.POINTER(PrologueDesc), C.POINTER(C.c_size_t)]
     L.mft_prologue_bwd.restype = C.c_int
     L.mft_prologue_bwd.argtypes = [C.POINTER(PrologueDesc), vp, vp, vp, vp, vp, vp, vp]
+    L.mft_prologue_fwd_n.restype = C.c_int
+    L.mft_prologue_fwd_n.argtypes = [C.c_int, C.POINTER(PrologueDesc), vp, vp, vp, vp]
+    L.mft_prologue_workspace_size_n.restype = C.c_int
+    L.mft_prologue_workspace_size_n.argtypes = [C.c_int, C.POINTER(PrologueDesc), C.POINTER(C.c_size_t)]
+    L.mft_prologue_bwd_n.restype = C.c_int
+    L.mft_prologue_bwd_n.argtypes = [C.c_int, C.POINTER(PrologueDesc)] + [vp] * 7
     L.mft_lm_ce_workspace_size.restype = C.c_int
     L.mft_lm_ce_workspace_size.argtypes = [C.POINTER(LmLossDesc), C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
     L.mft_lm_ce_fwd.restype = C.c_int
@@ -139,7 +146,7 @@ def lib():
     L.mft_lora_bwd.argtypes = [C.POINTER(LoraDesc)] + [vp] * 7
     L.mft_lora_merge.restype = C.c_int
     L.mft_lora_merge.argtypes = [C.POINTER(LoraDesc), vp, C.c_float, vp]
-    if L.mft_version() != 6:
+    if L.mft_version() != 7:
         raise RuntimeError("libmft_attn.so version mismatch")
     _lib = L
     return L
@@ -223,6 +230,35 @@ def prologue_fwd(d: PrologueDesc, x, w, y, stream) -> None:
 
 def prologue_bwd(d: PrologueDesc, x, w, dy, dx, dw, workspace, stream) -> None:
     check(lib().mft_prologue_bwd(C.byref(d), x, w, dy, dx, dw, workspace, stream))
+
+
+def _descs(ds):
+    arr = (PrologueDesc * len(ds))(*ds)
+    return len(ds), arr
+
+
+def _ptrs(ps):
+    return (C.c_void_p * len(ps))(*[p if p else None for p in ps])
+
+
+def prologue_workspace_size_n(ds) -> int:
+    """mft_prologue_workspace_size_n over a list of descriptors."""
+    n, arr = _descs(ds)
+    out = C.c_size_t()
+    check(lib().mft_prologue_workspace_size_n(n, arr, C.byref(out)))
+    return out.value
+
+
+def prologue_fwd_n(ds, x, w, y, stream) -> None:
+    """mft_prologue_fwd_n: ds a list of descriptors, x / w / y lists of device pointers."""
+    n, arr = _descs(ds)
+    check(lib().mft_prologue_fwd_n(n, arr, _ptrs(x), _ptrs(w), _ptrs(y), stream))
+
+
+def prologue_bwd_n(ds, x, w, dy, dx, dw, workspace, stream) -> None:
+    """mft_prologue_bwd_n: lists of device pointers per operand (dw entries may be 0)."""
+    n, arr = _descs(ds)
+    check(lib().mft_prologue_bwd_n(n, arr, _ptrs(x), _ptrs(w), _ptrs(dy), _ptrs(dx), _ptrs(dw), workspace, stream))
 
 
 def lm_loss_desc(B, S, V, H=0, dtype=MFT_F32, ignore_index=-100, reduction=MFT_REDUCE_MEAN, chunk=0) -> LmLossDesc:

@@ -177,7 +177,7 @@ mft_status scratch_for_current_device(void** out) {
 
 extern "C" {
 
-int mft_version(void) { return 6; }
+int mft_version(void) { return 7; }
 
 const char* mft_last_error(void) { return mft::capi::g_last_error.c_str(); }
 

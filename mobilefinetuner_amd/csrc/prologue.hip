@@ -314,8 +314,20 @@ __global__ __launch_bounds__(256) void prologue_bwd_kernel(PrologueArgs a) {
 // dw[c] = sum of the workgroup partials, in a fixed order: 64 slices per
 // column (slice t adds partials t, t + 64, ... in double, eight loads in
 // flight), then the slices in slice order.
-__global__ __launch_bounds__(1024) void prologue_dw_reduce_kernel(const float* part, int64_t nparts, int D,
-                                                                  float* dw) {
+struct DwReduce {
+    const float* part[kPrologueMaxBatch];
+    int64_t nparts[kPrologueMaxBatch];
+    float* dw[kPrologueMaxBatch];
+};
+__device__ __forceinline__ void prologue_dw_reduce(const float* part, int64_t nparts, int D, float* dw);
+// One launch for the dw of every tensor of a batch: blockIdx.y = tensor.
+__global__ __launch_bounds__(1024) void prologue_dw_reduce_kernel(DwReduce r, int D) {
+    if (blockIdx.y == 0)
+        prologue_dw_reduce(r.part[0], r.nparts[0], D, r.dw[0]);
+    else
+        prologue_dw_reduce(r.part[1], r.nparts[1], D, r.dw[1]);
+}
+__device__ __forceinline__ void prologue_dw_reduce(const float* part, int64_t nparts, int D, float* dw) {
     constexpr int NS = 64;
     __shared__ double acc[NS][16];
     const int cl = threadIdx.x & 15, sl = threadIdx.x >> 4;
@@ -372,8 +384,9 @@ template <int LPR> __device__ __forceinline__ double group_sum(double v) {
 // only the norm's sum of squares crosses lanes.  A lane takes GROUPS
 // consecutive rows (row_addr_hf order) and evaluates sincosf only when a
 // row's position differs from the previous row's.
+// blk: the workgroup's index within this tensor's launch range.
 template <typename T, int D>
-__global__ __launch_bounds__(256) void prologue_fwd_vec(PrologueArgs a) {
+__device__ __forceinline__ void prologue_fwd_vec_body(const PrologueArgs& a, int64_t blk) {
 #pragma clang fp contract(off)
     constexpr int EPL = 16 / (int)sizeof(T), H2 = EPL / 2, LPR = D / EPL, RPI = 64 / LPR, HALF = D / 2;
     static_assert(LPR >= 2 && LPR <= 64, "a row spans 2..64 lanes");
@@ -381,7 +394,7 @@ __global__ __launch_bounds__(256) void prologue_fwd_vec(PrologueArgs a) {
     const int lane = threadIdx.x & 63, gl = lane % LPR;
     const int q0 = gl * H2;  // this lane's first element of the first half
     // the lane's rows: lane_row0 + g, g < GROUPS
-    const int64_t lane_row0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * (RPI * GROUPS) + (lane / LPR) * GROUPS;
+    const int64_t lane_row0 = (blk * 4 + (threadIdx.x >> 6)) * (RPI * GROUPS) + (lane / LPR) * GROUPS;
     float v[GROUPS][2][H2];  // [group][half][element]
     RowAddr ra[GROUPS];
 #pragma unroll
@@ -458,7 +471,7 @@ __global__ __launch_bounds__(256) void prologue_fwd_vec(PrologueArgs a) {
 // summed per lane over its rows, then over the lanes of the wave that share
 // its columns and the 4 waves in fixed order.
 template <typename T, int D>
-__global__ __launch_bounds__(256) void prologue_bwd_vec(PrologueArgs a) {
+__device__ __forceinline__ void prologue_bwd_vec_body(const PrologueArgs& a, int64_t blk) {
 #pragma clang fp contract(off)
     constexpr int EPL = 4, H2 = EPL / 2, LPR = D / EPL, RPI = 64 / LPR, HALF = D / 2;
     static_assert(LPR >= 2 && LPR <= 64, "a row spans 2..64 lanes");
@@ -470,7 +483,7 @@ __global__ __launch_bounds__(256) void prologue_bwd_vec(PrologueArgs a) {
     const int q0 = gl * H2;  // this lane's first element of the first half
     const bool norm = a.norm != PROLOGUE_NORM_NONE;
     // the lane's rows: lane_row0 + g, g < GROUPS
-    const int64_t lane_row0 = (int64_t)blockIdx.x * ROWS_WG + w * (RPI * GROUPS) + (lane / LPR) * GROUPS;
+    const int64_t lane_row0 = blk * ROWS_WG + w * (RPI * GROUPS) + (lane / LPR) * GROUPS;
     // every row group's loads first; [group][half][element]
     float gv[GROUPS][2][H2], xv[GROUPS][2][H2];
     RowAddr ra[GROUPS];
@@ -572,7 +585,7 @@ __global__ __launch_bounds__(256) void prologue_bwd_vec(PrologueArgs a) {
     }
     __syncthreads();
     if (w == 0 && lane < LPR) {
-        float* part = a.dw_part + (int64_t)blockIdx.x * D;
+        float* part = a.dw_part + blk * D;
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
@@ -584,6 +597,28 @@ __global__ __launch_bounds__(256) void prologue_bwd_vec(PrologueArgs a) {
             }
     }
 }
+
+// The 16-byte-lane kernels over a batch of tensors (PrologueBatch): tensor
+// i takes workgroups first_block[i] .. first_block[i + 1] - 1, each the
+// workgroup of that index in a launch of its own; the branch picks a
+// statically indexed argument set.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void prologue_fwd_vec(PrologueBatch bb) {
+    const int64_t bx = blockIdx.x;
+    if (bb.n > 1 && bx >= bb.first_block[1])
+        prologue_fwd_vec_body<T, D>(bb.a[1], bx - bb.first_block[1]);
+    else
+        prologue_fwd_vec_body<T, D>(bb.a[0], bx);
+}
+template <typename T, int D>
+__global__ __launch_bounds__(256) void prologue_bwd_vec(PrologueBatch bb) {
+    const int64_t bx = blockIdx.x;
+    if (bb.n > 1 && bx >= bb.first_block[1])
+        prologue_bwd_vec_body<T, D>(bb.a[1], bx - bb.first_block[1]);
+    else
+        prologue_bwd_vec_body<T, D>(bb.a[0], bx);
+}
+static_assert(kPrologueMaxBatch == 2, "the batch kernels pick one of two argument sets");
 
 // Whether every row of a layout starts on a vbytes boundary.
 bool rows_aligned(const void* base, const Strides& st, int64_t esz, int vbytes) {
@@ -603,42 +638,71 @@ hipError_t launch_shape(const PrologueArgs& a, bool bwd, hipStream_t st) {
     return hipGetLastError();
 }
 
-// The 16-byte-lane kernels, when the head dim and every row allow them.
+// Whether the 16-byte-lane kernel of head dim D takes tensor a (its head
+// dim and every row's alignment allow it).
 template <typename T, int D>
-bool launch_vec(const PrologueArgs& a, bool bwd, hipStream_t st, hipError_t* e) {
+bool vec_takes(const PrologueArgs& a, bool bwd) {
     const int64_t esz = sizeof(T);
+    if (a.D != D) return false;
     if (bwd) {
         if constexpr (D / 4 > 64) {
             return false;
         } else {
             if (!rows_aligned(a.dy, a.sdy, 4, 16) || !rows_aligned(a.dx, a.sdx, 4, 16)) return false;
-            if (a.norm != PROLOGUE_NORM_NONE && !rows_aligned(a.x, a.sx, esz, 4 * (int)esz)) return false;
-            hipLaunchKernelGGL((prologue_bwd_vec<T, D>), dim3((unsigned)prologue_bwd_blocks(a.rows, D)), dim3(256), 0,
-                               st, a);
+            return a.norm == PROLOGUE_NORM_NONE || rows_aligned(a.x, a.sx, esz, 4 * (int)esz);
         }
     } else {
-        constexpr int LPR = D * (int)sizeof(T) / 16;
-        if constexpr (LPR > 64) {
+        if constexpr (D * (int)sizeof(T) / 16 > 64) {
             return false;
         } else {
-            if (!rows_aligned(a.x, a.sx, esz, 16) || !rows_aligned(a.y, a.sy, esz, 16)) return false;
-            const int64_t per_block = 4 * (64 / LPR) * kFwdVecGroups;
-            hipLaunchKernelGGL((prologue_fwd_vec<T, D>), dim3((unsigned)((a.rows + per_block - 1) / per_block)),
-                               dim3(256), 0, st, a);
+            return rows_aligned(a.x, a.sx, esz, 16) && rows_aligned(a.y, a.sy, esz, 16);
         }
     }
-    *e = hipGetLastError();
+}
+
+// Workgroups of the 16-byte-lane launch for one tensor.
+template <typename T, int D>
+int64_t vec_blocks(const PrologueArgs& a, bool bwd) {
+    if (bwd) return prologue_bwd_blocks(a.rows, D);
+    constexpr int LPR = D * (int)sizeof(T) / 16;
+    const int64_t per_block = 4 * (64 / (LPR < 64 ? LPR : 64)) * kFwdVecGroups;
+    return (a.rows + per_block - 1) / per_block;
+}
+
+// One 16-byte-lane launch over n <= kPrologueMaxBatch tensors it takes.
+template <typename T, int D>
+hipError_t launch_vec(const PrologueArgs* a, int n, bool bwd, hipStream_t st) {
+    PrologueBatch bb;
+    bb.n = n;
+    int64_t blocks = 0;
+    for (int i = 0; i < n; ++i) {
+        bb.a[i] = a[i];
+        bb.first_block[i] = blocks;
+        blocks += vec_blocks<T, D>(a[i], bwd);
+    }
+    for (int i = n; i <= kPrologueMaxBatch; ++i) bb.first_block[i] = blocks;
+    if (bwd) {
+        if constexpr (D / 4 <= 64)
+            hipLaunchKernelGGL((prologue_bwd_vec<T, D>), dim3((unsigned)blocks), dim3(256), 0, st, bb);
+    } else {
+        if constexpr (D * (int)sizeof(T) / 16 <= 64)
+            hipLaunchKernelGGL((prologue_fwd_vec<T, D>), dim3((unsigned)blocks), dim3(256), 0, st, bb);
+    }
+    return hipGetLastError();
+}
+
+template <typename T, int D>
+bool all_vec(const PrologueArgs* a, int n, bool bwd) {
+    for (int i = 0; i < n; ++i)
+        if (!vec_takes<T, D>(a[i], bwd)) return false;
     return true;
 }
 
+// One tensor by the one-wave-per-row kernels.
 template <typename T>
-hipError_t launch_t(const PrologueArgs& a, bool bwd, hipStream_t st) {
+hipError_t launch_rows(const PrologueArgs& a, bool bwd, hipStream_t st) {
     const int half = a.D / 2;
     const int64_t esz = sizeof(T);
-    hipError_t ve = hipSuccess;
-    if (a.D == 128 && launch_vec<T, 128>(a, bwd, st, &ve)) return ve;
-    if (a.D == 256 && launch_vec<T, 256>(a, bwd, st, &ve)) return ve;
-    if (a.D == 512 && launch_vec<T, 512>(a, bwd, st, &ve)) return ve;
     if (half == 64 || half == 128 || half == 256) {
         const int V = half / 64;  // contiguous elements per lane
         bool ok;
@@ -659,6 +723,25 @@ hipError_t launch_t(const PrologueArgs& a, bool bwd, hipStream_t st) {
     return launch_shape<T, 4, 1>(a, bwd, st);
 }
 
+// n tensors: one launch when the 16-byte-lane kernel of their common head
+// dim takes them all, otherwise one launch per tensor.
+template <typename T>
+hipError_t launch_t(const PrologueArgs* a, int n, bool bwd, hipStream_t st) {
+    const int D = a[0].D;
+    if (D == 128 && all_vec<T, 128>(a, n, bwd)) return launch_vec<T, 128>(a, n, bwd, st);
+    if (D == 256 && all_vec<T, 256>(a, n, bwd)) return launch_vec<T, 256>(a, n, bwd, st);
+    if (D == 512 && all_vec<T, 512>(a, n, bwd)) return launch_vec<T, 512>(a, n, bwd, st);
+    for (int i = 0; i < n; ++i) {
+        hipError_t e;
+        if (a[i].D == 128 && vec_takes<T, 128>(a[i], bwd)) e = launch_vec<T, 128>(a + i, 1, bwd, st);
+        else if (a[i].D == 256 && vec_takes<T, 256>(a[i], bwd)) e = launch_vec<T, 256>(a + i, 1, bwd, st);
+        else if (a[i].D == 512 && vec_takes<T, 512>(a[i], bwd)) e = launch_vec<T, 512>(a + i, 1, bwd, st);
+        else e = launch_rows<T>(a[i], bwd, st);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 }  // namespace
 
 int64_t prologue_bwd_blocks(int64_t rows, int D) {
@@ -666,17 +749,32 @@ int64_t prologue_bwd_blocks(int64_t rows, int D) {
     return (rows + rows_per_wg - 1) / rows_per_wg;
 }
 
-hipError_t launch_prologue_fwd(const PrologueArgs& a, bool is_bf16, hipStream_t st) {
-    return is_bf16 ? launch_t<bf16>(a, false, st) : launch_t<float>(a, false, st);
+hipError_t launch_prologue_fwd(const PrologueArgs* a, int n, bool is_bf16, hipStream_t st) {
+    return is_bf16 ? launch_t<bf16>(a, n, false, st) : launch_t<float>(a, n, false, st);
 }
 
-hipError_t launch_prologue_bwd(const PrologueArgs& a, bool is_bf16, float* dw, hipStream_t st) {
-    const hipError_t e = is_bf16 ? launch_t<bf16>(a, true, st) : launch_t<float>(a, true, st);
+hipError_t launch_prologue_bwd(const PrologueArgs* a, int n, bool is_bf16, float* const* dw, hipStream_t st) {
+    const hipError_t e = is_bf16 ? launch_t<bf16>(a, n, true, st) : launch_t<float>(a, n, true, st);
     if (e != hipSuccess) return e;
-    if (a.norm != PROLOGUE_NORM_NONE && dw && a.dw_part) {
-        hipLaunchKernelGGL(prologue_dw_reduce_kernel, dim3((unsigned)((a.D + 15) / 16)), dim3(1024), 0, st,
-                           (const float*)a.dw_part, prologue_bwd_blocks(a.rows, a.D), a.D, dw);
-        return hipGetLastError();
+    // dw of every tensor with a norm and a dw output: one launch per head
+    // dim (one in all when they share it, as the q and k heads do)
+    bool done[kPrologueMaxBatch] = {};
+    for (int i = 0; i < n; ++i) {
+        if (done[i] || a[i].norm == PROLOGUE_NORM_NONE || !dw[i] || !a[i].dw_part) continue;
+        DwReduce r{};
+        int m = 0;
+        for (int j = i; j < n; ++j) {
+            if (done[j] || a[j].norm == PROLOGUE_NORM_NONE || !dw[j] || !a[j].dw_part || a[j].D != a[i].D) continue;
+            r.part[m] = a[j].dw_part;
+            r.nparts[m] = prologue_bwd_blocks(a[j].rows, a[j].D);
+            r.dw[m] = dw[j];
+            done[j] = true;
+            ++m;
+        }
+        hipLaunchKernelGGL(prologue_dw_reduce_kernel, dim3((unsigned)((a[i].D + 15) / 16), (unsigned)m), dim3(1024), 0,
+                           st, r, a[i].D);
+        const hipError_t e2 = hipGetLastError();
+        if (e2 != hipSuccess) return e2;
     }
     return hipSuccess;
 }

@@ -64,25 +64,88 @@ mft_status check(const mft_prologue_desc* d, const char* who, mft::PrologueArgs*
 
 bool elem_aligned(const void* p, int64_t esz) { return (reinterpret_cast<uintptr_t>(p) % esz) == 0; }
 
+// Bytes of one tensor's dw partials, and of a batch's (each 256-byte aligned).
+size_t part_bytes(const mft_prologue_desc* d, const mft::PrologueArgs& a) {
+    return d->norm == MFT_NORM_NONE ? 0 : (size_t)(mft::prologue_bwd_blocks(a.rows, a.D) * a.D) * sizeof(float);
+}
+size_t up256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+mft_status check_n(int n, const mft_prologue_desc* descs, const char* who, mft::PrologueArgs* a) {
+    if (n < 1 || n > mft::kPrologueMaxBatch)
+        return fail(MFT_ERR_INVALID_ARG, std::string(who) + ": n must be 1 or 2");
+    if (!descs) return fail(MFT_ERR_INVALID_ARG, std::string(who) + ": descs is NULL");
+    for (int i = 0; i < n; ++i) {
+        const mft_status r = check(&descs[i], who, &a[i]);
+        if (r != MFT_OK) return r;
+        if (descs[i].dtype != descs[0].dtype)
+            return fail(MFT_ERR_INVALID_ARG, std::string(who) + ": every tensor of a batch has one dtype");
+    }
+    return MFT_OK;
+}
+
+mft_status fwd_n(int n, const mft_prologue_desc* descs, const void* const* x, const float* const* w, void* const* y,
+                 hipStream_t stream, const char* who) {
+    mft::PrologueArgs a[mft::kPrologueMaxBatch];
+    mft_status r = check_n(n, descs, who, a);
+    if (r != MFT_OK) return r;
+    if (!x || !w || !y) return fail(MFT_ERR_INVALID_ARG, std::string(who) + ": x, w and y must be non-NULL arrays");
+    for (int i = 0; i < n; ++i) {
+        if (!x[i] || !y[i]) return fail(MFT_ERR_INVALID_ARG, std::string(who) + ": x and y must be non-NULL");
+        if (descs[i].norm != MFT_NORM_NONE && !w[i])
+            return fail(MFT_ERR_INVALID_ARG, std::string(who) + ": a norm needs its weight w");
+        const int64_t esz = descs[i].dtype == MFT_BF16 ? 2 : 4;
+        if (!elem_aligned(x[i], esz) || !elem_aligned(y[i], esz) || (w[i] && !elem_aligned(w[i], 4)))
+            return fail(MFT_ERR_INVALID_ARG, std::string(who) + ": pointers must be element-aligned");
+        a[i].x = x[i];
+        a[i].w = w[i];
+        a[i].y = y[i];
+    }
+    return hip_status(mft::launch_prologue_fwd(a, n, descs[0].dtype == MFT_BF16, stream),
+                      (std::string(who) + " launch").c_str());
+}
+
+mft_status bwd_n(int n, const mft_prologue_desc* descs, const void* const* x, const float* const* w,
+                 const float* const* dy, float* const* dx, float* const* dw, void* workspace, hipStream_t stream,
+                 const char* who) {
+    mft::PrologueArgs a[mft::kPrologueMaxBatch];
+    mft_status r = check_n(n, descs, who, a);
+    if (r != MFT_OK) return r;
+    if (!x || !w || !dy || !dx || !dw)
+        return fail(MFT_ERR_INVALID_ARG, std::string(who) + ": x, w, dy, dx and dw must be non-NULL arrays");
+    size_t off = 0;
+    for (int i = 0; i < n; ++i) {
+        if (!dy[i] || !dx[i]) return fail(MFT_ERR_INVALID_ARG, std::string(who) + ": dy and dx must be non-NULL");
+        const bool norm = descs[i].norm != MFT_NORM_NONE;
+        if (norm && (!x[i] || !w[i]))
+            return fail(MFT_ERR_INVALID_ARG, std::string(who) + ": a norm needs x and its weight w");
+        if (norm && dw[i] && !workspace)
+            return fail(MFT_ERR_INVALID_ARG,
+                        std::string(who) + ": dw needs the workspace (mft_prologue_workspace_size)");
+        if (static_cast<const void*>(dx[i]) == x[i] || static_cast<const void*>(dx[i]) == static_cast<const void*>(dy[i]))
+            return fail(MFT_ERR_INVALID_ARG, std::string(who) + ": dx may not alias x or dy");
+        const int64_t esz = descs[i].dtype == MFT_BF16 ? 2 : 4;
+        if ((x[i] && !elem_aligned(x[i], esz)) || !elem_aligned(dy[i], 4) || !elem_aligned(dx[i], 4) ||
+            (w[i] && !elem_aligned(w[i], 4)) || (dw[i] && !elem_aligned(dw[i], 4)) ||
+            (workspace && !elem_aligned(workspace, 4)))
+            return fail(MFT_ERR_INVALID_ARG, std::string(who) + ": pointers must be element-aligned");
+        a[i].x = x[i];
+        a[i].w = w[i];
+        a[i].dy = dy[i];
+        a[i].dx = dx[i];
+        a[i].dw_part = norm && dw[i] ? reinterpret_cast<float*>(static_cast<char*>(workspace) + off) : nullptr;
+        off += up256(part_bytes(&descs[i], a[i]));
+    }
+    return hip_status(mft::launch_prologue_bwd(a, n, descs[0].dtype == MFT_BF16, dw, stream),
+                      (std::string(who) + " launch").c_str());
+}
+
 }  // namespace
 
 extern "C" {
 
 mft_status mft_prologue_fwd(const mft_prologue_desc* desc, const void* x, const float* w, void* y,
                             hipStream_t stream) {
-    mft::PrologueArgs a;
-    mft_status r = check(desc, "mft_prologue_fwd", &a);
-    if (r != MFT_OK) return r;
-    if (!x || !y) return fail(MFT_ERR_INVALID_ARG, "mft_prologue_fwd: x and y must be non-NULL");
-    if (desc->norm != MFT_NORM_NONE && !w)
-        return fail(MFT_ERR_INVALID_ARG, "mft_prologue_fwd: a norm needs its weight w");
-    const int64_t esz = desc->dtype == MFT_BF16 ? 2 : 4;
-    if (!elem_aligned(x, esz) || !elem_aligned(y, esz) || (w && !elem_aligned(w, 4)))
-        return fail(MFT_ERR_INVALID_ARG, "mft_prologue_fwd: pointers must be element-aligned");
-    a.x = x;
-    a.w = w;
-    a.y = y;
-    return hip_status(mft::launch_prologue_fwd(a, desc->dtype == MFT_BF16, stream), "mft_prologue_fwd launch");
+    return fwd_n(1, desc, &x, &w, &y, stream, "mft_prologue_fwd");
 }
 
 mft_status mft_prologue_workspace_size(const mft_prologue_desc* desc, size_t* bytes) {
@@ -90,32 +153,35 @@ mft_status mft_prologue_workspace_size(const mft_prologue_desc* desc, size_t* by
     mft_status r = check(desc, "mft_prologue_workspace_size", &a);
     if (r != MFT_OK) return r;
     if (!bytes) return fail(MFT_ERR_INVALID_ARG, "mft_prologue_workspace_size: bytes is NULL");
-    *bytes = desc->norm == MFT_NORM_NONE ? 0 : (size_t)(mft::prologue_bwd_blocks(a.rows, a.D) * a.D) * sizeof(float);
+    *bytes = part_bytes(desc, a);
     return MFT_OK;
 }
 
 mft_status mft_prologue_bwd(const mft_prologue_desc* desc, const void* x, const float* w, const float* dy,
                             float* dx, float* dw, void* workspace, hipStream_t stream) {
-    mft::PrologueArgs a;
-    mft_status r = check(desc, "mft_prologue_bwd", &a);
+    return bwd_n(1, desc, &x, &w, &dy, &dx, &dw, workspace, stream, "mft_prologue_bwd");
+}
+
+mft_status mft_prologue_fwd_n(int n, const mft_prologue_desc* descs, const void* const* x, const float* const* w,
+                              void* const* y, hipStream_t stream) {
+    return fwd_n(n, descs, x, w, y, stream, "mft_prologue_fwd_n");
+}
+
+mft_status mft_prologue_workspace_size_n(int n, const mft_prologue_desc* descs, size_t* bytes) {
+    mft::PrologueArgs a[mft::kPrologueMaxBatch];
+    mft_status r = check_n(n, descs, "mft_prologue_workspace_size_n", a);
     if (r != MFT_OK) return r;
-    if (!dy || !dx) return fail(MFT_ERR_INVALID_ARG, "mft_prologue_bwd: dy and dx must be non-NULL");
-    const bool norm = desc->norm != MFT_NORM_NONE;
-    if (norm && (!x || !w)) return fail(MFT_ERR_INVALID_ARG, "mft_prologue_bwd: a norm needs x and its weight w");
-    if (norm && dw && !workspace)
-        return fail(MFT_ERR_INVALID_ARG, "mft_prologue_bwd: dw needs the workspace (mft_prologue_workspace_size)");
-    if (static_cast<const void*>(dx) == x || static_cast<const void*>(dx) == static_cast<const void*>(dy))
-        return fail(MFT_ERR_INVALID_ARG, "mft_prologue_bwd: dx may not alias x or dy");
-    const int64_t esz = desc->dtype == MFT_BF16 ? 2 : 4;
-    if ((x && !elem_aligned(x, esz)) || !elem_aligned(dy, 4) || !elem_aligned(dx, 4) || (w && !elem_aligned(w, 4)) ||
-        (dw && !elem_aligned(dw, 4)) || (workspace && !elem_aligned(workspace, 4)))
-        return fail(MFT_ERR_INVALID_ARG, "mft_prologue_bwd: pointers must be element-aligned");
-    a.x = x;
-    a.w = w;
-    a.dy = dy;
-    a.dx = dx;
-    a.dw_part = norm && dw ? static_cast<float*>(workspace) : nullptr;
-    return hip_status(mft::launch_prologue_bwd(a, desc->dtype == MFT_BF16, dw, stream), "mft_prologue_bwd launch");
+    if (!bytes) return fail(MFT_ERR_INVALID_ARG, "mft_prologue_workspace_size_n: bytes is NULL");
+    size_t total = 0;
+    for (int i = 0; i < n; ++i) total += up256(part_bytes(&descs[i], a[i]));
+    *bytes = total;
+    return MFT_OK;
+}
+
+mft_status mft_prologue_bwd_n(int n, const mft_prologue_desc* descs, const void* const* x, const float* const* w,
+                              const float* const* dy, float* const* dx, float* const* dw, void* workspace,
+                              hipStream_t stream) {
+    return bwd_n(n, descs, x, w, dy, dx, dw, workspace, stream, "mft_prologue_bwd_n");
 }
 
 }  // extern "C"

@@ -39,7 +39,22 @@ constexpr int prologue_bwd_rows_per_wave(int elems) { return elems >= 4 ? 2 : 4;
 // one row of D floats per workgroup.
 int64_t prologue_bwd_blocks(int64_t rows, int D);
 
-hipError_t launch_prologue_fwd(const PrologueArgs& a, bool is_bf16, hipStream_t st);
-hipError_t launch_prologue_bwd(const PrologueArgs& a, bool is_bf16, float* dw, hipStream_t st);
+// Tensors one launch of the 16-byte-lane kernels takes (the q and the k
+// heads of a layer): tensor i runs workgroups first_block[i] ..
+// first_block[i + 1] - 1, each computing what the workgroup of that index
+// computes in a launch of its own.
+constexpr int kPrologueMaxBatch = 2;
+struct PrologueBatch {
+    PrologueArgs a[kPrologueMaxBatch];
+    int64_t first_block[kPrologueMaxBatch + 1];
+    int n;
+};
+
+// n (1 <= n <= kPrologueMaxBatch) tensors of one dtype: one launch per
+// direction when the 16-byte-lane kernel takes them all (same head dim,
+// aligned rows), otherwise one per tensor.  dw[i]: tensor i's dL/dw (NULL:
+// none), reduced from its a[i].dw_part.
+hipError_t launch_prologue_fwd(const PrologueArgs* a, int n, bool is_bf16, hipStream_t st);
+hipError_t launch_prologue_bwd(const PrologueArgs* a, int n, bool is_bf16, float* const* dw, hipStream_t st);
 
 }  // namespace mft

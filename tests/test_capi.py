@@ -55,7 +55,7 @@ def test_header_compiles_as_c(tmp_path):
     """The header is plain C (extern "C", C99 types, no torch types)."""
     src = tmp_path / "t.c"
     src.write_text('#include "mft/attention.h"\n#include "mft/prologue.h"\n#include "mft/lm_loss.h"\n'
-                   'int main(void){return mft_version()==6?0:1;}\n')
+                   'int main(void){return mft_version()==7?0:1;}\n')
     res = subprocess.run(["gcc", "-std=c99", "-fsyntax-only", "-D__HIP_PLATFORM_AMD__",
                           "-I", os.path.join(ROOT, "include"), "-I", "/opt/rocm/include", str(src)],
                          capture_output=True, text=True)
@@ -63,7 +63,7 @@ def test_header_compiles_as_c(tmp_path):
 
 
 def test_version(capi):
-    assert capi.lib().mft_version() == 6
+    assert capi.lib().mft_version() == 7
 
 
 def _err(capi, fn):

@@ -215,3 +215,59 @@ def test_unaligned_rows_take_the_scalar_path(orc, dev):
     print(f"[errs] {e}", flush=True)
     assert max(e) <= TOL["bf16"], e
 
+
+
+BATCH_CASES = [
+    # (B, S, [(H, D, dtype, layout)], norm): q and k heads of one layer
+    (1, 4096, [(4, 256, "bf16", "bshd"), (1, 256, "bf16", "bshd")], "gemma"),  # Gemma-3-1B, one launch
+    (2, 257, [(3, 128, "f32", "bhsd"), (1, 128, "f32", "bshd")], "affine"),     # one launch, mixed layouts
+    (1, 100, [(2, 512, "bf16", "bhsd"), (2, 512, "bf16", "bhsd")], "none"),     # RoPE only
+    (2, 70, [(14, 64, "f32", "bhsd"), (2, 64, "f32", "bhsd")], "gemma"),        # head dim 64: a launch each
+    (1, 33, [(2, 96, "f32", "bhsd")], "gemma"),                                 # n = 1, strided lanes
+]
+
+
+@pytest.mark.parametrize("case", BATCH_CASES, ids=[f"b{i}" for i in range(len(BATCH_CASES))])
+def test_batched_prologue_equals_separate_calls_bitwise(orc, dev, case):
+    """mft_prologue_fwd_n / _bwd_n on the q and k heads give the bits of one
+    mft_prologue_fwd / _bwd call per tensor (y, dx and dw)."""
+    import torch
+    from mobilefinetuner_amd import attention as A
+    B, S, tensors, norm = case
+    xs, ws, dys = [], [], []
+    for i, (H, D, dtype, layout) in enumerate(tensors):
+        x, w, dy = _inputs(orc, B, H, S, D, dtype, 50 + 7 * i)
+        if layout == "bshd":
+            xd = _dev(x.transpose(0, 2, 1, 3), dtype, dev).transpose(1, 2)
+        else:
+            xd = _dev(x, dtype, dev)
+        xs.append(xd)
+        ws.append(torch.from_numpy(w).to(dev) if norm != "none" else None)
+        dys.append(torch.from_numpy(dy).to(dev))
+    print(f"[case] B{B} S{S} {tensors} {norm}", flush=True)
+    ys = A.prologue_forward_n(xs, ws, norm, 1e-6, 1e4)
+    gs = A.prologue_backward_n(xs, ws, dys, norm, 1e-6, 1e4)
+    for i in range(len(xs)):
+        y1 = A.prologue_forward(xs[i], ws[i], norm, 1e-6, 1e4)
+        dx1, dw1 = A.prologue_backward(xs[i], ws[i], dys[i], norm, 1e-6, 1e4)
+        torch.cuda.synchronize()
+        assert torch.equal(ys[i], y1), i
+        assert torch.equal(gs[i][0], dx1), i
+        if norm != "none":
+            assert torch.equal(gs[i][1], dw1), i
+        else:
+            assert gs[i][1] is None and dw1 is None
+
+
+def test_batched_prologue_rejects_bad_batches(dev):
+    import torch
+    from mobilefinetuner_amd import capi
+    a = torch.zeros(1, 2, 8, 64, dtype=torch.float32, device=dev)
+    b = torch.zeros(1, 2, 8, 64, dtype=torch.bfloat16, device=dev)
+    d32 = capi.prologue_desc(1, 2, 8, 64, capi.MFT_F32, capi.MFT_NORM_NONE, 0.0, 1e4)
+    d16 = capi.prologue_desc(1, 2, 8, 64, capi.MFT_BF16, capi.MFT_NORM_NONE, 0.0, 1e4)
+    s = torch.cuda.current_stream().cuda_stream
+    with pytest.raises(capi.MftError):  # one dtype per batch
+        capi.prologue_fwd_n([d32, d16], [a.data_ptr(), b.data_ptr()], [0, 0], [a.data_ptr(), b.data_ptr()], s)
+    with pytest.raises(capi.MftError):  # at most two tensors
+        capi.prologue_fwd_n([d32] * 3, [a.data_ptr()] * 3, [0] * 3, [a.data_ptr()] * 3, s)
