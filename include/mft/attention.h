@@ -30,11 +30,13 @@
  *     (natural log, fp32, [B, Hq, S]).  The backward recomputes the softmax
  *     from it; no S x S tensor is ever stored.
  *   - All pointers are caller-owned device memory, 16-byte aligned; no call
- *     allocates device memory.  Loading the library takes a fixed 128 MiB
- *     per GPU it runs on (the workspace of mft_attn_bwd_noalloc, a
- *     __device__ array of its code object), whether or not that entry point
- *     is called.  Work is enqueued on `stream` (NULL = the null stream) and is
- *     ordered there; the calls return before the GPU finishes.
+ *     allocates device memory.  The workspace of mft_attn_bwd_noalloc, a
+ *     fixed 128 MiB __device__ array, sits in a code object of its own (no
+ *     kernel shares it), which the HIP runtime loads on a GPU at that entry
+ *     point's first call there (deferred code-object loading, the ROCm
+ *     default; with HIP_ENABLE_DEFERRED_LOADING=0 every code object loads
+ *     with the library).  Work is enqueued on `stream` (NULL = the null
+ *     stream) and is ordered there; the calls return before the GPU finishes.
  *   - Errors: a non-zero mft_status, and mft_last_error() returns a
  *     thread-local message.  The C++ adapter rethrows it as the reference's
  *     TensorError / std::runtime_error (core/memory_efficient_attention.cpp:86-99).
@@ -165,7 +167,8 @@ mft_status mft_attn_bwd(const mft_attn_desc* desc, const void* q, const void* k,
 
 /* Backward that allocates nothing and takes no workspace: the same kernels as
  * mft_attn_bwd, with the workspace in a library-owned device array of a fixed
- * 128 MiB per GPU (held until the process ends).  Shapes whose backward
+ * 128 MiB per GPU, taken at the first call on that GPU and held until the
+ * process ends.  Shapes whose backward
  * workspace (mft_attn_workspace_size) exceeds that return MFT_ERR_UNSUPPORTED
  * with a message.  Every call on one GPU shares that GPU's array: calls that
  * overlap on one GPU (other streams, other threads) race.

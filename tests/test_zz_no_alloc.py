@@ -67,3 +67,54 @@ def test_noalloc_rejects_shape_beyond_scratch():
     assert capi.workspace_size(d)[1] > capi.NOALLOC_SCRATCH_BYTES
     with pytest.raises(RuntimeError, match="fixed scratch"):
         capi.attn_bwd_noalloc(d, *([16] * 9), None)
+
+
+_MEMORY_PROBE = r'''
+import ctypes, sys
+sys.path.insert(0, sys.argv[1])
+import torch
+from mobilefinetuner_amd import attention as A, capi
+dev = torch.device("cuda:0")
+B, H, S, D = 1, 2, 256, 64
+mk = lambda: torch.randn(B, H, S, D, device=dev, dtype=torch.bfloat16)
+q, k, v, dO = mk(), mk(), mk(), mk()
+o, lse = torch.empty_like(q), torch.empty(B, H, S, device=dev)
+dq, dk, dv = (torch.empty(B, H, S, D, device=dev) for _ in range(3))
+ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+torch.cuda.synchronize()
+f0 = torch.cuda.mem_get_info()[0]
+d = A._desc(q, k, 0.125, True, 0, None)
+sp = torch.cuda.current_stream().cuda_stream
+L = capi.lib()
+capi.check(L.mft_attn_fwd(ctypes.byref(d), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                          ws.data_ptr(), sp))
+capi.check(L.mft_attn_bwd(ctypes.byref(d), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dO.data_ptr(),
+                          lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), sp))
+torch.cuda.synchronize()
+f1 = torch.cuda.mem_get_info()[0]
+capi.attn_bwd_noalloc(d, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dO.data_ptr(), lse.data_ptr(),
+                      dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), sp)
+torch.cuda.synchronize()
+f2 = torch.cuda.mem_get_info()[0]
+print("MIB", (f0 - f1) / 2**20, (f1 - f2) / 2**20, flush=True)
+'''
+
+
+def test_scratch_is_taken_only_by_the_first_noalloc_call():
+    """In a fresh process, the regular forward and backward leave the 128 MiB
+    array's code object unloaded (deferred loading); the first
+    mft_attn_bwd_noalloc call on the GPU loads it."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ)
+    env.pop("HIP_ENABLE_DEFERRED_LOADING", None)
+    res = subprocess.run([sys.executable, "-c", _MEMORY_PROBE, root], capture_output=True, text=True, timeout=110,
+                         env=env)
+    print(res.stdout[-500:], res.stderr[-1500:], flush=True)
+    assert res.returncode == 0
+    regular, first_noalloc = (float(x) for x in next(l for l in res.stdout.splitlines() if l.startswith("MIB"))
+                              .split()[1:])
+    assert regular < 64, regular
+    assert first_noalloc >= 128, first_noalloc
