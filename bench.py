@@ -534,7 +534,7 @@ def roofline_of(cfg_id, r):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="c5", choices=sorted(CONFIGS))
     ap.add_argument("--headline-only", action="store_true",
