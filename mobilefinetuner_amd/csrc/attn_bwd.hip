@@ -678,9 +678,9 @@ BwdPlan plan_bwd_fast(const AttnShape& s) {
     // at which every unit fits in one round; fewer, longer units than one
     // launch per role would take also mean fewer fp32 partial tiles for
     // REDUCE.
-    const int kvc = kv_tile_cost(s), qc = q_tile_cost(s);
-    const int64_t c_kv = make_unit_split(gkv, 1, kKvIterCost, kvc).ctot;  // one (batch, kv head)
-    const int64_t c_q = make_unit_split(gq, 1, kQIterCost, qc).ctot;      // one (batch, query head)
+    const int kvi = kv_iter_cost(s), qi = q_iter_cost(s), kvc = kv_tile_cost(s), qc = q_tile_cost(s);
+    const int64_t c_kv = make_unit_split(gkv, 1, kvi, kvc).ctot;  // one (batch, kv head)
+    const int64_t c_q = make_unit_split(gq, 1, qi, qc).ctot;  // one (batch, query head)
     const int64_t work = c_kv * pairs_kv + c_q * pairs_q;
     auto units = [&](int64_t T) { return pairs_kv * ((c_kv + T - 1) / T) + pairs_q * ((c_q + T - 1) / T); };
     int64_t T = std::max<int64_t>(1, (work + cus - 1) / cus);
@@ -689,8 +689,8 @@ BwdPlan plan_bwd_fast(const AttnShape& s) {
     while (T < T_max && units(T) > cus) T += std::max<int64_t>(1, T / 64);
     // Units no shorter than kMinUnitIters iterations, and no tile over
     // kSplitMaxSlots units (REDUCE keeps a tile's slot list in LDS).
-    p.kv = fit_unit_split(gkv, (c_kv + T - 1) / T, kKvIterCost, kvc, kMinUnitIters, kSplitMaxSlots, &p.kv_parts_max);
-    p.q = fit_unit_split(gq, (c_q + T - 1) / T, kQIterCost, qc, kMinUnitIters, kSplitMaxSlots, &p.q_parts_max);
+    p.kv = fit_unit_split(gkv, (c_kv + T - 1) / T, kvi, kvc, kMinUnitIters, kSplitMaxSlots, &p.kv_parts_max);
+    p.q = fit_unit_split(gq, (c_q + T - 1) / T, qi, qc, kMinUnitIters, kSplitMaxSlots, &p.q_parts_max);
     return p;
 }
 

@@ -105,16 +105,26 @@ struct BwdPlan {
 // (its rows loaded, its outputs or partial stored, the pipeline restarted),
 // from per-unit cycle counts of the D = 256 kernels.  Backward iterations
 // are priced against each other: a dK/dV one (32 rows x 128 keys, four
-// products) 2, a dQ one (128 rows x 64 keys, three products) 3.  The tile
-// costs were measured at D = 256 only; narrower heads split by iteration
-// count (tile cost 0), which measured faster there than the D = 256 costs.
-constexpr int kFwdIterCost = 1, kKvIterCost = 2, kQIterCost = 3;
+// products) 2, a dQ one (128 rows x 64 keys, three products) 3, in tenths
+// for bf16 (20 and 30).  At D = 256 in bf16 a dK/dV iteration is priced 22:
+// the dK/dV units then end with the dQ units (a sweep of 18-26 against 30
+// measured C5 and C4 1.1% and 2.8% faster at 22, C3 at D = 64 best at
+// 20-21).  fp32 keeps 2 and 3 (the planner's search steps are relative to
+// the costs' scale, and the fp32 plans measured best at that scale).  The
+// tile costs were measured at D = 256 only; narrower heads split by
+// iteration count (tile cost 0), which measured faster there than the
+// D = 256 costs.
+constexpr int kFwdIterCost = 1;
+inline int kv_iter_cost(int64_t D, bool bf16) { return bf16 ? (D >= 256 ? 22 : 20) : 2; }
+inline int q_iter_cost(bool bf16) { return bf16 ? 30 : 3; }
 inline int fwd_tile_cost(int64_t D) { return D >= 256 ? 2 : 0; }
-inline int kv_tile_cost(int64_t D) { return D >= 256 ? 11 : 0; }
-inline int q_tile_cost(int64_t D) { return D >= 256 ? 13 : 0; }
+inline int kv_tile_cost(int64_t D) { return D >= 256 ? 110 : 0; }
+inline int q_tile_cost(int64_t D) { return D >= 256 ? 130 : 0; }
 // fp32 iterations take about 16 times as long as bf16 ones (the fp32 MFMA
 // rate), so a tile's fixed costs are left out for fp32.
 inline int fwd_tile_cost(const AttnShape& s) { return s.bf16 ? fwd_tile_cost(s.D) : 0; }
+inline int kv_iter_cost(const AttnShape& s) { return kv_iter_cost(s.D, s.bf16); }
+inline int q_iter_cost(const AttnShape& s) { return q_iter_cost(s.bf16); }
 inline int kv_tile_cost(const AttnShape& s) { return s.bf16 ? kv_tile_cost(s.D) : 0; }
 inline int q_tile_cost(const AttnShape& s) { return s.bf16 ? q_tile_cost(s.D) : 0; }
 // The fewest iterations the planners give a unit: backward units 4, forward
