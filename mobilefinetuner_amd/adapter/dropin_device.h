@@ -268,17 +268,23 @@ public:
     // host holds the data.
     void download(const std::vector<Segment>& segs) {
         std::lock_guard<std::mutex> lock(mu_);
-        for (const Segment& g : segs)
-            for (size_t off = 0; off < g.n; off += kChunk) {
-                const int i = take();
-                const size_t len = std::min(kChunk, g.n - off);
-                hip_check("drop-in", hipMemcpyAsync(buf_[i], static_cast<const char*>(g.src) + off, len,
-                                                    hipMemcpyDeviceToHost, stream()),
-                          "copy to host");
-                hip_check("drop-in", hipEventRecord(ev_[i], stream()), "staging");
-                out_[i] = {static_cast<char*>(g.dst) + off, len};
-            }
-        for (int k = 0; k < kBufs; ++k) take();  // drain the rest in order
+        try {
+            for (const Segment& g : segs)
+                for (size_t off = 0; off < g.n; off += kChunk) {
+                    const int i = take();
+                    const size_t len = std::min(kChunk, g.n - off);
+                    hip_check("drop-in", hipMemcpyAsync(buf_[i], static_cast<const char*>(g.src) + off, len,
+                                                        hipMemcpyDeviceToHost, stream()),
+                              "copy to host");
+                    hip_check("drop-in", hipEventRecord(ev_[i], stream()), "staging");
+                    out_[i] = {static_cast<char*>(g.dst) + off, len};
+                }
+            for (int k = 0; k < kBufs; ++k) take();  // drain the rest in order
+        } catch (...) {
+            // The destinations belong to the failed call: never copy into them later.
+            for (Pending& p : out_) p = {};
+            throw;
+        }
     }
 
 private:
@@ -383,7 +389,13 @@ public:
             }
             held_ += cls;
         }
-        auto t = std::make_shared<Tensor>(shape, p, kFloat32, kCPU, true);
+        TensorPtr t;
+        try {
+            t = std::make_shared<Tensor>(shape, p, kFloat32, kCPU, true);
+        } catch (...) {
+            free_[cls].push_back(p);
+            throw;
+        }
         live_.push_back({t, p, cls});
         return t;
     }
