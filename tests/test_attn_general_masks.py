@@ -128,3 +128,37 @@ def test_mask_mode_rejects_window_and_kv_len(dev):
     with pytest.raises(MftError):
         A.attention_forward(q, q, q, 0.125, True, kv_len=torch.full((1,), 10, dtype=torch.int32, device=dev),
                             masks=[m])
+
+
+@pytest.mark.parametrize("cfg", ["c4", "c5"])
+def test_mask_mode_at_full_size_equals_the_fast_kernels(orc, dev, cfg):
+    """At the BASELINE shapes, where the CPU oracle would take minutes: the mask
+    mode with an explicit [S,S] causal mask (0 on and below the diagonal, -1e10
+    above, the reference's create_causal_mask) and the causal flag off gives
+    the causal fast kernels' O and gradients; adding an all-zero [B,1,1,S] mask
+    as the second mask changes nothing.  Same bf16 bar as the parity tests,
+    elementwise against the fast path (both round the same fp32 values)."""
+    import torch
+
+    from gpu_util import TOL, to_dev
+    from mobilefinetuner_amd import attention as A
+    c = orc.CONFIGS[cfg]
+    B, Hq, Hkv, S, D = c["B"], c["Hq"], c["Hkv"], c["S"], c["D"]
+    print(f"[case] {cfg} B{B} Hq{Hq} Hkv{Hkv} S{S} D{D}", flush=True)
+    q, k, v, dO = orc.make_inputs(B, Hq, Hkv, S, D, 77, "bf16", do_sigma=0.1)
+    tq, tk, tv, tg = (to_dev(x, "bf16", dev) for x in (q, k, v, dO))
+    causal = torch.zeros(S, S, device=dev)
+    causal.masked_fill_(torch.ones(S, S, device=dev, dtype=torch.bool).triu(1), -1e10)
+    zero_pad = torch.zeros(B, 1, 1, S, device=dev)
+    o0, lse0 = A.attention_forward(tq, tk, tv, c["scale"], True)
+    g0 = A.attention_backward(tq, tk, tv, o0, tg, lse0, c["scale"], True)
+    for masks in ([causal], [causal, zero_pad]):
+        o1, lse1 = A.attention_forward(tq, tk, tv, c["scale"], False, masks=masks)
+        g1 = A.attention_backward(tq, tk, tv, o1, tg, lse1, c["scale"], False, masks=masks)
+        torch.cuda.synchronize()
+        for n, a, b in (("o", o1, o0), ("dq", g1[0], g0[0]), ("dk", g1[1], g0[1]), ("dv", g1[2], g0[2])):
+            err = orc.max_rel(a.float().cpu().numpy(), b.float().cpu().numpy())
+            print(f"[errs] {len(masks)} masks {n} {err:.3e}", flush=True)
+            assert err <= TOL["bf16"], (n, err)
+        # the row terms give the same log-sum-exp: row max + ln(sum) = lse
+        assert torch.allclose(lse1[..., 0] + lse1[..., 1], lse0, rtol=1e-4, atol=1e-3), "lse"
