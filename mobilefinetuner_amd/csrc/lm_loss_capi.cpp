@@ -9,7 +9,9 @@
 //             row statistics of Z merged into the running (max, sum)
 //   backward  Z recomputed, G = (exp(Z - lse) - onehot) * coeff  (input dtype)
 //             grad_hidden += G . W_c,  grad_weight[c] = G^T . hidden
-// so the [N, V] logits never exist at once.
+// so the [N, V] logits never exist at once.  With bf16 operands and H a
+// multiple of 64 the forward runs the fused kernel of lm_loss_fused.hip
+// instead (the GEMM and the row statistics in one pass, no logits at all).
 #include "mft/lm_loss.h"
 
 #include <string>
@@ -28,7 +30,7 @@ constexpr size_t kBlasWorkspace = size_t(64) << 20;
 size_t up(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct Layout {
-    size_t m, s, tgt, nll, count, z, g, blas, total;
+    size_t m, s, tgt, nll, count, z, g, blas, part, total;
 };
 
 int64_t chunk_of(const mft_lm_loss_desc* d) {
@@ -51,6 +53,8 @@ Layout layout(const mft_lm_loss_desc* d, bool streaming) {
         l.z = o, o += up(N * c * 4);
         l.g = o, o += up(N * c * esz);
         l.blas = o, o += kBlasWorkspace;
+        // fused forward: (max, sum) pairs per position and vocabulary part
+        l.part = o, o += up(N * 2 * mft::kCeFusedMaxRanges * sizeof(float2));
     }
     l.total = o;
     return l;
@@ -166,6 +170,12 @@ mft_status mft_lm_ce_streaming_fwd(const mft_lm_loss_desc* desc, const void* hid
     a.loss = loss;
     a.status = status;
     char* w = static_cast<char*>(workspace);
+    if (mft::ce_fused_supported(desc->H, desc->dtype == MFT_BF16)) {
+        const mft::CeFusedArgs plan = mft::ce_fused_plan(a.N, desc->V, desc->H);
+        hipError_t e = mft::launch_ce_fused_fwd(a, plan, hidden, weight, reinterpret_cast<float2*>(w + l.part), stream);
+        if (e == hipSuccess) e = mft::launch_ce_finalize(a, stream);
+        return hip_status(e, "mft_lm_ce_streaming_fwd launch");
+    }
     float* Z = reinterpret_cast<float*>(w + l.z);
     const int64_t chunk = chunk_of(desc);
     auto lock = mft::blas::lock();

@@ -39,4 +39,26 @@ hipError_t launch_ce_count(const CeArgs& a, hipStream_t st);
 hipError_t launch_ce_grad(const CeArgs& a, const void* z, bool z_bf16, int64_t ld, int64_t ncols, int64_t v0, void* g,
                           bool g_bf16, int64_t ldg, hipStream_t st);
 
+// Fused streaming forward (lm_loss_fused.hip): the logits GEMM and the row
+// statistics in one kernel, for bf16 hidden and weight with H a multiple of
+// 64.  Workgroups cover 256 positions x a range of 256-row vocabulary tiles;
+// part[n * nparts + 2 * range + half] holds each range's (max, sum) pair per
+// position and vocabulary half, folded by a second kernel into run_m / run_s
+// (the same state the chunked path leaves for launch_ce_finalize).
+constexpr int kCeFusedMaxRanges = 64;
+struct CeFusedArgs {
+    const void* hidden;  // [N, H] bf16
+    const void* weight;  // [V, H] bf16
+    const int32_t* labels;
+    float* tgt;
+    float2* part;
+    int64_t N, V, S;
+    int H, ignore;
+    int nb_pos, ntiles_v, tiles_per_range, ranges, nparts;
+};
+bool ce_fused_supported(int64_t H, bool bf16);
+CeFusedArgs ce_fused_plan(int64_t N, int64_t V, int64_t H);  // the launch geometry (nparts: pairs per position)
+hipError_t launch_ce_fused_fwd(const CeArgs& a, const CeFusedArgs& plan, const void* hidden, const void* weight,
+                               float2* part, hipStream_t st);
+
 }  // namespace mft

@@ -94,13 +94,15 @@ def test_no_mfma_result_overlaps_its_operands(tmp_path):
     """The compiler (ROCm 7.2) may give an MFMA with a literal-zero
     accumulator result registers that overlap its A/B operands, which gave
     NaN gradients on gfx950; the kernels start every chain with the
-    early-clobber form instead.  Compile the attention translation units to
-    assembly, with the build's flags, and check that no MFMA does this."""
+    early-clobber form instead.  Compile the attention translation units and
+    the fused LM cross-entropy GEMM to assembly, with the build's flags, and
+    check that no MFMA does this."""
     import concurrent.futures as cf
     import sys
     sys.path.insert(0, ROOT)
     from mobilefinetuner_amd import build as B
-    units = sorted(f for f in os.listdir(B.CSRC) if f.startswith("attn_") and f.endswith(".hip"))
+    units = sorted(f for f in os.listdir(B.CSRC)
+                   if (f.startswith("attn_") or f == "lm_loss_fused.hip") and f.endswith(".hip"))
 
     def asm(name):
         out = tmp_path / (name + ".s")
