@@ -33,10 +33,7 @@ namespace mft {
 namespace {
 
 constexpr int kCfRows = 256;  // vocabulary rows and positions per workgroup tile
-constexpr int kCfBK = 64;     // k per pipeline stage
 constexpr int kCfThreads = 512;
-constexpr int kCfTileElems = kCfRows * kCfBK;  // one [256 x 64] bf16 tile (32 KiB)
-typedef TileDma<kCfBK, kCfRows, kCfThreads, SWZ_ROW> CfDma;
 
 // A zero accumulator the compiler cannot see as a constant: a builtin MFMA
 // chain that starts from a literal zero may get result registers that
@@ -47,19 +44,35 @@ __device__ __forceinline__ f32x16 zero_acc() {
     return z;
 }
 
-// Byte offset of row r's 16-byte chunk c in a swizzled [256 x 64] tile.
-__device__ __forceinline__ uint32_t cf_off(int r, int c) {
-    return (uint32_t)r * (kCfBK * 2) + 16u * (uint32_t)(c ^ swz_row<kCfBK / 8>(r));
+constexpr int kCfBK = 64;                       // k per pipeline stage
+constexpr int kCfTile = kCfRows * kCfBK;        // elements of one [256 x 64] tile (32 KiB)
+typedef TileDma<kCfBK, kCfRows, kCfThreads, SWZ_ROW> CfDma;
+
+// Workgroup -> (vocabulary range, position block).  After xcd_block each
+// XCD runs a contiguous run of logical indices; with xbr > 0 a run of
+// xbr * xbp indices is an xbr x xbp rectangle of ranges x position blocks, so
+// an XCD's workgroups, which move through their ranges at about the same
+// pace, read each weight slice xbp times and each hidden slice xbr times
+// through one L2 (per stage the XCD misses on xbr + xbp slices, not 2 xbr xbp).
+__device__ __forceinline__ void cf_place(const CeFusedArgs& a, int blk, int* range, int* pb) {
+    if (a.xbr > 0) {
+        const int per = a.xbr * a.xbp, x = blk / per, in = blk % per, xr = a.ranges / a.xbr;
+        *range = (x % xr) * a.xbr + in / a.xbp;
+        *pb = (x / xr) * a.xbp + in % a.xbp;
+    } else {
+        *range = blk / a.nb_pos;
+        *pb = blk % a.nb_pos;
+    }
 }
 
 template <bool FAST>
 __global__ __launch_bounds__(kCfThreads) void ce_fused_fwd(CeFusedArgs a) {
     // [W tile 0][W tile 1][hidden tile 0][hidden tile 1]
-    __shared__ __attribute__((aligned(1024))) bf16 smem[4 * kCfTileElems];
+    __shared__ __attribute__((aligned(1024))) bf16 smem[4 * kCfTile];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
     const int wv = w & 1, wn = w >> 1;
-    const int blk = xcd_block((int)blockIdx.x, (int)gridDim.x);
-    const int range = blk / a.nb_pos, pb = blk % a.nb_pos;
+    int range, pb;
+    cf_place(a, xcd_block((int)blockIdx.x, (int)gridDim.x), &range, &pb);
     const int64_t p0 = (int64_t)pb * kCfRows;
     const int t0 = range * a.tiles_per_range, t1 = min(t0 + a.tiles_per_range, a.ntiles_v);
     const int KS = a.H / kCfBK;
@@ -82,30 +95,41 @@ __global__ __launch_bounds__(kCfThreads) void ce_fused_fwd(CeFusedArgs a) {
     dw.init(lane, wave_id(), a.H);
     dh.init(lane, wave_id(), a.H);
     const uint32_t sbase = lds_addr(smem);
-    auto issue = [&](int g) {
-        const int t = t0 + g / KS, k0 = (g % KS) * kCfBK, b = g & 1;
-        const bf16* W = static_cast<const bf16*>(a.weight) + k0;
-        const bf16* Hd = static_cast<const bf16*>(a.hidden) + k0;
+    // The issue cursor: tile and k offset of the next stage to load.
+    int it = t0, ik = 0;
+    auto issue_next = [&](int buf) {
+        const bf16* W = static_cast<const bf16*>(a.weight) + ik;
+        const bf16* Hd = static_cast<const bf16*>(a.hidden) + ik;
 #pragma unroll
         for (int j = 0; j < CfDma::PER; ++j) {
-            issue_tile_j<FAST, kCfBK, kCfRows, kCfThreads, SWZ_ROW>(dw, W, t * kCfRows, (int)a.V, kCfBK, a.H,
-                                                                     smem + b * kCfTileElems,
-                                                                     sbase + 2u * (uint32_t)(b * kCfTileElems), j);
-            issue_tile_j<FAST, kCfBK, kCfRows, kCfThreads, SWZ_ROW>(
-                dh, Hd, (int)p0, (int)a.N, kCfBK, a.H, smem + (2 + b) * kCfTileElems,
-                sbase + 2u * (uint32_t)((2 + b) * kCfTileElems), j);
+            issue_tile_j<FAST, kCfBK, kCfRows, kCfThreads, SWZ_ROW>(dw, W, it * kCfRows, (int)a.V, kCfBK, a.H,
+                                                                     smem + buf * kCfTile,
+                                                                     sbase + 2u * (uint32_t)(buf * kCfTile), j);
+            issue_tile_j<FAST, kCfBK, kCfRows, kCfThreads, SWZ_ROW>(dh, Hd, (int)p0, (int)a.N, kCfBK, a.H,
+                                                                     smem + (2 + buf) * kCfTile,
+                                                                     sbase + 2u * (uint32_t)((2 + buf) * kCfTile), j);
+        }
+        ik += kCfBK;
+        if (ik == a.H) {
+            ik = 0;
+            ++it;
         }
     };
 
-    // Per-lane LDS read offsets (bytes, within a tile) of k-step c's chunk
-    // 2c + hh: A = vocabulary rows 128 wv + 32 mt + n, B = positions
-    // 64 wn + 32 nt + n.  swz_row depends on the row's bits 1..3 only, so
-    // the rows' 32-row bases leave it unchanged.
-    uint32_t ro[4];
+    // Per-lane LDS byte offsets of k-step c's chunk 2c + hh (= 2c ^ hh ^
+    // swz_row(n)) in buffer 0: A = vocabulary row 128 wv + n of the W tile,
+    // B = position 64 wn + n of the hidden tile.  swz_row depends on row bits
+    // 1..3 only, so the MFMA tiles' 32-row bases leave it unchanged and go
+    // into the instructions' immediate offsets.
+    constexpr uint32_t kRow = kCfBK * 2, kMt = 32 * kRow, kTileB = kCfTile * 2;
+    uint32_t ro_a[4], ro_b[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) ro[c] = cf_off(n, 2 * c + hh);
-    const uint32_t a_base = (uint32_t)(128 * wv) * (kCfBK * 2), b_base = (uint32_t)(64 * wn) * (kCfBK * 2);
-    constexpr uint32_t kMt = 32u * (kCfBK * 2);  // bytes of 32 tile rows
+    for (int c = 0; c < 4; ++c) {
+        const uint32_t y16 = 16u * (uint32_t)((2 * c + hh) ^ swz_row<kCfBK / 8>(n));
+        ro_a[c] = (uint32_t)(128 * wv + n) * kRow + y16;
+        ro_b[c] = 2 * kTileB + (uint32_t)(64 * wn + n) * kRow + y16;
+    }
+    const char* lds = reinterpret_cast<const char*>(smem);
 
     f32x16 acc[4][2];
 #pragma unroll
@@ -114,28 +138,29 @@ __global__ __launch_bounds__(kCfThreads) void ce_fused_fwd(CeFusedArgs a) {
         for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = zero_acc();
     float m_run[2] = {-INFINITY, -INFINITY}, s_run[2] = {0.f, 0.f};
 
-    issue(0);
+    issue_next(0);
+    int ct = t0, ck = 0;  // tile and k offset of the stage being multiplied
     for (int g = 0; g < total; ++g) {
-        const int b = g & 1;
         // Stage g has landed in every wave's share; every wave is done with
-        // the buffers stage g + 1 streams into.
+        // the buffer stage g + 1 streams into (stage g - 1's).
         wait_vmcnt<0>();
         lds_barrier();
-        if (g + 1 < total) issue(g + 1);
-        const char* At = reinterpret_cast<const char*>(smem + b * kCfTileElems) + a_base;
-        const char* Bt = reinterpret_cast<const char*>(smem + (2 + b) * kCfTileElems) + b_base;
+        if (g + 1 < total) issue_next((g + 1) & 1);
         // Four k-steps, each six operand reads and eight MFMAs; the reads of
         // step c + 1 are issued before the MFMAs of step c (pinned below), so
         // two steps' operands are live at most.
+        const uint32_t boff = (uint32_t)(g & 1) * kTileB;
         struct Ops {
             bf16x8 a[4], b[2];
         };
         auto read = [&](int c) {
             Ops o;
+            const char* pa = lds + (ro_a[c] + boff);
+            const char* pb = lds + (ro_b[c] + boff);
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) o.a[mt] = *reinterpret_cast<const bf16x8*>(At + mt * kMt + ro[c]);
+            for (int mt = 0; mt < 4; ++mt) o.a[mt] = *reinterpret_cast<const bf16x8*>(pa + mt * kMt);
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) o.b[nt] = *reinterpret_cast<const bf16x8*>(Bt + nt * kMt + ro[c]);
+            for (int nt = 0; nt < 2; ++nt) o.b[nt] = *reinterpret_cast<const bf16x8*>(pb + nt * kMt);
             return o;
         };
         Ops cur = read(0);
@@ -150,10 +175,13 @@ __global__ __launch_bounds__(kCfThreads) void ce_fused_fwd(CeFusedArgs a) {
             if (c + 1 < 4) cur = nxt;
         }
         pin_read_ahead<4, 1, 6, 8>();
-        if (g % KS != KS - 1) continue;
+        ck += kCfBK;
+        if (ck != a.H) continue;
+        ck = 0;
+        const int64_t vw = (int64_t)ct * kCfRows + 128 * wv;  // this wave's first vocabulary row
+        ++ct;
 
         // The tile's logits are complete: fold them into the running pairs.
-        const int64_t vw = (int64_t)(t0 + g / KS) * kCfRows + 128 * wv;  // this wave's first vocabulary row
         const bool partial_v = vw + 128 > a.V;
         // rows of the wave's 128 at or past V, as a bound on the row within
         // the wave less this half-wave's offset (row_of_reg(r, hh) - 4 hh is
@@ -194,7 +222,8 @@ __global__ __launch_bounds__(kCfThreads) void ce_fused_fwd(CeFusedArgs a) {
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[mt][nt][r] = __expf(acc[mt][nt][r] - m_new);
+                    for (int r = 0; r < 16; ++r)  // exp(z - m) as exp2(z log2 e - m log2 e), one fma
+                        acc[mt][nt][r] = fast_exp2(fmaf(acc[mt][nt][r], kLog2e, -m_new * kLog2e));
                 float s = m_run[nt] == -INFINITY ? 0.f : s_run[nt] * __expf(m_run[nt] - m_new);
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt)
@@ -235,7 +264,7 @@ __global__ __launch_bounds__(256) void ce_fused_merge(CeFusedArgs a, float* run_
 
 }  // namespace
 
-bool ce_fused_supported(int64_t H, bool bf16) { return bf16 && H >= kCfBK && H % kCfBK == 0; }
+bool ce_fused_supported(int64_t H, bool bf16) { return bf16 && H >= 64 && H % 64 == 0; }
 
 CeFusedArgs ce_fused_plan(int64_t N, int64_t V, int64_t H) {
     CeFusedArgs f{};
@@ -250,6 +279,23 @@ CeFusedArgs ce_fused_plan(int64_t N, int64_t V, int64_t H) {
     f.tiles_per_range = (f.ntiles_v + ranges - 1) / ranges;
     f.ranges = (f.ntiles_v + f.tiles_per_range - 1) / f.tiles_per_range;  // none empty
     f.nparts = 2 * f.ranges;
+    // The XCD rectangle: each XCD's run (grid / 8 workgroups) split as xbr
+    // ranges x xbp position blocks, xbr + xbp smallest; on a tie fewer
+    // ranges (weight slices, which come from HBM; the hidden rows are small
+    // enough to stay in the last-level cache).  None fits: xbr = 0, range-major.
+    f.xbr = f.xbp = 0;
+    const int grid = f.ranges * f.nb_pos;
+    if (grid % kXcds == 0) {
+        const int run = grid / kXcds;
+        for (int br = 1; br <= std::min(run, f.ranges); ++br) {
+            const int bp = run / br;
+            if (run % br || f.ranges % br || f.nb_pos % bp) continue;
+            if (f.xbr == 0 || br + bp < f.xbr + f.xbp) {
+                f.xbr = br;
+                f.xbp = bp;
+            }
+        }
+    }
     return f;
 }
 
@@ -264,7 +310,8 @@ hipError_t launch_ce_fused_fwd(const CeArgs& a, const CeFusedArgs& plan, const v
     f.S = a.S;
     f.ignore = a.ignore;
     const dim3 grid((unsigned)(f.nb_pos * f.ranges));
-    if (f.N % kCfRows == 0 && f.V % kCfRows == 0)
+    const bool fast = f.N % kCfRows == 0 && f.V % kCfRows == 0;
+    if (fast)
         hipLaunchKernelGGL(ce_fused_fwd<true>, grid, dim3(kCfThreads), 0, st, f);
     else
         hipLaunchKernelGGL(ce_fused_fwd<false>, grid, dim3(kCfThreads), 0, st, f);

@@ -55,6 +55,7 @@ struct CeFusedArgs {
     int64_t N, V, S;
     int H, ignore;
     int nb_pos, ntiles_v, tiles_per_range, ranges, nparts;
+    int xbr, xbp;  // XCD rectangle: ranges x position blocks per XCD run (0: range-major)
 };
 bool ce_fused_supported(int64_t H, bool bf16);
 CeFusedArgs ce_fused_plan(int64_t N, int64_t V, int64_t H);  // the launch geometry (nparts: pairs per position)

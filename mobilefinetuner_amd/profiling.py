@@ -41,6 +41,8 @@ KERNELS = {
     "prologue_fwd_kernel": "prologue_fwd",
     "prologue_bwd_kernel": "prologue_bwd",
     "prologue_dw_reduce": "prologue_dw_reduce",
+    "ce_fused_fwd": "ce_fused_fwd",
+    "ce_fused_merge": "ce_fused_merge",
     "ce_row_stats": "ce_row_stats",
     "ce_grad": "ce_grad",
     "ce_finalize": "ce_finalize",

@@ -96,6 +96,42 @@ def test_streaming_matches_oracle(orc, dev, case):
     assert max(e) <= TOL[dtype], e
 
 
+@pytest.mark.parametrize("shape", [(1, 2048, 256, 32768), (3, 500, 128, 20000), (2, 300, 64, 2999)],
+                         ids=lambda c: "B{}S{}H{}V{}".format(*c))
+def test_fused_forward_placements(orc, dev, shape):
+    """The fused bf16 forward at shapes whose workgroups are placed as XCD
+    rectangles of vocabulary ranges x position blocks (4 x 8 and 5 x 6 here,
+    the second and third with partial position and vocabulary tiles; the third
+    is range-major), against a torch fp32 reference on the same bf16 inputs:
+    LSE of every position and the mean NLL to 1e-5 relative."""
+    import torch
+    from mobilefinetuner_amd import lm_loss as L
+    B, S, H, V = shape
+    print(f"[case] fused forward {shape}", flush=True)
+    g = torch.Generator(device=dev)
+    g.manual_seed(B * S + V)
+    h = (0.5 * torch.randn(B, S, H, device=dev, generator=g)).to(torch.bfloat16)
+    w = (0.2 * torch.randn(V, H, device=dev, generator=g)).to(torch.bfloat16)
+    y = torch.randint(0, V, (B, S), device=dev, generator=g, dtype=torch.int32)
+    y[:, ::7] = -100
+    loss, lse = L.streaming_lm_cross_entropy(h, w, y)
+    z = h.float().reshape(B * S, H) @ w.float().t()
+    ref_lse = torch.logsumexp(z.double(), dim=1).reshape(B, S)
+    nxt = y[:, 1:].reshape(-1).long()
+    keep = nxt != -100
+    zz = z.reshape(B, S, V)[:, :-1].reshape(-1, V)[keep]
+    got = lse[:, :-1].reshape(-1)
+    ref = ref_lse[:, :-1].reshape(-1)
+    nll = ref[keep] - zz.double().gather(1, nxt[keep].unsqueeze(1)).squeeze(1)
+    torch.cuda.synchronize()
+    # the LSE is kept for scored positions; the others hold 0 (as the reference's)
+    e_lse = float(((got[keep].double() - ref[keep]).abs() / ref[keep].abs().clamp_min(1.0)).max())
+    e_loss = abs(float(loss) - float(nll.mean())) / abs(float(nll.mean()))
+    print(f"[errs] lse {e_lse:.2e} loss {e_loss:.2e}", flush=True)
+    assert e_lse <= 1e-5 and e_loss <= 1e-5, (e_lse, e_loss)
+    assert float(got[~keep].abs().max()) == 0.0 and float(lse[:, -1].abs().max()) == 0.0
+
+
 def test_streaming_equals_dense_on_the_gpu(orc, dev):
     """The reference test's check (core/test_selected_token_lm_loss.cpp:98-115):
     streaming loss and gradients equal the dense ones chained through
