@@ -18,12 +18,13 @@
  * NLL with 0 at unscored positions (dense variant only, as in the reference).
  *
  * Conventions are those of mft/attention.h (status codes, mft_last_error,
- * caller-owned device memory, stream ordering).  The streaming forward with
- * bf16 hidden and weight and H a multiple of 64 is one fused kernel (the
- * logits GEMM with the online log-sum-exp in its epilogue; no logits are
- * written).  The streaming backward, and the forward in the other cases, run
- * their vocabulary-chunk GEMMs with rocBLAS on a per-device handle created on
- * first use; the GEMM workspace comes from the caller's workspace.
+ * caller-owned device memory, stream ordering).  With bf16 hidden and weight
+ * and H a multiple of 64 the streaming forward is one fused kernel (the logits
+ * GEMM with the online log-sum-exp in its epilogue; no logits are written),
+ * and the backward's per-chunk G comes from the same kernel (logits
+ * recomputed, G written in bf16).  The backward's two GEMMs per chunk, and the
+ * logits GEMMs in the other cases, run on rocBLAS with a per-device handle
+ * created on first use; the GEMM workspace comes from the caller's workspace.
  *
  * A label outside [0, V) that is not ignore_index makes the reference throw
  * ("lm_cross_entropy: label out of range").  A device cannot throw: the

@@ -10,8 +10,10 @@
 //   backward  Z recomputed, G = (exp(Z - lse) - onehot) * coeff  (input dtype)
 //             grad_hidden += G . W_c,  grad_weight[c] = G^T . hidden
 // so the [N, V] logits never exist at once.  With bf16 operands and H a
-// multiple of 64 the forward runs the fused kernel of lm_loss_fused.hip
-// instead (the GEMM and the row statistics in one pass, no logits at all).
+// multiple of 64 the fused kernels of lm_loss_fused.hip replace the logits
+// GEMM and the passes over it: the forward computes the row statistics in
+// one pass with no logits at all, and the backward writes each chunk's G
+// straight from the recomputed logits (no fp32 chunk).
 #include "mft/lm_loss.h"
 
 #include <string>
@@ -50,8 +52,11 @@ Layout layout(const mft_lm_loss_desc* d, bool streaming) {
     if (streaming) {
         const size_t c = (size_t)chunk_of(d);
         const size_t esz = d->dtype == MFT_BF16 ? 2 : 4;
-        l.z = o, o += up(N * c * 4);
-        l.g = o, o += up(N * c * esz);
+        // the fused kernels need no fp32 logits chunk; their G rows are
+        // padded to a multiple of 8 elements (8-byte stores)
+        const bool fused = mft::ce_fused_supported(d->H, d->dtype == MFT_BF16);
+        l.z = o, o += fused ? 0 : up(N * c * 4);
+        l.g = o, o += up(N * (fused ? (c + 7) / 8 * 8 : c) * esz);
         l.blas = o, o += kBlasWorkspace;
         // fused forward: (max, sum) pairs per position and vocabulary part
         l.part = o, o += up(N * 2 * mft::kCeFusedMaxRanges * sizeof(float2));
@@ -213,19 +218,27 @@ mft_status mft_lm_ce_streaming_bwd(const mft_lm_loss_desc* desc, const void* hid
     auto lock = mft::blas::lock();
     rocblas_handle h;
     if ((r = mft::blas::bind("mft_lm_ce_streaming_bwd", stream, w + l.blas, kBlasWorkspace, &h)) != MFT_OK) return r;
+    const bool fused = mft::ce_fused_supported(H, bf);
+    const int64_t ldg = fused ? (chunk + 7) / 8 * 8 : chunk;
+    mft::CeFusedArgs plan{};
     for (int64_t v0 = 0; v0 < desc->V; v0 += chunk) {
         const int64_t nc = desc->V - v0 < chunk ? desc->V - v0 : chunk;
-        if ((r = logits_chunk(h, desc, hidden, weight, v0, nc, Z)) != MFT_OK) return r;
-        e = mft::launch_ce_grad(a, Z, false, nc, nc, v0, G, bf, nc, stream);
-        if (e != hipSuccess) return hip_status(e, "mft_lm_ce_streaming_bwd launch");
         const char* Wc = static_cast<const char*>(weight) + v0 * H * (bf ? 2 : 4);
+        if (fused) {  // G straight from the recomputed logits, no fp32 chunk
+            if (v0 == 0 || nc != chunk) plan = mft::ce_fused_plan(N, nc, H);
+            e = mft::launch_ce_fused_grad(a, plan, hidden, Wc, v0, G, ldg, stream);
+        } else {
+            if ((r = logits_chunk(h, desc, hidden, weight, v0, nc, Z)) != MFT_OK) return r;
+            e = mft::launch_ce_grad(a, Z, false, nc, nc, v0, G, bf, ldg, stream);
+        }
+        if (e != hipSuccess) return hip_status(e, "mft_lm_ce_streaming_bwd launch");
         // grad_hidden[N, H] (+)= G[N, nc] . W_c[nc, H]
-        if (grad_hidden && (r = mft::blas::gemm_rm("mft_lm_ce_streaming_bwd", h, N, H, nc, 1.f, G, nc, false, Wc, H,
+        if (grad_hidden && (r = mft::blas::gemm_rm("mft_lm_ce_streaming_bwd", h, N, H, nc, 1.f, G, ldg, false, Wc, H,
                                                    false, v0 > 0 ? 1.f : 0.f, grad_hidden, H, bf)) != MFT_OK)
             return r;
         // grad_weight[v0 : v0 + nc, :] = G^T . hidden
-        if (grad_weight && (r = mft::blas::gemm_rm("mft_lm_ce_streaming_bwd", h, nc, H, N, 1.f, G, nc, true, hidden, H,
-                                                   false, 0.f, grad_weight + v0 * H, H, bf)) != MFT_OK)
+        if (grad_weight && (r = mft::blas::gemm_rm("mft_lm_ce_streaming_bwd", h, nc, H, N, 1.f, G, ldg, true, hidden,
+                                                   H, false, 0.f, grad_weight + v0 * H, H, bf)) != MFT_OK)
             return r;
     }
     return MFT_OK;

@@ -1,7 +1,11 @@
-// Streaming LM cross-entropy forward with the logits GEMM and the row
-// statistics fused (bf16 hidden and weight, H a multiple of 64): the [N, V]
-// logits of ops::streaming_lm_cross_entropy (core/lm_loss.cpp:384-481) are
-// never written, not even a vocabulary chunk at a time.
+// Streaming LM cross-entropy with the logits GEMM fused into its consumers
+// (bf16 hidden and weight, H a multiple of 64).  Forward: the row statistics
+// in the GEMM's epilogue, so the [N, V] logits of
+// ops::streaming_lm_cross_entropy (core/lm_loss.cpp:384-481) are never
+// written, not even a vocabulary chunk at a time.  Backward
+// (SelectedTokenLMCrossEntropyBackward, :165-266): the same kernel recomputes
+// a vocabulary chunk's logits and writes G = (exp(z - lse) - onehot) * coeff
+// in bf16 for the chunk's dh and dW GEMMs (grad_tile).
 //
 // A workgroup (8 waves) owns 256 positions and a range of 256-row vocabulary
 // tiles.  Per tile it computes Z^T = W_tile . hidden_tile^T on
@@ -65,8 +69,56 @@ __device__ __forceinline__ void cf_place(const CeFusedArgs& a, int blk, int* ran
     }
 }
 
+// The backward's epilogue of one tile: g = (exp(z - lse) - [v == label]) *
+// coeff for the wave's 128 vocabulary rows (chunk-relative, from vw) and the
+// lane's two positions, stored in bf16 to G[pos, v] (row stride ldg, a
+// multiple of 8 elements).  Registers 4q .. 4q + 3 of an MFMA tile hold four
+// consecutive rows (row_of_reg), so each group is one 8-byte store.  The
+// accumulators are cleared for the next tile.
 template <bool FAST>
-__global__ __launch_bounds__(kCfThreads) void ce_fused_fwd(CeFusedArgs a) {
+__device__ __forceinline__ void grad_tile(const CeFusedArgs& a, f32x16 (&acc)[4][2], int64_t vw, const int64_t* pos,
+                                          const int* y, const float* lse2, const float* coeff, int hh) {
+    // Row bounds as offsets from this half-wave's first row (vw + 4 hh), so
+    // that each register's row is a compile-time value.
+    const int lim = (int)min<int64_t>(a.V - vw, 128) - 4 * hh;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        const bool live = FAST || pos[nt] < a.N;
+        bf16* grow = a.g + (live ? pos[nt] : 0) * a.ldg + vw + 4 * hh;
+        const int64_t yr = (int64_t)y[nt] - vw - 4 * hh;
+        const int yl = yr >= 0 && yr < 128 ? (int)yr : -1;
+        const float c = coeff[nt], ml = -lse2[nt];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int r0 = 32 * mt + 8 * q;  // row of register 4q, less 4 hh
+                bf16x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float x = fast_exp2(fmaf(acc[mt][nt][4 * q + e], kLog2e, ml));
+                    if (yl == r0 + e) x -= 1.0f;
+                    o[e] = (bf16)(c != 0.f ? x * c : 0.f);
+                }
+                if (!live) continue;
+                if (FAST || r0 + 4 <= lim) {
+                    *reinterpret_cast<bf16x4*>(grow + r0) = o;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (r0 + e < lim) grow[r0 + e] = o[e];
+                }
+            }
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) acc[mt][nt] = zero_acc();
+    }
+}
+
+// GRAD = false: the forward (row statistics and target logits).  GRAD =
+// true: the backward's logits recompute for one vocabulary chunk, writing
+// G = (exp(z - lse) - onehot(label)) * coeff in bf16 (ce_grad's arithmetic).
+template <bool FAST, bool GRAD>
+__global__ __launch_bounds__(kCfThreads) void ce_fused_kernel(CeFusedArgs a) {
     // [W tile 0][W tile 1][hidden tile 0][hidden tile 1]
     __shared__ __attribute__((aligned(1024))) bf16 smem[4 * kCfTile];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
@@ -79,15 +131,29 @@ __global__ __launch_bounds__(kCfThreads) void ce_fused_fwd(CeFusedArgs a) {
     const int total = (t1 - t0) * KS;  // pipeline stages of this workgroup (>= 1: ranges are never empty)
 
     // This lane's two positions and their target labels (INT_MIN: none).
+    // GRAD: labels relative to the chunk, the LSE times log2(e), and the
+    // coefficient (0 for a position that scores nothing or whose label is
+    // out of range, as ce_grad).
     int64_t pos[2];
     int y[2];
+    float lse2[2] = {0.f, 0.f}, coeff[2] = {0.f, 0.f};
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         pos[nt] = p0 + 64 * wn + 32 * nt + n;
         y[nt] = INT_MIN;
         if (pos[nt] < a.N && (pos[nt] % a.S) + 1 < a.S) {
             const int lab = a.labels[pos[nt] + 1];
-            if (lab != a.ignore) y[nt] = lab;
+            if constexpr (GRAD) {
+                if (lab != a.ignore && lab >= 0 && lab < a.vall) {
+                    const long long cnt = *a.count;
+                    const float outer = a.grad_loss ? a.grad_loss[0] : 1.f;
+                    coeff[nt] = outer * (a.reduction == CE_MEAN ? (cnt > 0 ? 1.0f / (float)cnt : 0.f) : 1.f);
+                    y[nt] = (int)(lab - a.v0);
+                    lse2[nt] = a.lse_in[pos[nt]] * kLog2e;
+                }
+            } else {
+                if (lab != a.ignore) y[nt] = lab;
+            }
         }
     }
 
@@ -180,6 +246,10 @@ __global__ __launch_bounds__(kCfThreads) void ce_fused_fwd(CeFusedArgs a) {
         ck = 0;
         const int64_t vw = (int64_t)ct * kCfRows + 128 * wv;  // this wave's first vocabulary row
         ++ct;
+        if constexpr (GRAD) {
+            grad_tile<FAST>(a, acc, vw, pos, y, lse2, coeff, hh);
+            continue;
+        }
 
         // The tile's logits are complete: fold them into the running pairs.
         const bool partial_v = vw + 128 > a.V;
@@ -237,6 +307,7 @@ __global__ __launch_bounds__(kCfThreads) void ce_fused_fwd(CeFusedArgs a) {
         }
     }
     wait_vmcnt<0>();
+    if constexpr (GRAD) return;
     // The two half-waves hold the same max and halves of the sum.
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
@@ -312,12 +383,36 @@ hipError_t launch_ce_fused_fwd(const CeArgs& a, const CeFusedArgs& plan, const v
     const dim3 grid((unsigned)(f.nb_pos * f.ranges));
     const bool fast = f.N % kCfRows == 0 && f.V % kCfRows == 0;
     if (fast)
-        hipLaunchKernelGGL(ce_fused_fwd<true>, grid, dim3(kCfThreads), 0, st, f);
+        hipLaunchKernelGGL((ce_fused_kernel<true, false>), grid, dim3(kCfThreads), 0, st, f);
     else
-        hipLaunchKernelGGL(ce_fused_fwd<false>, grid, dim3(kCfThreads), 0, st, f);
+        hipLaunchKernelGGL((ce_fused_kernel<false, false>), grid, dim3(kCfThreads), 0, st, f);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(ce_fused_merge, dim3((unsigned)((f.N + 255) / 256)), dim3(256), 0, st, f, a.run_m, a.run_s);
+    return hipGetLastError();
+}
+
+hipError_t launch_ce_fused_grad(const CeArgs& a, const CeFusedArgs& plan, const void* hidden, const void* weight_chunk,
+                                int64_t v0, void* g, int64_t ldg, hipStream_t st) {
+    CeFusedArgs f = plan;
+    f.hidden = hidden;
+    f.weight = weight_chunk;
+    f.labels = a.labels;
+    f.S = a.S;
+    f.ignore = a.ignore;
+    f.g = static_cast<bf16*>(g);
+    f.ldg = ldg;
+    f.v0 = v0;
+    f.vall = a.V;
+    f.lse_in = a.lse_in;
+    f.count = a.count;
+    f.grad_loss = a.grad_loss;
+    f.reduction = a.reduction;
+    const dim3 grid((unsigned)(f.nb_pos * f.ranges));
+    if (f.N % kCfRows == 0 && f.V % kCfRows == 0)
+        hipLaunchKernelGGL((ce_fused_kernel<true, true>), grid, dim3(kCfThreads), 0, st, f);
+    else
+        hipLaunchKernelGGL((ce_fused_kernel<false, true>), grid, dim3(kCfThreads), 0, st, f);
     return hipGetLastError();
 }
 

@@ -56,10 +56,23 @@ struct CeFusedArgs {
     int H, ignore;
     int nb_pos, ntiles_v, tiles_per_range, ranges, nparts;
     int xbr, xbp;  // XCD rectangle: ranges x position blocks per XCD run (0: range-major)
+    // backward (launch_ce_fused_grad): V above is the chunk's row count
+    __bf16* g;              // [N, ldg] bf16 gradient of the chunk's logits
+    int64_t ldg, v0, vall;  // row stride of g, chunk start, full vocabulary size
+    const float* lse_in;
+    const long long* count;
+    const float* grad_loss;
+    int reduction;
 };
 bool ce_fused_supported(int64_t H, bool bf16);
 CeFusedArgs ce_fused_plan(int64_t N, int64_t V, int64_t H);  // the launch geometry (nparts: pairs per position)
 hipError_t launch_ce_fused_fwd(const CeArgs& a, const CeFusedArgs& plan, const void* hidden, const void* weight,
                                float2* part, hipStream_t st);
+// The backward's logits recompute for vocabulary rows [v0, v0 + plan.V) with
+// G = (exp(z - lse) - onehot) * coeff written in bf16 to g (row stride ldg, a
+// multiple of 8) instead of the logits; plan = ce_fused_plan(N, chunk rows, H),
+// weight_chunk = the chunk's first weight row.  Needs the scored count.
+hipError_t launch_ce_fused_grad(const CeArgs& a, const CeFusedArgs& plan, const void* hidden, const void* weight_chunk,
+                                int64_t v0, void* g, int64_t ldg, hipStream_t st);
 
 }  // namespace mft

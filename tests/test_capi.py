@@ -216,9 +216,12 @@ def test_lm_loss_validation(capi):
     with pytest.raises(capi.MftError) as e:
         capi.lm_ce_fwd(d, None, 16, 16, 16, None, 16, None)
     assert "non-NULL" in str(e.value)
-    # streaming workspace: one fp32 and one input-dtype logits chunk plus the GEMM workspace
+    # streaming workspace, fp32: one fp32 logits chunk and one G chunk plus the GEMM workspace
+    f, b = capi.lm_ce_workspace_size(capi.lm_loss_desc(1, 4096, 262144, 1152, capi.MFT_F32))
+    assert f == b and 4096 * 16384 * 8 < f < 4096 * 16384 * 8 + (80 << 20)
+    # bf16 with H a multiple of 64 (fused kernels): no logits chunk, one bf16 G chunk
     f, b = capi.lm_ce_workspace_size(capi.lm_loss_desc(1, 4096, 262144, 1152, capi.MFT_BF16))
-    assert f == b and 4096 * 16384 * 6 < f < 4096 * 16384 * 6 + (80 << 20)
+    assert f == b and 4096 * 16384 * 2 < f < 4096 * 16384 * 2 + (80 << 20)
 
 
 

@@ -132,6 +132,46 @@ def test_fused_forward_placements(orc, dev, shape):
     assert float(got[~keep].abs().max()) == 0.0 and float(lse[:, -1].abs().max()) == 0.0
 
 
+@pytest.mark.parametrize("shape", [(1, 2048, 256, 32768, 0), (3, 500, 128, 20000, 4999), (2, 300, 64, 2999, 1000)],
+                         ids=lambda c: "B{}S{}H{}V{}-c{}".format(*c))
+def test_fused_backward_placements(orc, dev, shape):
+    """The fused bf16 backward (G from the recomputed logits, then the two
+    GEMMs) at the placement shapes above, with chunks that split V unevenly
+    and rows of G off the 8-element grid, against torch fp32 on the same bf16
+    inputs: max |error| over max |value| of grad_hidden and grad_weight within
+    the bf16 bar (G is rounded to bf16 before the GEMMs, as the reference's
+    bf16 path rounds it)."""
+    import torch
+    from mobilefinetuner_amd import lm_loss as L
+    B, S, H, V, chunk = shape
+    print(f"[case] fused backward {shape}", flush=True)
+    g = torch.Generator(device=dev)
+    g.manual_seed(B * S + V + 1)
+    h = (0.5 * torch.randn(B, S, H, device=dev, generator=g)).to(torch.bfloat16)
+    w = (0.2 * torch.randn(V, H, device=dev, generator=g)).to(torch.bfloat16)
+    y = torch.randint(0, V, (B, S), device=dev, generator=g, dtype=torch.int32)
+    y[:, ::5] = -100
+    loss, lse = L.streaming_lm_cross_entropy(h, w, y, chunk=chunk)
+    gl = torch.full((1,), 0.75, device=dev)
+    gh, gw = L.streaming_lm_cross_entropy_backward(h, w, y, lse, gl, chunk=chunk)
+    hf, wf = h.float().reshape(B * S, H), w.float()
+    z = hf @ wf.t()
+    nxt = torch.full((B, S), -100, dtype=torch.long, device=dev)
+    nxt[:, :-1] = y[:, 1:].long()
+    nxt = nxt.reshape(-1)
+    keep = nxt != -100
+    G = torch.softmax(z, dim=1)
+    G[torch.arange(B * S, device=dev)[keep], nxt[keep]] -= 1.0
+    G = G * keep.unsqueeze(1).float() * (0.75 / float(keep.sum()))
+    ref_h = (G @ wf).reshape(B, S, H)
+    ref_w = G.t().contiguous() @ hf
+    torch.cuda.synchronize()
+    e_h = float((gh - ref_h).abs().max() / ref_h.abs().max())
+    e_w = float((gw - ref_w).abs().max() / ref_w.abs().max())
+    print(f"[errs] gh {e_h:.2e} gw {e_w:.2e}", flush=True)
+    assert e_h <= TOL["bf16"] and e_w <= TOL["bf16"], (e_h, e_w)
+
+
 def test_streaming_equals_dense_on_the_gpu(orc, dev):
     """The reference test's check (core/test_selected_token_lm_loss.cpp:98-115):
     streaming loss and gradients equal the dense ones chained through
