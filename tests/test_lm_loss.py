@@ -213,6 +213,43 @@ def test_all_ignored_and_out_of_range_labels(orc, dev):
         L.streaming_lm_cross_entropy(h, w, y)
 
 
+def test_fused_all_ignored_and_out_of_range_labels(dev):
+    """The same edge cases on the fused bf16 kernels (H a multiple of 64):
+    all labels ignored gives a NaN mean with zero gradients; an out-of-range
+    label raises from the forward, and the backward (which the reference never
+    reaches) leaves that position's gradient row zero and the rest equal to a
+    run where the label is ignored."""
+    import torch
+    from mobilefinetuner_amd import lm_loss as L
+    B, S, H, V = 2, 300, 64, 700
+    g = torch.Generator(device=dev)
+    g.manual_seed(77)
+    h = (0.5 * torch.randn(B, S, H, device=dev, generator=g)).to(torch.bfloat16)
+    w = (0.3 * torch.randn(V, H, device=dev, generator=g)).to(torch.bfloat16)
+    y = torch.full((B, S), -100, dtype=torch.int32, device=dev)
+    loss, lse = L.streaming_lm_cross_entropy(h, w, y)
+    gh, gw = L.streaming_lm_cross_entropy_backward(h, w, y, lse, torch.ones(1, device=dev))
+    torch.cuda.synchronize()
+    assert torch.isnan(loss).all() and torch.count_nonzero(lse) == 0
+    assert torch.count_nonzero(gh) == 0 and torch.count_nonzero(gw) == 0
+    y = torch.randint(0, V, (B, S), device=dev, generator=g, dtype=torch.int32)
+    y_ign = y.clone()
+    y[1, 7] = V + 3
+    y_ign[1, 7] = -100
+    with pytest.raises(ValueError, match="out of range"):
+        L.streaming_lm_cross_entropy(h, w, y)
+    loss_i, lse_i = L.streaming_lm_cross_entropy(h, w, y_ign)
+    one = torch.ones(1, device=dev)
+    # the count of scored positions differs (the out-of-range one is counted
+    # as scored, as the reference's forward would before throwing), so
+    # compare with reduction "sum", where the coefficient is the same
+    gh, gw = L.streaming_lm_cross_entropy_backward(h, w, y, lse_i, one, reduction="sum")
+    gh_i, gw_i = L.streaming_lm_cross_entropy_backward(h, w, y_ign, lse_i, one, reduction="sum")
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(gh[1, 6]) == 0  # position 6 scores label [1, 7]
+    assert torch.equal(gh, gh_i) and torch.equal(gw, gw_i)
+
+
 def test_autograd_node(orc, dev):
     import torch
     from mobilefinetuner_amd import lm_loss as L
