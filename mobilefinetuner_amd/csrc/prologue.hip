@@ -21,7 +21,9 @@
 //   RMSNorm(Affine)Backward core/backward_functions.cpp:510-528, 548-567,
 //                                             in double, as there.
 // cosf/sinf are the device library's (the reference calls the host libm's);
-// both are faithfully rounded, so y agrees to a few ulp.
+// both are faithfully rounded, so y agrees to a few ulp.  The 16-byte-lane
+// forward divides by rms as div_by (one correctly rounded reciprocal per row
+// and a correction step per element), which gives the IEEE quotient.
 //
 // dL/dw: each backward workgroup (4 waves) sums its rows' terms (float,
 // fixed order) into one [D] partial, and a second kernel adds the partials in
@@ -369,6 +371,40 @@ __device__ __forceinline__ RowAddr row_addr_hf(const PrologueArgs& a, int64_t r)
     const int64_t bs = r / a.H;
     return RowAddr{bs / a.S, h, (int)(bs % a.S)};
 }
+// The row after ra in row_addr_hf order (head, then position, then batch).
+__device__ __forceinline__ RowAddr next_row_hf(const PrologueArgs& a, RowAddr ra) {
+    if (++ra.h == a.H) {
+        ra.h = 0;
+        if (++ra.s == a.S) {
+            ra.s = 0;
+            ++ra.b;
+        }
+    }
+    return ra;
+}
+// row_addr_hf of rows r0 .. r0 + G - 1 (r0 < rows): one division pair (32-bit
+// multiply-shift when rows < 2^31) and G - 1 steps.
+template <int G> __device__ __forceinline__ void rows_hf(const PrologueArgs& a, int64_t r0, RowAddr (&ra)[G]) {
+    if (a.rows32) {
+        const uint32_t r = (uint32_t)r0, bs = a.fh.div(r), b = a.fs.div(bs);
+        ra[0] = RowAddr{(int64_t)b, (int64_t)(r - bs * (uint32_t)a.H), (int)(bs - b * (uint32_t)a.S)};
+    } else {
+        ra[0] = row_addr_hf(a, r0);
+    }
+#pragma unroll
+    for (int g = 1; g < G; ++g) ra[g] = next_row_hf(a, ra[g - 1]);
+}
+
+// x / b, correctly rounded, from y = 1 / b (correctly rounded, once per row):
+// q = x y, r = x - q b (exact by an FMA), q + r y rounds to x / b
+// (Markstein's correction step; a 3 * 10^9-case random check against IEEE
+// division, b with all-ones and all-zeros significands included, found no
+// difference).
+__device__ __forceinline__ float div_by(float x, float b, float y) {
+    const float q = x * y;
+    return fmaf(fmaf(-q, b, x), y, q);
+}
+
 // Row groups per lane of the forward (all loaded before any is computed).
 constexpr int kFwdVecGroups = 2;
 
@@ -397,10 +433,10 @@ __device__ __forceinline__ void prologue_fwd_vec_body(const PrologueArgs& a, int
     const int64_t lane_row0 = (blk * 4 + (threadIdx.x >> 6)) * (RPI * GROUPS) + (lane / LPR) * GROUPS;
     float v[GROUPS][2][H2];  // [group][half][element]
     RowAddr ra[GROUPS];
+    rows_hf(a, lane_row0 < a.rows ? lane_row0 : 0, ra);
 #pragma unroll
     for (int g = 0; g < GROUPS; ++g) {
         const int64_t r = lane_row0 + g;
-        ra[g] = row_addr_hf(a, r < a.rows ? r : 0);
         if (r < a.rows) {
             const T* x = (const T*)a.x + a.sx.at(ra[g].b, ra[g].h) + (int64_t)ra[g].s * a.sx.s + q0;
             Vec<T, H2>::load(x, v[g][0]);
@@ -423,12 +459,12 @@ __device__ __forceinline__ void prologue_fwd_vec_body(const PrologueArgs& a, int
                 for (int e = 0; e < H2; ++e) ss += (double)v[g][hf][e] * (double)v[g][hf][e];
             ss = group_sum<LPR>(ss);
             if (a.norm == PROLOGUE_NORM_GEMMA) {
-                const float rms = (float)sqrt(ss / (double)D + (double)a.eps);
+                const float rms = (float)sqrt(ss / (double)D + (double)a.eps), rcp = 1.0f / rms;
 #pragma unroll
                 for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
                     for (int e = 0; e < H2; ++e)
-                        v[g][hf][e] = (v[g][hf][e] / rms) * (1.0f + a.w[hf * HALF + q0 + e]);
+                        v[g][hf][e] = div_by(v[g][hf][e], rms, rcp) * (1.0f + a.w[hf * HALF + q0 + e]);
             } else {
                 const float inv = (float)(1.0 / sqrt(ss / (double)D + (double)a.eps));
 #pragma unroll
@@ -487,11 +523,11 @@ __device__ __forceinline__ void prologue_bwd_vec_body(const PrologueArgs& a, int
     // every row group's loads first; [group][half][element]
     float gv[GROUPS][2][H2], xv[GROUPS][2][H2];
     RowAddr ra[GROUPS];
+    rows_hf(a, lane_row0 < a.rows ? lane_row0 : 0, ra);
 #pragma unroll
     for (int g = 0; g < GROUPS; ++g) {
         const int64_t r = lane_row0 + g;
         const bool live = r < a.rows;
-        ra[g] = row_addr_hf(a, live ? r : 0);
         if (live) {
             const float* dy = a.dy + a.sdy.at(ra[g].b, ra[g].h) + (int64_t)ra[g].s * a.sdy.s + q0;
             Vec<float, H2>::load(dy, gv[g][0]);

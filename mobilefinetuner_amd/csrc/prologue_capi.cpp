@@ -44,6 +44,11 @@ mft_status check(const mft_prologue_desc* d, const char* who, mft::PrologueArgs*
     a->H = d->H;
     a->S = d->S;
     a->rows = d->B * d->H * d->S;
+    a->rows32 = a->rows < (int64_t(1) << 31);
+    if (a->rows32) {
+        a->fh = mft::FastDiv::make((uint32_t)d->H);
+        a->fs = mft::FastDiv::make((uint32_t)d->S);
+    }
     a->D = (int)d->D;
     a->norm = d->norm;
     a->eps = d->eps;

@@ -12,8 +12,27 @@ namespace mft {
 enum { PROLOGUE_NORM_NONE = 0, PROLOGUE_NORM_GEMMA = 1, PROLOGUE_NORM_AFFINE = 2 };
 constexpr int PROLOGUE_MAX_D = 512;
 
+// n / d for 0 <= n < 2^31 as one multiply and a shift.  With l = ceil(log2 d)
+// and m = ceil(2^(31 + l) / d) (below 2^32), floor(n m / 2^(31 + l)) =
+// floor(n / d): n m / 2^(31 + l) = n / d + n e / (d 2^(31 + l)) with
+// e = m d - 2^(31 + l) < d <= 2^l, so the excess is below 1 / d and cannot
+// carry past the next integer.
+struct FastDiv {
+    uint32_t d, m;
+    int sh;
+    static FastDiv make(uint32_t d) {
+        int l = 0;
+        while ((uint64_t(1) << l) < d) ++l;
+        const uint64_t p = uint64_t(1) << (31 + l);
+        return FastDiv{d, (uint32_t)((p + d - 1) / d), 31 + l};
+    }
+    __host__ __device__ uint32_t div(uint32_t n) const { return (uint32_t)(((uint64_t)n * m) >> sh); }
+};
+
 struct PrologueArgs {
     int64_t B, H, S, rows;  // rows = B * H * S
+    FastDiv fh, fs;         // division by H and by S (rows32)
+    int rows32;             // rows < 2^31: 32-bit row addressing
     int D;
     int norm;
     float eps;

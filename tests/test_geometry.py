@@ -48,6 +48,19 @@ def test_lora_coldot_grid_stays_within_launch_limits(tmp_path):
     assert out.returncode == 0 and out.stdout.startswith("ok"), out.stdout + out.stderr
 
 
+def test_prologue_fast_division(tmp_path):
+    """The prologue's 32-bit row addressing divides by H and S with a
+    multiply and a shift (FastDiv); it must equal n / d for every n < 2^31."""
+    exe = tmp_path / "fastdiv_check"
+    subprocess.run(["/opt/rocm/bin/hipcc", "-x", "hip", "--offload-arch=gfx950", "--cuda-host-only", "-O1",
+                    "-std=c++17", "-I", os.path.join(ROOT, "mobilefinetuner_amd", "csrc"),
+                    os.path.join(ROOT, "tests", "native", "fastdiv_check.cpp"), "-o", str(exe)],
+                   check=True, capture_output=True, text=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert out.returncode == 0 and out.stdout.startswith("ok"), out.stdout + out.stderr
+    assert int(out.stdout.split()[1]) > 10_000_000
+
+
 def test_split_plans_stay_within_slot_limit(tmp_path):
     """The forward and backward split planners never give a tile more
     partial slots than the merge kernels hold (kSplitMaxSlots), over a sweep
