@@ -72,24 +72,27 @@ __device__ __forceinline__ void cf_place(const CeFusedArgs& a, int blk, int* ran
 // The backward's epilogue of one tile: g = (exp(z - lse) - [v == label]) *
 // coeff for the wave's 128 vocabulary rows (chunk-relative, from vw) and the
 // lane's two positions, stored in bf16 to G[pos, v] (row stride ldg, a
-// multiple of 8 elements).  Registers 4q .. 4q + 3 of an MFMA tile hold four
-// consecutive rows (row_of_reg), so each group is one 8-byte store.  The
-// accumulators are cleared for the next tile.
+// multiple of 8 elements).  Registers 4q .. 4q + 3 of an MFMA tile hold the
+// four consecutive rows 8q + 4hh ..; one v_permlane32_swap per register pair
+// gives the half-wave hh = 0 rows 16j .. 16j + 7 and hh = 1 rows 16j + 8 ..
+// 16j + 15 (q = 2j, 2j + 1), so each lane stores 16 bytes and a position's 32
+// bytes are contiguous.  The accumulators are cleared for the next tile.
 template <bool FAST>
 __device__ __forceinline__ void grad_tile(const CeFusedArgs& a, f32x16 (&acc)[4][2], int64_t vw, const int64_t* pos,
                                           const int* y, const float* lse2, const float* coeff, int hh) {
-    // Row bounds as offsets from this half-wave's first row (vw + 4 hh), so
-    // that each register's row is a compile-time value.
-    const int lim = (int)min<int64_t>(a.V - vw, 128) - 4 * hh;
+    // Row bound as an offset from this half-wave's first stored row
+    // (vw + 8 hh), so that each group's row is a compile-time value.
+    const int lim = (int)min<int64_t>(a.V - vw, 128) - 8 * hh;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         const bool live = FAST || pos[nt] < a.N;
-        bf16* grow = a.g + (live ? pos[nt] : 0) * a.ldg + vw + 4 * hh;
+        bf16* grow = a.g + (live ? pos[nt] : 0) * a.ldg + vw + 8 * hh;
         const int64_t yr = (int64_t)y[nt] - vw - 4 * hh;
-        const int yl = yr >= 0 && yr < 128 ? (int)yr : -1;
+        const int yl = yr >= 0 && yr < 128 ? (int)yr : -1;  // label row less 4 hh, or none
         const float c = coeff[nt], ml = -lse2[nt];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < 4; ++mt) {
+            uint32_t pk[4][2];  // [q][pair]: bf16 pairs of rows 8q + 4hh + 0..3
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int r0 = 32 * mt + 8 * q;  // row of register 4q, less 4 hh
@@ -100,15 +103,31 @@ __device__ __forceinline__ void grad_tile(const CeFusedArgs& a, f32x16 (&acc)[4]
                     if (yl == r0 + e) x -= 1.0f;
                     o[e] = (bf16)(c != 0.f ? x * c : 0.f);
                 }
-                if (!live) continue;
-                if (FAST || r0 + 4 <= lim) {
-                    *reinterpret_cast<bf16x4*>(grow + r0) = o;
-                } else {
+                const uint2 u = __builtin_bit_cast(uint2, o);
+                pk[q][0] = u.x;
+                pk[q][1] = u.y;
+            }
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (r0 + e < lim) grow[r0 + e] = o[e];
+            for (int j = 0; j < 2; ++j) {
+                uint4 o8;
+                const auto s0 = __builtin_amdgcn_permlane32_swap(pk[2 * j][0], pk[2 * j + 1][0], false, false);
+                const auto s1 = __builtin_amdgcn_permlane32_swap(pk[2 * j][1], pk[2 * j + 1][1], false, false);
+                o8.x = s0[0];
+                o8.y = s1[0];
+                o8.z = s0[1];
+                o8.w = s1[1];
+                if (!live) continue;
+                const int r0 = 32 * mt + 16 * j;  // first stored row, less 8 hh
+                if (FAST || r0 + 8 <= lim) {
+                    *reinterpret_cast<uint4*>(grow + r0) = o8;
+                } else {
+                    const bf16x8 v8 = __builtin_bit_cast(bf16x8, o8);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (r0 + e < lim) grow[r0 + e] = v8[e];
                 }
             }
+        }
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) acc[mt][nt] = zero_acc();
     }
