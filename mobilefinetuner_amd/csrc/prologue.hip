@@ -3,11 +3,13 @@
 //
 // Two lane layouts.  Head dims 128, 256 and 512 with 16-byte-aligned rows take
 // the 16-byte-lane kernels (prologue_*_vec below): a row spans D*size/16
-// lanes and a RoPE pair's partner value arrives by shuffle.  Other head dims
-// and unaligned rows take one wave per row (b, h, s), each wave RPW rows with
-// all loads issued first; a RoPE pair (p, p + D/2) never leaves its lane:
-// lane l owns the elements p = (l + 64 j) * V + e (j < NJ, e < V) of each
-// half.  The row's sum of squares is a shuffle reduction either way.
+// lanes, each holding elements of the first half and their rotate-half
+// partners.  Other head dims and unaligned rows take one wave per row
+// (b, h, s), each wave RPW rows with all loads issued first; lane l owns the
+// elements p = (l + 64 j) * V + e (j < NJ, e < V) of each half.  Either way a
+// RoPE pair (p, p + D/2) never leaves its lane.  The row's sum of squares is
+// a shuffle reduction in the one-wave kernels (wave_sum) and an in-register
+// DPP / permlane reduction in the 16-byte-lane kernels (group_sum).
 //
 // Arithmetic follows the reference operators step for step, without fused
 // multiply-adds (fp contract off):
@@ -356,12 +358,12 @@ __device__ __forceinline__ void prologue_dw_reduce(const float* part, int64_t np
 }
 
 // ---------------------------------------------------------------------------
-// 16-byte lanes (head dims 128, 256, 512): a row is LPR = D * sizeof / 16
-// consecutive lanes, each holding EPL contiguous elements, so every global
-// access is a 16-byte vector.  The first LPR/2 lanes of a row hold the first
-// half; a RoPE pair's partner element sits in lane ^ (LPR/2) at the same
-// slot and comes over by a shuffle.  Row sums are shuffles inside the row's
-// LPR-lane group.  Same arithmetic as the kernels above, element by element.
+// 16-byte lanes (head dims 128, 256, 512): a row is LPR consecutive lanes,
+// each holding EPL / 2 contiguous elements of each half (a 16-byte vector
+// per half in the forward), so every global access is a vector and a RoPE
+// pair stays in its lane.  Row sums are reductions inside the row's LPR-lane
+// group (group_sum).  Same arithmetic as the kernels above, element by
+// element, up to the order of the row sums' additions.
 
 // Row order of the 16-byte-lane kernels: head fastest, r -> (b, s, h) with
 // h = r % H, so that a lane's consecutive row groups are heads of one
@@ -408,9 +410,41 @@ __device__ __forceinline__ float div_by(float x, float b, float y) {
 // Row groups per lane of the forward (all loaded before any is computed).
 constexpr int kFwdVecGroups = 2;
 
+// Sum of v over each aligned group of LPR lanes (2 .. 64), the same value in
+// every lane of the group, by in-register exchanges (no LDS): DPP quad
+// permutes for lanes i ^ 1 and i ^ 2, then half-row and row mirrors (the other
+// quad of each 8, the other 8 of each 16: once a quad, or an 8, holds one
+// value, pairing with the mirror lane sums the same halves as i ^ 4 or i ^ 8),
+// and v_permlane16_swap / v_permlane32_swap for the other row of each 32 and
+// the other half-wave.  Each step adds two equal-rank partial sums, so every
+// lane of the group adds the same two values.
+template <int CTRL> __device__ __forceinline__ double dpp_d(double v) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_mov_dpp((int)b, CTRL, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_mov_dpp((int)(b >> 32), CTRL, 0xF, 0xF, false);
+    return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+}
+template <int ROWS> __device__ __forceinline__ double swap_sum(double v) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+    const unsigned lo = (unsigned)b, hi = (unsigned)(b >> 32);
+    // (first, second) after the swap: (x of this row, x of the paired row)
+    // in every lane of the pair, so first + second is the same in both
+    const auto l = ROWS == 16 ? __builtin_amdgcn_permlane16_swap(lo, lo, false, false)
+                              : __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto h = ROWS == 16 ? __builtin_amdgcn_permlane16_swap(hi, hi, false, false)
+                              : __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    const double a = __longlong_as_double((long long)(((unsigned long long)h[0] << 32) | l[0]));
+    const double c = __longlong_as_double((long long)(((unsigned long long)h[1] << 32) | l[1]));
+    return a + c;
+}
 template <int LPR> __device__ __forceinline__ double group_sum(double v) {
-#pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    static_assert(LPR >= 2 && LPR <= 64 && (LPR & (LPR - 1)) == 0, "groups of 2 .. 64 lanes");
+    v += dpp_d<0xB1>(v);                          // quad_perm [1,0,3,2]: lane i ^ 1
+    if constexpr (LPR >= 4) v += dpp_d<0x4E>(v);  // quad_perm [2,3,0,1]: lane i ^ 2
+    if constexpr (LPR >= 8) v += dpp_d<0x141>(v);  // row_half_mirror
+    if constexpr (LPR >= 16) v += dpp_d<0x140>(v); // row_mirror
+    if constexpr (LPR >= 32) v = swap_sum<16>(v);
+    if constexpr (LPR >= 64) v = swap_sum<32>(v);
     return v;
 }
 
