@@ -124,7 +124,28 @@ __device__ __forceinline__ void store4(T* __restrict__ row, int d0, int D, float
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-__device__ __forceinline__ float other_half(float x) { return __shfl_xor(x, 32); }
+// Max and sum of x over the lane pairs (i, i ^ 32) and (i, i ^ 16), the same
+// value in both lanes of a pair, in registers: v_permlane32_swap(x, x) gives
+// (x of lane i & 31, x of lane (i & 31) + 32) in every lane, and
+// v_permlane16_swap(x, x) the same for rows 2k and 2k + 1 of 16 lanes.  Both
+// lanes add the two values in one order, which is also the bits of
+// x + shfl_xor(x, 32) (addition commutes).  All lanes must be active.
+__device__ __forceinline__ float half_max(float x) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+__device__ __forceinline__ float half_sum(float x) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+__device__ __forceinline__ float row16_max(float x) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+__device__ __forceinline__ float row16_sum(float x) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
 
 // Keys visible to query row i: [lo(i), hi(i)], the reference's additive masks
 // (-1e10 entries, core/ops.cpp:2167-2180 and the Gemma sliding / padding masks

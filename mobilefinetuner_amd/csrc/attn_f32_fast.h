@@ -274,8 +274,7 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_split(FwdArgs a) {
                         st[kb][r] = x;
                         mx = fmaxf(mx, x);
                     }
-                mx = fmaxf(mx, __shfl_xor(mx, 16));
-                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                mx = half_max(row16_max(mx));
                 // Lazy rescaling (as the bf16 kernels): the reference point
                 // m_run moves, and O and l are rescaled, only when some row
                 // of the wave sees a max above m_run + 8, so exp2 arguments
@@ -331,8 +330,7 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_split(FwdArgs a) {
         // this unit's partial (unnormalised O, running max, sum).
         const bool more = i < niter;
         const int nsl = tile_units(tiles, a.us, qt);
-        float l_tot = l_run + __shfl_xor(l_run, 16);
-        l_tot += __shfl_xor(l_tot, 32);
+        const float l_tot = half_sum(row16_sum(l_run));
         if (row < S) {
             if (nsl <= 1) {
                 const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;

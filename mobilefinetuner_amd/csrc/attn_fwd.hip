@@ -175,7 +175,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
                 mx = fmaxf(mx, x);
             }
         }
-        mx = fmaxf(mx, other_half(mx));
+        mx = half_max(mx);
         // log2 units (MASK: natural units, scaled into the exponent below)
         const float m_new = fmaxf(m_run, MASK ? mx : mx * a.scale_log2);
         const float m_use = m_new == -INFINITY ? 0.f : m_new;
@@ -229,7 +229,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(FwdArgs a) {
     }
 
     if (wrow0 >= S) return;
-    const float l_tot = l_run + other_half(l_run);
+    const float l_tot = half_sum(l_run);
     if (row >= S) return;
     // A row that sees no key at all (key padding) gets O = 0 and LSE = +inf
     // here; attn_fwd_masked_rows then writes the reference's output for it.

@@ -197,7 +197,7 @@ __device__ __forceinline__ void fwd_tile(const FwdArgs& a, const char* smem, con
     for (int kk = 0; kk < NKK; ++kk)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kk][r]);
-    mx = fmaxf(mx, other_half(mx)) * a.scale_log2;
+    mx = half_max(mx) * a.scale_log2;
     // Lazy rescaling: the reference point m_run only moves (and O, l are
     // rescaled) when some row of the wave sees a max above m_run + 8, so
     // exp2 arguments stay <= 8 and P <= 256.  Any reference point gives
@@ -375,7 +375,7 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_fast(FwdArgs a) {
     wait_vmcnt<0>();
 
     if (wrow0 >= S) return;
-    const float l_tot = l_run + other_half(l_run);
+    const float l_tot = half_sum(l_run);
     if (row >= S) return;
     fwd_store_row<DP>(a, b, h, row, oacc, m_run, l_tot);
 }
@@ -497,7 +497,7 @@ __global__ __launch_bounds__(256) void attn_fwd_bf16_split(FwdArgs a) {
         // wave whose first row is in range (rows of a wave are all in range
         // or all out of range when FAST).
         if (wrow0 < S) {
-            const float l_tot = l_run + other_half(l_run);
+            const float l_tot = half_sum(l_run);
             if (nsl <= 1) {
                 if (row < S) fwd_store_row<DP>(a, b, h, row, oacc, m_run, l_tot);
             } else if (row < S) {

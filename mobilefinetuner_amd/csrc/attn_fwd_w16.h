@@ -143,8 +143,7 @@ __device__ __forceinline__ void fwd16_pv(const FwdArgs& a, const char* vb_, cons
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kb][i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32)) * a.scale_log2;
+    mx = half_max(row16_max(mx)) * a.scale_log2;
     // Lazy rescaling as in fwd_tile: the reference point moves (and O, l
     // are rescaled) only when some row's tile max exceeds it by 8.
     if (__any(mx > m_run + kLazyRescale)) {
@@ -330,8 +329,7 @@ __global__ __launch_bounds__(kW16Threads) void attn_fwd_bf16_split16(FwdArgs a) 
             load_q(qt);
         }
         if (wave_uniform(wrow0 < S)) {
-            float l_tot = l_run + __shfl_xor(l_run, 16);
-            l_tot += __shfl_xor(l_tot, 32);
+            const float l_tot = half_sum(row16_sum(l_run));
             if (nsl <= 1) {
                 fwd16_store_row<DP>(a, b, h, row, oacc, m_run, l_tot);
             } else {

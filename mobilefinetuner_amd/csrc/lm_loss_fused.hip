@@ -290,7 +290,7 @@ __global__ __launch_bounds__(kCfThreads) void ce_fused_kernel(CeFusedArgs a) {
             for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) mx = fmaxf(mx, acc[mt][nt][r]);
-            mx = fmaxf(mx, other_half(mx));
+            mx = half_max(mx);
             // the target logit, when this lane holds it
             const int64_t rel = (int64_t)y[nt] - vw;
             if (rel >= 0 && rel < 128) {
@@ -330,7 +330,7 @@ __global__ __launch_bounds__(kCfThreads) void ce_fused_kernel(CeFusedArgs a) {
     // The two half-waves hold the same max and halves of the sum.
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-        const float s = s_run[nt] + other_half(s_run[nt]);
+        const float s = half_sum(s_run[nt]);
         if (hh == 0 && pos[nt] < a.N)
             a.part[pos[nt] * a.nparts + 2 * range + wv] = make_float2(m_run[nt], s);
     }
