@@ -133,11 +133,69 @@ __device__ __forceinline__ void grad_tile(const CeFusedArgs& a, f32x16 (&acc)[4]
     }
 }
 
-// GRAD = false: the forward (row statistics and target logits).  GRAD =
-// true: the backward's logits recompute for one vocabulary chunk, writing
-// G = (exp(z - lse) - onehot(label)) * coeff in bf16 (ce_grad's arithmetic).
-template <bool FAST, bool GRAD>
+enum { kCeFwd = 0, kCeGrad = 1, kLoraFwd = 2 };
+
+// The LoRA forward's epilogue of one tile: the rank-r update accumulated
+// onto the GEMM's tile by v_mfma_f32_32x32x2_f32 (fp32 operands: lane (n, hh)
+// gives B(row 32 mt + n, k) * scale and u(position 32 nt + n, k) for k = 2 kk
+// + hh; the 32 x 32 output layout is the bf16 product's), then the bias, and
+// y stored 16 bytes per register group (four consecutive output columns of
+// one position).  Rows past out and positions past N are neither read nor
+// stored.  The accumulators are cleared for the next tile.
+template <bool FAST>
+__device__ __forceinline__ void lora_tile(const CeFusedArgs& a, f32x16 (&acc)[4][2], int64_t vw, const int64_t* pos,
+                                          int hh, int n) {
+    const int ksteps = (a.rank + 1) / 2;
+    for (int kk = 0; kk < ksteps; ++kk) {
+        const int k = 2 * kk + hh;
+        float ub[2], bb[4];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+            ub[nt] = (k < a.rank && (FAST || pos[nt] < a.N)) ? a.u[pos[nt] * a.ldu + k] : 0.f;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            const int64_t row = vw + 32 * mt + n;
+            bb[mt] = (k < a.rank && (FAST || row < a.V)) ? a.lb[row * a.lb_so + k * a.lb_sk] * a.scale : 0.f;
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = mfma_f32(bb[mt], ub[nt], acc[mt][nt]);
+    }
+    const int lim = (int)min<int64_t>(a.V - vw, 128) - 4 * hh;  // rows left, less this half-wave's offset
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        const bool live = FAST || pos[nt] < a.N;
+        float* yrow = a.y + (live ? pos[nt] : 0) * a.ldy + vw + 4 * hh;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int r0 = 32 * mt + 8 * q;  // row of register 4q, less 4 hh
+                f32x4 o{acc[mt][nt][4 * q], acc[mt][nt][4 * q + 1], acc[mt][nt][4 * q + 2], acc[mt][nt][4 * q + 3]};
+                if (!live) continue;
+                if (FAST || r0 + 4 <= lim) {
+                    if (a.bias) o += *reinterpret_cast<const f32x4*>(a.bias + vw + 4 * hh + r0);
+                    *reinterpret_cast<f32x4*>(yrow + r0) = o;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (r0 + e < lim) yrow[r0 + e] = o[e] + (a.bias ? a.bias[vw + 4 * hh + r0 + e] : 0.f);
+                }
+            }
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) acc[mt][nt] = zero_acc();
+    }
+}
+
+// MODE kCeFwd: the forward (row statistics and target logits).  kCeGrad: the
+// backward's logits recompute for one vocabulary chunk, writing G =
+// (exp(z - lse) - onehot(label)) * coeff in bf16 (ce_grad's arithmetic).
+// kLoraFwd: the LoRA layer's forward, y = x W^T + scale u B^T + bias
+// (lora_tile), W in the vocabulary's place and x in the positions'.
+template <bool FAST, int MODE>
 __global__ __launch_bounds__(kCfThreads) void ce_fused_kernel(CeFusedArgs a) {
+    constexpr bool GRAD = MODE == kCeGrad, LORA = MODE == kLoraFwd;
     // [W tile 0][W tile 1][hidden tile 0][hidden tile 1]
     __shared__ __attribute__((aligned(1024))) bf16 smem[4 * kCfTile];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 31, hh = lane >> 5;
@@ -160,7 +218,7 @@ __global__ __launch_bounds__(kCfThreads) void ce_fused_kernel(CeFusedArgs a) {
     for (int nt = 0; nt < 2; ++nt) {
         pos[nt] = p0 + 64 * wn + 32 * nt + n;
         y[nt] = INT_MIN;
-        if (pos[nt] < a.N && (pos[nt] % a.S) + 1 < a.S) {
+        if (!LORA && pos[nt] < a.N && (pos[nt] % a.S) + 1 < a.S) {
             const int lab = a.labels[pos[nt] + 1];
             if constexpr (GRAD) {
                 if (lab != a.ignore && lab >= 0 && lab < a.vall) {
@@ -269,6 +327,10 @@ __global__ __launch_bounds__(kCfThreads) void ce_fused_kernel(CeFusedArgs a) {
             grad_tile<FAST>(a, acc, vw, pos, y, lse2, coeff, hh);
             continue;
         }
+        if constexpr (LORA) {
+            lora_tile<FAST>(a, acc, vw, pos, hh, n);
+            continue;
+        }
 
         // The tile's logits are complete: fold them into the running pairs.
         const bool partial_v = vw + 128 > a.V;
@@ -326,7 +388,7 @@ __global__ __launch_bounds__(kCfThreads) void ce_fused_kernel(CeFusedArgs a) {
         }
     }
     wait_vmcnt<0>();
-    if constexpr (GRAD) return;
+    if constexpr (GRAD || LORA) return;
     // The two half-waves hold the same max and halves of the sum.
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
@@ -402,9 +464,9 @@ hipError_t launch_ce_fused_fwd(const CeArgs& a, const CeFusedArgs& plan, const v
     const dim3 grid((unsigned)(f.nb_pos * f.ranges));
     const bool fast = f.N % kCfRows == 0 && f.V % kCfRows == 0;
     if (fast)
-        hipLaunchKernelGGL((ce_fused_kernel<true, false>), grid, dim3(kCfThreads), 0, st, f);
+        hipLaunchKernelGGL((ce_fused_kernel<true, kCeFwd>), grid, dim3(kCfThreads), 0, st, f);
     else
-        hipLaunchKernelGGL((ce_fused_kernel<false, false>), grid, dim3(kCfThreads), 0, st, f);
+        hipLaunchKernelGGL((ce_fused_kernel<false, kCeFwd>), grid, dim3(kCfThreads), 0, st, f);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(ce_fused_merge, dim3((unsigned)((f.N + 255) / 256)), dim3(256), 0, st, f, a.run_m, a.run_s);
@@ -429,9 +491,18 @@ hipError_t launch_ce_fused_grad(const CeArgs& a, const CeFusedArgs& plan, const 
     f.reduction = a.reduction;
     const dim3 grid((unsigned)(f.nb_pos * f.ranges));
     if (f.N % kCfRows == 0 && f.V % kCfRows == 0)
-        hipLaunchKernelGGL((ce_fused_kernel<true, true>), grid, dim3(kCfThreads), 0, st, f);
+        hipLaunchKernelGGL((ce_fused_kernel<true, kCeGrad>), grid, dim3(kCfThreads), 0, st, f);
     else
-        hipLaunchKernelGGL((ce_fused_kernel<false, true>), grid, dim3(kCfThreads), 0, st, f);
+        hipLaunchKernelGGL((ce_fused_kernel<false, kCeGrad>), grid, dim3(kCfThreads), 0, st, f);
+    return hipGetLastError();
+}
+
+hipError_t launch_lora_fused_fwd(const CeFusedArgs& f, hipStream_t st) {
+    const dim3 grid((unsigned)(f.nb_pos * f.ranges));
+    if (f.N % kCfRows == 0 && f.V % kCfRows == 0)
+        hipLaunchKernelGGL((ce_fused_kernel<true, kLoraFwd>), grid, dim3(kCfThreads), 0, st, f);
+    else
+        hipLaunchKernelGGL((ce_fused_kernel<false, kLoraFwd>), grid, dim3(kCfThreads), 0, st, f);
     return hipGetLastError();
 }
 

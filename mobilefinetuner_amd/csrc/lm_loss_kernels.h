@@ -63,6 +63,16 @@ struct CeFusedArgs {
     const long long* count;
     const float* grad_loss;
     int reduction;
+    // LoRA forward (launch_lora_fused_fwd): weight = W [out, in] (V = out,
+    // H = in), hidden = x in bf16 [N, in]; y[n, o] = (x W^T)[n, o] +
+    // scale * sum_k u[n, k] B(o, k) (+ bias[o]), B(o, k) = lb[o * lb_so + k * lb_sk]
+    float* y;
+    int64_t ldy, ldu, lb_so, lb_sk;
+    const float* bias;
+    const float* u;
+    const float* lb;
+    int rank;
+    float scale;
 };
 bool ce_fused_supported(int64_t H, bool bf16);
 CeFusedArgs ce_fused_plan(int64_t N, int64_t V, int64_t H);  // the launch geometry (nparts: pairs per position)
@@ -74,5 +84,12 @@ hipError_t launch_ce_fused_fwd(const CeArgs& a, const CeFusedArgs& plan, const v
 // weight_chunk = the chunk's first weight row.  Needs the scored count.
 hipError_t launch_ce_fused_grad(const CeArgs& a, const CeFusedArgs& plan, const void* hidden, const void* weight_chunk,
                                 int64_t v0, void* g, int64_t ldg, hipStream_t st);
+
+// The same GEMM as the LoRA layer's forward (bf16 x and W [out, in], in a
+// multiple of 64) with the rank-r update and the bias in its epilogue: one
+// pass writes y.  plan = ce_fused_plan(N, out, in) with the LoRA fields set;
+// rank <= kLoraFusedMaxRank.
+constexpr int kLoraFusedMaxRank = 32;
+hipError_t launch_lora_fused_fwd(const CeFusedArgs& plan, hipStream_t st);
 
 }  // namespace mft

@@ -4,6 +4,11 @@
 // sum of the slices' ranks, s_i = scale_i:
 //   forward   y  = x . W (+ bias)                 rocBLAS; bf16 W: x staged
 //                                                  to bf16 by the first rowdot
+//                                                  (bf16 W [out, in] with one
+//                                                  full-width slice and a large
+//                                                  output: one fused kernel for
+//                                                  this line and the s_i u_i B_i
+//                                                  line, lora_fused_fwd_ok)
 //             u_i = x . A_i                        lora_rowdot, into u[:, ro_i ..]
 //             y[:, col0_i ..] += s_i u_i . B_i     rocBLAS fp32, beta = 1
 //   backward  g_i = s_i dy[:, col0_i ..] . B_i^T   lora_rowdot (workspace [N, R])
@@ -23,8 +28,10 @@
 #include <cmath>
 #include <string>
 
+#include "attn_kernels.h"
 #include "blas_util.h"
 #include "capi_util.h"
+#include "lm_loss_kernels.h"
 #include "lora_kernels.h"
 
 namespace {
@@ -160,6 +167,22 @@ WOperand w_for_backward(const mft_lora_desc* d) {
     return d->w_transposed ? WOperand{d->in_dim, false} : WOperand{d->out_dim, true};
 }
 
+// The forward as one fused kernel (launch_lora_fused_fwd: the bf16 GEMM with
+// the rank-r update and the bias in its epilogue) when W is bf16 [out, in]
+// with in a multiple of 64, there is at most one slice and it spans every
+// column with rank <= kLoraFusedMaxRank, and the 256 x 256 output tiles fill
+// the GPU (smaller outputs stay on the library GEMM, which splits K).
+bool lora_fused_fwd_ok(const mft_lora_desc* d, mft::CeFusedArgs* plan) {
+    if (d->w_dtype != MFT_BF16 || !d->w_transposed || !mft::ce_fused_supported(d->in_dim, true)) return false;
+    if (d->n_slices > 1) return false;
+    if (d->n_slices == 1) {
+        const mft_lora_slice& s = d->slices[0];
+        if (s.col0 != 0 || s.cols != d->out_dim || s.rank > mft::kLoraFusedMaxRank) return false;
+    }
+    *plan = mft::ce_fused_plan(d->N, d->out_dim, d->in_dim);
+    return (int64_t)plan->nb_pos * plan->ntiles_v >= mft::device_cus();
+}
+
 }  // namespace
 
 extern "C" {
@@ -185,8 +208,10 @@ mft_status mft_lora_fwd(const mft_lora_desc* desc, const float* x, const void* W
     const bool bf = desc->w_dtype == MFT_BF16;
     if (!u) u = reinterpret_cast<float*>(ws + l.u);
 
+    mft::CeFusedArgs plan{};
+    const bool fused = lora_fused_fwd_ok(desc, &plan);
     hipError_t e = hipSuccess;
-    if (bias) e = mft::launch_lora_fill_bias(y, bias, N, out, stream);
+    if (bias && !fused) e = mft::launch_lora_fill_bias(y, bias, N, out, stream);
     // bf16 W: the GEMM reads x rounded to bf16, written by the first slice's
     // rowdot (one read of x) or, without slices, by lora_round_bf16.
     uint16_t* xb = bf ? reinterpret_cast<uint16_t*>(ws + l.xb) : nullptr;
@@ -201,6 +226,26 @@ mft_status mft_lora_fwd(const mft_lora_desc* desc, const float* x, const void* W
                         i == 0 ? xb : nullptr)) != MFT_OK)
             return r;
         ro += s.rank;
+    }
+
+    if (fused) {
+        plan.hidden = xb;
+        plan.weight = W;
+        plan.S = 1;
+        plan.y = y;
+        plan.ldy = out;
+        plan.bias = bias;
+        plan.u = u;
+        plan.ldu = R;
+        if (desc->n_slices == 1) {
+            const mft_lora_slice& s = desc->slices[0];
+            plan.lb = s.B;  // B(o, k): [rank, cols] or, transposed, [cols, rank]
+            plan.lb_so = s.b_transposed ? s.rank : 1;
+            plan.lb_sk = s.b_transposed ? 1 : s.cols;
+            plan.rank = (int)s.rank;
+            plan.scale = s.scale;
+        }
+        return hip_status(mft::launch_lora_fused_fwd(plan, stream), "mft_lora_fwd launch");
     }
 
     auto lock = mft::blas::lock();

@@ -41,10 +41,14 @@ KERNELS = {
     "prologue_fwd_kernel": "prologue_fwd",
     "prologue_bwd_kernel": "prologue_bwd",
     "prologue_dw_reduce": "prologue_dw_reduce",
-    "ce_fused_kernel<true, true>": "ce_fused_grad",
-    "ce_fused_kernel<false, true>": "ce_fused_grad",
-    "ce_fused_kernelILb1ELb1E": "ce_fused_grad",
-    "ce_fused_kernelILb0ELb1E": "ce_fused_grad",
+    "ce_fused_kernel<true, 1>": "ce_fused_grad",
+    "ce_fused_kernel<false, 1>": "ce_fused_grad",
+    "ce_fused_kernelILb1ELi1E": "ce_fused_grad",
+    "ce_fused_kernelILb0ELi1E": "ce_fused_grad",
+    "ce_fused_kernel<true, 2>": "lora_fused_fwd",
+    "ce_fused_kernel<false, 2>": "lora_fused_fwd",
+    "ce_fused_kernelILb1ELi2E": "lora_fused_fwd",
+    "ce_fused_kernelILb0ELi2E": "lora_fused_fwd",
     "ce_fused_kernel": "ce_fused_fwd",
     "ce_fused_merge": "ce_fused_merge",
     "ce_row_stats": "ce_row_stats",

@@ -91,6 +91,12 @@ CASES = [
     (45, 35, 50, False, True, False, [(3, 1.5, 0, 50, False, False)], False),
     # bf16 W whose only slice is a column range without gradients (dy staged by lora_round_bf16)
     (64, 128, 96, False, True, True, [(4, 1.0, 32, 32, False, False)], False),
+    # bf16 W [out, in] with outputs large enough for the fused forward (GEMM, rank-r update and
+    # bias in one kernel): whole tiles; partial position and output tiles with B [rank, cols]
+    # and rank 16; and a plain layer (no slice) with a bias
+    (1024, 64, 16384, True, True, True, [(8, 2.0, 0, 16384, True, True)], False),
+    (1000, 128, 16500, True, True, False, [(16, 0.5, 0, 16500, False, False)], False),
+    (1024, 64, 16384, True, True, True, [], False),
 ]
 
 
