@@ -5,7 +5,10 @@
 // written, not even a vocabulary chunk at a time.  Backward
 // (SelectedTokenLMCrossEntropyBackward, :165-266): the same kernel recomputes
 // a vocabulary chunk's logits and writes G = (exp(z - lse) - onehot) * coeff
-// in bf16 for the chunk's dh and dW GEMMs (grad_tile).
+// in bf16 for the chunk's dh and dW GEMMs (grad_tile).  The LoRA layer's
+// forward (nn/lora_linear.cpp:336-444) runs the same GEMM with W in the
+// vocabulary's place and x in the positions', its rank-r update and bias in
+// the epilogue (lora_tile).
 //
 // A workgroup (8 waves) owns 256 positions and a range of 256-row vocabulary
 // tiles.  Per tile it computes Z^T = W_tile . hidden_tile^T on
