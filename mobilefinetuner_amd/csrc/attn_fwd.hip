@@ -411,8 +411,8 @@ FwdPlan plan_fwd_split(const AttnShape& s) {
     // slots or more run one workgroup per query tile: with S <= 1024 the
     // longest tile is at most 16 key tiles, and the split's partial stores
     // and combine launch cost more than its shorter units save (C4: forward
-    // 32.5 against 34.5 us; C3 at S = 2048 measured 50.2 against 41.3, so it
-    // stays split).
+    // 32.5 against 34.5 us; C3 at S = 2048 measured 50.2 against 41.3, and
+    // the fp32 fast path at C2 63.5 against 41.0, so those stay split).
     if (p.balanced && s.bf16 && s.S <= 1024) {
         const int64_t tiles = s.B * s.Hq * ((s.S + kFwdBM - 1) / kFwdBM), slots = fwd_unit_slots(s);
         if (2 * tiles >= slots && tiles <= slots) p.balanced = false;
