@@ -95,7 +95,10 @@ int main() {
                             return 1;
                         }
                         const int G = sh[1] / sh[2], Wv = (int)s.window, Si = (int)S;
-                        if (!check_split(mft::FastTiles{Si, causal, Wv, G, 0}, f.us, "fwd", mft::kMinFwdUnitIters) ||
+                        // a forward planned without the balanced launch (one
+                        // workgroup per query tile) has no unit split to check
+                        if ((f.balanced &&
+                             !check_split(mft::FastTiles{Si, causal, Wv, G, 0}, f.us, "fwd", mft::kMinFwdUnitIters)) ||
                             !check_split(mft::FastTiles{Si, causal, Wv, G, 1}, b.kv, "kv", mft::kMinUnitIters) ||
                             !check_split(mft::FastTiles{Si, causal, Wv, G, 0}, b.q, "q", mft::kMinUnitIters)) {
                             std::printf("  at S=%lld B=%d Hq=%d Hkv=%d D=%d causal=%d W=%d\n", S, sh[0], sh[1],
