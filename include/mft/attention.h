@@ -137,7 +137,9 @@ typedef struct {
 /* Workspace bytes of the calls.
  *   fwd: fp32 partial output tiles of query tiles whose key range is split
  *        across work units (the fast paths: bf16 with D % 8 == 0 and fp32
- *        with D % 4 == 0, 32 < D <= 256; 0 for the others).  The forward also
+ *        with D % 4 == 0, 32 < D <= 256; 0 for the others, and for bf16
+ *        shapes with S <= 1024 whose query tiles alone fill half the GPU or
+ *        more, which run one workgroup per query tile).  The forward also
  *        accepts workspace = NULL and then runs one workgroup per query tile
  *        (same results within the dtype's tolerance; no cross-unit load
  *        balancing, and for fp32 the general kernels).
