@@ -138,8 +138,9 @@ typedef struct {
  *   fwd: fp32 partial output tiles of query tiles whose key range is split
  *        across work units (the fast paths: bf16 with D % 8 == 0 and fp32
  *        with D % 4 == 0, 32 < D <= 256; 0 for the others, and for bf16
- *        shapes with S <= 1024 whose query tiles alone fill half the GPU or
- *        more, which run one workgroup per query tile).  The forward also
+ *        shapes whose query tiles alone fill half the GPU or more and see at
+ *        most 16 key tiles each (causal S <= 1024, or a short sliding
+ *        window), which run one workgroup per query tile).  The forward also
  *        accepts workspace = NULL and then runs one workgroup per query tile
  *        (same results within the dtype's tolerance; no cross-unit load
  *        balancing, and for fp32 the general kernels).

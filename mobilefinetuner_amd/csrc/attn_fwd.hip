@@ -407,15 +407,20 @@ int fwd_rows_per_block(const AttnShape&) { return 128; }
 FwdPlan plan_fwd_split(const AttnShape& s) {
     FwdPlan p{};
     p.balanced = !s.masked && ((s.bf16 && s.D % 8 == 0 && s.D > 32) || f32::fast_path(s));
-    // Short bf16 sequences whose query tiles alone fill half the launch's
-    // slots or more run one workgroup per query tile: with S <= 1024 the
-    // longest tile is at most 16 key tiles, and the split's partial stores
-    // and combine launch cost more than its shorter units save (C4: forward
-    // 32.5 against 34.5 us; C3 at S = 2048 measured 50.2 against 41.3, and
-    // the fp32 fast path at C2 63.5 against 41.0, so those stay split).
-    if (p.balanced && s.bf16 && s.S <= 1024) {
-        const int64_t tiles = s.B * s.Hq * ((s.S + kFwdBM - 1) / kFwdBM), slots = fwd_unit_slots(s);
-        if (2 * tiles >= slots && tiles <= slots) p.balanced = false;
+    // bf16 shapes whose query tiles alone fill half the launch's slots or
+    // more, and whose longest tile is at most 16 key tiles (causal S <= 1024,
+    // or a sliding window up to ~900 keys), run one workgroup per query tile:
+    // the split's partial stores and combine launch cost more than its
+    // shorter units save.  Measured: C4 forward 32.5 against 34.5 us, C5 with
+    // a 512-key window 25.4 against 37.4 us; C3 at S = 2048 (32 key tiles)
+    // 50.2 against 41.3, and the fp32 fast path at C2 63.5 against 41.0, so
+    // those stay split.
+    if (p.balanced && s.bf16) {
+        const int nqt = (int)((s.S + kFwdBM - 1) / kFwdBM);
+        const int64_t tiles = s.B * s.Hq * nqt, slots = fwd_unit_slots(s);
+        // the last query tile sees the most key tiles (causal or windowed)
+        const int longest = fast_q_n((int)s.S, s.causal ? 1 : 0, s.window, nqt - 1);
+        if (longest <= 16 && 2 * tiles >= slots && tiles <= slots) p.balanced = false;
     }
     if (!p.balanced) return p;
     const int S = (int)s.S, causal = s.causal ? 1 : 0, W = s.window;
