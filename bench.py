@@ -429,10 +429,10 @@ def _cpu_model():
 def _cpu_slice(task):
     """Worker process: one (batch, query head) slice of a config through the
     reference composite, forward + Engine backward; returns its seconds."""
-    cfg_id, b, h, S, kind = task
+    cfg_id, b, h, S, kind, rep = task
     from oracle import oracle as O
     c = CONFIGS[cfg_id]
-    q, k, v, dO = O.make_inputs(1, 1, 1, S, c["D"], 4242 + 97 * b + h, c["dtype"], c["do_sigma"])
+    q, k, v, dO = O.make_inputs(1, 1, 1, S, c["D"], 4242 + 97 * b + h + 7919 * rep, c["dtype"], c["do_sigma"])
     if kind == "reference":
         r = O.ref_composite(q, k, v, dO, scale=c["scale"], causal=True)
         return r["t_fwd"] + r["t_bwd"]
@@ -456,7 +456,9 @@ def cpu_leg(cfg_id, saved_cfgs=()):
     touched.  The reference operators are single-threaded, so the config is
     cut into (batch, query head) slices, each run by its own worker process
     (one core each) through the reference composite built from its own
-    sources; value = the slices' flops / the slowest slice's seconds.  The
+    sources; value = the slices' flops / the slowest slice's seconds.  When
+    the config has fewer slices than cores, whole copies of its slices (own
+    seeds) fill the cores, so the figure is the host's throughput.  The
     reference's CMake links BLAS only when find_package(BLAS) finds one
     (operator/CMakeLists.txt:164-190); this image has none, so the build is
     its pure-C++ GEMM (DISABLE_BLAS_COMPLETELY, core/ops.cpp:768-794).  Also
@@ -469,9 +471,12 @@ def cpu_leg(cfg_id, saved_cfgs=()):
         S //= 2
     kind = "reference" if O.ref_available() else "port"
     cores = _cpu_share()
-    slices = [(cfg_id, b, h, S, kind) for b in range(B) for h in range(Hq)]
+    slices = [(cfg_id, b, h, S, kind, 0) for b in range(B) for h in range(Hq)]
     if len(slices) > cores:  # whole rounds of one slice per worker
         slices = slices[:cores * (len(slices) // cores)]
+    else:  # whole copies of the config's slices, one slice per core
+        slices = [(cfg_id, b, h, S, kind, r) for r in range(cores // len(slices)) for (_, b, h, _, _, _) in slices]
+    copies = 1 + max(t[5] for t in slices)
     workers = min(cores, len(slices))
     ctx = mp.get_context("spawn")
     with ctx.Pool(workers) as pool:
@@ -484,7 +489,8 @@ def cpu_leg(cfg_id, saved_cfgs=()):
     return dict(value=round(flops / busiest / 1e12, 6), unit="TFLOP/s", cores=workers, kind=kind,
                 seconds=round(busiest, 3), cpu_seconds=round(sum(secs), 3), wall_seconds=round(wall, 3),
                 nproc=os.cpu_count(), cpu_share=cores, cpu_model=_cpu_model(), blas="none (pure C++ GEMM)",
-                sample=f"{cfg_id}: {len(slices)} (batch, query head) slices of S={S}, D={D}, one per worker "
+                sample=f"{cfg_id}: {len(slices)} (batch, query head) slices of S={S}, D={D}"
+                       f"{f' ({copies} copies of the config, own seeds)' if copies > 1 else ''}, one per worker "
                        f"process: fp32 reference composite fwd+bwd (transpose/matmul/mul/add-mask/softmax/"
                        f"matmul + Engine backward; a slice has one kv head, so no repeat_kv), reference "
                        f"sources built pure C++ (no BLAS in the image), 1 thread per slice"), saved
